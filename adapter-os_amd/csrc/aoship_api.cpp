@@ -1,0 +1,965 @@
+/*
+ * aoship_api.cpp — the C ABI declared in include/aoship.h: handles, weight upload, adapter tables,
+ * workspaces and the launch sequence of each forward.
+ *
+ * Conventions follow the reference's MLX FFI (crates/adapteros-lora-mlx-ffi/wrapper.h,
+ * src/mlx_cpp_wrapper_real.cpp): NULL from constructors and -1 from other calls on error, with a
+ * thread-local message (mlx_cpp_wrapper_real.cpp:27,1682-1684); weights are copied on upload
+ * (mlx_cpp_wrapper_real.cpp:3198-3199).
+ */
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "aos_exp.h"
+#include "aoship_internal.h"
+
+/* ------------------------------------------------------------------------------------------ */
+/* errors                                                                                     */
+/* ------------------------------------------------------------------------------------------ */
+
+static thread_local std::string g_last_error;
+
+static int set_err(const std::string &s) {
+  g_last_error = s;
+  return -1;
+}
+
+#define HIP_OR_FAIL(expr, what)                                                        \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess) return set_err(std::string(what) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+extern "C" const char *aoship_get_last_error(void) { return g_last_error.c_str(); }
+extern "C" void aoship_clear_error(void) { g_last_error.clear(); }
+extern "C" const char *aoship_version(void) { return "aoship 0.1.0 gfx950"; }
+
+/* Host build of the router's float64 exp, exported for its pinning test (not part of the ABI). */
+extern "C" double aoship_internal_exp_cr(double x) { return aos_exp_cr(x); }
+
+static int g_device = -1;
+
+static int ensure_device() {
+  if (g_device < 0) return set_err("aoship_init() has not been called");
+  HIP_OR_FAIL(hipSetDevice(g_device), "hipSetDevice");
+  return 0;
+}
+
+extern "C" int aoship_init(int device) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0) return set_err("no HIP device available");
+  if (device < 0 || device >= count) return set_err("device index out of range");
+  HIP_OR_FAIL(hipSetDevice(device), "hipSetDevice");
+  g_device = device;
+  return 0;
+}
+
+extern "C" int aoship_device_name(char *buf, int len) {
+  if (!buf || len <= 0) return set_err("aoship_device_name: null buffer");
+  if (ensure_device()) return -1;
+  hipDeviceProp_t prop;
+  HIP_OR_FAIL(hipGetDeviceProperties(&prop, g_device), "hipGetDeviceProperties");
+  snprintf(buf, (size_t)len, "%s (%s)", prop.name, prop.gcnArchName);
+  return 0;
+}
+
+extern "C" int aoship_sync(void) {
+  if (ensure_device()) return -1;
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return 0;
+}
+
+extern "C" int aoship_attest_determinism(char *buf, int len) {
+  const char *js =
+      "{\"backend\":\"hip\",\"arch\":\"gfx950\","
+      "\"rng_seed_method\":\"none: kernels draw no random numbers\","
+      "\"floating_point_mode\":\"ieee; no fast-math; fp32 denormals preserved; "
+      "router compiled with -ffp-contract=off\","
+      "\"reductions\":\"fixed order; no floating-point atomics\","
+      "\"router\":\"BitExact vs CPU (float64 softmax with correctly rounded exp)\","
+      "\"layer\":\"BitExact run-to-run; BoundedTolerance vs CPU (2e-2 relative, bf16)\","
+      "\"deterministic\":true}";
+  int n = (int)strlen(js);
+  if (buf && len > 0) snprintf(buf, (size_t)len, "%s", js);
+  return n;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* small helpers                                                                              */
+/* ------------------------------------------------------------------------------------------ */
+
+static uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static int module_index(const char *name) {
+  static const char *names[AOS_MAX_MODULES] = {"q_proj",    "k_proj",  "v_proj",   "o_proj",
+                                               "gate_proj", "up_proj", "down_proj"};
+  if (!name) return -1;
+  for (int i = 0; i < AOS_MAX_MODULES; ++i)
+    if (strcmp(name, names[i]) == 0) return i;
+  return -1;
+}
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  DevBuf(DevBuf &&o) noexcept : p(o.p), bytes(o.bytes) {
+    o.p = nullptr;
+    o.bytes = 0;
+  }
+  DevBuf &operator=(DevBuf &&o) noexcept {
+    if (this != &o) {
+      release();
+      p = o.p;
+      bytes = o.bytes;
+      o.p = nullptr;
+      o.bytes = 0;
+    }
+    return *this;
+  }
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  int alloc(size_t n, bool zero) {
+    release();
+    if (n == 0) n = 256;
+    HIP_OR_FAIL(hipMalloc(&p, n), "hipMalloc");
+    bytes = n;
+    if (zero) HIP_OR_FAIL(hipMemset(p, 0, n), "hipMemset");
+    return 0;
+  }
+  int upload(const void *src, size_t n) {
+    if (alloc(n, false)) return -1;
+    HIP_OR_FAIL(hipMemcpy(p, src, n, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    return 0;
+  }
+  template <class T>
+  T *as() const {
+    return (T *)p;
+  }
+};
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+/* ------------------------------------------------------------------------------------------ */
+/* router                                                                                     */
+/* ------------------------------------------------------------------------------------------ */
+
+struct aoship_router {
+  int n = 0, k = 1;
+  float tau = 1.0f, eps = 0.02f, bias = 1.0f;
+  DevBuf stable_id, allowed, counters, priors;
+  int counters_cap = 0, priors_cap = 0;
+  bool has_mask = false;
+  hipStream_t stream = nullptr;
+};
+
+extern "C" aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, float eps,
+                                              float routing_bias, const uint64_t *stable_ids) {
+  if (ensure_device()) return nullptr;
+  if (n_adapters < 1 || n_adapters > AOS_MAX_ADAPTERS) {
+    set_err("aoship_router_new: n_adapters must be in [1, 4096]");
+    return nullptr;
+  }
+  /* Router::new (router.rs:769-777) rejects k > MAX_K. */
+  if (k > AOSHIP_MAX_K) {
+    set_err("Adapter routing failed: K exceeds maximum allowed value of 8");
+    return nullptr;
+  }
+  auto *r = new aoship_router();
+  r->n = n_adapters;
+  r->k = k < 1 ? 1 : k; /* sanitize_k (router.rs:127-142) */
+  r->tau = (std::isfinite(tau) && tau > 0.0f) ? tau : 1.0f;                 /* :171-187 */
+  r->eps = (std::isfinite(eps) && eps >= 0.0f && eps <= 1.0f) ? eps : 0.02f; /* :146-166 */
+  r->bias = (std::isfinite(routing_bias) && routing_bias > 0.0f) ? routing_bias : 1.0f;
+  std::vector<uint64_t> ids((size_t)n_adapters, 0ull);
+  if (stable_ids) memcpy(ids.data(), stable_ids, sizeof(uint64_t) * (size_t)n_adapters);
+  if (r->stable_id.upload(ids.data(), ids.size() * sizeof(uint64_t))) {
+    delete r;
+    return nullptr;
+  }
+  return r;
+}
+
+extern "C" int aoship_router_set_policy_mask(aoship_router_t *r, const uint8_t *allowed) {
+  if (!r) return set_err("aoship_router_set_policy_mask: null router");
+  if (ensure_device()) return -1;
+  if (!allowed) {
+    r->has_mask = false;
+    r->allowed.release();
+    return 0;
+  }
+  if (r->allowed.upload(allowed, (size_t)r->n)) return -1;
+  r->has_mask = true;
+  return 0;
+}
+
+extern "C" int aoship_router_set_stream(aoship_router_t *r, void *stream) {
+  if (!r) return set_err("aoship_router_set_stream: null router");
+  r->stream = (hipStream_t)stream;
+  return 0;
+}
+
+extern "C" void aoship_router_free(aoship_router_t *r) { delete r; }
+
+static int route_common(aoship_router_t *r, const float *features, const float *router_w, int d,
+                        const float *priors_in, int T, aoship_ring_t *rings, float *priors_out,
+                        int32_t *status) {
+  if (!r) return set_err("aoship_route: null router");
+  if (T < 0 || T > (1 << 22)) return set_err("aoship_route: T out of range");
+  if (T == 0) return 0;
+  if (!rings) return set_err("aoship_route: null rings");
+  if (ensure_device()) return -1;
+  aos_route_params p;
+  memset(&p, 0, sizeof(p));
+  p.n = r->n;
+  p.d = d;
+  p.T = T;
+  p.k = r->k;
+  p.tau = r->tau;
+  p.eps = r->eps;
+  p.bias = r->bias;
+  p.stable_id = r->stable_id.as<uint64_t>();
+  p.allowed = r->has_mask ? r->allowed.as<uint8_t>() : nullptr;
+  p.rings = rings;
+  p.status = status;
+  p.priors_in = priors_in;
+  p.priors_per_block = 4;
+  if (features) {
+    if (!router_w || d <= 0) return set_err("aoship_route_features: bad router weights");
+    p.features = features;
+    p.router_w = router_w;
+    if (!priors_out) {
+      if (r->priors_cap < T) {
+        if (r->priors.alloc(sizeof(float) * (size_t)T * r->n, false)) return -1;
+        r->priors_cap = T;
+      }
+      priors_out = r->priors.as<float>();
+    }
+    p.priors_out = priors_out;
+    if (r->counters_cap < T) {
+      if (r->counters.alloc(sizeof(uint32_t) * (size_t)T, true)) return -1;
+      r->counters_cap = T;
+    }
+    p.counters = r->counters.as<uint32_t>();
+  } else if (!priors_in) {
+    return set_err("aoship_route: null priors");
+  }
+  int e = aos_launch_route(&p, r->stream);
+  if (e != 0) return set_err(std::string("route launch: ") + hipGetErrorString((hipError_t)e));
+  return 0;
+}
+
+extern "C" int aoship_route(aoship_router_t *r, const float *priors, int T, aoship_ring_t *rings,
+                            int32_t *status) {
+  return route_common(r, nullptr, nullptr, 0, priors, T, rings, nullptr, status);
+}
+
+extern "C" int aoship_route_features(aoship_router_t *r, const float *features,
+                                     const float *router_w, int d, int T, aoship_ring_t *rings,
+                                     float *priors_out, int32_t *status) {
+  if (!features) return set_err("aoship_route_features: null features");
+  return route_common(r, features, router_w, d, nullptr, T, rings, priors_out, status);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* LoRA adapters                                                                              */
+/* ------------------------------------------------------------------------------------------ */
+
+struct LoraModule {
+  bool valid = false;
+  int rank = 0, rpad = 0, in = 0, out = 0;
+  DevBuf A, B; /* bf16 [rpad][in], [out][rpad] */
+};
+
+struct aoship_lora_adapter {
+  int id = 0;
+  float scale = 1.0f;
+  std::vector<LoraModule> mods; /* [num_layers * 7] */
+  int num_layers = 0;
+  int refs = 1; /* the caller's handle + one per binding layer */
+};
+
+static void adapter_unref(aoship_lora_adapter *a) {
+  if (a && --a->refs == 0) delete a;
+}
+
+extern "C" aoship_lora_adapter_t *aoship_lora_adapter_new(int adapter_id, int num_layers,
+                                                          float scale) {
+  if (num_layers < 1 || num_layers > 4096) {
+    set_err("Failed to create LoRA adapter: num_layers out of range");
+    return nullptr;
+  }
+  auto *a = new aoship_lora_adapter();
+  a->id = adapter_id;
+  a->scale = scale;
+  a->num_layers = num_layers;
+  a->mods.resize((size_t)num_layers * AOS_MAX_MODULES);
+  return a;
+}
+
+extern "C" int aoship_lora_adapter_set_module(aoship_lora_adapter_t *a, int layer_idx,
+                                              const char *module, int rank, int in_features,
+                                              int out_features, const float *lora_a,
+                                              const float *lora_b) {
+  if (!a || !module || !lora_a || !lora_b)
+    return set_err("Null parameter in aoship_lora_adapter_set_module");
+  if (layer_idx < 0 || layer_idx >= a->num_layers)
+    return set_err("Layer index out of range: " + std::to_string(layer_idx));
+  int m = module_index(module);
+  if (m < 0) return set_err(std::string("Unknown module name: ") + module);
+  if (rank < 1 || rank > 128) return set_err("LoRA rank must be in [1, 128]");
+  if (in_features < 64 || in_features % 64 != 0)
+    return set_err("LoRA in_features must be a positive multiple of 64");
+  if (out_features < 32 || out_features % 32 != 0)
+    return set_err("LoRA out_features must be a positive multiple of 32");
+  if (ensure_device()) return -1;
+  const int rpad = (rank + 15) / 16 * 16;
+  std::vector<uint16_t> A((size_t)rpad * in_features, 0), B((size_t)out_features * rpad, 0);
+  for (int j = 0; j < rank; ++j)
+    for (int i = 0; i < in_features; ++i)
+      A[(size_t)j * in_features + i] = f32_to_bf16(lora_a[(size_t)j * in_features + i]);
+  for (int o = 0; o < out_features; ++o)
+    for (int j = 0; j < rank; ++j)
+      B[(size_t)o * rpad + j] = f32_to_bf16(lora_b[(size_t)o * rank + j]);
+  LoraModule &lm = a->mods[(size_t)layer_idx * AOS_MAX_MODULES + m];
+  if (lm.A.upload(A.data(), A.size() * 2)) return -1;
+  if (lm.B.upload(B.data(), B.size() * 2)) return -1;
+  lm.valid = true;
+  lm.rank = rank;
+  lm.rpad = rpad;
+  lm.in = in_features;
+  lm.out = out_features;
+  return 0;
+}
+
+extern "C" void aoship_lora_adapter_free(aoship_lora_adapter_t *a) { adapter_unref(a); }
+
+/* ------------------------------------------------------------------------------------------ */
+/* layers                                                                                     */
+/* ------------------------------------------------------------------------------------------ */
+
+struct Q4Mat {
+  bool valid = false;
+  int out = 0, in = 0, G = 0, RB = 0;
+  DevBuf qt, sb;
+  aos_q4_dev dev() const {
+    aos_q4_dev d;
+    d.out = out;
+    d.in = in;
+    d.G = G;
+    d.RB = RB;
+    d.qt = qt.as<uint32_t>();
+    d.sb = sb.as<uint32_t>();
+    return d;
+  }
+};
+
+struct ModTable {
+  int rpad = 0, in = 0, out = 0;
+  DevBuf A, B, scale;
+};
+
+struct KStat {
+  const char *name;
+  double ms = 0.0;
+  int64_t launches = 0;
+};
+
+struct PendingEvent {
+  int slot;
+  hipEvent_t a, b;
+};
+
+enum { KS_ROUTE = 0, KS_SHRINK_X, KS_GEMV_GU, KS_SHRINK_H, KS_GEMV_DOWN, KS_GEMV_PROJ, KS_COUNT };
+static const char *kStatNames[KS_COUNT] = {"route",         "lora_shrink_x", "q4_gemv_gate_up",
+                                           "lora_shrink_h", "q4_gemv_down",  "q4_gemv_proj"};
+
+struct aoship_layer {
+  int layer_idx = 0;
+  Q4Mat mats[AOS_MAX_MODULES];
+  std::vector<aoship_lora_adapter *> table;
+  ModTable tabs[AOS_MAX_MODULES];
+  DevBuf ws, counters;
+  size_t ws_cap = 0, ctr_cap = 0;
+  hipStream_t stream = nullptr;
+  bool profiling = false;
+  KStat stats[KS_COUNT];
+  std::vector<PendingEvent> pending;
+  std::vector<hipEvent_t> event_pool;
+};
+
+extern "C" aoship_layer_t *aoship_layer_new(int layer_idx, int group_size, int bits) {
+  if (group_size != AOSHIP_GROUP_SIZE || bits != AOSHIP_BITS) {
+    set_err("aoship_layer_new: only group_size 64 and bits 4 are supported");
+    return nullptr;
+  }
+  if (layer_idx < 0) {
+    set_err("aoship_layer_new: negative layer index");
+    return nullptr;
+  }
+  auto *l = new aoship_layer();
+  l->layer_idx = layer_idx;
+  for (int i = 0; i < KS_COUNT; ++i) l->stats[i].name = kStatNames[i];
+  return l;
+}
+
+static uint32_t shuffle_nibbles(uint32_t w) {
+  uint32_t r = 0;
+  for (int p = 0; p < 4; ++p) {
+    r |= ((w >> (8 * p)) & 0xFu) << (4 * p);
+    r |= ((w >> (8 * p + 4)) & 0xFu) << (4 * (p + 4));
+  }
+  return r;
+}
+
+extern "C" int aoship_layer_set_base(aoship_layer_t *l, const char *module, int out_features,
+                                     int in_features, const uint32_t *packed,
+                                     const uint16_t *scales_f16, const uint16_t *biases_f16) {
+  if (!l || !packed || !scales_f16) return set_err("aoship_layer_set_base: null argument");
+  int m = module_index(module);
+  if (m < 0) return set_err(std::string("Unknown module name: ") + (module ? module : "(null)"));
+  if (out_features < 32 || out_features % 32 != 0)
+    return set_err("aoship_layer_set_base: out_features must be a positive multiple of 32");
+  if (in_features < 64 || in_features % 64 != 0)
+    return set_err("aoship_layer_set_base: in_features must be a positive multiple of 64");
+  if (ensure_device()) return -1;
+  const int G = in_features / 64, RB = out_features / 32, wpr = in_features / 8;
+  std::vector<uint32_t> qt((size_t)RB * G * 256), sb((size_t)RB * G * 32);
+  for (int rb = 0; rb < RB; ++rb)
+    for (int g = 0; g < G; ++g) {
+      uint32_t *dst = qt.data() + ((size_t)rb * G + g) * 256;
+      for (int l2 = 0; l2 < 64; ++l2) {
+        const int n = l2 & 31, c = l2 >> 5;
+        const uint32_t *src = packed + (size_t)(rb * 32 + n) * wpr + g * 8 + 4 * c;
+        for (int j = 0; j < 4; ++j) dst[l2 * 4 + j] = shuffle_nibbles(src[j]);
+      }
+      uint32_t *sdst = sb.data() + ((size_t)rb * G + g) * 32;
+      for (int n = 0; n < 32; ++n) {
+        size_t idx = (size_t)(rb * 32 + n) * G + g;
+        uint32_t s = scales_f16[idx], b = biases_f16 ? biases_f16[idx] : 0u;
+        sdst[n] = s | (b << 16);
+      }
+    }
+  Q4Mat &q = l->mats[m];
+  if (q.qt.upload(qt.data(), qt.size() * 4)) return -1;
+  if (q.sb.upload(sb.data(), sb.size() * 4)) return -1;
+  q.valid = true;
+  q.out = out_features;
+  q.in = in_features;
+  q.G = G;
+  q.RB = RB;
+  return 0;
+}
+
+static void unbind_all(aoship_layer *l) {
+  for (auto *a : l->table) adapter_unref(a);
+  l->table.clear();
+  for (auto &t : l->tabs) {
+    t.A.release();
+    t.B.release();
+    t.scale.release();
+    t.rpad = 0;
+  }
+}
+
+extern "C" int aoship_layer_set_adapters(aoship_layer_t *l, aoship_lora_adapter_t *const *table,
+                                         int n) {
+  if (!l) return set_err("aoship_layer_set_adapters: null layer");
+  if (n < 0 || n > AOS_MAX_ADAPTERS) return set_err("aoship_layer_set_adapters: n out of range");
+  if (n > 0 && !table) return set_err("aoship_layer_set_adapters: null table");
+  if (ensure_device()) return -1;
+  /* validate ranks first */
+  int rp[AOS_MAX_MODULES] = {0};
+  for (int m = 0; m < AOS_MAX_MODULES; ++m)
+    for (int a = 0; a < n; ++a) {
+      aoship_lora_adapter *ad = table[a];
+      if (!ad || l->layer_idx >= ad->num_layers) continue;
+      const LoraModule &lm = ad->mods[(size_t)l->layer_idx * AOS_MAX_MODULES + m];
+      if (!lm.valid) continue;
+      if (rp[m] == 0) rp[m] = lm.rpad;
+      if (rp[m] != lm.rpad)
+        return set_err("aoship_layer_set_adapters: adapters bound to one module must share a rank");
+    }
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  unbind_all(l);
+  for (int a = 0; a < n; ++a) {
+    l->table.push_back(table[a]);
+    if (table[a]) table[a]->refs++;
+  }
+  for (int m = 0; m < AOS_MAX_MODULES; ++m) {
+    ModTable &t = l->tabs[m];
+    t.rpad = rp[m];
+    if (rp[m] == 0 || n == 0) continue;
+    std::vector<const void *> A((size_t)n, nullptr), B((size_t)n, nullptr);
+    std::vector<float> sc((size_t)n, 0.0f);
+    for (int a = 0; a < n; ++a) {
+      aoship_lora_adapter *ad = table[a];
+      if (!ad || l->layer_idx >= ad->num_layers) continue;
+      const LoraModule &lm = ad->mods[(size_t)l->layer_idx * AOS_MAX_MODULES + m];
+      if (!lm.valid) continue;
+      A[a] = lm.A.p;
+      B[a] = lm.B.p;
+      sc[a] = ad->scale;
+      t.in = lm.in;
+      t.out = lm.out;
+    }
+    if (t.A.upload(A.data(), A.size() * sizeof(void *))) return -1;
+    if (t.B.upload(B.data(), B.size() * sizeof(void *))) return -1;
+    if (t.scale.upload(sc.data(), sc.size() * sizeof(float))) return -1;
+  }
+  return 0;
+}
+
+extern "C" int aoship_layer_set_stream(aoship_layer_t *l, void *stream) {
+  if (!l) return set_err("aoship_layer_set_stream: null layer");
+  l->stream = (hipStream_t)stream;
+  return 0;
+}
+
+static aos_lora_tab lora_tab(const aoship_layer *l, int m, int in, int out) {
+  aos_lora_tab t;
+  memset(&t, 0, sizeof(t));
+  const ModTable &mt = l->tabs[m];
+  if (mt.rpad == 0 || l->table.empty()) return t;
+  if (mt.in != in || mt.out != out) return t; /* shapes that do not match this layer are unused */
+  t.n = (int)l->table.size();
+  t.rpad = mt.rpad;
+  t.A = mt.A.as<const uint16_t *const>();
+  t.B = mt.B.as<const uint16_t *const>();
+  t.scale = mt.scale.as<const float>();
+  return t;
+}
+
+/* ---- profiling ---- */
+
+static hipEvent_t get_event(aoship_layer *l) {
+  if (!l->event_pool.empty()) {
+    hipEvent_t e = l->event_pool.back();
+    l->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+static void resolve_events(aoship_layer *l) {
+  for (auto &pe : l->pending) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(pe.b) == hipSuccess && hipEventElapsedTime(&ms, pe.a, pe.b) == hipSuccess) {
+      l->stats[pe.slot].ms += ms;
+      l->stats[pe.slot].launches += 1;
+    }
+    l->event_pool.push_back(pe.a);
+    l->event_pool.push_back(pe.b);
+  }
+  l->pending.clear();
+}
+
+extern "C" int aoship_layer_set_profiling(aoship_layer_t *l, int enable) {
+  if (!l) return set_err("aoship_layer_set_profiling: null layer");
+  if (ensure_device()) return -1;
+  resolve_events(l);
+  l->profiling = enable != 0;
+  for (auto &s : l->stats) {
+    s.ms = 0.0;
+    s.launches = 0;
+  }
+  return 0;
+}
+
+extern "C" int aoship_layer_kernel_stats(aoship_layer_t *l, int idx, const char **name,
+                                         double *total_ms, int64_t *launches) {
+  if (!l) return set_err("aoship_layer_kernel_stats: null layer");
+  if (ensure_device()) return -1;
+  resolve_events(l);
+  if (idx >= 0 && idx < KS_COUNT) {
+    if (name) *name = l->stats[idx].name;
+    if (total_ms) *total_ms = l->stats[idx].ms;
+    if (launches) *launches = l->stats[idx].launches;
+  }
+  return KS_COUNT;
+}
+
+struct Timed {
+  aoship_layer *l;
+  int slot;
+  hipEvent_t a = nullptr, b = nullptr;
+  Timed(aoship_layer *l_, int s) : l(l_), slot(s) {
+    if (l->profiling) {
+      a = get_event(l);
+      b = get_event(l);
+      if (a) (void)hipEventRecord(a, l->stream);
+    }
+  }
+  ~Timed() {
+    if (l->profiling && a && b) {
+      (void)hipEventRecord(b, l->stream);
+      l->pending.push_back({slot, a, b});
+    }
+  }
+};
+
+/* ---- workspace ---- */
+
+struct Bump {
+  char *base;
+  size_t off = 0, cap;
+  Bump(void *b, size_t c) : base((char *)b), cap(c) {}
+  template <class T>
+  T *take(size_t n) {
+    off = (off + 255) & ~(size_t)255;
+    T *p = (T *)(base ? base + off : nullptr);
+    off += n * sizeof(T);
+    return p;
+  }
+};
+
+static int ws_reserve(aoship_layer *l, size_t bytes, size_t ctr_words) {
+  if (bytes > l->ws_cap) {
+    HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (l->ws.alloc(bytes, false)) return -1;
+    l->ws_cap = bytes;
+  }
+  if (ctr_words * 4 > l->ctr_cap) {
+    HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (l->counters.alloc(ctr_words * 4, true)) return -1;
+    l->ctr_cap = ctr_words * 4;
+  }
+  return 0;
+}
+
+static int gemv_ks(int RB, int G, int W) {
+  int ks = (1024 + RB - 1) / RB;
+  int maxks = G / (2 * W);
+  if (maxks < 1) maxks = 1;
+  if (ks > maxks) ks = maxks;
+  if (ks < 1) ks = 1;
+  return ks;
+}
+
+static int gemv_waves(int G) { return G >= 128 ? 8 : 4; }
+
+static int nv_for(int T) {
+  if (T <= 1) return 1;
+  if (T <= 2) return 2;
+  if (T <= 8) return 4;
+  if (T <= 16) return 8;
+  return 16;
+}
+
+static int shrink_kc(int G) {
+  int kc = G / 8;
+  return kc < 1 ? 1 : kc;
+}
+
+/* Plan of one decode chunk (T <= 32): workspace carve-up and launch parameters. */
+struct MlpPlan {
+  aos_shrink_params sh1, sh2;
+  aos_gemv_params gv1, gv2;
+  size_t bytes = 0, ctr = 0;
+};
+
+static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_ring_t *rings,
+                     uint16_t *y, void *ws, void *ctr, MlpPlan &P) {
+  const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
+  const int H = Wg.in, I = Wg.out;
+  aos_lora_tab tg = lora_tab(l, MOD_GATE, H, I), tu = lora_tab(l, MOD_UP, H, I),
+               td = lora_tab(l, MOD_DOWN, I, H);
+  const int nb = (int)l->table.size();
+  int umax = nb < 8 * T ? nb : 8 * T;
+  if (umax < 1) umax = 1;
+  Bump b(ws, 0);
+  uint32_t *cbase = (uint32_t *)ctr;
+  size_t coff = 0;
+  auto ctrs = [&](size_t n) {
+    uint32_t *p = cbase ? cbase + coff : nullptr;
+    coff += n;
+    return p;
+  };
+  uint16_t *Sg = b.take<uint16_t>((size_t)T * umax * (tg.rpad ? tg.rpad : 16));
+  uint16_t *Su = b.take<uint16_t>((size_t)T * umax * (tu.rpad ? tu.rpad : 16));
+  uint16_t *Sd = b.take<uint16_t>((size_t)T * umax * (td.rpad ? td.rpad : 16));
+  float *xs2 = b.take<float>((size_t)T * 2 * (H / 64));
+  uint16_t *h = b.take<uint16_t>((size_t)T * I);
+  float *hs2 = b.take<float>((size_t)T * (I / 32));
+
+  /* shrink of x for gate and up */
+  aos_shrink_params &s1 = P.sh1;
+  memset(&s1, 0, sizeof(s1));
+  s1.x = x;
+  s1.T = T;
+  s1.in = H;
+  s1.rings = rings;
+  s1.nmod = 2;
+  s1.tab[0] = tg;
+  s1.tab[1] = tu;
+  s1.S[0] = Sg;
+  s1.S[1] = Su;
+  s1.umax = umax;
+  s1.xs2 = xs2;
+  s1.kc = shrink_kc(H / 64);
+  int rpm1 = tg.rpad > tu.rpad ? tg.rpad : tu.rpad;
+  s1.n_col_tiles = (umax * (rpm1 ? rpm1 : 16) + 31) / 32;
+  s1.part = b.take<float>((size_t)2 * s1.n_col_tiles * s1.kc * 1024);
+  s1.counters = ctrs((size_t)2 * s1.n_col_tiles);
+
+  /* gate/up GEMV + SwiGLU */
+  aos_gemv_params &g1 = P.gv1;
+  memset(&g1, 0, sizeof(g1));
+  g1.w0 = Wg.dev();
+  g1.w1 = Wu.dev();
+  g1.x = x;
+  g1.xs2 = xs2;
+  g1.T = T;
+  g1.waves = 4;
+  g1.ks = gemv_ks(Wg.RB, Wg.G, g1.waves);
+  g1.tab0 = tg;
+  g1.tab1 = tu;
+  g1.S0 = Sg;
+  g1.S1 = Su;
+  g1.umax = umax;
+  g1.rings = rings;
+  g1.y = h;
+  g1.ys2 = hs2;
+  g1.part = b.take<float>((size_t)Wg.RB * g1.ks * 2 * nv_for(T) * 64);
+  g1.counters = ctrs((size_t)Wg.RB);
+
+  /* shrink of h for down */
+  aos_shrink_params &s2 = P.sh2;
+  memset(&s2, 0, sizeof(s2));
+  s2.x = h;
+  s2.T = T;
+  s2.in = I;
+  s2.rings = rings;
+  s2.nmod = 1;
+  s2.tab[0] = td;
+  s2.S[0] = Sd;
+  s2.umax = umax;
+  s2.xs2 = nullptr;
+  s2.kc = shrink_kc(I / 64);
+  s2.n_col_tiles = (umax * (td.rpad ? td.rpad : 16) + 31) / 32;
+  s2.part = b.take<float>((size_t)s2.n_col_tiles * s2.kc * 1024);
+  s2.counters = ctrs((size_t)s2.n_col_tiles);
+
+  /* down GEMV */
+  aos_gemv_params &g2 = P.gv2;
+  memset(&g2, 0, sizeof(g2));
+  g2.w0 = Wd.dev();
+  g2.x = h;
+  g2.xs2 = hs2;
+  g2.T = T;
+  g2.waves = gemv_waves(Wd.G);
+  g2.ks = gemv_ks(Wd.RB, Wd.G, g2.waves);
+  g2.tab0 = td;
+  g2.S0 = Sd;
+  g2.umax = umax;
+  g2.rings = rings;
+  g2.y = y;
+  g2.part = b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
+  g2.counters = ctrs((size_t)Wd.RB);
+
+  P.bytes = b.off + 256;
+  P.ctr = coff + 64;
+}
+
+extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
+  if (!l) return set_err("aoship_layer_reserve: null layer");
+  if (max_tokens < 1) return set_err("aoship_layer_reserve: max_tokens must be >= 1");
+  if (ensure_device()) return -1;
+  int T = max_tokens < AOS_DECODE_MAX_T ? max_tokens : AOS_DECODE_MAX_T;
+  size_t bytes = 0, ctr = 0;
+  if (l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid) {
+    MlpPlan P;
+    plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+    bytes = P.bytes;
+    ctr = P.ctr;
+  }
+  for (int m = 0; m < AOS_MAX_MODULES; ++m) {
+    if (!l->mats[m].valid) continue;
+    const Q4Mat &W = l->mats[m];
+    size_t need = (size_t)T * 8 * 128 * 2 + (size_t)T * 2 * W.G * 4 +
+                  (size_t)W.RB * 16 * 16 * 64 * 4 + (size_t)64 * 48 * 1024 * 4 + 65536;
+    if (need > bytes) bytes = need;
+    size_t c = (size_t)W.RB + 3 * 1024;
+    if (c > ctr) ctr = c;
+  }
+  return ws_reserve(l, bytes, ctr);
+}
+
+static int check_common(aoship_layer *l, const void *x, int T, const aoship_ring_t *rings,
+                        const void *y) {
+  if (!l) return set_err("forward: null layer");
+  if (!x || !y || !rings) return set_err("forward: null device pointer");
+  if (!aligned16(x) || !aligned16(y)) return set_err("forward: x and y must be 16-byte aligned");
+  if (T < 0) return set_err("forward: negative token count");
+  return ensure_device();
+}
+
+static int launch_err(int e, const char *what) {
+  if (e == 0) return 0;
+  return set_err(std::string(what) + ": " + hipGetErrorString((hipError_t)e));
+}
+
+extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int T,
+                                  const aoship_ring_t *rings, aoship_bf16_t *y) {
+  if (check_common(l, x, T, rings, y)) return -1;
+  if (!l->mats[MOD_GATE].valid || !l->mats[MOD_UP].valid || !l->mats[MOD_DOWN].valid)
+    return set_err("aoship_mlp_forward: gate_proj, up_proj and down_proj must be set");
+  const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
+  if (Wu.in != Wg.in || Wu.out != Wg.out || Wd.in != Wg.out || Wd.out != Wg.in)
+    return set_err("aoship_mlp_forward: gate/up/down shapes are inconsistent");
+  const int H = Wg.in;
+  for (int t0 = 0; t0 < T; t0 += AOS_DECODE_MAX_T) {
+    const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;
+    MlpPlan P;
+    plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+    if (ws_reserve(l, P.bytes, P.ctr)) return -1;
+    plan_mlp(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, P);
+    {
+      Timed tm(l, KS_SHRINK_X);
+      if (launch_err(aos_launch_shrink(&P.sh1, l->stream), "lora shrink")) return -1;
+    }
+    {
+      Timed tm(l, KS_GEMV_GU);
+      if (launch_err(aos_launch_gemv(&P.gv1, 1, l->stream), "q4 gemv gate/up")) return -1;
+    }
+    {
+      Timed tm(l, KS_SHRINK_H);
+      if (launch_err(aos_launch_shrink(&P.sh2, l->stream), "lora shrink down")) return -1;
+    }
+    {
+      Timed tm(l, KS_GEMV_DOWN);
+      if (launch_err(aos_launch_gemv(&P.gv2, 0, l->stream), "q4 gemv down")) return -1;
+    }
+  }
+  return 0;
+}
+
+/* One or more projections sharing the input x. */
+static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *x, int T,
+                      const aoship_ring_t *rings, uint16_t *const *ys) {
+  const int in = l->mats[mods[0]].in;
+  for (int i = 0; i < nm; ++i) {
+    if (!l->mats[mods[i]].valid) return set_err("projection weights not set");
+    if (l->mats[mods[i]].in != in) return set_err("projections sharing x must share in_features");
+    if (!ys[i] || !aligned16(ys[i])) return set_err("forward: output must be 16-byte aligned");
+  }
+  for (int t0 = 0; t0 < T; t0 += AOS_DECODE_MAX_T) {
+    const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;
+    const uint16_t *xc = x + (size_t)t0 * in;
+    const aoship_ring_t *rc = rings + t0;
+    const int nb = (int)l->table.size();
+    int umax = nb < 8 * Tc ? nb : 8 * Tc;
+    if (umax < 1) umax = 1;
+    aos_lora_tab tabs[3];
+    int rpm = 16;
+    for (int i = 0; i < nm; ++i) {
+      tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
+      if (tabs[i].rpad > rpm) rpm = tabs[i].rpad;
+    }
+    /* carve workspace */
+    for (int pass = 0; pass < 2; ++pass) {
+      Bump b(pass ? l->ws.p : nullptr, 0);
+      uint32_t *cb = pass ? (uint32_t *)l->counters.p : nullptr;
+      size_t coff = 0;
+      aos_shrink_params sp;
+      memset(&sp, 0, sizeof(sp));
+      sp.x = xc;
+      sp.T = Tc;
+      sp.in = in;
+      sp.rings = rc;
+      sp.nmod = nm;
+      sp.umax = umax;
+      for (int i = 0; i < nm; ++i) {
+        sp.tab[i] = tabs[i];
+        sp.S[i] = b.take<uint16_t>((size_t)Tc * umax * rpm);
+      }
+      sp.xs2 = b.take<float>((size_t)Tc * 2 * (in / 64));
+      sp.kc = shrink_kc(in / 64);
+      sp.n_col_tiles = (umax * rpm + 31) / 32;
+      sp.part = b.take<float>((size_t)nm * sp.n_col_tiles * sp.kc * 1024);
+      sp.counters = cb ? cb + coff : nullptr;
+      coff += (size_t)nm * sp.n_col_tiles;
+      aos_gemv_params gp[3];
+      for (int i = 0; i < nm; ++i) {
+        const Q4Mat &W = l->mats[mods[i]];
+        memset(&gp[i], 0, sizeof(gp[i]));
+        gp[i].w0 = W.dev();
+        gp[i].x = xc;
+        gp[i].xs2 = sp.xs2;
+        gp[i].T = Tc;
+        gp[i].waves = gemv_waves(W.G);
+        gp[i].ks = gemv_ks(W.RB, W.G, gp[i].waves);
+        gp[i].tab0 = tabs[i];
+        gp[i].S0 = sp.S[i];
+        gp[i].umax = umax;
+        gp[i].rings = rc;
+        gp[i].y = ys[i] + (size_t)t0 * W.out;
+        gp[i].part = b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
+        gp[i].counters = cb ? cb + coff : nullptr;
+        coff += (size_t)W.RB;
+      }
+      if (pass == 0) {
+        if (ws_reserve(l, b.off + 256, coff + 64)) return -1;
+        continue;
+      }
+      {
+        Timed tm(l, KS_SHRINK_X);
+        if (launch_err(aos_launch_shrink(&sp, l->stream), "lora shrink")) return -1;
+      }
+      for (int i = 0; i < nm; ++i) {
+        Timed tm(l, KS_GEMV_PROJ);
+        if (launch_err(aos_launch_gemv(&gp[i], 0, l->stream), "q4 gemv")) return -1;
+      }
+    }
+  }
+  return 0;
+}
+
+extern "C" int aoship_proj_forward(aoship_layer_t *l, const char *module, const aoship_bf16_t *x,
+                                   int T, const aoship_ring_t *rings, aoship_bf16_t *y) {
+  if (check_common(l, x, T, rings, y)) return -1;
+  int m = module_index(module);
+  if (m < 0) return set_err(std::string("Unknown module name: ") + (module ? module : "(null)"));
+  if (!l->mats[m].valid) return set_err(std::string("base weights not set for ") + module);
+  int mods[1] = {m};
+  uint16_t *ys[1] = {y};
+  return proj_multi(l, mods, 1, x, T, rings, ys);
+}
+
+extern "C" int aoship_qkv_forward(aoship_layer_t *l, const aoship_bf16_t *x, int T,
+                                  const aoship_ring_t *rings, aoship_bf16_t *q, aoship_bf16_t *k,
+                                  aoship_bf16_t *v) {
+  if (check_common(l, x, T, rings, q)) return -1;
+  int mods[3] = {MOD_Q, MOD_K, MOD_V};
+  uint16_t *ys[3] = {q, k, v};
+  return proj_multi(l, mods, 3, x, T, rings, ys);
+}
+
+extern "C" void aoship_layer_free(aoship_layer_t *l) {
+  if (!l) return;
+  (void)hipDeviceSynchronize();
+  resolve_events(l);
+  for (auto e : l->event_pool) (void)hipEventDestroy(e);
+  unbind_all(l);
+  delete l;
+}

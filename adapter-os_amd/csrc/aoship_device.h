@@ -1,0 +1,78 @@
+/*
+ * aoship_device.h — device-side types and helpers shared by the gfx950 kernels.
+ *
+ * Matrix-core fragments use v_mfma_f32_32x32x16_bf16. For an MFMA step, lane l = i + 32 c
+ * (i in 0..31, c in 0..1) supplies 8 consecutive K elements for row/column i, half c. The
+ * accumulator holds C[m][n] with n = l % 32 and m = 8 (v / 4) + 4 (l / 32) + v % 4 for
+ * register v in 0..15.
+ */
+#ifndef AOSHIP_DEVICE_H
+#define AOSHIP_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define AOS_WAVE 64
+
+__device__ __forceinline__ f32x16 aos_mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+/* Token (row of the MFMA M dimension) held by accumulator register v in lane l. */
+__device__ __forceinline__ int aos_acc_m(int v, int lane) {
+  return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+}
+
+__device__ __forceinline__ float aos_bf16_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+
+/* float32 -> bfloat16, round to nearest even (NaN kept quiet). */
+__device__ __forceinline__ uint16_t aos_f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float aos_f16_to_f32(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+/* Four packed bfloat16 pairs (128 + q) from one nibble-shuffled weight word: register p holds
+ * (q[2p], q[2p+1]) of the original MLX word as bf16 values 128 + q (exact). */
+__device__ __forceinline__ u32x4 aos_q4_magic(uint32_t w) {
+  u32x4 r;
+  r.x = (w & 0x000F000Fu) | 0x43004300u;
+  r.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  r.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  r.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return r;
+}
+
+__device__ __forceinline__ uint32_t aos_shfl(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+
+__device__ __forceinline__ float aos_shfl_f(float v, int src_lane) {
+  return __builtin_bit_cast(float, aos_shfl(__builtin_bit_cast(uint32_t, v), src_lane));
+}
+
+__device__ __forceinline__ uint64_t aos_shfl64(uint64_t v, int src_lane) {
+  uint32_t lo = aos_shfl((uint32_t)v, src_lane);
+  uint32_t hi = aos_shfl((uint32_t)(v >> 32), src_lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+/* Agent-scope release / acquire around the "last arriving workgroup" reductions. */
+__device__ __forceinline__ void aos_fence_release() { __threadfence(); }
+__device__ __forceinline__ void aos_fence_acquire() { __threadfence(); }
+
+#endif

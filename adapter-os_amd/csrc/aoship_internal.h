@@ -1,0 +1,121 @@
+/*
+ * aoship_internal.h — launch parameter blocks shared between the C ABI (host) and the kernels.
+ *
+ * Device data layouts:
+ *
+ *   int4 base matrix W[out][in] ("q4 tiles"), out % 32 == 0, in % 64 == 0, G = in / 64,
+ *   RB = out / 32 row blocks:
+ *     qt[((rb * G + g) * 64 + l) * 4 + j], l in 0..63, j in 0..3
+ *        = shuffle(Wp[rb*32 + l%32][g*8 + 4*(l/32) + j])
+ *     where Wp is the MLX word (8 nibbles, low nibble first) and shuffle reorders the nibbles
+ *     to (n0, n2, n4, n6, n1, n3, n5, n7) so that masking with 0x000F000F after a shift of
+ *     4p yields the natural pair (n[2p], n[2p+1]). One row block and group is one contiguous
+ *     1 KiB chunk: a wave reads it with one 16-byte load per lane.
+ *     sb[(rb * G + g) * 32 + n] = f16 scale | f16 bias << 16 for row rb*32+n, group g.
+ *
+ *   LoRA module: A[rpad][in] and B[out][rpad] bfloat16 row-major, rank zero-padded to rpad, a
+ *   multiple of 16.
+ *
+ *   Activations: bfloat16 [T][features] row-major. Group half-sums xs2[T][2G] (float32) hold
+ *   the sum of elements 32h..32h+31 of each 64-element group, used for the int4 bias term.
+ */
+#ifndef AOSHIP_INTERNAL_H
+#define AOSHIP_INTERNAL_H
+
+#include <stdint.h>
+
+#include "../../include/aoship.h"
+
+#define AOS_MAX_MODULES 7
+enum { MOD_Q = 0, MOD_K, MOD_V, MOD_O, MOD_GATE, MOD_UP, MOD_DOWN };
+
+#define AOS_MAX_ADAPTERS 4096
+#define AOS_DECODE_MAX_T 32
+
+typedef struct {
+  int out, in, G, RB;
+  const uint32_t *qt;
+  const uint32_t *sb;
+} aos_q4_dev;
+
+/* Per-module view of the bound adapter table. */
+typedef struct {
+  int n;        /* table length */
+  int rpad;     /* padded rank (multiple of 16), 0 if no adapter has this module */
+  const uint16_t *const *A; /* device array [n] of device pointers (NULL = absent) */
+  const uint16_t *const *B;
+  const float *scale;       /* device [n] alpha / rank */
+} aos_lora_tab;
+
+/* Union of adapters used by a token tile: list[u] ascending adapter index, count U. */
+typedef struct {
+  const aoship_ring_t *rings;
+  int T;
+  int n_bound;
+} aos_union_src;
+
+/* ---- router ---- */
+typedef struct {
+  int n, d, T, k;
+  float tau, eps, bias;
+  const float *features;
+  const float *router_w;
+  const float *priors_in;
+  float *priors_out;
+  const uint64_t *stable_id;
+  const uint8_t *allowed;
+  aoship_ring_t *rings;
+  int32_t *status;
+  uint32_t *counters; /* [T], zero between launches */
+  int priors_per_block;
+} aos_route_params;
+
+/* ---- LoRA shrink: S[t][u*rpad + j] = coef(t, u) * sum_i A_u[j][i] x[t][i] ----
+ * Up to 3 modules sharing the input x (gate+up, or q+k+v) in one launch (grid.y = module). */
+typedef struct {
+  const uint16_t *x; /* [T][in] bf16 */
+  int T, in;
+  const aoship_ring_t *rings;
+  int nmod;
+  aos_lora_tab tab[3];
+  uint16_t *S[3];    /* [T][umax * rpad] bf16 per module */
+  int umax;          /* S row stride is umax * rpad */
+  float *xs2;        /* [T][2G] group half sums, written if non-NULL */
+  float *part;       /* [nmod][n_col_tiles][kc][16*64] split-K partials */
+  uint32_t *counters;/* [nmod][n_col_tiles] zero between launches */
+  int kc;            /* K chunks */
+  int n_col_tiles;
+} aos_shrink_params;
+
+/* ---- decode GEMV ---- */
+typedef struct {
+  aos_q4_dev w0, w1;  /* w1 used in SwiGLU mode (up), w0 = gate or the single matrix */
+  const uint16_t *x;  /* [T][in] bf16 */
+  const float *xs2;   /* [T][2G] */
+  int T;
+  int ks;             /* workgroups per row block (split K) */
+  int waves;          /* waves per workgroup: 4 or 8 */
+  /* LoRA expand */
+  aos_lora_tab tab0, tab1;
+  const uint16_t *S0, *S1; /* [T][umax*rpad] */
+  int umax;
+  const aoship_ring_t *rings;
+  /* outputs */
+  uint16_t *y;        /* [T][out] bf16 (plain) or h (SwiGLU) */
+  float *ys2;         /* SwiGLU: h half sums [T][out/32] */
+  float *part;        /* [RB][ks][nacc][64*16] */
+  uint32_t *counters; /* [RB] zero between launches */
+} aos_gemv_params;
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+/* Host-side launchers (return hipError_t as int). */
+int aos_launch_route(const aos_route_params *p, void *stream);
+int aos_launch_shrink(const aos_shrink_params *p, void *stream);
+int aos_launch_gemv(const aos_gemv_params *p, int swiglu, void *stream);
+#ifdef __cplusplus
+}
+#endif
+
+#endif

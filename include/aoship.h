@@ -1,0 +1,195 @@
+/*
+ * aoship.h — C ABI of the MI355X (gfx950) adapter-augmented inference hot path.
+ *
+ * One hot path of adapterOS, rebuilt for one MI355X: the K-sparse router's Q15 top-K gating
+ * feeding fused int4 (MLX affine, group 64) linear layers — a SwiGLU MLP or the attention
+ * projections — that add the selected adapters' low-rank deltas
+ *     y = W_q4 . x + sum_k (scale_k * q_k / 32767) * B_k . (A_k . x).
+ *
+ * The ABI follows the conventions of the reference's MLX FFI
+ * (crates/adapteros-lora-mlx-ffi/wrapper.h):
+ *   - opaque handles; constructors return NULL on error, other calls return 0 / -1;
+ *   - the error text of the last failing call on this thread is read with
+ *     aoship_get_last_error() and cleared with aoship_clear_error();
+ *   - the caller owns every buffer it passes; weights are copied to device memory by the
+ *     set_* calls, so host arrays may be released when those return;
+ *   - calls on one handle must be serialised by the caller (the reference serialises every
+ *     forward with a mutex: crates/adapteros-lora-mlx-ffi/src/lib.rs:420-425,1250).
+ *
+ * Pointers documented as "device" are HIP device pointers on the device chosen by
+ * aoship_init(); the compute calls are asynchronous on the handle's stream (default: the null
+ * stream) and allocate nothing once aoship_layer_reserve() has sized the workspace.
+ */
+#ifndef AOSHIP_H
+#define AOSHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AOSHIP_MAX_K 8           /* crates/adapteros-core/src/defaults.rs:37 (MAX_K) */
+#define AOSHIP_Q15_DENOM 32767.0f /* crates/adapteros-core/src/invariants.rs:107 */
+#define AOSHIP_GROUP_SIZE 64
+#define AOSHIP_BITS 4
+
+/* Router decision handed to the layer kernels: the 40-byte GPU form of RouterRing
+ * (crates/adapteros-lora-kernel-api/src/lib.rs:57-71; byte layout of MetalRingBufferLayout,
+ * crates/adapteros-lora-kernel-mtl/src/ring_buffer.rs:52-58). Unused slots are zero. */
+typedef struct aoship_ring {
+  uint32_t top_k;
+  uint32_t current_pos;
+  uint16_t adapter_indices[8];
+  int16_t gates_q15[8];
+} aoship_ring_t;
+
+typedef uint16_t aoship_bf16_t; /* bfloat16 bit pattern */
+
+typedef struct aoship_router aoship_router_t;
+typedef struct aoship_layer aoship_layer_t;
+typedef struct aoship_lora_adapter aoship_lora_adapter_t;
+
+/* ---- errors, version, device -------------------------------------------------------------- */
+
+/* Replaces mlx_get_last_error / mlx_clear_error (wrapper.h:199-200). Thread-local text. */
+const char *aoship_get_last_error(void);
+void aoship_clear_error(void);
+
+/* Library version string. */
+const char *aoship_version(void);
+
+/* Select the HIP device used by later calls on this process (mirrors the MLX backend's device
+ * selection, crates/adapteros-lora-kernel-mtl/src/lib.rs:397-399). Returns 0 / -1. */
+int aoship_init(int device);
+
+/* Device name, as FusedKernels::device_name (crates/adapteros-lora-kernel-api/src/lib.rs:374).
+ * Writes at most len bytes including the terminator. Returns 0 / -1. */
+int aoship_device_name(char *buf, int len);
+
+/* Wait for all work on the device (the reference's commit/wait device boundary,
+ * crates/adapteros-lora-kernel-mtl/src/fused_mlp.rs:233-234). Returns 0 / -1. */
+int aoship_sync(void);
+
+/* Determinism attestation as JSON text, the counterpart of FusedKernels::attest_determinism
+ * (crates/adapteros-lora-kernel-api/src/lib.rs:383, DeterminismReport in attestation.rs:130-234).
+ * Returns the number of bytes needed (excluding the terminator) or -1. */
+int aoship_attest_determinism(char *buf, int len);
+
+/* ---- router ---------------------------------------------------------------------------------- */
+
+/* Router::new_with_weights(k, tau, eps) + set_routing_bias (crates/adapteros-lora-router/src/
+ * router.rs:397-428, 556-562, 769-785) for n_adapters adapters whose AdapterInfo::stable_id are
+ * stable_ids[n] (host; NULL = all zero, the AdapterInfo default, types.rs:645-664).
+ * k > 8 fails like Router::new; k == 0 is lifted to 1; tau and eps are sanitised as
+ * router.rs:146-187; a non-finite or non-positive routing_bias keeps 1.0. n_adapters <= 4096. */
+aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, float eps,
+                                   float routing_bias, const uint64_t *stable_ids);
+
+/* PolicyMask::allowed (crates/adapteros-lora-router/src/policy_mask.rs): allowed[n] host bytes,
+ * nonzero = allowed; NULL = allow all. Returns 0 / -1. */
+int aoship_router_set_policy_mask(aoship_router_t *router, const uint8_t *allowed);
+
+/* Stream (hipStream_t) for this router's launches; NULL = null stream. Returns 0 / -1. */
+int aoship_router_set_stream(aoship_router_t *router, void *stream);
+
+void aoship_router_free(aoship_router_t *router);
+
+/* Route T tokens, deterministic mode, empty feature vector: the replacement for
+ * Router::route_with_adapter_info_and_scope_with_ctx (router.rs:1567-1952) followed by
+ * Decision -> RouterRing (types.rs:699-706, kernel-api lib.rs:122-193).
+ *   priors  : device float[T * n_adapters]
+ *   rings   : device aoship_ring_t[T] (written)
+ *   status  : device int32[T] or NULL; 0 = decision written, -1 = non-finite prior or score
+ *             (AosError::DeterminismViolation, router.rs:611-625,1640-1686), ring zero-filled.
+ * Asynchronous. Returns 0 / -1 (argument errors only). */
+int aoship_route(aoship_router_t *router, const float *priors, int T, aoship_ring_t *rings,
+                 int32_t *status);
+
+/* Route with priors computed on the device from router features: priors[t, a] =
+ * sum_i router_w[a, i] * features[t, i] in float32 with a fixed reduction order (64 strided
+ * fused-multiply-add partial sums, then a xor butterfly), then as aoship_route.
+ *   features   : device float[T * d];  router_w : device float[n_adapters * d]
+ *   priors_out : device float[T * n_adapters] or NULL. */
+int aoship_route_features(aoship_router_t *router, const float *features, const float *router_w,
+                          int d, int T, aoship_ring_t *rings, float *priors_out,
+                          int32_t *status);
+
+/* ---- LoRA adapters (mirrors wrapper.h:375-420) --------------------------------------------- */
+
+/* mlx_lora_adapter_new (mlx_cpp_wrapper_real.cpp:3164-3175): scale = alpha / rank. */
+aoship_lora_adapter_t *aoship_lora_adapter_new(int adapter_id, int num_layers, float scale);
+
+/* mlx_lora_adapter_set_module (mlx_cpp_wrapper_real.cpp:3177-3205) with the arrays passed as
+ * host float32 data in MLX shapes: lora_a[rank * in_features], lora_b[out_features * rank].
+ * module is one of q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj. The weights
+ * are stored on the device as bfloat16, rank padded to a multiple of 16 with zeros.
+ * rank <= 128. Returns 0 / -1. */
+int aoship_lora_adapter_set_module(aoship_lora_adapter_t *adapter, int layer_idx,
+                                   const char *module, int rank, int in_features,
+                                   int out_features, const float *lora_a, const float *lora_b);
+
+/* mlx_lora_adapter_free (mlx_cpp_wrapper_real.cpp:3207-3211). Device memory is released when
+ * no layer still binds the adapter. */
+void aoship_lora_adapter_free(aoship_lora_adapter_t *adapter);
+
+/* ---- layers ----------------------------------------------------------------------------------- */
+
+/* A transformer layer's adapter-augmented projections (layer_idx selects the adapters' layer). */
+aoship_layer_t *aoship_layer_new(int layer_idx, int group_size, int bits);
+
+/* Upload one base projection in MLX 4-bit layout (get_weight_with_dequant,
+ * mlx_cpp_wrapper_real.cpp:925-956): packed[out * in/8] uint32 with 8 nibbles per word, low
+ * nibble first; scales_f16 / biases_f16[out * in/64] float16 bit patterns (biases NULL = 0).
+ * Requires out % 32 == 0 and in % 64 == 0. Returns 0 / -1. */
+int aoship_layer_set_base(aoship_layer_t *layer, const char *module, int out_features,
+                          int in_features, const uint32_t *packed, const uint16_t *scales_f16,
+                          const uint16_t *biases_f16);
+
+/* Bind the adapter table: ring adapter index a selects table[a] (NULL entries are skipped, as a
+ * missing FFI handle is in prepare_lora_for_ring, crates/adapteros-lora-mlx-ffi/src/
+ * backend.rs:398-428). All adapters bound for one module must share its rank. Returns 0 / -1. */
+int aoship_layer_set_adapters(aoship_layer_t *layer, aoship_lora_adapter_t *const *table, int n);
+
+/* Size the device workspace for up to max_tokens tokens per call. Returns 0 / -1. */
+int aoship_layer_reserve(aoship_layer_t *layer, int max_tokens);
+
+/* Stream (hipStream_t) for this layer's launches; NULL = null stream. Returns 0 / -1. */
+int aoship_layer_set_stream(aoship_layer_t *layer, void *stream);
+
+/* Per-kernel timing with HIP events on the layer's stream (FusedKernels::get_metrics,
+ * crates/adapteros-lora-kernel-api/src/lib.rs:559). enable != 0 turns it on and clears totals. */
+int aoship_layer_set_profiling(aoship_layer_t *layer, int enable);
+
+/* Kernel statistics slot idx: name, accumulated milliseconds, launches. Synchronises the
+ * stream. Returns the number of slots, or -1. */
+int aoship_layer_kernel_stats(aoship_layer_t *layer, int idx, const char **name,
+                              double *total_ms, int64_t *launches);
+
+void aoship_layer_free(aoship_layer_t *layer);
+
+/* SwiGLU MLP with LoRA on gate/up/down (mlx_cpp_wrapper_real.cpp:3509-3527):
+ *   gate = x Wg^T + dg(x); up = x Wu^T + du(x); h = gate * sigmoid(gate) * up;
+ *   y = h Wd^T + dd(h)
+ * where d(.) sums, over each token's ring slots with q > 0 and a bound adapter,
+ * (. A^T) B^T * (scale * q / 32767).
+ *   x : device bf16[T * hidden];  rings : device aoship_ring_t[T] (one per token);
+ *   y : device bf16[T * hidden]. Asynchronous. Returns 0 / -1. */
+int aoship_mlp_forward(aoship_layer_t *layer, const aoship_bf16_t *x, int T,
+                       const aoship_ring_t *rings, aoship_bf16_t *y);
+
+/* One projection with LoRA (mlx_cpp_wrapper_real.cpp:3445-3455 for q/k/v, 3499-3501 for o).
+ *   x : device bf16[T * in];  y : device bf16[T * out]. Returns 0 / -1. */
+int aoship_proj_forward(aoship_layer_t *layer, const char *module, const aoship_bf16_t *x,
+                        int T, const aoship_ring_t *rings, aoship_bf16_t *y);
+
+/* q/k/v projections of one input in one pass (mlx_cpp_wrapper_real.cpp:3445-3455). */
+int aoship_qkv_forward(aoship_layer_t *layer, const aoship_bf16_t *x, int T,
+                       const aoship_ring_t *rings, aoship_bf16_t *q, aoship_bf16_t *k,
+                       aoship_bf16_t *v);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

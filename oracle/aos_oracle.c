@@ -1,0 +1,543 @@
+/*
+ * aos_oracle.c — CPU restatement of adapterOS's router + int4 LoRA layer (test infrastructure).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never the product. See aos_oracle.h
+ * for the reference file:line each function follows and for how each one is pinned.
+ *
+ * Built with -O2 -ffp-contract=off and without fast-math, so every float operation below is
+ * the single IEEE operation written in the source (the reference forbids fast-math:
+ * crates/adapteros-lora-kernel-api/src/attestation.rs:211-219).
+ */
+#include "aos_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_MAX_K 8                 /* crates/adapteros-core/src/defaults.rs:37 */
+#define ORC_DEFAULT_EPS 0.02f       /* crates/adapteros-core/src/defaults.rs:24 */
+#define ORC_Q15_DENOM 32767.0f      /* crates/adapteros-lora-router/src/quantization.rs:22 */
+#define ORC_Q15_MAX 32767
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+/* The router's float64 exp: the C library's exp (Rust's f64::exp on the host platform), unless a
+ * test installs another implementation to show the outputs do not depend on the choice. */
+static double (*g_exp)(double) = exp;
+void orc_set_exp(double (*f)(double)) { g_exp = f ? f : exp; }
+double orc_exp(double x) { return g_exp(x); }
+
+static uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+static float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Router                                                                                     */
+/* ------------------------------------------------------------------------------------------ */
+
+/* f32::total_cmp key (core::f32::total_cmp): bits ^ (((bits as i32) >> 31) as u32 >> 1),
+ * compared as i32. Returned here biased to an unsigned key that sorts DESCENDING by score when
+ * compared ascending: key = 0x7fffffff - signed_key (as offset u32). */
+uint64_t orc_total_cmp_key_desc(float x) {
+  int32_t b = (int32_t)f32_bits(x);
+  int32_t t = b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+  /* ascending-comparable unsigned form of t, then inverted for descending */
+  uint32_t asc = (uint32_t)t ^ 0x80000000u;
+  return (uint64_t)(0xffffffffu - asc);
+}
+
+/* quantization.rs:172-175: (gate * 32767.0).round() as i32, clamped to [0, 32767].
+ * f32::round rounds half away from zero (== C roundf); `as i32` saturates, NaN -> 0. */
+int16_t orc_quantize_gate(float gate) {
+  float s = gate * ORC_Q15_DENOM;
+  float r = roundf(s);
+  int32_t v;
+  if (r != r) v = 0;
+  else if (r >= 2147483647.0f) v = 2147483647;
+  else if (r <= -2147483648.0f) v = (int32_t)0x80000000u;
+  else v = (int32_t)r;
+  if (v < 0) v = 0;
+  if (v > ORC_Q15_MAX) v = ORC_Q15_MAX;
+  return (int16_t)v;
+}
+
+typedef struct {
+  int idx;
+  float score;
+  uint64_t stable_id;
+} orc_cand_t;
+
+/* router.rs:234-264 comparator: score DESC (total_cmp), stable_id ASC; Rust's sort_by is stable,
+ * so remaining ties keep index order — made explicit here as the last key. */
+static int cmp_scored(const orc_cand_t *a, const orc_cand_t *b) {
+  uint64_t ka = orc_total_cmp_key_desc(a->score), kb = orc_total_cmp_key_desc(b->score);
+  if (ka != kb) return ka < kb ? -1 : 1;
+  if (a->stable_id != b->stable_id) return a->stable_id < b->stable_id ? -1 : 1;
+  if (a->idx != b->idx) return a->idx < b->idx ? -1 : 1;
+  return 0;
+}
+
+typedef struct {
+  int idx;
+  float raw;
+  int16_t q;
+  uint64_t stable_id;
+} orc_final_t;
+
+/* router.rs:1310-1325: gate_q15 DESC, raw_score DESC (total_cmp), stable_id ASC, adapter_idx ASC. */
+static int cmp_final(const orc_final_t *a, const orc_final_t *b) {
+  if (a->q != b->q) return a->q > b->q ? -1 : 1;
+  uint64_t ka = orc_total_cmp_key_desc(a->raw), kb = orc_total_cmp_key_desc(b->raw);
+  if (ka != kb) return ka < kb ? -1 : 1;
+  if (a->stable_id != b->stable_id) return a->stable_id < b->stable_id ? -1 : 1;
+  if (a->idx != b->idx) return a->idx < b->idx ? -1 : 1;
+  return 0;
+}
+
+/* Stable insertion sort (n is small; order is total so stability is moot). */
+static void sort_scored(orc_cand_t *c, int n) {
+  for (int i = 1; i < n; ++i) {
+    orc_cand_t v = c[i];
+    int j = i - 1;
+    while (j >= 0 && cmp_scored(&c[j], &v) > 0) {
+      c[j + 1] = c[j];
+      --j;
+    }
+    c[j + 1] = v;
+  }
+}
+
+static void sort_final(orc_final_t *c, int n) {
+  for (int i = 1; i < n; ++i) {
+    orc_final_t v = c[i];
+    int j = i - 1;
+    while (j >= 0 && cmp_final(&c[j], &v) > 0) {
+      c[j + 1] = c[j];
+      --j;
+    }
+    c[j + 1] = v;
+  }
+}
+
+/* router.rs:146-166 */
+static float sanitize_eps(float eps) {
+  if (!isfinite(eps)) return ORC_DEFAULT_EPS;
+  if (!(eps >= 0.0f && eps <= 1.0f)) return ORC_DEFAULT_EPS;
+  return eps;
+}
+
+/* router.rs:171-187 */
+static float sanitize_tau(float tau) {
+  if (!isfinite(tau)) return 1.0f;
+  if (tau <= 0.0f) return 1.0f;
+  return tau;
+}
+
+/* Rust f64::max (IEEE maxNum: a NaN operand yields the other operand). */
+static double rust_f64_max(double a, double b) {
+  if (a != a) return b;
+  if (b != b) return a;
+  return a > b ? a : (b > a ? b : a);
+}
+
+/* Rust f32::max */
+static float rust_f32_max(float a, float b) {
+  if (a != a) return b;
+  if (b != b) return a;
+  return a > b ? a : (b > a ? b : a);
+}
+
+int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
+                  int k, float tau, float eps, float routing_bias, uint16_t idx_out[8],
+                  int16_t q15_out[8]) {
+  for (int i = 0; i < 8; ++i) {
+    idx_out[i] = 0;
+    q15_out[i] = 0;
+  }
+  /* Router::new rejects k > MAX_K (router.rs:769-777); sanitize_k lifts 0 to 1 (:127-142). */
+  if (k > ORC_MAX_K || n < 0) return -1;
+  if (k < 1) k = 1;
+  tau = sanitize_tau(tau);
+  eps = sanitize_eps(eps);
+  /* set_routing_bias keeps the default 1.0 for a non-finite or non-positive bias (:556-562). */
+  if (!(isfinite(routing_bias) && routing_bias > 0.0f)) routing_bias = 1.0f;
+
+  /* validate_router_inputs (router.rs:611-625): every prior finite, masked or not. */
+  for (int i = 0; i < n; ++i)
+    if (!isfinite(priors[i])) return -1;
+
+  orc_cand_t *c = (orc_cand_t *)malloc(sizeof(orc_cand_t) * (size_t)(n > 0 ? n : 1));
+  int m = 0;
+  for (int i = 0; i < n; ++i) {
+    if (allowed && !allowed[i]) continue;
+    /* router.rs:1664-1676 with empty features (feature score 0.0, :985-988), no orthogonal
+     * penalty (0.0, :1490-1501), not MoE, version_weight 1.0 (types.rs:656). */
+    float sim = (priors[i] + 0.0f) - 0.0f;
+    float score = sim * routing_bias; /* scoring.rs:35-37 */
+    score *= 1.0f;                    /* clamp(version_weight, 0, 2) with the default 1.0 */
+    if (!isfinite(score)) {
+      free(c);
+      return -1;
+    }
+    c[m].idx = i;
+    c[m].score = score;
+    c[m].stable_id = stable_id ? stable_id[i] : 0;
+    ++m;
+  }
+  if (m == 0) {
+    free(c);
+    return 0;
+  }
+  sort_scored(c, m);
+  int kk = k < m ? k : m;
+
+  /* deterministic_softmax (router.rs:1340-1411). tau was sanitized to > 0 at construction, so
+   * the tau == 0 one-hot branch is unreachable through the router. */
+  double mx = -INFINITY;
+  for (int i = 0; i < kk; ++i) mx = rust_f64_max(mx, (double)c[i].score);
+  double e[ORC_MAX_K];
+  double sum = 0.0, comp = 0.0;
+  for (int i = 0; i < kk; ++i) {
+    double ex = orc_exp(((double)c[i].score - mx) / (double)tau);
+    double y = ex - comp;
+    double t = sum + y;
+    comp = (t - sum) - y;
+    sum = t;
+    e[i] = ex;
+  }
+  float g[ORC_MAX_K];
+  if (sum == 0.0) {
+    float u = 1.0f / (float)kk;
+    for (int i = 0; i < kk; ++i) g[i] = u;
+  } else {
+    for (int i = 0; i < kk; ++i) g[i] = (float)(e[i] / sum);
+  }
+  /* entropy floor (router.rs:1820-1827) */
+  float min_gate = eps / (float)kk;
+  for (int i = 0; i < kk; ++i) g[i] = rust_f32_max(g[i], min_gate);
+  /* renormalize (router.rs:1830-1842): f32 sum in order */
+  float s = 0.0f;
+  for (int i = 0; i < kk; ++i) s += g[i];
+  if (s <= 0.0f) {
+    free(c);
+    return 0;
+  }
+  for (int i = 0; i < kk; ++i) g[i] /= s;
+
+  orc_final_t f[ORC_MAX_K];
+  for (int i = 0; i < kk; ++i) {
+    f[i].idx = c[i].idx;
+    f[i].raw = c[i].score;
+    f[i].q = orc_quantize_gate(g[i]);
+    f[i].stable_id = c[i].stable_id;
+  }
+  free(c);
+  sort_final(f, kk);
+  for (int i = 0; i < kk; ++i) {
+    idx_out[i] = (uint16_t)f[i].idx;
+    q15_out[i] = f[i].q;
+  }
+  return kk;
+}
+
+int orc_route_batch(const float *priors, int T, int n, const uint64_t *stable_id,
+                    const uint8_t *allowed, int k, float tau, float eps, float routing_bias,
+                    orc_ring_t *rings, int *bad_token) {
+  int bad = -1;
+  for (int t = 0; t < T; ++t) {
+    orc_ring_t *r = &rings[t];
+    memset(r, 0, sizeof(*r));
+    int kk = orc_route_one(priors + (size_t)t * n, n, stable_id, allowed, k, tau, eps,
+                           routing_bias, r->adapter_indices, r->gates_q15);
+    if (kk < 0) {
+      if (bad < 0) bad = t;
+      continue;
+    }
+    r->top_k = (uint32_t)kk;
+    r->current_pos = (uint32_t)t;
+  }
+  if (bad_token) *bad_token = bad;
+  return bad < 0 ? 0 : -1;
+}
+
+void orc_priors(const float *features, const float *router_w, int T, int n, int d, float *priors) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int t = 0; t < T; ++t) {
+    for (int a = 0; a < n; ++a) {
+      const float *w = router_w + (size_t)a * d;
+      const float *f = features + (size_t)t * d;
+      float p[64];
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int i = l; i < d; i += 64) acc = fmaf(w[i], f[i], acc);
+        p[l] = acc;
+      }
+      for (int o = 32; o >= 1; o >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ o];
+        memcpy(p, q, sizeof(p));
+      }
+      priors[(size_t)t * n + a] = p[0];
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Number formats                                                                             */
+/* ------------------------------------------------------------------------------------------ */
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) << 31;
+  uint32_t exp = (h >> 10) & 0x1f;
+  uint32_t man = h & 0x3ff;
+  if (exp == 0) {
+    /* zero / subnormal: man * 2^-24 exactly */
+    float v = (float)man * 5.9604644775390625e-08f;
+    return sign ? -v : v;
+  }
+  if (exp == 31) return bits_f32(sign | 0x7f800000u | (man << 13));
+  return bits_f32(sign | ((exp + 112) << 23) | (man << 13));
+}
+
+float orc_bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u = f32_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u = f32_bits(f);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to >= 65520 -> inf */
+  if (a < 0x38800000u) {                                  /* below 2^-14: subnormal */
+    float v = bits_f32(a) * 16777216.0f;                  /* exact scaling to units of 2^-24 */
+    uint32_t q = (uint32_t)v;
+    float rem = v - (float)q;
+    if (rem > 0.5f || (rem == 0.5f && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t e = (a >> 23) - 112;
+  uint32_t m = a & 0x7fffffu;
+  uint32_t hm = m >> 13;
+  uint32_t rest = m & 0x1fffu;
+  uint32_t h = (e << 10) | hm;
+  if (rest > 0x1000u || (rest == 0x1000u && (hm & 1u))) ++h;
+  return (uint16_t)(sign | h);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* int4 base weights                                                                          */
+/* ------------------------------------------------------------------------------------------ */
+
+/* MLX affine dequant: w[o,i] = scale[o, i/64] * q + bias[o, i/64],
+ * q = (wp[o, i/8] >> (4 * (i % 8))) & 0xF. Evaluated in float32. */
+static inline float dq(const uint32_t *wrow, const uint16_t *srow, const uint16_t *brow, int i) {
+  uint32_t q = (wrow[i >> 3] >> (4 * (i & 7))) & 0xFu;
+  float s = orc_f16_to_f32(srow[i >> 6]);
+  float b = orc_f16_to_f32(brow[i >> 6]);
+  return s * (float)q + b;
+}
+
+void orc_dequant_q4(const uint32_t *wp, const uint16_t *scales, const uint16_t *biases, int out,
+                    int in, float *w) {
+  int gpr = in / 64;
+#pragma omp parallel for schedule(static)
+  for (int o = 0; o < out; ++o) {
+    const uint32_t *wr = wp + (size_t)o * (in / 8);
+    const uint16_t *sr = scales + (size_t)o * gpr;
+    const uint16_t *br = biases + (size_t)o * gpr;
+    for (int i = 0; i < in; ++i) w[(size_t)o * in + i] = dq(wr, sr, br, i);
+  }
+}
+
+static void linear_row(const float *x, const uint32_t *wr, const uint16_t *sr,
+                       const uint16_t *br, int in, float *yo, int mode) {
+  const int groups = in / 64;
+  if (mode == 0) {
+    float acc = 0.0f;
+    for (int g = 0; g < groups; ++g) {
+      const float s = orc_f16_to_f32(sr[g]), b = orc_f16_to_f32(br[g]);
+      for (int i = g * 64; i < g * 64 + 64; ++i) {
+        uint32_t q = (wr[i >> 3] >> (4 * (i & 7))) & 0xFu;
+        acc += x[i] * (s * (float)q + b);
+      }
+    }
+    *yo = acc;
+  } else {
+    double acc = 0.0;
+    for (int g = 0; g < groups; ++g) {
+      const double s = orc_f16_to_f32(sr[g]), b = orc_f16_to_f32(br[g]);
+      for (int i = g * 64; i < g * 64 + 64; ++i) {
+        uint32_t q = (wr[i >> 3] >> (4 * (i & 7))) & 0xFu;
+        acc += (double)x[i] * (s * (double)q + b);
+      }
+    }
+    *yo = (float)acc;
+  }
+}
+
+void orc_linear_q4(const float *x, int T, const uint32_t *wp, const uint16_t *scales,
+                   const uint16_t *biases, int out, int in, float *y, int mode) {
+  int gpr = in / 64;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int t = 0; t < T; ++t)
+    for (int o = 0; o < out; ++o)
+      linear_row(x + (size_t)t * in, wp + (size_t)o * (in / 8), scales + (size_t)o * gpr,
+                 biases + (size_t)o * gpr, in, y + (size_t)t * out + o, mode);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* LoRA                                                                                       */
+/* ------------------------------------------------------------------------------------------ */
+
+/* mlx_cpp_wrapper_real.cpp:3394-3419: lora_out = (x @ A^T) @ B^T, times (scale * blend); the
+ * first active adapter initialises delta, later ones are added in ring order. */
+void orc_lora_delta(const float *x, const float *A, const float *B, int r, int in, int out,
+                    float coef, float *delta, int first, int mode) {
+  float xa[256];
+  double xad[256];
+  for (int j = 0; j < r; ++j) {
+    const float *a = A + (size_t)j * in;
+    if (mode == 0) {
+      float acc = 0.0f;
+      for (int i = 0; i < in; ++i) acc += x[i] * a[i];
+      xa[j] = acc;
+    } else {
+      double acc = 0.0;
+      for (int i = 0; i < in; ++i) acc += (double)x[i] * (double)a[i];
+      xad[j] = acc;
+    }
+  }
+  for (int o = 0; o < out; ++o) {
+    const float *b = B + (size_t)o * r;
+    float v;
+    if (mode == 0) {
+      float acc = 0.0f;
+      for (int j = 0; j < r; ++j) acc += xa[j] * b[j];
+      v = acc * coef;
+    } else {
+      double acc = 0.0;
+      for (int j = 0; j < r; ++j) acc += xad[j] * (double)b[j];
+      v = (float)(acc * (double)coef);
+    }
+    delta[o] = first ? v : delta[o] + v;
+  }
+}
+
+/* liquid.rs:163-257: output.fill(0); for each adapter with coeff != 0: rank_buf = A x (f32,
+ * sequential), output[o] += coeff * (B[o,:] . rank_buf) * (alpha / rank). */
+int orc_liquid_blend(int n, const float *const *A, const float *const *B, const int *rank,
+                     const float *alpha, const float *coef, const float *x, int in, float *out,
+                     int out_len) {
+  if (n <= 0 || n > 3) return -1; /* LIQUID_MAX_ADAPTERS = 3 (liquid.rs:12) */
+  for (int o = 0; o < out_len; ++o) out[o] = 0.0f;
+  for (int a = 0; a < n; ++a) {
+    if (coef[a] == 0.0f) continue;
+    int r = rank[a];
+    float scaling = alpha[a] / (float)r;
+    float rb[256];
+    for (int j = 0; j < r; ++j) {
+      float acc = 0.0f;
+      for (int c = 0; c < in; ++c) acc += A[a][(size_t)j * in + c] * x[c];
+      rb[j] = acc;
+    }
+    for (int o = 0; o < out_len; ++o) {
+      float acc = 0.0f;
+      for (int j = 0; j < r; ++j) acc += B[a][(size_t)o * r + j] * rb[j];
+      out[o] += coef[a] * acc * scaling;
+    }
+  }
+  return 0;
+}
+
+/* Apply the ring's active adapters to base output y[out] for one token (backend.rs:398-428 then
+ * apply_lora). */
+static void add_lora_for_ring(const float *x, int in, int out, const orc_lora_mod_t *mods,
+                              int n_modules, int m, const float *scale, int n_adapters, int rank,
+                              const orc_ring_t *ring, float *y, int mode, float *scratch) {
+  int have = 0;
+  int kk = ring->top_k > 8 ? 8 : (int)ring->top_k;
+  for (int s = 0; s < kk; ++s) {
+    int16_t q = ring->gates_q15[s];
+    int a = ring->adapter_indices[s];
+    if (q <= 0) continue;
+    if (a >= n_adapters) continue;
+    const orc_lora_mod_t *md = &mods[(size_t)a * n_modules + m];
+    if (!md->A || !md->B) continue;
+    float blend = (float)q / ORC_Q15_DENOM;
+    float coef = scale[a] * blend;
+    orc_lora_delta(x, md->A, md->B, rank, in, out, coef, scratch, !have, mode);
+    have = 1;
+  }
+  if (have)
+    for (int o = 0; o < out; ++o) y[o] = y[o] + scratch[o];
+}
+
+static float silu_mul(float g, float u, int mode) {
+  if (mode == 0) {
+    float sg = 1.0f / (1.0f + expf(-g));
+    return (g * sg) * u;
+  }
+  double gd = g, sg = 1.0 / (1.0 + exp(-gd));
+  return (float)((gd * sg) * (double)u);
+}
+
+void orc_proj_forward(const float *x, int T, int in, int out, const orc_q4_t *w,
+                      const orc_lora_mod_t *mods, int n_modules, int m, const float *scale,
+                      int n_adapters, int rank, const orc_ring_t *rings, float *y, int mode) {
+  orc_linear_q4(x, T, w->wp, w->scales, w->biases, out, in, y, mode);
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < T; ++t) {
+    float *scr = (float *)malloc(sizeof(float) * (size_t)out);
+    add_lora_for_ring(x + (size_t)t * in, in, out, mods, n_modules, m, scale, n_adapters, rank,
+                      &rings[t], y + (size_t)t * out, mode, scr);
+    free(scr);
+  }
+}
+
+void orc_mlp_forward(const float *x, int T, int H, int I, const orc_q4_t *gate,
+                     const orc_q4_t *up, const orc_q4_t *down, const orc_lora_mod_t *mods,
+                     const float *scale, int n_adapters, int rank, const orc_ring_t *rings,
+                     float *y, int mode, float *h_out) {
+  float *g = (float *)malloc(sizeof(float) * (size_t)T * I);
+  float *u = (float *)malloc(sizeof(float) * (size_t)T * I);
+  float *h = h_out ? h_out : (float *)malloc(sizeof(float) * (size_t)T * I);
+  orc_proj_forward(x, T, H, I, gate, mods, 3, 0, scale, n_adapters, rank, rings, g, mode);
+  orc_proj_forward(x, T, H, I, up, mods, 3, 1, scale, n_adapters, rank, rings, u, mode);
+  for (size_t i = 0; i < (size_t)T * I; ++i) h[i] = silu_mul(g[i], u[i], mode);
+  orc_proj_forward(h, T, I, H, down, mods, 3, 2, scale, n_adapters, rank, rings, y, mode);
+  free(g);
+  free(u);
+  if (!h_out) free(h);
+}

@@ -1,0 +1,262 @@
+"""ctypes wrapper of the CPU oracle (oracle/liborc.so).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP path. Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg use it. See aos_oracle.h for the reference file:line each function
+restates and how each is pinned.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liborc.so"
+
+RING_DTYPE = np.dtype(
+    [("top_k", "<u4"), ("current_pos", "<u4"), ("adapter_indices", "<u2", (8,)), ("gates_q15", "<i2", (8,))]
+)
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+class _Q4(C.Structure):
+    _fields_ = [("wp", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p)]
+
+
+class _Mod(C.Structure):
+    _fields_ = [("A", C.c_void_p), ("B", C.c_void_p)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        P = C.c_void_p
+        L.orc_quantize_gate.restype = C.c_int16
+        L.orc_quantize_gate.argtypes = [C.c_float]
+        L.orc_total_cmp_key_desc.restype = C.c_uint64
+        L.orc_total_cmp_key_desc.argtypes = [C.c_float]
+        L.orc_route_one.restype = C.c_int
+        L.orc_route_one.argtypes = [P, C.c_int, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
+        L.orc_route_batch.restype = C.c_int
+        L.orc_route_batch.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
+        L.orc_priors.restype = None
+        L.orc_priors.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P]
+        L.orc_dequant_q4.restype = None
+        L.orc_dequant_q4.argtypes = [P, P, P, C.c_int, C.c_int, P]
+        L.orc_linear_q4.restype = None
+        L.orc_linear_q4.argtypes = [P, C.c_int, P, P, P, C.c_int, C.c_int, P, C.c_int]
+        L.orc_lora_delta.restype = None
+        L.orc_lora_delta.argtypes = [P, P, P, C.c_int, C.c_int, C.c_int, C.c_float, P, C.c_int, C.c_int]
+        L.orc_liquid_blend.restype = C.c_int
+        L.orc_liquid_blend.argtypes = [C.c_int, P, P, P, P, P, P, C.c_int, P, C.c_int]
+        L.orc_mlp_forward.restype = None
+        L.orc_mlp_forward.argtypes = [P, C.c_int, C.c_int, C.c_int, P, P, P, P, P, C.c_int, C.c_int, P, P,
+                                      C.c_int, P]
+        L.orc_proj_forward.restype = None
+        L.orc_proj_forward.argtypes = [P, C.c_int, C.c_int, C.c_int, P, P, C.c_int, C.c_int, P, C.c_int,
+                                       C.c_int, P, P, C.c_int]
+        L.orc_exp.restype = C.c_double
+        L.orc_exp.argtypes = [C.c_double]
+        L.orc_set_exp.restype = None
+        L.orc_set_exp.argtypes = [C.c_void_p]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_num_threads.restype = C.c_int
+        L.orc_set_num_threads.argtypes = [C.c_int]
+        _lib = L
+    return _lib
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def quantize_gate(g: float) -> int:
+    return int(lib().orc_quantize_gate(float(g)))
+
+
+def route_one(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None, allowed=None):
+    """Returns (indices, gates) lists, or raises ValueError for the reference's error cases."""
+    p = _c(priors, np.float32)
+    n = p.shape[0]
+    sid = None if stable_ids is None else _c(stable_ids, np.uint64)
+    al = None if allowed is None else _c(allowed, np.uint8)
+    idx = np.zeros(8, np.uint16)
+    q = np.zeros(8, np.int16)
+    kk = lib().orc_route_one(p.ctypes.data, n, sid.ctypes.data if sid is not None else None,
+                             al.ctypes.data if al is not None else None, k, tau, eps, routing_bias,
+                             idx.ctypes.data, q.ctypes.data)
+    if kk < 0:
+        raise ValueError("routing error (non-finite prior/score or k > 8)")
+    return idx[:kk].tolist(), q[:kk].tolist()
+
+
+def route_batch(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None, allowed=None):
+    """Rings for every token (a token whose routing fails gets an all-zero ring)."""
+    p = _c(priors, np.float32)
+    T, n = p.shape
+    sid = None if stable_ids is None else _c(stable_ids, np.uint64)
+    al = None if allowed is None else _c(allowed, np.uint8)
+    rings = np.zeros(T, RING_DTYPE)
+    bad = C.c_int(-1)
+    lib().orc_route_batch(p.ctypes.data, T, n, sid.ctypes.data if sid is not None else None,
+                          al.ctypes.data if al is not None else None, k, tau, eps, routing_bias,
+                          rings.ctypes.data, C.byref(bad))
+    return rings
+
+
+def priors(features, router_w):
+    f = _c(features, np.float32)
+    w = _c(router_w, np.float32)
+    T, d = f.shape
+    n = w.shape[0]
+    out = np.empty((T, n), np.float32)
+    lib().orc_priors(f.ctypes.data, w.ctypes.data, T, n, d, out.ctypes.data)
+    return out
+
+
+def dequant(packed, scales, biases):
+    wp = _c(packed, np.uint32)
+    out, w = wp.shape
+    s = np.ascontiguousarray(scales).view(np.uint16)
+    b = np.ascontiguousarray(biases).view(np.uint16)
+    dst = np.empty((out, w * 8), np.float32)
+    lib().orc_dequant_q4(wp.ctypes.data, s.ctypes.data, b.ctypes.data, out, w * 8, dst.ctypes.data)
+    return dst
+
+
+def linear_q4(x, packed, scales, biases, mode=0):
+    x = _c(x, np.float32)
+    wp = _c(packed, np.uint32)
+    out, w = wp.shape
+    s = np.ascontiguousarray(scales).view(np.uint16)
+    b = np.ascontiguousarray(biases).view(np.uint16)
+    y = np.empty((x.shape[0], out), np.float32)
+    lib().orc_linear_q4(x.ctypes.data, x.shape[0], wp.ctypes.data, s.ctypes.data, b.ctypes.data, out, w * 8,
+                        y.ctypes.data, mode)
+    return y
+
+
+def lora_delta(x, A, B, coef, mode=0):
+    x = _c(x, np.float32)
+    A = _c(A, np.float32)
+    B = _c(B, np.float32)
+    r, din = A.shape
+    dout = B.shape[0]
+    d = np.zeros(dout, np.float32)
+    lib().orc_lora_delta(x.ctypes.data, A.ctypes.data, B.ctypes.data, r, din, dout, coef, d.ctypes.data, 1, mode)
+    return d
+
+
+def liquid_blend(As, Bs, ranks, alphas, coefs, x, out_len):
+    n = len(As)
+    As = [_c(a, np.float32) for a in As]
+    Bs = [_c(b, np.float32) for b in Bs]
+    Ap = (C.c_void_p * n)(*[a.ctypes.data for a in As])
+    Bp = (C.c_void_p * n)(*[b.ctypes.data for b in Bs])
+    rk = _c(ranks, np.int32)
+    al = _c(alphas, np.float32)
+    cf = _c(coefs, np.float32)
+    x = _c(x, np.float32)
+    out = np.zeros(out_len, np.float32)
+    rc = lib().orc_liquid_blend(n, Ap, Bp, rk.ctypes.data, al.ctypes.data, cf.ctypes.data, x.ctypes.data,
+                                x.shape[0], out.ctypes.data, out_len)
+    if rc != 0:
+        raise ValueError("liquid blend rejected")
+    return out
+
+
+class _Keep:
+    """Keeps numpy buffers alive while C pointers to them are in use."""
+
+    def __init__(self):
+        self.items = []
+
+    def __call__(self, a):
+        self.items.append(a)
+        return a
+
+
+def _q4(keep, w):
+    packed, scales, biases = w
+    p = keep(_c(packed, np.uint32))
+    s = keep(np.ascontiguousarray(scales).view(np.uint16))
+    b = keep(np.ascontiguousarray(biases).view(np.uint16))
+    return _Q4(p.ctypes.data, s.ctypes.data, b.ctypes.data)
+
+
+def _mods(keep, lora, n_adapters, modules):
+    """lora[a][module] = (A, B) or None -> flat [n_adapters * n_modules] array."""
+    arr = (_Mod * (n_adapters * len(modules)))()
+    for a in range(n_adapters):
+        for mi, m in enumerate(modules):
+            ab = lora[a].get(m) if lora[a] is not None else None
+            if ab is None:
+                continue
+            A = keep(_c(ab[0], np.float32))
+            B = keep(_c(ab[1], np.float32))
+            arr[a * len(modules) + mi] = _Mod(A.ctypes.data, B.ctypes.data)
+    return arr
+
+
+def mlp_forward(x, gate, up, down, lora, scales, rank, rings, mode=0, return_h=False):
+    """SwiGLU MLP with per-token rings; lora[a] = {"gate_proj": (A, B), ...}."""
+    keep = _Keep()
+    x = keep(_c(x, np.float32))
+    T, H = x.shape
+    I = gate[0].shape[0]
+    g, u, d = _q4(keep, gate), _q4(keep, up), _q4(keep, down)
+    n = len(lora)
+    mods = _mods(keep, lora, n, ("gate_proj", "up_proj", "down_proj"))
+    sc = keep(_c(scales, np.float32))
+    rg = keep(np.ascontiguousarray(rings, dtype=RING_DTYPE))
+    y = np.empty((T, H), np.float32)
+    h = np.empty((T, I), np.float32) if return_h else None
+    lib().orc_mlp_forward(x.ctypes.data, T, H, I, C.byref(g), C.byref(u), C.byref(d), mods, sc.ctypes.data, n,
+                          rank, rg.ctypes.data, y.ctypes.data, mode, h.ctypes.data if h is not None else None)
+    return (y, h) if return_h else y
+
+
+def proj_forward(x, w, module, modules, lora, scales, rank, rings, mode=0):
+    keep = _Keep()
+    x = keep(_c(x, np.float32))
+    T, din = x.shape
+    dout = w[0].shape[0]
+    q = _q4(keep, w)
+    n = len(lora)
+    mods = _mods(keep, lora, n, modules)
+    sc = keep(_c(scales, np.float32))
+    rg = keep(np.ascontiguousarray(rings, dtype=RING_DTYPE))
+    y = np.empty((T, dout), np.float32)
+    lib().orc_proj_forward(x.ctypes.data, T, din, dout, C.byref(q), mods, len(modules), modules.index(module),
+                           sc.ctypes.data, n, rank, rg.ctypes.data, y.ctypes.data, mode)
+    return y
+
+
+def exp(x: float) -> float:
+    return lib().orc_exp(x)
+
+
+def set_exp(fn_ptr) -> None:
+    """Install a C function pointer (double -> double) as the router's exp; None restores libm."""
+    lib().orc_set_exp(fn_ptr)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_num_threads(n)
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()

@@ -1,0 +1,81 @@
+"""Shared builders for the parity tests: synthetic layers on the GPU and their oracle twins."""
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+
+import workloads as W
+
+# Float outputs must agree with the CPU oracle to 2e-2 relative (bf16): an element passes when
+# |gpu - ref| <= 2e-2 * (|ref| + rms(ref)); the rms term keeps outputs near zero from demanding a
+# relative precision no bf16 result has.
+REL_TOL = 2e-2
+
+
+def tol_ratio(y, ref) -> float:
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    return float(np.max(np.abs(y - ref) / (np.abs(ref) + rms)))
+
+
+@functools.lru_cache(maxsize=4)
+def base(cid: int):
+    cfg = W.CONFIGS[cid]
+    return {m: W.base_weights(cfg, m) for m in cfg.modules}
+
+
+@functools.lru_cache(maxsize=4)
+def lora(cid: int):
+    cfg = W.CONFIGS[cid]
+    return [{m: W.lora_weights(cfg, a, m) for m in cfg.modules} for a in range(cfg.n_adapters)]
+
+
+def rings_for(cid: int, T: int):
+    """Oracle rings for T tokens of config cid (and the priors that produced them)."""
+    import oracle
+
+    cfg = W.CONFIGS[cid]
+    if cfg.routing == "features":
+        f, w = W.router_inputs(cfg, T)
+        pri = oracle.priors(f, w)
+    else:
+        pri = W.priors(cfg, T)
+    sid = np.arange(cfg.n_adapters, dtype=np.uint64)
+    rings = oracle.route_batch(pri, cfg.k, cfg.tau, cfg.eps, 1.0, sid)
+    return rings, pri
+
+
+def gpu_layer(aoship, cid: int):
+    cfg = W.CONFIGS[cid]
+    layer = aoship.Layer(0)
+    for m, (p, s, b) in base(cid).items():
+        layer.set_base(m, p, s, b)
+    ads = []
+    for a, mods in enumerate(lora(cid)):
+        ad = aoship.LoraAdapter(a, 1, W.lora_scale(cfg))
+        for m, (A, B) in mods.items():
+            ad.set_module(0, m, A, B)
+        ads.append(ad)
+    layer.set_adapters(ads)
+    return layer, ads
+
+
+def oracle_mlp(cid: int, x, rings, mode=0):
+    import oracle
+
+    cfg = W.CONFIGS[cid]
+    bw = base(cid)
+    scales = np.full(cfg.n_adapters, W.lora_scale(cfg), np.float32)
+    return oracle.mlp_forward(x, bw["gate_proj"], bw["up_proj"], bw["down_proj"], lora(cid), scales, cfg.rank,
+                              rings, mode)
+
+
+def oracle_proj(cid: int, module: str, x, rings, mode=0):
+    import oracle
+
+    cfg = W.CONFIGS[cid]
+    scales = np.full(cfg.n_adapters, W.lora_scale(cfg), np.float32)
+    return oracle.proj_forward(x, base(cid)[module], module, list(cfg.modules), lora(cid), scales, cfg.rank, rings,
+                               mode)
