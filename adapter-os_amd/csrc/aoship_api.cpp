@@ -262,7 +262,8 @@ static int route_common(aoship_router_t *r, const float *features, const float *
   } else if (!priors_in) {
     return set_err("aoship_route: null priors");
   }
-  int e = aos_launch_route(&p, r->stream);
+  aos_launch_ctx ctx = {r->stream, nullptr, nullptr};
+  int e = aos_launch_route(&p, &ctx);
   if (e != 0) return set_err(std::string("route launch: ") + hipGetErrorString((hipError_t)e));
   return 0;
 }
@@ -599,24 +600,23 @@ extern "C" int aoship_layer_kernel_stats(aoship_layer_t *l, int idx, const char 
   return KS_COUNT;
 }
 
-struct Timed {
-  aoship_layer *l;
-  int slot;
-  hipEvent_t a = nullptr, b = nullptr;
-  Timed(aoship_layer *l_, int s) : l(l_), slot(s) {
-    if (l->profiling) {
-      a = get_event(l);
-      b = get_event(l);
-      if (a) (void)hipEventRecord(a, l->stream);
-    }
-  }
-  ~Timed() {
-    if (l->profiling && a && b) {
-      (void)hipEventRecord(b, l->stream);
+/* Launch context for one kernel of this layer: with profiling on, the dispatch records a pair
+ * of events at kernel start and end, resolved lazily by aoship_layer_kernel_stats. */
+static aos_launch_ctx launch_ctx(aoship_layer *l, int slot) {
+  aos_launch_ctx c;
+  c.stream = l->stream;
+  c.ev_start = nullptr;
+  c.ev_stop = nullptr;
+  if (l->profiling) {
+    hipEvent_t a = get_event(l), b = get_event(l);
+    if (a && b) {
+      c.ev_start = a;
+      c.ev_stop = b;
       l->pending.push_back({slot, a, b});
     }
   }
-};
+  return c;
+}
 
 /* ---- workspace ---- */
 
@@ -647,16 +647,7 @@ static int ws_reserve(aoship_layer *l, size_t bytes, size_t ctr_words) {
   return 0;
 }
 
-static int gemv_ks(int RB, int G, int W) {
-  int ks = (1024 + RB - 1) / RB;
-  int maxks = G / (2 * W);
-  if (maxks < 1) maxks = 1;
-  if (ks > maxks) ks = maxks;
-  if (ks < 1) ks = 1;
-  return ks;
-}
-
-static int gemv_waves(int G) { return G >= 128 ? 8 : 4; }
+static int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 static int nv_for(int T) {
   if (T <= 1) return 1;
@@ -666,10 +657,27 @@ static int nv_for(int T) {
   return 16;
 }
 
-static int shrink_kc(int G) {
-  int kc = G / 8;
-  return kc < 1 ? 1 : kc;
+/* Decode GEMV geometry: waves per workgroup, K splits across workgroups, dynamic LDS bytes.
+ * About 2048 waves stream the matrix; the x slice of a workgroup (T rows) plus its group sums
+ * must fit the LDS budget; one more workgroup per row block adds the LoRA expand when any bound
+ * adapter has this module. */
+static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g) {
+  const int W = swiglu ? 4 : (G >= 128 ? 8 : 4);
+  int ks = ceil_div(2048, RB * W);
+  int cap = G / W;
+  if (cap < 1) cap = 1;
+  if (ks > cap) ks = cap;
+  while (ks < G && (size_t)T * ceil_div(G, ks) * 136 > AOS_GEMV_LDS_MAX) ++ks;
+  const int NA = swiglu ? 2 : 1;
+  size_t lds_x = 128 + (size_t)T * ceil_div(G, ks) * 136;
+  size_t lds_r = (size_t)W * NA * nv_for(T) * 64 * 4;
+  g.waves = W;
+  g.ks = ks;
+  g.has_expand = lora ? 1 : 0;
+  g.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
 }
+
+static int shrink_kc(int G) { return ceil_div(G, 4 * AOS_SHRINK_GROUPS_PER_WAVE); }
 
 /* Plan of one decode chunk (T <= 32): workspace carve-up and launch parameters. */
 struct MlpPlan {
@@ -698,9 +706,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   uint16_t *Sg = b.take<uint16_t>((size_t)T * umax * (tg.rpad ? tg.rpad : 16));
   uint16_t *Su = b.take<uint16_t>((size_t)T * umax * (tu.rpad ? tu.rpad : 16));
   uint16_t *Sd = b.take<uint16_t>((size_t)T * umax * (td.rpad ? td.rpad : 16));
-  float *xs2 = b.take<float>((size_t)T * 2 * (H / 64));
   uint16_t *h = b.take<uint16_t>((size_t)T * I);
-  float *hs2 = b.take<float>((size_t)T * (I / 32));
 
   /* shrink of x for gate and up */
   aos_shrink_params &s1 = P.sh1;
@@ -715,7 +721,6 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   s1.S[0] = Sg;
   s1.S[1] = Su;
   s1.umax = umax;
-  s1.xs2 = xs2;
   s1.kc = shrink_kc(H / 64);
   int rpm1 = tg.rpad > tu.rpad ? tg.rpad : tu.rpad;
   s1.n_col_tiles = (umax * (rpm1 ? rpm1 : 16) + 31) / 32;
@@ -728,10 +733,8 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g1.w0 = Wg.dev();
   g1.w1 = Wu.dev();
   g1.x = x;
-  g1.xs2 = xs2;
   g1.T = T;
-  g1.waves = 4;
-  g1.ks = gemv_ks(Wg.RB, Wg.G, g1.waves);
+  gemv_geometry(Wg.RB, Wg.G, T, true, tg.rpad > 0 || tu.rpad > 0, g1);
   g1.tab0 = tg;
   g1.tab1 = tu;
   g1.S0 = Sg;
@@ -739,8 +742,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g1.umax = umax;
   g1.rings = rings;
   g1.y = h;
-  g1.ys2 = hs2;
-  g1.part = b.take<float>((size_t)Wg.RB * g1.ks * 2 * nv_for(T) * 64);
+  g1.part = b.take<float>((size_t)Wg.RB * (g1.ks + g1.has_expand) * 2 * nv_for(T) * 64);
   g1.counters = ctrs((size_t)Wg.RB);
 
   /* shrink of h for down */
@@ -754,7 +756,6 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   s2.tab[0] = td;
   s2.S[0] = Sd;
   s2.umax = umax;
-  s2.xs2 = nullptr;
   s2.kc = shrink_kc(I / 64);
   s2.n_col_tiles = (umax * (td.rpad ? td.rpad : 16) + 31) / 32;
   s2.part = b.take<float>((size_t)s2.n_col_tiles * s2.kc * 1024);
@@ -765,16 +766,14 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   memset(&g2, 0, sizeof(g2));
   g2.w0 = Wd.dev();
   g2.x = h;
-  g2.xs2 = hs2;
   g2.T = T;
-  g2.waves = gemv_waves(Wd.G);
-  g2.ks = gemv_ks(Wd.RB, Wd.G, g2.waves);
+  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2);
   g2.tab0 = td;
   g2.S0 = Sd;
   g2.umax = umax;
   g2.rings = rings;
   g2.y = y;
-  g2.part = b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
+  g2.part = b.take<float>((size_t)Wd.RB * (g2.ks + g2.has_expand) * nv_for(T) * 64);
   g2.counters = ctrs((size_t)Wd.RB);
 
   P.bytes = b.off + 256;
@@ -834,22 +833,14 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
     plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
     if (ws_reserve(l, P.bytes, P.ctr)) return -1;
     plan_mlp(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, P);
-    {
-      Timed tm(l, KS_SHRINK_X);
-      if (launch_err(aos_launch_shrink(&P.sh1, l->stream), "lora shrink")) return -1;
-    }
-    {
-      Timed tm(l, KS_GEMV_GU);
-      if (launch_err(aos_launch_gemv(&P.gv1, 1, l->stream), "q4 gemv gate/up")) return -1;
-    }
-    {
-      Timed tm(l, KS_SHRINK_H);
-      if (launch_err(aos_launch_shrink(&P.sh2, l->stream), "lora shrink down")) return -1;
-    }
-    {
-      Timed tm(l, KS_GEMV_DOWN);
-      if (launch_err(aos_launch_gemv(&P.gv2, 0, l->stream), "q4 gemv down")) return -1;
-    }
+    aos_launch_ctx c1 = launch_ctx(l, KS_SHRINK_X);
+    if (launch_err(aos_launch_shrink(&P.sh1, &c1), "lora shrink")) return -1;
+    aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
+    if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
+    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+    if (launch_err(aos_launch_shrink(&P.sh2, &c3), "lora shrink down")) return -1;
+    aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
+    if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
   }
   return 0;
 }
@@ -893,7 +884,6 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         sp.tab[i] = tabs[i];
         sp.S[i] = b.take<uint16_t>((size_t)Tc * umax * rpm);
       }
-      sp.xs2 = b.take<float>((size_t)Tc * 2 * (in / 64));
       sp.kc = shrink_kc(in / 64);
       sp.n_col_tiles = (umax * rpm + 31) / 32;
       sp.part = b.take<float>((size_t)nm * sp.n_col_tiles * sp.kc * 1024);
@@ -905,16 +895,14 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         memset(&gp[i], 0, sizeof(gp[i]));
         gp[i].w0 = W.dev();
         gp[i].x = xc;
-        gp[i].xs2 = sp.xs2;
         gp[i].T = Tc;
-        gp[i].waves = gemv_waves(W.G);
-        gp[i].ks = gemv_ks(W.RB, W.G, gp[i].waves);
+        gemv_geometry(W.RB, W.G, Tc, false, tabs[i].rpad > 0, gp[i]);
         gp[i].tab0 = tabs[i];
         gp[i].S0 = sp.S[i];
         gp[i].umax = umax;
         gp[i].rings = rc;
         gp[i].y = ys[i] + (size_t)t0 * W.out;
-        gp[i].part = b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
+        gp[i].part = b.take<float>((size_t)W.RB * (gp[i].ks + gp[i].has_expand) * nv_for(Tc) * 64);
         gp[i].counters = cb ? cb + coff : nullptr;
         coff += (size_t)W.RB;
       }
@@ -922,13 +910,11 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         if (ws_reserve(l, b.off + 256, coff + 64)) return -1;
         continue;
       }
-      {
-        Timed tm(l, KS_SHRINK_X);
-        if (launch_err(aos_launch_shrink(&sp, l->stream), "lora shrink")) return -1;
-      }
+      aos_launch_ctx cs = launch_ctx(l, KS_SHRINK_X);
+      if (launch_err(aos_launch_shrink(&sp, &cs), "lora shrink")) return -1;
       for (int i = 0; i < nm; ++i) {
-        Timed tm(l, KS_GEMV_PROJ);
-        if (launch_err(aos_launch_gemv(&gp[i], 0, l->stream), "q4 gemv")) return -1;
+        aos_launch_ctx cg = launch_ctx(l, KS_GEMV_PROJ);
+        if (launch_err(aos_launch_gemv(&gp[i], 0, &cg), "q4 gemv")) return -1;
       }
     }
   }

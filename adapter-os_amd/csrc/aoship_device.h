@@ -47,15 +47,27 @@ __device__ __forceinline__ float aos_f16_to_f32(uint32_t h16) {
 }
 
 /* Four packed bfloat16 pairs (128 + q) from one nibble-shuffled weight word: register p holds
- * (q[2p], q[2p+1]) of the original MLX word as bf16 values 128 + q (exact). */
-__device__ __forceinline__ u32x4 aos_q4_magic(uint32_t w) {
-  u32x4 r;
-  r.x = (w & 0x000F000Fu) | 0x43004300u;
-  r.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  r.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  r.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+ * (q[2p], q[2p+1]) of the original MLX word as bf16 values 128 + q (exact). One shift and one
+ * v_and_or_b32 per register; the mask lives in an SGPR and the exponent pattern in a VGPR
+ * (gfx950's VOP3 encoding takes no literal operands). */
+__device__ __forceinline__ uint32_t aos_and_or(uint32_t a, uint32_t smask, uint32_t vmagic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(smask), "v"(vmagic));
   return r;
 }
+
+__device__ __forceinline__ u32x4 aos_q4_magic(uint32_t w, uint32_t smask, uint32_t vmagic) {
+  u32x4 r;
+  r.x = aos_and_or(w, smask, vmagic);
+  r.y = aos_and_or(w >> 4, smask, vmagic);
+  r.z = aos_and_or(w >> 8, smask, vmagic);
+  r.w = aos_and_or(w >> 12, smask, vmagic);
+  return r;
+}
+
+/* Uniform (SGPR) copies of the extraction constants. */
+__device__ __forceinline__ uint32_t aos_q4_mask() { return __builtin_amdgcn_readfirstlane(0x000F000Fu); }
+__device__ __forceinline__ uint32_t aos_q4_exp() { return 0x43004300u; }
 
 __device__ __forceinline__ uint32_t aos_shfl(uint32_t v, int src_lane) {
   return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
@@ -71,8 +83,30 @@ __device__ __forceinline__ uint64_t aos_shfl64(uint64_t v, int src_lane) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-/* Agent-scope release / acquire around the "last arriving workgroup" reductions. */
-__device__ __forceinline__ void aos_fence_release() { __threadfence(); }
-__device__ __forceinline__ void aos_fence_acquire() { __threadfence(); }
+/* Cross-workgroup hand-over without cache flushes. A partial result is published with
+ * device-coherent stores (agent-scope relaxed atomic stores: write-through past the per-XCD L2),
+ * the storing wave waits until they are acknowledged, then counts its arrival with an
+ * agent-scope atomic add; the workgroup that arrives last reads every partial back with
+ * device-coherent loads, in a fixed order. An agent-scope fence would instead write back and
+ * invalidate the whole L2 of the XCD on every arrival. */
+__device__ __forceinline__ void aos_publish(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float aos_collect(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Wait for this wave's published stores, then count the arrival (call from one lane).
+ * Returns the previous count. */
+__device__ __forceinline__ uint32_t aos_arrive(uint32_t *ctr) {
+  __builtin_amdgcn_s_waitcnt(0);
+  return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Reset a counter for the next launch (the last arriver's job). */
+__device__ __forceinline__ void aos_reset(uint32_t *ctr) {
+  __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 #endif

@@ -7,85 +7,102 @@
  *
  * HBM-bound design for gfx950:
  *   - weights stream in the q4-tile layout: one 16-byte load per lane brings a full 1 KiB
- *     (32 rows x 64 K) chunk, i.e. one quantisation group of 32 rows;
+ *     chunk (32 rows x one 64-element group);
+ *   - each wave keeps D groups of loads in flight in a register ring (refilled as it consumes
+ *     them); x is staged once per workgroup in LDS, where the per-group sums of x used by the
+ *     bias term are also formed;
  *   - nibbles become bfloat16 (128 + q) with one and-or per pair (exact), and
  *     v_mfma_f32_32x32x16_bf16 forms t = sum (128 + q) x per group with the tokens as the M
  *     dimension (padded to 32); the group's scale and bias are applied to the accumulator:
  *         y += s * t + (b - 128 s) * sum(x over the group)
  *     so no per-element dequantisation arithmetic is needed;
  *   - K is split across the W waves of a workgroup and across ks workgroups per row block; the
- *     partials are summed in a fixed order (waves through LDS, workgroups by the last one to
- *     finish), so results are bit-identical run to run with no floating-point atomics;
- *   - the LoRA expand sum_u S[t, u] B_u[o, :] runs as extra MFMA K steps on the reduced
- *     accumulator, before the SwiGLU / store epilogue.
+ *     LoRA expand sum_u S[t, u] B_u[o, :] runs in one more workgroup per row block
+ *     (blockIdx.y == ks), so the base waves carry no expand registers; all partials are summed
+ *     in a fixed order (waves through LDS, workgroups by the last one to finish), so results
+ *     are bit-identical run to run with no floating-point atomics.
  */
 #include "aoship_device.h"
 #include "aoship_internal.h"
+#include <hip/hip_ext.h>
 #include "aoship_union.h"
 
 namespace {
 
+constexpr int XE = 4; /* x staging: 16-byte loads per thread issued ahead of the weights */
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+/* Apply one group's scale and bias to the accumulators. Lanes whose token m >= T read a
+ * clamped (valid) sum; their accumulators are never stored, so no branch is needed. */
 template <int NV>
-__device__ __forceinline__ void group_step(const u32x4 &wv, uint32_t sbv, const uint16_t *xrow,
-                                           int xoff, const float *xs2, int T, int g, int G2,
-                                           int lane, float (&acc)[NV]) {
-  f32x16 t = {};
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    u32x4 a = {0u, 0u, 0u, 0u};
-    if (xrow) a = *(const u32x4 *)(xrow + xoff + 8 * st);
-    t = aos_mfma32(a, aos_q4_magic(wv[st]), t);
-  }
+__device__ __forceinline__ void apply_group(const f32x16 &t, uint32_t sbv, const float *xs, int GR, int gl,
+                                            int T, int lane, float (&acc)[NV]) {
   const float s = aos_f16_to_f32(sbv & 0xffffu);
   const float b = aos_f16_to_f32(sbv >> 16);
   const float bp = fmaf(-128.0f, s, b);
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int m = aos_acc_m(v, lane);
-    float xs = 0.0f;
-    if (m < T) xs = xs2[(size_t)m * G2 + 2 * g] + xs2[(size_t)m * G2 + 2 * g + 1];
-    acc[v] = fmaf(s, t[v], fmaf(bp, xs, acc[v]));
+    int m = aos_acc_m(v, lane);
+    m = m < T ? m : T - 1;
+    const float sx = xs[(m * GR + gl) * 2] + xs[(m * GR + gl) * 2 + 1];
+    acc[v] = fmaf(s, t[v], fmaf(bp, sx, acc[v]));
   }
 }
 
-/* LoRA expand: acc += S[t, :] . B_u[row, :] over the union list. */
-__device__ __forceinline__ f32x16 lora_expand(f32x16 acc, const aos_lora_tab &tab,
-                                              const uint16_t *S, int stride, int T,
-                                              const uint16_t *list, int U, int row, int lane) {
-  const int rpad = tab.rpad;
-  if (rpad == 0) return acc;
+/* The expand workgroup of one row block: acc = sum over the union's (adapter, rank) steps of
+ * S[t, 16q..16q+15] . B_u[row, j0..j0+15]; the steps are dealt to the waves round-robin. */
+template <int NV, bool SW, int W>
+__device__ void expand_block(const aos_gemv_params &p, int rb, float (&acc0)[NV], float (&acc1)[NV],
+                             uint32_t *bits, uint16_t *list0, uint16_t *list1, int *cnt) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, c = lane >> 5;
-  for (int u = 0; u < U; ++u) {
-    const uint16_t *brow = tab.B[list[u]] + (size_t)row * rpad;
-    for (int j0 = 0; j0 < rpad; j0 += 16) {
+  const int row = rb * 32 + i;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    if (m == 1 && !SW) break;
+    const aos_lora_tab &tab = m == 0 ? p.tab0 : p.tab1;
+    const uint16_t *S = m == 0 ? p.S0 : p.S1;
+    uint16_t *list = m == 0 ? list0 : list1;
+    if (tab.rpad == 0) continue;
+    const int U = aos_build_union(p.rings, 0, p.T, tab, bits, list, cnt);
+    const int nq = U * tab.rpad / 16, stride = p.umax * tab.rpad;
+    f32x16 f = {};
+    for (int q = wave; q < nq; q += W) {
+      const int col = 16 * q, u = col / tab.rpad, j0 = col - u * tab.rpad;
       u32x4 a = {0u, 0u, 0u, 0u};
-      if (i < T) a = *(const u32x4 *)(S + (size_t)i * stride + u * rpad + j0 + 8 * c);
-      u32x4 b = *(const u32x4 *)(brow + j0 + 8 * c);
-      acc = aos_mfma32(a, b, acc);
+      if (i < p.T) a = *(const u32x4 *)(S + (size_t)i * stride + col + 8 * c);
+      const u32x4 b = *(const u32x4 *)(tab.B[list[u]] + (size_t)row * tab.rpad + j0 + 8 * c);
+      f = aos_mfma32(a, b, f);
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (m == 0) acc0[v] = f[v];
+      else acc1[v] = f[v];
     }
   }
-  return acc;
 }
 
-template <int NV, bool SW, int W>
+template <int NV, bool SW, int W, int D>
 __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
   constexpr int NA = SW ? 2 : 1;
-  __shared__ float red[W][NA * NV][64];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ uint32_t bits[AOS_UNION_WORDS];
   __shared__ uint16_t list0[256], list1[256];
   __shared__ int cnt;
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: keeps the loop scalar */
   const int rb = blockIdx.x, ksi = blockIdx.y;
-  /* Union lists for the expand (every workgroup builds them; only the last one uses them). */
-  int U0 = 0, U1 = 0;
-  if (p.tab0.rpad > 0) U0 = aos_build_union(p.rings, 0, p.T, p.tab0, bits, list0, &cnt);
-  if (SW && p.tab1.rpad > 0) U1 = aos_build_union(p.rings, 0, p.T, p.tab1, bits, list1, &cnt);
-  const int G = p.w0.G, G2 = 2 * G, in = p.w0.in;
-  const int s_tot = p.ks * W, s_idx = ksi * W + wave;
-  const int g0 = (int)((long)s_idx * G / s_tot), g1 = (int)((long)(s_idx + 1) * G / s_tot);
+  const int G = p.w0.G, in = p.w0.in, T = p.T;
   const int i = lane & 31, c = lane >> 5;
-  const uint16_t *xrow = (i < p.T) ? p.x + (size_t)i * in : nullptr;
+  const int row = rb * 32 + i;
+  const uint32_t qmask = aos_q4_mask(), qexp = aos_q4_exp();
 
   float acc0[NV], acc1[NV];
 #pragma unroll
@@ -93,141 +110,202 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     acc0[v] = 0.0f;
     acc1[v] = 0.0f;
   }
-  const u32x4 *q0 = (const u32x4 *)p.w0.qt + (size_t)rb * G * 64 + lane;
-  const uint32_t *s0 = p.w0.sb + (size_t)rb * G * 32 + (lane & 31);
-  const u32x4 *q1 = SW ? (const u32x4 *)p.w1.qt + (size_t)rb * G * 64 + lane : nullptr;
-  const uint32_t *s1 = SW ? p.w1.sb + (size_t)rb * G * 32 + (lane & 31) : nullptr;
 
-  for (int g = g0; g < g1; ++g) {
-    const u32x4 wv0 = q0[(size_t)g * 64];
-    const uint32_t sb0 = s0[(size_t)g * 32];
-    u32x4 wv1;
-    uint32_t sb1 = 0;
-    if (SW) {
-      wv1 = q1[(size_t)g * 64];
-      sb1 = s1[(size_t)g * 32];
+  if (ksi == p.ks) {
+    expand_block<NV, SW, W>(p, rb, acc0, acc1, bits, list0, list1, &cnt);
+  } else {
+    const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
+    const int GR = gw1 - gw0;
+    const int ga = gw0 + wave * GR / W, gb = gw0 + (wave + 1) * GR / W, ng = gb - ga;
+
+    /* (1) first x staging loads, ahead of the weights. Loads are unconditional (addresses
+     * clamped into range) so no control flow separates them from their use and the compiler
+     * can wait for exactly the load it needs. */
+    const int xchunks = GR * 8; /* 16-byte chunks per token row */
+    const int nx = T * xchunks;
+    u32x4 xv[XE];
+#pragma unroll
+    for (int j = 0; j < XE; ++j) {
+      int idx = tid + j * 64 * W;
+      idx = idx < nx ? idx : nx - 1;
+      const int t = idx / xchunks, r = idx - t * xchunks;
+      xv[j] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
     }
-    const int xoff = 64 * g + 32 * c;
-    group_step<NV>(wv0, sb0, xrow, xoff, p.xs2, p.T, g, G2, lane, acc0);
-    if (SW) group_step<NV>(wv1, sb1, xrow, xoff, p.xs2, p.T, g, G2, lane, acc1);
+
+    /* (2) the ring: groups ga .. ga+D-1 (every wave has at least one group) */
+    const u32x4 *q0 = (const u32x4 *)p.w0.qt + ((size_t)rb * G + ga) * 64 + lane;
+    const uint32_t *s0 = p.w0.sb + ((size_t)rb * G + ga) * 32 + i;
+    const u32x4 *q1 = SW ? (const u32x4 *)p.w1.qt + ((size_t)rb * G + ga) * 64 + lane : nullptr;
+    const uint32_t *s1 = SW ? p.w1.sb + ((size_t)rb * G + ga) * 32 + i : nullptr;
+    u32x4 wa[D], wb[D];
+    uint32_t sa[D], sb[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int jj = d < ng ? d : ng - 1;
+      wa[d] = q0[(size_t)jj * 64];
+      sa[d] = s0[(size_t)jj * 32];
+      if (SW) {
+        wb[d] = q1[(size_t)jj * 64];
+        sb[d] = s1[(size_t)jj * 32];
+      }
+    }
+
+    /* (3) x -> LDS (rest of the staging after the ring is in flight), group sums. LDS holds
+     * 128 zero bytes (read by lanes without a token), the T x rows, then the group sums. */
+    uint16_t *xl = (uint16_t *)(smem + 128);
+    float *xs = (float *)(smem + 128 + (size_t)T * GR * 128);
+    if (tid < 32) ((uint32_t *)smem)[tid] = 0u;
+    const int xstride = GR * 64;
+#pragma unroll
+    for (int j = 0; j < XE; ++j) {
+      const int idx = tid + j * 64 * W;
+      if (idx < nx) {
+        const int t = idx / xchunks, r = idx - t * xchunks;
+        *(u32x4 *)(xl + (size_t)t * xstride + r * 8) = xv[j];
+      }
+    }
+    for (int idx = tid + XE * 64 * W; idx < nx; idx += 64 * W) {
+      const int t = idx / xchunks, r = idx - t * xchunks;
+      *(u32x4 *)(xl + (size_t)t * xstride + r * 8) =
+          *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
+    }
+    lds_barrier();
+    for (int idx = tid; idx < T * GR * 2; idx += 64 * W) {
+      const int t = idx / (GR * 2), rem = idx - t * GR * 2;
+      const uint16_t *src = xl + (size_t)t * xstride + rem * 32;
+      float s = 0.0f;
+      for (int e = 0; e < 32; ++e) s += aos_bf16_to_f32(src[e]);
+      xs[idx] = s;
+    }
+    lds_barrier();
+
+    /* (4) consume the ring, refilling each slot D groups ahead (refills past the end reload
+     * the last group and are never used). x fragment address: lanes with a token step through
+     * their row, the others stay on the zero block. */
+    const int xbase = i < T ? 128 + i * xstride * 2 + 64 * c : 0;
+    const int xmult = i < T ? 128 : 0;
+    for (int base = 0; base < ng; base += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int j = base + d;
+        if (j < ng) {
+          const int gl = ga + j - gw0;
+          f32x16 t0 = {}, t1 = {};
+          u32x4 a[4];
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            a[st] = *(const u32x4 *)(smem + xbase + (size_t)gl * xmult + 16 * st);
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            t0 = aos_mfma32(a[st], aos_q4_magic(wa[d][st], qmask, qexp), t0);
+            if (SW) t1 = aos_mfma32(a[st], aos_q4_magic(wb[d][st], qmask, qexp), t1);
+          }
+          apply_group<NV>(t0, sa[d], xs, GR, gl, T, lane, acc0);
+          if (SW) apply_group<NV>(t1, sb[d], xs, GR, gl, T, lane, acc1);
+        }
+        int jn = j + D;
+        jn = jn < ng ? jn : ng - 1;
+        wa[d] = q0[(size_t)jn * 64];
+        sa[d] = s0[(size_t)jn * 32];
+        if (SW) {
+          wb[d] = q1[(size_t)jn * 64];
+          sb[d] = s1[(size_t)jn * 32];
+        }
+      }
+    }
   }
 
-  /* Fixed-order reduction over the waves of this workgroup. */
+  /* (5) fixed-order reduction over the waves (LDS reused once every wave is done with x) */
+  float *red = (float *)smem;
+  lds_barrier();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    red[wave][v][lane] = acc0[v];
-    if (SW) red[wave][NV + v][lane] = acc1[v];
+    red[(wave * NA * NV + v) * 64 + lane] = acc0[v];
+    if (SW) red[(wave * NA * NV + NV + v) * 64 + lane] = acc1[v];
   }
-  __syncthreads();
+  lds_barrier();
   if (wave != 0) return;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    float a0 = red[0][v][lane], a1 = SW ? red[0][NV + v][lane] : 0.0f;
+    float a0 = red[v * 64 + lane], a1 = SW ? red[(NV + v) * 64 + lane] : 0.0f;
     for (int w = 1; w < W; ++w) {
-      a0 += red[w][v][lane];
-      if (SW) a1 += red[w][NV + v][lane];
+      a0 += red[(w * NA * NV + v) * 64 + lane];
+      if (SW) a1 += red[(w * NA * NV + NV + v) * 64 + lane];
     }
     acc0[v] = a0;
     acc1[v] = a1;
   }
 
-  /* Fixed-order reduction over the ks workgroups of this row block: the last to arrive sums. */
-  if (p.ks > 1) {
-    float *part = p.part + ((size_t)rb * p.ks + ksi) * (NA * NV * 64);
+  /* (6) fixed-order reduction over the workgroups of this row block: the last one sums */
+  const int nsplit = p.ks + p.has_expand;
+  if (nsplit > 1) {
+    float *part = p.part + ((size_t)rb * nsplit + ksi) * (NA * NV * 64);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      part[v * 64 + lane] = acc0[v];
-      if (SW) part[(NV + v) * 64 + lane] = acc1[v];
+      aos_publish(part + v * 64 + lane, acc0[v]);
+      if (SW) aos_publish(part + (NV + v) * 64 + lane, acc1[v]);
     }
     uint32_t old = 0;
-    if (lane == 0) {
-      aos_fence_release();
-      old = __hip_atomic_fetch_add(&p.counters[rb], 1u, __ATOMIC_ACQ_REL,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (lane == 0) old = aos_arrive(&p.counters[rb]);
     old = aos_shfl(old, 0);
-    if (old != (uint32_t)p.ks - 1u) return;
-    aos_fence_acquire();
-    if (lane == 0) p.counters[rb] = 0u;
+    if (old != (uint32_t)nsplit - 1u) return;
+    if (lane == 0) aos_reset(&p.counters[rb]);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       acc0[v] = 0.0f;
       acc1[v] = 0.0f;
     }
-    for (int k = 0; k < p.ks; ++k) {
-      const float *pp = p.part + ((size_t)rb * p.ks + k) * (NA * NV * 64);
+    for (int k = 0; k < nsplit; ++k) {
+      const float *pp = p.part + ((size_t)rb * nsplit + k) * (NA * NV * 64);
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        acc0[v] += pp[v * 64 + lane];
-        if (SW) acc1[v] += pp[(NV + v) * 64 + lane];
+        acc0[v] += aos_collect(pp + v * 64 + lane);
+        if (SW) acc1[v] += aos_collect(pp + (NV + v) * 64 + lane);
       }
     }
   }
 
-  /* LoRA expand on the full accumulators. */
-  const int row = rb * 32 + (lane & 31);
-  f32x16 f0 = {}, f1 = {};
+  /* (7) epilogue */
+  const int out = p.w0.out;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    f0[v] = acc0[v];
-    f1[v] = acc1[v];
-  }
-  if (U0 > 0) f0 = lora_expand(f0, p.tab0, p.S0, p.umax * p.tab0.rpad, p.T, list0, U0, row, lane);
-  if (SW && U1 > 0)
-    f1 = lora_expand(f1, p.tab1, p.S1, p.umax * p.tab1.rpad, p.T, list1, U1, row, lane);
-
-  const int out = p.w0.out;
-  if (!SW) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int m = aos_acc_m(v, lane);
-      if (m < p.T) p.y[(size_t)m * out + row] = aos_f32_to_bf16(f0[v]);
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int m = aos_acc_m(v, lane);
-      const float gt = f0[v], up = f1[v];
+    const int m = aos_acc_m(v, lane);
+    if (m >= T) continue;
+    if (!SW) {
+      p.y[(size_t)m * out + row] = aos_f32_to_bf16(acc0[v]);
+    } else {
+      const float gt = acc0[v], up = acc1[v];
       const float sg = 1.0f / (1.0f + expf(-gt));
-      const uint16_t hb = aos_f32_to_bf16((gt * sg) * up);
-      float hs = aos_bf16_to_f32(hb);
-      /* half-group sum over the 32 rows of this block (lanes of the same half) */
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) hs = hs + aos_shfl_f(hs, lane ^ o);
-      if (m < p.T) {
-        p.y[(size_t)m * out + row] = hb;
-        if ((lane & 31) == 0) p.ys2[(size_t)m * (out / 32) + rb] = hs;
-      }
+      p.y[(size_t)m * out + row] = aos_f32_to_bf16((gt * sg) * up);
     }
   }
 }
 
 template <int NV>
-int launch_nv(const aos_gemv_params *p, int swiglu, int waves, hipStream_t st) {
-  dim3 grid(p->w0.RB, p->ks);
+int launch_nv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx) {
+  dim3 grid(p->w0.RB, p->ks + p->has_expand);
+  const size_t lds = p->lds_bytes;
   if (swiglu) {
-    hipLaunchKernelGGL((aos_gemv_kernel<NV, true, 4>), grid, dim3(256), 0, st, *p);
+    AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, true, 4, 8>), grid, dim3(256), lds, *p);
+  } else if (p->waves == 4) {
+    AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, false, 4, 12>), grid, dim3(256), lds, *p);
   } else {
-    if (waves == 4)
-      hipLaunchKernelGGL((aos_gemv_kernel<NV, false, 4>), grid, dim3(256), 0, st, *p);
-    else
-      hipLaunchKernelGGL((aos_gemv_kernel<NV, false, 8>), grid, dim3(512), 0, st, *p);
+    AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, false, 8, 12>), grid, dim3(512), lds, *p);
   }
   return (int)hipGetLastError();
 }
 
 }  // namespace
 
-extern "C" int aos_launch_gemv(const aos_gemv_params *p, int swiglu, void *stream) {
-  hipStream_t st = (hipStream_t)stream;
-  const int T = p->T;
+extern "C" int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *st) {
   const int waves = p->waves;
   if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
   if (swiglu && waves != 4) return (int)hipErrorInvalidValue;
-  if (T <= 1) return launch_nv<1>(p, swiglu, waves, st);
-  if (T <= 2) return launch_nv<2>(p, swiglu, waves, st);
-  if (T <= 4) return launch_nv<4>(p, swiglu, waves, st);
-  if (T <= 8) return launch_nv<4>(p, swiglu, waves, st);
-  if (T <= 16) return launch_nv<8>(p, swiglu, waves, st);
-  return launch_nv<16>(p, swiglu, waves, st);
+  const int T = p->T;
+  if (T < 1 || T > AOS_DECODE_MAX_T) return (int)hipErrorInvalidValue;
+  if (T <= 1) return launch_nv<1>(p, swiglu, st);
+  if (T <= 2) return launch_nv<2>(p, swiglu, st);
+  if (T <= 8) return launch_nv<4>(p, swiglu, st);
+  if (T <= 16) return launch_nv<8>(p, swiglu, st);
+  return launch_nv<16>(p, swiglu, st);
 }

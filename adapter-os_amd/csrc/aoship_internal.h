@@ -16,8 +16,7 @@
  *   LoRA module: A[rpad][in] and B[out][rpad] bfloat16 row-major, rank zero-padded to rpad, a
  *   multiple of 16.
  *
- *   Activations: bfloat16 [T][features] row-major. Group half-sums xs2[T][2G] (float32) hold
- *   the sum of elements 32h..32h+31 of each 64-element group, used for the int4 bias term.
+ *   Activations: bfloat16 [T][features] row-major.
  */
 #ifndef AOSHIP_INTERNAL_H
 #define AOSHIP_INTERNAL_H
@@ -31,6 +30,8 @@ enum { MOD_Q = 0, MOD_K, MOD_V, MOD_O, MOD_GATE, MOD_UP, MOD_DOWN };
 
 #define AOS_MAX_ADAPTERS 4096
 #define AOS_DECODE_MAX_T 32
+#define AOS_GEMV_LDS_MAX (64 * 1024)  /* dynamic LDS budget of one GEMV workgroup */
+#define AOS_SHRINK_GROUPS_PER_WAVE 2
 
 typedef struct {
   int out, in, G, RB;
@@ -80,10 +81,9 @@ typedef struct {
   aos_lora_tab tab[3];
   uint16_t *S[3];    /* [T][umax * rpad] bf16 per module */
   int umax;          /* S row stride is umax * rpad */
-  float *xs2;        /* [T][2G] group half sums, written if non-NULL */
   float *part;       /* [nmod][n_col_tiles][kc][16*64] split-K partials */
   uint32_t *counters;/* [nmod][n_col_tiles] zero between launches */
-  int kc;            /* K chunks */
+  int kc;            /* K chunks of 4 * AOS_SHRINK_GROUPS_PER_WAVE groups */
   int n_col_tiles;
 } aos_shrink_params;
 
@@ -91,10 +91,11 @@ typedef struct {
 typedef struct {
   aos_q4_dev w0, w1;  /* w1 used in SwiGLU mode (up), w0 = gate or the single matrix */
   const uint16_t *x;  /* [T][in] bf16 */
-  const float *xs2;   /* [T][2G] */
   int T;
   int ks;             /* workgroups per row block (split K) */
   int waves;          /* waves per workgroup: 4 or 8 */
+  int lds_bytes;      /* dynamic LDS: x staging + group sums, or the wave reduction */
+  int has_expand;     /* 1: one more workgroup per row block adds the LoRA expand */
   /* LoRA expand */
   aos_lora_tab tab0, tab1;
   const uint16_t *S0, *S1; /* [T][umax*rpad] */
@@ -102,18 +103,34 @@ typedef struct {
   const aoship_ring_t *rings;
   /* outputs */
   uint16_t *y;        /* [T][out] bf16 (plain) or h (SwiGLU) */
-  float *ys2;         /* SwiGLU: h half sums [T][out/32] */
-  float *part;        /* [RB][ks][nacc][64*16] */
+  float *part;        /* [RB][ks + has_expand][NA * NV * 64] */
   uint32_t *counters; /* [RB] zero between launches */
 } aos_gemv_params;
+
+/* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
+ * records at kernel start and end (hipExtLaunchKernelGGL). */
+typedef struct {
+  void *stream;
+  void *ev_start;
+  void *ev_stop;
+} aos_launch_ctx;
+
+#define AOS_LAUNCH(ctx, kernel, grid, block, lds, ...)                                            \
+  do {                                                                                            \
+    if ((ctx)->ev_start)                                                                          \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, (hipStream_t)(ctx)->stream,                 \
+                            (hipEvent_t)(ctx)->ev_start, (hipEvent_t)(ctx)->ev_stop, 0, __VA_ARGS__); \
+    else                                                                                          \
+      hipLaunchKernelGGL(kernel, grid, block, lds, (hipStream_t)(ctx)->stream, __VA_ARGS__);      \
+  } while (0)
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 /* Host-side launchers (return hipError_t as int). */
-int aos_launch_route(const aos_route_params *p, void *stream);
-int aos_launch_shrink(const aos_shrink_params *p, void *stream);
-int aos_launch_gemv(const aos_gemv_params *p, int swiglu, void *stream);
+int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx);
+int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ctx *ctx);
+int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx);
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,7 @@
 #include "aos_exp.h"
 #include "aoship_device.h"
 #include "aoship_internal.h"
+#include <hip/hip_ext.h>
 
 namespace {
 
@@ -90,7 +91,7 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
   const int n = p.n;
   bool bad = false;
   for (int i = lane; i < n; i += AOS_WAVE)
-    if (!__builtin_isfinite(priors[i])) bad = true;
+    if (!__builtin_isfinite(aos_collect(priors + i))) bad = true;
 
   uint64_t ka = ~0ull, kb = ~0ull;
   int m_allowed = 0;
@@ -99,7 +100,7 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
     b = ~0ull;
     if (i >= n) return false;
     if (p.allowed && !p.allowed[i]) return false;
-    float sim = (priors[i] + 0.0f) - 0.0f;
+    float sim = (aos_collect(priors + i) + 0.0f) - 0.0f;
     float score = sim * p.bias;
     score = score * 1.0f;
     if (!__builtin_isfinite(score)) bad = true;
@@ -244,23 +245,18 @@ __global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
       for (int i = lane; i < p.d; i += AOS_WAVE) acc = fmaf(w[i], f[i], acc);
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) acc = acc + aos_shfl_f(acc, lane ^ o);
-      if (lane == 0) p.priors_out[(size_t)t * p.n + a] = acc;
+      if (lane == 0) aos_publish(p.priors_out + (size_t)t * p.n + a, acc);
     }
-    /* make lane 0's stores visible to the lanes (and workgroups) that read them back */
-    __threadfence();
-    __syncthreads();
     if (gridDim.x > 1) {
       uint32_t old = 0;
-      if (lane == 0) {
-        aos_fence_release();
-        old = __hip_atomic_fetch_add(&p.counters[t], 1u, __ATOMIC_ACQ_REL,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-      }
+      if (lane == 0) old = aos_arrive(&p.counters[t]);
       old = aos_shfl(old, 0);
       if (old != gridDim.x - 1) return;
-      aos_fence_acquire();
-      if (lane == 0) p.counters[t] = 0u;
+      if (lane == 0) aos_reset(&p.counters[t]);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
     }
+    /* the priors are read back with device-coherent loads below */
     priors = p.priors_out + (size_t)t * p.n;
   } else {
     priors = p.priors_in + (size_t)t * p.n;
@@ -270,9 +266,9 @@ __global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
 
 }  // namespace
 
-extern "C" int aos_launch_route(const aos_route_params *p, void *stream) {
+extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx) {
   dim3 grid(1, p->T);
   if (p->features) grid.x = (p->n + p->priors_per_block - 1) / p->priors_per_block;
-  hipLaunchKernelGGL(aos_route_kernel, grid, dim3(64), 0, (hipStream_t)stream, *p);
+  AOS_LAUNCH(ctx, aos_route_kernel, grid, dim3(64), 0, *p);
   return (int)hipGetLastError();
 }

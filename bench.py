@@ -1,0 +1,278 @@
+"""Benchmark of the adapter-augmented layer hot path on one MI355X.
+
+One step = route the batch's tokens on the device (router features -> priors -> Q15 rings) and run
+the int4 SwiGLU MLP with each token's K LoRA adapters (shrink, fused int4 GEMV + expand + SwiGLU,
+shrink, down GEMV + expand). The headline workload is the Qwen2.5-7B-shaped decode step at one
+token (hidden 3584, intermediate 18944, 16 adapters of rank 16, K = 4); the same line reports the
+8-token decode batch and the 2048-token prefill with its MFMA utilisation, the roofline of the
+dominant kernel (live per-kernel times from dispatch-recorded HIP events) and the CPU baseline
+(the C oracle on this host's cores, a bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-prefill]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "adapter-os_amd"))
+
+METRIC = "decode tok/s + HBM GB/s; prefill MFMA util — Qwen7B-shape int4 SwiGLU+K=4 LoRA"
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class MlpCase:
+    """A device-resident layer, router and inputs for T tokens of a workload."""
+
+    def __init__(self, aoship, W, cid: int, T: int, torch):
+        self.cfg = cfg = W.CONFIGS[cid]
+        self.T = T
+        self.torch = torch
+        self.layer = aoship.Layer(0)
+        for m in cfg.modules:
+            p, s, b = W.base_weights(cfg, m)
+            self.layer.set_base(m, p, s, b)
+        self.adapters = []
+        for a in range(cfg.n_adapters):
+            ad = aoship.LoraAdapter(a, 1, W.lora_scale(cfg))
+            for m in cfg.modules:
+                A, B = W.lora_weights(cfg, a, m)
+                ad.set_module(0, m, A, B)
+            self.adapters.append(ad)
+        self.layer.set_adapters(self.adapters)
+        self.layer.reserve(T)
+        sid = np.arange(cfg.n_adapters, dtype=np.uint64)
+        self.router = aoship.Router(cfg.n_adapters, cfg.k, cfg.tau, cfg.eps, 1.0, sid)
+        xb, _ = W.activations(cfg, T)
+        self.x = torch.from_numpy(xb.view(np.int16)).cuda()
+        self.y = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
+        self.rings = torch.zeros(T * 40, dtype=torch.uint8, device="cuda")
+        if cfg.routing == "features":
+            f, w = W.router_inputs(cfg, T)
+            self.f = torch.from_numpy(f).cuda()
+            self.w = torch.from_numpy(w).cuda()
+            self.priors = None
+        else:
+            self.priors = torch.from_numpy(W.priors(cfg, T)).cuda()
+
+    def step(self):
+        if self.priors is None:
+            self.router.route_features(self.f, self.w, self.rings)
+        else:
+            self.router.route(self.priors, self.rings)
+        self.layer.mlp_forward(self.x, self.rings, self.y)
+
+    def distinct_adapters(self, aoship) -> int:
+        self.torch.cuda.synchronize()
+        r = aoship.rings_from_bytes(self.rings.cpu().numpy())
+        used = set()
+        for t in range(len(r)):
+            k = int(r[t]["top_k"])
+            for s in range(k):
+                if r[t]["gates_q15"][s] > 0:
+                    used.add(int(r[t]["adapter_indices"][s]))
+        return len(used)
+
+
+def time_steps(case, steps: int, warmup: int, torch) -> float:
+    """Milliseconds per step over `steps` steps, events on the launch stream (the null stream)."""
+    for _ in range(warmup):
+        case.step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        case.step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_times(case, steps: int, torch) -> dict:
+    """Average per-launch kernel durations (ms) from events the dispatches record."""
+    case.layer.set_profiling(True)
+    for _ in range(steps):
+        case.step()
+    torch.cuda.synchronize()
+    st = case.layer.kernel_stats()
+    case.layer.set_profiling(False)
+    return {k: ms / n for k, (ms, n) in st.items() if n}
+
+
+def gate_up_bytes(cfg, T: int, U: int) -> int:
+    """Algorithmic HBM bytes of one gate/up launch: both int4 matrices with their f16 scale and
+    bias, the bf16 LoRA B rows of the U distinct adapters for both modules, x in and h out."""
+    H, I = cfg.hidden, cfg.inter
+    base = 2 * (I * H // 2 + 2 * 2 * I * (H // 64))
+    lora = U * 2 * I * cfg.rank * 2
+    return base + lora + T * H * 2 + T * I * 2
+
+
+def cpu_baseline(W, T: int = 1) -> dict:
+    """The C oracle (float32, dequantising on the fly, OpenMP over output rows) on this host: a
+    bounded sample of the decode workload, routing included."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    cfg = W.CONFIGS[2]
+    bw = {m: W.base_weights(cfg, m) for m in cfg.modules}
+    lora = [{m: W.lora_weights(cfg, a, m) for m in cfg.modules} for a in range(cfg.n_adapters)]
+    scales = np.full(cfg.n_adapters, W.lora_scale(cfg), np.float32)
+    f, w = W.router_inputs(cfg, T)
+    _, xf = W.activations(cfg, T)
+    sid = np.arange(cfg.n_adapters, dtype=np.uint64)
+
+    def one():
+        pri = oracle.priors(f, w)
+        rings = oracle.route_batch(pri, cfg.k, cfg.tau, cfg.eps, 1.0, sid)
+        oracle.mlp_forward(xf, bw["gate_proj"], bw["up_proj"], bw["down_proj"], lora, scales, cfg.rank, rings)
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = min(threads, 16)
+    oracle.set_threads(threads)
+    one()
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or (time.perf_counter() - t0 < 8.0 and n < 200):
+        one()
+        n += 1
+    per = (time.perf_counter() - t0) / n
+    oracle.set_threads(1)
+    t1 = time.perf_counter()
+    one()
+    per1 = time.perf_counter() - t1
+    oracle.set_threads(threads)
+    return {
+        "value": T / per,
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"7B-shaped decode step (route + int4 SwiGLU MLP + K=4 LoRA), T={T}, {n} steps on "
+                  f"{threads} threads; 1 thread: {T / per1:.3f} tok/s",
+        "single_thread_tok_s": T / per1,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the hot path runs on a single MI355X and has no multi-GPU "
+              f"mode (asked for --gpus {args.gpus}).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import aoship
+    import workloads as W
+
+    aoship.init(0)
+    log(f"device: {aoship.device_name()}")
+
+    # ---- headline: 7B-shaped decode, one token ----
+    T = 1
+    dec = MlpCase(aoship, W, 2, T, torch)
+    ms = time_steps(dec, args.steps, args.warmup, torch)
+    U = dec.distinct_adapters(aoship)
+    kt = kernel_times(dec, max(20, args.steps // 4), torch)
+    cfg = dec.cfg
+    layer_bytes = W.algorithmic_bytes(cfg, T, U)
+    gu_ms = kt["q4_gemv_gate_up"]
+    gu_bytes = gate_up_bytes(cfg, T, U)
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    log(f"decode T=1: {ms * 1e3:.1f} us/step, kernels (us): " +
+        ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kt.items()))
+    result = {
+        "metric": METRIC,
+        "value": T / (ms * 1e-3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-7B-shaped int4 (g64) SwiGLU MLP, 16 rank-16 LoRA adapters on gate/up/down, "
+                        "K=4 Q15 router over 3584-dim features, decode of 1 token",
+            "hidden": cfg.hidden, "intermediate": cfg.inter, "tokens": T, "adapters": cfg.n_adapters,
+            "rank": cfg.rank, "k": cfg.k,
+        },
+        "layer_hbm_gbps": layer_bytes / (ms * 1e-3) / 1e9,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "q4_gemv_gate_up (int4 gate+up GEMV, fused LoRA expand and SwiGLU)",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": None,
+            "algorithmic_bytes": gu_bytes,
+            "avg_launch_us": gu_ms * 1e3,
+        },
+        "kernels_us": {k: v * 1e3 for k, v in kt.items()},
+    }
+    del dec
+
+    # ---- 8-token decode batch ----
+    T8 = 8
+    d8 = MlpCase(aoship, W, 2, T8, torch)
+    ms8 = time_steps(d8, args.steps, args.warmup, torch)
+    U8 = d8.distinct_adapters(aoship)
+    result["decode_t8"] = {
+        "tok_s": T8 / (ms8 * 1e-3),
+        "ms_per_step": ms8,
+        "distinct_adapters": U8,
+        "layer_hbm_gbps": W.algorithmic_bytes(cfg, T8, U8) / (ms8 * 1e-3) / 1e9,
+    }
+    log(f"decode T=8: {ms8 * 1e3:.1f} us/step")
+    del d8
+
+    # ---- 2048-token prefill ----
+    if not args.skip_prefill:
+        pf = MlpCase(aoship, W, 3, 2048, torch)
+        msp = time_steps(pf, max(3, args.steps // 20), 2, torch)
+        flops = W.algorithmic_flops(pf.cfg, 2048)
+        tflops = flops / (msp * 1e-3) / 1e12
+        result["prefill"] = {
+            "tokens": 2048,
+            "tok_s": 2048 / (msp * 1e-3),
+            "ms_per_step": msp,
+            "algorithmic_tflop": flops / 1e12,
+            "achieved_tflops": tflops,
+            "mfma_util": tflops / BF16_PEAK_TFLOPS,
+            "peak_tflops": BF16_PEAK_TFLOPS,
+        }
+        log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s")
+        del pf
+
+    if not args.skip_cpu:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(W)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
