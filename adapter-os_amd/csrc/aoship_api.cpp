@@ -243,7 +243,10 @@ static int route_common(aoship_router_t *r, const float *features, const float *
   p.priors_in = priors_in;
   p.priors_per_block = 4;
   if (features) {
-    if (!router_w || d <= 0) return set_err("aoship_route_features: bad router weights");
+    if (!router_w || d <= 0 || d % 4 != 0)
+      return set_err("aoship_route_features: router weights missing or d not a multiple of 4");
+    if (((uintptr_t)features & 15u) || ((uintptr_t)router_w & 15u))
+      return set_err("aoship_route_features: features and router_w must be 16-byte aligned");
     p.features = features;
     p.router_w = router_w;
     if (!priors_out) {
@@ -398,6 +401,8 @@ struct aoship_layer {
   Q4Mat mats[AOS_MAX_MODULES];
   std::vector<aoship_lora_adapter *> table;
   ModTable tabs[AOS_MAX_MODULES];
+  DevBuf bound, scale_all; /* [n] per bound adapter: 1 / alpha-over-rank */
+  DevBuf zeros;            /* device zeros read by lanes without an adapter row */
   DevBuf ws, counters;
   size_t ws_cap = 0, ctr_cap = 0;
   hipStream_t stream = nullptr;
@@ -408,6 +413,7 @@ struct aoship_layer {
 };
 
 extern "C" aoship_layer_t *aoship_layer_new(int layer_idx, int group_size, int bits) {
+  if (ensure_device()) return nullptr;
   if (group_size != AOSHIP_GROUP_SIZE || bits != AOSHIP_BITS) {
     set_err("aoship_layer_new: only group_size 64 and bits 4 are supported");
     return nullptr;
@@ -419,6 +425,10 @@ extern "C" aoship_layer_t *aoship_layer_new(int layer_idx, int group_size, int b
   auto *l = new aoship_layer();
   l->layer_idx = layer_idx;
   for (int i = 0; i < KS_COUNT; ++i) l->stats[i].name = kStatNames[i];
+  if (l->zeros.alloc(256, true)) {
+    delete l;
+    return nullptr;
+  }
   return l;
 }
 
@@ -526,6 +536,17 @@ extern "C" int aoship_layer_set_adapters(aoship_layer_t *l, aoship_lora_adapter_
     if (t.B.upload(B.data(), B.size() * sizeof(void *))) return -1;
     if (t.scale.upload(sc.data(), sc.size() * sizeof(float))) return -1;
   }
+  std::vector<uint8_t> bd((size_t)(n > 0 ? n : 1), 0);
+  std::vector<float> sa((size_t)(n > 0 ? n : 1), 0.0f);
+  for (int a = 0; a < n; ++a) {
+    aoship_lora_adapter *ad = table[a];
+    if (!ad || l->layer_idx >= ad->num_layers) continue;
+    for (int m = 0; m < AOS_MAX_MODULES; ++m)
+      if (ad->mods[(size_t)l->layer_idx * AOS_MAX_MODULES + m].valid) bd[a] = 1;
+    sa[a] = ad->scale;
+  }
+  if (l->bound.upload(bd.data(), bd.size())) return -1;
+  if (l->scale_all.upload(sa.data(), sa.size() * sizeof(float))) return -1;
   return 0;
 }
 
@@ -677,11 +698,102 @@ static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv
   g.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
 }
 
-static int shrink_kc(int G) { return ceil_div(G, 4 * AOS_SHRINK_GROUPS_PER_WAVE); }
+/* Shrink geometry: about 1024 waves over the row blocks, at least one group per wave, x slice
+ * within the LDS budget, at most 16 K splits (their partials are summed by one workgroup). */
+static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp) {
+  int ks = ceil_div(256, rb_total > 0 ? rb_total : 1);
+  int cap = G / 4;
+  if (cap < 1) cap = 1;
+  if (cap > 16) cap = 16;
+  if (ks > cap) ks = cap;
+  while (ks < G && 128 + (size_t)T * ceil_div(G, ks) * 128 > AOS_GEMV_LDS_MAX) ++ks;
+  size_t lds_x = 128 + (size_t)T * ceil_div(G, ks) * 128;
+  size_t lds_r = (size_t)4 * nv_for(T) * 64 * 4;
+  sp.ks = ks;
+  sp.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
+}
 
-/* Plan of one decode chunk (T <= 32): workspace carve-up and launch parameters. */
+/* One decode chunk (T <= 32 tokens) of a forward: the workspace carve-up and every launch's
+ * parameters. The same code sizes the workspace (base == nullptr) and fills it. */
+struct Carve {
+  Bump b;
+  uint32_t *cbase;
+  size_t coff = 0;
+  Carve(void *ws, void *ctr) : b(ws, 0), cbase((uint32_t *)ctr) {}
+  uint32_t *counters(size_t n) {
+    uint32_t *p = cbase ? cbase + coff : nullptr;
+    coff += n;
+    return p;
+  }
+};
+
+static aos_plan_params plan_params(aoship_layer *l, const aoship_ring_t *rings, int T, aos_plan *plan) {
+  aos_plan_params pp;
+  memset(&pp, 0, sizeof(pp));
+  pp.rings = rings;
+  pp.T = T;
+  pp.n = (int)l->table.size();
+  pp.bound = l->bound.as<uint8_t>();
+  pp.scale = l->scale_all.as<float>();
+  pp.plan = plan;
+  return pp;
+}
+
+/* Shrink of x for the given modules: every bound adapter ("all" mode, no rings needed) when that
+ * is at most twice the rows of the call's possible union, else the union (the plan is then
+ * built by a launch of its own first). */
+struct XShrink {
+  aos_shrink_params sp;
+  bool separate_plan = false;
+  aos_shrink_params plan_only;
+};
+
+static void plan_x_shrink(aoship_layer *l, Carve &cv, const uint16_t *x, int T, int in,
+                          const aos_lora_tab *tabs, int nm, aos_plan *plan,
+                          const aoship_ring_t *rings, XShrink &xs) {
+  const int n = (int)l->table.size();
+  int umax = n < 8 * T ? n : 8 * T;
+  if (umax < 1) umax = 1;
+  const bool all = n <= 2 * umax || n <= 16;
+  aos_shrink_params &sp = xs.sp;
+  memset(&sp, 0, sizeof(sp));
+  sp.x = x;
+  sp.T = T;
+  sp.in = in;
+  sp.nmod = nm;
+  sp.all_mode = all ? 1 : 0;
+  sp.plan = plan;
+  sp.zero_row = l->zeros.as<uint16_t>();
+  int rb_total = 0;
+  for (int i = 0; i < nm; ++i) {
+    sp.tab[i] = tabs[i];
+    const int rp = tabs[i].rpad;
+    const int slots = all ? n : umax;
+    sp.s_stride[i] = slots * (rp ? rp : 16);
+    sp.n_rb[i] = rp ? ceil_div(slots * rp, 32) : 0;
+    sp.S[i] = cv.b.take<float>((size_t)T * sp.s_stride[i]);
+    rb_total += sp.n_rb[i];
+  }
+  shrink_geometry(rb_total, in / 64, T, sp);
+  sp.part = cv.b.take<float>((size_t)rb_total * sp.ks * nv_for(T) * 64);
+  sp.counters = cv.counters((size_t)rb_total + 1);
+  xs.separate_plan = !all;
+  if (all) {
+    sp.plan_build = plan_params(l, rings, T, plan);
+  } else {
+    memset(&xs.plan_only, 0, sizeof(xs.plan_only));
+    xs.plan_only.T = T;
+    xs.plan_only.nmod = 1;
+    xs.plan_only.ks = 1;
+    xs.plan_only.plan_build = plan_params(l, rings, T, plan);
+    xs.plan_only.zero_row = sp.zero_row;
+  }
+}
+
+/* Plan of one decode chunk of the SwiGLU MLP. */
 struct MlpPlan {
-  aos_shrink_params sh1, sh2;
+  XShrink sx;
+  aos_shrink_params sh;
   aos_gemv_params gv1, gv2;
   size_t bytes = 0, ctr = 0;
 };
@@ -690,78 +802,53 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
                      uint16_t *y, void *ws, void *ctr, MlpPlan &P) {
   const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
   const int H = Wg.in, I = Wg.out;
-  aos_lora_tab tg = lora_tab(l, MOD_GATE, H, I), tu = lora_tab(l, MOD_UP, H, I),
-               td = lora_tab(l, MOD_DOWN, I, H);
-  const int nb = (int)l->table.size();
-  int umax = nb < 8 * T ? nb : 8 * T;
+  aos_lora_tab tabs_gu[2] = {lora_tab(l, MOD_GATE, H, I), lora_tab(l, MOD_UP, H, I)};
+  aos_lora_tab td = lora_tab(l, MOD_DOWN, I, H);
+  const int n = (int)l->table.size();
+  int umax = n < 8 * T ? n : 8 * T;
   if (umax < 1) umax = 1;
-  Bump b(ws, 0);
-  uint32_t *cbase = (uint32_t *)ctr;
-  size_t coff = 0;
-  auto ctrs = [&](size_t n) {
-    uint32_t *p = cbase ? cbase + coff : nullptr;
-    coff += n;
-    return p;
-  };
-  uint16_t *Sg = b.take<uint16_t>((size_t)T * umax * (tg.rpad ? tg.rpad : 16));
-  uint16_t *Su = b.take<uint16_t>((size_t)T * umax * (tu.rpad ? tu.rpad : 16));
-  uint16_t *Sd = b.take<uint16_t>((size_t)T * umax * (td.rpad ? td.rpad : 16));
-  uint16_t *h = b.take<uint16_t>((size_t)T * I);
+  Carve cv(ws, ctr);
+  aos_plan *plan = cv.b.take<aos_plan>(1);
+  uint16_t *h = cv.b.take<uint16_t>((size_t)T * I);
+  plan_x_shrink(l, cv, x, T, H, tabs_gu, 2, plan, rings, P.sx);
 
-  /* shrink of x for gate and up */
-  aos_shrink_params &s1 = P.sh1;
-  memset(&s1, 0, sizeof(s1));
-  s1.x = x;
-  s1.T = T;
-  s1.in = H;
-  s1.rings = rings;
-  s1.nmod = 2;
-  s1.tab[0] = tg;
-  s1.tab[1] = tu;
-  s1.S[0] = Sg;
-  s1.S[1] = Su;
-  s1.umax = umax;
-  s1.kc = shrink_kc(H / 64);
-  int rpm1 = tg.rpad > tu.rpad ? tg.rpad : tu.rpad;
-  s1.n_col_tiles = (umax * (rpm1 ? rpm1 : 16) + 31) / 32;
-  s1.part = b.take<float>((size_t)2 * s1.n_col_tiles * s1.kc * 1024);
-  s1.counters = ctrs((size_t)2 * s1.n_col_tiles);
-
-  /* gate/up GEMV + SwiGLU */
   aos_gemv_params &g1 = P.gv1;
   memset(&g1, 0, sizeof(g1));
   g1.w0 = Wg.dev();
   g1.w1 = Wu.dev();
   g1.x = x;
   g1.T = T;
-  gemv_geometry(Wg.RB, Wg.G, T, true, tg.rpad > 0 || tu.rpad > 0, g1);
-  g1.tab0 = tg;
-  g1.tab1 = tu;
-  g1.S0 = Sg;
-  g1.S1 = Su;
-  g1.umax = umax;
-  g1.rings = rings;
+  gemv_geometry(Wg.RB, Wg.G, T, true, tabs_gu[0].rpad > 0 || tabs_gu[1].rpad > 0, g1);
+  g1.tab0 = tabs_gu[0];
+  g1.tab1 = tabs_gu[1];
+  g1.S0 = P.sx.sp.S[0];
+  g1.S1 = P.sx.sp.S[1];
+  g1.s_stride0 = P.sx.sp.s_stride[0];
+  g1.s_stride1 = P.sx.sp.s_stride[1];
+  g1.s_all = P.sx.sp.all_mode;
+  g1.plan = plan;
+  g1.zero_row = l->zeros.as<uint16_t>();
   g1.y = h;
-  g1.part = b.take<float>((size_t)Wg.RB * (g1.ks + g1.has_expand) * 2 * nv_for(T) * 64);
-  g1.counters = ctrs((size_t)Wg.RB);
+  g1.part = cv.b.take<float>((size_t)Wg.RB * (g1.ks + g1.has_expand) * 2 * nv_for(T) * 64);
+  g1.counters = cv.counters((size_t)Wg.RB);
 
-  /* shrink of h for down */
-  aos_shrink_params &s2 = P.sh2;
+  aos_shrink_params &s2 = P.sh;
   memset(&s2, 0, sizeof(s2));
   s2.x = h;
   s2.T = T;
   s2.in = I;
-  s2.rings = rings;
   s2.nmod = 1;
   s2.tab[0] = td;
-  s2.S[0] = Sd;
-  s2.umax = umax;
-  s2.kc = shrink_kc(I / 64);
-  s2.n_col_tiles = (umax * (td.rpad ? td.rpad : 16) + 31) / 32;
-  s2.part = b.take<float>((size_t)s2.n_col_tiles * s2.kc * 1024);
-  s2.counters = ctrs((size_t)s2.n_col_tiles);
+  s2.all_mode = 0;
+  s2.plan = plan;
+  s2.zero_row = l->zeros.as<uint16_t>();
+  s2.s_stride[0] = umax * (td.rpad ? td.rpad : 16);
+  s2.n_rb[0] = td.rpad ? ceil_div(umax * td.rpad, 32) : 0;
+  s2.S[0] = cv.b.take<float>((size_t)T * s2.s_stride[0]);
+  shrink_geometry(s2.n_rb[0], I / 64, T, s2);
+  s2.part = cv.b.take<float>((size_t)(s2.n_rb[0] + 1) * s2.ks * nv_for(T) * 64);
+  s2.counters = cv.counters((size_t)s2.n_rb[0] + 1);
 
-  /* down GEMV */
   aos_gemv_params &g2 = P.gv2;
   memset(&g2, 0, sizeof(g2));
   g2.w0 = Wd.dev();
@@ -769,37 +856,31 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.T = T;
   gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2);
   g2.tab0 = td;
-  g2.S0 = Sd;
-  g2.umax = umax;
-  g2.rings = rings;
+  g2.S0 = s2.S[0];
+  g2.s_stride0 = s2.s_stride[0];
+  g2.s_all = 0;
+  g2.plan = plan;
+  g2.zero_row = l->zeros.as<uint16_t>();
   g2.y = y;
-  g2.part = b.take<float>((size_t)Wd.RB * (g2.ks + g2.has_expand) * nv_for(T) * 64);
-  g2.counters = ctrs((size_t)Wd.RB);
+  g2.part = cv.b.take<float>((size_t)Wd.RB * (g2.ks + g2.has_expand) * nv_for(T) * 64);
+  g2.counters = cv.counters((size_t)Wd.RB);
 
-  P.bytes = b.off + 256;
-  P.ctr = coff + 64;
+  P.bytes = cv.b.off + 256;
+  P.ctr = cv.coff + 64;
 }
 
 extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
   if (!l) return set_err("aoship_layer_reserve: null layer");
   if (max_tokens < 1) return set_err("aoship_layer_reserve: max_tokens must be >= 1");
   if (ensure_device()) return -1;
-  int T = max_tokens < AOS_DECODE_MAX_T ? max_tokens : AOS_DECODE_MAX_T;
   size_t bytes = 0, ctr = 0;
-  if (l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid) {
-    MlpPlan P;
-    plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, P);
-    bytes = P.bytes;
-    ctr = P.ctr;
-  }
-  for (int m = 0; m < AOS_MAX_MODULES; ++m) {
-    if (!l->mats[m].valid) continue;
-    const Q4Mat &W = l->mats[m];
-    size_t need = (size_t)T * 8 * 128 * 2 + (size_t)T * 2 * W.G * 4 +
-                  (size_t)W.RB * 16 * 16 * 64 * 4 + (size_t)64 * 48 * 1024 * 4 + 65536;
-    if (need > bytes) bytes = need;
-    size_t c = (size_t)W.RB + 3 * 1024;
-    if (c > ctr) ctr = c;
+  for (int T = 1; T <= AOS_DECODE_MAX_T && T <= max_tokens; T *= 2) {
+    if (l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid) {
+      MlpPlan P;
+      plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+      if (P.bytes > bytes) bytes = P.bytes;
+      if (P.ctr > ctr) ctr = P.ctr;
+    }
   }
   return ws_reserve(l, bytes, ctr);
 }
@@ -818,6 +899,15 @@ static int launch_err(int e, const char *what) {
   return set_err(std::string(what) + ": " + hipGetErrorString((hipError_t)e));
 }
 
+static int launch_x_shrink(aoship_layer *l, XShrink &xs) {
+  if (xs.separate_plan) {
+    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+    if (launch_err(aos_launch_shrink(&xs.plan_only, &c0), "adapter plan")) return -1;
+  }
+  aos_launch_ctx c1 = launch_ctx(l, KS_SHRINK_X);
+  return launch_err(aos_launch_shrink(&xs.sp, &c1), "lora shrink");
+}
+
 extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int T,
                                   const aoship_ring_t *rings, aoship_bf16_t *y) {
   if (check_common(l, x, T, rings, y)) return -1;
@@ -833,12 +923,11 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
     plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
     if (ws_reserve(l, P.bytes, P.ctr)) return -1;
     plan_mlp(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, P);
-    aos_launch_ctx c1 = launch_ctx(l, KS_SHRINK_X);
-    if (launch_err(aos_launch_shrink(&P.sh1, &c1), "lora shrink")) return -1;
+    if (launch_x_shrink(l, P.sx)) return -1;
     aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
     if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
     aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
-    if (launch_err(aos_launch_shrink(&P.sh2, &c3), "lora shrink down")) return -1;
+    if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;
     aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
     if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
   }
@@ -858,37 +947,13 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
     const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;
     const uint16_t *xc = x + (size_t)t0 * in;
     const aoship_ring_t *rc = rings + t0;
-    const int nb = (int)l->table.size();
-    int umax = nb < 8 * Tc ? nb : 8 * Tc;
-    if (umax < 1) umax = 1;
     aos_lora_tab tabs[3];
-    int rpm = 16;
-    for (int i = 0; i < nm; ++i) {
-      tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
-      if (tabs[i].rpad > rpm) rpm = tabs[i].rpad;
-    }
-    /* carve workspace */
+    for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
     for (int pass = 0; pass < 2; ++pass) {
-      Bump b(pass ? l->ws.p : nullptr, 0);
-      uint32_t *cb = pass ? (uint32_t *)l->counters.p : nullptr;
-      size_t coff = 0;
-      aos_shrink_params sp;
-      memset(&sp, 0, sizeof(sp));
-      sp.x = xc;
-      sp.T = Tc;
-      sp.in = in;
-      sp.rings = rc;
-      sp.nmod = nm;
-      sp.umax = umax;
-      for (int i = 0; i < nm; ++i) {
-        sp.tab[i] = tabs[i];
-        sp.S[i] = b.take<uint16_t>((size_t)Tc * umax * rpm);
-      }
-      sp.kc = shrink_kc(in / 64);
-      sp.n_col_tiles = (umax * rpm + 31) / 32;
-      sp.part = b.take<float>((size_t)nm * sp.n_col_tiles * sp.kc * 1024);
-      sp.counters = cb ? cb + coff : nullptr;
-      coff += (size_t)nm * sp.n_col_tiles;
+      Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr);
+      aos_plan *plan = cv.b.take<aos_plan>(1);
+      XShrink xs;
+      plan_x_shrink(l, cv, xc, Tc, in, tabs, nm, plan, rc, xs);
       aos_gemv_params gp[3];
       for (int i = 0; i < nm; ++i) {
         const Q4Mat &W = l->mats[mods[i]];
@@ -898,20 +963,20 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         gp[i].T = Tc;
         gemv_geometry(W.RB, W.G, Tc, false, tabs[i].rpad > 0, gp[i]);
         gp[i].tab0 = tabs[i];
-        gp[i].S0 = sp.S[i];
-        gp[i].umax = umax;
-        gp[i].rings = rc;
+        gp[i].S0 = xs.sp.S[i];
+        gp[i].s_stride0 = xs.sp.s_stride[i];
+        gp[i].s_all = xs.sp.all_mode;
+        gp[i].plan = plan;
+        gp[i].zero_row = l->zeros.as<uint16_t>();
         gp[i].y = ys[i] + (size_t)t0 * W.out;
-        gp[i].part = b.take<float>((size_t)W.RB * (gp[i].ks + gp[i].has_expand) * nv_for(Tc) * 64);
-        gp[i].counters = cb ? cb + coff : nullptr;
-        coff += (size_t)W.RB;
+        gp[i].part = cv.b.take<float>((size_t)W.RB * (gp[i].ks + gp[i].has_expand) * nv_for(Tc) * 64);
+        gp[i].counters = cv.counters((size_t)W.RB);
       }
       if (pass == 0) {
-        if (ws_reserve(l, b.off + 256, coff + 64)) return -1;
+        if (ws_reserve(l, cv.b.off + 256, cv.coff + 64)) return -1;
         continue;
       }
-      aos_launch_ctx cs = launch_ctx(l, KS_SHRINK_X);
-      if (launch_err(aos_launch_shrink(&sp, &cs), "lora shrink")) return -1;
+      if (launch_x_shrink(l, xs)) return -1;
       for (int i = 0; i < nm; ++i) {
         aos_launch_ctx cg = launch_ctx(l, KS_GEMV_PROJ);
         if (launch_err(aos_launch_gemv(&gp[i], 0, &cg), "q4 gemv")) return -1;

@@ -25,7 +25,6 @@
 #include "aoship_device.h"
 #include "aoship_internal.h"
 #include <hip/hip_ext.h>
-#include "aoship_union.h"
 
 namespace {
 
@@ -54,31 +53,48 @@ __device__ __forceinline__ void apply_group(const f32x16 &t, uint32_t sbv, const
   }
 }
 
-/* The expand workgroup of one row block: acc = sum over the union's (adapter, rank) steps of
- * S[t, 16q..16q+15] . B_u[row, j0..j0+15]; the steps are dealt to the waves round-robin. */
+/* bf16 pair from two floats, round to nearest even */
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (uint32_t)aos_f32_to_bf16(lo) | ((uint32_t)aos_f32_to_bf16(hi) << 16);
+}
+
+/* The expand workgroup of one row block: acc = sum over the plan's (adapter, rank) steps of
+ * coef(t, u) * S[t, col(u) + j0 .. +15] . B_list[u][row, j0 .. +15]; the steps are dealt to
+ * the waves round-robin. */
 template <int NV, bool SW, int W>
-__device__ void expand_block(const aos_gemv_params &p, int rb, float (&acc0)[NV], float (&acc1)[NV],
-                             uint32_t *bits, uint16_t *list0, uint16_t *list1, int *cnt) {
+__device__ void expand_block(const aos_gemv_params &p, int rb, float (&acc0)[NV], float (&acc1)[NV]) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, c = lane >> 5;
   const int row = rb * 32 + i;
+  const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
+  const int ti = i < p.T ? i : 0;
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     if (m == 1 && !SW) break;
     const aos_lora_tab &tab = m == 0 ? p.tab0 : p.tab1;
-    const uint16_t *S = m == 0 ? p.S0 : p.S1;
-    uint16_t *list = m == 0 ? list0 : list1;
-    if (tab.rpad == 0) continue;
-    const int U = aos_build_union(p.rings, 0, p.T, tab, bits, list, cnt);
-    const int nq = U * tab.rpad / 16, stride = p.umax * tab.rpad;
+    const float *S = m == 0 ? p.S0 : p.S1;
+    const int stride = m == 0 ? p.s_stride0 : p.s_stride1;
+    const int rpad = tab.rpad;
+    if (rpad == 0) continue;
+    const int nq = U * rpad / 16;
     f32x16 f = {};
     for (int q = wave; q < nq; q += W) {
-      const int col = 16 * q, u = col / tab.rpad, j0 = col - u * tab.rpad;
-      u32x4 a = {0u, 0u, 0u, 0u};
-      if (i < p.T) a = *(const u32x4 *)(S + (size_t)i * stride + col + 8 * c);
-      const u32x4 b = *(const u32x4 *)(tab.B[list[u]] + (size_t)row * tab.rpad + j0 + 8 * c);
-      f = aos_mfma32(a, b, f);
+      const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
+      const int a = p.plan->list[u];
+      const int scol = (p.s_all ? a : u) * rpad + j0 + 8 * c;
+      const float *sp = S + (size_t)ti * stride + scol;
+      const float4 s0 = *(const float4 *)sp, s1 = *(const float4 *)(sp + 4);
+      const float cf = i < p.T ? p.plan->coef[ti][u] : 0.0f;
+      u32x4 av;
+      av.x = pack_bf16(cf * s0.x, cf * s0.y);
+      av.y = pack_bf16(cf * s0.z, cf * s0.w);
+      av.z = pack_bf16(cf * s1.x, cf * s1.y);
+      av.w = pack_bf16(cf * s1.z, cf * s1.w);
+      const uint16_t *B = tab.B[a];
+      const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
+      const u32x4 bv = *(const u32x4 *)bp;
+      f = aos_mfma32(av, bv, f);
     }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
@@ -92,10 +108,6 @@ template <int NV, bool SW, int W, int D>
 __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
   constexpr int NA = SW ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  __shared__ uint32_t bits[AOS_UNION_WORDS];
-  __shared__ uint16_t list0[256], list1[256];
-  __shared__ int cnt;
-
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: keeps the loop scalar */
   const int rb = blockIdx.x, ksi = blockIdx.y;
@@ -112,7 +124,7 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
   }
 
   if (ksi == p.ks) {
-    expand_block<NV, SW, W>(p, rb, acc0, acc1, bits, list0, list1, &cnt);
+    expand_block<NV, SW, W>(p, rb, acc0, acc1);
   } else {
     const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
     const int GR = gw1 - gw0;
@@ -255,13 +267,28 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
       acc0[v] = 0.0f;
       acc1[v] = 0.0f;
     }
-    for (int k = 0; k < nsplit; ++k) {
-      const float *pp = p.part + ((size_t)rb * nsplit + k) * (NA * NV * 64);
+    /* partials are read 4 at a time (all loads in flight together) and summed in order */
+    for (int k0 = 0; k0 < nsplit; k0 += 4) {
+      float v0[4][NV], v1[4][NV];
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        acc0[v] += aos_collect(pp + v * 64 + lane);
-        if (SW) acc1[v] += aos_collect(pp + (NV + v) * 64 + lane);
+      for (int kk = 0; kk < 4; ++kk) {
+        const int k = k0 + kk < nsplit ? k0 + kk : nsplit - 1;
+        const float *pp = p.part + ((size_t)rb * nsplit + k) * (NA * NV * 64);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          v0[kk][v] = aos_collect(pp + v * 64 + lane);
+          v1[kk][v] = SW ? aos_collect(pp + (NV + v) * 64 + lane) : 0.0f;
+        }
       }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        if (k0 + kk < nsplit) {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+            acc0[v] += v0[kk][v];
+            if (SW) acc1[v] += v1[kk][v];
+          }
+        }
     }
   }
 

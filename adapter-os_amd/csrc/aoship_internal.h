@@ -48,12 +48,25 @@ typedef struct {
   const float *scale;       /* device [n] alpha / rank */
 } aos_lora_tab;
 
-/* Union of adapters used by a token tile: list[u] ascending adapter index, count U. */
+/* Adapter plan of one layer call (T <= 32 tokens), built once from the rings:
+ * the union of adapters used by the tokens (ascending index) and each token's coefficient
+ * scale * q / 32767 for each adapter of the union (0 when the token does not use it). */
+#define AOS_PLAN_MAXU 256
+typedef struct {
+  int U;
+  int pad[3];
+  uint16_t list[AOS_PLAN_MAXU];
+  float coef[AOS_DECODE_MAX_T][AOS_PLAN_MAXU];
+} aos_plan;
+
 typedef struct {
   const aoship_ring_t *rings;
   int T;
-  int n_bound;
-} aos_union_src;
+  int n;                 /* bound table length */
+  const uint8_t *bound;  /* [n] 1 = adapter bound for this layer */
+  const float *scale;    /* [n] */
+  aos_plan *plan;
+} aos_plan_params;
 
 /* ---- router ---- */
 typedef struct {
@@ -71,20 +84,27 @@ typedef struct {
   int priors_per_block;
 } aos_route_params;
 
-/* ---- LoRA shrink: S[t][u*rpad + j] = coef(t, u) * sum_i A_u[j][i] x[t][i] ----
- * Up to 3 modules sharing the input x (gate+up, or q+k+v) in one launch (grid.y = module). */
+/* ---- LoRA shrink for T <= 32 tokens: S[t][col] = sum_i A_row(col)[i] x[t][i], float32 ----
+ * Row col = (adapter slot u, rank row j) with u = col / rpad. In "all" mode slot u is adapter u
+ * of the table (no rings needed); otherwise slot u is plan->list[u] (the call's union). Up to 3
+ * modules sharing x in one launch. The grid is (row blocks of 32 summed over the modules, ks);
+ * one extra workgroup (blockIdx.x == n_rb_total) builds the plan when plan_build is set. */
 typedef struct {
   const uint16_t *x; /* [T][in] bf16 */
   int T, in;
-  const aoship_ring_t *rings;
   int nmod;
   aos_lora_tab tab[3];
-  uint16_t *S[3];    /* [T][umax * rpad] bf16 per module */
-  int umax;          /* S row stride is umax * rpad */
-  float *part;       /* [nmod][n_col_tiles][kc][16*64] split-K partials */
-  uint32_t *counters;/* [nmod][n_col_tiles] zero between launches */
-  int kc;            /* K chunks of 4 * AOS_SHRINK_GROUPS_PER_WAVE groups */
-  int n_col_tiles;
+  float *S[3];       /* [T][s_stride] float32 per module */
+  int s_stride[3];
+  int n_rb[3];       /* row blocks per module */
+  int all_mode;      /* 1: rows over every table slot; 0: over plan->list */
+  const aos_plan *plan;
+  int ks;            /* K splits across workgroups */
+  int lds_bytes;
+  float *part;       /* [rb_total][ks][16 * 64] */
+  uint32_t *counters;/* [rb_total] zero between launches */
+  aos_plan_params plan_build; /* used when plan_build.plan != NULL */
+  const uint16_t *zero_row;   /* device zeros, read by lanes without an adapter row */
 } aos_shrink_params;
 
 /* ---- decode GEMV ---- */
@@ -96,11 +116,13 @@ typedef struct {
   int waves;          /* waves per workgroup: 4 or 8 */
   int lds_bytes;      /* dynamic LDS: x staging + group sums, or the wave reduction */
   int has_expand;     /* 1: one more workgroup per row block adds the LoRA expand */
-  /* LoRA expand */
+  /* LoRA expand: coef(t, u) * S[t][col(u) + j] . B_list[u][row][j] over the plan's union */
   aos_lora_tab tab0, tab1;
-  const uint16_t *S0, *S1; /* [T][umax*rpad] */
-  int umax;
-  const aoship_ring_t *rings;
+  const float *S0, *S1;   /* [T][s_stride] float32 */
+  int s_stride0, s_stride1;
+  int s_all;              /* 1: S columns indexed by adapter, 0: by union slot */
+  const aos_plan *plan;
+  const uint16_t *zero_row;
   /* outputs */
   uint16_t *y;        /* [T][out] bf16 (plain) or h (SwiGLU) */
   float *part;        /* [RB][ks + has_expand][NA * NV * 64] */

@@ -16,8 +16,9 @@
  * exactly the order of Rust's stable sort. N > 64 adapters are streamed through the wave 56 at
  * a time while the best 8 stay in lanes 0..7. The softmax uses a correctly rounded float64 exp.
  *
- * Optionally the priors are first computed from router features (fixed-order float32 GEMV); the
- * workgroups of one token then hand over to the last one to finish, which routes.
+ * Optionally the priors are first computed from router features: one wave per (adapter, token)
+ * dot product in float32 with a fixed order (lane l sums elements 256k + 4l + e, then a xor
+ * butterfly); the workgroups of one token hand over to the last one to finish, which routes.
  */
 #include "aos_exp.h"
 #include "aoship_device.h"
@@ -89,18 +90,19 @@ __device__ __forceinline__ int quantize_q15(float g) {
 
 __device__ void route_one(const aos_route_params &p, const float *priors, int t, int lane) {
   const int n = p.n;
+  /* every prior is checked for finiteness, allowed or not (validate_router_inputs); the chunked
+   * passes below visit each index exactly once */
   bool bad = false;
-  for (int i = lane; i < n; i += AOS_WAVE)
-    if (!__builtin_isfinite(aos_collect(priors + i))) bad = true;
-
   uint64_t ka = ~0ull, kb = ~0ull;
   int m_allowed = 0;
   auto load_key = [&](int i, uint64_t &a, uint64_t &b) -> bool {
     a = ~0ull;
     b = ~0ull;
     if (i >= n) return false;
+    const float prior = aos_collect(priors + i);
+    if (!__builtin_isfinite(prior)) bad = true;
     if (p.allowed && !p.allowed[i]) return false;
-    float sim = (aos_collect(priors + i) + 0.0f) - 0.0f;
+    float sim = (prior + 0.0f) - 0.0f;
     float score = sim * p.bias;
     score = score * 1.0f;
     if (!__builtin_isfinite(score)) bad = true;
@@ -156,12 +158,24 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
 #pragma unroll
   for (int s = 0; s < 8; ++s)
     if (s < kk) mx = rust_f64_max(mx, (double)sc[s]);
+  /* lane s evaluates exp for top-K entry s (the same value the serial loop would produce), then
+   * every lane gathers the K values and runs the Kahan summation in top-K order */
+  double my_e;
+  {
+    const int s = lane & 7;
+    float my_sc = sc[0];
+#pragma unroll
+    for (int q = 1; q < 8; ++q)
+      if (s == q) my_sc = sc[q];
+    my_e = aos_exp_cr(((double)my_sc - mx) / (double)p.tau);
+  }
   double e[8];
   double sum = 0.0, comp = 0.0;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
+    const uint64_t bits = __builtin_bit_cast(uint64_t, my_e);
+    const double ex = __builtin_bit_cast(double, aos_shfl64(bits, s));
     if (s < kk) {
-      double ex = aos_exp_cr(((double)sc[s] - mx) / (double)p.tau);
       double y = ex - comp;
       double tt = sum + y;
       comp = (tt - sum) - y;
@@ -236,17 +250,47 @@ __global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
   const int t = blockIdx.y;
   const float *priors;
   if (p.features) {
-    const float *f = p.features + (size_t)t * p.d;
-    int a0 = blockIdx.x * p.priors_per_block;
-    int a1 = a0 + p.priors_per_block < p.n ? a0 + p.priors_per_block : p.n;
-    for (int a = a0; a < a1; ++a) {
-      const float *w = p.router_w + (size_t)a * p.d;
-      float acc = 0.0f;
-      for (int i = lane; i < p.d; i += AOS_WAVE) acc = fmaf(w[i], f[i], acc);
+    /* priors[t, a] for a = blockIdx.x: lane l accumulates elements 256k + 4l + e (k ascending,
+     * e = 0..3) with fused multiply-adds, then a xor butterfly over the 64 lanes. */
+    const int a = blockIdx.x;
+    const float4 *f4 = (const float4 *)(p.features + (size_t)t * p.d);
+    const float4 *w4 = (const float4 *)(p.router_w + (size_t)a * p.d);
+    const int nk = p.d >> 8;        /* full 256-element chunks */
+    const int tail = p.d & 255;     /* multiple of 4 */
+    float acc = 0.0f;
+    int k = 0;
+    for (; k + 4 <= nk; k += 4) {
+      float4 fv[4], wv[4];
 #pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc = acc + aos_shfl_f(acc, lane ^ o);
-      if (lane == 0) aos_publish(p.priors_out + (size_t)t * p.n + a, acc);
+      for (int j = 0; j < 4; ++j) {
+        fv[j] = f4[(k + j) * 64 + lane];
+        wv[j] = w4[(k + j) * 64 + lane];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = fmaf(wv[j].x, fv[j].x, acc);
+        acc = fmaf(wv[j].y, fv[j].y, acc);
+        acc = fmaf(wv[j].z, fv[j].z, acc);
+        acc = fmaf(wv[j].w, fv[j].w, acc);
+      }
     }
+    for (; k < nk; ++k) {
+      const float4 fv = f4[k * 64 + lane], wv = w4[k * 64 + lane];
+      acc = fmaf(wv.x, fv.x, acc);
+      acc = fmaf(wv.y, fv.y, acc);
+      acc = fmaf(wv.z, fv.z, acc);
+      acc = fmaf(wv.w, fv.w, acc);
+    }
+    if (4 * lane < tail) {
+      const float4 fv = f4[nk * 64 + lane], wv = w4[nk * 64 + lane];
+      acc = fmaf(wv.x, fv.x, acc);
+      acc = fmaf(wv.y, fv.y, acc);
+      acc = fmaf(wv.z, fv.z, acc);
+      acc = fmaf(wv.w, fv.w, acc);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc = acc + aos_shfl_f(acc, lane ^ o);
+    if (lane == 0) aos_publish(p.priors_out + (size_t)t * p.n + a, acc);
     if (gridDim.x > 1) {
       uint32_t old = 0;
       if (lane == 0) old = aos_arrive(&p.counters[t]);
@@ -268,7 +312,7 @@ __global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
 
 extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx) {
   dim3 grid(1, p->T);
-  if (p->features) grid.x = (p->n + p->priors_per_block - 1) / p->priors_per_block;
+  if (p->features) grid.x = p->n; /* one wave per (adapter, token) dot product */
   AOS_LAUNCH(ctx, aos_route_kernel, grid, dim3(64), 0, *p);
   return (int)hipGetLastError();
 }

@@ -294,7 +294,11 @@ void orc_priors(const float *features, const float *router_w, int T, int n, int 
       float p[64];
       for (int l = 0; l < 64; ++l) {
         float acc = 0.0f;
-        for (int i = l; i < d; i += 64) acc = fmaf(w[i], f[i], acc);
+        for (int base = 0; base < d; base += 256)
+          for (int e = 0; e < 4; ++e) {
+            int i = base + 4 * l + e;
+            if (i < d) acc = fmaf(w[i], f[i], acc);
+          }
         p[l] = acc;
       }
       for (int o = 32; o >= 1; o >>= 1) {

@@ -76,7 +76,8 @@ int orc_route_batch(const float *priors, int T, int n, const uint64_t *stable_id
                     orc_ring_t *rings, int *bad_token);
 
 /* Router-logit GEMV of the synthetic workloads: priors[t*n + a] = sum_i Wr[a*d+i] * f[t*d+i],
- * float32, fixed order: 64 strided fmaf partial sums then a xor butterfly. */
+ * float32, fixed order: partial sum l (of 64) takes elements 256k + 4l + e (k ascending,
+ * e = 0..3) with fmaf, then a xor butterfly over the 64 partial sums. d % 4 == 0. */
 void orc_priors(const float *features, const float *router_w, int T, int n, int d, float *priors);
 
 /* ---- int4 base weights (MLX layout) ---- */
