@@ -44,6 +44,7 @@ SOURCES = [
     "aoship_router.hip",
     "aoship_lora.hip",
     "aoship_gemv.hip",
+    "aoship_gemm.hip",
     "aoship_api.cpp",
 ]
 

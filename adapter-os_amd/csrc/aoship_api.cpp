@@ -173,7 +173,6 @@ struct aoship_router {
 
 extern "C" aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, float eps,
                                               float routing_bias, const uint64_t *stable_ids) {
-  if (ensure_device()) return nullptr;
   if (n_adapters < 1 || n_adapters > AOS_MAX_ADAPTERS) {
     set_err("aoship_router_new: n_adapters must be in [1, 4096]");
     return nullptr;
@@ -183,6 +182,7 @@ extern "C" aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, 
     set_err("Adapter routing failed: K exceeds maximum allowed value of 8");
     return nullptr;
   }
+  if (ensure_device()) return nullptr;
   auto *r = new aoship_router();
   r->n = n_adapters;
   r->k = k < 1 ? 1 : k; /* sanitize_k (router.rs:127-142) */
@@ -392,9 +392,28 @@ struct PendingEvent {
   hipEvent_t a, b;
 };
 
-enum { KS_ROUTE = 0, KS_SHRINK_X, KS_GEMV_GU, KS_SHRINK_H, KS_GEMV_DOWN, KS_GEMV_PROJ, KS_COUNT };
-static const char *kStatNames[KS_COUNT] = {"route",         "lora_shrink_x", "q4_gemv_gate_up",
-                                           "lora_shrink_h", "q4_gemv_down",  "q4_gemv_proj"};
+enum {
+  KS_ROUTE = 0,
+  KS_SHRINK_X,
+  KS_GEMV_GU,
+  KS_SHRINK_H,
+  KS_GEMV_DOWN,
+  KS_GEMV_PROJ,
+  KS_PPLAN,
+  KS_PSHRINK_X,
+  KS_PFINISH_X,
+  KS_GEMM_GU,
+  KS_PSHRINK_H,
+  KS_PFINISH_H,
+  KS_GEMM_DOWN,
+  KS_GEMM_PROJ,
+  KS_COUNT
+};
+static const char *kStatNames[KS_COUNT] = {
+    "route",         "lora_shrink_x",   "q4_gemv_gate_up", "lora_shrink_h",
+    "q4_gemv_down",  "q4_gemv_proj",    "prefill_plan",
+    "lora_pshrink_x", "lora_pfinish_x", "q4_gemm_gate_up", "lora_pshrink_h",
+    "lora_pfinish_h", "q4_gemm_down",   "q4_gemm_proj"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -869,18 +888,160 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   P.ctr = cv.coff + 64;
 }
 
+/* ---- prefill (T > 32 tokens) ---- */
+
+/* Plan of one prefill chunk: the adapter union and coefficients, then per module set a shrink
+ * (S over the union's rank rows, ks partial sums) and the GEMMs that consume it. */
+struct PrefillPlan {
+  aos_pplan_params pp;
+  int umax = 1, mtiles = 0;
+};
+
+static void plan_prefill_common(aoship_layer *l, Carve &cv, const aoship_ring_t *rings, int T, PrefillPlan &P) {
+  const int n = (int)l->table.size();
+  int umax = n < 8 * T ? n : 8 * T;
+  if (umax < 1) umax = 1;
+  P.umax = umax;
+  P.mtiles = ceil_div(T, AOS_GEMM_BM);
+  aos_pplan_params &pp = P.pp;
+  memset(&pp, 0, sizeof(pp));
+  pp.rings = rings;
+  pp.T = T;
+  pp.n = n;
+  pp.bound = l->bound.as<uint8_t>();
+  pp.scale = l->scale_all.as<float>();
+  pp.plan = cv.b.take<aos_pplan>(1);
+  pp.cstride = umax;
+  pp.coef = cv.b.take<float>((size_t)T * umax);
+  pp.mwords = ceil_div(umax, 32);
+  pp.tile_mask = cv.b.take<uint32_t>((size_t)P.mtiles * pp.mwords);
+}
+
+/* Shrink over the union for nm modules sharing x: K splits so that the grid has about 512
+ * workgroups, at least 4 groups per split and at most 16 splits. */
+static void plan_pshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const uint16_t *x, int T, int in,
+                         const aos_lora_tab *tabs, int nm, aos_pshrink_params &sp) {
+  memset(&sp, 0, sizeof(sp));
+  sp.x = x;
+  sp.T = T;
+  sp.in = in;
+  sp.nmod = nm;
+  sp.plan = P.pp.plan;
+  sp.umax = P.umax;
+  sp.coef = P.pp.coef;
+  sp.cstride = P.pp.cstride;
+  sp.mtiles = P.mtiles;
+  sp.zero_row = l->zeros.as<uint16_t>();
+  int off = 0, cols_max = 0;
+  for (int i = 0; i < nm; ++i) {
+    sp.tab[i] = tabs[i];
+    sp.s_off[i] = off;
+    const int c = P.umax * tabs[i].rpad;
+    off += c;
+    cols_max = c > cols_max ? c : cols_max;
+  }
+  sp.s_stride = off > 0 ? off : 16;
+  sp.cblocks = ceil_div(cols_max, 128);
+  const int G = in / 64;
+  const int wg = P.mtiles * (sp.cblocks > 0 ? sp.cblocks : 1) * nm;
+  int ks = ceil_div(512, wg);
+  int cap = G / 4;
+  if (cap < 1) cap = 1;
+  if (cap > 16) cap = 16;
+  if (ks > cap) ks = cap;
+  if (ks < 1) ks = 1;
+  sp.gpk = ceil_div(G, ks);
+  sp.ks = ceil_div(G, sp.gpk);
+  sp.SA = cv.b.take<uint16_t>((size_t)T * sp.s_stride);
+  sp.part = sp.ks > 1 ? cv.b.take<float>((size_t)sp.ks * T * sp.s_stride) : nullptr;
+}
+
+static void plan_gemm(const PrefillPlan &P, const aos_pshrink_params &sp, const Q4Mat &W0, const Q4Mat *W1,
+                      const uint16_t *x, int T, const aos_lora_tab &t0, int off0, const aos_lora_tab *t1,
+                      int off1, uint16_t *y, aos_gemm_params &g) {
+  memset(&g, 0, sizeof(g));
+  g.w0 = W0.dev();
+  if (W1) g.w1 = W1->dev();
+  g.x = x;
+  g.T = T;
+  g.mb = P.mtiles;
+  g.nb = ceil_div(W0.RB, 4); /* 4 row blocks (128 rows) per workgroup */
+  g.tab0 = t0;
+  if (t1) g.tab1 = *t1;
+  g.SA = sp.SA;
+  g.sa_stride = sp.s_stride;
+  g.s_off0 = off0;
+  g.s_off1 = off1;
+  g.plan = P.pp.plan;
+  g.tile_mask = P.pp.tile_mask;
+  g.mwords = P.pp.mwords;
+  g.y = y;
+}
+
+struct MlpPrefill {
+  PrefillPlan P;
+  aos_pshrink_params sx, sh;
+  aos_gemm_params g1, g2;
+  size_t bytes = 0, ctr = 0;
+};
+
+static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const aoship_ring_t *rings, uint16_t *y,
+                             void *ws, void *ctr, MlpPrefill &M) {
+  const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
+  const int H = Wg.in, I = Wg.out;
+  aos_lora_tab tgu[2] = {lora_tab(l, MOD_GATE, H, I), lora_tab(l, MOD_UP, H, I)};
+  aos_lora_tab td = lora_tab(l, MOD_DOWN, I, H);
+  Carve cv(ws, ctr);
+  plan_prefill_common(l, cv, rings, T, M.P);
+  uint16_t *h = cv.b.take<uint16_t>((size_t)T * I);
+  plan_pshrink(l, cv, M.P, x, T, H, tgu, 2, M.sx);
+  plan_gemm(M.P, M.sx, Wg, &Wu, x, T, tgu[0], M.sx.s_off[0], &tgu[1], M.sx.s_off[1], h, M.g1);
+  plan_pshrink(l, cv, M.P, h, T, I, &td, 1, M.sh);
+  plan_gemm(M.P, M.sh, Wd, nullptr, h, T, td, 0, nullptr, 0, y, M.g2);
+  M.bytes = cv.b.off + 256;
+  M.ctr = cv.coff + 64;
+}
+
+static int launch_err(int e, const char *what);
+
+/* Launch the prefill plan (union, coefficients, tile masks). */
+static int launch_pplan(aoship_layer *l, const aos_pplan_params &pp) {
+  aos_launch_ctx c0 = launch_ctx(l, KS_PPLAN);
+  return launch_err(aos_launch_pplan(&pp, &c0), "prefill plan");
+}
+
+/* Launch a prefill shrink and, with K splits, its finishing sum (nothing when no bound adapter
+ * has these modules). */
+static int launch_pshrink(aoship_layer *l, const aos_pshrink_params &sp, int slot_shrink, int slot_finish) {
+  if (sp.cblocks == 0) return 0;
+  aos_launch_ctx c0 = launch_ctx(l, slot_shrink);
+  if (launch_err(aos_launch_pshrink(&sp, &c0), "lora shrink (prefill)")) return -1;
+  if (sp.ks == 1) return 0;
+  aos_launch_ctx c1 = launch_ctx(l, slot_finish);
+  return launch_err(aos_launch_pfinish(&sp, &c1), "lora shrink sum (prefill)");
+}
+
+static int chunk_prefill_t(int T) { return T < AOS_PREFILL_MAX_T ? T : AOS_PREFILL_MAX_T; }
+
 extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
   if (!l) return set_err("aoship_layer_reserve: null layer");
   if (max_tokens < 1) return set_err("aoship_layer_reserve: max_tokens must be >= 1");
   if (ensure_device()) return -1;
   size_t bytes = 0, ctr = 0;
+  const bool mlp = l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid;
   for (int T = 1; T <= AOS_DECODE_MAX_T && T <= max_tokens; T *= 2) {
-    if (l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid) {
+    if (mlp) {
       MlpPlan P;
       plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, P);
       if (P.bytes > bytes) bytes = P.bytes;
       if (P.ctr > ctr) ctr = P.ctr;
     }
+  }
+  if (mlp && max_tokens > AOS_DECODE_MAX_T) {
+    MlpPrefill M;
+    plan_mlp_prefill(l, chunk_prefill_t(max_tokens), nullptr, nullptr, nullptr, nullptr, nullptr, M);
+    if (M.bytes > bytes) bytes = M.bytes;
+    if (M.ctr > ctr) ctr = M.ctr;
   }
   return ws_reserve(l, bytes, ctr);
 }
@@ -917,6 +1078,23 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
   if (Wu.in != Wg.in || Wu.out != Wg.out || Wd.in != Wg.out || Wd.out != Wg.in)
     return set_err("aoship_mlp_forward: gate/up/down shapes are inconsistent");
   const int H = Wg.in;
+  if (T > AOS_DECODE_MAX_T) {
+    for (int t0 = 0; t0 < T; t0 += AOS_PREFILL_MAX_T) {
+      const int Tc = chunk_prefill_t(T - t0);
+      MlpPrefill M;
+      plan_mlp_prefill(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, M);
+      if (ws_reserve(l, M.bytes, M.ctr)) return -1;
+      plan_mlp_prefill(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, M);
+      if (launch_pplan(l, M.P.pp)) return -1;
+      if (launch_pshrink(l, M.sx, KS_PSHRINK_X, KS_PFINISH_X)) return -1;
+      aos_launch_ctx c2 = launch_ctx(l, KS_GEMM_GU);
+      if (launch_err(aos_launch_gemm(&M.g1, 1, &c2), "q4 gemm gate/up")) return -1;
+      if (launch_pshrink(l, M.sh, KS_PSHRINK_H, KS_PFINISH_H)) return -1;
+      aos_launch_ctx c4 = launch_ctx(l, KS_GEMM_DOWN);
+      if (launch_err(aos_launch_gemm(&M.g2, 0, &c4), "q4 gemm down")) return -1;
+    }
+    return 0;
+  }
   for (int t0 = 0; t0 < T; t0 += AOS_DECODE_MAX_T) {
     const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;
     MlpPlan P;
@@ -942,6 +1120,33 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
     if (!l->mats[mods[i]].valid) return set_err("projection weights not set");
     if (l->mats[mods[i]].in != in) return set_err("projections sharing x must share in_features");
     if (!ys[i] || !aligned16(ys[i])) return set_err("forward: output must be 16-byte aligned");
+  }
+  if (T > AOS_DECODE_MAX_T) {
+    for (int t0 = 0; t0 < T; t0 += AOS_PREFILL_MAX_T) {
+      const int Tc = chunk_prefill_t(T - t0);
+      const uint16_t *xc = x + (size_t)t0 * in;
+      aos_lora_tab tabs[3];
+      for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
+      PrefillPlan P;
+      aos_pshrink_params sp;
+      aos_gemm_params gp[3];
+      for (int pass = 0; pass < 2; ++pass) {
+        Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr);
+        plan_prefill_common(l, cv, rings + t0, Tc, P);
+        plan_pshrink(l, cv, P, xc, Tc, in, tabs, nm, sp);
+        for (int i = 0; i < nm; ++i)
+          plan_gemm(P, sp, l->mats[mods[i]], nullptr, xc, Tc, tabs[i], sp.s_off[i], nullptr, 0,
+                    ys[i] + (size_t)t0 * l->mats[mods[i]].out, gp[i]);
+        if (pass == 0 && ws_reserve(l, cv.b.off + 256, cv.coff + 64)) return -1;
+      }
+      if (launch_pplan(l, P.pp)) return -1;
+      if (launch_pshrink(l, sp, KS_PSHRINK_X, KS_PFINISH_X)) return -1;
+      for (int i = 0; i < nm; ++i) {
+        aos_launch_ctx cg = launch_ctx(l, KS_GEMM_PROJ);
+        if (launch_err(aos_launch_gemm(&gp[i], 0, &cg), "q4 gemm")) return -1;
+      }
+    }
+    return 0;
   }
   for (int t0 = 0; t0 < T; t0 += AOS_DECODE_MAX_T) {
     const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;

@@ -129,6 +129,71 @@ typedef struct {
   uint32_t *counters; /* [RB] zero between launches */
 } aos_gemv_params;
 
+/* ---- prefill path (T > 32 tokens) ----
+ * The call's adapter union: list[u] = adapter of union slot u (ascending), slot[a] = u or -1.
+ * coef[t][u] = sum over token t's active ring slots of adapter list[u] of scale * q / 32767;
+ * tile_mask[mt][w] bit b = some token of M tile mt has a nonzero coefficient for slot 32 w + b. */
+#define AOS_PREFILL_MAX_T 4096
+#define AOS_GEMM_BM 128 /* tokens per M tile */
+typedef struct {
+  int U;
+  int pad[3];
+  uint16_t list[AOS_MAX_ADAPTERS];
+  int16_t slot[AOS_MAX_ADAPTERS];
+} aos_pplan;
+
+typedef struct {
+  const aoship_ring_t *rings;
+  int T, n;
+  const uint8_t *bound;
+  const float *scale;
+  aos_pplan *plan;
+  float *coef;          /* [T][cstride] */
+  int cstride;          /* >= union size bound */
+  uint32_t *tile_mask;  /* [mtiles][mwords] */
+  int mwords;
+} aos_pplan_params;
+
+/* Shrink over the union for T tokens, finished with the coefficients:
+ *   SA[t][s_off[i] + u * rpad_i + j] = bf16(coef[t][u] * sum_i x[t][i] A_{list[u]}[j][i])
+ * for module i. K is split over ks workgroups; with ks > 1 their float32 partials go to
+ * part[kz][t][...] and a second kernel adds them in split order. */
+typedef struct {
+  const uint16_t *x; /* [T][in] */
+  int T, in;
+  int nmod;
+  aos_lora_tab tab[3];
+  int s_off[3];
+  const aos_pplan *plan;
+  int umax;             /* union slots covered by the grid */
+  const float *coef;    /* [T][cstride] */
+  int cstride;
+  uint16_t *SA;         /* [T][s_stride] bf16 */
+  float *part;          /* [ks][T][s_stride] float32 (ks > 1) */
+  int s_stride;
+  int ks;               /* K splits */
+  int gpk;              /* groups per K split */
+  int mtiles, cblocks;  /* grid extents (column blocks of 128) */
+  const uint16_t *zero_row;
+} aos_pshrink_params;
+
+/* int4 GEMM with LoRA expand: y[t][o] = sum_i x[t][i] w[o][i] +
+ * sum_u SA[t][s_off + u * rpad + j] . B_{list[u]}[o][j] over the union slots u used by the token
+ * tile. SwiGLU mode computes gate (w0) and up (w1) and writes (g * sigmoid(g)) * u. */
+typedef struct {
+  aos_q4_dev w0, w1;
+  const uint16_t *x;  /* [T][in] */
+  int T;
+  int mb, nb;         /* M tiles, N blocks */
+  aos_lora_tab tab0, tab1;
+  const uint16_t *SA; /* [T][sa_stride] bf16 */
+  int sa_stride, s_off0, s_off1;
+  const aos_pplan *plan;
+  const uint32_t *tile_mask;
+  int mwords;
+  uint16_t *y;        /* [T][out] */
+} aos_gemm_params;
+
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
  * records at kernel start and end (hipExtLaunchKernelGGL). */
 typedef struct {
@@ -153,6 +218,10 @@ extern "C" {
 int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx);
 int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);
+int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
+int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
+int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 #ifdef __cplusplus
 }
 #endif

@@ -34,25 +34,37 @@ def log(msg: str) -> None:
 
 
 class MlpCase:
-    """A device-resident layer, router and inputs for T tokens of a workload."""
+    """Device-resident layers, router and inputs for T tokens of a workload.
 
-    def __init__(self, aoship, W, cid: int, T: int, torch):
+    n_layers distinct copies of the layer (own int4 weights and own LoRA weights per layer, as
+    consecutive transformer layers have) are cycled step by step, so that every step streams its
+    weights from HBM: one 7B-shaped layer (123 MB) would otherwise stay resident in the 256 MB
+    last-level cache across back-to-back calls."""
+
+    def __init__(self, aoship, W, cid: int, T: int, torch, n_layers: int = 1):
         self.cfg = cfg = W.CONFIGS[cid]
         self.T = T
         self.torch = torch
-        self.layer = aoship.Layer(0)
-        for m in cfg.modules:
-            p, s, b = W.base_weights(cfg, m)
-            self.layer.set_base(m, p, s, b)
+        self.n_layers = n_layers
+        base = {m: W.base_weights(cfg, m) for m in cfg.modules}
         self.adapters = []
         for a in range(cfg.n_adapters):
-            ad = aoship.LoraAdapter(a, 1, W.lora_scale(cfg))
+            ad = aoship.LoraAdapter(a, n_layers, W.lora_scale(cfg))
             for m in cfg.modules:
                 A, B = W.lora_weights(cfg, a, m)
-                ad.set_module(0, m, A, B)
+                for li in range(n_layers):
+                    ad.set_module(li, m, A, B)
             self.adapters.append(ad)
-        self.layer.set_adapters(self.adapters)
-        self.layer.reserve(T)
+        self.layers = []
+        for li in range(n_layers):
+            layer = aoship.Layer(li)
+            for m in cfg.modules:
+                p, s, b = base[m]
+                layer.set_base(m, p, s, b)
+            layer.set_adapters(self.adapters)
+            layer.reserve(T)
+            self.layers.append(layer)
+        del base
         sid = np.arange(cfg.n_adapters, dtype=np.uint64)
         self.router = aoship.Router(cfg.n_adapters, cfg.k, cfg.tau, cfg.eps, 1.0, sid)
         xb, _ = W.activations(cfg, T)
@@ -66,13 +78,27 @@ class MlpCase:
             self.priors = None
         else:
             self.priors = torch.from_numpy(W.priors(cfg, T)).cuda()
+        self.i = 0
 
     def step(self):
         if self.priors is None:
             self.router.route_features(self.f, self.w, self.rings)
         else:
             self.router.route(self.priors, self.rings)
-        self.layer.mlp_forward(self.x, self.rings, self.y)
+        self.layers[self.i % self.n_layers].mlp_forward(self.x, self.rings, self.y)
+        self.i += 1
+
+    def set_profiling(self, on: bool):
+        for layer in self.layers:
+            layer.set_profiling(on)
+
+    def kernel_stats(self) -> dict:
+        tot = {}
+        for layer in self.layers:
+            for k, (ms, n) in layer.kernel_stats().items():
+                a, b = tot.get(k, (0.0, 0))
+                tot[k] = (a + ms, b + n)
+        return tot
 
     def distinct_adapters(self, aoship) -> int:
         self.torch.cuda.synchronize()
@@ -102,12 +128,12 @@ def time_steps(case, steps: int, warmup: int, torch) -> float:
 
 def kernel_times(case, steps: int, torch) -> dict:
     """Average per-launch kernel durations (ms) from events the dispatches record."""
-    case.layer.set_profiling(True)
+    case.set_profiling(True)
     for _ in range(steps):
         case.step()
     torch.cuda.synchronize()
-    st = case.layer.kernel_stats()
-    case.layer.set_profiling(False)
+    st = case.kernel_stats()
+    case.set_profiling(False)
     return {k: ms / n for k, (ms, n) in st.items() if n}
 
 
@@ -171,6 +197,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--layers", type=int, default=4,
+                    help="distinct layer copies cycled by the decode steps (defeats the last-level cache)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the hot path runs on a single MI355X and has no multi-GPU "
@@ -187,7 +215,7 @@ def main() -> int:
 
     # ---- headline: 7B-shaped decode, one token ----
     T = 1
-    dec = MlpCase(aoship, W, 2, T, torch)
+    dec = MlpCase(aoship, W, 2, T, torch, args.layers)
     ms = time_steps(dec, args.steps, args.warmup, torch)
     U = dec.distinct_adapters(aoship)
     kt = kernel_times(dec, max(20, args.steps // 4), torch)
@@ -213,9 +241,10 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": "Qwen2.5-7B-shaped int4 (g64) SwiGLU MLP, 16 rank-16 LoRA adapters on gate/up/down, "
-                        "K=4 Q15 router over 3584-dim features, decode of 1 token",
+                        "K=4 Q15 router over 3584-dim features, decode of 1 token; each step routes the token "
+                        "and runs the next of %d distinct layer copies" % args.layers,
             "hidden": cfg.hidden, "intermediate": cfg.inter, "tokens": T, "adapters": cfg.n_adapters,
-            "rank": cfg.rank, "k": cfg.k,
+            "rank": cfg.rank, "k": cfg.k, "layers_cycled": args.layers,
         },
         "layer_hbm_gbps": layer_bytes / (ms * 1e-3) / 1e9,
         "roofline": {
@@ -235,7 +264,7 @@ def main() -> int:
 
     # ---- 8-token decode batch ----
     T8 = 8
-    d8 = MlpCase(aoship, W, 2, T8, torch)
+    d8 = MlpCase(aoship, W, 2, T8, torch, args.layers)
     ms8 = time_steps(d8, args.steps, args.warmup, torch)
     U8 = d8.distinct_adapters(aoship)
     result["decode_t8"] = {
@@ -249,10 +278,13 @@ def main() -> int:
 
     # ---- 2048-token prefill ----
     if not args.skip_prefill:
-        pf = MlpCase(aoship, W, 3, 2048, torch)
-        msp = time_steps(pf, max(3, args.steps // 20), 2, torch)
+        pf = MlpCase(aoship, W, 3, 2048, torch, 1)
+        msp = time_steps(pf, max(5, args.steps // 10), 3, torch)
+        kp = kernel_times(pf, max(5, args.steps // 20), torch)
         flops = W.algorithmic_flops(pf.cfg, 2048)
         tflops = flops / (msp * 1e-3) / 1e12
+        H, I = pf.cfg.hidden, pf.cfg.inter
+        gu_flops = 2 * 2048 * H * 2 * I
         result["prefill"] = {
             "tokens": 2048,
             "tok_s": 2048 / (msp * 1e-3),
@@ -261,8 +293,11 @@ def main() -> int:
             "achieved_tflops": tflops,
             "mfma_util": tflops / BF16_PEAK_TFLOPS,
             "peak_tflops": BF16_PEAK_TFLOPS,
+            "kernels_us": {k: v * 1e3 for k, v in kp.items()},
+            "gemm_gate_up_tflops": gu_flops / (kp["q4_gemm_gate_up"] * 1e-3) / 1e12 if "q4_gemm_gate_up" in kp else None,
         }
-        log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s")
+        log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s; kernels (us): " +
+            ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kp.items()))
         del pf
 
     if not args.skip_cpu:

@@ -27,7 +27,7 @@
  *       :3445-3455 (q/k/v + LoRA), :3499-3501 (o + LoRA), :3509-3527 (MLP + LoRA).
  *   - CPU multi-LoRA blend: crates/adapteros-lora-kernel-api/src/liquid.rs:163-257.
  *
- * Parity status per function (how each is pinned is listed in tests/test_oracle_*.py):
+ * Parity status per function (how each is pinned: tests/test_oracle_router.py, tests/test_oracle_layer.py):
  *   orc_route_*        pinned by the reference's router KATs, Q15 KATs, closed forms and
  *                      brute force over tie permutations.
  *   orc_quantize_gate  pinned by quantization.rs:335-349 known answers.

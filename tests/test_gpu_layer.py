@@ -56,16 +56,117 @@ def test_mlp_no_adapters_matches_base(hip):
 
 
 def test_mlp_prefill_shape_parity(hip):
-    """2048-token prefill of the 7B-shaped layer, checked on a sample of tokens."""
+    """2048-token prefill of the 7B-shaped layer (matrix-core GEMM path), checked on a sample
+    of tokens across tile boundaries, and bit-identical run to run."""
     cid, T = 3, 2048
     xb, xf = W.activations(W.CONFIGS[cid], T)
     rings, _ = rings_for(cid, T)
     layer, ads = gpu_layer(hip, cid)
     y = _run_mlp(hip, layer, xb, rings)
-    sample = np.array([0, 1, 2, 31, 32, 33, 511, 1024, 1500, 2046, 2047])
+    y2 = _run_mlp(hip, layer, xb, rings)
+    assert np.array_equal(y, y2), "run-to-run outputs differ"
+    sample = np.array([0, 1, 2, 31, 32, 33, 127, 128, 511, 1024, 1500, 2046, 2047])
     ref = oracle_mlp(cid, xf[sample], rings[sample])
     got = W.bf16_bits_to_f32(y.reshape(T, -1)[sample])
     assert tol_ratio(got, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("T", [33, 100, 128, 129, 300])
+def test_mlp_prefill_ragged_full_parity(hip, T):
+    """Prefill path at token counts around the 128-token tile (0.5B-shaped layer, every token
+    checked)."""
+    cid = 1
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    y = _run_mlp(hip, layer, xb, rings)
+    ref = oracle_mlp(cid, xf, rings)
+    ratio = tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
+    assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
+
+
+def test_mlp_prefill_mixed_rings(hip):
+    """Prefill with empty rings, zero gates and out-of-table indices mixed in: those slots add
+    nothing (backend.rs:409-425)."""
+    cid, T = 1, 160
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    rings = rings.copy()
+    rings[5:40] = np.zeros(35, dtype=rings.dtype)
+    rings["gates_q15"][50:60, 0] = 0
+    rings["adapter_indices"][70:80, 1] = 999
+    layer, ads = gpu_layer(hip, cid)
+    y = _run_mlp(hip, layer, xb, rings)
+    ref = oracle_mlp(cid, xf, rings)
+    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+
+
+def test_projections_prefill_parity(hip):
+    """q/k/v and o projections of the 3B-shaped attention layer at 96 tokens (GEMM path)."""
+    import torch
+
+    cid, T = 4, 96
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    x = _dev(xb.view(np.int16))
+    r = _dev(rings.view(np.uint8))
+    q = torch.empty((T, cfg.q_out), dtype=torch.int16, device="cuda")
+    k = torch.empty((T, cfg.kv_out), dtype=torch.int16, device="cuda")
+    v = torch.empty((T, cfg.kv_out), dtype=torch.int16, device="cuda")
+    layer.qkv_forward(x, r, q, k, v)
+    o = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
+    layer.proj_forward("o_proj", x, r, o)
+    torch.cuda.synchronize()
+    for name, dev in (("q_proj", q), ("k_proj", k), ("v_proj", v), ("o_proj", o)):
+        got = W.bf16_bits_to_f32(dev.cpu().numpy().view(np.uint16))
+        ref = oracle_proj(cid, name, xf, rings)
+        ratio = tol_ratio(got.reshape(ref.shape), ref)
+        assert ratio <= REL_TOL, f"{name}: {ratio:.4g}"
+
+
+def test_lora_projection_known_answer(hip):
+    """crates/adapteros-lora-mlx-ffi/src/lora_cpp_tests.rs:57-119 through the C ABI: W = I,
+    x = [2, 3], A = [[1, 1]], B = [[1], [2]], scale 1, gate q = 16384 -> [2 + 5g, 3 + 10g],
+    g = 16384 / 32767 (the 2x2 case embedded in a 32 x 64 int4 projection), on the decode and
+    the prefill path."""
+    import torch
+
+    out, n = 32, 64
+    q = np.zeros((out, n), np.uint32)
+    for o in range(out):
+        q[o, o] = 1
+    packed = np.zeros((out, n // 8), np.uint32)
+    for j in range(8):
+        packed |= q[:, j::8] << np.uint32(4 * j)
+    scales = np.full((out, 1), 0x3C00, np.uint16)  # float16 1.0
+    biases = np.zeros((out, 1), np.uint16)
+    layer = hip.Layer(0)
+    layer.set_base("q_proj", packed, scales, biases)
+    A = np.zeros((1, n), np.float32)
+    A[0, :2] = 1
+    B = np.zeros((out, 1), np.float32)
+    B[:2, 0] = [1, 2]
+    ad = hip.LoraAdapter(1, 1, 1.0)
+    ad.set_module(0, "q_proj", A, B)
+    layer.set_adapters([ad])
+    g = np.float32(16384) / np.float32(32767)
+    for T in (1, 40):
+        xb = np.zeros((T, n), np.uint16)
+        xb[:, 0] = 0x4000  # bf16 2.0
+        xb[:, 1] = 0x4040  # bf16 3.0
+        rings = np.zeros(T, hip.RING_DTYPE)
+        rings["top_k"] = 1
+        rings["gates_q15"][:, 0] = 16384
+        y = torch.empty((T, out), dtype=torch.int16, device="cuda")
+        layer.proj_forward("q_proj", _dev(xb.view(np.int16)), _dev(rings.view(np.uint8)), y)
+        torch.cuda.synchronize()
+        yf = W.bf16_bits_to_f32(y.cpu().numpy().view(np.uint16)).reshape(T, out)
+        # bf16 output: 2 + 5 g = 4.50008 rounds to 4.5, 3 + 10 g = 8.00015 to 8.0
+        assert np.allclose(yf[:, 0], 2 + 5 * g, atol=2e-2) and np.allclose(yf[:, 1], 3 + 10 * g, atol=4e-2)
+        assert np.all(yf[:, 2:] == 0)
 
 
 def test_attention_projections_parity(hip):

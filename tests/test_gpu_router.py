@@ -6,6 +6,9 @@ device for configs 1, 2, 4; prototype priors for 3; adversarial ties / signed ze
 boundaries / dominance with eps = 0 for 5), N above one wavefront, policy masks and the
 non-finite error path.
 """
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -48,37 +51,36 @@ def _first_diff(g, o):
     return "equal"
 
 
-KATS = [
-    # determinism.rs:38-87 -> [1, 2, 0]
-    dict(priors=[0.5, 0.5, 0.5, 0.3, 0.2], ids=[300, 100, 200, 400, 500], k=3, eps=0.01, idx=[1, 2, 0]),
-    # determinism.rs:537-574 -> [0, 2, 1]
-    dict(priors=[0.9, 0.5, 0.5, 0.5, 0.1], ids=[10, 200, 100, 300, 400], k=3, eps=0.01, idx=[0, 2, 1]),
-    # determinism.rs:908-1090: equal priors -> 0..K
-    dict(priors=[0.25] * 8, ids=None, k=4, eps=0.02, idx=[0, 1, 2, 3]),
-    # q15_edge_cases.rs:155-192: single adapter -> 32767
-    dict(priors=[1.0], ids=None, k=1, eps=0.02, idx=[0], q=[32767]),
-]
+GOLDEN = Path(__file__).resolve().parent / "golden"
+KATS = json.loads((GOLDEN / "router_kats.json").read_text())["cases"]
 
 
-@pytest.mark.parametrize("kat", KATS)
+@pytest.mark.parametrize("kat", KATS, ids=lambda c: c["name"])
 def test_router_reference_kats(hip, kat):
+    """The reference's router known answers (sources cited in the fixture), bit-exact with the
+    oracle and equal to the asserted indices / gates."""
     pri = np.array([kat["priors"]], np.float32)
-    ids = None if kat["ids"] is None else np.array(kat["ids"], np.uint64)
-    g, st = _gpu_route(hip, pri, kat["k"], 1.0, kat["eps"], 1.0, ids)
-    o = _oracle_rings(pri, kat["k"], 1.0, kat["eps"], 1.0, ids)
+    ids = np.array(kat["stable_ids"], np.uint64)
+    allowed = None if kat.get("allowed") is None else np.array(kat["allowed"], np.uint8)
+    g, st = _gpu_route(hip, pri, kat["k"], kat["tau"], kat["eps"], 1.0, ids, allowed)
+    o = _oracle_rings(pri, kat["k"], kat["tau"], kat["eps"], 1.0, ids, allowed)
     assert st[0] == 0
     _assert_rings_equal(g, o)
     kk = int(g[0]["top_k"])
-    assert list(g[0]["adapter_indices"][:kk]) == kat["idx"]
-    if "q" in kat:
-        assert list(g[0]["gates_q15"][:kk]) == kat["q"]
+    assert list(g[0]["adapter_indices"][:kk]) == kat["expect_indices"]
+    if kat.get("expect_gates") is not None:
+        assert list(g[0]["gates_q15"][:kk]) == kat["expect_gates"]
 
 
-def test_router_masked_single(hip):
-    # q15_edge_cases.rs:74-135: the other adapter denied by policy -> one adapter, gate 32767
-    pri = np.array([[1.0, 1.0]], np.float32)
-    g, _ = _gpu_route(hip, pri, 2, allowed=np.array([1, 0], np.uint8))
-    assert int(g[0]["top_k"]) == 1 and g[0]["adapter_indices"][0] == 0 and g[0]["gates_q15"][0] == 32767
+def test_router_adversarial_fixture(hip):
+    """Committed 64-adapter adversarial vectors (ties, signed zeros, Q15 boundaries with eps = 0,
+    a dominant adapter): the device rings equal the fixture byte for byte."""
+    fx = np.load(GOLDEN / "router_adversarial.npz")
+    pri = fx["priors"]
+    sid = np.arange(pri.shape[1], dtype=np.uint64)
+    g, st = _gpu_route(hip, pri, int(fx["k"]), float(fx["tau"]), float(fx["eps"]), 1.0, sid)
+    assert (st == 0).all()
+    assert g.tobytes() == fx["rings"].tobytes()
 
 
 @pytest.mark.parametrize("cid,T", [(1, 1), (2, 1), (2, 8), (3, 2048), (4, 32), (5, 4096)])
