@@ -146,6 +146,37 @@ def gate_up_bytes(cfg, T: int, U: int) -> int:
     return base + lora + T * H * 2 + T * I * 2
 
 
+PROFILES = ROOT / "profiles"
+TRAFFIC_FILE = PROFILES / "q4_gemv_gate_up__qwen7b_decode_t1__hbm_traffic.md"
+COPY_BYTES = 512 << 20
+
+
+def probe(aoship, W, torch, layers: int) -> int:
+    """Workload for the hardware-counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): 50 decode
+    steps of the headline workload, then one device copy of COPY_BYTES that calibrates the
+    counters (it reads and writes exactly COPY_BYTES)."""
+    dec = MlpCase(aoship, W, 2, 1, torch, layers)
+    for _ in range(50):
+        dec.step()
+    torch.cuda.synchronize()
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("probe done")
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate/up GEMV from the committed counter summary, or None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(W, T: int = 1) -> dict:
     """The C oracle (float32, dequantising on the fly, OpenMP over output rows) on this host: a
     bounded sample of the decode workload, routing included."""
@@ -197,6 +228,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="run the hardware-counter workload only (see probe())")
     ap.add_argument("--layers", type=int, default=4,
                     help="distinct layer copies cycled by the decode steps (defeats the last-level cache)")
     args = ap.parse_args()
@@ -212,6 +245,8 @@ def main() -> int:
 
     aoship.init(0)
     log(f"device: {aoship.device_name()}")
+    if args.probe:
+        return probe(aoship, W, torch, args.layers)
 
     # ---- headline: 7B-shaped decode, one token ----
     T = 1
@@ -254,7 +289,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_bytes": gu_bytes,
             "avg_launch_us": gu_ms * 1e3,
         },

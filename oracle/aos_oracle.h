@@ -30,7 +30,7 @@
  * Parity status per function (how each is pinned: tests/test_oracle_router.py, tests/test_oracle_layer.py):
  *   orc_route_*        pinned by the reference's router KATs, Q15 KATs, closed forms and
  *                      brute force over tie permutations.
- *   orc_quantize_gate  pinned by quantization.rs:335-349 known answers.
+ *   orc_quantize_gate  pinned by quantization.rs:239-252 known answers.
  *   orc_dequant_q4     pinned by the closed form over every nibble value and lane position.
  *   orc_liquid_blend   pinned by liquid.rs:267-336 (-> [2.0, 4.0]).
  *   orc_lora_delta     pinned by the lora_cpp_tests.rs:57-119 KAT and closed forms.
