@@ -1,0 +1,426 @@
+// aos_kernel_api.hpp — C++ host side of the MI355X hot path, above the C ABI (include/aoship.h).
+//
+// Mirrors, for the adapter-augmented layer path, the Rust types a backend of adapterOS works with:
+//   RouterRing                crates/adapteros-lora-kernel-api/src/lib.rs:57-214
+//   AdapterLoadMetadata       crates/adapteros-lora-kernel-api/src/lib.rs:249-257
+//   AdapterInfo / Decision    crates/adapteros-lora-router/src/types.rs:645-707
+//   PolicyMask (allow/deny)   crates/adapteros-lora-router/src/policy_mask.rs
+//   Router                    crates/adapteros-lora-router/src/router.rs:397-428, 556-562,
+//                             769-785 (construction), 1567-1952 (deterministic routing)
+//   FusedKernels (hot-swap, device_name, attest_determinism, layer forwards)
+//                             crates/adapteros-lora-kernel-api/src/lib.rs:308-716
+// Errors are thrown as AosError with the reference's error kinds (AosError::Kernel, ::Validation,
+// ::Routing, ::DeterminismViolation); a Rust Result<T> maps to a return value or a throw.
+//
+// Header-only; link against libaoship.so and the HIP runtime (device buffers for the host-side
+// routing convenience call).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/aoship.h"
+
+namespace adapteros {
+
+enum class ErrorKind { Kernel, Validation, Routing, DeterminismViolation };
+
+class AosError : public std::runtime_error {
+ public:
+  AosError(ErrorKind kind, const std::string &msg) : std::runtime_error(msg), kind_(kind) {}
+  ErrorKind kind() const { return kind_; }
+
+ private:
+  ErrorKind kind_;
+};
+
+namespace detail {
+inline std::string last_error() {
+  const char *e = aoship_get_last_error();
+  return e ? std::string(e) : std::string();
+}
+inline void check(int rc, ErrorKind kind, const char *what) {
+  if (rc != 0) throw AosError(kind, std::string(what) + ": " + last_error());
+}
+inline void hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw AosError(ErrorKind::Kernel, std::string(what) + ": " + hipGetErrorString(e));
+}
+}  // namespace detail
+
+// ---- RouterRing (kernel-api/src/lib.rs:57-214), release-build semantics -----------------------
+
+struct RouterRing {
+  std::array<uint16_t, 8> indices{};
+  std::array<int16_t, 8> gates_q15{};
+  size_t position = 0;
+  size_t k = 0;
+  uint32_t dropout_seed = 0;
+  float dropout_rate = 0.0f;
+
+  // RouterRing::new(k): K above 8 is clamped (the release-build behaviour).
+  static RouterRing with_k(size_t k) {
+    RouterRing r;
+    r.k = k < 8 ? k : 8;
+    return r;
+  }
+
+  size_t len() const { return k; }
+  bool is_empty() const { return k == 0; }
+
+  void set(const std::vector<uint16_t> &idx, const std::vector<int16_t> &gates) {
+    set_with_max_adapter(idx, gates, UINT16_MAX);
+  }
+
+  // set_with_max_adapter (lib.rs:122-193): mismatched lengths or an index >= max_adapter
+  // zero-fill the ring (release builds); K is clamped to 8; unused entries are zeroed.
+  void set_with_max_adapter(const std::vector<uint16_t> &idx, const std::vector<int16_t> &gates,
+                            uint16_t max_adapter) {
+    if (idx.size() != gates.size()) {
+      indices.fill(0);
+      gates_q15.fill(0);
+      k = 0;
+      return;
+    }
+    const size_t kk = idx.size() < 8 ? idx.size() : 8;
+    for (size_t i = 0; i < idx.size(); ++i)
+      if (idx[i] >= max_adapter) {
+        indices.fill(0);
+        gates_q15.fill(0);
+        k = 0;
+        return;
+      }
+    indices.fill(0);
+    gates_q15.fill(0);
+    for (size_t i = 0; i < kk; ++i) {
+      indices[i] = idx[i];
+      gates_q15[i] = gates[i];
+    }
+    k = kk;
+  }
+
+  std::vector<uint16_t> active_indices() const { return {indices.begin(), indices.begin() + k}; }
+  std::vector<int16_t> active_gates() const { return {gates_q15.begin(), gates_q15.begin() + k}; }
+
+  // The 40-byte device form (MetalRingBufferLayout, kernel-mtl/src/ring_buffer.rs:52-58).
+  aoship_ring_t to_device() const {
+    aoship_ring_t r;
+    std::memset(&r, 0, sizeof(r));
+    r.top_k = (uint32_t)k;
+    r.current_pos = (uint32_t)position;
+    for (size_t i = 0; i < 8; ++i) {
+      r.adapter_indices[i] = indices[i];
+      r.gates_q15[i] = gates_q15[i];
+    }
+    return r;
+  }
+
+  static RouterRing from_device(const aoship_ring_t &d) {
+    RouterRing r = with_k(d.top_k);
+    r.position = d.current_pos;
+    for (size_t i = 0; i < 8; ++i) {
+      r.indices[i] = d.adapter_indices[i];
+      r.gates_q15[i] = d.gates_q15[i];
+    }
+    return r;
+  }
+};
+
+// ---- router-side types (router/src/types.rs) ----------------------------------------------------
+
+struct AdapterInfo {
+  std::string id;
+  uint64_t stable_id = 0;
+};
+
+struct Decision {
+  std::vector<uint16_t> indices;
+  std::vector<int16_t> gates_q15;
+
+  std::vector<float> gates_f32() const {
+    std::vector<float> g;
+    for (int16_t q : gates_q15) g.push_back((float)q / AOSHIP_Q15_DENOM);
+    return g;
+  }
+
+  // Decision::to_router_ring (types.rs:699-706).
+  RouterRing to_router_ring() const {
+    if (indices.size() > 8) throw AosError(ErrorKind::Validation, "Decision has too many adapters (k > 8)");
+    RouterRing r = RouterRing::with_k(indices.size());
+    r.set(indices, gates_q15);
+    return r;
+  }
+};
+
+// PolicyMask: allowed[i] for adapter i (allow_all, or deny by adapter id).
+struct PolicyMask {
+  std::vector<uint8_t> allowed;
+  static PolicyMask allow_all(size_t n) { return PolicyMask{std::vector<uint8_t>(n, 1)}; }
+  static PolicyMask deny(const std::vector<AdapterInfo> &info, const std::vector<std::string> &denied) {
+    PolicyMask m = allow_all(info.size());
+    for (size_t i = 0; i < info.size(); ++i)
+      for (const auto &d : denied)
+        if (info[i].id == d) m.allowed[i] = 0;
+    return m;
+  }
+};
+
+// ---- Router (deterministic mode, empty feature vector) -------------------------------------------
+
+class Router {
+ public:
+  // Router::new_with_weights(.., k, tau, eps): k > 8 fails with AosError::Routing (router.rs:769-777);
+  // tau / eps are sanitised by the device router as router.rs:146-187.
+  // The device (default 0) is selected on first use.
+  Router(size_t k, float tau, float eps, int device = 0) : k_(k), tau_(tau), eps_(eps), device_(device) {
+    if (k > AOSHIP_MAX_K)
+      throw AosError(ErrorKind::Routing, "Adapter routing failed: K exceeds maximum allowed value of 8");
+  }
+  ~Router() { release(); }
+  Router(const Router &) = delete;
+  Router &operator=(const Router &) = delete;
+
+  void set_routing_bias(float bias) {
+    bias_ = bias;
+    release();
+  }
+
+  // One token, host priors (the reference's per-step router call); runs on the device.
+  Decision route_with_adapter_info(const std::vector<float> &features, const std::vector<float> &priors,
+                                   const std::vector<AdapterInfo> &info, const PolicyMask &mask) {
+    if (!features.empty())
+      throw AosError(ErrorKind::Validation, "feature scoring is not part of this path: pass empty features");
+    if (priors.size() != info.size())
+      throw AosError(ErrorKind::Validation, "priors and adapter_info lengths differ");
+    if (!mask.allowed.empty() && mask.allowed.size() != info.size())
+      throw AosError(ErrorKind::Validation, "policy mask length differs from adapter_info");
+    if (info.empty()) return Decision{};
+    bind(info);
+    detail::check(aoship_router_set_policy_mask(h_, mask.allowed.empty() ? nullptr : mask.allowed.data()),
+                  ErrorKind::Validation, "aoship_router_set_policy_mask");
+    const size_t n = info.size();
+    detail::hip_check(hipMemcpy(d_priors_, priors.data(), n * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+    detail::check(aoship_route(h_, d_priors_, 1, d_ring_, d_status_), ErrorKind::Routing, "aoship_route");
+    aoship_ring_t ring;
+    int32_t status = 0;
+    detail::hip_check(hipMemcpy(&ring, d_ring_, sizeof(ring), hipMemcpyDeviceToHost), "hipMemcpy");
+    detail::hip_check(hipMemcpy(&status, d_status_, sizeof(status), hipMemcpyDeviceToHost), "hipMemcpy");
+    if (status != 0)
+      throw AosError(ErrorKind::DeterminismViolation, "non-finite prior or score");
+    Decision d;
+    for (uint32_t i = 0; i < ring.top_k; ++i) {
+      d.indices.push_back(ring.adapter_indices[i]);
+      d.gates_q15.push_back(ring.gates_q15[i]);
+    }
+    return d;
+  }
+
+  // Batch form on device buffers: priors[T * n] -> rings[T] (status[T] may be null).
+  void route_device(const std::vector<AdapterInfo> &info, const float *priors_dev, int T, aoship_ring_t *rings_dev,
+                    int32_t *status_dev) {
+    bind(info);
+    detail::check(aoship_route(h_, priors_dev, T, rings_dev, status_dev), ErrorKind::Routing, "aoship_route");
+  }
+
+ private:
+  void bind(const std::vector<AdapterInfo> &info) {
+    std::vector<uint64_t> ids;
+    for (const auto &a : info) ids.push_back(a.stable_id);
+    if (h_ && ids == ids_) return;
+    release();
+    detail::check(aoship_init(device_), ErrorKind::Kernel, "aoship_init");
+    h_ = aoship_router_new((int)ids.size(), (int)k_, tau_, eps_, bias_, ids.data());
+    if (!h_) throw AosError(ErrorKind::Routing, "aoship_router_new: " + detail::last_error());
+    ids_ = ids;
+    detail::hip_check(hipMalloc(&d_priors_, ids.size() * sizeof(float)), "hipMalloc");
+    detail::hip_check(hipMalloc(&d_ring_, sizeof(aoship_ring_t)), "hipMalloc");
+    detail::hip_check(hipMalloc(&d_status_, sizeof(int32_t)), "hipMalloc");
+  }
+  void release() {
+    if (h_) aoship_router_free(h_);
+    h_ = nullptr;
+    if (d_priors_) (void)hipFree(d_priors_);
+    if (d_ring_) (void)hipFree(d_ring_);
+    if (d_status_) (void)hipFree(d_status_);
+    d_priors_ = nullptr;
+    d_ring_ = nullptr;
+    d_status_ = nullptr;
+    ids_.clear();
+  }
+
+  size_t k_;
+  float tau_, eps_, bias_ = 1.0f;
+  int device_;
+  aoship_router_t *h_ = nullptr;
+  std::vector<uint64_t> ids_;
+  float *d_priors_ = nullptr;
+  aoship_ring_t *d_ring_ = nullptr;
+  int32_t *d_status_ = nullptr;
+};
+
+// ---- FusedKernels surface for the layer path -----------------------------------------------------
+
+struct AdapterLoadMetadata {
+  std::string adapter_id;
+  uint32_t rank = 0;
+  float alpha = 0.0f;
+  std::vector<std::string> target_modules;
+};
+
+// One module's LoRA weights in MLX shapes: A [rank, in], B [out, rank], float32.
+struct LoraModuleWeights {
+  int in_features = 0, out_features = 0;
+  std::vector<float> A, B;
+};
+
+// Per layer: module name -> weights.
+using LoraLayerWeights = std::map<std::string, LoraModuleWeights>;
+
+class HipKernels {
+ public:
+  // device ordinal; num_layers layer handles (layer_idx 0..num_layers-1).
+  HipKernels(int device, int num_layers) {
+    detail::check(aoship_init(device), ErrorKind::Kernel, "aoship_init");
+    for (int i = 0; i < num_layers; ++i) {
+      aoship_layer_t *l = aoship_layer_new(i, AOSHIP_GROUP_SIZE, AOSHIP_BITS);
+      if (!l) throw AosError(ErrorKind::Kernel, "aoship_layer_new: " + detail::last_error());
+      layers_.push_back(l);
+    }
+    char buf[256];
+    detail::check(aoship_device_name(buf, sizeof(buf)), ErrorKind::Kernel, "aoship_device_name");
+    device_name_ = buf;
+  }
+  ~HipKernels() {
+    for (auto *l : layers_) aoship_layer_free(l);
+    for (auto &kv : adapters_) aoship_lora_adapter_free(kv.second);
+  }
+  HipKernels(const HipKernels &) = delete;
+  HipKernels &operator=(const HipKernels &) = delete;
+
+  // FusedKernels::device_name (lib.rs:374)
+  const std::string &device_name() const { return device_name_; }
+
+  // FusedKernels::attest_determinism (lib.rs:383): the report as JSON text.
+  std::string attest_determinism() const {
+    const int n = aoship_attest_determinism(nullptr, 0);
+    std::string s((size_t)n + 1, '\0');
+    aoship_attest_determinism(&s[0], n + 1);
+    s.resize((size_t)n);
+    return s;
+  }
+
+  // Base projection of a layer in the MLX 4-bit layout.
+  void set_base(int layer, const std::string &module, int out_features, int in_features, const uint32_t *packed,
+                const uint16_t *scales_f16, const uint16_t *biases_f16) {
+    detail::check(aoship_layer_set_base(layer_at(layer), module.c_str(), out_features, in_features, packed,
+                                        scales_f16, biases_f16),
+                  ErrorKind::Kernel, "aoship_layer_set_base");
+  }
+
+  // FusedKernels::load_adapter_with_metadata (lib.rs:398-405): scale = alpha / rank
+  // (backend.rs:462); weights[layer][module]. The adapter is attached to every layer.
+  void load_adapter_with_metadata(uint16_t id, const std::vector<LoraLayerWeights> &weights,
+                                  const AdapterLoadMetadata &md) {
+    if (md.rank == 0) throw AosError(ErrorKind::Validation, "adapter rank must be positive");
+    if (adapters_.count(id)) unload_adapter(id);
+    const float scale = md.alpha / (float)md.rank;
+    aoship_lora_adapter_t *a = aoship_lora_adapter_new(id, (int)weights.size(), scale);
+    if (!a) throw AosError(ErrorKind::Kernel, "aoship_lora_adapter_new: " + detail::last_error());
+    for (size_t li = 0; li < weights.size(); ++li)
+      for (const auto &kv : weights[li]) {
+        if (!md.target_modules.empty()) {
+          bool wanted = false;
+          for (const auto &t : md.target_modules) wanted = wanted || t == kv.first;
+          if (!wanted) continue;
+        }
+        const LoraModuleWeights &w = kv.second;
+        if (aoship_lora_adapter_set_module(a, (int)li, kv.first.c_str(), (int)md.rank, w.in_features,
+                                           w.out_features, w.A.data(), w.B.data()) != 0) {
+          const std::string err = detail::last_error();
+          aoship_lora_adapter_free(a);
+          throw AosError(ErrorKind::Kernel, "aoship_lora_adapter_set_module: " + err);
+        }
+      }
+    adapters_[id] = a;
+    attached_[id] = true;
+    rebind();
+  }
+
+  // attach / detach / unload (lib.rs:410-432). A detached adapter stays loaded; its ring index
+  // then contributes nothing until it is attached again.
+  void attach_adapter(uint16_t id) {
+    if (!adapters_.count(id)) throw AosError(ErrorKind::Kernel, "adapter not loaded");
+    attached_[id] = true;
+    rebind();
+  }
+  void detach_adapter(uint16_t id) {
+    if (!adapters_.count(id)) throw AosError(ErrorKind::Kernel, "adapter not loaded");
+    attached_.erase(id);
+    rebind();
+  }
+  void unload_adapter(uint16_t id) {
+    auto it = adapters_.find(id);
+    if (it == adapters_.end()) throw AosError(ErrorKind::Kernel, "adapter not loaded");
+    attached_.erase(id);
+    aoship_lora_adapter_t *a = it->second;
+    adapters_.erase(it);
+    rebind();  // layers drop their reference first
+    aoship_lora_adapter_free(a);
+  }
+
+  // Ring index a selects adapter id a.
+  size_t adapter_table_len() const { return table_len_; }
+
+  void reserve(int max_tokens) {
+    for (auto *l : layers_) detail::check(aoship_layer_reserve(l, max_tokens), ErrorKind::Kernel, "aoship_layer_reserve");
+  }
+
+  // Layer forwards on device buffers (bf16 activations, one 40-byte ring per token).
+  void mlp_forward(int layer, const aoship_bf16_t *x, int T, const aoship_ring_t *rings, aoship_bf16_t *y) {
+    detail::check(aoship_mlp_forward(layer_at(layer), x, T, rings, y), ErrorKind::Kernel, "aoship_mlp_forward");
+  }
+  void proj_forward(int layer, const std::string &module, const aoship_bf16_t *x, int T, const aoship_ring_t *rings,
+                    aoship_bf16_t *y) {
+    detail::check(aoship_proj_forward(layer_at(layer), module.c_str(), x, T, rings, y), ErrorKind::Kernel,
+                  "aoship_proj_forward");
+  }
+  void qkv_forward(int layer, const aoship_bf16_t *x, int T, const aoship_ring_t *rings, aoship_bf16_t *q,
+                   aoship_bf16_t *k, aoship_bf16_t *v) {
+    detail::check(aoship_qkv_forward(layer_at(layer), x, T, rings, q, k, v), ErrorKind::Kernel,
+                  "aoship_qkv_forward");
+  }
+
+ private:
+  aoship_layer_t *layer_at(int i) {
+    if (i < 0 || i >= (int)layers_.size()) throw AosError(ErrorKind::Validation, "layer index out of range");
+    return layers_[(size_t)i];
+  }
+  // Table: position = adapter id; detached or unloaded ids are null (skipped like a missing
+  // handle in prepare_lora_for_ring, backend.rs:398-428).
+  void rebind() {
+    size_t n = 0;
+    for (const auto &kv : adapters_) n = (size_t)kv.first + 1 > n ? (size_t)kv.first + 1 : n;
+    std::vector<aoship_lora_adapter_t *> table(n, nullptr);
+    for (const auto &kv : adapters_)
+      if (attached_.count(kv.first)) table[kv.first] = kv.second;
+    for (auto *l : layers_)
+      detail::check(aoship_layer_set_adapters(l, table.data(), (int)table.size()), ErrorKind::Kernel,
+                    "aoship_layer_set_adapters");
+    table_len_ = n;
+  }
+
+  std::vector<aoship_layer_t *> layers_;
+  std::map<uint16_t, aoship_lora_adapter_t *> adapters_;
+  std::map<uint16_t, bool> attached_;
+  size_t table_len_ = 0;
+  std::string device_name_;
+};
+
+}  // namespace adapteros

@@ -71,6 +71,37 @@ def test_mlp_prefill_shape_parity(hip):
     assert tol_ratio(got, ref) <= REL_TOL
 
 
+def test_mlp_stress_32b_prefill(hip):
+    """Qwen2.5-32B-shaped stress layer: 4096 tokens, 64 rank-64 adapters on gate/up/down, K = 8
+    with adversarial routing (ties, signed zeros, Q15 rounding boundaries, a dominant adapter).
+    Device-routed rings equal the oracle's; outputs within tolerance on a sample of tokens across
+    tiles; bit-identical run to run."""
+    import torch
+
+    cid, T = 5, 4096
+    cfg = W.CONFIGS[cid]
+    rings, pri = rings_for(cid, T)
+    router = hip.Router(cfg.n_adapters, cfg.k, cfg.tau, cfg.eps, 1.0, np.arange(cfg.n_adapters, dtype=np.uint64))
+    rdev = torch.zeros(T * 40, dtype=torch.uint8, device="cuda")
+    router.route(_dev(pri), rdev)
+    torch.cuda.synchronize()
+    assert rdev.cpu().numpy().tobytes() == rings.view(np.uint8).tobytes()
+    xb, xf = W.activations(cfg, T)
+    layer, ads = gpu_layer(hip, cid)
+    x = _dev(xb.view(np.int16))
+    y1 = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
+    y2 = torch.empty_like(y1)
+    layer.mlp_forward(x, rdev, y1)
+    layer.mlp_forward(x, rdev, y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), "run-to-run outputs differ"
+    sample = np.array([0, 1, 127, 128, 1000, 2047, 2048, 3001, 4094, 4095])
+    ref = oracle_mlp(cid, xf[sample], rings[sample])
+    got = W.bf16_bits_to_f32(y1.cpu().numpy().view(np.uint16)[sample])
+    ratio = tol_ratio(got, ref)
+    assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
+
+
 @pytest.mark.parametrize("T", [33, 100, 128, 129, 300])
 def test_mlp_prefill_ragged_full_parity(hip, T):
     """Prefill path at token counts around the 128-token tile (0.5B-shaped layer, every token
