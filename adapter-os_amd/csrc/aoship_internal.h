@@ -211,6 +211,16 @@ typedef struct {
       hipLaunchKernelGGL(kernel, grid, block, lds, (hipStream_t)(ctx)->stream, __VA_ARGS__);      \
   } while (0)
 
+/* A launcher with nothing to do still closes its profiling interval (zero length), so that
+ * pooled events never report a stale time. */
+#define AOS_SKIP(ctx)                                                                             \
+  do {                                                                                            \
+    if ((ctx)->ev_start) {                                                                        \
+      (void)hipEventRecord((hipEvent_t)(ctx)->ev_start, (hipStream_t)(ctx)->stream);              \
+      (void)hipEventRecord((hipEvent_t)(ctx)->ev_stop, (hipStream_t)(ctx)->stream);               \
+    }                                                                                             \
+  } while (0)
+
 #ifdef __cplusplus
 extern "C" {
 #endif

@@ -248,6 +248,10 @@ template <int NV>
 int launch_nv(const aos_shrink_params *p, const aos_launch_ctx *ctx) {
   const int rb_total = p->n_rb[0] + (p->nmod > 1 ? p->n_rb[1] : 0) + (p->nmod > 2 ? p->n_rb[2] : 0);
   dim3 grid(rb_total + (p->plan_build.plan ? 1 : 0), p->ks);
+  if (grid.x == 0) { /* no adapter rows and no plan to build (no bound adapter has the module) */
+    AOS_SKIP(ctx);
+    return 0;
+  }
   AOS_LAUNCH(ctx, (aos_shrink_kernel<NV, 4, 4>), grid, dim3(256), (size_t)p->lds_bytes, *p);
   return (int)hipGetLastError();
 }

@@ -55,6 +55,20 @@ def test_mlp_no_adapters_matches_base(hip):
     assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("T", [1, 8, 40])
+def test_mlp_without_bound_adapters(hip, T):
+    """A layer with no adapter bound at all (decode and prefill paths): the plain int4 SwiGLU MLP,
+    whatever the rings say."""
+    cid = 1
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    layer.set_adapters([])
+    y = _run_mlp(hip, layer, xb, rings)
+    ref = oracle_mlp(cid, xf, np.zeros(T, dtype=hip.RING_DTYPE))
+    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+
+
 def test_mlp_prefill_shape_parity(hip):
     """2048-token prefill of the 7B-shaped layer (matrix-core GEMM path), checked on a sample
     of tokens across tile boundaries, and bit-identical run to run."""
