@@ -699,8 +699,8 @@ static int nv_for(int T) {
 
 /* Decode GEMV geometry: waves per workgroup, K splits across workgroups, dynamic LDS bytes.
  * About 2048 waves stream the matrix; the x slice of a workgroup (T rows) plus its group sums
- * must fit the LDS budget; one more workgroup per row block adds the LoRA expand when any bound
- * adapter has this module. */
+ * must fit the LDS budget; the K-split-0 workgroup of each row block adds the LoRA expand when
+ * any bound adapter has this module. */
 static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g) {
   const int W = swiglu ? 4 : (G >= 128 ? 8 : 4);
   int ks = ceil_div(2048, RB * W);
@@ -848,7 +848,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g1.plan = plan;
   g1.zero_row = l->zeros.as<uint16_t>();
   g1.y = h;
-  g1.part = cv.b.take<float>((size_t)Wg.RB * (g1.ks + g1.has_expand) * 2 * nv_for(T) * 64);
+  g1.part = cv.b.take<float>((size_t)Wg.RB * g1.ks * 2 * nv_for(T) * 64);
   g1.counters = cv.counters((size_t)Wg.RB);
 
   aos_shrink_params &s2 = P.sh;
@@ -881,7 +881,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.plan = plan;
   g2.zero_row = l->zeros.as<uint16_t>();
   g2.y = y;
-  g2.part = cv.b.take<float>((size_t)Wd.RB * (g2.ks + g2.has_expand) * nv_for(T) * 64);
+  g2.part = cv.b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
   g2.counters = cv.counters((size_t)Wd.RB);
 
   P.bytes = cv.b.off + 256;
@@ -1174,7 +1174,7 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         gp[i].plan = plan;
         gp[i].zero_row = l->zeros.as<uint16_t>();
         gp[i].y = ys[i] + (size_t)t0 * W.out;
-        gp[i].part = cv.b.take<float>((size_t)W.RB * (gp[i].ks + gp[i].has_expand) * nv_for(Tc) * 64);
+        gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
         gp[i].counters = cv.counters((size_t)W.RB);
       }
       if (pass == 0) {

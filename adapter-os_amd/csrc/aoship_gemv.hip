@@ -17,10 +17,12 @@
  *         y += s * t + (b - 128 s) * sum(x over the group)
  *     so no per-element dequantisation arithmetic is needed;
  *   - K is split across the W waves of a workgroup and across ks workgroups per row block; the
- *     LoRA expand sum_u S[t, u] B_u[o, :] runs in one more workgroup per row block
- *     (blockIdx.y == ks), so the base waves carry no expand registers; all partials are summed
- *     in a fixed order (waves through LDS, workgroups by the last one to finish), so results
- *     are bit-identical run to run with no floating-point atomics.
+ *     LoRA expand sum_u coef(t, u) S[t, u] B_u[o, :] (S from the shrink launch before) is added
+ *     by the K-split-0 workgroup of each row block, its waves taking the (adapter, 16-rank)
+ *     steps round-robin; in the SwiGLU kernel each wave loads its first step's operands before
+ *     its K loop, so the expand adds no memory round trip at the end; all partials are summed in a fixed order
+ *     (waves through LDS, workgroups by the last one to finish), so results are bit-identical
+ *     run to run with no floating-point atomics.
  */
 #include "aoship_device.h"
 #include "aoship_internal.h"
@@ -58,50 +60,38 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return (uint32_t)aos_f32_to_bf16(lo) | ((uint32_t)aos_f32_to_bf16(hi) << 16);
 }
 
-/* The expand workgroup of one row block: acc = sum over the plan's (adapter, rank) steps of
- * coef(t, u) * S[t, col(u) + j0 .. +15] . B_list[u][row, j0 .. +15]; the steps are dealt to
- * the waves round-robin. */
-template <int NV, bool SW, int W>
-__device__ void expand_block(const aos_gemv_params &p, int rb, float (&acc0)[NV], float (&acc1)[NV]) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+/* One LoRA expand step of a wave: union slot u = 16 q / rpad, rank rows j0 .. j0 + 15. The A
+ * operand is coef(t, u) * S[t, col(u) + j0 + 8c ..], the B operand B_list[u][row, j0 + 8c ..]. */
+struct ExpandStep {
+  float4 s0, s1;
+  float cf;
+  u32x4 b;
+};
+
+__device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
+                                            int stride, int q, int row, int lane, ExpandStep &e) {
   const int i = lane & 31, c = lane >> 5;
-  const int row = rb * 32 + i;
-  const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
   const int ti = i < p.T ? i : 0;
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    if (m == 1 && !SW) break;
-    const aos_lora_tab &tab = m == 0 ? p.tab0 : p.tab1;
-    const float *S = m == 0 ? p.S0 : p.S1;
-    const int stride = m == 0 ? p.s_stride0 : p.s_stride1;
-    const int rpad = tab.rpad;
-    if (rpad == 0) continue;
-    const int nq = U * rpad / 16;
-    f32x16 f = {};
-    for (int q = wave; q < nq; q += W) {
-      const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
-      const int a = p.plan->list[u];
-      const int scol = (p.s_all ? a : u) * rpad + j0 + 8 * c;
-      const float *sp = S + (size_t)ti * stride + scol;
-      const float4 s0 = *(const float4 *)sp, s1 = *(const float4 *)(sp + 4);
-      const float cf = i < p.T ? p.plan->coef[ti][u] : 0.0f;
-      u32x4 av;
-      av.x = pack_bf16(cf * s0.x, cf * s0.y);
-      av.y = pack_bf16(cf * s0.z, cf * s0.w);
-      av.z = pack_bf16(cf * s1.x, cf * s1.y);
-      av.w = pack_bf16(cf * s1.z, cf * s1.w);
-      const uint16_t *B = tab.B[a];
-      const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
-      const u32x4 bv = *(const u32x4 *)bp;
-      f = aos_mfma32(av, bv, f);
-    }
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      if (m == 0) acc0[v] = f[v];
-      else acc1[v] = f[v];
-    }
-  }
+  const int rpad = tab.rpad;
+  const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
+  const int a = p.plan->list[u];
+  const int scol = (p.s_all ? a : u) * rpad + j0 + 8 * c;
+  const float *sp = S + (size_t)ti * stride + scol;
+  e.s0 = *(const float4 *)sp;
+  e.s1 = *(const float4 *)(sp + 4);
+  e.cf = i < p.T ? p.plan->coef[ti][u] : 0.0f;
+  const uint16_t *B = tab.B[a];
+  const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
+  e.b = *(const u32x4 *)bp;
+}
+
+__device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
+  u32x4 av;
+  av.x = pack_bf16(e.cf * e.s0.x, e.cf * e.s0.y);
+  av.y = pack_bf16(e.cf * e.s0.z, e.cf * e.s0.w);
+  av.z = pack_bf16(e.cf * e.s1.x, e.cf * e.s1.y);
+  av.w = pack_bf16(e.cf * e.s1.z, e.cf * e.s1.w);
+  f = aos_mfma32(av, e.b, f);
 }
 
 template <int NV, bool SW, int W, int D>
@@ -123,9 +113,20 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     acc1[v] = 0.0f;
   }
 
-  if (ksi == p.ks) {
-    expand_block<NV, SW, W>(p, rb, acc0, acc1);
-  } else {
+  /* the expand: number of steps per module, first step's operands loaded ahead of the K loop */
+  const bool expands = p.has_expand && ksi == 0;
+  int nq0 = 0, nq1 = 0;
+  ExpandStep e0, e1;
+  if (expands) {
+    const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
+    nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
+    nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
+    /* the SwiGLU kernel loads its first steps ahead; the single-matrix kernel keeps its
+     * registers (and its occupancy) and loads them after the K loop */
+    if (SW && wave < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, wave, row, lane, e0);
+    if (SW && wave < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, wave, row, lane, e1);
+  }
+  {
     const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
     const int GR = gw1 - gw0;
     const int ga = gw0 + wave * GR / W, gb = gw0 + (wave + 1) * GR / W, ng = gb - ga;
@@ -227,6 +228,28 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     }
   }
 
+  /* (4b) the expand, added to the waves' accumulators */
+  if (expands) {
+    f32x16 f0 = {}, f1 = {};
+    if (!SW && wave < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, wave, row, lane, e0);
+    if (wave < nq0) expand_apply(e0, f0);
+    if (SW && wave < nq1) expand_apply(e1, f1);
+    for (int q = wave + W; q < nq0; q += W) {
+      expand_load(p, p.tab0, p.S0, p.s_stride0, q, row, lane, e0);
+      expand_apply(e0, f0);
+    }
+    if (SW)
+      for (int q = wave + W; q < nq1; q += W) {
+        expand_load(p, p.tab1, p.S1, p.s_stride1, q, row, lane, e1);
+        expand_apply(e1, f1);
+      }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      acc0[v] += f0[v];
+      if (SW) acc1[v] += f1[v];
+    }
+  }
+
   /* (5) fixed-order reduction over the waves (LDS reused once every wave is done with x) */
   float *red = (float *)smem;
   lds_barrier();
@@ -249,7 +272,7 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
   }
 
   /* (6) fixed-order reduction over the workgroups of this row block: the last one sums */
-  const int nsplit = p.ks + p.has_expand;
+  const int nsplit = p.ks;
   if (nsplit > 1) {
     float *part = p.part + ((size_t)rb * nsplit + ksi) * (NA * NV * 64);
 #pragma unroll
@@ -310,10 +333,10 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
 
 template <int NV>
 int launch_nv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx) {
-  dim3 grid(p->w0.RB, p->ks + p->has_expand);
+  dim3 grid(p->w0.RB, p->ks);
   const size_t lds = p->lds_bytes;
   if (swiglu) {
-    AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, true, 4, 8>), grid, dim3(256), lds, *p);
+    AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, true, 4, 4>), grid, dim3(256), lds, *p);
   } else if (p->waves == 4) {
     AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, false, 4, 12>), grid, dim3(256), lds, *p);
   } else {

@@ -115,7 +115,7 @@ typedef struct {
   int ks;             /* workgroups per row block (split K) */
   int waves;          /* waves per workgroup: 4 or 8 */
   int lds_bytes;      /* dynamic LDS: x staging + group sums, or the wave reduction */
-  int has_expand;     /* 1: one more workgroup per row block adds the LoRA expand */
+  int has_expand;     /* 1: the K-split-0 workgroup of each row block adds the LoRA expand */
   /* LoRA expand: coef(t, u) * S[t][col(u) + j] . B_list[u][row][j] over the plan's union */
   aos_lora_tab tab0, tab1;
   const float *S0, *S1;   /* [T][s_stride] float32 */
@@ -125,7 +125,7 @@ typedef struct {
   const uint16_t *zero_row;
   /* outputs */
   uint16_t *y;        /* [T][out] bf16 (plain) or h (SwiGLU) */
-  float *part;        /* [RB][ks + has_expand][NA * NV * 64] */
+  float *part;        /* [RB][ks][NA * NV * 64] */
   uint32_t *counters; /* [RB] zero between launches */
 } aos_gemv_params;
 
