@@ -165,8 +165,7 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 struct aoship_router {
   int n = 0, k = 1;
   float tau = 1.0f, eps = 0.02f, bias = 1.0f;
-  DevBuf stable_id, allowed, counters, priors;
-  int counters_cap = 0, priors_cap = 0;
+  DevBuf stable_id, allowed;
   bool has_mask = false;
   hipStream_t stream = nullptr;
 };
@@ -241,27 +240,16 @@ static int route_common(aoship_router_t *r, const float *features, const float *
   p.rings = rings;
   p.status = status;
   p.priors_in = priors_in;
-  p.priors_per_block = 4;
   if (features) {
     if (!router_w || d <= 0 || d % 4 != 0)
       return set_err("aoship_route_features: router weights missing or d not a multiple of 4");
+    if ((size_t)(d + r->n) * sizeof(float) > 60 * 1024)
+      return set_err("aoship_route_features: d + n_adapters must not exceed 15360");
     if (((uintptr_t)features & 15u) || ((uintptr_t)router_w & 15u))
       return set_err("aoship_route_features: features and router_w must be 16-byte aligned");
     p.features = features;
     p.router_w = router_w;
-    if (!priors_out) {
-      if (r->priors_cap < T) {
-        if (r->priors.alloc(sizeof(float) * (size_t)T * r->n, false)) return -1;
-        r->priors_cap = T;
-      }
-      priors_out = r->priors.as<float>();
-    }
-    p.priors_out = priors_out;
-    if (r->counters_cap < T) {
-      if (r->counters.alloc(sizeof(uint32_t) * (size_t)T, true)) return -1;
-      r->counters_cap = T;
-    }
-    p.counters = r->counters.as<uint32_t>();
+    p.priors_out = priors_out; /* optional: the kernel hands the priors over in LDS */
   } else if (!priors_in) {
     return set_err("aoship_route: null priors");
   }
@@ -719,8 +707,11 @@ static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv
 
 /* Shrink geometry: about 1024 waves over the row blocks, at least one group per wave, x slice
  * within the LDS budget, at most 16 K splits (their partials are summed by one workgroup). */
+#ifndef AOS_SHRINK_WGS
+#define AOS_SHRINK_WGS 256
+#endif
 static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp) {
-  int ks = ceil_div(256, rb_total > 0 ? rb_total : 1);
+  int ks = ceil_div(AOS_SHRINK_WGS, rb_total > 0 ? rb_total : 1);
   int cap = G / 4;
   if (cap < 1) cap = 1;
   if (cap > 16) cap = 16;

@@ -80,8 +80,6 @@ typedef struct {
   const uint8_t *allowed;
   aoship_ring_t *rings;
   int32_t *status;
-  uint32_t *counters; /* [T], zero between launches */
-  int priors_per_block;
 } aos_route_params;
 
 /* ---- LoRA shrink for T <= 32 tokens: S[t][col] = sum_i A_row(col)[i] x[t][i], float32 ----

@@ -11,14 +11,16 @@
  *   Q15 = clamp(round_half_away(g * 32767.0f), 0, 32767)                  (quantization.rs:172-175)
  *   canonical re-sort: Q15 DESC, score DESC, stable_id ASC, index ASC     (:1310-1325)
  *
- * Selection is a wavefront bitonic sort over 128-bit composite keys
- * (total-order score key, stable_id, index), which makes every key unique, so the sort yields
- * exactly the order of Rust's stable sort. N > 64 adapters are streamed through the wave 56 at
- * a time while the best 8 stay in lanes 0..7. The softmax uses a correctly rounded float64 exp.
+ * Selection orders 128-bit composite keys (total-order score key, stable_id, index), which makes
+ * every key unique, so it yields exactly the order of Rust's stable sort: for N <= 64 by ranking
+ * (each lane counts the smaller keys), for larger N by a wavefront bitonic sort, streaming the
+ * adapters through the wave 56 at a time while the best 8 stay in lanes 0..7. The softmax uses a correctly rounded float64 exp.
  *
- * Optionally the priors are first computed from router features: one wave per (adapter, token)
- * dot product in float32 with a fixed order (lane l sums elements 256k + 4l + e, then a xor
- * butterfly); the workgroups of one token hand over to the last one to finish, which routes.
+ * Optionally the priors are first computed from router features: one workgroup per token, up to
+ * 16 waves, each wave computing whole (adapter, token) dot products in float32 with a fixed order
+ * (lane l sums elements 256k + 4l + e with fused multiply-adds, then a xor butterfly), all of a
+ * dot product's loads issued before its arithmetic; the priors go through LDS to wave 0, which
+ * routes.
  */
 #include "aos_exp.h"
 #include "aoship_device.h"
@@ -88,6 +90,7 @@ __device__ __forceinline__ int quantize_q15(float g) {
   return (int)r;
 }
 
+template <bool LDS>
 __device__ void route_one(const aos_route_params &p, const float *priors, int t, int lane) {
   const int n = p.n;
   /* every prior is checked for finiteness, allowed or not (validate_router_inputs); the chunked
@@ -99,7 +102,7 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
     a = ~0ull;
     b = ~0ull;
     if (i >= n) return false;
-    const float prior = aos_collect(priors + i);
+    const float prior = LDS ? priors[i] : priors[i];
     if (!__builtin_isfinite(prior)) bad = true;
     if (p.allowed && !p.allowed[i]) return false;
     float sim = (prior + 0.0f) - 0.0f;
@@ -114,7 +117,32 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
   {
     bool v = load_key(lane, ka, kb);
     m_allowed += __popcll(__ballot(v));
-    bitonic64(ka, kb, lane);
+    if (n <= AOS_WAVE) {
+      /* n <= 64: rank selection. Keys are unique (they end in the index), so lane i's rank is
+       * the number of smaller keys; the 8 smallest are scattered to lanes 0..7 through LDS. */
+      __shared__ uint64_t keys[2 * AOS_WAVE];
+      __shared__ uint64_t top[2 * 8];
+      keys[2 * lane] = ka;
+      keys[2 * lane + 1] = kb;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      int rank = 0;
+      for (int j = 0; j < n; ++j) {
+        const uint64_t a = keys[2 * j], b = keys[2 * j + 1];
+        rank += key_less(a, b, ka, kb) ? 1 : 0;
+      }
+      if (lane < n && rank < 8) {
+        top[2 * rank] = ka;
+        top[2 * rank + 1] = kb;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      const int src = lane < 8 && lane < n ? lane : -1;
+      ka = src >= 0 ? top[2 * src] : ~0ull;
+      kb = src >= 0 ? top[2 * src + 1] : ~0ull;
+    } else {
+      bitonic64(ka, kb, lane);
+    }
   }
   for (int base = AOS_WAVE; base < n; base += AOS_WAVE - 8) {
     bool v = false;
@@ -245,74 +273,83 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
   }
 }
 
-__global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
-  const int lane = threadIdx.x;
-  const int t = blockIdx.y;
-  const float *priors;
-  if (p.features) {
-    /* priors[t, a] for a = blockIdx.x: lane l accumulates elements 256k + 4l + e (k ascending,
-     * e = 0..3) with fused multiply-adds, then a xor butterfly over the 64 lanes. */
-    const int a = blockIdx.x;
-    const float4 *f4 = (const float4 *)(p.features + (size_t)t * p.d);
-    const float4 *w4 = (const float4 *)(p.router_w + (size_t)a * p.d);
-    const int nk = p.d >> 8;        /* full 256-element chunks */
-    const int tail = p.d & 255;     /* multiple of 4 */
-    float acc = 0.0f;
-    int k = 0;
-    for (; k + 4 <= nk; k += 4) {
-      float4 fv[4], wv[4];
+/* Dot products of router features (staged in LDS) with router weight rows: lane l sums elements
+ * 256k + 4l + e (k ascending, e = 0..3) with fused multiply-adds, then a xor butterfly over the
+ * 64 lanes. Up to 16 chunks of 256 weights are loaded before any arithmetic. */
+__device__ __forceinline__ float router_dot(const float *f_lds, const float *w, int d, int lane) {
+  const float4 *f4 = (const float4 *)f_lds;
+  const float4 *w4 = (const float4 *)w;
+  const int nk = d >> 8;    /* full 256-element chunks */
+  const int tail = d & 255; /* multiple of 4 */
+  float acc = 0.0f;
+  for (int k0 = 0; k0 < nk; k0 += 16) {
+    float4 wv[16];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        fv[j] = f4[(k + j) * 64 + lane];
-        wv[j] = w4[(k + j) * 64 + lane];
-      }
+    for (int j = 0; j < 16; ++j) {
+      const int k = k0 + j < nk ? k0 + j : nk - 1;
+      wv[j] = w4[k * 64 + lane];
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc = fmaf(wv[j].x, fv[j].x, acc);
-        acc = fmaf(wv[j].y, fv[j].y, acc);
-        acc = fmaf(wv[j].z, fv[j].z, acc);
-        acc = fmaf(wv[j].w, fv[j].w, acc);
+    for (int j = 0; j < 16; ++j) {
+      if (k0 + j < nk) {
+        const float4 fv = f4[(k0 + j) * 64 + lane];
+        acc = fmaf(wv[j].x, fv.x, acc);
+        acc = fmaf(wv[j].y, fv.y, acc);
+        acc = fmaf(wv[j].z, fv.z, acc);
+        acc = fmaf(wv[j].w, fv.w, acc);
       }
     }
-    for (; k < nk; ++k) {
-      const float4 fv = f4[k * 64 + lane], wv = w4[k * 64 + lane];
-      acc = fmaf(wv.x, fv.x, acc);
-      acc = fmaf(wv.y, fv.y, acc);
-      acc = fmaf(wv.z, fv.z, acc);
-      acc = fmaf(wv.w, fv.w, acc);
-    }
-    if (4 * lane < tail) {
-      const float4 fv = f4[nk * 64 + lane], wv = w4[nk * 64 + lane];
-      acc = fmaf(wv.x, fv.x, acc);
-      acc = fmaf(wv.y, fv.y, acc);
-      acc = fmaf(wv.z, fv.z, acc);
-      acc = fmaf(wv.w, fv.w, acc);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc = acc + aos_shfl_f(acc, lane ^ o);
-    if (lane == 0) aos_publish(p.priors_out + (size_t)t * p.n + a, acc);
-    if (gridDim.x > 1) {
-      uint32_t old = 0;
-      if (lane == 0) old = aos_arrive(&p.counters[t]);
-      old = aos_shfl(old, 0);
-      if (old != gridDim.x - 1) return;
-      if (lane == 0) aos_reset(&p.counters[t]);
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
-    }
-    /* the priors are read back with device-coherent loads below */
-    priors = p.priors_out + (size_t)t * p.n;
-  } else {
-    priors = p.priors_in + (size_t)t * p.n;
   }
-  route_one(p, priors, t, lane);
+  if (4 * lane < tail) {
+    const float4 fv = f4[nk * 64 + lane], wv = w4[nk * 64 + lane];
+    acc = fmaf(wv.x, fv.x, acc);
+    acc = fmaf(wv.y, fv.y, acc);
+    acc = fmaf(wv.z, fv.z, acc);
+    acc = fmaf(wv.w, fv.w, acc);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc = acc + aos_shfl_f(acc, lane ^ o);
+  return acc;
+}
+
+/* Routing from priors already in memory: one wave per token. */
+__global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
+  const int t = blockIdx.x;
+  route_one<false>(p, p.priors_in + (size_t)t * p.n, t, threadIdx.x);
+}
+
+/* Routing from router features: one workgroup per token; wave w computes the priors of
+ * adapters w, w + W, ... into LDS (and priors_out), then wave 0 routes. */
+__global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_params p) {
+  extern __shared__ float lds[]; /* features [d], then priors [n] */
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  float *lds_f = lds, *lds_priors = lds + p.d;
+  const float4 *f4 = (const float4 *)(p.features + (size_t)t * p.d);
+  for (int e = threadIdx.x; e < p.d / 4; e += blockDim.x) ((float4 *)lds_f)[e] = f4[e];
+  __syncthreads();
+  for (int a = wave; a < p.n; a += nw) {
+    const float v = router_dot(lds_f, p.router_w + (size_t)a * p.d, p.d, lane);
+    if (lane == 0) {
+      lds_priors[a] = v;
+      if (p.priors_out) p.priors_out[(size_t)t * p.n + a] = v;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) route_one<true>(p, lds_priors, t, lane);
 }
 
 }  // namespace
 
 extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx) {
-  dim3 grid(1, p->T);
-  if (p->features) grid.x = p->n; /* one wave per (adapter, token) dot product */
-  AOS_LAUNCH(ctx, aos_route_kernel, grid, dim3(64), 0, *p);
+  if (p->features) {
+    const int waves = p->n < 16 ? p->n : 16;
+    AOS_LAUNCH(ctx, aos_route_features_kernel, dim3(p->T), dim3(64 * waves),
+               (size_t)(p->d + p->n) * sizeof(float), *p);
+  } else {
+    AOS_LAUNCH(ctx, aos_route_kernel, dim3(p->T), dim3(64), 0, *p);
+  }
   return (int)hipGetLastError();
 }

@@ -110,7 +110,7 @@ int aoship_route(aoship_router_t *router, const float *priors, int T, aoship_rin
 /* Route with priors computed on the device from router features: priors[t, a] =
  * sum_i router_w[a, i] * features[t, i] in float32 with a fixed reduction order (64 partial
  * sums, partial l taking elements 256k + 4l + e in order with fused multiply-adds, then a xor
- * butterfly), then as aoship_route. d must be a multiple of 4.
+ * butterfly), then as aoship_route. d must be a multiple of 4 and d + n_adapters <= 15360.
  *   features   : device float[T * d];  router_w : device float[n_adapters * d]
  *   priors_out : device float[T * n_adapters] or NULL. */
 int aoship_route_features(aoship_router_t *router, const float *features, const float *router_w,
