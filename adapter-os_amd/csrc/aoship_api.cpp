@@ -686,12 +686,18 @@ static int nv_for(int T) {
 }
 
 /* Decode GEMV geometry: waves per workgroup, K splits across workgroups, dynamic LDS bytes.
- * About 2048 waves stream the matrix; the x slice of a workgroup (T rows) plus its group sums
+ * About 1024 waves stream the matrix (fewer K splits, less reduction); the x slice of a workgroup (T rows) plus its group sums
  * must fit the LDS budget; the K-split-0 workgroup of each row block adds the LoRA expand when
  * any bound adapter has this module. */
+#ifndef AOS_GEMV_WAVES
+#define AOS_GEMV_WAVES 1024 /* waves streaming one matrix (measured best at decode) */
+#endif
+#ifndef AOS_GEMV_W8_MIN_G
+#define AOS_GEMV_W8_MIN_G 128 /* single-matrix GEMVs with at least this many groups use 8 waves */
+#endif
 static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g) {
-  const int W = swiglu ? 4 : (G >= 128 ? 8 : 4);
-  int ks = ceil_div(2048, RB * W);
+  const int W = swiglu ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
+  int ks = ceil_div(AOS_GEMV_WAVES, RB * W);
   int cap = G / W;
   if (cap < 1) cap = 1;
   if (ks > cap) ks = cap;

@@ -185,9 +185,16 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     lds_barrier();
     for (int idx = tid; idx < T * GR * 2; idx += 64 * W) {
       const int t = idx / (GR * 2), rem = idx - t * GR * 2;
-      const uint16_t *src = xl + (size_t)t * xstride + rem * 32;
-      float s = 0.0f;
-      for (int e = 0; e < 32; ++e) s += aos_bf16_to_f32(src[e]);
+      const u32x4 *src = (const u32x4 *)(xl + (size_t)t * xstride + rem * 32);
+      const u32x4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+      const uint32_t w[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                              v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+      float s = 0.0f; /* the 32 elements in order */
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        s += __builtin_bit_cast(float, w[e] << 16);
+        s += __builtin_bit_cast(float, w[e] & 0xffff0000u);
+      }
       xs[idx] = s;
     }
     lds_barrier();
