@@ -18,8 +18,8 @@
  *     so no per-element dequantisation arithmetic is needed;
  *   - K is split across the W waves of a workgroup and across ks workgroups per row block; the
  *     LoRA expand sum_u coef(t, u) S[t, u] B_u[o, :] (S from the shrink launch before) is added
- *     by the K-split-0 workgroup of each row block, its waves taking the (adapter, 16-rank)
- *     steps round-robin; in the SwiGLU kernel each wave loads its first step's operands before
+ *     by the row block's workgroups, which take the (adapter, 16-rank) steps round-robin over
+ *     workgroups and waves; in the SwiGLU kernel each wave loads its first step's operands before
  *     its K loop, so the expand adds no memory round trip at the end; all partials are summed in a fixed order
  *     (waves through LDS, workgroups by the last one to finish), so results are bit-identical
  *     run to run with no floating-point atomics.
@@ -113,18 +113,20 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     acc1[v] = 0.0f;
   }
 
-  /* the expand: number of steps per module, first step's operands loaded ahead of the K loop */
-  const bool expands = p.has_expand && ksi == 0;
+  /* the expand: steps q of each module are dealt round-robin to the row block's ks workgroups
+   * and then to their waves (q = ksi + ks * (wave + W * j)); the SwiGLU kernel loads its first
+   * step's operands ahead of the K loop, the single-matrix kernel keeps its registers (and its
+   * occupancy) and loads them after the K loop */
+  const bool expands = p.has_expand != 0;
+  const int q_first = ksi + p.ks * wave, q_step = p.ks * W;
   int nq0 = 0, nq1 = 0;
   ExpandStep e0, e1;
   if (expands) {
     const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
     nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
     nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
-    /* the SwiGLU kernel loads its first steps ahead; the single-matrix kernel keeps its
-     * registers (and its occupancy) and loads them after the K loop */
-    if (SW && wave < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, wave, row, lane, e0);
-    if (SW && wave < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, wave, row, lane, e1);
+    if (SW && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
+    if (SW && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1);
   }
   {
     const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
@@ -238,15 +240,15 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
   /* (4b) the expand, added to the waves' accumulators */
   if (expands) {
     f32x16 f0 = {}, f1 = {};
-    if (!SW && wave < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, wave, row, lane, e0);
-    if (wave < nq0) expand_apply(e0, f0);
-    if (SW && wave < nq1) expand_apply(e1, f1);
-    for (int q = wave + W; q < nq0; q += W) {
+    if (!SW && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
+    if (q_first < nq0) expand_apply(e0, f0);
+    if (SW && q_first < nq1) expand_apply(e1, f1);
+    for (int q = q_first + q_step; q < nq0; q += q_step) {
       expand_load(p, p.tab0, p.S0, p.s_stride0, q, row, lane, e0);
       expand_apply(e0, f0);
     }
     if (SW)
-      for (int q = wave + W; q < nq1; q += W) {
+      for (int q = q_first + q_step; q < nq1; q += q_step) {
         expand_load(p, p.tab1, p.S1, p.s_stride1, q, row, lane, e1);
         expand_apply(e1, f1);
       }

@@ -30,7 +30,9 @@ enum { MOD_Q = 0, MOD_K, MOD_V, MOD_O, MOD_GATE, MOD_UP, MOD_DOWN };
 
 #define AOS_MAX_ADAPTERS 4096
 #define AOS_DECODE_MAX_T 32
-#define AOS_GEMV_LDS_MAX (64 * 1024)  /* dynamic LDS budget of one GEMV workgroup */
+#ifndef AOS_GEMV_LDS_MAX
+#define AOS_GEMV_LDS_MAX (32 * 1024) /* dynamic LDS budget of one GEMV workgroup (measured) */
+#endif
 #define AOS_SHRINK_GROUPS_PER_WAVE 2
 
 typedef struct {
@@ -113,7 +115,7 @@ typedef struct {
   int ks;             /* workgroups per row block (split K) */
   int waves;          /* waves per workgroup: 4 or 8 */
   int lds_bytes;      /* dynamic LDS: x staging + group sums, or the wave reduction */
-  int has_expand;     /* 1: the K-split-0 workgroup of each row block adds the LoRA expand */
+  int has_expand;     /* 1: the K-split workgroups of each row block add the LoRA expand */
   /* LoRA expand: coef(t, u) * S[t][col(u) + j] . B_list[u][row][j] over the plan's union */
   aos_lora_tab tab0, tab1;
   const float *S0, *S1;   /* [T][s_stride] float32 */
