@@ -894,7 +894,10 @@ struct PrefillPlan {
   int umax = 1, mtiles = 0;
 };
 
-static void plan_prefill_common(aoship_layer *l, Carve &cv, const aoship_ring_t *rings, int T, PrefillPlan &P) {
+/* Union plan of one prefill call; tabs are the modules (in the order of the call's GEMMs) whose
+ * per-slot B pointers the plan tabulates. */
+static void plan_prefill_common(aoship_layer *l, Carve &cv, const aoship_ring_t *rings, int T,
+                                const aos_lora_tab *tabs, int nm, PrefillPlan &P) {
   const int n = (int)l->table.size();
   int umax = n < 8 * T ? n : 8 * T;
   if (umax < 1) umax = 1;
@@ -912,6 +915,9 @@ static void plan_prefill_common(aoship_layer *l, Carve &cv, const aoship_ring_t 
   pp.coef = cv.b.take<float>((size_t)T * umax);
   pp.mwords = ceil_div(umax, 32);
   pp.tile_mask = cv.b.take<uint32_t>((size_t)P.mtiles * pp.mwords);
+  pp.nmod = nm;
+  for (int i = 0; i < nm; ++i) pp.tab[i] = tabs[i];
+  pp.bp = cv.b.take<const uint16_t *>((size_t)nm * umax);
 }
 
 /* Shrink over the union for nm modules sharing x: K splits so that the grid has about 512
@@ -953,16 +959,18 @@ static void plan_pshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const
   sp.part = sp.ks > 1 ? cv.b.take<float>((size_t)sp.ks * T * sp.s_stride) : nullptr;
 }
 
-static void plan_gemm(const PrefillPlan &P, const aos_pshrink_params &sp, const Q4Mat &W0, const Q4Mat *W1,
-                      const uint16_t *x, int T, const aos_lora_tab &t0, int off0, const aos_lora_tab *t1,
-                      int off1, uint16_t *y, aos_gemm_params &g) {
+/* GEMM of matrix W0 (module mi0 of the plan's tables) or, in SwiGLU mode, W0 and W1 (module
+ * mi0 + 1). */
+static void plan_gemm(aoship_layer *l, const PrefillPlan &P, const aos_pshrink_params &sp, const Q4Mat &W0,
+                      const Q4Mat *W1, const uint16_t *x, int T, int mi0, const aos_lora_tab &t0, int off0,
+                      const aos_lora_tab *t1, int off1, uint16_t *y, aos_gemm_params &g) {
   memset(&g, 0, sizeof(g));
   g.w0 = W0.dev();
   if (W1) g.w1 = W1->dev();
   g.x = x;
   g.T = T;
   g.mb = P.mtiles;
-  g.nb = ceil_div(W0.RB, 4); /* 4 row blocks (128 rows) per workgroup */
+  g.nb = ceil_div(W0.RB, aos_gemm_waves(W1 != nullptr)); /* one 32-row block per wave */
   g.tab0 = t0;
   if (t1) g.tab1 = *t1;
   g.SA = sp.SA;
@@ -972,6 +980,11 @@ static void plan_gemm(const PrefillPlan &P, const aos_pshrink_params &sp, const 
   g.plan = P.pp.plan;
   g.tile_mask = P.pp.tile_mask;
   g.mwords = P.pp.mwords;
+  g.umax = P.umax;
+  g.bp0 = P.pp.bp ? P.pp.bp + (size_t)mi0 * P.umax : nullptr;
+  g.bp1 = P.pp.bp && t1 ? P.pp.bp + (size_t)(mi0 + 1) * P.umax : nullptr;
+  g.lsteps_max = aos_lstep_bound(P.umax, t0.rpad) + (t1 ? aos_lstep_bound(P.umax, t1->rpad) : 0);
+  g.zero = l->zeros.as<uint16_t>();
   g.y = y;
 }
 
@@ -989,12 +1002,13 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
   aos_lora_tab tgu[2] = {lora_tab(l, MOD_GATE, H, I), lora_tab(l, MOD_UP, H, I)};
   aos_lora_tab td = lora_tab(l, MOD_DOWN, I, H);
   Carve cv(ws, ctr);
-  plan_prefill_common(l, cv, rings, T, M.P);
+  const aos_lora_tab tall[3] = {tgu[0], tgu[1], td};
+  plan_prefill_common(l, cv, rings, T, tall, 3, M.P);
   uint16_t *h = cv.b.take<uint16_t>((size_t)T * I);
   plan_pshrink(l, cv, M.P, x, T, H, tgu, 2, M.sx);
-  plan_gemm(M.P, M.sx, Wg, &Wu, x, T, tgu[0], M.sx.s_off[0], &tgu[1], M.sx.s_off[1], h, M.g1);
+  plan_gemm(l, M.P, M.sx, Wg, &Wu, x, T, 0, tgu[0], M.sx.s_off[0], &tgu[1], M.sx.s_off[1], h, M.g1);
   plan_pshrink(l, cv, M.P, h, T, I, &td, 1, M.sh);
-  plan_gemm(M.P, M.sh, Wd, nullptr, h, T, td, 0, nullptr, 0, y, M.g2);
+  plan_gemm(l, M.P, M.sh, Wd, nullptr, h, T, 2, td, 0, nullptr, 0, y, M.g2);
   M.bytes = cv.b.off + 256;
   M.ctr = cv.coff + 64;
 }
@@ -1129,10 +1143,10 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
       aos_gemm_params gp[3];
       for (int pass = 0; pass < 2; ++pass) {
         Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr);
-        plan_prefill_common(l, cv, rings + t0, Tc, P);
+        plan_prefill_common(l, cv, rings + t0, Tc, tabs, nm, P);
         plan_pshrink(l, cv, P, xc, Tc, in, tabs, nm, sp);
         for (int i = 0; i < nm; ++i)
-          plan_gemm(P, sp, l->mats[mods[i]], nullptr, xc, Tc, tabs[i], sp.s_off[i], nullptr, 0,
+          plan_gemm(l, P, sp, l->mats[mods[i]], nullptr, xc, Tc, i, tabs[i], sp.s_off[i], nullptr, 0,
                     ys[i] + (size_t)t0 * l->mats[mods[i]].out, gp[i]);
         if (pass == 0 && ws_reserve(l, cv.b.off + 256, cv.coff + 64)) return -1;
       }

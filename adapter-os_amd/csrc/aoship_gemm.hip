@@ -52,10 +52,16 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-/* Byte k of w as a float (one v_cvt_f32_ubyte<k>). */
+/* Byte k of w as a float: one v_cvt_f32_ubyte<k> (left to itself the compiler extracts each
+ * nibble with v_bfe_u32 and converts byte 0, twice the instructions). */
 template <int k>
 __device__ __forceinline__ float ubyte(uint32_t w) {
-  return (float)((w >> (8 * k)) & 0xffu);
+  float r;
+  if (k == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+  else if (k == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+  else if (k == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+  return r;
 }
 
 /* Dequantise one nibble-shuffled word (nibbles stored as e0 e2 e4 e6 e1 e3 e5 e7) into the
@@ -72,28 +78,45 @@ __device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float b) {
 }
 
 /* LDS token tile: rows of 64 bf16 (eight 16-byte chunks); chunk c of row r sits in slot
- * c ^ (r & 7). */
-__device__ __forceinline__ int tile_off(int r, int chunk) { return r * 128 + ((chunk ^ (r & 7)) << 4); }
+ * c ^ ((r >> 1) & 7). A row is 128 bytes, half of the 64 four-byte banks: even and odd rows use
+ * the two halves, and the slot rotation spreads 8 rows of equal parity over the 8 slots, so 16
+ * consecutive rows read one chunk each without a bank conflict. */
+__device__ __forceinline__ int tile_off(int r, int chunk) { return r * 128 + ((chunk ^ ((r >> 1) & 7)) << 4); }
 
-/* Stage the [BM x 64] bf16 slice of group g of the token rows m0... Rows past the last token
- * repeat it: they only feed accumulator rows that are never stored. */
-template <int BM>
+/* Stage the [BM x 64] bf16 slice of group g of the token rows m0... with NT threads. Rows past
+ * the last token repeat it: they only feed accumulator rows that are never stored. */
+template <int BM, int NT = 256>
 struct Stager {
-  static constexpr int CH = BM * 8 / 256; /* 16-byte chunks per thread */
+  static constexpr int CH = BM * 8 / NT; /* 16-byte chunks per thread */
   u32x4 v[CH];
   __device__ __forceinline__ void load(const uint16_t *x, int in, int T, int m0, int g, int tid) {
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
-      const int idx = tid + k * 256;
+      const int idx = tid + k * NT;
       const int r = idx >> 3, ch = idx & 7;
       const int tok = m0 + r < T ? m0 + r : T - 1;
       v[k] = *(const u32x4 *)(x + (size_t)tok * in + (size_t)g * 64 + ch * 8);
     }
   }
+  /* 64 columns of the rows of a tile-based buffer (rows bytes apart, rows >= nrows repeat the
+   * last): byte columns cb .. cb + 127; chunks at or past lim bytes read as zeros (an offset
+   * past the buffer's end). */
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t rs, int row_bytes, int nrows, int cb, int lim,
+                                           int tid) {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int idx = tid + k * NT;
+      const int r = idx >> 3, ch = idx & 7;
+      const int rr = r < nrows ? r : nrows - 1;
+      const int c = cb + ch * 16;
+      const int off = c < lim ? rr * row_bytes + c : (int)0x80000000;
+      v[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
+  }
   __device__ __forceinline__ void store(unsigned char *buf, int tid) const {
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
-      const int idx = tid + k * 256;
+      const int idx = tid + k * NT;
       const int r = idx >> 3, ch = idx & 7;
       *(u32x4 *)(buf + tile_off(r, ch)) = v[k];
     }
@@ -149,10 +172,15 @@ __global__ void __launch_bounds__(256) aos_pplan_kernel(aos_pplan_params p) {
         const int u = base[a >> 5] + __builtin_popcount(m & ((1u << (a & 31)) - 1u));
         p.plan->list[u] = (uint16_t)a;
         p.plan->slot[a] = (int16_t)u;
+        if (u < p.cstride)
+          for (int k = 0; k < p.nmod; ++k)
+            p.bp[(size_t)k * p.cstride + u] = p.tab[k].rpad && a < p.tab[k].n ? p.tab[k].B[a] : nullptr;
       } else {
         p.plan->slot[a] = -1;
       }
     }
+    for (int u = base[words] + tid; u < p.cstride; u += 256)
+      for (int k = 0; k < p.nmod; ++k) p.bp[(size_t)k * p.cstride + u] = nullptr;
   }
   /* this tile's coefficient rows: zero, then each token's slots in ring order by one thread */
   const int t0 = blockIdx.x * AOS_GEMM_BM;
@@ -309,114 +337,77 @@ __global__ void __launch_bounds__(256) aos_pfinish_kernel(aos_pshrink_params p) 
 /* int4 GEMM + LoRA expand (+ SwiGLU)                                                          */
 /* ------------------------------------------------------------------------------------------ */
 
-/* First union slot >= from whose bit is set in the tile mask and whose adapter has module B;
- * -1 if none. Uniform. */
-__device__ __forceinline__ int next_slot(const aos_gemm_params &p, const aos_lora_tab &tab, const uint32_t *mask,
-                                         int from) {
-  for (int w = from >> 5; w < p.mwords; ++w) {
-    uint32_t bits = mask[w];
-    if (w == (from >> 5)) bits &= ~0u << (from & 31);
-    while (bits) {
-      const int u = w * 32 + __builtin_ctz(bits);
-      bits &= bits - 1u;
-      if (tab.B[p.plan->list[u]] != nullptr) return u;
-    }
-  }
-  return -1;
-}
+/* Expand K steps: the LoRA expand of a token tile runs as extra K steps of 64 columns after the
+ * weight groups. The token operand is SA (coefficient-scaled shrink of the union slots, staged in
+ * LDS like x), the weight operand the union adapters' B rows (bf16, straight to registers). A
+ * step is listed as (module << 15) | j, j = index of its 64 columns among the module's union
+ * columns u * rpad + r; a tile lists only the steps that hold a slot one of its tokens uses. */
 
-/* Expand of one module: for each (slot u, 16 rank rows j0) step the A operand is SA[t][s_off +
- * u * rpad + j0 + 8c ..] (coefficient already applied) and the B operand the adapter's B rows of
- * this wave's row block(s). Fragments of the next step are loaded before the current step's
- * matrix-core work. Rows of dead row blocks and tokens past T read clamped (valid) addresses;
- * their accumulators are never stored. */
-template <int MT, int NX>
-__device__ __forceinline__ void expand_module(const aos_gemm_params &p, const aos_lora_tab &tab, int s_off,
-                                              const int (&row)[2], int m0, int mbi,
-                                              int lane, f32x16 (&acc0)[MT], f32x16 (&acc1)[MT]) {
-  const int rpad = tab.rpad;
-  if (rpad == 0) return;
-  const int i = lane & 31, c = lane >> 5;
-  const uint32_t *mask = p.tile_mask + (size_t)mbi * p.mwords;
-  int u = next_slot(p, tab, mask, 0);
-  if (u < 0) return;
-  int j0 = 0;
-  const uint16_t *sa_row[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int t = m0 + mt * 32 + i;
-    sa_row[mt] = p.SA + (size_t)(t < p.T ? t : p.T - 1) * p.sa_stride + s_off + 8 * c;
-  }
-  u32x4 bv[NX], av[MT];
-  auto load = [&](int uu, int jj, u32x4 (&b)[NX], u32x4 (&a)[MT]) {
-    const uint16_t *B = tab.B[p.plan->list[uu]];
-#pragma unroll
-    for (int x = 0; x < NX; ++x) b[x] = *(const u32x4 *)(B + (size_t)row[x] * rpad + jj + 8 * c);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) a[mt] = *(const u32x4 *)(sa_row[mt] + (size_t)uu * rpad + jj);
-  };
-  load(u, j0, bv, av);
-  while (true) {
-    int un = u, jn = j0 + 16;
-    if (jn == rpad) {
-      jn = 0;
-      un = next_slot(p, tab, mask, u + 1);
-    }
-    u32x4 bn[NX], an[MT];
-    if (un >= 0) load(un, jn, bn, an);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc0[mt] = aos_mfma32(av[mt], bv[0], acc0[mt]);
-      if (NX == 2) acc1[mt] = aos_mfma32(av[mt], bv[NX - 1], acc1[mt]);
-    }
-    if (un < 0) break;
-    u = un;
-    j0 = jn;
-#pragma unroll
-    for (int x = 0; x < NX; ++x) bv[x] = bn[x];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) av[mt] = an[mt];
-  }
-}
+/* LDS after the token tiles: 16 bytes of counts, the slot mask words, LBP B pointers per module
+ * (two modules), then the step list. */
+constexpr int LBP = 256;
+constexpr int GEMM_AUX = 16 + 4 * AOS_MAX_ADAPTERS / 32 + 2 * LBP * 8;
 
-/* SW: SwiGLU (gate and up rows, NR = 2); NR: row blocks per wave; MT: 32-token sub-tiles;
- * D: weight ring depth (divides the group count); DB: token tile loads two groups ahead (two
- * register stages); APF: next sub-tile's LDS fragments loaded before the current MFMAs. Two
- * workgroups per CU (two waves per SIMD) let one wave's dequantisation overlap the other's
- * matrix-core work. */
-template <bool SW, int NR, int MT, int D, bool DBT, bool APF>
-__global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
-  static_assert(!SW || NR == 2, "SwiGLU pairs gate and up rows");
+/* Expand steps per chunk: their token tiles occupy LDS regions of 16 KB each. */
+#ifndef AOS_GEMM_LC_SW
+#define AOS_GEMM_LC_SW 2
+#endif
+__host__ __device__ constexpr int gemm_lchunk(bool sw) { return sw ? AOS_GEMM_LC_SW : 4; }
+
+/* SW: SwiGLU (gate and up rows of one row block per wave) or a single matrix (one row block per
+ * wave); MT: 32-token sub-tiles; D: weight ring depth (divides the group count); DB: token tile
+ * loads two groups ahead (two register stages); APF: next sub-tile's LDS fragments loaded before
+ * the current MFMAs; WV: waves per workgroup. */
+template <bool SW, int MT, int D, bool DBT, bool APF, int WV>
+__global__ void __launch_bounds__(64 * WV, 2) aos_gemm_kernel(aos_gemm_params p) {
   constexpr int BM = 32 * MT;
   constexpr int TILE = BM * 128;
+  constexpr int NT = 64 * WV;
+  constexpr int LC = gemm_lchunk(SW);
+  constexpr int NTILE = LC > 2 ? LC : 2;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  /* after the token tiles: step counts, the tile's slot mask, the union's B pointers (when the
+   * union bound is at most LBP) and the step list */
+  unsigned char *aux = smem + NTILE * TILE;
+  int *ls_n = (int *)aux;
+  uint32_t *mw = (uint32_t *)(aux + 16);
+  const uint16_t **lbp = (const uint16_t **)(aux + 16 + 4 * AOS_MAX_ADAPTERS / 32);
+  uint16_t *ls = (uint16_t *)(aux + GEMM_AUX);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, c = lane >> 5;
 
-  /* XCD-aware order: workgroup b runs on XCD b % 8; tiles are numbered with the token tile
-   * fastest and dealt out so that each XCD gets a contiguous range of them. */
+  /* XCD-aware order: workgroup b runs on XCD b % 8. With a multiple of 8 token tiles each XCD
+   * takes its own token tiles against every weight block (its L2 keeps those token rows while
+   * the weights stream); otherwise each XCD takes a contiguous range of tiles (token tile
+   * fastest), so a weight block's token tiles share its L2. */
   const int nt = p.mb * p.nb;
   const int b = blockIdx.x;
-  int tile = b;
-  if (nt % 8 == 0) tile = (b & 7) * (nt / 8) + (b >> 3);
-  const int mbi = tile % p.mb, nbk = tile / p.mb;
+  int mbi, nbk;
+  if (p.mb % 8 == 0) {
+    const int mpx = p.mb / 8, k = b >> 3;
+    mbi = (b & 7) * mpx + k % mpx;
+    nbk = k / mpx;
+  } else {
+    int tile = b;
+    if (nt % 8 == 0) tile = (b & 7) * (nt / 8) + (b >> 3);
+    mbi = tile % p.mb;
+    nbk = tile / p.mb;
+  }
   const int m0 = mbi * BM;
   const int G = p.w0.G, in = p.w0.in, RB = p.w0.RB;
 
-  /* weight row blocks of this wave */
-  const int rb0 = SW ? nbk * 4 + wave : nbk * 4 * NR + NR * wave;
-  const int rb1 = SW ? rb0 : rb0 + 1;
-  const bool live0 = rb0 < RB;
-  const bool live1 = SW ? live0 : (NR == 2 && rb1 < RB);
-  const int r0 = live0 ? rb0 : RB - 1;
-  const int r1 = SW ? r0 : (live1 ? rb1 : r0);
+  /* this wave's weight row block (dead blocks past RB read the last one and store nothing) */
+  const int rb = nbk * WV + wave;
+  const bool live = rb < RB;
+  const int r0 = live ? rb : RB - 1;
   const aos_q4_dev &W0 = p.w0;
   const aos_q4_dev &W1 = SW ? p.w1 : p.w0;
   const u32x4 *q0 = (const u32x4 *)W0.qt + (size_t)r0 * G * 64 + lane;
-  const u32x4 *q1 = (const u32x4 *)W1.qt + (size_t)r1 * G * 64 + lane;
+  const u32x4 *q1 = (const u32x4 *)W1.qt + (size_t)r0 * G * 64 + lane;
   const uint32_t *s0p = W0.sb + (size_t)r0 * G * 32 + i;
-  const uint32_t *s1p = W1.sb + (size_t)r1 * G * 32 + i;
+  const uint32_t *s1p = W1.sb + (size_t)r0 * G * 32 + i;
+  const int row = r0 * 32 + i;
 
   f32x16 acc0[MT], acc1[MT];
 #pragma unroll
@@ -432,7 +423,7 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
   for (int d = 0; d < D; ++d) {
     wq0[d] = q0[(size_t)d * 64];
     ws0[d] = s0p[(size_t)d * 32];
-    if (NR == 2) {
+    if (SW) {
       wq1[d] = q1[(size_t)d * 64];
       ws1[d] = s1p[(size_t)d * 32];
     }
@@ -441,24 +432,48 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
    * flight. With D even, two register stages let the loads run two groups ahead of their LDS
    * store. */
   constexpr bool DB = DBT && (D % 2) == 0;
-  Stager<BM> st0, st1;
+  Stager<BM, NT> st0, st1;
   st0.load(p.x, in, p.T, m0, 0, tid);
+
+  /* LoRA bookkeeping for the expand steps after the K loop: the tile's slot mask words and
+   * (union bound <= LBP) the union's B pointers go straight to LDS now; their loads complete
+   * during the K loop. */
+  const bool lora = (p.tab0.rpad | (SW ? p.tab1.rpad : 0)) != 0;
+  const int Ue = p.plan->U < p.umax ? p.plan->U : p.umax;
+  const bool bp_lds = p.umax <= LBP;
+  if (lora) {
+    const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.tile_mask + (size_t)mbi * p.mwords), (short)0, p.mwords * 4, 0x00020000);
+    for (int w0 = wave * 64; w0 < p.mwords; w0 += NT)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (__attribute__((address_space(3))) void *)(mw + w0), 4,
+                                               (w0 + lane) * 4, 0, 0, 0);
+    if (bp_lds) {
+#pragma unroll
+      for (int m = 0; m < (SW ? 2 : 1); ++m) {
+        const __amdgpu_buffer_rsrc_t rb =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(m ? p.bp1 : p.bp0), (short)0, p.umax * 8, 0x00020000);
+        for (int d0 = wave * 64; d0 < 2 * p.umax; d0 += NT)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rb, (__attribute__((address_space(3))) void *)((uint32_t *)(lbp + m * LBP) + d0), 4,
+              (d0 + lane) * 4, 0, 0, 0);
+      }
+    }
+  }
   st0.store(smem, tid);
-  if (DB) st1.load(p.x, in, p.T, m0, G > 1 ? 1 : 0, tid);
   lds_barrier();
 
+  /* token tile of weight group gx (clamped: the tiles staged past the last group are not read) */
+  auto stage = [&](Stager<BM, NT> &st, const int gx) { st.load(p.x, in, p.T, m0, gx < G ? gx : G - 1, tid); };
+  if (DB) stage(st1, 1);
+
   /* one K group: ld receives group g + 2 (g + 1 without DB), sto holds group g + 1 */
-  auto group = [&](const int g, const int d, Stager<BM> &ld, Stager<BM> &sto) {
+  auto group = [&](const int g, const int d, Stager<BM, NT> &ld, Stager<BM, NT> &sto) {
     const unsigned char *tb = smem + (g & 1) * TILE;
     /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
     u32x4 a[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(i, 4 * c + s));
-    {
-      const int ahead = DB ? 2 : 1;
-      const int gx = g + ahead < G ? g + ahead : G - 1;
-      ld.load(p.x, in, p.T, m0, gx, tid);
-    }
+    stage(ld, g + (DB ? 2 : 1));
     /* dequantise this group's row blocks into B fragments */
     u32x4 f0[4], f1[4];
     {
@@ -466,7 +481,7 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) f0[s] = dequant_word(wq0[d][s], sc, bi);
     }
-    if (NR == 2) {
+    if (SW) {
       const float sc = aos_f16_to_f32(ws1[d] & 0xffffu), bi = aos_f16_to_f32(ws1[d] >> 16);
 #pragma unroll
       for (int s = 0; s < 4; ++s) f1[s] = dequant_word(wq1[d][s], sc, bi);
@@ -476,7 +491,7 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
       const int gn = g + D < G ? g + D : G - 1;
       wq0[d] = q0[(size_t)gn * 64];
       ws0[d] = s0p[(size_t)gn * 32];
-      if (NR == 2) {
+      if (SW) {
         wq1[d] = q1[(size_t)gn * 64];
         ws1[d] = s1p[(size_t)gn * 32];
       }
@@ -496,7 +511,7 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
       for (int s = 0; s < 4; ++s) {
         /* word s of lane (i, c) covers K elements 32 c + 8 s .. +7: chunk 4 c + s */
         acc0[mt] = aos_mfma32(a[s], f0[s], acc0[mt]);
-        if (NR == 2) acc1[mt] = aos_mfma32(a[s], f1[s], acc1[mt]);
+        if (SW) acc1[mt] = aos_mfma32(a[s], f1[s], acc1[mt]);
       }
       if (APF && mt + 1 < MT) {
 #pragma unroll
@@ -520,18 +535,149 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
     }
   }
 
-  /* LoRA expand over the tile's union slots */
-  const int row0 = r0 * 32 + i, row1 = r1 * 32 + i;
-  if (SW) {
-    const int rows[2] = {row0, row0};
-    expand_module<MT, 1>(p, p.tab0, p.s_off0, rows, m0, mbi, lane, acc0, acc0);
-    expand_module<MT, 1>(p, p.tab1, p.s_off1, rows, m0, mbi, lane, acc1, acc1);
-  } else {
-    const int rows[2] = {row0, row1};
-    expand_module<MT, NR>(p, p.tab0, p.s_off0, rows, m0, mbi, lane, acc0, acc1);
+  /* LoRA expand steps, in chunks of LC steps that stay within one module. A chunk's token
+   * tiles (the steps' SA columns, through a buffer resource over the tile's rows; chunks past
+   * the union read as zeros) go straight from memory to LDS regions 0 .. LC - 1, its B fragments
+   * to registers: word s of lane (i, c) holds union columns k = 64 j + 32 c + 8 s .. +7 of this
+   * wave's row, B_{list[u]}[row][k - u * rpad .. +7] with u = k / rpad (zeros past the union or
+   * for an adapter without the module; rpad is a multiple of 16, so words 0-1 and 2-3 each share
+   * a slot). One wait per chunk; the next chunk's B pointers load meanwhile. */
+  int nls = 0;
+  if (lora) {
+    /* the tile's expand steps, listed by wave 0 (ascending module, then column) */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    if (wave == 0) {
+      int n = 0;
+#pragma unroll
+      for (int m = 0; m < (SW ? 2 : 1); ++m) {
+        if (m == 1 && lane == 0) ls_n[1] = n < p.lsteps_max ? n : p.lsteps_max; /* gate steps */
+        const int rpad = m ? p.tab1.rpad : p.tab0.rpad;
+        const int nj = rpad ? (Ue * rpad + 63) >> 6 : 0;
+        for (int j0 = 0; j0 < nj; j0 += 64) {
+          const int j = j0 + lane;
+          bool act = false;
+          if (j < nj) {
+            const int ulo = (64 * j) / rpad;
+            int uhi = (64 * j + 63) / rpad;
+            uhi = uhi < Ue - 1 ? uhi : Ue - 1;
+            for (int u = ulo; u <= uhi; ++u) act |= ((mw[u >> 5] >> (u & 31)) & 1u) != 0;
+          }
+          const uint64_t bal = __ballot(act);
+          const int at = n + __popcll(bal & ((1ull << lane) - 1ull));
+          if (act && at < p.lsteps_max) ls[at] = (uint16_t)((m << 15) | j);
+          n += __popcll(bal);
+        }
+      }
+      if (lane == 0) ls_n[0] = n < p.lsteps_max ? n : p.lsteps_max;
+    }
+    lds_barrier();
+    nls = __builtin_amdgcn_readfirstlane(ls_n[0]);
+  }
+  if (nls > 0) {
+    const int rows = p.T - m0 < BM ? p.T - m0 : BM;
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.SA + (size_t)m0 * p.sa_stride), (short)0, rows * p.sa_stride * 2, 0x00020000);
+    const int n0 = SW ? __builtin_amdgcn_readfirstlane(ls_n[1]) : nls; /* gate steps, then up */
+    auto step_of = [&](int l, int &m, int &j, int &rpad) {
+      l = l < nls ? l : nls - 1;
+      const int d = __builtin_amdgcn_readfirstlane((int)ls[l > 0 ? l : 0]);
+      m = d >> 15;
+      j = d & 0x7fff;
+      rpad = m ? p.tab1.rpad : p.tab0.rpad;
+    };
+    auto load_ptrs = [&](int l, const uint16_t *(&pr)[2]) {
+      int m, j, rpad;
+      step_of(l, m, j, rpad);
+      const uint16_t *const *bp = m ? p.bp1 : p.bp0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int u = (64 * j + 32 * c + 16 * h) / rpad;
+        u = u < Ue ? u : Ue - 1;
+        pr[h] = bp_lds ? lbp[m * LBP + u] : bp[u];
+      }
+    };
+    auto load_frags = [&](int l, const uint16_t *const (&pr)[2], u32x4 (&bv)[4]) {
+      int m, j, rpad;
+      step_of(l, m, j, rpad);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 64 * j + 32 * c + 16 * h;
+        const int u = k / rpad;
+        const uint16_t *src = (u < Ue && pr[h]) ? pr[h] + (size_t)row * rpad + (k - u * rpad) : p.zero;
+        bv[2 * h] = *(const u32x4 *)src;
+        bv[2 * h + 1] = *(const u32x4 *)((u < Ue && pr[h]) ? src + 8 : p.zero);
+      }
+    };
+    /* token tile of step l into LDS region q: 16 blocks of 8 rows (1 KB), lane l of a block
+     * writing bytes 16 l, i.e. row 8 b + l / 8, slot l % 8, which holds chunk slot ^ ((r >> 1) & 7) */
+    auto dma_tile = [&](int q, int l) {
+      int m, j, rpad;
+      step_of(l, m, j, rpad);
+      const int off = m ? p.s_off1 : p.s_off0;
+      const int cb = (off + 64 * j) * 2, lim = (off + Ue * rpad) * 2, rb = p.sa_stride * 2;
+#pragma unroll
+      for (int k = 0; k < 16 / WV; ++k) {
+        const int bk = k * WV + wave;
+        const int r = bk * 8 + (lane >> 3);
+        const int ch = (lane & 7) ^ ((r >> 1) & 7);
+        const int rr = r < rows ? r : rows - 1;
+        const int col = cb + ch * 16;
+        const int vo = col < lim ? rr * rb + col : (int)0x80000000;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, 0);
+      }
+    };
+    auto mma = [&](const unsigned char *tb, const u32x4 (&bv)[4], f32x16 (&acc)[MT]) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 a[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[mt] = aos_mfma32(a[s], bv[s], acc[mt]);
+      }
+    };
+    /* B pointers of the chunk starting at step l (steps past its module's end repeat its last) */
+    const uint16_t *pr[LC][2];
+    auto chunk_ptrs = [&](int l) {
+      const int e = l < n0 ? n0 : nls;
+#pragma unroll
+      for (int q = 0; q < LC; ++q) load_ptrs(l + q < e ? l + q : e - 1, pr[q]);
+    };
+    chunk_ptrs(0);
+    int l0 = 0;
+    while (l0 < nls) {
+      const int end = l0 < n0 ? n0 : nls;
+      const int n = end - l0 < LC ? end - l0 : LC;
+      u32x4 bv[LC][4];
+#pragma unroll
+      for (int q = 0; q < LC; ++q) {
+        if (q < n) {
+          dma_tile(q, l0 + q);
+          load_frags(l0 + q, pr[q], bv[q]);
+        }
+      }
+      if (l0 + n < nls) chunk_ptrs(l0 + n);
+      /* the LDS writes of the buffer loads are complete once vmcnt drains */
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();
+      if (!SW || l0 < n0) {
+#pragma unroll
+        for (int q = 0; q < LC; ++q)
+          if (q < n) mma(smem + q * TILE, bv[q], acc0);
+      } else {
+#pragma unroll
+        for (int q = 0; q < LC; ++q)
+          if (q < n) mma(smem + q * TILE, bv[q], acc1);
+      }
+      lds_barrier();
+      l0 += n;
+    }
   }
 
   /* epilogue */
+  if (!live) return;
   const int out = p.w0.out;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -540,13 +686,11 @@ __global__ void __launch_bounds__(256, 2) aos_gemm_kernel(aos_gemm_params p) {
       const int tok = m0 + mt * 32 + aos_acc_m(v, lane);
       if (tok >= p.T) continue;
       if (SW) {
-        if (!live0) continue;
         const float gt = acc0[mt][v], up = acc1[mt][v];
         const float sg = 1.0f / (1.0f + expf(-gt));
-        p.y[(size_t)tok * out + row0] = aos_f32_to_bf16((gt * sg) * up);
+        p.y[(size_t)tok * out + row] = aos_f32_to_bf16((gt * sg) * up);
       } else {
-        if (live0) p.y[(size_t)tok * out + row0] = aos_f32_to_bf16(acc0[mt][v]);
-        if (NR == 2 && live1) p.y[(size_t)tok * out + row1] = aos_f32_to_bf16(acc1[mt][v]);
+        p.y[(size_t)tok * out + row] = aos_f32_to_bf16(acc0[mt][v]);
       }
     }
   }
@@ -574,27 +718,33 @@ extern "C" int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_
 }
 
 /* Measured on the 7B-shaped layer at 2048 tokens: the SwiGLU kernel is fastest with a shallow
- * ring and single staging (fewer registers), the single-matrix kernel with the deep pipeline. */
-template <bool SW, int NR>
+ * ring, single staging and 4-wave workgroups (two per CU); the single-matrix kernel with the
+ * deep pipeline and 8-wave workgroups (256 weight rows against one token tile). */
+static constexpr int gemm_waves(bool sw) { return sw ? 4 : 8; }
+
+template <bool SW>
 static void launch_gemm_d(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
-  constexpr int MT = AOS_GEMM_BM / 32;
+  constexpr int MT = AOS_GEMM_BM / 32, WV = gemm_waves(SW);
   constexpr int D4 = SW ? 2 : 4;
   constexpr bool DBT = !SW, APF = !SW;
-  const size_t lds = 2 * AOS_GEMM_BM * 128;
-  const dim3 grid(p->mb * p->nb);
+  constexpr int LC = gemm_lchunk(SW), NTILE = LC > 2 ? LC : 2;
+  const size_t lds = (size_t)NTILE * AOS_GEMM_BM * 128 + GEMM_AUX + ((size_t)p->lsteps_max * 2 + 15) / 16 * 16;
+  const dim3 grid(p->mb * p->nb), block(64 * WV);
   const int G = p->w0.G;
   if (G % D4 == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, NR, MT, D4, DBT, APF>), grid, dim3(256), lds, *p);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, D4, DBT, APF, WV>), grid, block, lds, *p);
   else if (G % 2 == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, NR, MT, 2, DBT, APF>), grid, dim3(256), lds, *p);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 2, DBT, APF, WV>), grid, block, lds, *p);
   else
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, NR, MT, 1, DBT, APF>), grid, dim3(256), lds, *p);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 1, DBT, APF, WV>), grid, block, lds, *p);
 }
+
+extern "C" int aos_gemm_waves(int swiglu) { return gemm_waves(swiglu != 0); }
 
 extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx) {
   if (swiglu)
-    launch_gemm_d<true, 2>(p, ctx);
+    launch_gemm_d<true>(p, ctx);
   else
-    launch_gemm_d<false, 1>(p, ctx);
+    launch_gemm_d<false>(p, ctx);
   return (int)hipGetLastError();
 }

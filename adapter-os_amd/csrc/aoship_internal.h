@@ -152,6 +152,9 @@ typedef struct {
   int cstride;          /* >= union size bound */
   uint32_t *tile_mask;  /* [mtiles][mwords] */
   int mwords;
+  int nmod;             /* modules whose B tables bp receives */
+  aos_lora_tab tab[3];
+  const uint16_t **bp;  /* [nmod][cstride]: B of union slot u, NULL when absent or u >= U */
 } aos_pplan_params;
 
 /* Shrink over the union for T tokens, finished with the coefficients:
@@ -179,7 +182,8 @@ typedef struct {
 
 /* int4 GEMM with LoRA expand: y[t][o] = sum_i x[t][i] w[o][i] +
  * sum_u SA[t][s_off + u * rpad + j] . B_{list[u]}[o][j] over the union slots u used by the token
- * tile. SwiGLU mode computes gate (w0) and up (w1) and writes (g * sigmoid(g)) * u. */
+ * tile, the expand taken as extra K steps of 64 union columns (those holding a slot the tile
+ * uses). SwiGLU mode computes gate (w0) and up (w1) and writes (g * sigmoid(g)) * u. */
 typedef struct {
   aos_q4_dev w0, w1;
   const uint16_t *x;  /* [T][in] */
@@ -191,8 +195,21 @@ typedef struct {
   const aos_pplan *plan;
   const uint32_t *tile_mask;
   int mwords;
+  const uint16_t *const *bp0, *const *bp1; /* [umax] B per union slot (plan table rows) */
+  int umax;
+  int lsteps_max;     /* bound on the expand K steps of a tile (LDS list length) */
+  const uint16_t *zero; /* 16 zero bytes: source of SA chunks past the union */
   uint16_t *y;        /* [T][out] */
 } aos_gemm_params;
+
+/* Bound on the expand K steps of one M tile for a module: all the 64-column steps of its union
+ * columns, and at most 8 slots per token, each spanning at most rpad / 64 + 2 steps. */
+static inline int aos_lstep_bound(int umax, int rpad) {
+  if (rpad == 0) return 0;
+  const int all = (umax * rpad + 63) / 64;
+  const int used = AOS_GEMM_BM * 8 * (rpad / 64 + 2);
+  return all < used ? all : used;
+}
 
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
  * records at kernel start and end (hipExtLaunchKernelGGL). */
@@ -232,6 +249,7 @@ int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_gemm_waves(int swiglu); /* waves per GEMM workgroup (32 weight rows each) */
 #ifdef __cplusplus
 }
 #endif
