@@ -969,8 +969,7 @@ static void plan_gemm(aoship_layer *l, const PrefillPlan &P, const aos_pshrink_p
   if (W1) g.w1 = W1->dev();
   g.x = x;
   g.T = T;
-  g.mb = P.mtiles;
-  g.nb = ceil_div(W0.RB, aos_gemm_waves(W1 != nullptr)); /* one 32-row block per wave */
+
   g.tab0 = t0;
   if (t1) g.tab1 = *t1;
   g.SA = sp.SA;

@@ -338,66 +338,254 @@ __global__ void __launch_bounds__(256) aos_pfinish_kernel(aos_pshrink_params p) 
 /* ------------------------------------------------------------------------------------------ */
 
 /* Expand K steps: the LoRA expand of a token tile runs as extra K steps of 64 columns after the
- * weight groups. The token operand is SA (coefficient-scaled shrink of the union slots, staged in
- * LDS like x), the weight operand the union adapters' B rows (bf16, straight to registers). A
- * step is listed as (module << 15) | j, j = index of its 64 columns among the module's union
- * columns u * rpad + r; a tile lists only the steps that hold a slot one of its tokens uses. */
-
-/* LDS after the token tiles: 16 bytes of counts, the slot mask words, LBP B pointers per module
- * (two modules), then the step list. */
+ * weight groups. The token operand is SA (coefficient-scaled shrink of the union slots), the
+ * weight operand the union adapters' B rows (bf16). A step is listed as (module << 15) | j, j =
+ * index of its 64 columns among the module's union columns u * rpad + r; a tile lists only the
+ * steps that hold a slot one of its tokens uses.
+ *
+ * LDS after the token tiles: 16 bytes of counts, the slot mask words of the BM / 128 plan tiles
+ * the token tile spans, LBP B pointers per module (two modules), then the step list. */
 constexpr int LBP = 256;
-constexpr int GEMM_AUX = 16 + 4 * AOS_MAX_ADAPTERS / 32 + 2 * LBP * 8;
+constexpr int MASK_WORDS = AOS_MAX_ADAPTERS / 32;
+__host__ __device__ constexpr int gemm_aux(int bm) { return 16 + 4 * MASK_WORDS * (bm / AOS_GEMM_BM) + 2 * LBP * 8; }
 
-/* Expand steps per chunk: their token tiles occupy LDS regions of 16 KB each. */
-#ifndef AOS_GEMM_LC_SW
-#define AOS_GEMM_LC_SW 2
-#endif
-__host__ __device__ constexpr int gemm_lchunk(bool sw) { return sw ? AOS_GEMM_LC_SW : 4; }
-
-/* SW: SwiGLU (gate and up rows of one row block per wave) or a single matrix (one row block per
- * wave); MT: 32-token sub-tiles; D: weight ring depth (divides the group count); DB: token tile
- * loads two groups ahead (two register stages); APF: next sub-tile's LDS fragments loaded before
- * the current MFMAs; WV: waves per workgroup. */
-template <bool SW, int MT, int D, bool DBT, bool APF, int WV>
-__global__ void __launch_bounds__(64 * WV, 2) aos_gemm_kernel(aos_gemm_params p) {
-  constexpr int BM = 32 * MT;
-  constexpr int TILE = BM * 128;
-  constexpr int NT = 64 * WV;
-  constexpr int LC = gemm_lchunk(SW);
-  constexpr int NTILE = LC > 2 ? LC : 2;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  /* after the token tiles: step counts, the tile's slot mask, the union's B pointers (when the
-   * union bound is at most LBP) and the step list */
-  unsigned char *aux = smem + NTILE * TILE;
-  int *ls_n = (int *)aux;
-  uint32_t *mw = (uint32_t *)(aux + 16);
-  const uint16_t **lbp = (const uint16_t **)(aux + 16 + 4 * AOS_MAX_ADAPTERS / 32);
-  uint16_t *ls = (uint16_t *)(aux + GEMM_AUX);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int i = lane & 31, c = lane >> 5;
-
-  /* XCD-aware order: workgroup b runs on XCD b % 8. With a multiple of 8 token tiles each XCD
-   * takes its own token tiles against every weight block (its L2 keeps those token rows while
-   * the weights stream); otherwise each XCD takes a contiguous range of tiles (token tile
-   * fastest), so a weight block's token tiles share its L2. */
-  const int nt = p.mb * p.nb;
-  const int b = blockIdx.x;
-  int mbi, nbk;
-  if (p.mb % 8 == 0) {
-    const int mpx = p.mb / 8, k = b >> 3;
+/* Workgroup b of a grid of mb token tiles x nb weight blocks -> (token tile, weight block).
+ * Workgroup b runs on XCD b % 8. With a multiple of 8 token tiles each XCD takes its own token
+ * tiles against every weight block (its L2 keeps those token rows while the weights stream);
+ * otherwise each XCD takes a contiguous range of tiles (token tile fastest), so a weight block's
+ * token tiles share its L2. */
+__device__ __forceinline__ void gemm_tile_of(int b, int mb, int nb, int &mbi, int &nbk) {
+  if (mb % 8 == 0) {
+    const int mpx = mb / 8, k = b >> 3;
     mbi = (b & 7) * mpx + k % mpx;
     nbk = k / mpx;
   } else {
+    const int nt = mb * nb;
     int tile = b;
     if (nt % 8 == 0) tile = (b & 7) * (nt / 8) + (b >> 3);
-    mbi = tile % p.mb;
-    nbk = tile / p.mb;
+    mbi = tile % mb;
+    nbk = tile / mb;
   }
+}
+
+/* The expand steps of one token tile (BM tokens, WV waves, NM modules). Each lane's B fragment
+ * word w of a step holds union columns k = 64 j + koff[w] .. +7 of the lane's weight row:
+ * B_{list[u]}[row][k - u * rpad .. +7] with u = k / rpad, zeros past the union or for an adapter
+ * without the module (rpad is a multiple of 16, so 8 columns never straddle two slots). Words
+ * w and w + 1 share a slot when NW / NP = 2 (koff 16-aligned for w even). */
+template <int BM, int WV, int NM, int NW, int NP>
+struct Expand {
+  static constexpr int MR = BM / AOS_GEMM_BM; /* plan tiles per token tile */
+  static constexpr int TILE = BM * 128;
+  const aos_gemm_params &p;
+  unsigned char *smem;
+  int *ls_n;
+  uint32_t *mw;
+  const uint16_t **lbp;
+  uint16_t *ls;
+  int wave, lane, m0, mbi, row, Ue;
+  bool lora, bp_lds;
+
+  /* row: the lane's weight row (of every module) */
+  __device__ Expand(const aos_gemm_params &p_, unsigned char *smem_, int ntile, int wave_, int lane_, int m0_,
+                    int mbi_, int row_)
+      : p(p_), smem(smem_), wave(wave_), lane(lane_), m0(m0_), mbi(mbi_), row(row_) {
+    unsigned char *aux = smem + ntile * TILE;
+    ls_n = (int *)aux;
+    mw = (uint32_t *)(aux + 16);
+    lbp = (const uint16_t **)(aux + 16 + 4 * MASK_WORDS * MR);
+    ls = (uint16_t *)(aux + gemm_aux(BM));
+    lora = (p.tab0.rpad | (NM == 2 ? p.tab1.rpad : 0)) != 0;
+    Ue = p.plan->U < p.umax ? p.plan->U : p.umax;
+    bp_lds = p.umax <= LBP;
+  }
+
+  /* At kernel start: the tile's slot mask words and (union bound <= LBP) the union's B pointers
+   * go straight to LDS; their loads complete during the K loop. */
+  __device__ void prefetch() {
+    if (!lora) return;
+    constexpr int NT = 64 * WV;
+    const int ptiles = (p.T + AOS_GEMM_BM - 1) / AOS_GEMM_BM;
+    const int pr0 = mbi * MR;
+    const int npr = ptiles - pr0 < MR ? ptiles - pr0 : MR;
+    const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.tile_mask + (size_t)pr0 * p.mwords), (short)0, npr * p.mwords * 4, 0x00020000);
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+      for (int w0 = wave * 64; w0 < p.mwords; w0 += NT)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rm, (__attribute__((address_space(3))) void *)(mw + r * MASK_WORDS + w0), 4,
+            r < npr ? (r * p.mwords + w0 + lane) * 4 : (int)0x80000000, 0, 0, 0);
+    if (bp_lds) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        const __amdgpu_buffer_rsrc_t rb =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(m ? p.bp1 : p.bp0), (short)0, p.umax * 8, 0x00020000);
+        for (int d0 = wave * 64; d0 < 2 * p.umax; d0 += NT)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rb, (__attribute__((address_space(3))) void *)((uint32_t *)(lbp + m * LBP) + d0), 4,
+              (d0 + lane) * 4, 0, 0, 0);
+      }
+    }
+  }
+
+  /* After the K loop (all waves): wave 0 lists the tile's steps, ascending module then column.
+   * Returns the step count; n0 receives the count of module 0's steps. */
+  __device__ int build(int &n0) {
+    n0 = 0;
+    if (!lora) return 0;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    if (wave == 0) {
+      int n = 0;
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        if (m == 1 && lane == 0) ls_n[1] = n < p.lsteps_max ? n : p.lsteps_max;
+        const int rpad = m ? p.tab1.rpad : p.tab0.rpad;
+        const int nj = rpad ? (Ue * rpad + 63) >> 6 : 0;
+        for (int j0 = 0; j0 < nj; j0 += 64) {
+          const int j = j0 + lane;
+          bool act = false;
+          if (j < nj) {
+            const int ulo = (64 * j) / rpad;
+            int uhi = (64 * j + 63) / rpad;
+            uhi = uhi < Ue - 1 ? uhi : Ue - 1;
+            for (int u = ulo; u <= uhi; ++u) {
+              uint32_t wd = 0;
+#pragma unroll
+              for (int r = 0; r < MR; ++r) wd |= mw[r * MASK_WORDS + (u >> 5)];
+              act |= ((wd >> (u & 31)) & 1u) != 0;
+            }
+          }
+          const uint64_t bal = __ballot(act);
+          const int at = n + __popcll(bal & ((1ull << lane) - 1ull));
+          if (act && at < p.lsteps_max) ls[at] = (uint16_t)((m << 15) | j);
+          n += __popcll(bal);
+        }
+      }
+      if (lane == 0) ls_n[0] = n < p.lsteps_max ? n : p.lsteps_max;
+    }
+    lds_barrier();
+    const int nls = __builtin_amdgcn_readfirstlane(ls_n[0]);
+    n0 = NM == 2 ? __builtin_amdgcn_readfirstlane(ls_n[1]) : nls;
+    return nls;
+  }
+
+  __device__ void step_of(int l, int nls, int &m, int &j, int &rpad) const {
+    l = l < nls ? l : nls - 1;
+    const int d = __builtin_amdgcn_readfirstlane((int)ls[l > 0 ? l : 0]);
+    m = d >> 15;
+    j = d & 0x7fff;
+    rpad = m ? p.tab1.rpad : p.tab0.rpad;
+  }
+
+  /* Runs the nls steps in chunks of LC steps within one module. A chunk's token tiles (the
+   * steps' SA columns, through a buffer resource over the tile's rows; chunks past the union
+   * read as zeros) go straight from memory to LDS regions 0 .. LC - 1, its B fragments to
+   * registers; one wait per chunk, the next chunk's B pointers loading meanwhile. mma(m, n, bv)
+   * adds the chunk's n steps of module m (token tile q at smem + q * TILE). */
+  template <int LC, class Mma>
+  __device__ void run(int nls, int n0, const int (&koff)[NW], Mma &&mma) {
+    const int rows = p.T - m0 < BM ? p.T - m0 : BM;
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.SA + (size_t)m0 * p.sa_stride), (short)0, rows * p.sa_stride * 2, 0x00020000);
+    auto load_ptrs = [&](int l, const uint16_t *(&pr)[NP]) {
+      int m, j, rpad;
+      step_of(l, nls, m, j, rpad);
+      const uint16_t *const *bp = m ? p.bp1 : p.bp0;
+#pragma unroll
+      for (int h = 0; h < NP; ++h) {
+        int u = (64 * j + koff[h * (NW / NP)]) / rpad;
+        u = u < Ue ? u : Ue - 1;
+        pr[h] = bp_lds ? lbp[m * LBP + u] : bp[u];
+      }
+    };
+    auto load_frags = [&](int l, const uint16_t *const (&pr)[NP], u32x4 (&bv)[NW]) {
+      int m, j, rpad;
+      step_of(l, nls, m, j, rpad);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const uint16_t *b = pr[w / (NW / NP)];
+        const int k = 64 * j + koff[w];
+        const int u = k / rpad;
+        const uint16_t *src = (u < Ue && b) ? b + (size_t)row * rpad + (k - u * rpad) : p.zero;
+        bv[w] = *(const u32x4 *)src;
+      }
+    };
+    /* token tile of step l into LDS region q: BM / 8 blocks of 8 rows (1 KB), lane l of a block
+     * writing bytes 16 l, i.e. row 8 b + l / 8, slot l % 8, which holds chunk slot ^ ((r >> 1) & 7) */
+    auto dma_tile = [&](int q, int l) {
+      int m, j, rpad;
+      step_of(l, nls, m, j, rpad);
+      const int off = m ? p.s_off1 : p.s_off0;
+      const int cb = (off + 64 * j) * 2, lim = (off + Ue * rpad) * 2, rb = p.sa_stride * 2;
+#pragma unroll
+      for (int k = 0; k < BM / 8 / WV; ++k) {
+        const int bk = k * WV + wave;
+        const int r = bk * 8 + (lane >> 3);
+        const int ch = (lane & 7) ^ ((r >> 1) & 7);
+        const int rr = r < rows ? r : rows - 1;
+        const int col = cb + ch * 16;
+        const int vo = col < lim ? rr * rb + col : (int)0x80000000;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, 0);
+      }
+    };
+    const uint16_t *pr[LC][NP];
+    auto chunk_ptrs = [&](int l) {
+      const int e = l < n0 ? n0 : nls;
+#pragma unroll
+      for (int q = 0; q < LC; ++q) load_ptrs(l + q < e ? l + q : e - 1, pr[q]);
+    };
+    chunk_ptrs(0);
+    int l0 = 0;
+    while (l0 < nls) {
+      const int end = l0 < n0 ? n0 : nls;
+      const int n = end - l0 < LC ? end - l0 : LC;
+      u32x4 bv[LC][NW];
+#pragma unroll
+      for (int q = 0; q < LC; ++q) {
+        if (q < n) {
+          dma_tile(q, l0 + q);
+          load_frags(l0 + q, pr[q], bv[q]);
+        }
+      }
+      if (l0 + n < nls) chunk_ptrs(l0 + n);
+      /* the LDS writes of the buffer loads are complete once vmcnt drains */
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();
+      mma(l0 < n0 ? 0 : 1, n, bv);
+      lds_barrier();
+      l0 += n;
+    }
+  }
+};
+
+/* Single-matrix kernel (and SwiGLU for short prefills) on v_mfma_f32_32x32x16_bf16.
+ * SW: SwiGLU (gate and up rows of one 32-row block per wave) or a single matrix (one 32-row
+ * block per wave); MT: 32-token sub-tiles (token tile of 32 MT rows, a multiple of the 128-token
+ * plan tile); D: weight ring depth (divides the group count); DB: token tile loads two groups
+ * ahead (two register stages); APF: next sub-tile's LDS fragments loaded before the current
+ * MFMAs; WV: waves per workgroup; OCC: waves per SIMD the registers are sized for; LC: expand
+ * steps per chunk (their token tiles occupy LC LDS regions). */
+template <bool SW, int MT, int D, bool DBT, bool APF, int WV, int OCC, int LC>
+__global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params p) {
+  static_assert(MT % 4 == 0, "token tiles are whole plan tiles");
+  constexpr int BM = 32 * MT;
+  constexpr int TILE = BM * 128;
+  constexpr int NT = 64 * WV;
+  constexpr int NTILE = LC > 2 ? LC : 2;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, c = lane >> 5;
+  int mbi, nbk;
+  gemm_tile_of(blockIdx.x, p.mb, p.nb, mbi, nbk);
   const int m0 = mbi * BM;
   const int G = p.w0.G, in = p.w0.in, RB = p.w0.RB;
 
-  /* this wave's weight row block (dead blocks past RB read the last one and store nothing) */
+  /* this wave's 32-row block (of gate and of up for SW); dead blocks past the last read it and
+   * store nothing */
   const int rb = nbk * WV + wave;
   const bool live = rb < RB;
   const int r0 = live ? rb : RB - 1;
@@ -434,31 +622,8 @@ __global__ void __launch_bounds__(64 * WV, 2) aos_gemm_kernel(aos_gemm_params p)
   constexpr bool DB = DBT && (D % 2) == 0;
   Stager<BM, NT> st0, st1;
   st0.load(p.x, in, p.T, m0, 0, tid);
-
-  /* LoRA bookkeeping for the expand steps after the K loop: the tile's slot mask words and
-   * (union bound <= LBP) the union's B pointers go straight to LDS now; their loads complete
-   * during the K loop. */
-  const bool lora = (p.tab0.rpad | (SW ? p.tab1.rpad : 0)) != 0;
-  const int Ue = p.plan->U < p.umax ? p.plan->U : p.umax;
-  const bool bp_lds = p.umax <= LBP;
-  if (lora) {
-    const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.tile_mask + (size_t)mbi * p.mwords), (short)0, p.mwords * 4, 0x00020000);
-    for (int w0 = wave * 64; w0 < p.mwords; w0 += NT)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (__attribute__((address_space(3))) void *)(mw + w0), 4,
-                                               (w0 + lane) * 4, 0, 0, 0);
-    if (bp_lds) {
-#pragma unroll
-      for (int m = 0; m < (SW ? 2 : 1); ++m) {
-        const __amdgpu_buffer_rsrc_t rb =
-            __builtin_amdgcn_make_buffer_rsrc((void *)(m ? p.bp1 : p.bp0), (short)0, p.umax * 8, 0x00020000);
-        for (int d0 = wave * 64; d0 < 2 * p.umax; d0 += NT)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rb, (__attribute__((address_space(3))) void *)((uint32_t *)(lbp + m * LBP) + d0), 4,
-              (d0 + lane) * 4, 0, 0, 0);
-      }
-    }
-  }
+  Expand<BM, WV, SW ? 2 : 1, 4, 2> ex(p, smem, NTILE, wave, lane, m0, mbi, row);
+  ex.prefetch();
   st0.store(smem, tid);
   lds_barrier();
 
@@ -466,16 +631,8 @@ __global__ void __launch_bounds__(64 * WV, 2) aos_gemm_kernel(aos_gemm_params p)
   auto stage = [&](Stager<BM, NT> &st, const int gx) { st.load(p.x, in, p.T, m0, gx < G ? gx : G - 1, tid); };
   if (DB) stage(st1, 1);
 
-  /* one K group: ld receives group g + 2 (g + 1 without DB), sto holds group g + 1 */
-  auto group = [&](const int g, const int d, Stager<BM, NT> &ld, Stager<BM, NT> &sto) {
-    const unsigned char *tb = smem + (g & 1) * TILE;
-    /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
-    u32x4 a[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(i, 4 * c + s));
-    stage(ld, g + (DB ? 2 : 1));
-    /* dequantise this group's row blocks into B fragments */
-    u32x4 f0[4], f1[4];
+  /* dequantise ring slot d into B fragments, then refill it with group gn */
+  auto dequant_slot = [&](const int d, const int gn, u32x4 (&f0)[4], u32x4 (&f1)[4]) {
     {
       const float sc = aos_f16_to_f32(ws0[d] & 0xffffu), bi = aos_f16_to_f32(ws0[d] >> 16);
 #pragma unroll
@@ -486,16 +643,25 @@ __global__ void __launch_bounds__(64 * WV, 2) aos_gemm_kernel(aos_gemm_params p)
 #pragma unroll
       for (int s = 0; s < 4; ++s) f1[s] = dequant_word(wq1[d][s], sc, bi);
     }
-    /* refill the ring slot */
-    {
-      const int gn = g + D < G ? g + D : G - 1;
-      wq0[d] = q0[(size_t)gn * 64];
-      ws0[d] = s0p[(size_t)gn * 32];
-      if (SW) {
-        wq1[d] = q1[(size_t)gn * 64];
-        ws1[d] = s1p[(size_t)gn * 32];
-      }
+    const int gc = gn < G ? gn : G - 1;
+    wq0[d] = q0[(size_t)gc * 64];
+    ws0[d] = s0p[(size_t)gc * 32];
+    if (SW) {
+      wq1[d] = q1[(size_t)gc * 64];
+      ws1[d] = s1p[(size_t)gc * 32];
     }
+  };
+
+  /* one K group: ld receives group g + 2 (g + 1 without DB), sto holds group g + 1 */
+  auto group = [&](const int g, const int d, Stager<BM, NT> &ld, Stager<BM, NT> &sto) {
+    const unsigned char *tb = smem + (g & 1) * TILE;
+    /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
+    u32x4 a[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(i, 4 * c + s));
+    stage(ld, g + (DB ? 2 : 1));
+    u32x4 f0[4], f1[4];
+    dequant_slot(d, g + D, f0, f1);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       u32x4 an[4];
@@ -535,145 +701,32 @@ __global__ void __launch_bounds__(64 * WV, 2) aos_gemm_kernel(aos_gemm_params p)
     }
   }
 
-  /* LoRA expand steps, in chunks of LC steps that stay within one module. A chunk's token
-   * tiles (the steps' SA columns, through a buffer resource over the tile's rows; chunks past
-   * the union read as zeros) go straight from memory to LDS regions 0 .. LC - 1, its B fragments
-   * to registers: word s of lane (i, c) holds union columns k = 64 j + 32 c + 8 s .. +7 of this
-   * wave's row, B_{list[u]}[row][k - u * rpad .. +7] with u = k / rpad (zeros past the union or
-   * for an adapter without the module; rpad is a multiple of 16, so words 0-1 and 2-3 each share
-   * a slot). One wait per chunk; the next chunk's B pointers load meanwhile. */
-  int nls = 0;
-  if (lora) {
-    /* the tile's expand steps, listed by wave 0 (ascending module, then column) */
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();
-    if (wave == 0) {
-      int n = 0;
-#pragma unroll
-      for (int m = 0; m < (SW ? 2 : 1); ++m) {
-        if (m == 1 && lane == 0) ls_n[1] = n < p.lsteps_max ? n : p.lsteps_max; /* gate steps */
-        const int rpad = m ? p.tab1.rpad : p.tab0.rpad;
-        const int nj = rpad ? (Ue * rpad + 63) >> 6 : 0;
-        for (int j0 = 0; j0 < nj; j0 += 64) {
-          const int j = j0 + lane;
-          bool act = false;
-          if (j < nj) {
-            const int ulo = (64 * j) / rpad;
-            int uhi = (64 * j + 63) / rpad;
-            uhi = uhi < Ue - 1 ? uhi : Ue - 1;
-            for (int u = ulo; u <= uhi; ++u) act |= ((mw[u >> 5] >> (u & 31)) & 1u) != 0;
-          }
-          const uint64_t bal = __ballot(act);
-          const int at = n + __popcll(bal & ((1ull << lane) - 1ull));
-          if (act && at < p.lsteps_max) ls[at] = (uint16_t)((m << 15) | j);
-          n += __popcll(bal);
-        }
-      }
-      if (lane == 0) ls_n[0] = n < p.lsteps_max ? n : p.lsteps_max;
-    }
-    lds_barrier();
-    nls = __builtin_amdgcn_readfirstlane(ls_n[0]);
-  }
+  /* LoRA expand: word s of lane (i, c) covers step columns 32 c + 8 s .. +7 */
+  int n0;
+  const int nls = ex.build(n0);
   if (nls > 0) {
-    const int rows = p.T - m0 < BM ? p.T - m0 : BM;
-    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.SA + (size_t)m0 * p.sa_stride), (short)0, rows * p.sa_stride * 2, 0x00020000);
-    const int n0 = SW ? __builtin_amdgcn_readfirstlane(ls_n[1]) : nls; /* gate steps, then up */
-    auto step_of = [&](int l, int &m, int &j, int &rpad) {
-      l = l < nls ? l : nls - 1;
-      const int d = __builtin_amdgcn_readfirstlane((int)ls[l > 0 ? l : 0]);
-      m = d >> 15;
-      j = d & 0x7fff;
-      rpad = m ? p.tab1.rpad : p.tab0.rpad;
-    };
-    auto load_ptrs = [&](int l, const uint16_t *(&pr)[2]) {
-      int m, j, rpad;
-      step_of(l, m, j, rpad);
-      const uint16_t *const *bp = m ? p.bp1 : p.bp0;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int u = (64 * j + 32 * c + 16 * h) / rpad;
-        u = u < Ue ? u : Ue - 1;
-        pr[h] = bp_lds ? lbp[m * LBP + u] : bp[u];
-      }
-    };
-    auto load_frags = [&](int l, const uint16_t *const (&pr)[2], u32x4 (&bv)[4]) {
-      int m, j, rpad;
-      step_of(l, m, j, rpad);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k = 64 * j + 32 * c + 16 * h;
-        const int u = k / rpad;
-        const uint16_t *src = (u < Ue && pr[h]) ? pr[h] + (size_t)row * rpad + (k - u * rpad) : p.zero;
-        bv[2 * h] = *(const u32x4 *)src;
-        bv[2 * h + 1] = *(const u32x4 *)((u < Ue && pr[h]) ? src + 8 : p.zero);
-      }
-    };
-    /* token tile of step l into LDS region q: 16 blocks of 8 rows (1 KB), lane l of a block
-     * writing bytes 16 l, i.e. row 8 b + l / 8, slot l % 8, which holds chunk slot ^ ((r >> 1) & 7) */
-    auto dma_tile = [&](int q, int l) {
-      int m, j, rpad;
-      step_of(l, m, j, rpad);
-      const int off = m ? p.s_off1 : p.s_off0;
-      const int cb = (off + 64 * j) * 2, lim = (off + Ue * rpad) * 2, rb = p.sa_stride * 2;
-#pragma unroll
-      for (int k = 0; k < 16 / WV; ++k) {
-        const int bk = k * WV + wave;
-        const int r = bk * 8 + (lane >> 3);
-        const int ch = (lane & 7) ^ ((r >> 1) & 7);
-        const int rr = r < rows ? r : rows - 1;
-        const int col = cb + ch * 16;
-        const int vo = col < lim ? rr * rb + col : (int)0x80000000;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, 0);
-      }
-    };
-    auto mma = [&](const unsigned char *tb, const u32x4 (&bv)[4], f32x16 (&acc)[MT]) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        u32x4 a[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc[mt] = aos_mfma32(a[s], bv[s], acc[mt]);
-      }
-    };
-    /* B pointers of the chunk starting at step l (steps past its module's end repeat its last) */
-    const uint16_t *pr[LC][2];
-    auto chunk_ptrs = [&](int l) {
-      const int e = l < n0 ? n0 : nls;
-#pragma unroll
-      for (int q = 0; q < LC; ++q) load_ptrs(l + q < e ? l + q : e - 1, pr[q]);
-    };
-    chunk_ptrs(0);
-    int l0 = 0;
-    while (l0 < nls) {
-      const int end = l0 < n0 ? n0 : nls;
-      const int n = end - l0 < LC ? end - l0 : LC;
-      u32x4 bv[LC][4];
+    const int koff[4] = {32 * c, 32 * c + 8, 32 * c + 16, 32 * c + 24};
+    auto mma_into = [&](int n, const u32x4 (&bv)[LC][4], f32x16 (&acc)[MT]) {
 #pragma unroll
       for (int q = 0; q < LC; ++q) {
-        if (q < n) {
-          dma_tile(q, l0 + q);
-          load_frags(l0 + q, pr[q], bv[q]);
+        if (q >= n) continue;
+        const unsigned char *tb = smem + q * TILE;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          u32x4 a[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc[mt] = aos_mfma32(a[s], bv[q][s], acc[mt]);
         }
       }
-      if (l0 + n < nls) chunk_ptrs(l0 + n);
-      /* the LDS writes of the buffer loads are complete once vmcnt drains */
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      lds_barrier();
-      if (!SW || l0 < n0) {
-#pragma unroll
-        for (int q = 0; q < LC; ++q)
-          if (q < n) mma(smem + q * TILE, bv[q], acc0);
-      } else {
-#pragma unroll
-        for (int q = 0; q < LC; ++q)
-          if (q < n) mma(smem + q * TILE, bv[q], acc1);
-      }
-      lds_barrier();
-      l0 += n;
-    }
+    };
+    ex.template run<LC>(nls, n0, koff, [&](int m, int n, const u32x4 (&bv)[LC][4]) {
+      if (!SW || m == 0)
+        mma_into(n, bv, acc0);
+      else
+        mma_into(n, bv, acc1);
+    });
   }
 
   /* epilogue */
@@ -717,34 +770,31 @@ extern "C" int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_
   return (int)hipGetLastError();
 }
 
-/* Measured on the 7B-shaped layer at 2048 tokens: the SwiGLU kernel is fastest with a shallow
- * ring, single staging and 4-wave workgroups (two per CU); the single-matrix kernel with the
- * deep pipeline and 8-wave workgroups (256 weight rows against one token tile). */
-static constexpr int gemm_waves(bool sw) { return sw ? 4 : 8; }
-
-template <bool SW>
-static void launch_gemm_d(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
-  constexpr int MT = AOS_GEMM_BM / 32, WV = gemm_waves(SW);
-  constexpr int D4 = SW ? 2 : 4;
-  constexpr bool DBT = !SW, APF = !SW;
-  constexpr int LC = gemm_lchunk(SW), NTILE = LC > 2 ? LC : 2;
-  const size_t lds = (size_t)NTILE * AOS_GEMM_BM * 128 + GEMM_AUX + ((size_t)p->lsteps_max * 2 + 15) / 16 * 16;
-  const dim3 grid(p->mb * p->nb), block(64 * WV);
-  const int G = p->w0.G;
-  if (G % D4 == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, D4, DBT, APF, WV>), grid, block, lds, *p);
+/* Kernel shapes (measured on the 7B-shaped layer at 2048 tokens): 128-token tiles at two waves
+ * per SIMD, so that one wave's dequantisation overlaps the other's matrix-core work; SwiGLU with
+ * a shallow ring and single staging in 4-wave workgroups (two per CU), the single-matrix kernel
+ * with the deep pipeline in 8-wave workgroups. */
+template <bool SW, int MT, int D, bool DBT, bool APF, int WV, int OCC, int LC>
+static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
+  constexpr int BM = 32 * MT, NTILE = LC > 2 ? LC : 2;
+  aos_gemm_params q = *p;
+  q.mb = (q.T + BM - 1) / BM;
+  q.nb = (q.w0.RB + WV - 1) / WV;
+  const size_t lds = (size_t)NTILE * BM * 128 + gemm_aux(BM) + ((size_t)q.lsteps_max * 2 + 15) / 16 * 16;
+  const dim3 grid(q.mb * q.nb), block(64 * WV);
+  const int G = q.w0.G;
+  if (G % D == 0)
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, D, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
   else if (G % 2 == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 2, DBT, APF, WV>), grid, block, lds, *p);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 2, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
   else
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 1, DBT, APF, WV>), grid, block, lds, *p);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 1, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
 }
-
-extern "C" int aos_gemm_waves(int swiglu) { return gemm_waves(swiglu != 0); }
 
 extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx) {
   if (swiglu)
-    launch_gemm_d<true>(p, ctx);
+    launch_gemm_cfg<true, 4, 2, false, false, 4, 2, 2>(p, ctx);
   else
-    launch_gemm_d<false>(p, ctx);
+    launch_gemm_cfg<false, 4, 4, true, true, 8, 2, 4>(p, ctx);
   return (int)hipGetLastError();
 }

@@ -188,7 +188,7 @@ typedef struct {
   aos_q4_dev w0, w1;
   const uint16_t *x;  /* [T][in] */
   int T;
-  int mb, nb;         /* M tiles, N blocks */
+  int mb, nb;         /* token tiles, weight blocks (set by the launcher for its kernel shape) */
   aos_lora_tab tab0, tab1;
   const uint16_t *SA; /* [T][sa_stride] bf16 */
   int sa_stride, s_off0, s_off1;
@@ -202,12 +202,14 @@ typedef struct {
   uint16_t *y;        /* [T][out] */
 } aos_gemm_params;
 
-/* Bound on the expand K steps of one M tile for a module: all the 64-column steps of its union
- * columns, and at most 8 slots per token, each spanning at most rpad / 64 + 2 steps. */
+/* Bound on the expand K steps of one GEMM token tile (at most AOS_GEMM_TILE_MAX tokens) for a
+ * module: all the 64-column steps of its union columns, and at most 8 slots per token, each
+ * spanning at most rpad / 64 + 2 steps. */
+#define AOS_GEMM_TILE_MAX 256
 static inline int aos_lstep_bound(int umax, int rpad) {
   if (rpad == 0) return 0;
   const int all = (umax * rpad + 63) / 64;
-  const int used = AOS_GEMM_BM * 8 * (rpad / 64 + 2);
+  const int used = AOS_GEMM_TILE_MAX * 8 * (rpad / 64 + 2);
   return all < used ? all : used;
 }
 
@@ -249,7 +251,6 @@ int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
-int aos_gemm_waves(int swiglu); /* waves per GEMM workgroup (32 weight rows each) */
 #ifdef __cplusplus
 }
 #endif
