@@ -236,3 +236,40 @@ def test_attention_projections_parity(hip):
         ref = oracle_proj(cid, name, xf, rings)
         ratio = tol_ratio(got.reshape(ref.shape), ref)
         assert ratio <= REL_TOL, f"{name}: {ratio:.4g}"
+
+
+@pytest.mark.parametrize("T", [1, 40, 200])
+def test_mlp_rank_not_multiple_of_16_and_missing_modules(hip, T):
+    """Rank-40 adapters (rows padded to 48, so a 64-column expand step spans two slots) where
+    some adapters have no up_proj or no down_proj (those slots add nothing for that module), on
+    the decode and prefill paths against the oracle."""
+    import dataclasses
+
+    import oracle
+
+    cfg = dataclasses.replace(W.CONFIGS[1], rank=40, n_adapters=6)
+    missing = {1: "up_proj", 4: "up_proj", 2: "down_proj"}
+    lora = []
+    for a in range(cfg.n_adapters):
+        lora.append({m: W.lora_weights(cfg, a, m) for m in cfg.modules if missing.get(a) != m})
+    base = {m: W.base_weights(cfg, m) for m in cfg.modules}
+    layer = hip.Layer(0)
+    for m, (p, s, b) in base.items():
+        layer.set_base(m, p, s, b)
+    ads = []
+    for a, mods in enumerate(lora):
+        ad = hip.LoraAdapter(a, 1, W.lora_scale(cfg))
+        for m, (A, B) in mods.items():
+            ad.set_module(0, m, A, B)
+        ads.append(ad)
+    layer.set_adapters(ads)
+    f, w = W.router_inputs(cfg, T)
+    rings = oracle.route_batch(oracle.priors(f, w), cfg.k, cfg.tau, cfg.eps, 1.0,
+                               np.arange(cfg.n_adapters, dtype=np.uint64))
+    xb, xf = W.activations(cfg, T)
+    y = _run_mlp(hip, layer, xb, rings)
+    scales = np.full(cfg.n_adapters, W.lora_scale(cfg), np.float32)
+    ref = oracle.mlp_forward(xf, base["gate_proj"], base["up_proj"], base["down_proj"], lora, scales, cfg.rank,
+                             rings)
+    ratio = tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
+    assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
