@@ -1,247 +1,20 @@
 /*
- * aoship_lora.hip — the decode path's LoRA shrink and adapter plan.
- *
- * The MLX forward computes each adapter's delta as ((x @ A^T) @ B^T) * (scale * blend)
- * (mlx_cpp_wrapper_real.cpp:3394-3419; blend = q / 32767 from prepare_lora_for_ring,
- * crates/adapteros-lora-mlx-ffi/src/backend.rs:398-428). The first product ("shrink",
- * S = x . A^T) is computed here once per call, unscaled, in float32; the base-layer kernels add
- * the second product ("expand") as extra matrix-core steps with each token's coefficient
- * applied to S on the fly.
- *
- * The shrink is a skinny GEMM (T <= 32 tokens, a few hundred rank rows, K = in_features) bound by
- * reading the bf16 A rows, so it is built like the int4 GEMV: 32-row blocks, K split over the
- * waves of a workgroup and over ks workgroups, a register ring keeping D groups of A in flight
- * per wave, x staged once per workgroup in LDS, v_mfma_f32_32x32x16_bf16 with the tokens as M,
- * and a fixed-order reduction (waves in LDS, workgroups by the last one to finish).
+ * aoship_lora.hip — the decode path's LoRA shrink launch (the shrink and the adapter plan
+ * themselves are in aoship_shrink.h).
  *
  * The plan (union of the tokens' adapters and their coefficients) is built by one extra
  * workgroup of the first shrink launch, which needs no plan itself because it covers every
  * bound adapter.
  */
-#include "aoship_device.h"
-#include "aoship_internal.h"
+#include "aoship_shrink.h"
 #include <hip/hip_ext.h>
 
 namespace {
 
-constexpr int XE = 4;
-
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-/* Plan of one call: ring slot s of token t contributes adapter a = adapter_indices[s] when
- * s < top_k, its gate q > 0 and the adapter is bound (backend.rs:409-425 skips q <= 0 and
- * unknown handles). coef[t][u] = sum over such slots of scale[a] * (float(q) / 32767.0f), the
- * product mod.scale * blend_weights[i] of the MLX forward. */
-__device__ void build_plan(const aos_plan_params &pp) {
-  __shared__ uint32_t bits[AOS_MAX_ADAPTERS / 32];
-  __shared__ uint16_t list[AOS_PLAN_MAXU];
-  __shared__ int cntU;
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const int words = (pp.n + 31) >> 5;
-  for (int w = tid; w < words; w += nt) bits[w] = 0u;
-  __syncthreads();
-  for (int e = tid; e < pp.T * 8; e += nt) {
-    const aoship_ring_t &r = pp.rings[e >> 3];
-    const int s = e & 7;
-    const int a = r.adapter_indices[s];
-    if (s < (int)r.top_k && r.gates_q15[s] > 0 && a < pp.n && pp.bound[a])
-      atomicOr(&bits[a >> 5], 1u << (a & 31));
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int u = 0;
-    for (int w = 0; w < words; ++w) {
-      uint32_t m = bits[w];
-      while (m) {
-        const int b = __builtin_ctz(m);
-        m &= m - 1u;
-        list[u] = (uint16_t)((w << 5) + b);
-        pp.plan->list[u] = list[u];
-        ++u;
-      }
-    }
-    cntU = u;
-    pp.plan->U = u;
-  }
-  __syncthreads();
-  const int U = cntU;
-  for (int idx = tid; idx < pp.T * U; idx += nt) {
-    const int t = idx / U, u = idx - t * U;
-    const int a = list[u];
-    const aoship_ring_t &r = pp.rings[t];
-    float c = 0.0f;
-    for (int s = 0; s < 8; ++s) {
-      if (s < (int)r.top_k && r.adapter_indices[s] == a && r.gates_q15[s] > 0) {
-        const float blend = (float)r.gates_q15[s] / 32767.0f;
-        c += pp.scale[a] * blend;
-      }
-    }
-    pp.plan->coef[t][u] = c;
-  }
-}
-
 template <int NV, int W, int D>
 __global__ void __launch_bounds__(64 * W) aos_shrink_kernel(aos_shrink_params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int lrb = blockIdx.x;
-  const int ksi = blockIdx.y;
-  const int rb_total = p.n_rb[0] + (p.nmod > 1 ? p.n_rb[1] : 0) + (p.nmod > 2 ? p.n_rb[2] : 0);
-  if (lrb == rb_total) {
-    if (ksi == 0 && p.plan_build.plan) build_plan(p.plan_build);
-    return;
-  }
-  const int rb_global = lrb;
-  int m = 0;
-  while (m < p.nmod - 1 && lrb >= p.n_rb[m]) {
-    lrb -= p.n_rb[m];
-    ++m;
-  }
-  const aos_lora_tab &tab = p.tab[m];
-  const int rpad = tab.rpad;
-  if (rpad == 0) return;
-  const int nslots = p.all_mode ? tab.n : p.plan->U;
-  if (lrb * 32 >= nslots * rpad) return; /* uniform for every K split of this row block */
-
-  const int T = p.T, in = p.in, G = in >> 6;
-  const int i = lane & 31, c = lane >> 5;
-  const int col = lrb * 32 + i;
-  const int u = col / rpad, j = col - u * rpad;
-  const uint16_t *arow = p.zero_row;
-  bool valid = false;
-  if (u < nslots) {
-    const int a = p.all_mode ? u : p.plan->list[u];
-    const uint16_t *A = tab.A[a];
-    if (A) {
-      arow = A + (size_t)j * in;
-      valid = true;
-    }
-  }
-
-  const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
-  const int GR = gw1 - gw0;
-  const int ga = gw0 + wave * GR / W, gb = gw0 + (wave + 1) * GR / W, ng = gb - ga;
-
-  /* x staging (first loads ahead of the ring), then the ring of A rows. Lanes without a valid
-   * row read the zero buffer at a fixed offset. */
-  const int xchunks = GR * 8, nx = T * xchunks;
-  u32x4 xv[XE];
-#pragma unroll
-  for (int jx = 0; jx < XE; ++jx) {
-    int idx = tid + jx * 64 * W;
-    idx = idx < nx ? idx : nx - 1;
-    const int t = idx / xchunks, r = idx - t * xchunks;
-    xv[jx] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
-  }
-  /* lane half c takes elements 32c + 8st .. +7 of each group, as the staged x fragments do */
-  const uint16_t *ap = valid ? arow + (size_t)ga * 64 + 32 * c : p.zero_row;
-  const int astep = valid ? 64 : 0;
-  const int sstep = valid ? 8 : 0;
-  u32x4 ring[D][4];
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    const int jj = d < ng ? d : ng - 1;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) ring[d][st] = *(const u32x4 *)(ap + (size_t)jj * astep + sstep * st);
-  }
-  uint16_t *xl = (uint16_t *)(smem + 128);
-  const int xstride = GR * 64;
-  if (tid < 32) ((uint32_t *)smem)[tid] = 0u;
-#pragma unroll
-  for (int jx = 0; jx < XE; ++jx) {
-    const int idx = tid + jx * 64 * W;
-    if (idx < nx) {
-      const int t = idx / xchunks, r = idx - t * xchunks;
-      *(u32x4 *)(xl + (size_t)t * xstride + r * 8) = xv[jx];
-    }
-  }
-  for (int idx = tid + XE * 64 * W; idx < nx; idx += 64 * W) {
-    const int t = idx / xchunks, r = idx - t * xchunks;
-    *(u32x4 *)(xl + (size_t)t * xstride + r * 8) =
-        *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
-  }
-  lds_barrier();
-
-  const int xbase = i < T ? 128 + i * xstride * 2 + 64 * c : 0;
-  const int xmult = i < T ? 128 : 0;
-  f32x16 acc = {};
-  for (int base = 0; base < ng; base += D) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int jg = base + d;
-      if (jg < ng) {
-        const int gl = ga + jg - gw0;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const u32x4 a = *(const u32x4 *)(smem + xbase + (size_t)gl * xmult + 16 * st);
-          acc = aos_mfma32(a, ring[d][st], acc);
-        }
-      }
-      int jn = jg + D;
-      jn = jn < ng ? jn : ng - 1;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) ring[d][st] = *(const u32x4 *)(ap + (size_t)jn * astep + sstep * st);
-    }
-  }
-
-  /* fixed-order reduction: waves through LDS, then the K splits */
-  float *red = (float *)smem;
-  lds_barrier();
-#pragma unroll
-  for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc[v];
-  lds_barrier();
-  if (wave != 0) return;
-  float tot[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float s = red[v * 64 + lane];
-    for (int w = 1; w < W; ++w) s += red[(w * NV + v) * 64 + lane];
-    tot[v] = s;
-  }
-  if (p.ks > 1) {
-    float *part = p.part + ((size_t)rb_global * p.ks + ksi) * (NV * 64);
-#pragma unroll
-    for (int v = 0; v < NV; ++v) aos_publish(part + v * 64 + lane, tot[v]);
-    uint32_t old = 0;
-    if (lane == 0) old = aos_arrive(&p.counters[rb_global]);
-    old = aos_shfl(old, 0);
-    if (old != (uint32_t)p.ks - 1u) return;
-    if (lane == 0) aos_reset(&p.counters[rb_global]);
-#pragma unroll
-    for (int v = 0; v < NV; ++v) tot[v] = 0.0f;
-    /* partials are read 8 at a time (all loads in flight together) and summed in order */
-    for (int k0 = 0; k0 < p.ks; k0 += 8) {
-      float vals[8][NV];
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int k = k0 + kk < p.ks ? k0 + kk : p.ks - 1;
-        const float *pp = p.part + ((size_t)rb_global * p.ks + k) * (NV * 64);
-#pragma unroll
-        for (int v = 0; v < NV; ++v) vals[kk][v] = aos_collect(pp + v * 64 + lane);
-      }
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        if (k0 + kk < p.ks) {
-#pragma unroll
-          for (int v = 0; v < NV; ++v) tot[v] += vals[kk][v];
-        }
-    }
-  }
-  /* S[t][col] (float32, unscaled); absent adapters give zero columns */
-  if (u < nslots) {
-    float *S = p.S[m];
-    const int stride = p.s_stride[m];
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int mt = aos_acc_m(v, lane);
-      if (mt < T) S[(size_t)mt * stride + col] = valid ? tot[v] : 0.0f;
-    }
-  }
+  aos_shrink::shrink_block<NV, W, D>(p, blockIdx.x, blockIdx.y, smem);
 }
 
 template <int NV>
