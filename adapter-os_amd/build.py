@@ -1,4 +1,5 @@
-"""Build the gfx950 library (libaoship.so) and the synthetic-input helper (libaos_synth.so).
+"""Build the gfx950 library (libaoship.so), the synthetic-input helper (libaos_synth.so) and the
+matrix-core peak probe the bench reports beside the datasheet peak (libaos_peak.so).
 
 Every HIP translation unit is compiled for gfx950 only, with IEEE float semantics: no fast-math,
 no floating-point contraction, float32 denormals kept, and packed-FP32 instruction selection
@@ -21,6 +22,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libaoship.so"
 SYNTH = PKG / "libaos_synth.so"
+PEAK = PKG / "libaos_peak.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -81,6 +83,10 @@ def build(jobs: int = 4) -> None:
     _run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
           "-o", str(tmp), str(PKG / "synth" / "aos_synth.c"), "-lm"])
     os.replace(tmp, SYNTH)
+    tmp = PEAK.with_suffix(".so.tmp")
+    _run([HIPCC, "-x", "hip", *HIP_FLAGS, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          str(PKG / "probe" / "aos_mfma_peak.hip")])
+    os.replace(tmp, PEAK)
 
 
 if __name__ == "__main__":
@@ -88,4 +94,4 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=4)
     a = ap.parse_args()
     build(a.jobs)
-    print(f"built {LIB} and {SYNTH}")
+    print(f"built {LIB}, {SYNTH} and {PEAK}")

@@ -9,6 +9,7 @@ dominant kernel (live per-kernel times from dispatch-recorded HIP events) and th
 (the C oracle on this host's cores, a bounded sample).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-prefill]
+       python bench.py --probe | --probe-prefill   (workloads for the hardware-counter runs)
 """
 from __future__ import annotations
 
@@ -167,6 +168,31 @@ def probe(aoship, W, torch, layers: int) -> int:
     return 0
 
 
+def probe_prefill(aoship, W, torch) -> int:
+    """Workload for the prefill counter runs: 6 steps of the 2048-token prefill."""
+    pf = MlpCase(aoship, W, 3, 2048, torch, 1)
+    for _ in range(6):
+        pf.step()
+    torch.cuda.synchronize()
+    log("prefill probe done")
+    return 0
+
+
+def measured_mfma_peak() -> float | None:
+    """Achievable dense bf16 MFMA TFLOP/s on this GPU (chains of v_mfma_f32_32x32x16_bf16 on every
+    SIMD, no memory traffic), from the probe library the build compiles; None when absent."""
+    import ctypes
+
+    path = ROOT / "adapter-os_amd" / "libaos_peak.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.aos_mfma_peak_tflops.restype = ctypes.c_double
+    lib.aos_mfma_peak_tflops.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    tf = lib.aos_mfma_peak_tflops(2048, 4096, 5)
+    return tf if tf > 0 else None
+
+
 def measured_traffic():
     """HBM bytes per launch of the gate/up GEMV from the committed counter summary, or None."""
     if not TRAFFIC_FILE.exists():
@@ -230,6 +256,8 @@ def main() -> int:
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--probe", action="store_true",
                     help="run the hardware-counter workload only (see probe())")
+    ap.add_argument("--probe-prefill", action="store_true",
+                    help="run the prefill hardware-counter workload only (see probe_prefill())")
     ap.add_argument("--layers", type=int, default=4,
                     help="distinct layer copies cycled by the decode steps (defeats the last-level cache)")
     args = ap.parse_args()
@@ -247,6 +275,8 @@ def main() -> int:
     log(f"device: {aoship.device_name()}")
     if args.probe:
         return probe(aoship, W, torch, args.layers)
+    if args.probe_prefill:
+        return probe_prefill(aoship, W, torch)
 
     # ---- headline: 7B-shaped decode, one token ----
     T = 1
@@ -317,6 +347,7 @@ def main() -> int:
         msp = time_steps(pf, max(5, args.steps // 10), 3, torch)
         kp = kernel_times(pf, max(5, args.steps // 20), torch)
         flops = W.algorithmic_flops(pf.cfg, 2048)
+        peak_meas = measured_mfma_peak()
         tflops = flops / (msp * 1e-3) / 1e12
         H, I = pf.cfg.hidden, pf.cfg.inter
         gu_flops = 2 * 2048 * H * 2 * I
@@ -328,6 +359,8 @@ def main() -> int:
             "achieved_tflops": tflops,
             "mfma_util": tflops / BF16_PEAK_TFLOPS,
             "peak_tflops": BF16_PEAK_TFLOPS,
+            "peak_measured_tflops": peak_meas,
+            "mfma_util_of_measured_peak": tflops / peak_meas if peak_meas else None,
             "kernels_us": {k: v * 1e3 for k, v in kp.items()},
             "gemm_gate_up_tflops": gu_flops / (kp["q4_gemm_gate_up"] * 1e-3) / 1e12 if "q4_gemm_gate_up" in kp else None,
         }
