@@ -9,8 +9,12 @@
 //                             769-785 (construction), 1567-1952 (deterministic routing)
 //   FusedKernels (hot-swap, device_name, attest_determinism, layer forwards)
 //                             crates/adapteros-lora-kernel-api/src/lib.rs:308-716
+//   adapter ingest            crates/adapteros-lora-mlx-ffi/src/backend.rs:891-893, 1017-1210
+//                             (safetensors bytes + metadata), 448-522 (every layer, failed modules
+//                             skipped); base weights as mlx_cpp_wrapper_real.cpp:683, 925-956 read them
 // Errors are thrown as AosError with the reference's error kinds (AosError::Kernel, ::Validation,
-// ::Routing, ::DeterminismViolation); a Rust Result<T> maps to a return value or a throw.
+// ::Routing, ::DeterminismViolation, ::Parse, ::Io); a Rust Result<T> maps to a return value or a
+// throw.
 //
 // Header-only; link against libaoship.so and the HIP runtime (device buffers for the host-side
 // routing convenience call).
@@ -28,10 +32,11 @@
 #include <vector>
 
 #include "../../include/aoship.h"
+#include "aos_ingest.hpp"
 
 namespace adapteros {
 
-enum class ErrorKind { Kernel, Validation, Routing, DeterminismViolation };
+enum class ErrorKind { Kernel, Validation, Routing, DeterminismViolation, Parse, Io };
 
 class AosError : public std::runtime_error {
  public:
@@ -348,9 +353,99 @@ class HipKernels {
           throw AosError(ErrorKind::Kernel, "aoship_lora_adapter_set_module: " + err);
         }
       }
-    adapters_[id] = a;
-    attached_[id] = true;
-    rebind();
+    install(id, a);
+  }
+
+  // MLXFFIBackend::load_adapter (backend.rs:891-893): safetensors bytes, no metadata.
+  void load_adapter(uint16_t id, const uint8_t *bytes, size_t len) {
+    load_adapter_with_metadata(id, bytes, len, nullptr);
+  }
+
+  // MLXFFIBackend::load_adapter_with_metadata (backend.rs:1017-1110): safetensors bytes and the
+  // metadata object as JSON text (null or empty: none). scale = alpha / rank of the resolved
+  // config; each module keeps the rank of its A tensor and is set on every layer. A module the
+  // device path rejects (a name outside q/k/v/o/gate/up/down_proj, rank > 128, in % 64 or
+  // out % 32 not 0, B columns != A rows) is skipped with a warning, as add_adapter_internal skips a failed set_module
+  // (backend.rs:496-522); load_warnings() lists them. Returns the resolved config.
+  ingest::AdapterSpec load_adapter_with_metadata(uint16_t id, const uint8_t *bytes, size_t len,
+                                                 const char *metadata_json) {
+    ingest::AdapterSpec spec;
+    try {
+      const ingest::SafeTensors st = ingest::SafeTensors::parse(bytes, len);
+      ingest::Json md;
+      const bool has_md = metadata_json && *metadata_json;
+      if (has_md) md = ingest::parse_json(metadata_json);
+      spec = ingest::read_adapter(st, has_md ? &md : nullptr);
+    } catch (const ingest::IngestError &e) {
+      throw AosError(kind_of(e), std::string("Failed to parse adapter weights: ") + e.what());
+    }
+    register_adapter(id, spec);
+    return spec;
+  }
+
+  // MLXFFIBackend::register_adapter (backend.rs:549-551, 448-522) for an adapter read by
+  // ingest::read_adapter or ingest::load_lora (LoRAAdapter::load, lora.rs:154-216): replaces id,
+  // attaches it, sets each module on every layer, skipping (with a warning) what the device path
+  // rejects.
+  void register_adapter(uint16_t id, const ingest::AdapterSpec &spec) {
+    if (spec.rank == 0) throw AosError(ErrorKind::Validation, "adapter rank must be positive");
+    warnings_.clear();
+    if (adapters_.count(id)) unload_adapter(id);
+    aoship_lora_adapter_t *a = aoship_lora_adapter_new(id, (int)layers_.size(), spec.scale());
+    if (!a) throw AosError(ErrorKind::Kernel, "aoship_lora_adapter_new: " + detail::last_error());
+    for (const auto &m : spec.modules) {
+      if (!m.problem.empty()) {
+        warnings_.push_back("module " + m.name + " skipped: " + m.problem);
+        continue;
+      }
+      for (size_t li = 0; li < layers_.size(); ++li)
+        if (aoship_lora_adapter_set_module(a, (int)li, m.name.c_str(), m.rank, m.in_features, m.out_features,
+                                           m.A.data(), m.B.data()) != 0) {
+          warnings_.push_back("module " + m.name + " skipped: " + detail::last_error());
+          break;  // the same weights go to every layer, so every layer would fail alike
+        }
+    }
+    install(id, a);
+  }
+
+  // Messages for the modules the last safetensors load skipped.
+  const std::vector<std::string> &load_warnings() const { return warnings_; }
+
+  // Base projections from an MLX-community 4-bit safetensors file, or one shard of it: per layer
+  // i < num_layers, "model.layers.<i>.self_attn.{q,k,v,o}_proj" and
+  // "model.layers.<i>.mlp.{gate,up,down}_proj" (.weight / .scales / .biases, read as
+  // get_weight_with_dequant reads them). Keys the file does not hold are left unset, so shards
+  // load one after another. Returns the number of projections set.
+  int load_base_safetensors(const uint8_t *bytes, size_t len) {
+    static const char *const kAttn[] = {"q_proj", "k_proj", "v_proj", "o_proj"};
+    static const char *const kMlp[] = {"gate_proj", "up_proj", "down_proj"};
+    int n = 0;
+    try {
+      const ingest::SafeTensors st = ingest::SafeTensors::parse(bytes, len);
+      for (size_t li = 0; li < layers_.size(); ++li) {
+        const std::string prefix = "model.layers." + std::to_string(li);
+        auto one = [&](const std::string &group, const char *module) {
+          ingest::BaseProjection bp;
+          if (!ingest::read_base(st, prefix + group + module, bp)) return;
+          set_base((int)li, module, bp.out_features, bp.in_features, bp.packed.data(), bp.scales_f16.data(),
+                   bp.biases_f16.data());
+          ++n;
+        };
+        for (const char *m : kAttn) one(".self_attn.", m);
+        for (const char *m : kMlp) one(".mlp.", m);
+      }
+    } catch (const ingest::IngestError &e) {
+      throw AosError(kind_of(e), e.what());
+    }
+    return n;
+  }
+  int load_base_safetensors(const std::string &path) {
+    try {
+      const ingest::MappedFile f(path);
+      return load_base_safetensors(f.data(), f.size());
+    } catch (const ingest::IngestError &e) {
+      throw AosError(kind_of(e), e.what());
+    }
   }
 
   // attach / detach / unload (lib.rs:410-432). A detached adapter stays loaded; its ring index
@@ -402,6 +497,18 @@ class HipKernels {
     if (i < 0 || i >= (int)layers_.size()) throw AosError(ErrorKind::Validation, "layer index out of range");
     return layers_[(size_t)i];
   }
+  static ErrorKind kind_of(const ingest::IngestError &e) {
+    switch (e.kind()) {
+      case ingest::IngestError::Kind::Parse: return ErrorKind::Parse;
+      case ingest::IngestError::Kind::Io: return ErrorKind::Io;
+      default: return ErrorKind::Validation;
+    }
+  }
+  void install(uint16_t id, aoship_lora_adapter_t *a) {
+    adapters_[id] = a;
+    attached_[id] = true;
+    rebind();
+  }
   // Table: position = adapter id; detached or unloaded ids are null (skipped like a missing
   // handle in prepare_lora_for_ring, backend.rs:398-428).
   void rebind() {
@@ -421,6 +528,7 @@ class HipKernels {
   std::map<uint16_t, bool> attached_;
   size_t table_len_ = 0;
   std::string device_name_;
+  std::vector<std::string> warnings_;
 };
 
 }  // namespace adapteros

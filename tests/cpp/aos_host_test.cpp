@@ -1,8 +1,15 @@
 // C++ host-side tests of adapter-os_amd/host/aos_kernel_api.hpp, written like the reference's own
 // Rust tests they restate (each names its source). Mode "cpu" runs the tests that touch no GPU;
 // mode "gpu" runs the device ones. Prints "ok <name>" per test; exits 1 on the first failure.
+// The ingest modes read safetensors files that tests/test_host_cpp.py writes with the safetensors
+// Python package: "ingest-adapter FILE [METADATA_JSON]", "ingest-lora FILE RANK ALPHA TARGETS" and
+// "ingest-base FILE KEY" print what the parser read as one JSON line (no GPU); "gpu-ingest DIR ..." loads the same weights from the
+// files and from raw arrays and checks that the layer forwards agree bit for bit.
 #include <cmath>
+#include <cinttypes>
 #include <cstdio>
+#include <fstream>
+#include <sstream>
 #include <cstdlib>
 #include <functional>
 #include <string>
@@ -240,16 +247,258 @@ void gpu_tests() {
   });
 }
 
+// ---- ingest: what the parser reads, as JSON for the Python side to check ----
+
+std::string jstr(const std::string &s) {
+  std::string o = "\"";
+  for (char c : s) {
+    if (c == '"' || c == '\\') o += '\\';
+    if ((unsigned char)c < 0x20) {
+      char b[8];
+      std::snprintf(b, sizeof b, "\\u%04x", (unsigned)(unsigned char)c);
+      o += b;
+      continue;
+    }
+    o += c;
+  }
+  return o + "\"";
+}
+
+template <class T>
+std::string jlist(const std::vector<T> &v) {
+  std::string o = "[";
+  for (size_t i = 0; i < v.size(); ++i) o += (i ? "," : "") + std::to_string(v[i]);
+  return o + "]";
+}
+
+std::vector<uint32_t> f32_bits(const std::vector<float> &v) {
+  std::vector<uint32_t> b(v.size());
+  std::memcpy(b.data(), v.data(), v.size() * 4);
+  return b;
+}
+
+std::string read_text(const std::string &path) {
+  std::ifstream f(path, std::ios::binary);
+  std::stringstream ss;
+  ss << f.rdbuf();
+  return ss.str();
+}
+
+int ingest_error(const ingest::IngestError &e) {
+  std::printf("{\"error\":%s,\"message\":%s}\n",
+              jstr(e.kind() == ingest::IngestError::Kind::Parse ? "Parse"
+                   : e.kind() == ingest::IngestError::Kind::Io  ? "Io"
+                                                                : "Validation")
+                  .c_str(),
+              jstr(e.what()).c_str());
+  return 0;
+}
+
+void print_spec(const ingest::AdapterSpec &spec) {
+    float alpha = spec.alpha, scale = spec.scale();
+    uint32_t ab, sb;
+    std::memcpy(&ab, &alpha, 4);
+    std::memcpy(&sb, &scale, 4);
+    std::string targets = "[";
+    for (size_t i = 0; i < spec.target_modules.size(); ++i) targets += (i ? "," : "") + jstr(spec.target_modules[i]);
+    targets += "]";
+    std::string mods = "[";
+    for (size_t i = 0; i < spec.modules.size(); ++i) {
+      const auto &m = spec.modules[i];
+      mods += (i ? "," : "") + std::string("{\"name\":") + jstr(m.name) + ",\"rank\":" + std::to_string(m.rank) +
+              ",\"in\":" + std::to_string(m.in_features) + ",\"out\":" + std::to_string(m.out_features) +
+              ",\"A\":" + jlist(f32_bits(m.A)) + ",\"B\":" + jlist(f32_bits(m.B)) + ",\"problem\":" + jstr(m.problem) +
+              "}";
+    }
+    mods += "]";
+    std::printf("{\"rank\":%" PRIu64 ",\"alpha_bits\":%u,\"scale_bits\":%u,\"target_modules\":%s,\"modules\":%s}\n",
+                spec.rank, ab, sb, targets.c_str(), mods.c_str());
+}
+
+int ingest_adapter_mode(const std::string &file, const char *metadata_json) {
+  try {
+    const ingest::MappedFile f(file);
+    const ingest::SafeTensors st = ingest::SafeTensors::parse(f.data(), f.size());
+    ingest::Json md;
+    if (metadata_json) md = ingest::parse_json(metadata_json);
+    print_spec(ingest::read_adapter(st, metadata_json ? &md : nullptr));
+  } catch (const ingest::IngestError &e) {
+    return ingest_error(e);
+  }
+  return 0;
+}
+
+// LoRAAdapter::load with config (rank, alpha, comma-separated targets)
+int ingest_lora_mode(const std::string &file, const char *rank, const char *alpha, const std::string &targets) {
+  try {
+    ingest::AdapterSpec cfg;
+    cfg.rank = std::strtoull(rank, nullptr, 10);
+    cfg.alpha = std::strtof(alpha, nullptr);
+    cfg.target_modules.clear();
+    size_t b = 0;
+    while (b < targets.size()) {
+      size_t e = targets.find(',', b);
+      if (e == std::string::npos) e = targets.size();
+      if (e > b) cfg.target_modules.push_back(targets.substr(b, e - b));
+      b = e + 1;
+    }
+    print_spec(ingest::load_lora(file, cfg));
+  } catch (const ingest::IngestError &e) {
+    return ingest_error(e);
+  }
+  return 0;
+}
+
+int ingest_base_mode(const std::string &file, const std::string &key) {
+  try {
+    const ingest::MappedFile f(file);
+    const ingest::SafeTensors st = ingest::SafeTensors::parse(f.data(), f.size());
+    ingest::BaseProjection bp;
+    if (!ingest::read_base(st, key, bp)) {
+      std::printf("{\"found\":false}\n");
+      return 0;
+    }
+    std::printf("{\"found\":true,\"out\":%d,\"in\":%d,\"packed\":%s,\"scales\":%s,\"biases\":%s}\n",
+                bp.out_features, bp.in_features, jlist(bp.packed).c_str(), jlist(bp.scales_f16).c_str(),
+                jlist(bp.biases_f16).c_str());
+  } catch (const ingest::IngestError &e) {
+    return ingest_error(e);
+  }
+  return 0;
+}
+
+// ---- gpu-ingest: safetensors-loaded layers against array-loaded ones, bit for bit ----
+
+template <class T>
+std::vector<T> read_raw(const std::string &path, size_t n) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) throw std::runtime_error("cannot open " + path);
+  std::vector<T> v(n);
+  f.read(reinterpret_cast<char *>(v.data()), (std::streamsize)(n * sizeof(T)));
+  if ((size_t)f.gcount() != n * sizeof(T)) throw std::runtime_error("short read " + path);
+  return v;
+}
+
+// DIR holds base.safetensors, adapter1.safetensors (+ adapter1.json metadata), adapter2.safetensors
+// and the same arrays raw: L<l>.<module>.{packed,scales,biases}.bin, a<id>.<module>.{A,B}.bin.
+int gpu_ingest_mode(const std::string &dir, int L, int H, int I, int KV, int r1, float alpha1, int r2) {
+  const char *mods[] = {"q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"};
+  auto shape = [&](const std::string &m, int &out, int &in) {
+    in = m == "down_proj" ? I : H;
+    out = (m == "gate_proj" || m == "up_proj") ? I : (m == "k_proj" || m == "v_proj") ? KV : H;
+  };
+  run("gpu_ingest_safetensors_matches_arrays", [&] {
+    HipKernels ks(0, L), ka(0, L);
+    const ingest::MappedFile base(dir + "/base.safetensors");
+    CHECK(ks.load_base_safetensors(base.data(), base.size()) == 7 * L);
+    for (int l = 0; l < L; ++l)
+      for (const char *m : mods) {
+        int out, in;
+        shape(m, out, in);
+        const std::string pre = dir + "/L" + std::to_string(l) + "." + m + ".";
+        auto p = read_raw<uint32_t>(pre + "packed.bin", (size_t)out * in / 8);
+        auto sc = read_raw<uint16_t>(pre + "scales.bin", (size_t)out * in / 64);
+        auto bi = read_raw<uint16_t>(pre + "biases.bin", (size_t)out * in / 64);
+        ka.set_base(l, m, out, in, p.data(), sc.data(), bi.data());
+      }
+    // adapter 1: prefix keys, metadata (rank, alpha) and an lm_head pair the device path skips
+    const ingest::MappedFile a1(dir + "/adapter1.safetensors");
+    const std::string md1 = read_text(dir + "/adapter1.json");
+    const ingest::AdapterSpec s1 = ks.load_adapter_with_metadata(1, a1.data(), a1.size(), md1.c_str());
+    CHECK(s1.rank == (uint64_t)r1 && s1.alpha == alpha1);
+    CHECK(ks.load_warnings().size() == 1 && ks.load_warnings()[0].find("lm_head") != std::string::npos);
+    // adapter 2: suffix keys, no metadata (rank 4, alpha 16)
+    const ingest::MappedFile a2(dir + "/adapter2.safetensors");
+    ks.load_adapter(2, a2.data(), a2.size());
+    CHECK(ks.load_warnings().empty());
+    auto arrays = [&](int id, const std::vector<std::string> &names, int r) {
+      std::vector<LoraLayerWeights> w((size_t)L);
+      for (const auto &m : names) {
+        int out, in;
+        shape(m, out, in);
+        LoraModuleWeights mw;
+        mw.in_features = in;
+        mw.out_features = out;
+        const std::string pre = dir + "/a" + std::to_string(id) + "." + m + ".";
+        mw.A = read_raw<float>(pre + "A.bin", (size_t)r * in);
+        mw.B = read_raw<float>(pre + "B.bin", (size_t)out * r);
+        for (int l = 0; l < L; ++l) w[(size_t)l][m] = mw;
+      }
+      return w;
+    };
+    ka.load_adapter_with_metadata(1, arrays(1, {"q_proj", "v_proj", "o_proj", "gate_proj", "down_proj"}, r1),
+                                  AdapterLoadMetadata{"a1", (uint32_t)r1, alpha1, {}});
+    ka.load_adapter_with_metadata(2, arrays(2, {"k_proj", "up_proj"}, r2), AdapterLoadMetadata{"a2", 4, 16.0f, {}});
+    const int Tmax = 40;
+    ks.reserve(Tmax);
+    ka.reserve(Tmax);
+    auto x = read_raw<uint16_t>(dir + "/x.bin", (size_t)Tmax * I);
+    uint16_t *dx, *dy1, *dy2, *dq1, *dq2;
+    aoship_ring_t *dr;
+    const size_t ybytes = (size_t)Tmax * I * 2;
+    detail::hip_check(hipMalloc(&dx, x.size() * 2), "hipMalloc");
+    detail::hip_check(hipMalloc(&dy1, ybytes), "hipMalloc");
+    detail::hip_check(hipMalloc(&dy2, ybytes), "hipMalloc");
+    detail::hip_check(hipMalloc(&dq1, 3 * ybytes), "hipMalloc");
+    detail::hip_check(hipMalloc(&dq2, 3 * ybytes), "hipMalloc");
+    detail::hip_check(hipMalloc(&dr, sizeof(aoship_ring_t) * Tmax), "hipMalloc");
+    detail::hip_check(hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    std::vector<aoship_ring_t> rings((size_t)Tmax);
+    for (int t = 0; t < Tmax; ++t) {
+      RouterRing ring = RouterRing::with_k(2);
+      const int16_t g = (int16_t)(1000 + (t * 977) % 30000);
+      ring.set({(uint16_t)(1 + t % 2), (uint16_t)(2 - t % 2)}, {g, (int16_t)(32767 - g)});
+      rings[(size_t)t] = ring.to_device();
+    }
+    detail::hip_check(hipMemcpy(dr, rings.data(), sizeof(aoship_ring_t) * Tmax, hipMemcpyHostToDevice), "hipMemcpy");
+    auto same = [&](const uint16_t *a, const uint16_t *b, size_t n) {
+      std::vector<uint16_t> ha(n), hb(n);
+      detail::hip_check(hipMemcpy(ha.data(), a, n * 2, hipMemcpyDeviceToHost), "hipMemcpy");
+      detail::hip_check(hipMemcpy(hb.data(), b, n * 2, hipMemcpyDeviceToHost), "hipMemcpy");
+      bool nonzero = false;
+      for (size_t i = 0; i < n; ++i) nonzero = nonzero || (ha[i] & 0x7FFF);
+      return nonzero && std::memcmp(ha.data(), hb.data(), n * 2) == 0;
+    };
+    for (int T : {1, 5, Tmax})
+      for (int l = 0; l < L; ++l) {
+        std::printf("  case T=%d layer=%d\n", T, l);
+        std::fflush(stdout);
+        ks.mlp_forward(l, dx, T, dr, dy1);
+        ka.mlp_forward(l, dx, T, dr, dy2);
+        CHECK(same(dy1, dy2, (size_t)T * H));
+        ks.qkv_forward(l, dx, T, dr, dq1, dq1 + (size_t)T * H, dq1 + (size_t)T * (H + KV));
+        ka.qkv_forward(l, dx, T, dr, dq2, dq2 + (size_t)T * H, dq2 + (size_t)T * (H + KV));
+        CHECK(same(dq1, dq2, (size_t)T * (H + 2 * KV)));
+        ks.proj_forward(l, "o_proj", dx, T, dr, dy1);
+        ka.proj_forward(l, "o_proj", dx, T, dr, dy2);
+        CHECK(same(dy1, dy2, (size_t)T * H));
+      }
+    for (void *p : {(void *)dx, (void *)dy1, (void *)dy2, (void *)dq1, (void *)dq2, (void *)dr}) (void)hipFree(p);
+  });
+  std::printf("gpu-ingest: %d failed\n", g_failed);
+  return g_failed ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
   const std::string mode = argc > 1 ? argv[1] : "cpu";
+  if (mode == "ingest-adapter" && (argc == 3 || argc == 4)) return ingest_adapter_mode(argv[2], argc == 4 ? argv[3] : nullptr);
+  if (mode == "ingest-base" && argc == 4) return ingest_base_mode(argv[2], argv[3]);
+  if (mode == "ingest-lora" && argc == 6) return ingest_lora_mode(argv[2], argv[3], argv[4], argv[5]);
+  if (mode == "gpu-ingest" && argc == 10)
+    return gpu_ingest_mode(argv[2], std::atoi(argv[3]), std::atoi(argv[4]), std::atoi(argv[5]), std::atoi(argv[6]),
+                           std::atoi(argv[7]), (float)std::atof(argv[8]), std::atoi(argv[9]));
   if (mode == "cpu")
     cpu_tests();
   else if (mode == "gpu")
     gpu_tests();
   else {
-    std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
+    std::fprintf(stderr,
+                 "usage: %s cpu | gpu | ingest-adapter FILE [METADATA_JSON] | ingest-base FILE KEY |\n"
+                 "       ingest-lora FILE RANK ALPHA TARGET[,TARGET...] |\n"
+                 "       gpu-ingest DIR LAYERS HIDDEN INTERMEDIATE KV_OUT RANK1 ALPHA1 RANK2\n",
+                 argv[0]);
     return 2;
   }
   std::printf("%s: %d failed\n", mode.c_str(), g_failed);
