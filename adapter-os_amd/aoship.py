@@ -35,6 +35,13 @@ _SIGS = {
     "aoship_router_new": (_P, [C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, _P]),
     "aoship_router_set_policy_mask": (C.c_int, [_P, _P]),
     "aoship_router_set_stream": (C.c_int, [_P, _P]),
+    "aoship_router_set_scope": (C.c_int, [_P, _P]),
+    "aoship_router_set_adaptive_seed": (C.c_int, [_P, _P]),
+    "aoship_adaptive_tie_breakers": (C.c_int, [_P, C.c_int, _P]),
+    "aoship_router_set_decision_policy": (C.c_int, [_P, _P, C.c_int]),
+    "aoship_router_set_ring_mapping": (C.c_int, [_P, _P, _P]),
+    "aoship_router_set_decision_hashing": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "aoship_blake3": (C.c_int, [_P, C.c_size_t, _P]),
     "aoship_router_free": (None, [_P]),
     "aoship_route": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "aoship_route_features": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, _P, _P, _P]),
@@ -128,6 +135,37 @@ def attest_determinism() -> str:
     return buf.value.decode()
 
 
+def _host(a, dtype, n: int):
+    if a is None:
+        return None
+    a = np.ascontiguousarray(np.asarray(a, dtype=dtype))
+    if a.shape != (n,):
+        raise ValueError(f"expected {n} entries, got shape {a.shape}")
+    return a
+
+
+def _hptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def adaptive_tie_breakers(seed: bytes, n: int) -> np.ndarray:
+    """ChaCha20Rng::from_seed(seed).gen::<u64>() x n, computed by the library on the host."""
+    sd = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+    if sd.size != 32:
+        raise ValueError("the tie-break seed has 32 bytes")
+    out = np.zeros(max(n, 1), np.uint64)
+    _check(lib().aoship_adaptive_tie_breakers(sd.ctypes.data, n, out.ctypes.data), "aoship_adaptive_tie_breakers")
+    return out[:n]
+
+
+def blake3(data: bytes) -> bytes:
+    """B3Hash::hash through the library (host)."""
+    buf = C.create_string_buffer(bytes(data), max(len(data), 1))
+    out = (C.c_uint8 * 32)()
+    _check(lib().aoship_blake3(buf, len(data), out), "aoship_blake3")
+    return bytes(out)
+
+
 def rings_from_bytes(raw: np.ndarray) -> np.ndarray:
     return np.frombuffer(np.ascontiguousarray(raw).tobytes(), dtype=RING_DTYPE)
 
@@ -154,6 +192,43 @@ class Router:
 
     def set_stream(self, stream_ptr: int | None) -> None:
         _check(lib().aoship_router_set_stream(self.h, stream_ptr), "aoship_router_set_stream")
+
+    def set_scope(self, in_scope) -> None:
+        """Scope hint: 1 where the adapter's scope_path equals the hint (None = no hint)."""
+        a = _host(in_scope, np.uint8, self.n)
+        _check(lib().aoship_router_set_scope(self.h, _hptr(a)), "aoship_router_set_scope")
+
+    def set_adaptive_seed(self, seed: bytes | None) -> None:
+        """Adaptive mode with the 32-byte tie-break seed (None = deterministic mode)."""
+        a = None if seed is None else np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+        if a is not None and a.size != 32:
+            raise ValueError("the tie-break seed has 32 bytes")
+        _check(lib().aoship_router_set_adaptive_seed(self.h, _hptr(a)), "aoship_router_set_adaptive_seed")
+
+    def set_decision_policy(self, allowed, max_adapters_per_token: int | None = None) -> None:
+        """filter_decision_by_policy on every decision (allowed None = no policy)."""
+        a = _host(allowed, np.uint8, self.n)
+        cap = -1 if max_adapters_per_token is None else int(max_adapters_per_token)
+        _check(lib().aoship_router_set_decision_policy(self.h, _hptr(a), cap), "aoship_router_set_decision_policy")
+
+    def set_ring_mapping(self, active_ids=None, strengths=None) -> None:
+        """Ring index = active_ids[decision index]; gates scaled by strengths[decision index]."""
+        a = _host(active_ids, np.uint16, self.n)
+        s = _host(strengths, np.float32, self.n)
+        _check(lib().aoship_router_set_ring_mapping(self.h, _hptr(a), _hptr(s)), "aoship_router_set_ring_mapping")
+
+    def set_decision_hashing(self, hashes, reasoning_hash: bytes | None = None,
+                             backend_identity_hash: bytes | None = None) -> None:
+        """Decision hashes into hashes (a device uint8 tensor of 96 bytes per token; None = off)."""
+        cap = 0 if hashes is None else hashes.numel() // 96
+        r = None if reasoning_hash is None else np.frombuffer(bytes(reasoning_hash), np.uint8).copy()
+        b = None if backend_identity_hash is None else np.frombuffer(bytes(backend_identity_hash), np.uint8).copy()
+        for a in (r, b):
+            if a is not None and a.size != 32:
+                raise ValueError("reasoning / backend identity hashes have 32 bytes")
+        self._hashes = hashes  # keep the buffer alive while the router may write it
+        _check(lib().aoship_router_set_decision_hashing(self.h, _ptr(hashes), cap, _hptr(r), _hptr(b)),
+               "aoship_router_set_decision_hashing")
 
     def route(self, priors, rings, status=None) -> None:
         T = priors.shape[0]

@@ -9,12 +9,14 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
 #include <vector>
 
+#include "aos_blake3.h"
 #include "aos_exp.h"
 #include "aoship_internal.h"
 
@@ -167,8 +169,87 @@ struct aoship_router {
   float tau = 1.0f, eps = 0.02f, bias = 1.0f;
   DevBuf stable_id, allowed;
   bool has_mask = false;
+  std::vector<uint64_t> h_stable_id;
+  /* extras: each buffer is released when its feature is off */
+  DevBuf scope, tie_key, post_allowed, active_ids, strengths;
+  int post_max = -1;
+  uint8_t *hashes = nullptr; /* caller's device buffer, [hash_max_tokens][96] */
+  int hash_max_tokens = 0;
+  DevBuf hash_extra;         /* reasoning hash words 0-7, backend identity hash words 8-15 */
+  int hash_reasoning = 0, hash_backend = 0;
   hipStream_t stream = nullptr;
 };
+
+/* ChaCha20 block (RFC 8439 section 2.3: 20 rounds, output = rounds(state) + state) over the state
+ * layout of rand_chacha 0.3: "expand 32-byte k", the 32-byte key, a 64-bit block counter in words
+ * 12-13 and a 64-bit stream id in words 14-15. */
+static void chacha20_block(const uint32_t key[8], uint64_t counter, uint64_t stream, uint32_t out[16]) {
+  uint32_t st[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u, key[0], key[1], key[2], key[3],
+                     key[4],      key[5],      key[6],      key[7],      (uint32_t)counter,
+                     (uint32_t)(counter >> 32), (uint32_t)stream, (uint32_t)(stream >> 32)};
+  uint32_t x[16];
+  memcpy(x, st, sizeof x);
+  auto rotl = [](uint32_t v, int c) { return (v << c) | (v >> (32 - c)); };
+  auto qr = [&](int a, int b, int c, int d) {
+    x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 16);
+    x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 12);
+    x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 8);
+    x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 7);
+  };
+  for (int i = 0; i < 10; ++i) {
+    qr(0, 4, 8, 12); qr(1, 5, 9, 13); qr(2, 6, 10, 14); qr(3, 7, 11, 15);
+    qr(0, 5, 10, 15); qr(1, 6, 11, 12); qr(2, 7, 8, 13); qr(3, 4, 9, 14);
+  }
+  for (int i = 0; i < 16; ++i) out[i] = x[i] + st[i];
+}
+
+/* ChaCha20Rng::from_seed(seed) then n x gen::<u64>(): next_u64 joins consecutive keystream words
+ * low word first (rand_core BlockRng), the stream starting at block 0 of stream 0. */
+extern "C" int aoship_adaptive_tie_breakers(const uint8_t *seed, int n, uint64_t *out) {
+  if (!seed || !out || n < 0) return set_err("aoship_adaptive_tie_breakers: bad arguments");
+  uint32_t key[8];
+  for (int i = 0; i < 8; ++i)
+    key[i] = (uint32_t)seed[4 * i] | ((uint32_t)seed[4 * i + 1] << 8) | ((uint32_t)seed[4 * i + 2] << 16) |
+             ((uint32_t)seed[4 * i + 3] << 24);
+  uint32_t blk[16];
+  for (int a = 0; a < n; ++a) {
+    if ((a & 7) == 0) chacha20_block(key, (uint64_t)(a >> 3), 0, blk);
+    const int w = 2 * (a & 7);
+    out[a] = (uint64_t)blk[w] | ((uint64_t)blk[w + 1] << 32);
+  }
+  return 0;
+}
+
+extern "C" int aoship_blake3(const void *data, size_t len, uint8_t *out) {
+  if ((!data && len) || !out) return set_err("aoship_blake3: null argument");
+  const uint8_t *bytes = (const uint8_t *)data;
+  auto word = [&](size_t j) {
+    uint32_t v = 0;
+    for (int b = 0; b < 4; ++b)
+      if (4 * j + (size_t)b < len) v |= (uint32_t)bytes[4 * j + (size_t)b] << (8 * b);
+    return v;
+  };
+  const int n = aos_b3_nchunks(len);
+  uint32_t h[8];
+  if (n == 1) {
+    aos_b3_chunk(word, len, 0, true, h);
+  } else {
+    std::vector<uint32_t> cvs((size_t)n * 8);
+    uint32_t(*cv)[8] = (uint32_t(*)[8])cvs.data();
+    for (int c = 0; c < n; ++c) aos_b3_chunk(word, len, (uint64_t)c, false, cv[c]);
+    aos_b3_merge(cv, n, h);
+  }
+  for (int i = 0; i < 32; ++i) out[i] = (uint8_t)(h[i / 4] >> (8 * (i % 4)));
+  return 0;
+}
+
+static int upload_or_release(DevBuf &b, const void *src, size_t bytes) {
+  if (!src) {
+    b.release();
+    return 0;
+  }
+  return b.upload(src, bytes);
+}
 
 extern "C" aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, float eps,
                                               float routing_bias, const uint64_t *stable_ids) {
@@ -194,7 +275,71 @@ extern "C" aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, 
     delete r;
     return nullptr;
   }
+  r->h_stable_id = ids;
   return r;
+}
+
+extern "C" int aoship_router_set_scope(aoship_router_t *r, const uint8_t *in_scope) {
+  if (!r) return set_err("aoship_router_set_scope: null router");
+  if (ensure_device()) return -1;
+  return upload_or_release(r->scope, in_scope, (size_t)r->n);
+}
+
+extern "C" int aoship_router_set_adaptive_seed(aoship_router_t *r, const uint8_t *seed) {
+  if (!r) return set_err("aoship_router_set_adaptive_seed: null router");
+  if (ensure_device()) return -1;
+  if (!seed) {
+    r->tie_key.release();
+    return 0;
+  }
+  /* The rank of each adapter in (breaker, stable_id, index) order: equal scores compare by it
+   * exactly as sort_scores_adaptive compares them, and it fits the device's 64-bit key field. */
+  const int n = r->n;
+  std::vector<uint64_t> brk((size_t)n), rank((size_t)n);
+  std::vector<int> order((size_t)n);
+  aoship_adaptive_tie_breakers(seed, n, brk.data());
+  for (int i = 0; i < n; ++i) order[(size_t)i] = i;
+  std::sort(order.begin(), order.end(), [&](int a, int b) {
+    if (brk[(size_t)a] != brk[(size_t)b]) return brk[(size_t)a] < brk[(size_t)b];
+    if (r->h_stable_id[(size_t)a] != r->h_stable_id[(size_t)b])
+      return r->h_stable_id[(size_t)a] < r->h_stable_id[(size_t)b];
+    return a < b;
+  });
+  for (int pos = 0; pos < n; ++pos) rank[(size_t)order[(size_t)pos]] = (uint64_t)pos;
+  return r->tie_key.upload(rank.data(), rank.size() * sizeof(uint64_t));
+}
+
+extern "C" int aoship_router_set_decision_policy(aoship_router_t *r, const uint8_t *allowed,
+                                                 int max_adapters_per_token) {
+  if (!r) return set_err("aoship_router_set_decision_policy: null router");
+  if (ensure_device()) return -1;
+  r->post_max = max_adapters_per_token < 0 ? -1 : max_adapters_per_token;
+  return upload_or_release(r->post_allowed, allowed, (size_t)r->n);
+}
+
+extern "C" int aoship_router_set_decision_hashing(aoship_router_t *r, uint8_t *hashes, int max_tokens,
+                                                  const uint8_t *reasoning_hash,
+                                                  const uint8_t *backend_identity_hash) {
+  if (!r) return set_err("aoship_router_set_decision_hashing: null router");
+  if (hashes && max_tokens < 1) return set_err("aoship_router_set_decision_hashing: max_tokens must be >= 1");
+  if (ensure_device()) return -1;
+  uint8_t extra[64] = {0};
+  if (reasoning_hash) memcpy(extra, reasoning_hash, 32);
+  if (backend_identity_hash) memcpy(extra + 32, backend_identity_hash, 32);
+  if (hashes && r->hash_extra.upload(extra, sizeof extra)) return -1;
+  r->hashes = hashes;
+  r->hash_max_tokens = hashes ? max_tokens : 0;
+  r->hash_reasoning = reasoning_hash ? 1 : 0;
+  r->hash_backend = backend_identity_hash ? 1 : 0;
+  return 0;
+}
+
+extern "C" int aoship_router_set_ring_mapping(aoship_router_t *r, const uint16_t *active_ids,
+                                              const float *strengths) {
+  if (!r) return set_err("aoship_router_set_ring_mapping: null router");
+  if (ensure_device()) return -1;
+  if (upload_or_release(r->active_ids, active_ids, (size_t)r->n * sizeof(uint16_t))) return -1;
+  return upload_or_release(r->strengths, strengths, (size_t)r->n * sizeof(float));
 }
 
 extern "C" int aoship_router_set_policy_mask(aoship_router_t *r, const uint8_t *allowed) {
@@ -240,6 +385,21 @@ static int route_common(aoship_router_t *r, const float *features, const float *
   p.rings = rings;
   p.status = status;
   p.priors_in = priors_in;
+  p.scope = r->scope.p ? r->scope.as<uint8_t>() : nullptr;
+  p.tie_key = r->tie_key.p ? r->tie_key.as<uint64_t>() : nullptr;
+  p.post_allowed = r->post_allowed.p ? r->post_allowed.as<uint8_t>() : nullptr;
+  p.post_max = r->post_max;
+  p.active_ids = r->active_ids.p ? r->active_ids.as<uint16_t>() : nullptr;
+  p.strengths = r->strengths.p ? r->strengths.as<float>() : nullptr;
+  if (r->hashes) {
+    if (T > r->hash_max_tokens)
+      return set_err("aoship_route: T exceeds the decision-hash buffer (" + std::to_string(r->hash_max_tokens) +
+                     " tokens)");
+    p.hashes = r->hashes;
+    p.hash_extra = r->hash_extra.as<uint32_t>();
+    p.hash_reasoning = r->hash_reasoning;
+    p.hash_backend = r->hash_backend;
+  }
   if (features) {
     if (!router_w || d <= 0 || d % 4 != 0)
       return set_err("aoship_route_features: router weights missing or d not a multiple of 4");

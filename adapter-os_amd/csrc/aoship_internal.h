@@ -82,6 +82,16 @@ typedef struct {
   const uint8_t *allowed;
   aoship_ring_t *rings;
   int32_t *status;
+  /* router extras, each NULL when off */
+  const uint8_t *scope;        /* [n] 0 = prior replaced by -1e9 (scope hint) */
+  const uint64_t *tie_key;     /* [n] adaptive mode: rank of (breaker, stable_id, index) */
+  const uint8_t *post_allowed; /* [n] decision policy: 1 = the adapter passes the policy sets */
+  int post_max;                /* decision policy: max adapters per token, -1 = no cap */
+  const uint16_t *active_ids;  /* [n] ring index for a decision index */
+  const float *strengths;      /* [n] gate scaling by decision index */
+  uint8_t *hashes;             /* [T][96] decision hashes (input, output, combined) */
+  const uint32_t *hash_extra;  /* [16] reasoning hash words 0-7, backend identity hash words 8-15 */
+  int hash_reasoning, hash_backend;
 } aos_route_params;
 
 /* ---- LoRA shrink for T <= 32 tokens: S[t][col] = sum_i A_row(col)[i] x[t][i], float32 ----

@@ -22,6 +22,7 @@
  * dot product's loads issued before its arithmetic; the priors go through LDS to wave 0, which
  * routes.
  */
+#include "aos_blake3.h"
 #include "aos_exp.h"
 #include "aoship_device.h"
 #include "aoship_internal.h"
@@ -90,8 +91,136 @@ __device__ __forceinline__ int quantize_q15(float g) {
   return (int)r;
 }
 
+/* A zero ring; code 0 keeps the token's position (an empty decision), -1 / -2 (errors) do not. */
+__device__ __forceinline__ void ring_empty(aoship_ring_t *ring, int32_t *status, int t, int lane, int code) {
+  if (lane < 10) ((uint32_t *)ring)[lane] = 0u;
+  if (lane == 0) {
+    if (code == 0) ring->current_pos = (uint32_t)t;
+    if (status) status[t] = code;
+  }
+}
+
+/* No decision, no hash: 96 zero bytes. */
+__device__ __forceinline__ void hash_empty(uint8_t *hashes, int t, int lane) {
+  if (hashes && lane < 24) ((uint32_t *)(hashes + (size_t)96 * t))[lane] = 0u;
+}
+
+#define AOS_B3_MAX_CHUNKS (AOS_MAX_ADAPTERS * 4 / AOS_B3_CHUNK_LEN + 1)
+
+/* Router::compute_decision_hash (router.rs:1427-1484) with an empty feature vector, for the
+ * decision (didx, dq)[0..kk) in canonical order: input = BLAKE3(priors as routed, float32 LE
+ * [|| reasoning]), lane c hashing chunk c and lane 0 merging the tree; output = BLAKE3(indices
+ * u16 LE || gates i16 LE [|| reasoning]); combined = BLAKE3(input || output [|| reasoning]
+ * [|| backend]). Written to hashes[96 t ..]. */
+__device__ __noinline__ void decision_hash(uint8_t *hashes, const float *priors, const uint8_t *scope, int n,
+                                           const uint32_t *extra, int reasoning, int backend, int t, int lane, int kk,
+                                           uint32_t ow0, uint32_t ow1, uint32_t ow2, uint32_t ow3, uint32_t ow4,
+                                           uint32_t ow5, uint32_t ow6, uint32_t ow7) {
+  __shared__ uint32_t cvs[AOS_B3_MAX_CHUNKS][8];
+  const size_t in_len = (size_t)n * 4 + (reasoning ? 32 : 0);
+  auto in_word = [&](size_t j) -> uint32_t {
+    if (j < (size_t)n) {
+      const float v = (scope && !scope[j]) ? -1.0e9f : priors[j];
+      return __builtin_bit_cast(uint32_t, v);
+    }
+    return extra[j - (size_t)n];
+  };
+  const int C = aos_b3_nchunks(in_len);
+  uint32_t h_in[8];
+  if (C > 1) {
+    if (lane < C) {
+      uint32_t cv[8];
+      aos_b3_chunk(in_word, in_len, (uint64_t)lane, false, cv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cvs[lane][i] = cv[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  }
+  if (lane != 0) return;
+  if (C > 1) aos_b3_merge(cvs, C, h_in);
+  else aos_b3_chunk(in_word, in_len, 0, true, h_in);
+
+  /* output: the packed words of the kk indices and kk gates, then the reasoning hash */
+  const uint32_t ow[8] = {ow0, ow1, ow2, ow3, ow4, ow5, ow6, ow7};
+  const size_t out_len = (size_t)kk * 4 + (reasoning ? 32 : 0);
+  auto out_word = [&](size_t j) -> uint32_t {
+    uint32_t v = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+      if ((size_t)w == j) v = ow[w];
+    return j < (size_t)kk ? v : extra[j - (size_t)kk];
+  };
+  uint32_t h_out[8];
+  aos_b3_chunk(out_word, out_len, 0, true, h_out);
+
+  const size_t comb_len = 64 + (reasoning ? 32 : 0) + (backend ? 32 : 0);
+  auto comb_word = [&](size_t j) -> uint32_t {
+    uint32_t v = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      if ((size_t)w == j) v = h_in[w];
+      if ((size_t)w + 8 == j) v = h_out[w];
+    }
+    if (j >= 16) {
+      const size_t e = j - 16;
+      v = (reasoning && e < 8) ? extra[e] : extra[8 + (reasoning ? e - 8 : e)];
+    }
+    return v;
+  };
+  uint32_t h_comb[8];
+  aos_b3_chunk(comb_word, comb_len, 0, true, h_comb);
+  uint32_t *dst = (uint32_t *)(hashes + (size_t)96 * t);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    dst[i] = h_in[i];
+    dst[8 + i] = h_out[i];
+    dst[16 + i] = h_comb[i];
+  }
+}
+
+/* renormalize_gates_q15 (policy_mask.rs:164-213): one gate -> 32767; otherwise g = q / 32767 in
+ * float64 with Kahan summation in order, q' = quantize(float(g / sum)), or the float32 uniform
+ * 1/n quantised when the sum is 0. */
+__device__ __forceinline__ void renormalize_q15(int (&q)[8], int n) {
+  if (n == 1) {
+    q[0] = 32767;
+    return;
+  }
+  double g[8];
+  double sum = 0.0, c = 0.0;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    g[s] = (double)q[s] / 32767.0;
+    if (s < n) {
+      const double y = g[s] - c;
+      const double tt = sum + y;
+      c = (tt - sum) - y;
+      sum = tt;
+    }
+  }
+  const float uni = 1.0f / (float)n;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    if (s < n) q[s] = sum > 0.0 ? quantize_q15((float)(g[s] / sum)) : quantize_q15(uni);
+}
+
+/* Strength scaling (router_bridge.rs:168-186): round_half_away(q * clamp(strength, 0, 1)) as i16,
+ * clamped to +-32767; a NaN strength gives 0 (NaN survives the clamp and casts to 0). */
+__device__ __forceinline__ int scale_gate(int q, float strength) {
+  if (strength != strength) return 0;
+  const float st = strength < 0.0f ? 0.0f : (strength > 1.0f ? 1.0f : strength);
+  const float v = (float)q * st;
+  float r = truncf(v);
+  if (fabsf(v - r) >= 0.5f) r += copysignf(1.0f, v);
+  if (r > 32767.0f) r = 32767.0f;
+  if (r < -32767.0f) r = -32767.0f;
+  return (int)r;
+}
+
 template <bool LDS>
-__device__ void route_one(const aos_route_params &p, const float *priors, int t, int lane) {
+__device__ __forceinline__ void route_one(const aos_route_params &p, const float *priors, int t, int lane) {
   const int n = p.n;
   /* every prior is checked for finiteness, allowed or not (validate_router_inputs); the chunked
    * passes below visit each index exactly once */
@@ -102,14 +231,18 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
     a = ~0ull;
     b = ~0ull;
     if (i >= n) return false;
-    const float prior = LDS ? priors[i] : priors[i];
-    if (!__builtin_isfinite(prior)) bad = true;
+    const float raw = priors[i];
+    if (!__builtin_isfinite(raw)) bad = true;
     if (p.allowed && !p.allowed[i]) return false;
+    /* scope hint (router.rs:1587-1602): adapters outside the scope score from -1e9 */
+    const float prior = (p.scope && !p.scope[i]) ? -1.0e9f : raw;
     float sim = (prior + 0.0f) - 0.0f;
     float score = sim * p.bias;
     score = score * 1.0f;
     if (!__builtin_isfinite(score)) bad = true;
-    uint64_t sid = p.stable_id ? p.stable_id[i] : 0ull;
+    /* adaptive mode (sort_scores_adaptive, router.rs:265-306): the rank of (breaker, stable_id,
+     * index) stands in for stable_id, which orders equal scores exactly as those three keys do */
+    uint64_t sid = p.tie_key ? p.tie_key[i] : (p.stable_id ? p.stable_id[i] : 0ull);
     a = ((uint64_t)score_key_desc(score) << 32) | (sid >> 32);
     b = ((sid & 0xffffffffull) << 32) | (uint64_t)(uint32_t)i;
     return true;
@@ -158,13 +291,12 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
 
   aoship_ring_t *ring = p.rings + t;
   const bool any_bad = __ballot(bad) != 0ull;
+  const bool policy = p.post_allowed != nullptr;
   int kk = p.k < m_allowed ? p.k : m_allowed;
   if (any_bad || kk <= 0) {
-    if (lane < 10) ((uint32_t *)ring)[lane] = 0u;
-    if (lane == 0) {
-      if (!any_bad) ring->current_pos = (uint32_t)t;
-      if (p.status) p.status[t] = any_bad ? -1 : 0;
-    }
+    /* an empty decision under a decision policy is a PolicyViolation (policy_mask.rs:330-337) */
+    ring_empty(ring, p.status, t, lane, any_bad ? -1 : (policy ? -2 : 0));
+    hash_empty(p.hashes, t, lane);
     return;
   }
 
@@ -179,6 +311,11 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
     sc[s] = score_from_key(skey[s]);
     ssid[s] = ((a & 0xffffffffull) << 32) | (b >> 32);
     sidx[s] = (uint32_t)b;
+  }
+  if (p.tie_key) {
+    /* the canonical re-sort keeps stable_id in adaptive mode (router.rs:1305-1325) */
+#pragma unroll
+    for (int s = 0; s < 8; ++s) ssid[s] = (s < kk && p.stable_id) ? p.stable_id[sidx[s]] : 0ull;
   }
 
   /* deterministic_softmax (router.rs:1340-1411); tau > 0 after sanitising. */
@@ -226,11 +363,8 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
   for (int s = 0; s < 8; ++s)
     if (s < kk) S += g[s];
   if (!(S > 0.0f)) {
-    if (lane < 10) ((uint32_t *)ring)[lane] = 0u;
-    if (lane == 0) {
-      ring->current_pos = (uint32_t)t;
-      if (p.status) p.status[t] = 0;
-    }
+    ring_empty(ring, p.status, t, lane, policy ? -2 : 0);
+    hash_empty(p.hashes, t, lane);
     return;
   }
   int q[8];
@@ -254,20 +388,107 @@ __device__ void route_one(const aos_route_params &p, const float *priors, int t,
     }
     rank[i] = r;
   }
+  /* the decision in canonical order, in every lane */
+  uint32_t didx[8];
+  int dq[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    didx[s] = 0;
+    dq[s] = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (i < kk && rank[i] == s) {
+        didx[s] = sidx[i];
+        dq[s] = q[i];
+      }
+  /* the decision hash belongs to the router's decision, before any policy filter */
+  if (p.hashes) {
+    /* kk indices (u16 LE) then kk gates (i16 LE), packed two halves to a word */
+    uint32_t hw[16];
+#pragma unroll
+    for (int pos = 0; pos < 16; ++pos) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if (s < kk && pos == s) v = didx[s] & 0xFFFFu;
+        if (s < kk && pos == kk + s) v = (uint32_t)(uint16_t)(int16_t)dq[s];
+      }
+      hw[pos] = v;
+    }
+    decision_hash(p.hashes, priors, p.scope, p.n, p.hash_extra, p.hash_reasoning, p.hash_backend, t, lane, kk,
+                  hw[0] | hw[1] << 16, hw[2] | hw[3] << 16, hw[4] | hw[5] << 16,
+                  hw[6] | hw[7] << 16, hw[8] | hw[9] << 16, hw[10] | hw[11] << 16, hw[12] | hw[13] << 16,
+                  hw[14] | hw[15] << 16);
+  }
+  int m = kk;
+  if (policy) {
+    /* filter_decision_by_policy (policy_mask.rs:221-355): keep passing entries in decision
+     * order, cap at max_adapters_per_token, renormalise when anything was removed */
+    uint32_t fidx[8];
+    int fq[8];
+    int kept = 0;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      fidx[s] = 0;
+      fq[s] = 0;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bool keep = s < kk && p.post_allowed[didx[s]] != 0;
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        if (keep && d == kept) {
+          fidx[d] = didx[s];
+          fq[d] = dq[s];
+        }
+      kept += keep ? 1 : 0;
+    }
+    if (p.post_max >= 0 && kept > p.post_max) kept = p.post_max;
+    if (kept == 0) {
+      ring_empty(ring, p.status, t, lane, -2);
+      return;
+    }
+    if (kept < kk) renormalize_q15(fq, kept);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      didx[s] = s < kept ? fidx[s] : 0u;
+      dq[s] = s < kept ? fq[s] : 0;
+    }
+    m = kept;
+  }
+  /* decision_to_router_ring_with_active_ids_and_strengths (router_bridge.rs:137-186) */
+  bool zero_fill = false;
+  uint32_t ridx[8];
+  int rq[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    ridx[s] = (s < m && p.active_ids) ? (uint32_t)p.active_ids[didx[s]] : didx[s];
+    /* set_with_max_adapter(.., u16::MAX): an index of 65535 zero-fills the ring (lib.rs:163-179) */
+    zero_fill = zero_fill || (s < m && ridx[s] >= 0xFFFFu);
+    rq[s] = dq[s];
+    if (s < m && p.strengths) rq[s] = scale_gate(dq[s], p.strengths[didx[s]]);
+  }
+  if (zero_fill) {
+    ring_empty(ring, p.status, t, lane, 0);
+    return;
+  }
   if (lane < 8) {
     uint32_t oi = 0;
     int oq = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (i < kk && rank[i] == lane) {
-        oi = sidx[i];
-        oq = q[i];
+    for (int s = 0; s < 8; ++s)
+      if (s == lane && s < m) {
+        oi = ridx[s];
+        oq = rq[s];
       }
     ring->adapter_indices[lane] = (uint16_t)oi;
     ring->gates_q15[lane] = (int16_t)oq;
   }
   if (lane == 0) {
-    ring->top_k = (uint32_t)kk;
+    ring->top_k = (uint32_t)m;
     ring->current_pos = (uint32_t)t;
     if (p.status) p.status[t] = 0;
   }

@@ -77,6 +77,11 @@ int aoship_sync(void);
  * Returns the number of bytes needed (excluding the terminator) or -1. */
 int aoship_attest_determinism(char *buf, int len);
 
+/* B3Hash::hash (adapteros-core, crate blake3 1.8.3): the 32-byte BLAKE3 hash of len bytes,
+ * computed on the host with the same compression and tree code the router kernel uses for
+ * decision hashes. Returns 0 / -1. */
+int aoship_blake3(const void *data, size_t len, uint8_t *out);
+
 /* ---- router ---------------------------------------------------------------------------------- */
 
 /* Router::new_with_weights(k, tau, eps) + set_routing_bias (crates/adapteros-lora-router/src/
@@ -91,18 +96,70 @@ aoship_router_t *aoship_router_new(int n_adapters, int k, float tau, float eps,
  * nonzero = allowed; NULL = allow all. Returns 0 / -1. */
 int aoship_router_set_policy_mask(aoship_router_t *router, const uint8_t *allowed);
 
+/* Scope hint of Router::route_with_adapter_info_and_scope_with_ctx (router.rs:1587-1602):
+ * in_scope[n] host bytes, nonzero where AdapterInfo::scope_path equals the hint; the other
+ * adapters score from a prior of -1e9 (the decision hash, when on, sees those priors). The
+ * reference ignores a hint that matches no adapter: pass NULL then, as for no hint. */
+int aoship_router_set_scope(aoship_router_t *router, const uint8_t *in_scope);
+
+/* Adaptive routing (Router::set_adaptive_routing, router.rs:577; tie-breakers :1705-1724):
+ * seed[32] = DeterminismContext::router_tiebreak_seed() (adapteros-core/src/determinism.rs:
+ * 172-176). Adapter a gets breaker_a, the a-th ChaCha20Rng::from_seed(seed).gen::<u64>()
+ * (rand 0.8.5, rand_chacha 0.3.1), and equal scores are ordered by (breaker, stable_id, index)
+ * (sort_scores_adaptive, router.rs:265-306); the canonical re-sort keeps stable_id. NULL = back
+ * to deterministic mode. Returns 0 / -1. */
+int aoship_router_set_adaptive_seed(aoship_router_t *router, const uint8_t *seed);
+
+/* The breakers of aoship_router_set_adaptive_seed, computed on the host (no device needed):
+ * out[a] = the a-th ChaCha20Rng::from_seed(seed).gen::<u64>() for a < n, what the reference
+ * reports in its tie-break diagnostics (router.rs:1780-1800). Returns 0 / -1. */
+int aoship_adaptive_tie_breakers(const uint8_t *seed, int n, uint64_t *out);
+
+/* filter_decision_by_policy (crates/adapteros-lora-router/src/policy_mask.rs:221-355) on every
+ * decision before its ring is written: allowed[n] host bytes, nonzero where the adapter passes the
+ * RoutingPolicy's id and cluster allow/deny sets; max_adapters_per_token < 0 = no cap. Entries
+ * keep decision order; when any is removed the gates are renormalised (renormalize_gates_q15,
+ * :164-213). No entry left (or a cap of 0) is AosError::PolicyViolation: status -2. NULL allowed
+ * = no policy. Returns 0 / -1. */
+int aoship_router_set_decision_policy(aoship_router_t *router, const uint8_t *allowed,
+                                      int max_adapters_per_token);
+
+/* Decision -> ring as decision_to_router_ring_with_active_ids_and_strengths
+ * (crates/adapteros-lora-worker/src/router_bridge.rs:137-186): ring index = active_ids[decision
+ * index] (NULL = the decision index; 65535 zero-fills the ring as set_with_max_adapter does),
+ * gate = round(gate * clamp(strengths[decision index], 0, 1)) (NULL = unscaled). Host arrays of
+ * n_adapters entries. Returns 0 / -1. */
+int aoship_router_set_ring_mapping(aoship_router_t *router, const uint16_t *active_ids,
+                                   const float *strengths);
+
+/* RouterDeterminismConfig::enable_decision_hashing (router.rs:1879-1890): with hashes != NULL,
+ * each later route call writes, for token t, 96 bytes at hashes + 96 t: the input, output and
+ * combined BLAKE3 hashes of Router::compute_decision_hash (router.rs:1427-1484) for the router's
+ * decision (before any decision policy) with an empty feature vector:
+ *   input    = BLAKE3(the routed priors, float32 LE [|| reasoning_hash])
+ *   output   = BLAKE3(indices u16 LE || gates i16 LE [|| reasoning_hash])
+ *   combined = BLAKE3(input || output [|| reasoning_hash] [|| backend_identity_hash])
+ * 96 zero bytes for a token without a decision (the reference's decision_hash: None). DecisionHash
+ * reports the first 8 bytes of each as hex (B3Hash::to_short_hex). hashes: device buffer of
+ * max_tokens * 96 bytes, used until this is called again; reasoning_hash / backend_identity_hash:
+ * 32-byte host hashes or NULL. hashes == NULL turns hashing off. Returns 0 / -1. */
+int aoship_router_set_decision_hashing(aoship_router_t *router, uint8_t *hashes, int max_tokens,
+                                       const uint8_t *reasoning_hash,
+                                       const uint8_t *backend_identity_hash);
+
 /* Stream (hipStream_t) for this router's launches; NULL = null stream. Returns 0 / -1. */
 int aoship_router_set_stream(aoship_router_t *router, void *stream);
 
 void aoship_router_free(aoship_router_t *router);
 
-/* Route T tokens, deterministic mode, empty feature vector: the replacement for
+/* Route T tokens with an empty feature vector: the replacement for
  * Router::route_with_adapter_info_and_scope_with_ctx (router.rs:1567-1952) followed by
- * Decision -> RouterRing (types.rs:699-706, kernel-api lib.rs:122-193).
+ * Decision -> RouterRing (types.rs:699-706, kernel-api lib.rs:122-193), with the extras set above.
  *   priors  : device float[T * n_adapters]
  *   rings   : device aoship_ring_t[T] (written)
  *   status  : device int32[T] or NULL; 0 = decision written, -1 = non-finite prior or score
- *             (AosError::DeterminismViolation, router.rs:611-625,1640-1686), ring zero-filled.
+ *             (AosError::DeterminismViolation, router.rs:611-625,1640-1686), -2 = decision
+ *             policy left no adapter (AosError::PolicyViolation); ring zero-filled on -1 / -2.
  * Asynchronous. Returns 0 / -1 (argument errors only). */
 int aoship_route(aoship_router_t *router, const float *priors, int T, aoship_ring_t *rings,
                  int32_t *status);

@@ -89,14 +89,17 @@ int16_t orc_quantize_gate(float gate) {
 typedef struct {
   int idx;
   float score;
+  uint64_t breaker; /* adaptive mode only; 0 for every candidate otherwise */
   uint64_t stable_id;
 } orc_cand_t;
 
 /* router.rs:234-264 comparator: score DESC (total_cmp), stable_id ASC; Rust's sort_by is stable,
- * so remaining ties keep index order — made explicit here as the last key. */
+ * so remaining ties keep index order — made explicit here as the last key. Adaptive mode
+ * (sort_scores_adaptive, router.rs:265-306) puts the seeded breaker between score and stable_id. */
 static int cmp_scored(const orc_cand_t *a, const orc_cand_t *b) {
   uint64_t ka = orc_total_cmp_key_desc(a->score), kb = orc_total_cmp_key_desc(b->score);
   if (ka != kb) return ka < kb ? -1 : 1;
+  if (a->breaker != b->breaker) return a->breaker < b->breaker ? -1 : 1;
   if (a->stable_id != b->stable_id) return a->stable_id < b->stable_id ? -1 : 1;
   if (a->idx != b->idx) return a->idx < b->idx ? -1 : 1;
   return 0;
@@ -175,6 +178,13 @@ static float rust_f32_max(float a, float b) {
 int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
                   int k, float tau, float eps, float routing_bias, uint16_t idx_out[8],
                   int16_t q15_out[8]) {
+  return orc_route_one_ex(priors, n, stable_id, allowed, NULL, NULL, k, tau, eps, routing_bias, idx_out,
+                          q15_out);
+}
+
+int orc_route_one_ex(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
+                     const uint8_t *scope, const uint64_t *breakers, int k, float tau, float eps,
+                     float routing_bias, uint16_t idx_out[8], int16_t q15_out[8]) {
   for (int i = 0; i < 8; ++i) {
     idx_out[i] = 0;
     q15_out[i] = 0;
@@ -196,8 +206,10 @@ int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const u
   for (int i = 0; i < n; ++i) {
     if (allowed && !allowed[i]) continue;
     /* router.rs:1664-1676 with empty features (feature score 0.0, :985-988), no orthogonal
-     * penalty (0.0, :1490-1501), not MoE, version_weight 1.0 (types.rs:656). */
-    float sim = (priors[i] + 0.0f) - 0.0f;
+     * penalty (0.0, :1490-1501), not MoE, version_weight 1.0 (types.rs:656). A scope hint
+     * (router.rs:1587-1602) replaces the priors outside the scope with -1e9 first. */
+    const float prior = (scope && !scope[i]) ? -1.0e9f : priors[i];
+    float sim = (prior + 0.0f) - 0.0f;
     float score = sim * routing_bias; /* scoring.rs:35-37 */
     score *= 1.0f;                    /* clamp(version_weight, 0, 2) with the default 1.0 */
     if (!isfinite(score)) {
@@ -206,6 +218,7 @@ int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const u
     }
     c[m].idx = i;
     c[m].score = score;
+    c[m].breaker = breakers ? breakers[i] : 0;
     c[m].stable_id = stable_id ? stable_id[i] : 0;
     ++m;
   }
@@ -283,6 +296,362 @@ int orc_route_batch(const float *priors, int T, int n, const uint64_t *stable_id
   }
   if (bad_token) *bad_token = bad;
   return bad < 0 ? 0 : -1;
+}
+
+/* renormalize_gates_q15 (crates/adapteros-lora-router/src/policy_mask.rs:164-213). */
+void orc_renormalize_q15(const int16_t *q, int n, int16_t *out) {
+  if (n <= 0) return;
+  if (n == 1) {
+    out[0] = orc_quantize_gate(1.0f);
+    return;
+  }
+  const double denom = (double)ORC_Q15_DENOM;
+  double sum = 0.0, c = 0.0, g[ORC_MAX_K];
+  for (int i = 0; i < n; ++i) {
+    g[i] = (double)q[i] / denom;
+    double y = g[i] - c;
+    double t = sum + y;
+    c = (t - sum) - y;
+    sum = t;
+  }
+  if (sum > 0.0) {
+    for (int i = 0; i < n; ++i) out[i] = orc_quantize_gate((float)(g[i] / sum));
+  } else {
+    float u = 1.0f / (float)n;
+    for (int i = 0; i < n; ++i) out[i] = orc_quantize_gate(u);
+  }
+}
+
+/* filter_decision_by_policy (policy_mask.rs:221-355), the id and cluster sets reduced to
+ * allowed[n] (nonzero = passes). Returns the new length or -2 (AosError::PolicyViolation). */
+int orc_filter_decision(const uint16_t *idx, const int16_t *q, int kk, const uint8_t *allowed,
+                        int max_per_token, uint16_t *idx_out, int16_t *q_out) {
+  uint16_t fi[ORC_MAX_K];
+  int16_t fq[ORC_MAX_K];
+  int m = 0;
+  for (int i = 0; i < kk; ++i) {
+    if (!allowed[idx[i]]) continue;
+    fi[m] = idx[i];
+    fq[m] = q[i];
+    ++m;
+  }
+  if (max_per_token >= 0) {
+    if (max_per_token == 0) return -2; /* :318-322 */
+    if (m > max_per_token) m = max_per_token;
+  }
+  if (m == 0) return -2; /* :330-337 */
+  if (m < kk) {
+    orc_renormalize_q15(fq, m, q_out); /* :339-345, only when something was removed */
+  } else {
+    for (int i = 0; i < m; ++i) q_out[i] = fq[i];
+  }
+  for (int i = 0; i < m; ++i) idx_out[i] = fi[i];
+  return m;
+}
+
+/* decision_to_router_ring_with_active_ids_and_strengths
+ * (crates/adapteros-lora-worker/src/router_bridge.rs:137-186). active_ids (NULL = identity) and
+ * strengths (NULL = none) have n_active entries. Returns 0, or -1 for a decision index outside
+ * the active set (AosError::Routing). */
+int orc_decision_to_ring(const uint16_t *idx, const int16_t *q, int kk, const uint16_t *active_ids,
+                         const float *strengths, int n_active, int position, orc_ring_t *ring) {
+  uint16_t mapped[ORC_MAX_K];
+  for (int i = 0; i < kk; ++i) {
+    if (active_ids && idx[i] >= n_active) return -1;
+    mapped[i] = active_ids ? active_ids[idx[i]] : idx[i];
+  }
+  memset(ring, 0, sizeof(*ring));
+  ring->current_pos = (uint32_t)position;
+  /* RouterRing::set_with_max_adapter(mapped, gates, u16::MAX), release build (lib.rs:122-193) */
+  int zero = 0;
+  for (int i = 0; i < kk; ++i) zero |= mapped[i] >= 0xFFFFu;
+  if (!zero) {
+    for (int i = 0; i < kk; ++i) {
+      ring->adapter_indices[i] = mapped[i];
+      ring->gates_q15[i] = q[i];
+    }
+    ring->top_k = (uint32_t)kk;
+  }
+  if (strengths) {
+    for (int slot = 0; slot < kk; ++slot) {
+      float s = idx[slot] < n_active ? strengths[idx[slot]] : 1.0f; /* unwrap_or(1.0) */
+      /* f32::clamp keeps NaN; NaN * q rounds to NaN, and `as i16` maps NaN to 0 */
+      if (s == s) s = s < 0.0f ? 0.0f : (s > 1.0f ? 1.0f : s);
+      float v = roundf((float)ring->gates_q15[slot] * s);
+      int32_t iv;
+      if (v != v) iv = 0;
+      else if (v >= 32767.0f) iv = 32767;
+      else if (v <= -32768.0f) iv = -32768;
+      else iv = (int32_t)v;
+      if (iv > ORC_Q15_MAX) iv = ORC_Q15_MAX;
+      if (iv < -ORC_Q15_MAX) iv = -ORC_Q15_MAX;
+      ring->gates_q15[slot] = (int16_t)iv;
+    }
+  }
+  return 0;
+}
+
+/* What one device routing call produces per token: route, then (policy) filter, then the ring.
+ * status[t]: 0, -1 (DeterminismViolation: ring zero) or -2 (PolicyViolation: ring zero). */
+void orc_route_batch_ex(const float *priors, int T, int n, const uint64_t *stable_id,
+                        const uint8_t *allowed, const uint8_t *scope, const uint64_t *breakers, int k,
+                        float tau, float eps, float routing_bias, const uint8_t *post_allowed,
+                        int post_max, const uint16_t *active_ids, const float *strengths,
+                        orc_ring_t *rings, int32_t *status) {
+  for (int t = 0; t < T; ++t) {
+    uint16_t idx[ORC_MAX_K], fi[ORC_MAX_K];
+    int16_t q[ORC_MAX_K], fq[ORC_MAX_K];
+    orc_ring_t *r = &rings[t];
+    memset(r, 0, sizeof(*r));
+    int kk = orc_route_one_ex(priors + (size_t)t * n, n, stable_id, allowed, scope, breakers, k, tau,
+                              eps, routing_bias, idx, q);
+    if (kk < 0) {
+      status[t] = -1;
+      continue;
+    }
+    if (post_allowed) {
+      kk = orc_filter_decision(idx, q, kk, post_allowed, post_max, fi, fq);
+      if (kk < 0) {
+        status[t] = -2;
+        continue;
+      }
+      memcpy(idx, fi, sizeof(idx));
+      memcpy(q, fq, sizeof(q));
+    }
+    orc_decision_to_ring(idx, q, kk, active_ids, strengths, n, t, r);
+    status[t] = 0;
+  }
+}
+
+/* ChaCha20 block function, RFC 8439 section 2.3: twenty rounds of quarter rounds over the 16
+ * input words (columns then diagonals), the input added to the result. */
+void orc_chacha20_block(const uint32_t in[16], uint32_t out[16]) {
+#define ORC_ROTL(v, c) (((v) << (c)) | ((v) >> (32 - (c))))
+#define ORC_QR(a, b, c, d)                                      \
+  x[a] += x[b]; x[d] ^= x[a]; x[d] = ORC_ROTL(x[d], 16);        \
+  x[c] += x[d]; x[b] ^= x[c]; x[b] = ORC_ROTL(x[b], 12);        \
+  x[a] += x[b]; x[d] ^= x[a]; x[d] = ORC_ROTL(x[d], 8);         \
+  x[c] += x[d]; x[b] ^= x[c]; x[b] = ORC_ROTL(x[b], 7);
+  uint32_t x[16];
+  for (int i = 0; i < 16; ++i) x[i] = in[i];
+  for (int round = 0; round < 20; round += 2) {
+    ORC_QR(0, 4, 8, 12) ORC_QR(1, 5, 9, 13) ORC_QR(2, 6, 10, 14) ORC_QR(3, 7, 11, 15)
+    ORC_QR(0, 5, 10, 15) ORC_QR(1, 6, 11, 12) ORC_QR(2, 7, 8, 13) ORC_QR(3, 4, 9, 14)
+  }
+  for (int i = 0; i < 16; ++i) out[i] = x[i] + in[i];
+#undef ORC_QR
+#undef ORC_ROTL
+}
+
+/* ChaCha20Rng::from_seed(seed) (rand_chacha 0.3.1) then n x gen::<u64>() (rand 0.8.5): the
+ * keystream of key = seed, 64-bit block counter from 0 (words 12-13), stream 0 (words 14-15),
+ * serialised little-endian; value a is bytes 8a .. 8a+7 of it, little-endian. */
+void orc_tie_breakers(const uint8_t seed[32], int n, uint64_t *out) {
+  uint8_t ks[64];
+  long have_block = -1;
+  for (int a = 0; a < n; ++a) {
+    uint64_t v = 0;
+    for (int byte = 7; byte >= 0; --byte) {
+      long pos = 8L * a + byte;
+      long blk = pos / 64;
+      if (blk != have_block) {
+        uint32_t st[16], o[16];
+        st[0] = 0x61707865u; /* "expa" */
+        st[1] = 0x3320646eu; /* "nd 3" */
+        st[2] = 0x79622d32u; /* "2-by" */
+        st[3] = 0x6b206574u; /* "te k" */
+        for (int w = 0; w < 8; ++w)
+          st[4 + w] = (uint32_t)seed[4 * w] | ((uint32_t)seed[4 * w + 1] << 8) |
+                      ((uint32_t)seed[4 * w + 2] << 16) | ((uint32_t)seed[4 * w + 3] << 24);
+        st[12] = (uint32_t)blk;
+        st[13] = (uint32_t)((uint64_t)blk >> 32);
+        st[14] = 0;
+        st[15] = 0;
+        orc_chacha20_block(st, o);
+        for (int w = 0; w < 16; ++w)
+          for (int b = 0; b < 4; ++b) ks[4 * w + b] = (uint8_t)(o[w] >> (8 * b));
+        have_block = blk;
+      }
+      v = (v << 8) | ks[pos % 64];
+    }
+    out[a] = v;
+  }
+}
+
+/* ---- BLAKE3 (the specification's incremental hasher, byte oriented) ---------------------------- */
+
+static const uint32_t B3_IV[8] = {0x6A09E667u, 0xBB67AE85u, 0x3C6EF372u, 0xA54FF53Au,
+                                  0x510E527Fu, 0x9B05688Cu, 0x1F83D9ABu, 0x5BE0CD19u};
+static const int B3_PERM[16] = {2, 6, 3, 10, 7, 0, 4, 13, 1, 11, 12, 5, 9, 14, 15, 8};
+
+static uint32_t b3_rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
+
+/* compression: 7 rounds; round r reads message word sched[r][i], sched[0] = identity and
+ * sched[r+1][i] = sched[r][PERM[i]] */
+static void b3_compress(const uint32_t cv[8], const uint8_t block[64], uint32_t block_len, uint64_t counter,
+                        uint32_t flags, uint32_t out[16]) {
+  uint32_t m[16], v[16];
+  int sched[16], next[16];
+  for (int i = 0; i < 16; ++i) {
+    m[i] = (uint32_t)block[4 * i] | ((uint32_t)block[4 * i + 1] << 8) | ((uint32_t)block[4 * i + 2] << 16) |
+           ((uint32_t)block[4 * i + 3] << 24);
+    sched[i] = i;
+  }
+  for (int i = 0; i < 8; ++i) v[i] = cv[i];
+  for (int i = 0; i < 4; ++i) v[8 + i] = B3_IV[i];
+  v[12] = (uint32_t)(counter & 0xffffffffu);
+  v[13] = (uint32_t)(counter >> 32);
+  v[14] = block_len;
+  v[15] = flags;
+  static const int cols[8][4] = {{0, 4, 8, 12}, {1, 5, 9, 13}, {2, 6, 10, 14}, {3, 7, 11, 15},
+                                 {0, 5, 10, 15}, {1, 6, 11, 12}, {2, 7, 8, 13}, {3, 4, 9, 14}};
+  for (int r = 0; r < 7; ++r) {
+    for (int g = 0; g < 8; ++g) {
+      int a = cols[g][0], b = cols[g][1], c = cols[g][2], d = cols[g][3];
+      uint32_t x = m[sched[2 * g]], y = m[sched[2 * g + 1]];
+      v[a] = v[a] + v[b] + x;
+      v[d] = b3_rotr(v[d] ^ v[a], 16);
+      v[c] = v[c] + v[d];
+      v[b] = b3_rotr(v[b] ^ v[c], 12);
+      v[a] = v[a] + v[b] + y;
+      v[d] = b3_rotr(v[d] ^ v[a], 8);
+      v[c] = v[c] + v[d];
+      v[b] = b3_rotr(v[b] ^ v[c], 7);
+    }
+    for (int i = 0; i < 16; ++i) next[i] = sched[B3_PERM[i]];
+    for (int i = 0; i < 16; ++i) sched[i] = next[i];
+  }
+  for (int i = 0; i < 8; ++i) {
+    out[i] = v[i] ^ v[i + 8];
+    out[i + 8] = v[i + 8] ^ cv[i];
+  }
+}
+
+typedef struct {
+  uint32_t cv[8];
+  uint64_t counter;
+  uint8_t block[64];
+  uint32_t block_len;
+  uint32_t blocks_done;
+} b3_chunk_t;
+
+static void b3_chunk_init(b3_chunk_t *c, uint64_t counter) {
+  memcpy(c->cv, B3_IV, sizeof(B3_IV));
+  c->counter = counter;
+  memset(c->block, 0, 64);
+  c->block_len = 0;
+  c->blocks_done = 0;
+}
+
+static uint32_t b3_chunk_flags(const b3_chunk_t *c) { return c->blocks_done == 0 ? 1u : 0u; /* CHUNK_START */ }
+
+/* the chunk's final block compressed with CHUNK_END (and extra flags) */
+static void b3_chunk_output(const b3_chunk_t *c, uint32_t extra, uint32_t out[16]) {
+  b3_compress(c->cv, c->block, c->block_len, c->counter, b3_chunk_flags(c) | 2u | extra, out);
+}
+
+static void b3_parent_output(const uint32_t l[8], const uint32_t r[8], uint32_t extra, uint32_t out[16]) {
+  uint8_t blk[64];
+  for (int i = 0; i < 8; ++i)
+    for (int b = 0; b < 4; ++b) {
+      blk[4 * i + b] = (uint8_t)(l[i] >> (8 * b));
+      blk[32 + 4 * i + b] = (uint8_t)(r[i] >> (8 * b));
+    }
+  b3_compress(B3_IV, blk, 64, 0, 4u | extra, out);
+}
+
+void orc_blake3(const uint8_t *in, size_t len, uint8_t out[32]) {
+  uint32_t stack[64][8];
+  int depth = 0;
+  b3_chunk_t ch;
+  b3_chunk_init(&ch, 0);
+  size_t pos = 0;
+  while (pos < len) {
+    /* a full chunk followed by more input: push its chaining value, merging finished subtrees */
+    if (ch.blocks_done * 64 + ch.block_len == 1024) {
+      uint32_t o[16], cv[8];
+      b3_chunk_output(&ch, 0, o);
+      memcpy(cv, o, sizeof(cv));
+      const uint64_t next_counter = ch.counter + 1;
+      uint64_t total = next_counter; /* chunks completed so far */
+      while ((total & 1) == 0) {
+        b3_parent_output(stack[--depth], cv, 0, o);
+        memcpy(cv, o, sizeof(cv));
+        total >>= 1;
+      }
+      memcpy(stack[depth++], cv, sizeof(cv));
+      b3_chunk_init(&ch, next_counter);
+    }
+    /* a full block followed by more input: compress it */
+    if (ch.block_len == 64) {
+      uint32_t o[16];
+      b3_compress(ch.cv, ch.block, 64, ch.counter, b3_chunk_flags(&ch), o);
+      memcpy(ch.cv, o, 32);
+      ch.blocks_done++;
+      memset(ch.block, 0, 64);
+      ch.block_len = 0;
+    }
+    ch.block[ch.block_len++] = in[pos++];
+  }
+  uint32_t o[16];
+  if (depth == 0) {
+    b3_chunk_output(&ch, 8u /* ROOT */, o);
+  } else {
+    uint32_t cv[8];
+    b3_chunk_output(&ch, 0, o);
+    memcpy(cv, o, sizeof(cv));
+    while (depth > 0) {
+      --depth;
+      b3_parent_output(stack[depth], cv, depth == 0 ? 8u : 0u, o);
+      memcpy(cv, o, sizeof(cv));
+    }
+  }
+  for (int i = 0; i < 32; ++i) out[i] = (uint8_t)(o[i / 4] >> (8 * (i % 4)));
+}
+
+/* Router::compute_decision_hash (router.rs:1427-1484) with an empty feature vector: out[0..32) =
+ * BLAKE3(priors LE [|| reasoning]), out[32..64) = BLAKE3(indices u16 LE || gates i16 LE
+ * [|| reasoning]), out[64..96) = BLAKE3(input || output [|| reasoning] [|| backend]). */
+void orc_decision_hash(const float *priors, int n, const uint16_t *idx, const int16_t *q, int kk,
+                       const uint8_t *reasoning, const uint8_t *backend, uint8_t out[96]) {
+  size_t inl = (size_t)n * 4 + (reasoning ? 32 : 0);
+  uint8_t *buf = (uint8_t *)malloc(inl > 160 ? inl : 160);
+  for (int i = 0; i < n; ++i) {
+    uint32_t b = f32_bits(priors[i]);
+    for (int j = 0; j < 4; ++j) buf[4 * i + j] = (uint8_t)(b >> (8 * j));
+  }
+  if (reasoning) memcpy(buf + (size_t)n * 4, reasoning, 32);
+  orc_blake3(buf, inl, out);
+  size_t ol = 0;
+  for (int i = 0; i < kk; ++i) {
+    buf[ol++] = (uint8_t)(idx[i] & 0xff);
+    buf[ol++] = (uint8_t)(idx[i] >> 8);
+  }
+  for (int i = 0; i < kk; ++i) {
+    uint16_t g = (uint16_t)q[i];
+    buf[ol++] = (uint8_t)(g & 0xff);
+    buf[ol++] = (uint8_t)(g >> 8);
+  }
+  if (reasoning) {
+    memcpy(buf + ol, reasoning, 32);
+    ol += 32;
+  }
+  orc_blake3(buf, ol, out + 32);
+  size_t cl = 0;
+  memcpy(buf + cl, out, 32);
+  cl += 32;
+  memcpy(buf + cl, out + 32, 32);
+  cl += 32;
+  if (reasoning) {
+    memcpy(buf + cl, reasoning, 32);
+    cl += 32;
+  }
+  if (backend) {
+    memcpy(buf + cl, backend, 32);
+    cl += 32;
+  }
+  orc_blake3(buf, cl, out + 64);
+  free(buf);
 }
 
 void orc_priors(const float *features, const float *router_w, int T, int n, int d, float *priors) {

@@ -41,10 +41,24 @@
  *                      tolerance only.
  *   orc_priors         defines the router-logit GEMV of the synthetic workloads (the
  *                      reference takes priors as an input); pinned by a float64 evaluation.
+ *   orc_route_one_ex / orc_renormalize_q15 / orc_filter_decision / orc_decision_to_ring
+ *                      (router extras: scope hint, adaptive tie-breakers, decision policy,
+ *                      active ids and strengths) pinned by the reference's policy_mask.rs and
+ *                      router_bridge.rs tests, worker_enforcement_tests.rs, exact rational
+ *                      arithmetic for renormalisation, and brute force over tie orders.
+ *   orc_blake3 / orc_decision_hash
+ *                      pinned by the BLAKE3 hashes the reference holds (B3Hash of "" and of
+ *                      "hello world"; the BLAKE3 checksums of its source files in
+ *                      sbom/cargo-sbom.json, multi-chunk inputs) and by the specification's
+ *                      known answer for "abc".
+ *   orc_chacha20_block / orc_tie_breakers
+ *                      pinned by the RFC 8439 block-function test vectors (section 2.3.2 and
+ *                      appendix A.1) and by sorting against the breakers on ties.
  */
 #ifndef AOS_ORACLE_H
 #define AOS_ORACLE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -69,6 +83,46 @@ uint64_t orc_total_cmp_key_desc(float x);
 int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
                   int k, float tau, float eps, float routing_bias, uint16_t idx_out[8],
                   int16_t q15_out[8]);
+
+/* orc_route_one with the router extras: scope[n] (NULL = no hint) replaces the priors of
+ * adapters outside the scope with -1e9 (router.rs:1587-1602); breakers[n] (NULL = deterministic
+ * mode) order equal scores before stable_id (sort_scores_adaptive, router.rs:265-306). */
+int orc_route_one_ex(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
+                     const uint8_t *scope, const uint64_t *breakers, int k, float tau, float eps,
+                     float routing_bias, uint16_t idx_out[8], int16_t q15_out[8]);
+
+/* renormalize_gates_q15 (policy_mask.rs:164-213): out[n]. */
+void orc_renormalize_q15(const int16_t *q, int n, int16_t *out);
+
+/* filter_decision_by_policy (policy_mask.rs:221-355) over a decision of kk entries with the
+ * policy's id/cluster sets as allowed[n] and max_per_token (< 0 = no cap). Returns the new length
+ * or -2 (PolicyViolation). */
+int orc_filter_decision(const uint16_t *idx, const int16_t *q, int kk, const uint8_t *allowed,
+                        int max_per_token, uint16_t *idx_out, int16_t *q_out);
+
+/* decision_to_router_ring_with_active_ids_and_strengths (router_bridge.rs:137-186). Returns 0
+ * or -1 (AosError::Routing). */
+int orc_decision_to_ring(const uint16_t *idx, const int16_t *q, int kk, const uint16_t *active_ids,
+                         const float *strengths, int n_active, int position, orc_ring_t *ring);
+
+/* Route + policy filter + ring conversion for T tokens; status[t] = 0, -1 or -2. */
+void orc_route_batch_ex(const float *priors, int T, int n, const uint64_t *stable_id,
+                        const uint8_t *allowed, const uint8_t *scope, const uint64_t *breakers, int k,
+                        float tau, float eps, float routing_bias, const uint8_t *post_allowed,
+                        int post_max, const uint16_t *active_ids, const float *strengths,
+                        orc_ring_t *rings, int32_t *status);
+
+/* ChaCha20 block function (RFC 8439 section 2.3) and the adaptive tie-breakers
+ * ChaCha20Rng::from_seed(seed).gen::<u64>() x n (rand_chacha 0.3.1, rand 0.8.5). */
+void orc_chacha20_block(const uint32_t in[16], uint32_t out[16]);
+void orc_tie_breakers(const uint8_t seed[32], int n, uint64_t *out);
+
+/* BLAKE3 (B3Hash::hash; crate blake3 1.8.3) of len bytes, and Router::compute_decision_hash
+ * (router.rs:1427-1484) for an empty feature vector: out[96] = input, output, combined hashes.
+ * reasoning / backend: 32-byte hashes or NULL. */
+void orc_blake3(const uint8_t *in, size_t len, uint8_t out[32]);
+void orc_decision_hash(const float *priors, int n, const uint16_t *idx, const int16_t *q, int kk,
+                       const uint8_t *reasoning, const uint8_t *backend, uint8_t out[96]);
 
 /* Route T tokens (priors[T*n]) into rings[T]. Returns 0 or -1 (first failing token in *bad_token). */
 int orc_route_batch(const float *priors, int T, int n, const uint64_t *stable_id,

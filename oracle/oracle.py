@@ -49,6 +49,25 @@ def lib():
         L.orc_route_one.argtypes = [P, C.c_int, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
         L.orc_route_batch.restype = C.c_int
         L.orc_route_batch.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
+        L.orc_route_one_ex.restype = C.c_int
+        L.orc_route_one_ex.argtypes = [P, C.c_int, P, P, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
+        L.orc_renormalize_q15.restype = None
+        L.orc_renormalize_q15.argtypes = [P, C.c_int, P]
+        L.orc_filter_decision.restype = C.c_int
+        L.orc_filter_decision.argtypes = [P, P, C.c_int, P, C.c_int, P, P]
+        L.orc_decision_to_ring.restype = C.c_int
+        L.orc_decision_to_ring.argtypes = [P, P, C.c_int, P, P, C.c_int, C.c_int, P]
+        L.orc_route_batch_ex.restype = None
+        L.orc_route_batch_ex.argtypes = [P, C.c_int, C.c_int, P, P, P, P, C.c_int, C.c_float, C.c_float,
+                                         C.c_float, P, C.c_int, P, P, P, P]
+        L.orc_chacha20_block.restype = None
+        L.orc_chacha20_block.argtypes = [P, P]
+        L.orc_tie_breakers.restype = None
+        L.orc_tie_breakers.argtypes = [P, C.c_int, P]
+        L.orc_blake3.restype = None
+        L.orc_blake3.argtypes = [P, C.c_size_t, P]
+        L.orc_decision_hash.restype = None
+        L.orc_decision_hash.argtypes = [P, C.c_int, P, P, C.c_int, P, P, P]
         L.orc_priors.restype = None
         L.orc_priors.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P]
         L.orc_dequant_q4.restype = None
@@ -115,6 +134,114 @@ def route_batch(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None,
                           al.ctypes.data if al is not None else None, k, tau, eps, routing_bias,
                           rings.ctypes.data, C.byref(bad))
     return rings
+
+
+def _opt(a, dtype):
+    return None if a is None else _c(a, dtype)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def route_one_ex(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None, allowed=None,
+                 scope=None, breakers=None):
+    """route_one with a scope hint (bytes per adapter) and adaptive tie-breakers (u64 per adapter)."""
+    p = _c(priors, np.float32)
+    arrs = [_opt(stable_ids, np.uint64), _opt(allowed, np.uint8), _opt(scope, np.uint8), _opt(breakers, np.uint64)]
+    idx = np.zeros(8, np.uint16)
+    q = np.zeros(8, np.int16)
+    kk = lib().orc_route_one_ex(p.ctypes.data, p.shape[0], *[_ptr(a) for a in arrs], k, tau, eps, routing_bias,
+                                idx.ctypes.data, q.ctypes.data)
+    if kk < 0:
+        raise ValueError("routing error (non-finite prior/score or k > 8)")
+    return idx[:kk].tolist(), q[:kk].tolist()
+
+
+def renormalize_q15(gates) -> list[int]:
+    g = _c(gates, np.int16)
+    out = np.zeros(max(len(g), 1), np.int16)
+    lib().orc_renormalize_q15(g.ctypes.data, len(g), out.ctypes.data)
+    return out[:len(g)].tolist()
+
+
+def filter_decision(indices, gates, allowed, max_per_token=-1):
+    """(indices, gates) after the policy filter; raises PermissionError for a PolicyViolation."""
+    i = _c(indices, np.uint16)
+    g = _c(gates, np.int16)
+    al = _c(allowed, np.uint8)
+    oi = np.zeros(8, np.uint16)
+    og = np.zeros(8, np.int16)
+    m = lib().orc_filter_decision(i.ctypes.data, g.ctypes.data, len(i), al.ctypes.data, max_per_token,
+                                  oi.ctypes.data, og.ctypes.data)
+    if m < 0:
+        raise PermissionError("PolicyViolation: routing policy denied all adapters")
+    return oi[:m].tolist(), og[:m].tolist()
+
+
+def decision_to_ring(indices, gates, active_ids=None, strengths=None, n_active=None, position=0):
+    i = _c(indices, np.uint16)
+    g = _c(gates, np.int16)
+    a = _opt(active_ids, np.uint16)
+    s = _opt(strengths, np.float32)
+    n = n_active if n_active is not None else (len(a) if a is not None else (len(s) if s is not None else 65536))
+    ring = np.zeros(1, RING_DTYPE)
+    rc = lib().orc_decision_to_ring(i.ctypes.data, g.ctypes.data, len(i), _ptr(a), _ptr(s), n, position,
+                                    ring.ctypes.data)
+    if rc < 0:
+        raise LookupError("Routing: decision index not in active set")
+    return ring[0]
+
+
+def route_batch_ex(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None, allowed=None, scope=None,
+                   breakers=None, post_allowed=None, post_max=-1, active_ids=None, strengths=None):
+    """(rings, status) of one device routing call with the router extras."""
+    p = _c(priors, np.float32)
+    T, n = p.shape
+    arrs = [_opt(stable_ids, np.uint64), _opt(allowed, np.uint8), _opt(scope, np.uint8), _opt(breakers, np.uint64)]
+    post = [_opt(post_allowed, np.uint8)]
+    tail = [_opt(active_ids, np.uint16), _opt(strengths, np.float32)]
+    rings = np.zeros(T, RING_DTYPE)
+    status = np.zeros(T, np.int32)
+    lib().orc_route_batch_ex(p.ctypes.data, T, n, *[_ptr(a) for a in arrs], k, tau, eps, routing_bias,
+                             _ptr(post[0]), post_max, *[_ptr(a) for a in tail], rings.ctypes.data,
+                             status.ctypes.data)
+    return rings, status
+
+
+def chacha20_block(words) -> list[int]:
+    w = _c(words, np.uint32)
+    out = np.zeros(16, np.uint32)
+    lib().orc_chacha20_block(w.ctypes.data, out.ctypes.data)
+    return out.tolist()
+
+
+def tie_breakers(seed: bytes, n: int) -> np.ndarray:
+    sd = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+    assert sd.size == 32
+    out = np.zeros(max(n, 1), np.uint64)
+    lib().orc_tie_breakers(sd.ctypes.data, n, out.ctypes.data)
+    return out[:n]
+
+
+def blake3(data: bytes) -> bytes:
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    out = np.zeros(32, np.uint8)
+    lib().orc_blake3(buf.ctypes.data, len(data), out.ctypes.data)
+    return out.tobytes()
+
+
+def decision_hash(priors, indices, gates, reasoning: bytes | None = None, backend: bytes | None = None) -> bytes:
+    """96 bytes: the input, output and combined hashes of Router::compute_decision_hash."""
+    p = _c(priors, np.float32)
+    i = _c(indices, np.uint16) if len(indices) else np.zeros(1, np.uint16)
+    g = _c(gates, np.int16) if len(gates) else np.zeros(1, np.int16)
+    r = None if reasoning is None else np.frombuffer(reasoning, np.uint8).copy()
+    b = None if backend is None else np.frombuffer(backend, np.uint8).copy()
+    out = np.zeros(96, np.uint8)
+    lib().orc_decision_hash(p.ctypes.data, p.shape[0], i.ctypes.data, g.ctypes.data, len(indices), _ptr(r), _ptr(b),
+                            out.ctypes.data)
+    return out.tobytes()
 
 
 def priors(features, router_w):
