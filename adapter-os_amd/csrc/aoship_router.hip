@@ -180,30 +180,25 @@ __device__ __noinline__ void decision_hash(uint8_t *hashes, const float *priors,
   }
 }
 
-/* renormalize_gates_q15 (policy_mask.rs:164-213): one gate -> 32767; otherwise g = q / 32767 in
- * float64 with Kahan summation in order, q' = quantize(float(g / sum)), or the float32 uniform
- * 1/n quantised when the sum is 0. */
-__device__ __forceinline__ void renormalize_q15(int (&q)[8], int n) {
-  if (n == 1) {
-    q[0] = 32767;
-    return;
-  }
-  double g[8];
+/* renormalize_gates_q15 (policy_mask.rs:164-213) with gate s in lane s < n: one gate -> 32767;
+ * otherwise g = q / 32767 in float64 summed with Kahan in slot order, q' = quantize(float(g / sum)),
+ * or the float32 uniform 1/n quantised when the sum is 0. Returns this lane's new gate. */
+__device__ __forceinline__ int renormalize_q15_lane(int my_q, int n, int lane) {
+  if (n == 1) return lane == 0 ? 32767 : 0;
   double sum = 0.0, c = 0.0;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    g[s] = (double)q[s] / 32767.0;
+    const double g = (double)(int)aos_shfl((uint32_t)my_q, s) / 32767.0;
     if (s < n) {
-      const double y = g[s] - c;
+      const double y = g - c;
       const double tt = sum + y;
       c = (tt - sum) - y;
       sum = tt;
     }
   }
-  const float uni = 1.0f / (float)n;
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-    if (s < n) q[s] = sum > 0.0 ? quantize_q15((float)(g[s] / sum)) : quantize_q15(uni);
+  if (lane >= n) return 0;
+  const double mine = (double)my_q / 32767.0;
+  return sum > 0.0 ? quantize_q15((float)(mine / sum)) : quantize_q15(1.0f / (float)n);
 }
 
 /* Strength scaling (router_bridge.rs:168-186): round_half_away(q * clamp(strength, 0, 1)) as i16,
@@ -219,9 +214,17 @@ __device__ __forceinline__ int scale_gate(int q, float strength) {
   return (int)r;
 }
 
-template <bool LDS>
+/* X: the extras (scope, adaptive keys, decision policy, ring mapping, decision hashes) are
+ * compiled in; the X = false instance is the plain router, launched when none is set. */
+template <bool LDS, bool X>
 __device__ __forceinline__ void route_one(const aos_route_params &p, const float *priors, int t, int lane) {
   const int n = p.n;
+  const uint8_t *scope = X ? p.scope : nullptr;
+  const uint64_t *tie_key = X ? p.tie_key : nullptr;
+  const uint8_t *post_allowed = X ? p.post_allowed : nullptr;
+  const uint16_t *active_ids = X ? p.active_ids : nullptr;
+  const float *strengths = X ? p.strengths : nullptr;
+  uint8_t *hashes = X ? p.hashes : nullptr;
   /* every prior is checked for finiteness, allowed or not (validate_router_inputs); the chunked
    * passes below visit each index exactly once */
   bool bad = false;
@@ -235,14 +238,14 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     if (!__builtin_isfinite(raw)) bad = true;
     if (p.allowed && !p.allowed[i]) return false;
     /* scope hint (router.rs:1587-1602): adapters outside the scope score from -1e9 */
-    const float prior = (p.scope && !p.scope[i]) ? -1.0e9f : raw;
+    const float prior = (scope && !scope[i]) ? -1.0e9f : raw;
     float sim = (prior + 0.0f) - 0.0f;
     float score = sim * p.bias;
     score = score * 1.0f;
     if (!__builtin_isfinite(score)) bad = true;
     /* adaptive mode (sort_scores_adaptive, router.rs:265-306): the rank of (breaker, stable_id,
      * index) stands in for stable_id, which orders equal scores exactly as those three keys do */
-    uint64_t sid = p.tie_key ? p.tie_key[i] : (p.stable_id ? p.stable_id[i] : 0ull);
+    uint64_t sid = tie_key ? tie_key[i] : (p.stable_id ? p.stable_id[i] : 0ull);
     a = ((uint64_t)score_key_desc(score) << 32) | (sid >> 32);
     b = ((sid & 0xffffffffull) << 32) | (uint64_t)(uint32_t)i;
     return true;
@@ -291,12 +294,12 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
 
   aoship_ring_t *ring = p.rings + t;
   const bool any_bad = __ballot(bad) != 0ull;
-  const bool policy = p.post_allowed != nullptr;
+  const bool policy = post_allowed != nullptr;
   int kk = p.k < m_allowed ? p.k : m_allowed;
   if (any_bad || kk <= 0) {
     /* an empty decision under a decision policy is a PolicyViolation (policy_mask.rs:330-337) */
     ring_empty(ring, p.status, t, lane, any_bad ? -1 : (policy ? -2 : 0));
-    hash_empty(p.hashes, t, lane);
+    hash_empty(hashes, t, lane);
     return;
   }
 
@@ -312,7 +315,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     ssid[s] = ((a & 0xffffffffull) << 32) | (b >> 32);
     sidx[s] = (uint32_t)b;
   }
-  if (p.tie_key) {
+  if (tie_key) {
     /* the canonical re-sort keeps stable_id in adaptive mode (router.rs:1305-1325) */
 #pragma unroll
     for (int s = 0; s < 8; ++s) ssid[s] = (s < kk && p.stable_id) ? p.stable_id[sidx[s]] : 0ull;
@@ -364,7 +367,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     if (s < kk) S += g[s];
   if (!(S > 0.0f)) {
     ring_empty(ring, p.status, t, lane, policy ? -2 : 0);
-    hash_empty(p.hashes, t, lane);
+    hash_empty(hashes, t, lane);
     return;
   }
   int q[8];
@@ -388,104 +391,80 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     }
     rank[i] = r;
   }
-  /* the decision in canonical order, in every lane */
-  uint32_t didx[8];
-  int dq[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    didx[s] = 0;
-    dq[s] = 0;
-  }
+  /* lane s < kk holds decision entry s (canonical order) */
+  uint32_t my_i = 0;
+  int my_q = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-      if (i < kk && rank[i] == s) {
-        didx[s] = sidx[i];
-        dq[s] = q[i];
-      }
-  /* the decision hash belongs to the router's decision, before any policy filter */
-  if (p.hashes) {
-    /* kk indices (u16 LE) then kk gates (i16 LE), packed two halves to a word */
+    if (i < kk && rank[i] == lane) {
+      my_i = sidx[i];
+      my_q = q[i];
+    }
+  if (X && hashes) {
+    /* the decision hash belongs to the router's decision, before any policy filter: kk indices
+     * (u16 LE) then kk gates (i16 LE), packed two halves to a word */
     uint32_t hw[16];
 #pragma unroll
-    for (int pos = 0; pos < 16; ++pos) {
-      uint32_t v = 0;
+    for (int pos = 0; pos < 16; ++pos) hw[pos] = 0;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (s < kk && pos == s) v = didx[s] & 0xFFFFu;
-        if (s < kk && pos == kk + s) v = (uint32_t)(uint16_t)(int16_t)dq[s];
+    for (int s = 0; s < 8; ++s) {
+      const uint32_t is = aos_shfl(my_i, s) & 0xFFFFu;
+      const uint32_t qs = (uint32_t)(uint16_t)(int16_t)(int)aos_shfl((uint32_t)my_q, s);
+#pragma unroll
+      for (int pos = 0; pos < 16; ++pos) {
+        if (s < kk && pos == s) hw[pos] = is;
+        if (s < kk && pos == kk + s) hw[pos] = qs;
       }
-      hw[pos] = v;
     }
-    decision_hash(p.hashes, priors, p.scope, p.n, p.hash_extra, p.hash_reasoning, p.hash_backend, t, lane, kk,
-                  hw[0] | hw[1] << 16, hw[2] | hw[3] << 16, hw[4] | hw[5] << 16,
-                  hw[6] | hw[7] << 16, hw[8] | hw[9] << 16, hw[10] | hw[11] << 16, hw[12] | hw[13] << 16,
-                  hw[14] | hw[15] << 16);
+    decision_hash(hashes, priors, scope, p.n, p.hash_extra, p.hash_reasoning, p.hash_backend, t, lane, kk,
+                  hw[0] | hw[1] << 16, hw[2] | hw[3] << 16, hw[4] | hw[5] << 16, hw[6] | hw[7] << 16,
+                  hw[8] | hw[9] << 16, hw[10] | hw[11] << 16, hw[12] | hw[13] << 16, hw[14] | hw[15] << 16);
   }
   int m = kk;
-  if (policy) {
-    /* filter_decision_by_policy (policy_mask.rs:221-355): keep passing entries in decision
-     * order, cap at max_adapters_per_token, renormalise when anything was removed */
-    uint32_t fidx[8];
-    int fq[8];
-    int kept = 0;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      fidx[s] = 0;
-      fq[s] = 0;
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const bool keep = s < kk && p.post_allowed[didx[s]] != 0;
-#pragma unroll
-      for (int d = 0; d < 8; ++d)
-        if (keep && d == kept) {
-          fidx[d] = didx[s];
-          fq[d] = dq[s];
-        }
-      kept += keep ? 1 : 0;
-    }
+  if (X && policy) {
+    /* filter_decision_by_policy (policy_mask.rs:221-355): passing entries keep decision order,
+     * capped at max_adapters_per_token; anything removed renormalises the gates */
+    const bool keep = lane < kk && post_allowed[my_i] != 0;
+    const uint32_t km = (uint32_t)__ballot(keep) & 0xFFu;
+    int kept = __popc(km);
     if (p.post_max >= 0 && kept > p.post_max) kept = p.post_max;
     if (kept == 0) {
       ring_empty(ring, p.status, t, lane, -2);
       return;
     }
-    if (kept < kk) renormalize_q15(fq, kept);
+    /* slot s takes the s-th passing entry */
+    int src = 0;
+    uint32_t rest = km;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      didx[s] = s < kept ? fidx[s] : 0u;
-      dq[s] = s < kept ? fq[s] : 0;
+      const int b = rest ? __ffs(rest) - 1 : 0;
+      if (s == lane) src = b;
+      rest &= rest - 1u;
     }
+    my_i = aos_shfl(my_i, src);
+    my_q = (int)aos_shfl((uint32_t)my_q, src);
+    if (lane >= kept) {
+      my_i = 0;
+      my_q = 0;
+    }
+    if (kept < kk) my_q = renormalize_q15_lane(my_q, kept, lane);
     m = kept;
   }
   /* decision_to_router_ring_with_active_ids_and_strengths (router_bridge.rs:137-186) */
-  bool zero_fill = false;
-  uint32_t ridx[8];
-  int rq[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    ridx[s] = (s < m && p.active_ids) ? (uint32_t)p.active_ids[didx[s]] : didx[s];
+  uint32_t oi = my_i;
+  int oq = my_q;
+  if (X && (active_ids || strengths)) {
+    if (lane < m && active_ids) oi = active_ids[my_i];
+    if (lane < m && strengths) oq = scale_gate(my_q, strengths[my_i]);
     /* set_with_max_adapter(.., u16::MAX): an index of 65535 zero-fills the ring (lib.rs:163-179) */
-    zero_fill = zero_fill || (s < m && ridx[s] >= 0xFFFFu);
-    rq[s] = dq[s];
-    if (s < m && p.strengths) rq[s] = scale_gate(dq[s], p.strengths[didx[s]]);
-  }
-  if (zero_fill) {
-    ring_empty(ring, p.status, t, lane, 0);
-    return;
+    if (__ballot(lane < m && oi >= 0xFFFFu) != 0ull) {
+      ring_empty(ring, p.status, t, lane, 0);
+      return;
+    }
   }
   if (lane < 8) {
-    uint32_t oi = 0;
-    int oq = 0;
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-      if (s == lane && s < m) {
-        oi = ridx[s];
-        oq = rq[s];
-      }
-    ring->adapter_indices[lane] = (uint16_t)oi;
-    ring->gates_q15[lane] = (int16_t)oq;
+    ring->adapter_indices[lane] = (uint16_t)(lane < m ? oi : 0u);
+    ring->gates_q15[lane] = (int16_t)(lane < m ? oq : 0);
   }
   if (lane == 0) {
     ring->top_k = (uint32_t)m;
@@ -534,13 +513,15 @@ __device__ __forceinline__ float router_dot(const float *f_lds, const float *w, 
 }
 
 /* Routing from priors already in memory: one wave per token. */
+template <bool X>
 __global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
   const int t = blockIdx.x;
-  route_one<false>(p, p.priors_in + (size_t)t * p.n, t, threadIdx.x);
+  route_one<false, X>(p, p.priors_in + (size_t)t * p.n, t, threadIdx.x);
 }
 
 /* Routing from router features: one workgroup per token; wave w computes the priors of
  * adapters w, w + W, ... into LDS (and priors_out), then wave 0 routes. */
+template <bool X>
 __global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_params p) {
   extern __shared__ float lds[]; /* features [d], then priors [n] */
   const int t = blockIdx.x;
@@ -559,18 +540,21 @@ __global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_para
     }
   }
   __syncthreads();
-  if (wave == 0) route_one<true>(p, lds_priors, t, lane);
+  if (wave == 0) route_one<true, X>(p, lds_priors, t, lane);
 }
 
 }  // namespace
 
 extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx) {
+  const bool x = p->scope || p->tie_key || p->post_allowed || p->active_ids || p->strengths || p->hashes;
   if (p->features) {
     const int waves = p->n < 16 ? p->n : 16;
-    AOS_LAUNCH(ctx, aos_route_features_kernel, dim3(p->T), dim3(64 * waves),
-               (size_t)(p->d + p->n) * sizeof(float), *p);
+    const size_t lds = (size_t)(p->d + p->n) * sizeof(float);
+    if (x) AOS_LAUNCH(ctx, aos_route_features_kernel<true>, dim3(p->T), dim3(64 * waves), lds, *p);
+    else AOS_LAUNCH(ctx, aos_route_features_kernel<false>, dim3(p->T), dim3(64 * waves), lds, *p);
   } else {
-    AOS_LAUNCH(ctx, aos_route_kernel, dim3(p->T), dim3(64), 0, *p);
+    if (x) AOS_LAUNCH(ctx, aos_route_kernel<true>, dim3(p->T), dim3(64), 0, *p);
+    else AOS_LAUNCH(ctx, aos_route_kernel<false>, dim3(p->T), dim3(64), 0, *p);
   }
   return (int)hipGetLastError();
 }
