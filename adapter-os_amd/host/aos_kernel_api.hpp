@@ -6,15 +6,18 @@
 //   AdapterInfo / Decision    crates/adapteros-lora-router/src/types.rs:645-707
 //   PolicyMask (allow/deny)   crates/adapteros-lora-router/src/policy_mask.rs
 //   Router                    crates/adapteros-lora-router/src/router.rs:397-428, 556-562,
-//                             769-785 (construction), 1567-1952 (deterministic routing)
+//                             769-785 (construction), 1567-1952 (routing: scope hint, adaptive
+//                             tie-breakers, decision hash), 1427-1484 (compute_decision_hash)
+//   RoutingPolicy filter      crates/adapteros-lora-router/src/policy_mask.rs:221-355
+//   ring conversion           crates/adapteros-lora-worker/src/router_bridge.rs:137-186
 //   FusedKernels (hot-swap, device_name, attest_determinism, layer forwards)
 //                             crates/adapteros-lora-kernel-api/src/lib.rs:308-716
 //   adapter ingest            crates/adapteros-lora-mlx-ffi/src/backend.rs:891-893, 1017-1210
 //                             (safetensors bytes + metadata), 448-522 (every layer, failed modules
 //                             skipped); base weights as mlx_cpp_wrapper_real.cpp:683, 925-956 read them
 // Errors are thrown as AosError with the reference's error kinds (AosError::Kernel, ::Validation,
-// ::Routing, ::DeterminismViolation, ::Parse, ::Io); a Rust Result<T> maps to a return value or a
-// throw.
+// ::Routing, ::DeterminismViolation, ::Parse, ::Io, ::PolicyViolation, ::Config); a Rust Result<T>
+// maps to a return value or a throw.
 //
 // Header-only; link against libaoship.so and the HIP runtime (device buffers for the host-side
 // routing convenience call).
@@ -22,21 +25,26 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <array>
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <map>
 #include <memory>
+#include <optional>
+#include <set>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "../../include/aoship.h"
+#include "aos_determinism.hpp"
 #include "aos_ingest.hpp"
 
 namespace adapteros {
 
-enum class ErrorKind { Kernel, Validation, Routing, DeterminismViolation, Parse, Io };
+enum class ErrorKind { Kernel, Validation, Routing, DeterminismViolation, Parse, Io, PolicyViolation, Config };
 
 class AosError : public std::runtime_error {
  public:
@@ -143,11 +151,27 @@ struct RouterRing {
 struct AdapterInfo {
   std::string id;
   uint64_t stable_id = 0;
+  std::optional<std::string> scope_path;
+};
+
+// DecisionHash (types.rs:386-415): short hex (first 8 bytes) of each BLAKE3 hash.
+struct DecisionHash {
+  std::string input_hash, output_hash, combined_hash;
+  std::optional<std::string> reasoning_hash, backend_identity_hash;
+  float tau = 0.0f, eps = 0.0f;
+  size_t k = 0;
+};
+
+// RouterDeterminismConfig (types.rs:370-384); decision hashing is on by default there too.
+struct RouterDeterminismConfig {
+  bool ieee754_deterministic = true;
+  bool enable_decision_hashing = true;
 };
 
 struct Decision {
   std::vector<uint16_t> indices;
   std::vector<int16_t> gates_q15;
+  std::optional<DecisionHash> decision_hash;
 
   std::vector<float> gates_f32() const {
     std::vector<float> g;
@@ -177,7 +201,41 @@ struct PolicyMask {
   }
 };
 
-// ---- Router (deterministic mode, empty feature vector) -------------------------------------------
+// RoutingPolicy (the fields filter_decision_by_policy reads, adapteros-api-types) and the per-adapter
+// pass bytes the device filter takes: an adapter passes when it is in allowed_adapter_ids (if set),
+// not in denied_adapter_ids, has a cluster in allowed_clusters (if set) and no cluster in
+// denied_clusters (policy_mask.rs:246-315).
+struct RoutingPolicy {
+  std::optional<std::vector<std::string>> allowed_adapter_ids, denied_adapter_ids, allowed_clusters,
+      denied_clusters;
+  std::optional<size_t> max_adapters_per_token;
+};
+
+inline std::vector<uint8_t> routing_policy_pass_bytes(const RoutingPolicy &policy,
+                                                     const std::vector<std::string> &adapter_ids,
+                                                     const std::vector<std::optional<std::string>> &clusters) {
+  if (adapter_ids.size() != clusters.size())
+    throw AosError(ErrorKind::PolicyViolation, "RoutingPolicy adapter ids/clusters length mismatch");
+  auto as_set = [](const std::optional<std::vector<std::string>> &v) {
+    return v ? std::optional<std::set<std::string>>(std::set<std::string>(v->begin(), v->end())) : std::nullopt;
+  };
+  const auto allowed = as_set(policy.allowed_adapter_ids), denied = as_set(policy.denied_adapter_ids),
+             allowed_c = as_set(policy.allowed_clusters), denied_c = as_set(policy.denied_clusters);
+  std::vector<uint8_t> pass(adapter_ids.size(), 0);
+  for (size_t i = 0; i < adapter_ids.size(); ++i) {
+    const std::string &id = adapter_ids[i];
+    const std::optional<std::string> &c = clusters[i];
+    bool ok = true;
+    if (allowed && !allowed->count(id)) ok = false;
+    if (denied && denied->count(id)) ok = false;
+    if (allowed_c && (!c || !allowed_c->count(*c))) ok = false;
+    if (denied_c && c && denied_c->count(*c)) ok = false;
+    pass[i] = ok ? 1 : 0;
+  }
+  return pass;
+}
+
+// ---- Router (empty feature vector) ------------------------------------------------------------------
 
 class Router {
  public:
@@ -197,9 +255,43 @@ class Router {
     release();
   }
 
-  // One token, host priors (the reference's per-step router call); runs on the device.
+  // Router::set_routing_determinism_mode (router.rs:577): adaptive tie-breaking on exact ties.
+  void set_routing_determinism_mode(bool adaptive) { adaptive_ = adaptive; }
+  bool adaptive_routing() const { return adaptive_; }
+  void set_determinism_config(const RouterDeterminismConfig &c) { config_ = c; }
+
+  // filter_decision_by_policy on every decision (nullptr = no policy); adapter_ids / clusters
+  // describe the adapters routed over, in order.
+  void set_decision_policy(const RoutingPolicy *policy, const std::vector<std::string> &adapter_ids = {},
+                           const std::vector<std::optional<std::string>> &clusters = {}) {
+    if (!policy) {
+      policy_pass_.clear();
+      policy_max_ = -1;
+      has_policy_ = false;
+      return;
+    }
+    policy_pass_ = routing_policy_pass_bytes(*policy, adapter_ids, clusters);
+    policy_max_ = policy->max_adapters_per_token ? (int)std::min<size_t>(*policy->max_adapters_per_token, 1u << 30) : -1;
+    has_policy_ = true;
+  }
+
   Decision route_with_adapter_info(const std::vector<float> &features, const std::vector<float> &priors,
                                    const std::vector<AdapterInfo> &info, const PolicyMask &mask) {
+    return route_with_adapter_info_and_scope_with_ctx(features, priors, info, mask, nullptr, nullptr);
+  }
+  Decision route_with_adapter_info_with_ctx(const std::vector<float> &features, const std::vector<float> &priors,
+                                            const std::vector<AdapterInfo> &info, const PolicyMask &mask,
+                                            const det::DeterminismContext *ctx) {
+    return route_with_adapter_info_and_scope_with_ctx(features, priors, info, mask, nullptr, ctx);
+  }
+
+  // One token, host priors (the reference's per-step router call); runs on the device. A decision
+  // policy, when set, is applied to the result (a PolicyViolation throws).
+  Decision route_with_adapter_info_and_scope_with_ctx(const std::vector<float> &features,
+                                                      const std::vector<float> &priors,
+                                                      const std::vector<AdapterInfo> &info, const PolicyMask &mask,
+                                                      const std::string *scope_hint,
+                                                      const det::DeterminismContext *ctx) {
     if (!features.empty())
       throw AosError(ErrorKind::Validation, "feature scoring is not part of this path: pass empty features");
     if (priors.size() != info.size())
@@ -207,30 +299,72 @@ class Router {
     if (!mask.allowed.empty() && mask.allowed.size() != info.size())
       throw AosError(ErrorKind::Validation, "policy mask length differs from adapter_info");
     if (info.empty()) return Decision{};
+    if (has_policy_ && policy_pass_.size() != info.size())
+      throw AosError(ErrorKind::PolicyViolation, "RoutingPolicy adapter ids/clusters length mismatch");
     bind(info);
     detail::check(aoship_router_set_policy_mask(h_, mask.allowed.empty() ? nullptr : mask.allowed.data()),
                   ErrorKind::Validation, "aoship_router_set_policy_mask");
+    apply_extras(info, scope_hint, ctx);
+    detail::check(aoship_router_set_ring_mapping(h_, nullptr, nullptr), ErrorKind::Validation,
+                  "aoship_router_set_ring_mapping");
+    detail::check(aoship_router_set_decision_hashing(h_, config_.enable_decision_hashing ? d_hash_ : nullptr, 1,
+                                                     nullptr, nullptr),
+                  ErrorKind::Validation, "aoship_router_set_decision_hashing");
     const size_t n = info.size();
     detail::hip_check(hipMemcpy(d_priors_, priors.data(), n * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
     detail::check(aoship_route(h_, d_priors_, 1, d_ring_, d_status_), ErrorKind::Routing, "aoship_route");
     aoship_ring_t ring;
     int32_t status = 0;
+    uint8_t hashes[96];
     detail::hip_check(hipMemcpy(&ring, d_ring_, sizeof(ring), hipMemcpyDeviceToHost), "hipMemcpy");
     detail::hip_check(hipMemcpy(&status, d_status_, sizeof(status), hipMemcpyDeviceToHost), "hipMemcpy");
-    if (status != 0)
-      throw AosError(ErrorKind::DeterminismViolation, "non-finite prior or score");
+    if (config_.enable_decision_hashing)
+      detail::hip_check(hipMemcpy(hashes, d_hash_, 96, hipMemcpyDeviceToHost), "hipMemcpy");
+    if (status == -1) throw AosError(ErrorKind::DeterminismViolation, "non-finite prior or score");
+    if (status == -2) throw AosError(ErrorKind::PolicyViolation, "Routing policy denied all adapters for this token");
     Decision d;
     for (uint32_t i = 0; i < ring.top_k; ++i) {
       d.indices.push_back(ring.adapter_indices[i]);
       d.gates_q15.push_back(ring.gates_q15[i]);
     }
+    if (config_.enable_decision_hashing && ring.top_k > 0) {
+      DecisionHash h;
+      h.input_hash = det::B3Hash::hex(hashes, 8);
+      h.output_hash = det::B3Hash::hex(hashes + 32, 8);
+      h.combined_hash = det::B3Hash::hex(hashes + 64, 8);
+      h.tau = tau_clean();
+      h.eps = eps_clean();
+      h.k = k_ < 1 ? 1 : k_;
+      d.decision_hash = h;
+    }
     return d;
   }
 
-  // Batch form on device buffers: priors[T * n] -> rings[T] (status[T] may be null).
+  // decision_to_router_ring_with_active_ids_and_strengths for route_device's rings
+  // (active_ids / strengths: one entry per adapter, empty = off).
+  void set_ring_mapping(const std::vector<uint16_t> &active_ids, const std::vector<float> &strengths) {
+    active_ids_ = active_ids;
+    strengths_ = strengths;
+  }
+
+  // Batch form on device buffers: priors[T * n] -> rings[T] (status[T] may be null; -1 / -2 as
+  // aoship_route), with the scope hint, determinism context, decision policy and ring mapping
+  // applied; decision hashes into hashes_dev[T * 96] when it is given.
   void route_device(const std::vector<AdapterInfo> &info, const float *priors_dev, int T, aoship_ring_t *rings_dev,
-                    int32_t *status_dev) {
+                    int32_t *status_dev, const std::string *scope_hint = nullptr,
+                    const det::DeterminismContext *ctx = nullptr, uint8_t *hashes_dev = nullptr) {
+    if (has_policy_ && policy_pass_.size() != info.size())
+      throw AosError(ErrorKind::PolicyViolation, "RoutingPolicy adapter ids/clusters length mismatch");
+    if ((!active_ids_.empty() && active_ids_.size() != info.size()) ||
+        (!strengths_.empty() && strengths_.size() != info.size()))
+      throw AosError(ErrorKind::Routing, "Strengths / active ids length does not match active adapters");
     bind(info);
+    apply_extras(info, scope_hint, ctx);
+    detail::check(aoship_router_set_ring_mapping(h_, active_ids_.empty() ? nullptr : active_ids_.data(),
+                                                 strengths_.empty() ? nullptr : strengths_.data()),
+                  ErrorKind::Validation, "aoship_router_set_ring_mapping");
+    detail::check(aoship_router_set_decision_hashing(h_, hashes_dev, T, nullptr, nullptr), ErrorKind::Validation,
+                  "aoship_router_set_decision_hashing");
     detail::check(aoship_route(h_, priors_dev, T, rings_dev, status_dev), ErrorKind::Routing, "aoship_route");
   }
 
@@ -247,6 +381,41 @@ class Router {
     detail::hip_check(hipMalloc(&d_priors_, ids.size() * sizeof(float)), "hipMalloc");
     detail::hip_check(hipMalloc(&d_ring_, sizeof(aoship_ring_t)), "hipMalloc");
     detail::hip_check(hipMalloc(&d_status_, sizeof(int32_t)), "hipMalloc");
+    detail::hip_check(hipMalloc(&d_hash_, 96), "hipMalloc");
+    seed_.reset();
+  }
+  // Router::new sanitises tau and eps (router.rs:146-187); DecisionHash reports them.
+  float tau_clean() const { return (std::isfinite(tau_) && tau_ > 0.0f) ? tau_ : 1.0f; }
+  float eps_clean() const { return (std::isfinite(eps_) && eps_ >= 0.0f && eps_ <= 1.0f) ? eps_ : 0.02f; }
+  // scope hint (router.rs:1587-1602), adaptive seed (:1606-1612, 1705-1724), decision policy
+  void apply_extras(const std::vector<AdapterInfo> &info, const std::string *scope_hint,
+                    const det::DeterminismContext *ctx) {
+    std::vector<uint8_t> in_scope;
+    if (scope_hint) {
+      bool matched = false;
+      for (const auto &a : info) {
+        const bool m = a.scope_path && *a.scope_path == *scope_hint;
+        in_scope.push_back(m ? 1 : 0);
+        matched = matched || m;
+      }
+      if (!matched) in_scope.clear();
+    }
+    detail::check(aoship_router_set_scope(h_, in_scope.empty() ? nullptr : in_scope.data()), ErrorKind::Validation,
+                  "aoship_router_set_scope");
+    if (adaptive_ && !ctx)
+      throw AosError(ErrorKind::Config,
+                     "Adaptive routing configuration error: determinism context is required for seeded "
+                     "tie-breaking when adaptive routing is enabled. Provide a determinism context in the "
+                     "request or disable adaptive routing.");
+    std::optional<det::Bytes32> seed;
+    if (adaptive_) seed = ctx->router_tiebreak_seed();
+    if (seed != seed_) {
+      detail::check(aoship_router_set_adaptive_seed(h_, seed ? seed->data() : nullptr), ErrorKind::Validation,
+                    "aoship_router_set_adaptive_seed");
+      seed_ = seed;
+    }
+    detail::check(aoship_router_set_decision_policy(h_, has_policy_ ? policy_pass_.data() : nullptr, policy_max_),
+                  ErrorKind::Validation, "aoship_router_set_decision_policy");
   }
   void release() {
     if (h_) aoship_router_free(h_);
@@ -254,6 +423,8 @@ class Router {
     if (d_priors_) (void)hipFree(d_priors_);
     if (d_ring_) (void)hipFree(d_ring_);
     if (d_status_) (void)hipFree(d_status_);
+    if (d_hash_) (void)hipFree(d_hash_);
+    d_hash_ = nullptr;
     d_priors_ = nullptr;
     d_ring_ = nullptr;
     d_status_ = nullptr;
@@ -268,6 +439,15 @@ class Router {
   float *d_priors_ = nullptr;
   aoship_ring_t *d_ring_ = nullptr;
   int32_t *d_status_ = nullptr;
+  uint8_t *d_hash_ = nullptr;
+  bool adaptive_ = false;
+  RouterDeterminismConfig config_;
+  std::optional<det::Bytes32> seed_;
+  bool has_policy_ = false;
+  std::vector<uint8_t> policy_pass_;
+  int policy_max_ = -1;
+  std::vector<uint16_t> active_ids_;
+  std::vector<float> strengths_;
 };
 
 // ---- FusedKernels surface for the layer path -----------------------------------------------------

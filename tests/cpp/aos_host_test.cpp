@@ -122,6 +122,49 @@ void cpu_tests() {
   run("router_new_k_above_max", [] {  // router.rs:769-777
     CHECK(error_kind_of([] { Router r(9, 1.0f, 0.02f); }) == ErrorKind::Routing);
   });
+  // FIPS 180-4 examples and RFC 5869 appendix A test cases 1 and 3
+  run("sha256_hmac_hkdf_known_answers", [] {
+    auto hx = [](const uint8_t *p, size_t n) { return det::B3Hash::hex(p, n); };
+    CHECK(hx(det::sha256((const uint8_t *)"abc", 3).data(), 32) ==
+          "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad");
+    CHECK(hx(det::sha256(nullptr, 0).data(), 32) == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855");
+    const std::string m448 = "abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq";
+    CHECK(hx(det::sha256((const uint8_t *)m448.data(), m448.size()).data(), 32) ==
+          "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1");
+    std::vector<uint8_t> ikm(22, 0x0b), salt, info;
+    for (int i = 0; i <= 12; ++i) salt.push_back((uint8_t)i);
+    for (int i = 0xf0; i <= 0xf9; ++i) info.push_back((uint8_t)i);
+    auto okm = det::hkdf_sha256(salt.data(), salt.size(), ikm.data(), ikm.size(), info.data(), info.size(), 42);
+    CHECK(hx(okm.data(), okm.size()) ==
+          "3cb25f25faacd57a90434f64d0362f2a2d2d0a90cf1a5a4c5db02d56ecc4c5bf34007208d5b887185865");
+    okm = det::hkdf_sha256(nullptr, 0, ikm.data(), ikm.size(), nullptr, 0, 42);
+    CHECK(hx(okm.data(), okm.size()) ==
+          "8da4e775a563c18f715f802a063c5a31b8a11f5c5ee1879ec3454e5f3c738d2d9d201395faa4b61a96c8");
+  });
+  run("b3hash_hex_forms", [] {  // hash.rs:57-84
+    const det::B3Hash h = det::B3Hash::hash("hello world");
+    CHECK(h.to_hex() == "d74981efa70a0c880b8d8c1985d075dbcbf679b99a5f9914e5aaf96b831a9e24");
+    CHECK(h.to_short_hex() == "d74981efa70a0c88");
+    CHECK(det::B3Hash::from_hex("D74981EFA70A0C880B8D8C1985D075DBCBF679B99A5F9914E5AAF96B831A9E24") == h);
+    CHECK(!det::B3Hash::from_hex("d74981") && !det::B3Hash::from_hex(std::string(64, 'g')));
+  });
+  // policy_mask.rs:246-315 set semantics
+  run("routing_policy_pass_bytes", [] {
+    const std::vector<std::string> ids = {"a", "b", "c", "d"};
+    const std::vector<std::optional<std::string>> cl = {std::string("x"), std::nullopt, std::string("y"),
+                                                        std::string("x")};
+    RoutingPolicy p;
+    CHECK((routing_policy_pass_bytes(p, ids, cl) == std::vector<uint8_t>{1, 1, 1, 1}));
+    p.denied_adapter_ids = std::vector<std::string>{"c", "nonexistent"};
+    CHECK((routing_policy_pass_bytes(p, ids, cl) == std::vector<uint8_t>{1, 1, 0, 1}));
+    p.allowed_clusters = std::vector<std::string>{"x"};  // an adapter without cluster fails it
+    CHECK((routing_policy_pass_bytes(p, ids, cl) == std::vector<uint8_t>{1, 0, 0, 1}));
+    RoutingPolicy q;
+    q.denied_clusters = std::vector<std::string>{"x"};  // an adapter without cluster passes it
+    q.allowed_adapter_ids = std::vector<std::string>{"a", "b", "c"};
+    CHECK((routing_policy_pass_bytes(q, ids, cl) == std::vector<uint8_t>{0, 1, 1, 0}));
+    CHECK(error_kind_of([&] { routing_policy_pass_bytes(q, ids, {std::nullopt}); }) == ErrorKind::PolicyViolation);
+  });
 }
 
 // ---- GPU ----
@@ -239,6 +282,113 @@ void gpu_tests() {
     (void)hipFree(dx);
     (void)hipFree(dy);
     (void)hipFree(dr);
+  });
+  // router/src/tests.rs:856-925 with the C++ Router: exact ties select the first K of
+  // (breaker, stable_id) order for each request seed, and the two seeds select differently
+  run("adaptive_routing_applies_seeded_order_for_exact_ties", [] {
+    const size_t n = 8, k = 3;
+    std::vector<AdapterInfo> info;
+    for (size_t i = 0; i < n; ++i) info.push_back({"adaptive_tie_adapter_" + std::to_string(i), i + 1, std::nullopt});
+    std::vector<std::vector<uint16_t>> sel;
+    for (uint8_t b : {1, 2}) {
+      det::Bytes32 seed;
+      seed.fill(b);
+      const det::DeterminismContext ctx(seed, nullptr, det::RoutingDeterminismMode::Adaptive);
+      std::vector<uint64_t> br(n);
+      const det::Bytes32 ts = ctx.router_tiebreak_seed();
+      CHECK(aoship_adaptive_tie_breakers(ts.data(), (int)n, br.data()) == 0);
+      std::vector<uint16_t> order(n);
+      for (size_t i = 0; i < n; ++i) order[i] = (uint16_t)i;
+      std::sort(order.begin(), order.end(), [&](uint16_t a, uint16_t c) {
+        return br[a] != br[c] ? br[a] < br[c] : info[a].stable_id < info[c].stable_id;
+      });
+      std::vector<uint16_t> want(order.begin(), order.begin() + k);
+      std::sort(want.begin(), want.end());
+      Router router(k, 1.0f, 0.02f);
+      router.set_routing_determinism_mode(true);
+      Decision d = router.route_with_adapter_info_with_ctx({}, std::vector<float>(n, 0.5f), info,
+                                                           PolicyMask::allow_all(n), &ctx);
+      std::vector<uint16_t> got = d.indices;
+      std::sort(got.begin(), got.end());
+      CHECK(got == want);
+      sel.push_back(got);
+      // without a determinism context adaptive routing is a configuration error (router.rs:1606-1612)
+      CHECK(error_kind_of([&] {
+              router.route_with_adapter_info({}, std::vector<float>(n, 0.5f), info, PolicyMask::allow_all(n));
+            }) == ErrorKind::Config);
+    }
+    CHECK(sel[0] != sel[1]);
+  });
+  // router/src/tests.rs:928-972 (with an empty feature vector): the hash is filled in; its parts are
+  // BLAKE3 of the priors, of the indices and gates, and of both hashes
+  run("test_decision_hash_computation", [] {
+    Router router(3, 1.0f, 0.02f);
+    const std::vector<float> priors = {0.1f, 0.9f, 0.5f, 0.3f, 0.7f};
+    std::vector<AdapterInfo> info;
+    for (size_t i = 0; i < priors.size(); ++i) info.push_back({"adapter_" + std::to_string(i), 0, std::nullopt});
+    Decision d = router.route_with_adapter_info({}, priors, info, PolicyMask::allow_all(priors.size()));
+    CHECK(d.decision_hash.has_value());
+    const DecisionHash &h = *d.decision_hash;
+    CHECK(h.tau == 1.0f && h.eps == 0.02f && h.k == 3);
+    std::vector<uint8_t> in(priors.size() * 4), out;
+    std::memcpy(in.data(), priors.data(), in.size());
+    for (uint16_t i : d.indices) {
+      out.push_back((uint8_t)i);
+      out.push_back((uint8_t)(i >> 8));
+    }
+    for (int16_t g : d.gates_q15) {
+      out.push_back((uint8_t)(uint16_t)g);
+      out.push_back((uint8_t)((uint16_t)g >> 8));
+    }
+    const det::B3Hash hin = det::B3Hash::hash(in.data(), in.size()), hout = det::B3Hash::hash(out.data(), out.size());
+    std::vector<uint8_t> comb(hin.bytes.begin(), hin.bytes.end());
+    comb.insert(comb.end(), hout.bytes.begin(), hout.bytes.end());
+    CHECK(h.input_hash == hin.to_short_hex() && h.output_hash == hout.to_short_hex());
+    CHECK(h.combined_hash == det::B3Hash::hash(comb.data(), comb.size()).to_short_hex());
+    // reproducible, and off when the config says so (tests.rs:974-1110)
+    Router again(3, 1.0f, 0.02f);
+    Decision d2 = again.route_with_adapter_info({}, priors, info, PolicyMask::allow_all(priors.size()));
+    CHECK(d2.decision_hash->combined_hash == h.combined_hash);
+    RouterDeterminismConfig off;
+    off.enable_decision_hashing = false;
+    again.set_determinism_config(off);
+    CHECK(!again.route_with_adapter_info({}, priors, info, PolicyMask::allow_all(priors.size())).decision_hash);
+  });
+  // worker_enforcement_tests.rs:127-215 through the router's decision policy
+  run("routing_policy_on_decisions", [] {
+    std::vector<AdapterInfo> info = {{"adapter_a", 0, std::nullopt}, {"adapter_b", 0, std::nullopt}};
+    Router router(2, 1.0f, 0.02f);
+    RoutingPolicy p;
+    p.denied_adapter_ids = std::vector<std::string>{"adapter_b"};
+    p.max_adapters_per_token = 2;
+    router.set_decision_policy(&p, {"adapter_a", "adapter_b"}, {std::nullopt, std::nullopt});
+    Decision d = router.route_with_adapter_info({}, {0.8f, 0.7f}, info, PolicyMask::allow_all(2));
+    CHECK(d.indices == std::vector<uint16_t>{0} && d.gates_q15 == std::vector<int16_t>{32767});
+    RoutingPolicy all;
+    all.allowed_adapter_ids = std::vector<std::string>{"other"};
+    router.set_decision_policy(&all, {"adapter_a", "adapter_b"}, {std::nullopt, std::nullopt});
+    CHECK(error_kind_of([&] { router.route_with_adapter_info({}, {0.8f, 0.7f}, info, PolicyMask::allow_all(2)); }) ==
+          ErrorKind::PolicyViolation);
+    router.set_decision_policy(nullptr);
+    CHECK(router.route_with_adapter_info({}, {0.8f, 0.7f}, info, PolicyMask::allow_all(2)).indices.size() == 2);
+  });
+  // router.rs:1587-1602: a scope hint keeps routing inside the matching adapters
+  run("scope_hint", [] {
+    std::vector<AdapterInfo> info = {{"a", 0, std::string("src/x")},
+                                     {"b", 0, std::string("src/y")},
+                                     {"c", 0, std::string("src/x")},
+                                     {"d", 0, std::nullopt}};
+    Router router(2, 1.0f, 0.02f);
+    const std::vector<float> priors = {0.1f, 0.9f, 0.3f, 0.8f};
+    const std::string hint = "src/x", none = "src/z";
+    Decision d = router.route_with_adapter_info_and_scope_with_ctx({}, priors, info, PolicyMask::allow_all(4), &hint,
+                                                                   nullptr);
+    std::vector<uint16_t> got = d.indices;
+    std::sort(got.begin(), got.end());
+    CHECK((got == std::vector<uint16_t>{0, 2}));
+    // a hint no adapter matches is ignored
+    d = router.route_with_adapter_info_and_scope_with_ctx({}, priors, info, PolicyMask::allow_all(4), &none, nullptr);
+    CHECK((d.indices == std::vector<uint16_t>{1, 3}));
   });
   run("device_name_and_attestation", [] {  // kernel-api/src/lib.rs:374, 383
     HipKernels k(0, 1);
@@ -367,6 +517,26 @@ int ingest_base_mode(const std::string &file, const std::string &key) {
   return 0;
 }
 
+// ---- seeds: the DeterminismContext chain for a request seed (hex) and an optional router seed text ----
+
+int seeds_mode(const std::string &request_hex, const char *router_seed_text) {
+  const std::optional<det::B3Hash> rs = det::B3Hash::from_hex(request_hex);
+  if (!rs) {
+    std::fprintf(stderr, "request seed must be 64 hex digits\n");
+    return 2;
+  }
+  const det::DeterminismContext ctx =
+      router_seed_text ? det::DeterminismContext(rs->bytes, std::string(router_seed_text), det::RoutingDeterminismMode::Adaptive)
+                       : det::DeterminismContext(rs->bytes, nullptr, det::RoutingDeterminismMode::Adaptive);
+  const det::Bytes32 ts = ctx.router_tiebreak_seed();
+  const det::B3Hash manifest = det::B3Hash::hash("manifest");
+  const det::DeterminismContext with_manifest(rs->bytes, &manifest, det::RoutingDeterminismMode::Adaptive);
+  std::printf("{\"router_seed_hex\":%s,\"tiebreak_seed\":%s,\"router_seed_with_manifest\":%s,\"low64\":%llu}\n",
+              jstr(ctx.router_seed_hex()).c_str(), jstr(det::B3Hash::hex(ts.data(), 32)).c_str(),
+              jstr(with_manifest.router_seed_hex()).c_str(), (unsigned long long)ctx.request_seed_low64());
+  return 0;
+}
+
 // ---- gpu-ingest: safetensors-loaded layers against array-loaded ones, bit for bit ----
 
 template <class T>
@@ -485,6 +655,7 @@ int main(int argc, char **argv) {
   const std::string mode = argc > 1 ? argv[1] : "cpu";
   if (mode == "ingest-adapter" && (argc == 3 || argc == 4)) return ingest_adapter_mode(argv[2], argc == 4 ? argv[3] : nullptr);
   if (mode == "ingest-base" && argc == 4) return ingest_base_mode(argv[2], argv[3]);
+  if (mode == "seeds" && (argc == 3 || argc == 4)) return seeds_mode(argv[2], argc == 4 ? argv[3] : nullptr);
   if (mode == "ingest-lora" && argc == 6) return ingest_lora_mode(argv[2], argv[3], argv[4], argv[5]);
   if (mode == "gpu-ingest" && argc == 10)
     return gpu_ingest_mode(argv[2], std::atoi(argv[3]), std::atoi(argv[4]), std::atoi(argv[5]), std::atoi(argv[6]),
@@ -496,7 +667,7 @@ int main(int argc, char **argv) {
   else {
     std::fprintf(stderr,
                  "usage: %s cpu | gpu | ingest-adapter FILE [METADATA_JSON] | ingest-base FILE KEY |\n"
-                 "       ingest-lora FILE RANK ALPHA TARGET[,TARGET...] |\n"
+                 "       ingest-lora FILE RANK ALPHA TARGET[,TARGET...] | seeds REQUEST_SEED_HEX [ROUTER_SEED] |\n"
                  "       gpu-ingest DIR LAYERS HIDDEN INTERMEDIATE KV_OUT RANK1 ALPHA1 RANK2\n",
                  argv[0]);
     return 2;
