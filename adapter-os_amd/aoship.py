@@ -59,7 +59,27 @@ _SIGS = {
     "aoship_mlp_forward": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "aoship_proj_forward": (C.c_int, [_P, C.c_char_p, _P, C.c_int, _P, _P]),
     "aoship_qkv_forward": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P]),
+    "aoship_model_new": (_P, [_P]),
+    "aoship_model_free": (None, [_P]),
+    "aoship_model_layer": (_P, [_P, C.c_int]),
+    "aoship_model_set_embedding": (C.c_int, [_P, _P, _P, _P, _P]),
+    "aoship_model_set_lm_head": (C.c_int, [_P, _P, _P, _P]),
+    "aoship_model_set_norm": (C.c_int, [_P, C.c_int, C.c_int, _P]),
+    "aoship_model_set_bias": (C.c_int, [_P, C.c_int, C.c_char_p, _P]),
+    "aoship_model_set_adapters": (C.c_int, [_P, _P, C.c_int]),
+    "aoship_model_set_stream": (C.c_int, [_P, _P]),
+    "aoship_model_reserve": (C.c_int, [_P, C.c_int]),
+    "aoship_model_reset_cache": (C.c_int, [_P]),
+    "aoship_model_cache_len": (C.c_int, [_P]),
+    "aoship_model_forward": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P]),
 }
+
+
+class ModelConfig(C.Structure):
+    """aoship_model_config_t"""
+    _fields_ = [("num_layers", C.c_int), ("hidden", C.c_int), ("intermediate", C.c_int), ("num_heads", C.c_int),
+                ("num_kv_heads", C.c_int), ("head_dim", C.c_int), ("vocab", C.c_int), ("max_seq", C.c_int),
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float)]
 
 _lib = None
 
@@ -277,8 +297,9 @@ class LoraAdapter:
 class Layer:
     """aoship_layer_t: int4 base projections + bound adapter table."""
 
-    def __init__(self, layer_idx: int = 0):
-        h = lib().aoship_layer_new(layer_idx, 64, 4)
+    def __init__(self, layer_idx: int = 0, handle=None):
+        self.owned = handle is None
+        h = lib().aoship_layer_new(layer_idx, 64, 4) if handle is None else handle
         if not h:
             raise AosError(f"aoship_layer_new: {last_error()}")
         self.h = h
@@ -332,11 +353,83 @@ class Layer:
                "aoship_qkv_forward")
 
     def __del__(self):
-        if getattr(self, "h", None) and _lib is not None:
+        if getattr(self, "h", None) and _lib is not None and getattr(self, "owned", True):
             _lib.aoship_layer_free(self.h)
-            self.h = None
+        self.h = None
 
 
 def exp_cr(x: float) -> float:
     """Host build of the router's correctly rounded float64 exp (for its pinning test)."""
     return lib().aoship_internal_exp_cr(x)
+
+
+def _u16(a):
+    return None if a is None else np.ascontiguousarray(a).view(np.uint16)
+
+
+class Model:
+    """aoship_model_t: a decoder model over the adapter-augmented layers, with its KV cache
+    (mlx_model_forward_with_cache_and_lora)."""
+
+    def __init__(self, num_layers, hidden, intermediate, num_heads, num_kv_heads, head_dim, vocab, max_seq,
+                 rope_theta=10000.0, rms_eps=1e-6):
+        self.cfg = ModelConfig(num_layers, hidden, intermediate, num_heads, num_kv_heads, head_dim, vocab, max_seq,
+                               rope_theta, rms_eps)
+        h = lib().aoship_model_new(C.byref(self.cfg))
+        if not h:
+            raise AosError(f"aoship_model_new: {last_error()}")
+        self.h = h
+        self.layers = [Layer(i, handle=lib().aoship_model_layer(h, i)) for i in range(num_layers)]
+        self._adapters = []
+
+    def set_embedding(self, packed=None, scales_f16=None, biases_f16=None, rows_bf16=None) -> None:
+        p = None if packed is None else np.ascontiguousarray(packed, dtype=np.uint32)
+        s, b, r = _u16(scales_f16), _u16(biases_f16), _u16(rows_bf16)
+        _check(lib().aoship_model_set_embedding(self.h, *[None if a is None else a.ctypes.data for a in (p, s, b, r)]),
+               "aoship_model_set_embedding")
+
+    def set_lm_head(self, packed, scales_f16, biases_f16=None) -> None:
+        p = np.ascontiguousarray(packed, dtype=np.uint32)
+        s, b = _u16(scales_f16), _u16(biases_f16)
+        _check(lib().aoship_model_set_lm_head(self.h, p.ctypes.data, s.ctypes.data, None if b is None else b.ctypes.data),
+               "aoship_model_set_lm_head")
+
+    def set_norm(self, layer_idx: int, which: int, weight) -> None:
+        w = np.ascontiguousarray(weight, dtype=np.float32)
+        _check(lib().aoship_model_set_norm(self.h, layer_idx, which, w.ctypes.data), "aoship_model_set_norm")
+
+    def set_bias(self, layer_idx: int, module: str, bias) -> None:
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        _check(lib().aoship_model_set_bias(self.h, layer_idx, module.encode(), None if b is None else b.ctypes.data),
+               "aoship_model_set_bias")
+
+    def set_adapters(self, adapters) -> None:
+        arr = (C.c_void_p * max(1, len(adapters)))(*[a.h if a is not None else None for a in adapters])
+        _check(lib().aoship_model_set_adapters(self.h, arr, len(adapters)), "aoship_model_set_adapters")
+        self._adapters = list(adapters)
+
+    def set_stream(self, stream_ptr) -> None:
+        _check(lib().aoship_model_set_stream(self.h, stream_ptr), "aoship_model_set_stream")
+
+    def reserve(self, max_tokens: int) -> None:
+        _check(lib().aoship_model_reserve(self.h, max_tokens), "aoship_model_reserve")
+
+    def reset_cache(self) -> None:
+        _check(lib().aoship_model_reset_cache(self.h), "aoship_model_reset_cache")
+
+    def cache_len(self) -> int:
+        return lib().aoship_model_cache_len(self.h)
+
+    def forward(self, ids, rings, logits, position_offset: int | None = None) -> None:
+        """ids: device int32 [T]; rings: device uint8 [T * 40]; logits: device float32 [vocab]."""
+        T = ids.numel()
+        off = self.cache_len() if position_offset is None else position_offset
+        _check(lib().aoship_model_forward(self.h, _ptr(ids), T, off, _ptr(rings), _ptr(logits)),
+               "aoship_model_forward")
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            for layer in getattr(self, "layers", []):
+                layer.h = None
+            _lib.aoship_model_free(self.h)
+            self.h = None

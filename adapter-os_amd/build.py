@@ -47,6 +47,7 @@ SOURCES = [
     "aoship_lora.hip",
     "aoship_gemv.hip",
     "aoship_gemm.hip",
+    "aoship_model.hip",
     "aoship_api.cpp",
 ]
 

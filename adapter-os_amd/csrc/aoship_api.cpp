@@ -608,6 +608,9 @@ static uint32_t shuffle_nibbles(uint32_t w) {
   return r;
 }
 
+static int q4_upload(Q4Mat &q, int out_features, int in_features, const uint32_t *packed,
+                     const uint16_t *scales_f16, const uint16_t *biases_f16);
+
 extern "C" int aoship_layer_set_base(aoship_layer_t *l, const char *module, int out_features,
                                      int in_features, const uint32_t *packed,
                                      const uint16_t *scales_f16, const uint16_t *biases_f16) {
@@ -619,6 +622,14 @@ extern "C" int aoship_layer_set_base(aoship_layer_t *l, const char *module, int 
   if (in_features < 64 || in_features % 64 != 0)
     return set_err("aoship_layer_set_base: in_features must be a positive multiple of 64");
   if (ensure_device()) return -1;
+  return q4_upload(l->mats[m], out_features, in_features, packed, scales_f16, biases_f16);
+}
+
+/* MLX 4-bit rows -> the device tile layout: a 1 KiB chunk per (32-row block, group), lane
+ * i + 32c holding row i's 32 nibbles of K 32c .. 32c+31 (word s: K 32c+8s .. +7), and one word per
+ * (row, group) with the float16 scale (low half) and bias (high half). */
+static int q4_upload(Q4Mat &q, int out_features, int in_features, const uint32_t *packed,
+                     const uint16_t *scales_f16, const uint16_t *biases_f16) {
   const int G = in_features / 64, RB = out_features / 32, wpr = in_features / 8;
   std::vector<uint32_t> qt((size_t)RB * G * 256), sb((size_t)RB * G * 32);
   for (int rb = 0; rb < RB; ++rb)
@@ -636,7 +647,6 @@ extern "C" int aoship_layer_set_base(aoship_layer_t *l, const char *module, int 
         sdst[n] = s | (b << 16);
       }
     }
-  Q4Mat &q = l->mats[m];
   if (q.qt.upload(qt.data(), qt.size() * 4)) return -1;
   if (q.sb.upload(sb.data(), sb.size() * 4)) return -1;
   q.valid = true;
@@ -1388,4 +1398,330 @@ extern "C" void aoship_layer_free(aoship_layer_t *l) {
   for (auto e : l->event_pool) (void)hipEventDestroy(e);
   unbind_all(l);
   delete l;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* decoder model: embedding -> layers (norm, q/k/v + LoRA, RoPE + KV cache, attention, o + LoRA,  */
+/* residual, norm, SwiGLU MLP + LoRA, residual) -> final norm -> LM head                       */
+/* ------------------------------------------------------------------------------------------ */
+
+struct aoship_model {
+  aoship_model_config_t cfg;
+  std::vector<aoship_layer *> layers;
+  DevBuf emb_q4, emb_s, emb_b, emb_bf16; /* MLX rows, as loaded */
+  bool emb_set = false;
+  Q4Mat lm;
+  DevBuf lm_part, lm_ctr;
+  std::vector<DevBuf> norm_in, norm_post, bias; /* bias: [layer * 3 + {q,k,v}] */
+  DevBuf norm_final;
+  DevBuf kc, vc; /* [layers][nkv][max_seq][hd] bf16 */
+  DevBuf inv_freq;
+  DevBuf ws;     /* per-call buffers, sized for ws_T tokens */
+  int ws_T = 0;
+  int cache_len = 0;
+  hipStream_t stream = nullptr;
+};
+
+extern "C" aoship_model_t *aoship_model_new(const aoship_model_config_t *c) {
+  if (!c) {
+    set_err("aoship_model_new: null config");
+    return nullptr;
+  }
+  if (ensure_device()) return nullptr;
+  if (c->num_layers < 1 || c->hidden < 64 || c->hidden % 64 || c->intermediate < 64 || c->intermediate % 64 ||
+      c->num_heads < 1 || c->num_kv_heads < 1 || c->num_heads % c->num_kv_heads || c->head_dim < 8 ||
+      c->head_dim % 8 || c->head_dim > AOS_ATTN_MAX_HD || c->vocab < 32 || c->vocab % 32 || c->max_seq < 1) {
+    set_err("aoship_model_new: unsupported shape (hidden and intermediate multiples of 64, heads divisible by "
+            "kv heads, head_dim a multiple of 8 up to 256, vocab a multiple of 32)");
+    return nullptr;
+  }
+  if ((c->num_heads * c->head_dim) % 64 || (c->num_kv_heads * c->head_dim) % 32) {
+    set_err("aoship_model_new: num_heads * head_dim must be a multiple of 64 and num_kv_heads * head_dim of 32");
+    return nullptr;
+  }
+  auto *m = new aoship_model();
+  m->cfg = *c;
+  if (!(std::isfinite(m->cfg.rms_eps) && m->cfg.rms_eps >= 0.0f)) m->cfg.rms_eps = 1e-6f;
+  const int L = c->num_layers;
+  m->norm_in.resize((size_t)L);
+  m->norm_post.resize((size_t)L);
+  m->bias.resize((size_t)L * 3);
+  for (int i = 0; i < L; ++i) {
+    aoship_layer_t *l = aoship_layer_new(i, AOSHIP_GROUP_SIZE, AOSHIP_BITS);
+    if (!l) {
+      aoship_model_free(m);
+      return nullptr;
+    }
+    m->layers.push_back(l);
+  }
+  /* RoPE inverse frequencies as the fused forward computes them (…real.cpp:3252-3257) */
+  const int half = c->head_dim / 2;
+  std::vector<float> inv((size_t)half);
+  for (int i = 0; i < half; ++i) {
+    const float exp_val = -2.0f * (float)i / (float)c->head_dim;
+    inv[(size_t)i] = 1.0f / std::pow(c->rope_theta, exp_val);
+  }
+  std::vector<float> ones((size_t)c->hidden, 1.0f);
+  const size_t cache = (size_t)L * c->num_kv_heads * c->max_seq * c->head_dim * 2;
+  if (m->inv_freq.upload(inv.data(), inv.size() * 4) || m->kc.alloc(cache, true) || m->vc.alloc(cache, true) ||
+      m->norm_final.upload(ones.data(), ones.size() * 4)) {
+    aoship_model_free(m);
+    return nullptr;
+  }
+  for (int i = 0; i < L; ++i)
+    if (m->norm_in[(size_t)i].upload(ones.data(), ones.size() * 4) ||
+        m->norm_post[(size_t)i].upload(ones.data(), ones.size() * 4)) {
+      aoship_model_free(m);
+      return nullptr;
+    }
+  return m;
+}
+
+extern "C" void aoship_model_free(aoship_model_t *m) {
+  if (!m) return;
+  (void)hipDeviceSynchronize();
+  for (auto *l : m->layers) aoship_layer_free(l);
+  delete m;
+}
+
+extern "C" aoship_layer_t *aoship_model_layer(aoship_model_t *m, int layer_idx) {
+  if (!m || layer_idx < 0 || layer_idx >= (int)m->layers.size()) {
+    set_err("aoship_model_layer: layer index out of range");
+    return nullptr;
+  }
+  return m->layers[(size_t)layer_idx];
+}
+
+extern "C" int aoship_model_set_embedding(aoship_model_t *m, const uint32_t *packed, const uint16_t *scales_f16,
+                                          const uint16_t *biases_f16, const uint16_t *rows_bf16) {
+  if (!m) return set_err("aoship_model_set_embedding: null model");
+  if (ensure_device()) return -1;
+  const size_t V = (size_t)m->cfg.vocab, H = (size_t)m->cfg.hidden;
+  m->emb_q4.release();
+  m->emb_s.release();
+  m->emb_b.release();
+  m->emb_bf16.release();
+  m->emb_set = false;
+  if (packed) {
+    if (!scales_f16) return set_err("aoship_model_set_embedding: 4-bit rows need scales");
+    if (m->emb_q4.upload(packed, V * H / 2) || m->emb_s.upload(scales_f16, V * (H / 64) * 2)) return -1;
+    if (biases_f16 && m->emb_b.upload(biases_f16, V * (H / 64) * 2)) return -1;
+  } else if (rows_bf16) {
+    if (m->emb_bf16.upload(rows_bf16, V * H * 2)) return -1;
+  } else {
+    return set_err("aoship_model_set_embedding: no rows given");
+  }
+  m->emb_set = true;
+  return 0;
+}
+
+extern "C" int aoship_model_set_lm_head(aoship_model_t *m, const uint32_t *packed, const uint16_t *scales_f16,
+                                        const uint16_t *biases_f16) {
+  if (!m || !packed || !scales_f16) return set_err("aoship_model_set_lm_head: null argument");
+  if (ensure_device()) return -1;
+  return q4_upload(m->lm, m->cfg.vocab, m->cfg.hidden, packed, scales_f16, biases_f16);
+}
+
+extern "C" int aoship_model_set_norm(aoship_model_t *m, int layer_idx, int which, const float *w) {
+  if (!m || !w) return set_err("aoship_model_set_norm: null argument");
+  if (ensure_device()) return -1;
+  const size_t bytes = (size_t)m->cfg.hidden * 4;
+  if (layer_idx == -1) return m->norm_final.upload(w, bytes);
+  if (layer_idx < 0 || layer_idx >= m->cfg.num_layers || (which != 0 && which != 1))
+    return set_err("aoship_model_set_norm: layer or norm index out of range");
+  return (which == 0 ? m->norm_in : m->norm_post)[(size_t)layer_idx].upload(w, bytes);
+}
+
+extern "C" int aoship_model_set_bias(aoship_model_t *m, int layer_idx, const char *module, const float *b) {
+  if (!m) return set_err("aoship_model_set_bias: null model");
+  const int mi = module_index(module);
+  if (layer_idx < 0 || layer_idx >= m->cfg.num_layers || mi < MOD_Q || mi > MOD_V)
+    return set_err("aoship_model_set_bias: layer out of range or module not q_proj / k_proj / v_proj");
+  if (ensure_device()) return -1;
+  const int width = (mi == MOD_Q ? m->cfg.num_heads : m->cfg.num_kv_heads) * m->cfg.head_dim;
+  DevBuf &d = m->bias[(size_t)layer_idx * 3 + (size_t)(mi - MOD_Q)];
+  if (!b) {
+    d.release();
+    return 0;
+  }
+  return d.upload(b, (size_t)width * 4);
+}
+
+extern "C" int aoship_model_set_adapters(aoship_model_t *m, aoship_lora_adapter_t *const *table, int n) {
+  if (!m) return set_err("aoship_model_set_adapters: null model");
+  for (auto *l : m->layers)
+    if (aoship_layer_set_adapters(l, table, n)) return -1;
+  return 0;
+}
+
+extern "C" int aoship_model_set_stream(aoship_model_t *m, void *stream) {
+  if (!m) return set_err("aoship_model_set_stream: null model");
+  m->stream = (hipStream_t)stream;
+  for (auto *l : m->layers)
+    if (aoship_layer_set_stream(l, stream)) return -1;
+  return 0;
+}
+
+extern "C" int aoship_model_reset_cache(aoship_model_t *m) {
+  if (!m) return set_err("aoship_model_reset_cache: null model");
+  m->cache_len = 0;
+  return 0;
+}
+
+extern "C" int aoship_model_cache_len(const aoship_model_t *m) { return m ? m->cache_len : -1; }
+
+/* per-call buffers: hidden f32, normed / q / k / v / attention / y bf16, rotated q f32, the
+ * attention splits' partials */
+static int attn_splits(const aoship_model *m, int T, int visible_max) {
+  const int chunks = ceil_div(visible_max, 64);
+  int s = ceil_div(1024, m->cfg.num_heads * T);
+  if (s > chunks) s = chunks;
+  return s < 1 ? 1 : s;
+}
+
+struct ModelWs {
+  float *hidden, *qr, *part;
+  uint16_t *normed, *q, *k, *v, *attn, *y;
+  size_t bytes;
+};
+
+static ModelWs model_ws(const aoship_model *m, int T, void *base) {
+  const aoship_model_config_t &c = m->cfg;
+  const int splits = attn_splits(m, T, c.max_seq);
+  Bump b(base, 0);
+  ModelWs w;
+  w.hidden = b.take<float>((size_t)T * c.hidden);
+  w.qr = b.take<float>((size_t)T * c.num_heads * c.head_dim);
+  w.part = b.take<float>((size_t)T * c.num_heads * splits * (c.head_dim + 2));
+  w.normed = b.take<uint16_t>((size_t)T * c.hidden);
+  w.q = b.take<uint16_t>((size_t)T * c.num_heads * c.head_dim);
+  w.k = b.take<uint16_t>((size_t)T * c.num_kv_heads * c.head_dim);
+  w.v = b.take<uint16_t>((size_t)T * c.num_kv_heads * c.head_dim);
+  w.attn = b.take<uint16_t>((size_t)T * c.num_heads * c.head_dim);
+  w.y = b.take<uint16_t>((size_t)T * c.hidden);
+  w.bytes = b.off;
+  return w;
+}
+
+extern "C" int aoship_model_reserve(aoship_model_t *m, int max_tokens) {
+  if (!m || max_tokens < 1) return set_err("aoship_model_reserve: bad arguments");
+  if (ensure_device()) return -1;
+  for (auto *l : m->layers)
+    if (aoship_layer_reserve(l, max_tokens)) return -1;
+  if (max_tokens > m->ws_T) {
+    if (m->ws.alloc(model_ws(m, max_tokens, nullptr).bytes, false)) return -1;
+    m->ws_T = max_tokens;
+  }
+  return 0;
+}
+
+extern "C" int aoship_model_forward(aoship_model_t *m, const int32_t *ids, int T, int position_offset,
+                                    const aoship_ring_t *rings, float *logits) {
+  if (!m || !ids || !rings || !logits) return set_err("aoship_model_forward: null argument");
+  const aoship_model_config_t &c = m->cfg;
+  if (T < 1) return set_err("aoship_model_forward: T must be positive");
+  if (position_offset != m->cache_len)
+    return set_err("aoship_model_forward: position_offset must equal the cache length (" +
+                   std::to_string(m->cache_len) + ")");
+  if (position_offset + T > c.max_seq) return set_err("aoship_model_forward: the KV cache is full");
+  if (!m->emb_set) return set_err("aoship_model_forward: embedding not set");
+  if (!m->lm.valid) return set_err("aoship_model_forward: LM head not set");
+  if (ensure_device()) return -1;
+  if (T > m->ws_T) {
+    const size_t bytes = model_ws(m, T, nullptr).bytes;
+    if (m->ws.alloc(bytes, false)) return -1;
+    m->ws_T = T;
+  }
+  const ModelWs w = model_ws(m, T, m->ws.p);
+  aos_launch_ctx ctx = {m->stream, nullptr, nullptr};
+  const int hd = c.head_dim, nh = c.num_heads, nkv = c.num_kv_heads;
+
+  aos_embed_params ep;
+  memset(&ep, 0, sizeof(ep));
+  ep.ids = ids;
+  ep.T = T;
+  ep.H = c.hidden;
+  ep.vocab = c.vocab;
+  ep.q4 = m->emb_q4.p ? m->emb_q4.as<uint32_t>() : nullptr;
+  ep.s16 = m->emb_s.p ? m->emb_s.as<uint16_t>() : nullptr;
+  ep.b16 = m->emb_b.p ? m->emb_b.as<uint16_t>() : nullptr;
+  ep.bf16 = m->emb_bf16.p ? m->emb_bf16.as<uint16_t>() : nullptr;
+  ep.hidden = w.hidden;
+  if (launch_err(aos_launch_embed(&ep, &ctx), "embedding")) return -1;
+
+  auto norm = [&](const uint16_t *add, const DevBuf &wt, int rows, float *hid, uint16_t *out) {
+    aos_norm_params np;
+    np.hidden = hid;
+    np.add = add;
+    np.w = wt.as<float>();
+    np.eps = c.rms_eps;
+    np.T = rows;
+    np.H = c.hidden;
+    np.out = out;
+    return launch_err(aos_launch_norm(&np, &ctx), "rms norm");
+  };
+  const size_t layer_cache = (size_t)nkv * c.max_seq * hd;
+  for (int li = 0; li < c.num_layers; ++li) {
+    aoship_layer *l = m->layers[(size_t)li];
+    if (norm(li == 0 ? nullptr : w.y, m->norm_in[(size_t)li], T, w.hidden, w.normed)) return -1;
+    if (aoship_qkv_forward(l, w.normed, T, rings, w.q, w.k, w.v)) return -1;
+    aos_rope_params rp;
+    rp.q = w.q;
+    rp.k = w.k;
+    rp.v = w.v;
+    rp.bq = m->bias[(size_t)li * 3].p ? m->bias[(size_t)li * 3].as<float>() : nullptr;
+    rp.bk = m->bias[(size_t)li * 3 + 1].p ? m->bias[(size_t)li * 3 + 1].as<float>() : nullptr;
+    rp.bv = m->bias[(size_t)li * 3 + 2].p ? m->bias[(size_t)li * 3 + 2].as<float>() : nullptr;
+    rp.inv_freq = m->inv_freq.as<float>();
+    rp.T = T;
+    rp.nh = nh;
+    rp.nkv = nkv;
+    rp.hd = hd;
+    rp.offset = position_offset;
+    rp.max_seq = c.max_seq;
+    rp.qr = w.qr;
+    rp.kc = m->kc.as<uint16_t>() + (size_t)li * layer_cache;
+    rp.vc = m->vc.as<uint16_t>() + (size_t)li * layer_cache;
+    if (launch_err(aos_launch_rope(&rp, &ctx), "rope")) return -1;
+    aos_attn_params ap;
+    ap.q = w.qr;
+    ap.kc = rp.kc;
+    ap.vc = rp.vc;
+    ap.T = T;
+    ap.nh = nh;
+    ap.nkv = nkv;
+    ap.hd = hd;
+    ap.offset = position_offset;
+    ap.max_seq = c.max_seq;
+    ap.splits = attn_splits(m, T, position_offset + T);
+    ap.chunk = ceil_div(ceil_div(position_offset + T, ap.splits), 64) * 64;
+    ap.scale = 1.0f / std::sqrt((float)hd);
+    ap.part = w.part;
+    ap.out = w.attn;
+    if (launch_err(aos_launch_attention(&ap, &ctx), "attention")) return -1;
+    if (aoship_proj_forward(l, "o_proj", w.attn, T, rings, w.y)) return -1;
+    if (norm(w.y, m->norm_post[(size_t)li], T, w.hidden, w.normed)) return -1;
+    if (aoship_mlp_forward(l, w.normed, T, rings, w.y)) return -1;
+  }
+  /* residual of the last MLP and the final norm, for the last token only */
+  const size_t lastH = (size_t)(T - 1) * c.hidden;
+  if (norm(w.y + lastH, m->norm_final, 1, w.hidden + lastH, w.normed + lastH)) return -1;
+  aos_gemv_params g;
+  memset(&g, 0, sizeof(g));
+  g.w0 = m->lm.dev();
+  g.x = w.normed + lastH;
+  g.T = 1;
+  g.yf = logits;
+  g.zero_row = m->layers[0]->zeros.as<uint16_t>();
+  gemv_geometry(m->lm.RB, m->lm.G, 1, false, false, g);
+  if (g.ks > 1) {
+    const size_t part = (size_t)m->lm.RB * g.ks * 64 * 4;
+    if (m->lm_part.bytes < part && m->lm_part.alloc(part, false)) return -1;
+    if (m->lm_ctr.bytes < (size_t)m->lm.RB * 4 && m->lm_ctr.alloc((size_t)m->lm.RB * 4, true)) return -1;
+    g.part = m->lm_part.as<float>();
+    g.counters = m->lm_ctr.as<uint32_t>();
+  }
+  if (launch_err(aos_launch_gemv(&g, 0, &ctx), "lm head")) return -1;
+  m->cache_len += T;
+  return 0;
 }

@@ -331,7 +331,8 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     const int m = aos_acc_m(v, lane);
     if (m >= T) continue;
     if (!SW) {
-      p.y[(size_t)m * out + row] = aos_f32_to_bf16(acc0[v]);
+      if (p.yf) p.yf[(size_t)m * out + row] = acc0[v];
+      else p.y[(size_t)m * out + row] = aos_f32_to_bf16(acc0[v]);
     } else {
       const float gt = acc0[v], up = acc1[v];
       const float sg = 1.0f / (1.0f + expf(-gt));

@@ -135,6 +135,7 @@ typedef struct {
   const uint16_t *zero_row;
   /* outputs */
   uint16_t *y;        /* [T][out] bf16 (plain) or h (SwiGLU) */
+  float *yf;          /* plain mode: [T][out] float32 instead of y when not NULL */
   float *part;        /* [RB][ks][NA * NV * 64] */
   uint32_t *counters; /* [RB] zero between launches */
 } aos_gemv_params;
@@ -231,6 +232,47 @@ typedef struct {
   void *ev_stop;
 } aos_launch_ctx;
 
+/* ---- full decoder step (embedding, norms, RoPE + KV cache, attention) ---- */
+#define AOS_ATTN_MAX_HD 256
+typedef struct {
+  const int32_t *ids; /* [T] */
+  int T, H, vocab;
+  const uint32_t *q4;     /* [vocab][H / 8] MLX 4-bit rows, or NULL */
+  const uint16_t *s16;    /* [vocab][H / 64] float16 scales */
+  const uint16_t *b16;    /* [vocab][H / 64] float16 biases (NULL = 0) */
+  const uint16_t *bf16;   /* [vocab][H] bfloat16 rows when q4 is NULL */
+  float *hidden;          /* [T][H] float32 */
+  int32_t *status;        /* set to 1 when an id is out of range (that row is zero) */
+} aos_embed_params;
+
+typedef struct {
+  float *hidden;          /* [T][H] float32 residual stream */
+  const uint16_t *add;    /* [T][H] bf16 added to hidden first, or NULL */
+  const float *w;         /* [H] norm weight */
+  float eps;
+  int T, H;
+  uint16_t *out;          /* [T][H] bf16 normalised */
+} aos_norm_params;
+
+typedef struct {
+  const uint16_t *q, *k, *v; /* [T][nh*hd], [T][nkv*hd], [T][nkv*hd] bf16 projections */
+  const float *bq, *bk, *bv; /* biases or NULL */
+  const float *inv_freq;     /* [hd / 2] */
+  int T, nh, nkv, hd, offset, max_seq;
+  float *qr;                 /* [T][nh][hd] float32, rotated */
+  uint16_t *kc, *vc;         /* [nkv][max_seq][hd] bf16 caches of this layer */
+} aos_rope_params;
+
+typedef struct {
+  const float *q;            /* [T][nh][hd] rotated */
+  const uint16_t *kc, *vc;   /* [nkv][max_seq][hd] */
+  int T, nh, nkv, hd, offset, max_seq;
+  int splits, chunk;         /* key positions per split (multiple of 64) */
+  float scale;
+  float *part;               /* [T][nh][splits][hd + 2]: acc, running max, sum */
+  uint16_t *out;             /* [T][nh * hd] bf16 */
+} aos_attn_params;
+
 #define AOS_LAUNCH(ctx, kernel, grid, block, lds, ...)                                            \
   do {                                                                                            \
     if ((ctx)->ev_start)                                                                          \
@@ -255,6 +297,10 @@ extern "C" {
 #endif
 /* Host-side launchers (return hipError_t as int). */
 int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx);
+int aos_launch_embed(const aos_embed_params *p, const aos_launch_ctx *ctx);
+int aos_launch_norm(const aos_norm_params *p, const aos_launch_ctx *ctx);
+int aos_launch_rope(const aos_rope_params *p, const aos_launch_ctx *ctx);
+int aos_launch_attention(const aos_attn_params *p, const aos_launch_ctx *ctx);
 int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);

@@ -247,6 +247,67 @@ int aoship_qkv_forward(aoship_layer_t *layer, const aoship_bf16_t *x, int T,
                        const aoship_ring_t *rings, aoship_bf16_t *q, aoship_bf16_t *k,
                        aoship_bf16_t *v);
 
+/* ---- decoder model: FusedKernels::run_step's token -> logits path ---------------------------- */
+
+typedef struct aoship_model aoship_model_t;
+
+/* Shape of a decoder-only model (the MLX wrapper's model config). max_seq sizes the KV cache. */
+typedef struct {
+  int num_layers, hidden, intermediate, num_heads, num_kv_heads, head_dim, vocab, max_seq;
+  float rope_theta, rms_eps;
+} aoship_model_config_t;
+
+/* A model of num_layers layers with its KV cache (mlx_model_load + mlx_kv_cache_new,
+ * wrapper.h). hidden and intermediate multiples of 64; num_heads a multiple of num_kv_heads;
+ * head_dim a multiple of 8 up to 256; vocab a multiple of 32. Norm weights start at 1, biases
+ * absent. NULL on error. */
+aoship_model_t *aoship_model_new(const aoship_model_config_t *config);
+void aoship_model_free(aoship_model_t *model);
+
+/* Layer i of the model: set its seven projections with aoship_layer_set_base. */
+aoship_layer_t *aoship_model_layer(aoship_model_t *model, int layer_idx);
+
+/* model.embed_tokens: MLX 4-bit rows (packed[vocab * hidden/8], float16 scales and biases
+ * [vocab * hidden/64], biases NULL = 0) or, with packed NULL, bfloat16 rows[vocab * hidden]
+ * (the fused forward's take(embed, ids), mlx_cpp_wrapper_real.cpp:3421-3432). Host arrays. */
+int aoship_model_set_embedding(aoship_model_t *model, const uint32_t *packed, const uint16_t *scales_f16,
+                               const uint16_t *biases_f16, const uint16_t *rows_bf16);
+
+/* lm_head in MLX 4-bit layout [vocab x hidden] (a model with tied embeddings passes its
+ * embedding arrays). Host arrays. */
+int aoship_model_set_lm_head(aoship_model_t *model, const uint32_t *packed, const uint16_t *scales_f16,
+                             const uint16_t *biases_f16);
+
+/* RMSNorm weights (float32 host [hidden]): layer_idx >= 0 with which 0 = input_layernorm,
+ * 1 = post_attention_layernorm; layer_idx = -1 = model.norm. */
+int aoship_model_set_norm(aoship_model_t *model, int layer_idx, int which, const float *weight);
+
+/* q_proj / k_proj / v_proj bias of a layer (float32 host [out]; NULL removes it). */
+int aoship_model_set_bias(aoship_model_t *model, int layer_idx, const char *module, const float *bias);
+
+/* aoship_layer_set_adapters on every layer. */
+int aoship_model_set_adapters(aoship_model_t *model, aoship_lora_adapter_t *const *table, int n);
+
+/* Stream for the model's launches (its layers included); NULL = null stream. */
+int aoship_model_set_stream(aoship_model_t *model, void *stream);
+
+/* Sizes every workspace for calls of up to max_tokens tokens, so forwards allocate nothing. */
+int aoship_model_reserve(aoship_model_t *model, int max_tokens);
+
+/* The KV cache: emptied, and its length (positions held). */
+int aoship_model_reset_cache(aoship_model_t *model);
+int aoship_model_cache_len(const aoship_model_t *model);
+
+/* mlx_model_forward_with_cache_and_lora (mlx_cpp_wrapper_real.cpp:3339-3527) for T tokens:
+ * embedding, then per layer RMSNorm, q/k/v (+bias, +LoRA), RoPE, K/V appended to the cache,
+ * causal GQA attention over the cache, o_proj (+LoRA), residual, RMSNorm, SwiGLU MLP (+LoRA),
+ * residual; final RMSNorm; logits[vocab] (device float32) of the last token.
+ *   ids   : device int32[T];  rings : device aoship_ring_t[T] (each token's adapters and gates)
+ *   position_offset must equal aoship_model_cache_len (tokens extend the cached sequence), and
+ *   the cache must hold position_offset + T positions. Asynchronous. Returns 0 / -1. */
+int aoship_model_forward(aoship_model_t *model, const int32_t *ids, int T, int position_offset,
+                         const aoship_ring_t *rings, float *logits);
+
 #ifdef __cplusplus
 }
 #endif

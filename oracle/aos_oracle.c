@@ -654,6 +654,104 @@ void orc_decision_hash(const float *priors, int n, const uint16_t *idx, const in
   free(buf);
 }
 
+/* ---- decoder step pieces (mlx_cpp_wrapper_real.cpp, fused forward) ----------------------------- */
+
+/* rms_norm (…real.cpp:3384-3390): y = x * (w / sqrt(mean(x^2) + eps)). mode 0: float32 with the
+ * sum of squares in order; mode 1: float64. */
+void orc_rmsnorm(const float *x, int T, int H, const float *w, float eps, float *y, int mode) {
+  for (int t = 0; t < T; ++t) {
+    const float *r = x + (size_t)t * H;
+    float *o = y + (size_t)t * H;
+    if (mode == 0) {
+      float ss = 0.0f;
+      for (int e = 0; e < H; ++e) ss += r[e] * r[e];
+      float d = sqrtf(ss / (float)H + eps);
+      for (int e = 0; e < H; ++e) o[e] = r[e] * (w[e] / d);
+    } else {
+      double ss = 0.0;
+      for (int e = 0; e < H; ++e) ss += (double)r[e] * (double)r[e];
+      double d = sqrt(ss / (double)H + (double)eps);
+      for (int e = 0; e < H; ++e) o[e] = (float)((double)r[e] * ((double)w[e] / d));
+    }
+  }
+}
+
+/* RoPE of the fused forward (…real.cpp:3249-3279), in place on x[T][heads][hd]: inv_freq_i =
+ * 1 / theta^(-2i/hd) (float32 powf), angle = (offset + t) * inv_freq_i, halves x1 = x[:hd/2],
+ * x2 = x[hd/2:] -> [x1 cos - x2 sin, x1 sin + x2 cos]. */
+void orc_rope(float *x, int T, int heads, int hd, int offset, float theta) {
+  int half = hd / 2;
+  for (int t = 0; t < T; ++t)
+    for (int h = 0; h < heads; ++h) {
+      float *r = x + ((size_t)t * heads + h) * hd;
+      for (int i = 0; i < half; ++i) {
+        float inv = 1.0f / powf(theta, -2.0f * (float)i / (float)hd);
+        float ang = (float)(offset + t) * inv;
+        float c = cosf(ang), s = sinf(ang);
+        float x1 = r[i], x2 = r[i + half];
+        r[i] = x1 * c - x2 * s;
+        r[i + half] = x1 * s + x2 * c;
+      }
+    }
+}
+
+/* Causal scaled dot-product attention of the fused forward (…real.cpp:3282-3327): q[T][nh][hd]
+ * (rotated), k / v[L][nkv][hd] for positions 0 .. L-1 (the cache then the new tokens,
+ * L = offset + T); token t attends to positions <= offset + t (the -1e9 mask), head h to kv head
+ * h / (nh / nkv); scores (q . k) * (1 / sqrt(hd)), softmax over the row, . v -> out[T][nh][hd].
+ * mode 0: float32 (max-subtracted softmax, sums in position order); mode 1: float64. */
+void orc_attention(const float *q, const float *k, const float *v, int T, int offset, int nh, int nkv, int hd,
+                   float *out, int mode) {
+  int L = offset + T, rep = nh / nkv;
+  double *sc = (double *)malloc(sizeof(double) * (size_t)(L > 0 ? L : 1));
+  float scale = 1.0f / sqrtf((float)hd);
+  for (int t = 0; t < T; ++t)
+    for (int h = 0; h < nh; ++h) {
+      const float *qr = q + ((size_t)t * nh + h) * hd;
+      int kvh = h / rep, vis = offset + t + 1;
+      double mx = -INFINITY;
+      for (int p = 0; p < vis; ++p) {
+        const float *kr = k + ((size_t)p * nkv + kvh) * hd;
+        if (mode == 0) {
+          float dot = 0.0f;
+          for (int d = 0; d < hd; ++d) dot += qr[d] * kr[d];
+          sc[p] = (double)(dot * scale);
+        } else {
+          double dot = 0.0;
+          for (int d = 0; d < hd; ++d) dot += (double)qr[d] * (double)kr[d];
+          sc[p] = dot * (double)scale;
+        }
+        if (sc[p] > mx) mx = sc[p];
+      }
+      float *o = out + ((size_t)t * nh + h) * hd;
+      if (mode == 0) {
+        float sum = 0.0f;
+        for (int p = 0; p < vis; ++p) {
+          float e = expf((float)sc[p] - (float)mx);
+          sc[p] = (double)e;
+          sum += e;
+        }
+        for (int d = 0; d < hd; ++d) {
+          float a = 0.0f;
+          for (int p = 0; p < vis; ++p) a += ((float)sc[p] / sum) * v[((size_t)p * nkv + kvh) * hd + d];
+          o[d] = a;
+        }
+      } else {
+        double sum = 0.0;
+        for (int p = 0; p < vis; ++p) {
+          sc[p] = exp(sc[p] - mx);
+          sum += sc[p];
+        }
+        for (int d = 0; d < hd; ++d) {
+          double a = 0.0;
+          for (int p = 0; p < vis; ++p) a += (sc[p] / sum) * (double)v[((size_t)p * nkv + kvh) * hd + d];
+          o[d] = (float)a;
+        }
+      }
+    }
+  free(sc);
+}
+
 void orc_priors(const float *features, const float *router_w, int T, int n, int d, float *priors) {
 #pragma omp parallel for collapse(2) schedule(static)
   for (int t = 0; t < T; ++t) {

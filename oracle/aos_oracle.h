@@ -46,6 +46,12 @@
  *                      active ids and strengths) pinned by the reference's policy_mask.rs and
  *                      router_bridge.rs tests, worker_enforcement_tests.rs, exact rational
  *                      arithmetic for renormalisation, and brute force over tie orders.
+ *   orc_rmsnorm / orc_rope / orc_attention (decoder step)
+ *                      pinned by the reference's RoPE tests (attention.rs:893-980: position 0 is
+ *                      the identity, positions 1 and 5 rotate by 1 and 5 radians), closed forms
+ *                      (a constant row normalises to the weights, one visible key returns its
+ *                      value, equal scores average the values, causality) and float64
+ *                      evaluation.
  *   orc_blake3 / orc_decision_hash
  *                      pinned by the BLAKE3 hashes the reference holds (B3Hash of "" and of
  *                      "hello world"; the BLAKE3 checksums of its source files in
@@ -123,6 +129,14 @@ void orc_tie_breakers(const uint8_t seed[32], int n, uint64_t *out);
 void orc_blake3(const uint8_t *in, size_t len, uint8_t out[32]);
 void orc_decision_hash(const float *priors, int n, const uint16_t *idx, const int16_t *q, int kk,
                        const uint8_t *reasoning, const uint8_t *backend, uint8_t out[96]);
+
+/* Decoder step pieces of the fused forward (mlx_cpp_wrapper_real.cpp:3249-3390): RMSNorm, RoPE
+ * (the fused forward's inv_freq = 1 / theta^(-2i/hd) and half rotation), causal GQA attention over
+ * k / v[L][nkv][hd]. mode 0 float32, mode 1 float64. */
+void orc_rmsnorm(const float *x, int T, int H, const float *w, float eps, float *y, int mode);
+void orc_rope(float *x, int T, int heads, int hd, int offset, float theta);
+void orc_attention(const float *q, const float *k, const float *v, int T, int offset, int nh, int nkv, int hd,
+                   float *out, int mode);
 
 /* Route T tokens (priors[T*n]) into rings[T]. Returns 0 or -1 (first failing token in *bad_token). */
 int orc_route_batch(const float *priors, int T, int n, const uint64_t *stable_id,

@@ -68,6 +68,12 @@ def lib():
         L.orc_blake3.argtypes = [P, C.c_size_t, P]
         L.orc_decision_hash.restype = None
         L.orc_decision_hash.argtypes = [P, C.c_int, P, P, C.c_int, P, P, P]
+        L.orc_rmsnorm.restype = None
+        L.orc_rmsnorm.argtypes = [P, C.c_int, C.c_int, P, C.c_float, P, C.c_int]
+        L.orc_rope.restype = None
+        L.orc_rope.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.orc_attention.restype = None
+        L.orc_attention.argtypes = [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, C.c_int]
         L.orc_priors.restype = None
         L.orc_priors.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P]
         L.orc_dequant_q4.restype = None
@@ -370,6 +376,92 @@ def proj_forward(x, w, module, modules, lora, scales, rank, rings, mode=0):
     lib().orc_proj_forward(x.ctypes.data, T, din, dout, C.byref(q), mods, len(modules), modules.index(module),
                            sc.ctypes.data, n, rank, rg.ctypes.data, y.ctypes.data, mode)
     return y
+
+
+def rmsnorm(x, w, eps, mode=0):
+    x = _c(x, np.float32)
+    T, H = x.shape
+    w = _c(w, np.float32)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(x.ctypes.data, T, H, w.ctypes.data, eps, y.ctypes.data, mode)
+    return y
+
+
+def rope(x, offset, theta):
+    """x[T][heads][hd] rotated (a copy)."""
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    T, heads, hd = x.shape
+    lib().orc_rope(x.ctypes.data, T, heads, hd, offset, theta)
+    return x
+
+
+def attention(q, k, v, offset, mode=0):
+    """q[T][nh][hd]; k, v[L][nkv][hd] with L = offset + T -> out[T][nh][hd]."""
+    q = _c(q, np.float32)
+    k = _c(k, np.float32)
+    v = _c(v, np.float32)
+    T, nh, hd = q.shape
+    nkv = k.shape[1]
+    assert k.shape[0] == offset + T and v.shape == k.shape
+    out = np.empty_like(q)
+    lib().orc_attention(q.ctypes.data, k.ctypes.data, v.ctypes.data, T, offset, nh, nkv, hd, out.ctypes.data, mode)
+    return out
+
+
+class ModelOracle:
+    """mlx_model_forward_with_cache_and_lora (mlx_cpp_wrapper_real.cpp:3339-3527) on the CPU with its
+    KV cache: embedding, per layer RMSNorm -> q/k/v (+bias, +LoRA) -> RoPE -> cache -> causal GQA
+    attention -> o_proj (+LoRA) -> residual -> RMSNorm -> SwiGLU MLP (+LoRA) -> residual, final
+    RMSNorm, LM head on the last token. float32 activations throughout (MLX promotes to float32
+    after RoPE).
+
+    cfg: dict of num_layers, hidden, intermediate, num_heads, num_kv_heads, head_dim, vocab,
+    rope_theta, rms_eps. w: {"embed": (packed, scales, biases) or "embed_bf16": uint16 rows,
+    "lm_head": (packed, scales, biases), "norm": [H], "layers": [{"input_norm", "post_norm",
+    "q_proj" .. "down_proj": (packed, scales, biases), "bias": {"q_proj": [out] or None, ..}}]}.
+    lora[layer][a] = {module: (A, B)} for n adapters of one rank; scales[a] = alpha / rank."""
+
+    ATTN = ("q_proj", "k_proj", "v_proj", "o_proj")
+
+    def __init__(self, cfg, w, lora, scales, rank):
+        self.cfg, self.w, self.lora, self.scales, self.rank = cfg, w, lora, scales, rank
+        if "embed" in w:
+            self.embed = dequant(*w["embed"])
+        else:
+            self.embed = (np.ascontiguousarray(w["embed_bf16"], np.uint16).astype(np.uint32) << 16).view(np.float32)
+        self.reset()
+
+    def reset(self):
+        L, nkv, hd = self.cfg["num_layers"], self.cfg["num_kv_heads"], self.cfg["head_dim"]
+        self.kc = [np.zeros((0, nkv, hd), np.float32) for _ in range(L)]
+        self.vc = [np.zeros((0, nkv, hd), np.float32) for _ in range(L)]
+
+    def forward(self, ids, rings, mode=0):
+        c, w = self.cfg, self.w
+        T = len(ids)
+        nh, nkv, hd, eps = c["num_heads"], c["num_kv_heads"], c["head_dim"], c["rms_eps"]
+        offset = self.kc[0].shape[0]
+        x = self.embed[np.asarray(ids)].astype(np.float32)
+        for li, lw in enumerate(w["layers"]):
+            lo = self.lora[li]
+            normed = rmsnorm(x, lw["input_norm"], eps, mode)
+            qkv = []
+            for m in ("q_proj", "k_proj", "v_proj"):
+                y = proj_forward(normed, lw[m], m, self.ATTN, lo, self.scales, self.rank, rings, mode)
+                b = lw.get("bias", {}).get(m)
+                qkv.append(y + np.asarray(b, np.float32) if b is not None else y)
+            q = rope(qkv[0].reshape(T, nh, hd), offset, c["rope_theta"])
+            k = rope(qkv[1].reshape(T, nkv, hd), offset, c["rope_theta"])
+            v = qkv[2].reshape(T, nkv, hd)
+            self.kc[li] = np.concatenate([self.kc[li], k])
+            self.vc[li] = np.concatenate([self.vc[li], v])
+            a = attention(q, self.kc[li], self.vc[li], offset, mode).reshape(T, nh * hd)
+            x = x + proj_forward(a, lw["o_proj"], "o_proj", self.ATTN, lo, self.scales, self.rank, rings, mode)
+            normed = rmsnorm(x, lw["post_norm"], eps, mode)
+            x = x + mlp_forward(normed, lw["gate_proj"], lw["up_proj"], lw["down_proj"], lo, self.scales,
+                                self.rank, rings, mode)
+        final = rmsnorm(x[-1:], w["norm"], eps, mode)
+        return linear_q4(final, *w["lm_head"], mode=mode)[0]
 
 
 def exp(x: float) -> float:
