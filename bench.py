@@ -8,7 +8,10 @@ token (hidden 3584, intermediate 18944, 16 adapters of rank 16, K = 4); the same
 dominant kernel (live per-kernel times from dispatch-recorded HIP events) and the CPU baseline
 (the C oracle on this host's cores, a bounded sample).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-prefill]
+The line also carries the token decode of a whole Qwen2.5-7B-shaped model (embedding, 28 decoder
+layers with attention over a 512-token KV cache, LM head) through aoship_model_forward.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-prefill] [--skip-model]
        python bench.py --probe | --probe-prefill   (workloads for the hardware-counter runs)
 """
 from __future__ import annotations
@@ -247,6 +250,92 @@ def cpu_baseline(W, T: int = 1) -> dict:
     }
 
 
+def model_decode(aoship, W, torch, n_layers: int, ctx: int, steps: int, warmup: int) -> dict:
+    """Token decode of a Qwen2.5-7B-shaped model through aoship_model_forward: n_layers decoder
+    layers (hidden 3584, intermediate 18944, 28 query and 4 key-value heads of 128, rope theta 1e6,
+    vocab 152064, q/k/v biases), each with its own int4 weights on the device (four generated sets
+    reused on the host), 16 rank-16 adapters on all seven projections, the token routed (K=4) by
+    the device router before each step. The KV cache is first filled with ctx - 1 tokens by one
+    prefill call; then each timed step routes one token and runs the whole model for it."""
+    import dataclasses
+
+    mlp = W.CONFIGS[2]
+    attn = W.Config(6, "qwen7b-attn", "attn", mlp.hidden, q_out=3584, kv_out=512, n_adapters=mlp.n_adapters,
+                    rank=mlp.rank, k=mlp.k, modules=("q_proj", "k_proj", "v_proj", "o_proj"))
+    H, I, vocab, nh, nkv, hd = mlp.hidden, mlp.inter, 152064, 28, 4, 128
+    max_seq = ctx + warmup + steps + 8
+    model = aoship.Model(n_layers, H, I, nh, nkv, hd, vocab, max_seq, 1.0e6, 1e-6)
+    sets = []
+    for j in range(4):
+        mc, ac = dataclasses.replace(mlp, cid=100 + j), dataclasses.replace(attn, cid=200 + j)
+        sets.append({**{m: W.base_weights(mc, m) for m in mc.modules}, **{m: W.base_weights(ac, m) for m in ac.modules}})
+    rng = np.random.default_rng(0xAD05)
+    emb = (rng.integers(0, 2 ** 32, (vocab, H // 8), dtype=np.uint32),
+           (rng.standard_normal((vocab, H // 64)) * 0.02).astype(np.float16),
+           (rng.standard_normal((vocab, H // 64)) * 0.01).astype(np.float16))
+    model.set_embedding(*emb)
+    model.set_lm_head(*emb)
+    bias = {m: (rng.standard_normal(n) * 0.02).astype(np.float32) for m, n in (("q_proj", nh * hd), ("k_proj", nkv * hd),
+                                                                                ("v_proj", nkv * hd))}
+    for li in range(n_layers):
+        for m, w in sets[li % 4].items():
+            model.layers[li].set_base(m, *w)
+        for m, b in bias.items():
+            model.set_bias(li, m, b)
+    del sets
+    adapters = []
+    for a in range(mlp.n_adapters):
+        ad = aoship.LoraAdapter(a, n_layers, W.lora_scale(mlp))
+        for cfg in (mlp, attn):
+            for m in cfg.modules:
+                A, B = W.lora_weights(cfg, a, m)
+                for li in range(n_layers):
+                    ad.set_module(li, m, A, B)
+        adapters.append(ad)
+    model.set_adapters(adapters)
+    model.reserve(ctx)
+    router = aoship.Router(mlp.n_adapters, mlp.k, mlp.tau, mlp.eps, 1.0, np.arange(mlp.n_adapters, dtype=np.uint64))
+    f, rw = W.router_inputs(mlp, ctx + warmup + steps)
+    f, rw = torch.from_numpy(f).cuda(), torch.from_numpy(rw).cuda()
+    ids = torch.from_numpy(rng.integers(0, vocab, ctx + warmup + steps).astype(np.int32)).cuda()
+    rings = torch.zeros((ctx + warmup + steps) * 40, dtype=torch.uint8, device="cuda")
+    logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
+    n0 = ctx - 1
+    router.route_features(f[:n0], rw, rings[: n0 * 40])
+    model.forward(ids[:n0], rings[: n0 * 40], logits)
+    torch.cuda.synchronize()
+
+    def step(i):
+        router.route_features(f[i:i + 1], rw, rings[i * 40:(i + 1) * 40])
+        model.forward(ids[i:i + 1], rings[i * 40:(i + 1) * 40], logits)
+
+    for i in range(n0, n0 + warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(n0 + warmup, n0 + warmup + steps):
+        step(i)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    assert bool(torch.isfinite(logits).all())
+    # per layer: int4 weights + f16 scales/biases and the K routed adapters' bf16 rows of all seven
+    # projections, and the bf16 keys and values of the (average) context; then the LM head
+    layer_w = W.algorithmic_bytes(mlp, 1, mlp.k) + W.algorithmic_bytes(attn, 1, attn.k)
+    kv = 2 * nkv * hd * 2 * (ctx + warmup + steps // 2)
+    lm = vocab * H // 2 + vocab * (H // 64) * 4
+    bytes_tok = n_layers * (layer_w + kv) + lm
+    del model, adapters
+    return {
+        "workload": f"Qwen2.5-7B-shaped decoder, {n_layers} layers, 28/4 heads of 128, vocab 152064, int4 g64, "
+                    f"16 rank-16 adapters on all projections, K=4 routed per token, context {ctx}",
+        "layers": n_layers, "context": ctx, "steps": steps,
+        "ms_per_token": ms, "tok_s": 1.0 / (ms * 1e-3),
+        "approx_hbm_bytes_per_token": bytes_tok, "approx_hbm_gbps": bytes_tok / (ms * 1e-3) / 1e9,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +347,10 @@ def main() -> int:
                     help="run the hardware-counter workload only (see probe())")
     ap.add_argument("--probe-prefill", action="store_true",
                     help="run the prefill hardware-counter workload only (see probe_prefill())")
+    ap.add_argument("--skip-model", action="store_true", help="skip the full-model decode line")
+    ap.add_argument("--probe-model", action="store_true",
+                    help="run the full-model decode only (--model-layers layers) and print its figures")
+    ap.add_argument("--model-layers", type=int, default=28)
     ap.add_argument("--layers", type=int, default=4,
                     help="distinct layer copies cycled by the decode steps (defeats the last-level cache)")
     args = ap.parse_args()
@@ -277,6 +370,9 @@ def main() -> int:
         return probe(aoship, W, torch, args.layers)
     if args.probe_prefill:
         return probe_prefill(aoship, W, torch)
+    if args.probe_model:
+        print(json.dumps(model_decode(aoship, W, torch, args.model_layers, 512, 40, 5)), flush=True)
+        return 0
 
     # ---- headline: 7B-shaped decode, one token ----
     T = 1
@@ -367,6 +463,13 @@ def main() -> int:
         log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s; kernels (us): " +
             ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kp.items()))
         del pf
+
+    # ---- the whole decoder, token by token ----
+    if not args.skip_model:
+        md = model_decode(aoship, W, torch, args.model_layers, 512, max(20, args.steps // 8), 5)
+        result["model_decode"] = md
+        log(f"model decode ({md['layers']} layers, context {md['context']}): {md['ms_per_token']:.3f} ms/token, "
+            f"{md['tok_s']:.1f} tok/s, ~{md['approx_hbm_gbps']:.0f} GB/s")
 
     if not args.skip_cpu:
         log("cpu baseline ...")
