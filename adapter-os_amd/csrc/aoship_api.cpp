@@ -886,15 +886,15 @@ static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv
 #ifndef AOS_SHRINK_WGS
 #define AOS_SHRINK_WGS 256
 #endif
-static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp) {
+static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, int waves = 4) {
   int ks = ceil_div(AOS_SHRINK_WGS, rb_total > 0 ? rb_total : 1);
-  int cap = G / 4;
+  int cap = G / waves; /* every wave of a workgroup gets at least one group */
   if (cap < 1) cap = 1;
   if (cap > 16) cap = 16;
   if (ks > cap) ks = cap;
   while (ks < G && 128 + (size_t)T * ceil_div(G, ks) * 128 > AOS_GEMV_LDS_MAX) ++ks;
   size_t lds_x = 128 + (size_t)T * ceil_div(G, ks) * 128;
-  size_t lds_r = (size_t)4 * nv_for(T) * 64 * 4;
+  size_t lds_r = (size_t)waves * nv_for(T) * 64 * 4;
   sp.ks = ks;
   sp.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
 }
@@ -910,6 +910,11 @@ struct Carve {
     uint32_t *p = cbase ? cbase + coff : nullptr;
     coff += n;
     return p;
+  }
+  /* counters starting on a 128-byte line (the base is 256-byte aligned) */
+  uint32_t *counter_lines(size_t n) {
+    coff = (coff + 31) & ~(size_t)31;
+    return counters(n);
   }
 };
 
@@ -933,6 +938,14 @@ struct XShrink {
   bool separate_plan = false;
   aos_shrink_params plan_only;
 };
+
+/* Counter words of a fused launch: the arrival counter and the timeout flag on lines of their
+ * own, then one 128-byte line per GEMV workgroup for its ready flag. */
+static size_t fused_sync_words(const aos_gemv_params *gp, int n) {
+  size_t c = 0;
+  for (int i = 0; i < n; ++i) c += (size_t)gp[i].w0.RB * gp[i].ks;
+  return 64 + 32 * c;
+}
 
 static void plan_x_shrink(aoship_layer *l, Carve &cv, const uint16_t *x, int T, int in,
                           const aos_lora_tab *tabs, int nm, aos_plan *plan,
@@ -960,7 +973,8 @@ static void plan_x_shrink(aoship_layer *l, Carve &cv, const uint16_t *x, int T, 
     sp.S[i] = cv.b.take<float>((size_t)T * sp.s_stride[i]);
     rb_total += sp.n_rb[i];
   }
-  shrink_geometry(rb_total, in / 64, T, sp);
+  /* sized for the waves of the GEMV it may be fused with (valid for the 4-wave launch too) */
+  shrink_geometry(rb_total, in / 64, T, sp, in / 64 >= AOS_GEMV_W8_MIN_G ? 8 : 4);
   sp.part = cv.b.take<float>((size_t)rb_total * sp.ks * nv_for(T) * 64);
   sp.counters = cv.counters((size_t)rb_total + 1);
   xs.separate_plan = !all;
@@ -981,6 +995,7 @@ struct MlpPlan {
   XShrink sx;
   aos_shrink_params sh;
   aos_gemv_params gv1, gv2;
+  uint32_t *sync1, *sync2; /* the fused launches' arrival counter, timeout flag and ready flags */
   size_t bytes = 0, ctr = 0;
 };
 
@@ -1031,7 +1046,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   s2.s_stride[0] = umax * (td.rpad ? td.rpad : 16);
   s2.n_rb[0] = td.rpad ? ceil_div(umax * td.rpad, 32) : 0;
   s2.S[0] = cv.b.take<float>((size_t)T * s2.s_stride[0]);
-  shrink_geometry(s2.n_rb[0], I / 64, T, s2);
+  shrink_geometry(s2.n_rb[0], I / 64, T, s2, 8); /* valid for the 4-wave launch and the 8-wave fused one */
   s2.part = cv.b.take<float>((size_t)(s2.n_rb[0] + 1) * s2.ks * nv_for(T) * 64);
   s2.counters = cv.counters((size_t)s2.n_rb[0] + 1);
 
@@ -1051,9 +1066,12 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.part = cv.b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
   g2.counters = cv.counters((size_t)Wd.RB);
 
+  P.sync1 = cv.counter_lines(fused_sync_words(&g1, 1));
+  P.sync2 = cv.counter_lines(fused_sync_words(&g2, 1));
   P.bytes = cv.b.off + 256;
   P.ctr = cv.coff + 64;
 }
+
 
 /* ---- prefill (T > 32 tokens) ---- */
 
@@ -1249,6 +1267,44 @@ static int launch_x_shrink(aoship_layer *l, XShrink &xs) {
   return launch_err(aos_launch_shrink(&xs.sp, &c1), "lora shrink");
 }
 
+/* A decode shrink and the GEMV that reads its S fused into one launch (the shrink's workgroups
+ * first). Off while AOSHIP_UNFUSED_SHRINK is set in the environment: separate launches of the
+ * same device code, with the same results. */
+static bool fuse_shrinks() { return getenv("AOSHIP_UNFUSED_SHRINK") == nullptr; }
+
+static int shrink_wgs(const aos_shrink_params &sp) {
+  return (sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) + (sp.plan_build.plan ? 1 : 0)) *
+         sp.ks;
+}
+
+static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
+                        int swiglu, int slot, const char *what) {
+  aos_gemv_fused_params f;
+  memset(&f, 0, sizeof(f));
+  f.sp = sp;
+  f.pre_rows = sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) +
+               (sp.plan_build.plan ? 1 : 0);
+  f.n_pre = f.pre_rows * sp.ks;
+  f.n = n;
+  f.sync = sync;          /* its own 128-byte line */
+  f.flags = sync + 64;    /* line 1 holds the timeout flag */
+  int end = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (i < n) {
+      f.gp[i] = gp[i];
+      f.gp[i].sync = f.sync;
+      f.gp[i].flags = f.flags + (size_t)end * 32;
+      f.gp[i].sync_target = (uint32_t)f.n_pre;
+      f.gp[i].timeout = sync + 32;
+      end += gp[i].w0.RB * gp[i].ks;
+    }
+    f.wg_end[i] = end;
+  }
+  f.n_cons = (uint32_t)end;
+  aos_launch_ctx c = launch_ctx(l, slot);
+  return launch_err(aos_launch_gemv_fused(&f, swiglu, &c), what);
+}
+
 extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int T,
                                   const aoship_ring_t *rings, aoship_bf16_t *y) {
   if (check_common(l, x, T, rings, y)) return -1;
@@ -1281,13 +1337,30 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
     plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
     if (ws_reserve(l, P.bytes, P.ctr)) return -1;
     plan_mlp(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, P);
-    if (launch_x_shrink(l, P.sx)) return -1;
-    aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
-    if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
-    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
-    if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;
-    aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
-    if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
+    const bool fuse = fuse_shrinks();
+    if (fuse && P.gv1.has_expand) {
+      aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+      if (P.sx.separate_plan) {
+        if (launch_err(aos_launch_shrink(&P.sx.plan_only, &c0), "adapter plan")) return -1;
+      } else {
+        AOS_SKIP(&c0);
+      }
+      if (launch_fused(l, P.sx.sp, &P.gv1, 1, P.sync1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up")) return -1;
+    } else {
+      if (launch_x_shrink(l, P.sx)) return -1;
+      aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
+      if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
+    }
+    if (fuse && P.gv2.has_expand && P.sh.n_rb[0] > 0) {
+      aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+      AOS_SKIP(&c3);
+      if (launch_fused(l, P.sh, &P.gv2, 1, P.sync2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down")) return -1;
+    } else {
+      aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+      if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;
+      aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
+      if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
+    }
   }
   return 0;
 }
@@ -1339,14 +1412,18 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
       aos_plan *plan = cv.b.take<aos_plan>(1);
       XShrink xs;
       plan_x_shrink(l, cv, xc, Tc, in, tabs, nm, plan, rc, xs);
-      aos_gemv_params gp[3];
+      /* matrices sharing x run in one launch, with a K split sized for their rows together */
+      aos_gemv3_params g3;
+      memset(&g3, 0, sizeof(g3));
+      aos_gemv_params *gp = g3.p;
+      int rb_all = 0;
+      for (int i = 0; i < nm; ++i) rb_all += l->mats[mods[i]].RB;
       for (int i = 0; i < nm; ++i) {
         const Q4Mat &W = l->mats[mods[i]];
-        memset(&gp[i], 0, sizeof(gp[i]));
         gp[i].w0 = W.dev();
         gp[i].x = xc;
         gp[i].T = Tc;
-        gemv_geometry(W.RB, W.G, Tc, false, tabs[i].rpad > 0, gp[i]);
+        gemv_geometry(rb_all, W.G, Tc, false, tabs[i].rpad > 0, gp[i]);
         gp[i].tab0 = tabs[i];
         gp[i].S0 = xs.sp.S[i];
         gp[i].s_stride0 = xs.sp.s_stride[i];
@@ -1357,14 +1434,35 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
         gp[i].counters = cv.counters((size_t)W.RB);
       }
+      uint32_t *sync = cv.counter_lines(fused_sync_words(gp, nm));
       if (pass == 0) {
         if (ws_reserve(l, cv.b.off + 256, cv.coff + 64)) return -1;
         continue;
       }
+      bool expands = false;
+      for (int i = 0; i < nm; ++i) expands = expands || gp[i].has_expand;
+      if (fuse_shrinks() && expands && shrink_wgs(xs.sp) > 0) {
+        aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+        if (xs.separate_plan) {
+          if (launch_err(aos_launch_shrink(&xs.plan_only, &c0), "adapter plan")) return -1;
+        } else {
+          AOS_SKIP(&c0);
+        }
+        if (launch_fused(l, xs.sp, gp, nm, sync, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
+        continue;
+      }
       if (launch_x_shrink(l, xs)) return -1;
-      for (int i = 0; i < nm; ++i) {
-        aos_launch_ctx cg = launch_ctx(l, KS_GEMV_PROJ);
-        if (launch_err(aos_launch_gemv(&gp[i], 0, &cg), "q4 gemv")) return -1;
+      aos_launch_ctx cg = launch_ctx(l, KS_GEMV_PROJ);
+      if (nm == 1) {
+        if (launch_err(aos_launch_gemv(&gp[0], 0, &cg), "q4 gemv")) return -1;
+      } else {
+        g3.n = nm;
+        int end = 0;
+        for (int i = 0; i < 3; ++i) {
+          if (i < nm) end += gp[i].w0.RB * gp[i].ks;
+          g3.wg_end[i] = end;
+        }
+        if (launch_err(aos_launch_gemv3(&g3, &cg), "q4 gemv")) return -1;
       }
     }
   }
@@ -1430,9 +1528,10 @@ extern "C" aoship_model_t *aoship_model_new(const aoship_model_config_t *c) {
   if (ensure_device()) return nullptr;
   if (c->num_layers < 1 || c->hidden < 64 || c->hidden % 64 || c->intermediate < 64 || c->intermediate % 64 ||
       c->num_heads < 1 || c->num_kv_heads < 1 || c->num_heads % c->num_kv_heads || c->head_dim < 8 ||
-      c->head_dim % 8 || c->head_dim > AOS_ATTN_MAX_HD || c->vocab < 32 || c->vocab % 32 || c->max_seq < 1) {
-    set_err("aoship_model_new: unsupported shape (hidden and intermediate multiples of 64, heads divisible by "
-            "kv heads, head_dim a multiple of 8 up to 256, vocab a multiple of 32)");
+      c->head_dim % 8 || c->head_dim > AOS_ATTN_MAX_HD || c->vocab < 32 || c->vocab % 32 || c->max_seq < 1 ||
+      c->hidden > 16384) {
+    set_err("aoship_model_new: unsupported shape (hidden a multiple of 64 up to 16384, intermediate a multiple "
+            "of 64, heads divisible by kv heads, head_dim a multiple of 8 up to 256, vocab a multiple of 32)");
     return nullptr;
   }
   if ((c->num_heads * c->head_dim) % 64 || (c->num_kv_heads * c->head_dim) % 32) {

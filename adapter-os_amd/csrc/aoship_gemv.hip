@@ -26,6 +26,7 @@
  */
 #include "aoship_device.h"
 #include "aoship_internal.h"
+#include "aoship_shrink.h"
 #include <hip/hip_ext.h>
 
 namespace {
@@ -68,18 +69,31 @@ struct ExpandStep {
   u32x4 b;
 };
 
+/* coherent: S and the plan were stored by this launch (a fused launch) and are read with
+ * device-scope loads, which see other workgroups' device-scope stores. */
+__device__ __forceinline__ float load_f(const float *a, bool coherent) {
+  return coherent ? __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *a;
+}
+
 __device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
-                                            int stride, int q, int row, int lane, ExpandStep &e) {
+                                            int stride, int q, int row, int lane, ExpandStep &e,
+                                            bool coherent = false) {
   const int i = lane & 31, c = lane >> 5;
   const int ti = i < p.T ? i : 0;
   const int rpad = tab.rpad;
   const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
-  const int a = p.plan->list[u];
+  const int a = coherent ? (int)__hip_atomic_load(&p.plan->list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : (int)p.plan->list[u];
   const int scol = (p.s_all ? a : u) * rpad + j0 + 8 * c;
   const float *sp = S + (size_t)ti * stride + scol;
-  e.s0 = *(const float4 *)sp;
-  e.s1 = *(const float4 *)(sp + 4);
-  e.cf = i < p.T ? p.plan->coef[ti][u] : 0.0f;
+  if (coherent) {
+    e.s0 = make_float4(load_f(sp, true), load_f(sp + 1, true), load_f(sp + 2, true), load_f(sp + 3, true));
+    e.s1 = make_float4(load_f(sp + 4, true), load_f(sp + 5, true), load_f(sp + 6, true), load_f(sp + 7, true));
+  } else {
+    e.s0 = *(const float4 *)sp;
+    e.s1 = *(const float4 *)(sp + 4);
+  }
+  e.cf = i < p.T ? load_f(&p.plan->coef[ti][u], coherent) : 0.0f;
   const uint16_t *B = tab.B[a];
   const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
   e.b = *(const u32x4 *)bp;
@@ -94,13 +108,13 @@ __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
   f = aos_mfma32(av, e.b, f);
 }
 
+/* Row block rb, K split ksi of one matrix (or of the gate/up pair). */
 template <int NV, bool SW, int W, int D>
-__global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
+__device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int ksi) {
   constexpr int NA = SW ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: keeps the loop scalar */
-  const int rb = blockIdx.x, ksi = blockIdx.y;
   const int G = p.w0.G, in = p.w0.in, T = p.T;
   const int i = lane & 31, c = lane >> 5;
   const int row = rb * 32 + i;
@@ -118,10 +132,11 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
    * step's operands ahead of the K loop, the single-matrix kernel keeps its registers (and its
    * occupancy) and loads them after the K loop */
   const bool expands = p.has_expand != 0;
+  const bool fused = p.sync != nullptr; /* S and the plan are produced by this launch */
   const int q_first = ksi + p.ks * wave, q_step = p.ks * W;
   int nq0 = 0, nq1 = 0;
   ExpandStep e0, e1;
-  if (expands) {
+  if (expands && !fused) {
     const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
     nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
     nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
@@ -237,19 +252,50 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
     }
   }
 
+  /* (4a) fused launch: wait for this workgroup's ready flag, raised once every shrink
+   * workgroup of the grid is done (they have the lowest workgroup ids, so they are dispatched
+   * before any GEMV workgroup, and they never wait), then clear it for the next launch. Each
+   * workgroup polls a line of its own. The wait is bounded: past about a second it gives up,
+   * sets p.timeout and finishes. */
+  if (fused) {
+    __shared__ uint32_t ok;
+    if (tid == 0) {
+      uint32_t *flag = p.flags + ((size_t)ksi * p.w0.RB + rb) * 32;
+      uint32_t spins = 0, done = 1;
+      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins > (1u << 24)) {
+          done = 0;
+          break;
+        }
+      }
+      ok = done;
+      __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    lds_barrier();
+    if (!ok && tid == 0 && p.timeout) *p.timeout = 1u;
+    if (expands) {
+      const int U = __builtin_amdgcn_readfirstlane(
+          __hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
+      nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
+    }
+  }
+
   /* (4b) the expand, added to the waves' accumulators */
   if (expands) {
     f32x16 f0 = {}, f1 = {};
-    if (!SW && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
+    if ((!SW || fused) && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0, fused);
+    if (SW && fused && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1, fused);
     if (q_first < nq0) expand_apply(e0, f0);
     if (SW && q_first < nq1) expand_apply(e1, f1);
     for (int q = q_first + q_step; q < nq0; q += q_step) {
-      expand_load(p, p.tab0, p.S0, p.s_stride0, q, row, lane, e0);
+      expand_load(p, p.tab0, p.S0, p.s_stride0, q, row, lane, e0, fused);
       expand_apply(e0, f0);
     }
     if (SW)
       for (int q = q_first + q_step; q < nq1; q += q_step) {
-        expand_load(p, p.tab1, p.S1, p.s_stride1, q, row, lane, e1);
+        expand_load(p, p.tab1, p.S1, p.s_stride1, q, row, lane, e1, fused);
         expand_apply(e1, f1);
       }
 #pragma unroll
@@ -341,6 +387,92 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
   }
 }
 
+template <int NV, bool SW, int W, int D>
+__global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
+  gemv_body<NV, SW, W, D>(p, blockIdx.x, blockIdx.y);
+}
+
+/* Up to three matrices sharing x (q, k and v) in one launch: workgroup b of the 1-D grid is row
+ * block b % RB, K split b / RB of the matrix whose range of workgroups holds it. */
+template <int NV, int W, int D>
+__global__ void __launch_bounds__(64 * W) aos_gemv3_kernel(aos_gemv3_params mp) {
+  const int b = blockIdx.x;
+  if (b < mp.wg_end[0]) {
+    gemv_body<NV, false, W, D>(mp.p[0], b % mp.p[0].w0.RB, b / mp.p[0].w0.RB);
+  } else if (b < mp.wg_end[1]) {
+    const int r = b - mp.wg_end[0];
+    gemv_body<NV, false, W, D>(mp.p[1], r % mp.p[1].w0.RB, r / mp.p[1].w0.RB);
+  } else {
+    const int r = b - mp.wg_end[1];
+    gemv_body<NV, false, W, D>(mp.p[2], r % mp.p[2].w0.RB, r / mp.p[2].w0.RB);
+  }
+}
+
+/* A shrink (workgroups [0, n_pre)) and the GEMVs consuming its S (the rest) in one launch. Each
+ * shrink workgroup, once its stores are complete, counts itself into sync; the last one raises
+ * every GEMV workgroup's ready flag. */
+template <int NV, bool SW, int W, int D>
+__global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_params fp) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int b = blockIdx.x;
+  if (b < fp.n_pre) {
+    __shared__ uint32_t last;
+    aos_shrink::shrink_block<NV, W, 4>(fp.sp, b % fp.pre_rows, b / fp.pre_rows, smem);
+    /* S and the plan went out as device-scope stores: wait for them, then count this
+     * workgroup in (no cache write-back is needed) */
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(fp.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == (uint32_t)fp.n_pre - 1u;
+      if (last) __hip_atomic_store(fp.sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (last) /* every shrink workgroup is done: raise the GEMV workgroups' flags */
+      for (uint32_t c = threadIdx.x; c < fp.n_cons; c += blockDim.x)
+        __hip_atomic_store(fp.flags + (size_t)c * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int r = b - fp.n_pre;
+  if (SW || r < fp.wg_end[0]) {
+    gemv_body<NV, SW, W, D>(fp.gp[0], r % fp.gp[0].w0.RB, r / fp.gp[0].w0.RB);
+  } else if (r < fp.wg_end[1]) {
+    const int r1 = r - fp.wg_end[0];
+    gemv_body<NV, false, W, D>(fp.gp[1], r1 % fp.gp[1].w0.RB, r1 / fp.gp[1].w0.RB);
+  } else {
+    const int r2 = r - fp.wg_end[1];
+    gemv_body<NV, false, W, D>(fp.gp[2], r2 % fp.gp[2].w0.RB, r2 / fp.gp[2].w0.RB);
+  }
+}
+
+template <int NV>
+int launchf_nv(const aos_gemv_fused_params *fp, int swiglu, const aos_launch_ctx *ctx) {
+  const int nwg = fp->n_pre + (int)fp->n_cons;
+  size_t lds = (size_t)fp->sp.lds_bytes;
+  for (int i = 0; i < fp->n; ++i) lds = lds > (size_t)fp->gp[i].lds_bytes ? lds : (size_t)fp->gp[i].lds_bytes;
+  if (swiglu) {
+    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, true, 4, 4>), dim3(nwg), dim3(256), lds, *fp);
+  } else if (fp->gp[0].waves == 4) {
+    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, false, 4, 12>), dim3(nwg), dim3(256), lds, *fp);
+  } else {
+    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, false, 8, 12>), dim3(nwg), dim3(512), lds, *fp);
+  }
+  return (int)hipGetLastError();
+}
+
+template <int NV>
+int launch3_nv(const aos_gemv3_params *mp, const aos_launch_ctx *ctx) {
+  const int nwg = mp->wg_end[mp->n - 1];
+  size_t lds = 0;
+  for (int i = 0; i < mp->n; ++i) lds = lds > (size_t)mp->p[i].lds_bytes ? lds : (size_t)mp->p[i].lds_bytes;
+  if (mp->p[0].waves == 4) {
+    AOS_LAUNCH(ctx, (aos_gemv3_kernel<NV, 4, 12>), dim3(nwg), dim3(256), lds, *mp);
+  } else {
+    AOS_LAUNCH(ctx, (aos_gemv3_kernel<NV, 8, 12>), dim3(nwg), dim3(512), lds, *mp);
+  }
+  return (int)hipGetLastError();
+}
+
 template <int NV>
 int launch_nv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx) {
   dim3 grid(p->w0.RB, p->ks);
@@ -368,4 +500,55 @@ extern "C" int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_l
   if (T <= 8) return launch_nv<4>(p, swiglu, st);
   if (T <= 16) return launch_nv<8>(p, swiglu, st);
   return launch_nv<16>(p, swiglu, st);
+}
+
+extern "C" int aos_launch_gemv3(const aos_gemv3_params *mp, const aos_launch_ctx *st) {
+  const int n = mp->n;
+  if (n < 1 || n > 3) return (int)hipErrorInvalidValue;
+  const int waves = mp->p[0].waves, T = mp->p[0].T;
+  if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
+  if (T < 1 || T > AOS_DECODE_MAX_T) return (int)hipErrorInvalidValue;
+  int end = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (i < n) {
+      const aos_gemv_params &p = mp->p[i];
+      if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1) return (int)hipErrorInvalidValue;
+      end += p.w0.RB * p.ks;
+    }
+    if (mp->wg_end[i] != end) return (int)hipErrorInvalidValue;
+  }
+  if (T <= 1) return launch3_nv<1>(mp, st);
+  if (T <= 2) return launch3_nv<2>(mp, st);
+  if (T <= 8) return launch3_nv<4>(mp, st);
+  if (T <= 16) return launch3_nv<8>(mp, st);
+  return launch3_nv<16>(mp, st);
+}
+
+extern "C" int aos_launch_gemv_fused(const aos_gemv_fused_params *fp, int swiglu, const aos_launch_ctx *st) {
+  const int n = fp->n;
+  if (n < 1 || n > 3 || (swiglu && n != 1)) return (int)hipErrorInvalidValue;
+  const int waves = fp->gp[0].waves, T = fp->gp[0].T;
+  if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
+  if (swiglu && waves != 4) return (int)hipErrorInvalidValue;
+  if (T < 1 || T > AOS_DECODE_MAX_T || fp->sp.T != T) return (int)hipErrorInvalidValue;
+  if (!fp->sync || !fp->flags || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows ||
+      fp->n_pre / fp->pre_rows != fp->sp.ks)
+    return (int)hipErrorInvalidValue;
+  int end = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (i < n) {
+      const aos_gemv_params &p = fp->gp[i];
+      if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1 || p.sync != fp->sync ||
+          p.flags != fp->flags + (size_t)end * 32 || p.sync_target != (uint32_t)fp->n_pre)
+        return (int)hipErrorInvalidValue;
+      end += p.w0.RB * p.ks;
+    }
+    if (fp->wg_end[i] != end) return (int)hipErrorInvalidValue;
+  }
+  if (fp->n_cons != (uint32_t)end) return (int)hipErrorInvalidValue;
+  if (T <= 1) return launchf_nv<1>(fp, swiglu, st);
+  if (T <= 2) return launchf_nv<2>(fp, swiglu, st);
+  if (T <= 8) return launchf_nv<4>(fp, swiglu, st);
+  if (T <= 16) return launchf_nv<8>(fp, swiglu, st);
+  return launchf_nv<16>(fp, swiglu, st);
 }

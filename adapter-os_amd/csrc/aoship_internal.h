@@ -138,7 +138,39 @@ typedef struct {
   float *yf;          /* plain mode: [T][out] float32 instead of y when not NULL */
   float *part;        /* [RB][ks][NA * NV * 64] */
   uint32_t *counters; /* [RB] zero between launches */
+  /* fused launch (aos_launch_gemv_fused): the shrink that produces S0 / S1 (and the plan) runs
+   * in the first workgroups of the same grid. The last of its sync_target workgroups to finish
+   * raises one ready flag per GEMV workgroup; each GEMV workgroup waits for its own flag (and
+   * clears it) before its expand. NULL sync: S and the plan come from earlier launches. */
+  uint32_t *sync;     /* [1] producer arrivals; zero between launches */
+  uint32_t *flags;    /* this matrix's ready flags [RB * ks * 32], one per 128-byte line */
+  uint32_t sync_target;
+  uint32_t *timeout;  /* set to 1 if a wait gave up (the launch still ends) */
 } aos_gemv_params;
+
+/* A shrink and the GEMVs that consume its S in one launch: workgroups [0, n_pre) run the shrink
+ * (row block b % pre_rows, K split b / pre_rows; pre_rows counts the plan workgroup), workgroup
+ * n_pre + r the GEMV of matrix i for r in [wg_end[i - 1], wg_end[i]) (n = 1 in SwiGLU mode).
+ * gp[i].sync = sync, gp[i].flags = flags + 32 * wg_end[i - 1], gp[i].sync_target = n_pre. */
+typedef struct {
+  aos_shrink_params sp;
+  aos_gemv_params gp[3];
+  int wg_end[3];
+  int n;
+  int n_pre, pre_rows;
+  uint32_t *sync;     /* [1] producer arrivals */
+  uint32_t *flags;    /* [n_cons * 32] */
+  uint32_t n_cons;    /* wg_end[n - 1] */
+} aos_gemv_fused_params;
+
+/* q, k and v (or any n <= 3 matrices with the same x, T and waves) in one launch: matrix i owns
+ * workgroups [wg_end[i - 1], wg_end[i]) of a 1-D grid, wg_end[i] - wg_end[i - 1] = RB_i * ks_i;
+ * entries past n repeat wg_end[n - 1]. */
+typedef struct {
+  aos_gemv_params p[3];
+  int wg_end[3];
+  int n;
+} aos_gemv3_params;
 
 /* ---- prefill path (T > 32 tokens) ----
  * The call's adapter union: list[u] = adapter of union slot u (ascending), slot[a] = u or -1.
@@ -303,6 +335,8 @@ int aos_launch_rope(const aos_rope_params *p, const aos_launch_ctx *ctx);
 int aos_launch_attention(const aos_attn_params *p, const aos_launch_ctx *ctx);
 int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_launch_gemv3(const aos_gemv3_params *p, const aos_launch_ctx *ctx);
+int aos_launch_gemv_fused(const aos_gemv_fused_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx);

@@ -25,98 +25,143 @@ namespace {
 
 /* ---- embedding -------------------------------------------------------------------------------- */
 
+/* One thread per 8 elements of a row (one packed word, or 16 bytes of bfloat16), so every load of
+ * the launch is in flight at once. */
 __global__ void __launch_bounds__(256) aos_embed_kernel(aos_embed_params p) {
-  const int t = blockIdx.x;
+  const int t = blockIdx.y, g = blockIdx.x * 256 + threadIdx.x;
+  if (8 * g >= p.H) return;
   const int id = p.ids[t];
-  float *dst = p.hidden + (size_t)t * p.H;
+  float4 *dst = (float4 *)(p.hidden + (size_t)t * p.H + 8 * g);
   if (id < 0 || id >= p.vocab) {
-    for (int e = threadIdx.x; e < p.H; e += blockDim.x) dst[e] = 0.0f;
-    if (threadIdx.x == 0 && p.status) p.status[0] = 1;
+    dst[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    dst[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (g == 0 && p.status) p.status[0] = 1;
     return;
   }
+  float v[8];
   if (p.q4) {
-    const uint32_t *row = p.q4 + (size_t)id * (p.H / 8);
-    const uint16_t *sr = p.s16 + (size_t)id * (p.H / 64);
-    const uint16_t *br = p.b16 ? p.b16 + (size_t)id * (p.H / 64) : nullptr;
-    for (int e = threadIdx.x; e < p.H; e += blockDim.x) {
-      const uint32_t q = (row[e >> 3] >> (4 * (e & 7))) & 15u; /* low nibble first */
-      const float s = aos_f16_to_f32(sr[e >> 6]);
-      const float b = br ? aos_f16_to_f32(br[e >> 6]) : 0.0f;
-      dst[e] = s * (float)q + b;
-    }
+    const uint32_t w = p.q4[(size_t)id * (p.H / 8) + g];
+    const size_t gi = (size_t)id * (p.H / 64) + (g >> 3);
+    const float s = aos_f16_to_f32(p.s16[gi]);
+    const float b = p.b16 ? aos_f16_to_f32(p.b16[gi]) : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = s * (float)((w >> (4 * e)) & 15u) + b; /* low nibble first */
   } else {
-    const uint16_t *row = p.bf16 + (size_t)id * p.H;
-    for (int e = threadIdx.x; e < p.H; e += blockDim.x) dst[e] = aos_bf16_to_f32(row[e]);
+    const u32x4 r = *(const u32x4 *)(p.bf16 + (size_t)id * p.H + 8 * g);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = __builtin_bit_cast(float, w[e] << 16);
+      v[2 * e + 1] = __builtin_bit_cast(float, w[e] & 0xffff0000u);
+    }
   }
+  dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+  dst[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 /* ---- residual add + RMSNorm ------------------------------------------------------------------- */
 
-__global__ void __launch_bounds__(256) aos_norm_kernel(aos_norm_params p) {
-  __shared__ float red[256];
-  const int t = blockIdx.x, tid = threadIdx.x;
-  float *x = p.hidden + (size_t)t * p.H;
-  const uint16_t *a = p.add ? p.add + (size_t)t * p.H : nullptr;
-  float ss = 0.0f;
-  for (int e = tid; e < p.H; e += 256) {
-    float v = x[e];
-    if (a) {
-      v = v + aos_bf16_to_f32(a[e]);
-      x[e] = v;
+/* One workgroup of 1024 threads per token; each thread holds up to NORM_J runs of 4 elements
+ * (H <= 16384), loaded together before any arithmetic. The sum of squares is formed per thread
+ * in element order, across each wave by a butterfly and across the 16 waves in wave order. */
+constexpr int NORM_J = 4;
+
+__global__ void __launch_bounds__(1024) aos_norm_kernel(aos_norm_params p) {
+  __shared__ float red[16];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, H = p.H;
+  float *x = p.hidden + (size_t)t * H;
+  const uint16_t *a = p.add ? p.add + (size_t)t * H : nullptr;
+  float4 xv[NORM_J], wv[NORM_J];
+  u32x2 av[NORM_J];
+#pragma unroll
+  for (int j = 0; j < NORM_J; ++j) {
+    const int e = 4 * (tid + 1024 * j);
+    if (e < H) {
+      xv[j] = *(const float4 *)(x + e);
+      wv[j] = *(const float4 *)(p.w + e);
+      if (a) av[j] = *(const u32x2 *)(a + e);
     }
-    ss += v * v;
   }
-  red[tid] = ss;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NORM_J; ++j) {
+    const int e = 4 * (tid + 1024 * j);
+    if (e < H) {
+      if (a) {
+        xv[j].x = xv[j].x + __builtin_bit_cast(float, av[j].x << 16);
+        xv[j].y = xv[j].y + __builtin_bit_cast(float, av[j].x & 0xffff0000u);
+        xv[j].z = xv[j].z + __builtin_bit_cast(float, av[j].y << 16);
+        xv[j].w = xv[j].w + __builtin_bit_cast(float, av[j].y & 0xffff0000u);
+        *(float4 *)(x + e) = xv[j];
+      }
+      ss += xv[j].x * xv[j].x;
+      ss += xv[j].y * xv[j].y;
+      ss += xv[j].z * xv[j].z;
+      ss += xv[j].w * xv[j].w;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss = ss + aos_shfl_f(ss, lane ^ o);
+  if (lane == 0) red[tid >> 6] = ss;
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) { /* fixed-order tree */
-    if (tid < w) red[tid] = red[tid] + red[tid + w];
-    __syncthreads();
-  }
-  const float mean = red[0] / (float)p.H;
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) tot += red[w];
+  const float mean = tot / (float)H;
   const float d = sqrtf(mean + p.eps);
-  uint16_t *o = p.out + (size_t)t * p.H;
-  for (int e = tid; e < p.H; e += 256) o[e] = aos_f32_to_bf16(x[e] * (p.w[e] / d));
+  uint16_t *o = p.out + (size_t)t * H;
+#pragma unroll
+  for (int j = 0; j < NORM_J; ++j) {
+    const int e = 4 * (tid + 1024 * j);
+    if (e < H) {
+      u32x2 r;
+      r.x = (uint32_t)aos_f32_to_bf16(xv[j].x * (wv[j].x / d)) | ((uint32_t)aos_f32_to_bf16(xv[j].y * (wv[j].y / d)) << 16);
+      r.y = (uint32_t)aos_f32_to_bf16(xv[j].z * (wv[j].z / d)) | ((uint32_t)aos_f32_to_bf16(xv[j].w * (wv[j].w / d)) << 16);
+      *(u32x2 *)(o + e) = r;
+    }
+  }
 }
 
 /* ---- RoPE, biases, KV cache append ---------------------------------------------------------- */
 
+/* One thread per rotated pair of q or k, or per element of v. */
 __global__ void __launch_bounds__(256) aos_rope_kernel(aos_rope_params p) {
-  const int t = blockIdx.x, half = p.hd / 2;
+  const int t = blockIdx.y, half = p.hd / 2;
   const int pos = p.offset + t;
   const float fpos = (float)pos;
   const int nq = p.nh * half, nk = p.nkv * half, nv = p.nkv * p.hd;
-  for (int w = threadIdx.x; w < nq + nk + nv; w += blockDim.x) {
-    if (w < nq + nk) {
-      const bool isq = w < nq;
-      const int idx = isq ? w : w - nq;
-      const int h = idx / half, i = idx - h * half;
-      const int width = (isq ? p.nh : p.nkv) * p.hd;
-      const uint16_t *src = (isq ? p.q : p.k) + (size_t)t * width + (size_t)h * p.hd;
-      const float *bias = isq ? p.bq : p.bk;
-      float x1 = aos_bf16_to_f32(src[i]), x2 = aos_bf16_to_f32(src[i + half]);
-      if (bias) {
-        x1 = x1 + bias[h * p.hd + i];
-        x2 = x2 + bias[h * p.hd + i + half];
-      }
-      const float ang = fpos * p.inv_freq[i];
-      const float c = cosf(ang), s = sinf(ang);
-      const float r1 = x1 * c - x2 * s, r2 = x1 * s + x2 * c;
-      if (isq) {
-        float *dst = p.qr + ((size_t)t * p.nh + h) * p.hd;
-        dst[i] = r1;
-        dst[i + half] = r2;
-      } else {
-        uint16_t *dst = p.kc + ((size_t)h * p.max_seq + pos) * p.hd;
-        dst[i] = aos_f32_to_bf16(r1);
-        dst[i + half] = aos_f32_to_bf16(r2);
-      }
-    } else {
-      const int idx = w - nq - nk;
-      const int h = idx / p.hd, d = idx - h * p.hd;
-      float v = aos_bf16_to_f32(p.v[(size_t)t * nv + idx]);
-      if (p.bv) v = v + p.bv[idx];
-      p.vc[((size_t)h * p.max_seq + pos) * p.hd + d] = aos_f32_to_bf16(v);
+  const int w = blockIdx.x * 256 + threadIdx.x;
+  if (w >= nq + nk + nv) return;
+  if (w < nq + nk) {
+    const bool isq = w < nq;
+    const int idx = isq ? w : w - nq;
+    const int h = idx / half, i = idx - h * half;
+    const int width = (isq ? p.nh : p.nkv) * p.hd;
+    const uint16_t *src = (isq ? p.q : p.k) + (size_t)t * width + (size_t)h * p.hd;
+    const float *bias = isq ? p.bq : p.bk;
+    float x1 = aos_bf16_to_f32(src[i]), x2 = aos_bf16_to_f32(src[i + half]);
+    if (bias) {
+      x1 = x1 + bias[h * p.hd + i];
+      x2 = x2 + bias[h * p.hd + i + half];
     }
+    const float ang = fpos * p.inv_freq[i];
+    const float c = cosf(ang), s = sinf(ang);
+    const float r1 = x1 * c - x2 * s, r2 = x1 * s + x2 * c;
+    if (isq) {
+      float *dst = p.qr + ((size_t)t * p.nh + h) * p.hd;
+      dst[i] = r1;
+      dst[i + half] = r2;
+    } else {
+      uint16_t *dst = p.kc + ((size_t)h * p.max_seq + pos) * p.hd;
+      dst[i] = aos_f32_to_bf16(r1);
+      dst[i + half] = aos_f32_to_bf16(r2);
+    }
+  } else {
+    const int idx = w - nq - nk;
+    const int h = idx / p.hd, d = idx - h * p.hd;
+    float v = aos_bf16_to_f32(p.v[(size_t)t * nv + idx]);
+    if (p.bv) v = v + p.bv[idx];
+    p.vc[((size_t)h * p.max_seq + pos) * p.hd + d] = aos_f32_to_bf16(v);
   }
 }
 
@@ -134,45 +179,74 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-/* One wave: positions [split * chunk, min(+chunk, visible)) of token t for head h. Phase 1 puts
- * one position on each lane (its score, q . k in order over d), phase 2 one or more dimensions on
- * each lane (acc += p . v over the 64 positions in order). */
+/* One wave: positions [split * chunk, min(+chunk, visible)) of token t for head h, in blocks of
+ * 64. Phase 1 puts one position on each lane: its key row (hd <= 64 * DPL) is loaded whole, then
+ * the score q . k is formed in order over d. Phase 2 puts one or two 32-bit words of the value row
+ * (two dimensions each) on each lane and adds p . v over the block's positions in order. A
+ * block's key rows and its first PB value rows are loaded before anything waits on memory (the
+ * query is staged into LDS behind them), so a block costs about one memory round trip. */
 template <int DPL>
 __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
+  constexpr int NC = 8 * DPL;            /* 16-byte chunks of the longest key row */
+  constexpr int NW = (DPL + 1) / 2;      /* value words per lane */
+  constexpr int PB = DPL > 2 ? 32 : 64;  /* value rows loaded per batch */
   __shared__ float qs[AOS_ATTN_MAX_HD];
   __shared__ float ps[64];
   const int split = blockIdx.x, h = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
-  const int hd = p.hd, kvh = h / (p.nh / p.nkv);
+  const int hd = p.hd, hw = hd / 2, kvh = h / (p.nh / p.nkv);
   const int visible = p.offset + t + 1;
   const int beg = split * p.chunk;
   const int end = min(beg + p.chunk, visible);
   const float *q = p.q + ((size_t)t * p.nh + h) * hd;
-  for (int d = lane; d < hd; d += 64) qs[d] = q[d];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
   const uint16_t *kbase = p.kc + (size_t)kvh * p.max_seq * hd;
-  const uint16_t *vbase = p.vc + (size_t)kvh * p.max_seq * hd;
-  float m = -__builtin_inff(), l = 0.0f, acc[DPL];
+  const uint32_t *vbase = (const uint32_t *)(p.vc + (size_t)kvh * p.max_seq * hd);
+  float m = -__builtin_inff(), l = 0.0f, acc[2 * NW];
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
+  for (int j = 0; j < 2 * NW; ++j) acc[j] = 0.0f;
+  int wi[NW];
+#pragma unroll
+  for (int jw = 0; jw < NW; ++jw) {
+    const int w = lane + 64 * jw;
+    wi[jw] = w < hw ? w : 0;
+  }
   for (int base = beg; base < end; base += 64) {
     const int pos = base + lane;
     const bool valid = pos < end;
-    float s = -__builtin_inff();
-    if (valid) {
-      const u32x4 *kr = (const u32x4 *)(kbase + (size_t)pos * hd);
-      float dot = 0.0f;
-      for (int c = 0; c < hd / 8; ++c) {
-        const u32x4 w = kr[c];
-        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    const int n = min(64, end - base);
+    u32x4 kv[NC];
+    {
+      const u32x4 *kr = (const u32x4 *)(kbase + (size_t)(valid ? pos : base) * hd);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dot = dot + qs[8 * c + 2 * e] * __builtin_bit_cast(float, wv[e] << 16);
-          dot = dot + qs[8 * c + 2 * e + 1] * __builtin_bit_cast(float, wv[e] & 0xffff0000u);
+      for (int c = 0; c < NC; ++c) kv[c] = c < hd / 8 ? kr[c] : kv[0];
+    }
+    uint32_t vv[PB][NW];
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int jj = u < n ? u : n - 1;
+#pragma unroll
+      for (int jw = 0; jw < NW; ++jw) vv[u][jw] = vbase[(size_t)(base + jj) * hw + wi[jw]];
+    }
+    if (base == beg) {
+      for (int d = lane; d < hd; d += 64) qs[d] = q[d];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    }
+    float s = -__builtin_inff();
+    {
+      float dot = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        if (c < hd / 8) {
+          const uint32_t wv[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dot = dot + qs[8 * c + 2 * e] * __builtin_bit_cast(float, wv[e] << 16);
+            dot = dot + qs[8 * c + 2 * e + 1] * __builtin_bit_cast(float, wv[e] & 0xffff0000u);
+          }
         }
       }
-      s = dot * p.scale;
+      if (valid) s = dot * p.scale;
     }
     const float mc = wave_max(s);
     const float mn = fmaxf(m, mc);
@@ -183,14 +257,28 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    const int n = min(64, end - base);
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int d = lane + 64 * j;
-      float a = acc[j] * alpha;
-      if (d < hd)
-        for (int jj = 0; jj < n; ++jj) a = a + ps[jj] * aos_bf16_to_f32(vbase[(size_t)(base + jj) * hd + d]);
-      acc[j] = a;
+    for (int j = 0; j < 2 * NW; ++j) acc[j] = acc[j] * alpha;
+    for (int j0 = 0; j0 < n; j0 += PB) {
+      if (j0 > 0) {
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+          const int jj = j0 + u < n ? j0 + u : n - 1;
+#pragma unroll
+          for (int jw = 0; jw < NW; ++jw) vv[u][jw] = vbase[(size_t)(base + jj) * hw + wi[jw]];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        if (j0 + u < n) {
+          const float pj = ps[j0 + u];
+#pragma unroll
+          for (int jw = 0; jw < NW; ++jw) {
+            acc[2 * jw] = acc[2 * jw] + pj * __builtin_bit_cast(float, vv[u][jw] << 16);
+            acc[2 * jw + 1] = acc[2 * jw + 1] + pj * __builtin_bit_cast(float, vv[u][jw] & 0xffff0000u);
+          }
+        }
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
@@ -198,19 +286,23 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
     m = mn;
   }
   if (p.splits == 1) {
-    uint16_t *o = p.out + (size_t)t * p.nh * hd + (size_t)h * hd;
+    uint32_t *o = (uint32_t *)(p.out + (size_t)t * p.nh * hd + (size_t)h * hd);
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int d = lane + 64 * j;
-      if (d < hd) o[d] = aos_f32_to_bf16(acc[j] / l);
+    for (int jw = 0; jw < NW; ++jw) {
+      const int w = lane + 64 * jw;
+      if (w < hw)
+        o[w] = (uint32_t)aos_f32_to_bf16(acc[2 * jw] / l) | ((uint32_t)aos_f32_to_bf16(acc[2 * jw + 1] / l) << 16);
     }
     return;
   }
   float *pp = p.part + (((size_t)t * p.nh + h) * p.splits + split) * (hd + 2);
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) {
-    const int d = lane + 64 * j;
-    if (d < hd) pp[d] = acc[j];
+  for (int jw = 0; jw < NW; ++jw) {
+    const int w = lane + 64 * jw;
+    if (w < hw) {
+      pp[2 * w] = acc[2 * jw];
+      pp[2 * w + 1] = acc[2 * jw + 1];
+    }
   }
   if (lane == 0) {
     pp[hd] = m;
@@ -219,26 +311,54 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
 }
 
 /* Merge of the splits of (head, token), in split order. A split past the visible positions has
- * max -inf and sum 0 and adds nothing. */
+ * max -inf and sum 0 and adds nothing. The splits' maxima and sums are read one split per lane;
+ * the partial outputs 16 splits at a time. */
+constexpr int ATTN_MAX_SPLITS = 1024;
+constexpr int MERGE_B = 16;
+
 template <int DPL>
 __global__ void __launch_bounds__(64) aos_attn_merge_kernel(aos_attn_params p) {
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, hd = p.hd;
-  const float *pp = p.part + ((size_t)t * p.nh + h) * p.splits * (hd + 2);
-  float M = -__builtin_inff();
-  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, pp[(size_t)s * (hd + 2) + hd]);
+  __shared__ float fs[ATTN_MAX_SPLITS], lf[ATTN_MAX_SPLITS];
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, hd = p.hd, S = p.splits;
+  const float *pp = p.part + ((size_t)t * p.nh + h) * S * (hd + 2);
+  float mloc = -__builtin_inff();
+  for (int s = lane; s < S; s += 64) mloc = fmaxf(mloc, pp[(size_t)s * (hd + 2) + hd]);
+  const float M = wave_max(mloc);
+  for (int s = lane; s < S; s += 64) {
+    const float ms = pp[(size_t)s * (hd + 2) + hd], ls = pp[(size_t)s * (hd + 2) + hd + 1];
+    const bool live = ls > 0.0f;
+    const float f = live ? expf(ms - M) : 0.0f;
+    fs[s] = f;
+    lf[s] = live ? ls * f : 0.0f;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
   float L = 0.0f, acc[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
-  for (int s = 0; s < p.splits; ++s) {
-    const float *q = pp + (size_t)s * (hd + 2);
-    const float ms = q[hd], ls = q[hd + 1];
-    if (!(ls > 0.0f)) continue;
-    const float f = expf(ms - M);
-    L = L + ls * f;
+  int di[DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int d = lane + 64 * j;
-      if (d < hd) acc[j] = acc[j] + q[d] * f;
+  for (int j = 0; j < DPL; ++j) {
+    const int d = lane + 64 * j;
+    di[j] = d < hd ? d : 0;
+  }
+  for (int s0 = 0; s0 < S; s0 += MERGE_B) {
+    float qv[MERGE_B][DPL];
+#pragma unroll
+    for (int u = 0; u < MERGE_B; ++u) {
+      const int s = s0 + u < S ? s0 + u : S - 1;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) qv[u][j] = pp[(size_t)s * (hd + 2) + di[j]];
+    }
+#pragma unroll
+    for (int u = 0; u < MERGE_B; ++u) {
+      if (s0 + u < S && fs[s0 + u] != 0.0f) {
+        const float f = fs[s0 + u];
+        L = L + lf[s0 + u];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = acc[j] + qv[u][j] * f;
+      }
     }
   }
   uint16_t *o = p.out + (size_t)t * p.nh * hd + (size_t)h * hd;
@@ -259,21 +379,26 @@ int launch_attn(const aos_attn_params *p, const aos_launch_ctx *ctx) {
 }  // namespace
 
 extern "C" int aos_launch_embed(const aos_embed_params *p, const aos_launch_ctx *ctx) {
-  AOS_LAUNCH(ctx, aos_embed_kernel, dim3(p->T), dim3(256), 0, *p);
+  if (p->H % 64) return (int)hipErrorInvalidValue;
+  AOS_LAUNCH(ctx, aos_embed_kernel, dim3((p->H / 8 + 255) / 256, p->T), dim3(256), 0, *p);
   return (int)hipGetLastError();
 }
 
 extern "C" int aos_launch_norm(const aos_norm_params *p, const aos_launch_ctx *ctx) {
-  AOS_LAUNCH(ctx, aos_norm_kernel, dim3(p->T), dim3(256), 0, *p);
+  if (p->H % 64 || p->H > 4 * 1024 * NORM_J) return (int)hipErrorInvalidValue;
+  AOS_LAUNCH(ctx, aos_norm_kernel, dim3(p->T), dim3(1024), 0, *p);
   return (int)hipGetLastError();
 }
 
 extern "C" int aos_launch_rope(const aos_rope_params *p, const aos_launch_ctx *ctx) {
-  AOS_LAUNCH(ctx, aos_rope_kernel, dim3(p->T), dim3(256), 0, *p);
+  const int items = p->nh * (p->hd / 2) + p->nkv * (p->hd / 2) + p->nkv * p->hd;
+  AOS_LAUNCH(ctx, aos_rope_kernel, dim3((items + 255) / 256, p->T), dim3(256), 0, *p);
   return (int)hipGetLastError();
 }
 
 extern "C" int aos_launch_attention(const aos_attn_params *p, const aos_launch_ctx *ctx) {
+  if (p->hd % 8 || p->hd > AOS_ATTN_MAX_HD || p->splits < 1 || p->splits > ATTN_MAX_SPLITS || p->chunk % 64)
+    return (int)hipErrorInvalidValue;
   if (p->hd <= 64) return launch_attn<1>(p, ctx);
   if (p->hd <= 128) return launch_attn<2>(p, ctx);
   return launch_attn<4>(p, ctx);

@@ -13,7 +13,8 @@
  * waves of a workgroup and over ks workgroups, a register ring keeping D groups of A in flight
  * per wave, x staged once per workgroup in LDS, v_mfma_f32_32x32x16_bf16 with the tokens as M,
  * and a fixed-order reduction (waves in LDS, workgroups by the last one to finish). S and the
- * plan are read by later launches.
+ * plan are read by later launches, or, in a fused launch, by the GEMV workgroups of the same
+ * grid: S and the plan are therefore stored with device-scope (cache-coherent) stores.
  */
 #ifndef AOSHIP_SHRINK_H
 #define AOSHIP_SHRINK_H
@@ -60,12 +61,12 @@ __device__ void build_plan(const aos_plan_params &pp) {
         const int b = __builtin_ctz(m);
         m &= m - 1u;
         list[u] = (uint16_t)((w << 5) + b);
-        pp.plan->list[u] = list[u];
+        __hip_atomic_store(&pp.plan->list[u], list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ++u;
       }
     }
     cntU = u;
-    pp.plan->U = u;
+    __hip_atomic_store(&pp.plan->U, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   const int U = cntU;
@@ -80,7 +81,7 @@ __device__ void build_plan(const aos_plan_params &pp) {
         c += pp.scale[a] * blend;
       }
     }
-    pp.plan->coef[t][u] = c;
+    aos_publish(&pp.plan->coef[t][u], c);
   }
 }
 
@@ -243,7 +244,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int mt = aos_acc_m(v, lane);
-      if (mt < T) S[(size_t)mt * stride + col] = valid ? tot[v] : 0.0f;
+      if (mt < T) aos_publish(&S[(size_t)mt * stride + col], valid ? tot[v] : 0.0f);
     }
   }
 }

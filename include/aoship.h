@@ -258,7 +258,8 @@ typedef struct {
 } aoship_model_config_t;
 
 /* A model of num_layers layers with its KV cache (mlx_model_load + mlx_kv_cache_new,
- * wrapper.h). hidden and intermediate multiples of 64; num_heads a multiple of num_kv_heads;
+ * wrapper.h). hidden a multiple of 64 up to 16384, intermediate a multiple of 64; num_heads a
+ * multiple of num_kv_heads;
  * head_dim a multiple of 8 up to 256; vocab a multiple of 32. Norm weights start at 1, biases
  * absent. NULL on error. */
 aoship_model_t *aoship_model_new(const aoship_model_config_t *config);

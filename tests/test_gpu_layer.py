@@ -44,6 +44,26 @@ def test_mlp_decode_parity(hip, cid, T):
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
 
 
+@pytest.mark.parametrize("T", [1, 8])
+def test_mlp_decode_unfused_launches(hip, T, monkeypatch):
+    """The decode MLP with each shrink in a launch of its own (AOSHIP_UNFUSED_SHRINK) instead of
+    in the first workgroups of the GEMV launch that reads it: the same tolerance, bit-identical run
+    to run, and the fused path afterwards still matches its own earlier output."""
+    cid = 2
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    fused = _run_mlp(hip, layer, xb, rings)
+    monkeypatch.setenv("AOSHIP_UNFUSED_SHRINK", "1")
+    y1 = _run_mlp(hip, layer, xb, rings)
+    y2 = _run_mlp(hip, layer, xb, rings)
+    monkeypatch.delenv("AOSHIP_UNFUSED_SHRINK")
+    assert np.array_equal(y1, y2), "run-to-run outputs differ"
+    ref = oracle_mlp(cid, xf, rings)
+    assert tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref) <= REL_TOL
+    assert np.array_equal(_run_mlp(hip, layer, xb, rings), fused)
+
+
 def test_mlp_no_adapters_matches_base(hip):
     """Zero gates / empty rings: the layer is the plain int4 SwiGLU MLP."""
     cid, T = 1, 4
@@ -214,10 +234,16 @@ def test_lora_projection_known_answer(hip):
         assert np.all(yf[:, 2:] == 0)
 
 
-def test_attention_projections_parity(hip):
+@pytest.mark.parametrize("unfused", [False, True], ids=["fused", "unfused"])
+@pytest.mark.parametrize("T", [1, 32])
+def test_attention_projections_parity(hip, T, unfused, monkeypatch):
+    """q/k/v in one launch (with the x shrink in its first workgroups, or in a launch of its own)
+    and o: each within tolerance of the oracle and bit-identical run to run."""
     import torch
 
-    cid, T = 4, 32
+    if unfused:
+        monkeypatch.setenv("AOSHIP_UNFUSED_SHRINK", "1")
+    cid = 4
     cfg = W.CONFIGS[cid]
     xb, xf = W.activations(cfg, T)
     rings, _ = rings_for(cid, T)
@@ -231,6 +257,12 @@ def test_attention_projections_parity(hip):
     o = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
     layer.proj_forward("o_proj", x, r, o)  # o's input: any [T, 3072] activation; reuse x
     torch.cuda.synchronize()
+    first = [t.cpu().numpy().copy() for t in (q, k, v, o)]
+    layer.qkv_forward(x, r, q, k, v)
+    layer.proj_forward("o_proj", x, r, o)
+    torch.cuda.synchronize()
+    for a, t in zip(first, (q, k, v, o)):
+        assert np.array_equal(a, t.cpu().numpy()), "run-to-run outputs differ"
     for name, dev in (("q_proj", q), ("k_proj", k), ("v_proj", v), ("o_proj", o)):
         got = W.bf16_bits_to_f32(dev.cpu().numpy().view(np.uint16))
         ref = oracle_proj(cid, name, xf, rings)
