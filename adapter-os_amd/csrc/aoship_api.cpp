@@ -865,9 +865,10 @@ static int nv_for(int T) {
 #ifndef AOS_GEMV_W8_MIN_G
 #define AOS_GEMV_W8_MIN_G 128 /* single-matrix GEMVs with at least this many groups use 8 waves */
 #endif
-static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g) {
+static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g,
+                          int waves_target = AOS_GEMV_WAVES) {
   const int W = swiglu ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
-  int ks = ceil_div(AOS_GEMV_WAVES, RB * W);
+  int ks = ceil_div(waves_target, RB * W);
   int cap = G / W;
   if (cap < 1) cap = 1;
   if (ks > cap) ks = cap;
@@ -881,13 +882,16 @@ static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv
   g.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
 }
 
-/* Shrink geometry: about 1024 waves over the row blocks, at least one group per wave, x slice
- * within the LDS budget, at most 16 K splits (their partials are summed by one workgroup). */
+/* Shrink geometry: a target number of workgroups over the row blocks (512 waves for 4-wave
+ * workgroups, 2048 for 8-wave ones; measured best at decode with the shrink running beside its
+ * GEMV), at least one group per wave, x slice within the LDS budget, at most 16 K splits (their
+ * partials are summed by one workgroup). */
 #ifndef AOS_SHRINK_WGS
 #define AOS_SHRINK_WGS 256
 #endif
 static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, int waves = 4) {
-  int ks = ceil_div(AOS_SHRINK_WGS, rb_total > 0 ? rb_total : 1);
+  const int target = waves == 8 ? AOS_SHRINK_WGS : AOS_SHRINK_WGS / 2;
+  int ks = ceil_div(target, rb_total > 0 ? rb_total : 1);
   int cap = G / waves; /* every wave of a workgroup gets at least one group */
   if (cap < 1) cap = 1;
   if (cap > 16) cap = 16;
@@ -1055,7 +1059,9 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.w0 = Wd.dev();
   g2.x = h;
   g2.T = T;
-  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2);
+  /* the down GEMV streams beside the h shrink of its launch: more K splits (measured: 3 at the
+   * 7B shape) keep its tail short */
+  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, 2 * AOS_GEMV_WAVES);
   g2.tab0 = td;
   g2.S0 = s2.S[0];
   g2.s_stride0 = s2.s_stride[0];
