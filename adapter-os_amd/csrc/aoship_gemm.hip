@@ -129,28 +129,46 @@ struct Stager {
 
 /* One workgroup per M tile of AOS_GEMM_BM tokens. Every workgroup scans all the rings and
  * derives the same union (workgroup 0 stores it); each then writes the coefficient rows of its
- * own tokens and its tile's slot mask. */
-__global__ void __launch_bounds__(256) aos_pplan_kernel(aos_pplan_params p) {
+ * own tokens and its tile's slot mask. Every ring a thread scans, the bound flags and the
+ * scales are loaded before anything waits, so the scan costs one memory round trip. */
+constexpr int PLAN_NT = 1024;
+constexpr int PLAN_RINGS = AOS_PREFILL_MAX_T / PLAN_NT; /* rings per thread */
+
+__global__ void __launch_bounds__(PLAN_NT) aos_pplan_kernel(aos_pplan_params p) {
   __shared__ uint32_t bits[AOS_MAX_ADAPTERS / 32];
   __shared__ uint32_t mask[AOS_MAX_ADAPTERS / 32];
   __shared__ int base[AOS_MAX_ADAPTERS / 32 + 1];
+  __shared__ uint8_t bound_s[AOS_MAX_ADAPTERS];
+  __shared__ float scale_s[AOS_MAX_ADAPTERS];
   const int tid = threadIdx.x;
   const int words = (p.n + 31) >> 5;
-  for (int w = tid; w < words; w += 256) bits[w] = 0u;
-  for (int w = tid; w < p.mwords; w += 256) mask[w] = 0u;
+  u32x2 rw[PLAN_RINGS][5];
+#pragma unroll
+  for (int j = 0; j < PLAN_RINGS; ++j) {
+    const int t = tid + j * PLAN_NT;
+    const u32x2 *r = (const u32x2 *)(p.rings + (t < p.T ? t : p.T - 1));
+#pragma unroll
+    for (int w = 0; w < 5; ++w) rw[j][w] = r[w];
+  }
+  for (int a = tid; a < p.n; a += PLAN_NT) {
+    bound_s[a] = p.bound[a];
+    scale_s[a] = p.scale[a];
+  }
+  for (int w = tid; w < words; w += PLAN_NT) bits[w] = 0u;
+  for (int w = tid; w < p.mwords; w += PLAN_NT) mask[w] = 0u;
   __syncthreads();
-  /* union over every token's active slots: one ring per thread and step, read in 8-byte words */
-  for (int t = tid; t < p.T; t += 256) {
-    const u32x2 *rw = (const u32x2 *)(p.rings + t);
-    const u32x2 w0 = rw[0], w1 = rw[1], w2 = rw[2], w3 = rw[3], w4 = rw[4];
-    const uint32_t k = w0.x;
-    const uint32_t idx[4] = {w1.x, w1.y, w2.x, w2.y}; /* adapter_indices, two per word */
-    const uint32_t gq[4] = {w3.x, w3.y, w4.x, w4.y};  /* gates_q15, two per word */
+  /* union over every token's active slots */
+#pragma unroll
+  for (int j = 0; j < PLAN_RINGS; ++j) {
+    if (tid + j * PLAN_NT >= p.T) continue;
+    const uint32_t k = rw[j][0].x;
+    const uint32_t idx[4] = {rw[j][1].x, rw[j][1].y, rw[j][2].x, rw[j][2].y}; /* adapter_indices */
+    const uint32_t gq[4] = {rw[j][3].x, rw[j][3].y, rw[j][4].x, rw[j][4].y};  /* gates_q15 */
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int a = (int)((idx[s >> 1] >> (16 * (s & 1))) & 0xffffu);
       const int q = (int)(int16_t)((gq[s >> 1] >> (16 * (s & 1))) & 0xffffu);
-      if (s < (int)k && q > 0 && a < p.n && p.bound[a] && !((bits[a >> 5] >> (a & 31)) & 1u))
+      if (s < (int)k && q > 0 && a < p.n && bound_s[a] && !((bits[a >> 5] >> (a & 31)) & 1u))
         atomicOr(&bits[a >> 5], 1u << (a & 31));
     }
   }
@@ -166,7 +184,7 @@ __global__ void __launch_bounds__(256) aos_pplan_kernel(aos_pplan_params p) {
   }
   __syncthreads();
   if (blockIdx.x == 0) {
-    for (int a = tid; a < p.n; a += 256) {
+    for (int a = tid; a < p.n; a += PLAN_NT) {
       const uint32_t m = bits[a >> 5];
       if ((m >> (a & 31)) & 1u) {
         const int u = base[a >> 5] + __builtin_popcount(m & ((1u << (a & 31)) - 1u));
@@ -179,31 +197,50 @@ __global__ void __launch_bounds__(256) aos_pplan_kernel(aos_pplan_params p) {
         p.plan->slot[a] = -1;
       }
     }
-    for (int u = base[words] + tid; u < p.cstride; u += 256)
+    for (int u = base[words] + tid; u < p.cstride; u += PLAN_NT)
       for (int k = 0; k < p.nmod; ++k) p.bp[(size_t)k * p.cstride + u] = nullptr;
   }
-  /* this tile's coefficient rows: zero, then each token's slots in ring order by one thread */
+  /* this tile's coefficient rows: zero, then each token's slots by one thread, summed in ring
+   * order per union slot (a slot named twice adds up in order) */
   const int t0 = blockIdx.x * AOS_GEMM_BM;
   const int tn = (p.T - t0) < AOS_GEMM_BM ? (p.T - t0) : AOS_GEMM_BM;
   const int cs = p.cstride;
-  for (int e = tid; e < tn * cs; e += 256) p.coef[(size_t)t0 * cs + e] = 0.0f;
+  for (int e = tid; e < tn * cs; e += PLAN_NT) p.coef[(size_t)t0 * cs + e] = 0.0f;
   __syncthreads();
   if (tid < tn) {
     const aoship_ring_t &r = p.rings[t0 + tid];
     float *row = p.coef + (size_t)(t0 + tid) * cs;
+    int us[8];
+    float cv[8];
+#pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int a = r.adapter_indices[s];
       const int q = r.gates_q15[s];
-      if (s < (int)r.top_k && q > 0 && a < p.n && p.bound[a]) {
+      us[s] = -1;
+      cv[s] = 0.0f;
+      if (s < (int)r.top_k && q > 0 && a < p.n && bound_s[a]) {
         const uint32_t m = bits[a >> 5];
         const int u = base[a >> 5] + __builtin_popcount(m & ((1u << (a & 31)) - 1u));
-        row[u] += p.scale[a] * ((float)q / 32767.0f);
+        const float c = scale_s[a] * ((float)q / 32767.0f);
+        int first = s;
+#pragma unroll
+        for (int s2 = 0; s2 < s; ++s2)
+          if (first == s && us[s2] == u) first = s2;
+        if (first == s) {
+          us[s] = u;
+          cv[s] = 0.0f + c;
+        } else {
+          cv[first] += c;
+        }
         if (!((mask[u >> 5] >> (u & 31)) & 1u)) atomicOr(&mask[u >> 5], 1u << (u & 31));
       }
     }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (us[s] >= 0) row[us[s]] = cv[s];
   }
   __syncthreads();
-  for (int w = tid; w < p.mwords; w += 256) p.tile_mask[(size_t)blockIdx.x * p.mwords + w] = mask[w];
+  for (int w = tid; w < p.mwords; w += PLAN_NT) p.tile_mask[(size_t)blockIdx.x * p.mwords + w] = mask[w];
 }
 
 /* ------------------------------------------------------------------------------------------ */
@@ -753,7 +790,8 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
 
 extern "C" int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx) {
   const int mtiles = (p->T + AOS_GEMM_BM - 1) / AOS_GEMM_BM;
-  AOS_LAUNCH(ctx, aos_pplan_kernel, dim3(mtiles), dim3(256), 0, *p);
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->n > AOS_MAX_ADAPTERS) return (int)hipErrorInvalidValue;
+  AOS_LAUNCH(ctx, aos_pplan_kernel, dim3(mtiles), dim3(PLAN_NT), 0, *p);
   return (int)hipGetLastError();
 }
 

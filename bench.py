@@ -266,6 +266,30 @@ def cpu_baseline(W, T: int = 1) -> dict:
     }
 
 
+def library_gemm_reference(torch, T: int, H: int, I: int) -> dict:
+    """The vendor library's dense bfloat16 GEMM (torch.mm, hipBLASLt) on the prefill's shapes,
+    with weights already in bfloat16 (no dequantisation, no LoRA, no SwiGLU): the gate and up
+    projections as one [T, H] x [H, 2I] product, and down as [T, I] x [I, H]. A reference point
+    for the int4 kernels, not part of the path."""
+    out = {}
+    for name, (m, k, n) in (("gate_up", (T, H, 2 * I)), ("down", (T, I, H))):
+        a = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(n, k, device="cuda", dtype=torch.bfloat16)
+        for _ in range(3):
+            torch.mm(a, b.t())
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            torch.mm(a, b.t())
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 10 * 1e3
+        out[name] = {"us": us, "tflops": 2 * m * k * n / (us * 1e-6) / 1e12}
+        del a, b
+    return out
+
+
 def model_decode(aoship, W, torch, n_layers: int, ctx: int, steps: int, warmup: int) -> dict:
     """Token decode of a Qwen2.5-7B-shaped model through aoship_model_forward: n_layers decoder
     layers (hidden 3584, intermediate 18944, 28 query and 4 key-value heads of 128, rope theta 1e6,
@@ -478,6 +502,7 @@ def main() -> int:
             "mfma_util_of_measured_peak": tflops / peak_meas if peak_meas else None,
             "kernels_us": {k: v * 1e3 for k, v in kp.items()},
             "gemm_gate_up_tflops": gu_flops / (kp["q4_gemm_gate_up"] * 1e-3) / 1e12 if "q4_gemm_gate_up" in kp else None,
+            "library_bf16_gemm": library_gemm_reference(torch, 2048, H, I),
         }
         log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s; kernels (us): " +
             ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kp.items()))

@@ -167,6 +167,27 @@ def test_mlp_prefill_mixed_rings(hip):
     assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("T", [5, 160])
+def test_mlp_rings_naming_an_adapter_twice(hip, T):
+    """A ring may name one adapter in two slots: both gates apply (the plan sums the two
+    coefficients in ring order), on the decode and the prefill path."""
+    cid = 1
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    rings = rings.copy()
+    rng = np.random.default_rng(T)
+    for t in range(0, T, 2):
+        rings["top_k"][t] = 3
+        a = int(rng.integers(0, cfg.n_adapters))
+        rings["adapter_indices"][t, :3] = [a, (a + 1) % cfg.n_adapters, a]
+        rings["gates_q15"][t, :3] = rng.integers(1000, 20000, 3)
+    layer, ads = gpu_layer(hip, cid)
+    y = _run_mlp(hip, layer, xb, rings)
+    ref = oracle_mlp(cid, xf, rings)
+    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+
+
 def test_projections_prefill_parity(hip):
     """q/k/v and o projections of the 3B-shaped attention layer at 96 tokens (GEMM path)."""
     import torch
