@@ -1516,6 +1516,7 @@ struct aoship_model {
   bool emb_set = false;
   Q4Mat lm;
   DevBuf lm_part, lm_ctr;
+  DevBuf attn_ctr; /* [ws_T][num_heads] split arrivals, zero between launches */
   std::vector<DevBuf> norm_in, norm_post, bias; /* bias: [layer * 3 + {q,k,v}] */
   DevBuf norm_final;
   DevBuf kc, vc; /* [layers][nkv][max_seq][hd] bf16 */
@@ -1714,7 +1715,9 @@ extern "C" int aoship_model_reserve(aoship_model_t *m, int max_tokens) {
   for (auto *l : m->layers)
     if (aoship_layer_reserve(l, max_tokens)) return -1;
   if (max_tokens > m->ws_T) {
-    if (m->ws.alloc(model_ws(m, max_tokens, nullptr).bytes, false)) return -1;
+    if (m->ws.alloc(model_ws(m, max_tokens, nullptr).bytes, false) ||
+        m->attn_ctr.alloc((size_t)max_tokens * m->cfg.num_heads * 4, true))
+      return -1;
     m->ws_T = max_tokens;
   }
   return 0;
@@ -1734,7 +1737,7 @@ extern "C" int aoship_model_forward(aoship_model_t *m, const int32_t *ids, int T
   if (ensure_device()) return -1;
   if (T > m->ws_T) {
     const size_t bytes = model_ws(m, T, nullptr).bytes;
-    if (m->ws.alloc(bytes, false)) return -1;
+    if (m->ws.alloc(bytes, false) || m->attn_ctr.alloc((size_t)T * c.num_heads * 4, true)) return -1;
     m->ws_T = T;
   }
   const ModelWs w = model_ws(m, T, m->ws.p);
@@ -1787,8 +1790,11 @@ extern "C" int aoship_model_forward(aoship_model_t *m, const int32_t *ids, int T
     rp.qr = w.qr;
     rp.kc = m->kc.as<uint16_t>() + (size_t)li * layer_cache;
     rp.vc = m->vc.as<uint16_t>() + (size_t)li * layer_cache;
-    if (launch_err(aos_launch_rope(&rp, &ctx), "rope")) return -1;
+    /* one token: RoPE, the biases and the cache append run inside the attention launch */
+    const bool fuse_rope = T == 1;
+    if (!fuse_rope && launch_err(aos_launch_rope(&rp, &ctx), "rope")) return -1;
     aos_attn_params ap;
+    memset(&ap, 0, sizeof(ap));
     ap.q = w.qr;
     ap.kc = rp.kc;
     ap.vc = rp.vc;
@@ -1803,6 +1809,17 @@ extern "C" int aoship_model_forward(aoship_model_t *m, const int32_t *ids, int T
     ap.scale = 1.0f / std::sqrt((float)hd);
     ap.part = w.part;
     ap.out = w.attn;
+    ap.counters = m->attn_ctr.as<uint32_t>();
+    if (fuse_rope) {
+      ap.rope_fused = 1;
+      ap.qb = w.q;
+      ap.kb = w.k;
+      ap.vb = w.v;
+      ap.bq = rp.bq;
+      ap.bk = rp.bk;
+      ap.bv = rp.bv;
+      ap.inv_freq = rp.inv_freq;
+    }
     if (launch_err(aos_launch_attention(&ap, &ctx), "attention")) return -1;
     if (aoship_proj_forward(l, "o_proj", w.attn, T, rings, w.y)) return -1;
     if (norm(w.y, m->norm_post[(size_t)li], T, w.hidden, w.normed)) return -1;

@@ -297,12 +297,22 @@ typedef struct {
 
 typedef struct {
   const float *q;            /* [T][nh][hd] rotated */
-  const uint16_t *kc, *vc;   /* [nkv][max_seq][hd] */
+  uint16_t *kc, *vc;         /* [nkv][max_seq][hd] (written only with rope_fused) */
   int T, nh, nkv, hd, offset, max_seq;
   int splits, chunk;         /* key positions per split (multiple of 64) */
   float scale;
   float *part;               /* [T][nh][splits][hd + 2]: acc, running max, sum */
   uint16_t *out;             /* [T][nh * hd] bf16 */
+  /* splits > 1: the last wave of (token, head) to finish merges the splits; counters [T][nh]
+   * are zero between launches (that wave resets its own) */
+  uint32_t *counters;
+  /* rope_fused (T == 1): q, k and v come as the bf16 projections below; the attention applies
+   * the biases and RoPE itself, uses the current token's key and value from LDS and appends them
+   * to the cache (kv heads once each); q above is unused */
+  int rope_fused;
+  const uint16_t *qb, *kb, *vb;
+  const float *bq, *bk, *bv;
+  const float *inv_freq;
 } aos_attn_params;
 
 #define AOS_LAUNCH(ctx, kernel, grid, block, lds, ...)                                            \

@@ -185,6 +185,21 @@ __device__ __forceinline__ float wave_sum(float v) {
  * (two dimensions each) on each lane and adds p . v over the block's positions in order. A
  * block's key rows and its first PB value rows are loaded before anything waits on memory (the
  * query is staged into LDS behind them), so a block costs about one memory round trip. */
+constexpr int ATTN_MAX_SPLITS = 1024;
+constexpr int MERGE_B = 16;
+
+/* RoPE of one pair (x1, x2) = (x[i], x[i + hd/2]) at position pos, as the separate RoPE kernel
+ * computes it. */
+__device__ __forceinline__ void rope_pair(float x1, float x2, float fpos, float invf, float &r1, float &r2) {
+  const float ang = fpos * invf;
+  const float c = cosf(ang), s = sinf(ang);
+  r1 = x1 * c - x2 * s;
+  r2 = x1 * s + x2 * c;
+}
+
+template <int DPL>
+__device__ void attn_merge(const aos_attn_params &p, int h, int t, int lane, float *fs, float *lf);
+
 template <int DPL>
 __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
   constexpr int NC = 8 * DPL;            /* 16-byte chunks of the longest key row */
@@ -192,12 +207,17 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
   constexpr int PB = DPL > 2 ? 32 : 64;  /* value rows loaded per batch */
   __shared__ float qs[AOS_ATTN_MAX_HD];
   __shared__ float ps[64];
+  __shared__ __attribute__((aligned(16))) uint32_t kcur[AOS_ATTN_MAX_HD / 2]; /* current key, bf16 pairs */
+  __shared__ uint32_t vcur[AOS_ATTN_MAX_HD / 2];                             /* current value */
   const int split = blockIdx.x, h = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
   const int hd = p.hd, hw = hd / 2, kvh = h / (p.nh / p.nkv);
   const int visible = p.offset + t + 1;
   const int beg = split * p.chunk;
   const int end = min(beg + p.chunk, visible);
   const float *q = p.q + ((size_t)t * p.nh + h) * hd;
+  /* rope_fused: this token's own key and value are formed here, not read from the cache */
+  const int cur = p.offset + t;
+  const bool has_cur = p.rope_fused && beg <= cur && cur < end;
   const uint16_t *kbase = p.kc + (size_t)kvh * p.max_seq * hd;
   const uint32_t *vbase = (const uint32_t *)(p.vc + (size_t)kvh * p.max_seq * hd);
   float m = -__builtin_inff(), l = 0.0f, acc[2 * NW];
@@ -227,10 +247,64 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
       for (int jw = 0; jw < NW; ++jw) vv[u][jw] = vbase[(size_t)(base + jj) * hw + wi[jw]];
     }
     if (base == beg) {
-      for (int d = lane; d < hd; d += 64) qs[d] = q[d];
+      if (p.rope_fused) {
+        const float fpos = (float)cur;
+        const uint16_t *qb = p.qb + (size_t)h * hd;
+        for (int i = lane; i < hw; i += 64) {
+          float x1 = aos_bf16_to_f32(qb[i]), x2 = aos_bf16_to_f32(qb[i + hw]);
+          if (p.bq) {
+            x1 = x1 + p.bq[h * hd + i];
+            x2 = x2 + p.bq[h * hd + i + hw];
+          }
+          rope_pair(x1, x2, fpos, p.inv_freq[i], qs[i], qs[i + hw]);
+        }
+        if (has_cur) {
+          /* the key and value as the cache holds them (bf16); the first head of the group
+           * appends them */
+          const bool writer = h % (p.nh / p.nkv) == 0;
+          const uint16_t *kb = p.kb + (size_t)kvh * hd;
+          uint16_t *kdst = p.kc + ((size_t)kvh * p.max_seq + cur) * hd;
+          for (int i = lane; i < hw; i += 64) {
+            float x1 = aos_bf16_to_f32(kb[i]), x2 = aos_bf16_to_f32(kb[i + hw]);
+            if (p.bk) {
+              x1 = x1 + p.bk[kvh * hd + i];
+              x2 = x2 + p.bk[kvh * hd + i + hw];
+            }
+            float r1, r2;
+            rope_pair(x1, x2, fpos, p.inv_freq[i], r1, r2);
+            const uint16_t b1 = aos_f32_to_bf16(r1), b2 = aos_f32_to_bf16(r2);
+            ((uint16_t *)kcur)[i] = b1;
+            ((uint16_t *)kcur)[i + hw] = b2;
+            if (writer) {
+              kdst[i] = b1;
+              kdst[i + hw] = b2;
+            }
+          }
+          const uint32_t *vb = (const uint32_t *)(p.vb + (size_t)kvh * hd);
+          uint32_t *vdst = (uint32_t *)(p.vc + ((size_t)kvh * p.max_seq + cur) * hd);
+          for (int w = lane; w < hw; w += 64) {
+            const uint32_t pr = vb[w];
+            float v0 = __builtin_bit_cast(float, pr << 16), v1 = __builtin_bit_cast(float, pr & 0xffff0000u);
+            if (p.bv) {
+              v0 = v0 + p.bv[kvh * hd + 2 * w];
+              v1 = v1 + p.bv[kvh * hd + 2 * w + 1];
+            }
+            const uint32_t o = (uint32_t)aos_f32_to_bf16(v0) | ((uint32_t)aos_f32_to_bf16(v1) << 16);
+            vcur[w] = o;
+            if (writer) vdst[w] = o;
+          }
+        }
+      } else {
+        for (int d = lane; d < hd; d += 64) qs[d] = q[d];
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    }
+    if (has_cur && pos == cur) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (c < hd / 8) kv[c] = ((const u32x4 *)kcur)[c];
     }
     float s = -__builtin_inff();
     {
@@ -268,6 +342,15 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
           for (int jw = 0; jw < NW; ++jw) vv[u][jw] = vbase[(size_t)(base + jj) * hw + wi[jw]];
         }
       }
+      if (has_cur && cur >= base + j0 && cur < base + j0 + PB) { /* uniform */
+        const int uc = cur - base - j0;
+#pragma unroll
+        for (int u = 0; u < PB; ++u)
+          if (u == uc) {
+#pragma unroll
+            for (int jw = 0; jw < NW; ++jw) vv[u][jw] = vcur[wi[jw]];
+          }
+      }
 #pragma unroll
       for (int u = 0; u < PB; ++u) {
         if (j0 + u < n) {
@@ -296,36 +379,59 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
     return;
   }
   float *pp = p.part + (((size_t)t * p.nh + h) * p.splits + split) * (hd + 2);
+  if (!p.counters) {
+#pragma unroll
+    for (int jw = 0; jw < NW; ++jw) {
+      const int w = lane + 64 * jw;
+      if (w < hw) {
+        pp[2 * w] = acc[2 * jw];
+        pp[2 * w + 1] = acc[2 * jw + 1];
+      }
+    }
+    if (lane == 0) {
+      pp[hd] = m;
+      pp[hd + 1] = l;
+    }
+    return;
+  }
+  /* device-scope stores, then the arrival count; the last split of (token, head) merges */
 #pragma unroll
   for (int jw = 0; jw < NW; ++jw) {
     const int w = lane + 64 * jw;
     if (w < hw) {
-      pp[2 * w] = acc[2 * jw];
-      pp[2 * w + 1] = acc[2 * jw + 1];
+      aos_publish(pp + 2 * w, acc[2 * jw]);
+      aos_publish(pp + 2 * w + 1, acc[2 * jw + 1]);
     }
   }
   if (lane == 0) {
-    pp[hd] = m;
-    pp[hd + 1] = l;
+    aos_publish(pp + hd, m);
+    aos_publish(pp + hd + 1, l);
   }
+  uint32_t *ctr = p.counters + (size_t)t * p.nh + h;
+  uint32_t old = 0;
+  if (lane == 0) old = aos_arrive(ctr);
+  old = aos_shfl(old, 0);
+  if (old != (uint32_t)p.splits - 1u) return;
+  if (lane == 0) aos_reset(ctr);
+  __shared__ float fs[1024], lf[1024];
+  attn_merge<DPL>(p, h, t, lane, fs, lf);
 }
 
 /* Merge of the splits of (head, token), in split order. A split past the visible positions has
  * max -inf and sum 0 and adds nothing. The splits' maxima and sums are read one split per lane;
  * the partial outputs 16 splits at a time. */
-constexpr int ATTN_MAX_SPLITS = 1024;
-constexpr int MERGE_B = 16;
 
 template <int DPL>
-__global__ void __launch_bounds__(64) aos_attn_merge_kernel(aos_attn_params p) {
-  __shared__ float fs[ATTN_MAX_SPLITS], lf[ATTN_MAX_SPLITS];
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, hd = p.hd, S = p.splits;
+__device__ void attn_merge(const aos_attn_params &p, int h, int t, int lane, float *fs, float *lf) {
+  const int hd = p.hd, S = p.splits;
+  const bool co = p.counters != nullptr; /* partials of this launch: device-scope loads */
+  auto ld = [&](const float *a) { return co ? aos_collect(a) : *a; };
   const float *pp = p.part + ((size_t)t * p.nh + h) * S * (hd + 2);
   float mloc = -__builtin_inff();
-  for (int s = lane; s < S; s += 64) mloc = fmaxf(mloc, pp[(size_t)s * (hd + 2) + hd]);
+  for (int s = lane; s < S; s += 64) mloc = fmaxf(mloc, ld(pp + (size_t)s * (hd + 2) + hd));
   const float M = wave_max(mloc);
   for (int s = lane; s < S; s += 64) {
-    const float ms = pp[(size_t)s * (hd + 2) + hd], ls = pp[(size_t)s * (hd + 2) + hd + 1];
+    const float ms = ld(pp + (size_t)s * (hd + 2) + hd), ls = ld(pp + (size_t)s * (hd + 2) + hd + 1);
     const bool live = ls > 0.0f;
     const float f = live ? expf(ms - M) : 0.0f;
     fs[s] = f;
@@ -349,7 +455,7 @@ __global__ void __launch_bounds__(64) aos_attn_merge_kernel(aos_attn_params p) {
     for (int u = 0; u < MERGE_B; ++u) {
       const int s = s0 + u < S ? s0 + u : S - 1;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) qv[u][j] = pp[(size_t)s * (hd + 2) + di[j]];
+      for (int j = 0; j < DPL; ++j) qv[u][j] = ld(pp + (size_t)s * (hd + 2) + di[j]);
     }
 #pragma unroll
     for (int u = 0; u < MERGE_B; ++u) {
@@ -370,9 +476,15 @@ __global__ void __launch_bounds__(64) aos_attn_merge_kernel(aos_attn_params p) {
 }
 
 template <int DPL>
+__global__ void __launch_bounds__(64) aos_attn_merge_kernel(aos_attn_params p) {
+  __shared__ float fs[ATTN_MAX_SPLITS], lf[ATTN_MAX_SPLITS];
+  attn_merge<DPL>(p, blockIdx.x, blockIdx.y, threadIdx.x, fs, lf);
+}
+
+template <int DPL>
 int launch_attn(const aos_attn_params *p, const aos_launch_ctx *ctx) {
   AOS_LAUNCH(ctx, aos_attn_kernel<DPL>, dim3(p->splits, p->nh, p->T), dim3(64), 0, *p);
-  if (p->splits > 1) AOS_LAUNCH(ctx, aos_attn_merge_kernel<DPL>, dim3(p->nh, p->T), dim3(64), 0, *p);
+  if (p->splits > 1 && !p->counters) AOS_LAUNCH(ctx, aos_attn_merge_kernel<DPL>, dim3(p->nh, p->T), dim3(64), 0, *p);
   return (int)hipGetLastError();
 }
 
@@ -399,6 +511,7 @@ extern "C" int aos_launch_rope(const aos_rope_params *p, const aos_launch_ctx *c
 extern "C" int aos_launch_attention(const aos_attn_params *p, const aos_launch_ctx *ctx) {
   if (p->hd % 8 || p->hd > AOS_ATTN_MAX_HD || p->splits < 1 || p->splits > ATTN_MAX_SPLITS || p->chunk % 64)
     return (int)hipErrorInvalidValue;
+  if (p->rope_fused && (p->T != 1 || !p->qb || !p->kb || !p->vb || !p->inv_freq)) return (int)hipErrorInvalidValue;
   if (p->hd <= 64) return launch_attn<1>(p, ctx);
   if (p->hd <= 128) return launch_attn<2>(p, ctx);
   return launch_attn<4>(p, ctx);

@@ -111,3 +111,31 @@ def test_model_cache_errors(hip):
     with pytest.raises(hip.AosError, match="full"):
         dm.forward(ids, rg, logits)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("hd", [32, 128])
+def test_model_long_context_attention_splits(hip, hd):
+    """Contexts past one 64-position block: the attention runs in several splits whose last wave
+    merges them, for a 190-token prefill (the separate RoPE launch), single-token steps (RoPE and
+    the cache append inside the attention launch) and a 5-token step; every call against the
+    oracle, and the cache written by the single-token steps serves the steps after it."""
+    cfg, w, lora, scales, rank = tiny_model(seed=3, hd=hd, bias=True)
+    rng = np.random.default_rng(hd)
+    spans = [(0, 190), (190, 191), (191, 192), (192, 193), (193, 198), (198, 199)]
+    n = spans[-1][1]
+    ids = rng.integers(0, cfg["vocab"], n)
+    rg = rings(rng, n, len(scales))
+    dm = _device_model(hip, cfg, w, lora, scales, rank, max_seq=256)
+    om = oracle.ModelOracle(cfg, w, lora, scales, rank)
+    for a, b in spans:
+        print(f"hd {hd} span {a}:{b}", flush=True)
+        g = _run(hip, dm, ids[a:b], rg[a:b])
+        r = om.forward(ids[a:b], rg[a:b])
+        ok, worst = _close(g, r)
+        print(f"  worst relative error {worst:.3g}", flush=True)
+        assert ok, f"span {a}:{b}: worst relative error {worst:.3g}"
+    dm.reset_cache()
+    again = [_run(hip, dm, ids[a:b], rg[a:b]) for a, b in spans]
+    dm.reset_cache()
+    third = [_run(hip, dm, ids[a:b], rg[a:b]) for a, b in spans]
+    assert all(np.array_equal(x, y) for x, y in zip(again, third))
