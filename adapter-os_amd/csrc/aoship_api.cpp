@@ -1000,6 +1000,7 @@ struct MlpPlan {
   aos_shrink_params sh;
   aos_gemv_params gv1, gv2;
   uint32_t *sync1, *sync2; /* the fused launches' arrival counter, timeout flag and ready flags */
+  float *hpart;            /* [RB of gate/up][T][s_stride of the down shrink]: the h shrink's partials */
   size_t bytes = 0, ctr = 0;
 };
 
@@ -1072,6 +1073,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.part = cv.b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
   g2.counters = cv.counters((size_t)Wd.RB);
 
+  P.hpart = cv.b.take<float>((size_t)Wg.RB * T * s2.s_stride[0]);
   P.sync1 = cv.counter_lines(fused_sync_words(&g1, 1));
   P.sync2 = cv.counter_lines(fused_sync_words(&g2, 1));
   P.bytes = cv.b.off + 256;
@@ -1284,13 +1286,20 @@ static int shrink_wgs(const aos_shrink_params &sp) {
 }
 
 static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
-                        int swiglu, int slot, const char *what) {
+                        int swiglu, int slot, const char *what, const aos_hsum_params *hs = nullptr) {
   aos_gemv_fused_params f;
   memset(&f, 0, sizeof(f));
-  f.sp = sp;
-  f.pre_rows = sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) +
-               (sp.plan_build.plan ? 1 : 0);
-  f.n_pre = f.pre_rows * sp.ks;
+  if (hs) { /* the first workgroups sum the h shrink's partials instead of running a shrink */
+    f.hsum = 1;
+    f.hs = *hs;
+    f.n_pre = ceil_div(hs->T * hs->stride, AOS_HSUM_V);
+    f.pre_rows = f.n_pre;
+  } else {
+    f.sp = sp;
+    f.pre_rows = sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) +
+                 (sp.plan_build.plan ? 1 : 0);
+    f.n_pre = f.pre_rows * sp.ks;
+  }
   f.n = n;
   f.sync = sync;          /* its own 128-byte line */
   f.flags = sync + 64;    /* line 1 holds the timeout flag */
@@ -1344,6 +1353,10 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
     if (ws_reserve(l, P.bytes, P.ctr)) return -1;
     plan_mlp(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, P);
     const bool fuse = fuse_shrinks();
+    const bool fuse_down = fuse && P.gv2.has_expand && P.sh.n_rb[0] > 0;
+    /* with both launches fused, the gate/up launch also forms the h shrink's partials over its
+     * row blocks, and the down launch only sums them */
+    const bool h_in_gu = fuse && P.gv1.has_expand && fuse_down && Tc <= 2; /* measured: slower at 8 tokens */
     if (fuse && P.gv1.has_expand) {
       aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
       if (P.sx.separate_plan) {
@@ -1351,16 +1364,34 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       } else {
         AOS_SKIP(&c0);
       }
-      if (launch_fused(l, P.sx.sp, &P.gv1, 1, P.sync1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up")) return -1;
+      aos_gemv_params g1 = P.gv1;
+      if (h_in_gu) {
+        g1.htab = P.sh.tab[0];
+        g1.hpart = P.hpart;
+        g1.hstride = P.sh.s_stride[0];
+      }
+      if (launch_fused(l, P.sx.sp, &g1, 1, P.sync1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up")) return -1;
     } else {
       if (launch_x_shrink(l, P.sx)) return -1;
       aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
       if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
     }
-    if (fuse && P.gv2.has_expand && P.sh.n_rb[0] > 0) {
+    if (fuse_down) {
       aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
       AOS_SKIP(&c3);
-      if (launch_fused(l, P.sh, &P.gv2, 1, P.sync2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down")) return -1;
+      aos_hsum_params hs;
+      memset(&hs, 0, sizeof(hs));
+      hs.hpart = P.hpart;
+      hs.RB = P.gv1.w0.RB;
+      hs.T = Tc;
+      hs.stride = P.sh.s_stride[0];
+      hs.rpad = P.sh.tab[0].rpad;
+      hs.plan = P.sh.plan;
+      hs.S = P.sh.S[0];
+      hs.values_per_wg = AOS_HSUM_V;
+      if (launch_fused(l, P.sh, &P.gv2, 1, P.sync2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
+                       h_in_gu ? &hs : nullptr))
+        return -1;
     } else {
       aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
       if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;

@@ -109,6 +109,122 @@ __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
 }
 
 /* Row block rb, K split ksi of one matrix (or of the gate/up pair). */
+/* The down projection's LoRA shrink over the 32 rows of h this row block produced (wave 0 only,
+ * after the SwiGLU): h goes through LDS as a [token][row] bf16 tile (the MFMA's token operand);
+ * the union adapters' A_down rows at these 32 positions are the other operand, 32 union columns
+ * per step; the partials land in hpart[rb][t][col]. The plan was produced by this launch, so it
+ * is read with device-scope loads. */
+/* A_down fragments of union column block cb (32 columns, two 16-row K steps) at this row block */
+__device__ __forceinline__ void h_a_load(const aos_gemv_params &p, int rb, int lane, int U, int cb, u32x4 (&b)[2]) {
+  const int i = lane & 31, c = lane >> 5;
+  const int rpad = p.htab.rpad, in = p.w0.out;
+  const int col = cb * 32 + i;
+  const int u = col / rpad, j = col - u * rpad;
+  const uint16_t *arow = p.zero_row;
+  int step = 0;
+  if (u < U) {
+    const int aid = __hip_atomic_load(&p.plan->list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint16_t *A = p.htab.A[aid];
+    if (A) {
+      arow = A + (size_t)j * in + (size_t)rb * 32 + 8 * c;
+      step = 16;
+    }
+  }
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) b[k2] = *(const u32x4 *)(arow + step * k2);
+}
+
+template <int NV>
+__device__ __forceinline__ void h_shrink_partial(const aos_gemv_params &p, int rb, int lane, const uint16_t (&hb)[NV],
+                                                 unsigned char *smem, int U, const u32x4 (&pre)[2][2]) {
+  const int T = p.T, i = lane & 31, c = lane >> 5;
+  uint32_t *hw = (uint32_t *)smem; /* [32 tokens][32 rows] bf16 */
+#pragma unroll
+  for (int e = 0; e < 8; ++e) hw[lane + 64 * e] = 0u;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  uint16_t *hl = (uint16_t *)smem;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int m = aos_acc_m(v, lane);
+    if (m < T) hl[m * 32 + i] = hb[v];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  u32x4 a[2];
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) a[k2] = *(const u32x4 *)(hl + i * 32 + 16 * k2 + 8 * c);
+  const int cols = U * p.htab.rpad;
+  for (int cb = 0; cb * 32 < cols; ++cb) {
+    const int col = cb * 32 + i;
+    u32x4 b[2];
+    if (cb < 2) { /* loaded right after the wait for the plan */
+      b[0] = cb == 0 ? pre[0][0] : pre[1][0];
+      b[1] = cb == 0 ? pre[0][1] : pre[1][1];
+    } else {
+      h_a_load(p, rb, lane, U, cb, b);
+    }
+    f32x16 acc = {};
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) acc = aos_mfma32(a[k2], b[k2], acc);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int m = aos_acc_m(v, lane);
+      if (m < T && col < cols) p.hpart[((size_t)rb * T + m) * p.hstride + col] = acc[v];
+    }
+  }
+}
+
+/* S[t][col] = sum over the row blocks, in order, of hpart[rb][t][col]: each thread sums row
+ * blocks tid, tid + NT, ... in order, then a fixed pairwise tree over the threads. */
+constexpr int HSUM_V = AOS_HSUM_V;
+template <int NT>
+__device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, unsigned char *smem) {
+  float *red = (float *)smem; /* [HSUM_V][NT] */
+  const int tid = threadIdx.x;
+  const int U = __builtin_amdgcn_readfirstlane(__hip_atomic_load(&hs.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const int cols = U * hs.rpad;
+  float sum[HSUM_V];
+  int t[HSUM_V], col[HSUM_V];
+#pragma unroll
+  for (int k = 0; k < HSUM_V; ++k) {
+    const int idx = b * HSUM_V + k;
+    t[k] = idx / hs.stride;
+    col[k] = idx - t[k] * hs.stride;
+    sum[k] = 0.0f;
+  }
+  for (int r0 = 0; r0 < hs.RB; r0 += 4 * NT) {
+    float v[4][HSUM_V];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = r0 + q * NT + tid;
+#pragma unroll
+      for (int k = 0; k < HSUM_V; ++k) {
+        const bool ok = r < hs.RB && t[k] < hs.T && col[k] < cols;
+        v[q][k] = ok ? hs.hpart[((size_t)r * hs.T + t[k]) * hs.stride + col[k]] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int k = 0; k < HSUM_V; ++k) sum[k] += v[q][k];
+  }
+#pragma unroll
+  for (int k = 0; k < HSUM_V; ++k) red[k * NT + tid] = sum[k];
+  __syncthreads();
+#pragma unroll
+  for (int w = NT / 2; w > 0; w >>= 1) {
+    if (tid < w) {
+#pragma unroll
+      for (int k = 0; k < HSUM_V; ++k) red[k * NT + tid] = red[k * NT + tid] + red[k * NT + tid + w];
+    }
+    __syncthreads();
+  }
+  if (tid < HSUM_V && t[tid] < hs.T && col[tid] < cols) aos_publish(&hs.S[(size_t)t[tid] * hs.stride + col[tid]], red[tid * NT]);
+}
+
 template <int NV, bool SW, int W, int D>
 __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int ksi) {
   constexpr int NA = SW ? 2 : 1;
@@ -133,6 +249,8 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
    * occupancy) and loads them after the K loop */
   const bool expands = p.has_expand != 0;
   const bool fused = p.sync != nullptr; /* S and the plan are produced by this launch */
+  int hU = 0;
+  u32x4 hpre[2][2];
   const int q_first = ksi + p.ks * wave, q_step = p.ks * W;
   int nq0 = 0, nq1 = 0;
   ExpandStep e0, e1;
@@ -279,6 +397,12 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
           __hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
       nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
       nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
+      hU = U;
+    }
+    /* the h shrink's first A_down fragments (wave 0 forms the partials at the end) */
+    if (SW && p.hpart && wave == 0) {
+      h_a_load(p, rb, lane, hU, 0, hpre[0]);
+      h_a_load(p, rb, lane, hU, 1, hpre[1]);
     }
   }
 
@@ -372,9 +496,11 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
 
   /* (7) epilogue */
   const int out = p.w0.out;
+  uint16_t hb[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int m = aos_acc_m(v, lane);
+    hb[v] = 0;
     if (m >= T) continue;
     if (!SW) {
       if (p.yf) p.yf[(size_t)m * out + row] = acc0[v];
@@ -382,9 +508,11 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     } else {
       const float gt = acc0[v], up = acc1[v];
       const float sg = 1.0f / (1.0f + expf(-gt));
-      p.y[(size_t)m * out + row] = aos_f32_to_bf16((gt * sg) * up);
+      hb[v] = aos_f32_to_bf16((gt * sg) * up);
+      p.y[(size_t)m * out + row] = hb[v];
     }
   }
+  if (SW && p.hpart) h_shrink_partial<NV>(p, rb, lane, hb, smem, hU, hpre);
 }
 
 template <int NV, bool SW, int W, int D>
@@ -417,7 +545,10 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
   const int b = blockIdx.x;
   if (b < fp.n_pre) {
     __shared__ uint32_t last;
-    aos_shrink::shrink_block<NV, W, 4>(fp.sp, b % fp.pre_rows, b / fp.pre_rows, smem);
+    if (fp.hsum)
+      hsum_block<64 * W>(fp.hs, b, smem);
+    else
+      aos_shrink::shrink_block<NV, W, 4>(fp.sp, b % fp.pre_rows, b / fp.pre_rows, smem);
     /* S and the plan went out as device-scope stores: wait for them, then count this
      * workgroup in (no cache write-back is needed) */
     __builtin_amdgcn_s_waitcnt(0);
@@ -448,7 +579,7 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
 template <int NV>
 int launchf_nv(const aos_gemv_fused_params *fp, int swiglu, const aos_launch_ctx *ctx) {
   const int nwg = fp->n_pre + (int)fp->n_cons;
-  size_t lds = (size_t)fp->sp.lds_bytes;
+  size_t lds = fp->hsum ? (size_t)HSUM_V * 64 * (fp->gp[0].waves) * 4 : (size_t)fp->sp.lds_bytes;
   for (int i = 0; i < fp->n; ++i) lds = lds > (size_t)fp->gp[i].lds_bytes ? lds : (size_t)fp->gp[i].lds_bytes;
   if (swiglu) {
     AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, true, 4, 4>), dim3(nwg), dim3(256), lds, *fp);
@@ -530,9 +661,12 @@ extern "C" int aos_launch_gemv_fused(const aos_gemv_fused_params *fp, int swiglu
   const int waves = fp->gp[0].waves, T = fp->gp[0].T;
   if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
   if (swiglu && waves != 4) return (int)hipErrorInvalidValue;
-  if (T < 1 || T > AOS_DECODE_MAX_T || fp->sp.T != T) return (int)hipErrorInvalidValue;
-  if (!fp->sync || !fp->flags || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows ||
-      fp->n_pre / fp->pre_rows != fp->sp.ks)
+  if (T < 1 || T > AOS_DECODE_MAX_T || (fp->hsum ? fp->hs.T : fp->sp.T) != T) return (int)hipErrorInvalidValue;
+  if (!fp->sync || !fp->flags || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows)
+    return (int)hipErrorInvalidValue;
+  if (fp->hsum ? (fp->pre_rows != fp->n_pre || !fp->hs.hpart || !fp->hs.S || fp->hs.values_per_wg != HSUM_V ||
+                  (size_t)fp->n_pre * HSUM_V < (size_t)fp->hs.T * fp->hs.stride)
+               : fp->n_pre / fp->pre_rows != fp->sp.ks)
     return (int)hipErrorInvalidValue;
   int end = 0;
   for (int i = 0; i < 3; ++i) {

@@ -146,7 +146,24 @@ typedef struct {
   uint32_t *flags;    /* this matrix's ready flags [RB * ks * 32], one per 128-byte line */
   uint32_t sync_target;
   uint32_t *timeout;  /* set to 1 if a wait gave up (the launch still ends) */
+  /* SwiGLU mode, fused launch: the down projection's LoRA shrink over this row block's 32 rows of
+   * h, hpart[rb][t][col] = sum_r h[t][32 rb + r] A_down(col)[32 rb + r] for the plan's union
+   * columns col < U * htab.rpad (NULL: not formed) */
+  aos_lora_tab htab;
+  float *hpart;
+  int hstride;
 } aos_gemv_params;
+
+/* The sum of those partials over the row blocks, in row-block order: S[t][col] for col <
+ * U * rpad, values_per_wg (= AOS_HSUM_V) consecutive (t, col) values per workgroup. */
+#define AOS_HSUM_V 4
+typedef struct {
+  const float *hpart; /* [RB][T][stride] */
+  int RB, T, stride, rpad;
+  const aos_plan *plan;
+  float *S;           /* [T][stride] */
+  int values_per_wg;
+} aos_hsum_params;
 
 /* A shrink and the GEMVs that consume its S in one launch: workgroups [0, n_pre) run the shrink
  * (row block b % pre_rows, K split b / pre_rows; pre_rows counts the plan workgroup), workgroup
@@ -158,6 +175,8 @@ typedef struct {
   int wg_end[3];
   int n;
   int n_pre, pre_rows;
+  int hsum;           /* 1: the first workgroups run hs (pre_rows = n_pre) instead of the shrink sp */
+  aos_hsum_params hs;
   uint32_t *sync;     /* [1] producer arrivals */
   uint32_t *flags;    /* [n_cons * 32] */
   uint32_t n_cons;    /* wg_end[n - 1] */

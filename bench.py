@@ -151,10 +151,13 @@ def gate_up_bytes(cfg, T: int, U: int) -> int:
     bias, the bf16 LoRA B rows of the U distinct adapters for both modules, x in and h out; with
     the x shrink in the same launch also the U adapters' bf16 A rows for both modules (the shrink
     reads every bound adapter's rows when that is cheaper than waiting for the plan: the excess
-    is traffic above the algorithmic bytes)."""
+    is traffic above the algorithmic bytes), and at 1 or 2 tokens the U adapters' A_down rows,
+    whose products with h this launch forms for the down projection's shrink."""
     H, I = cfg.hidden, cfg.inter
     base = 2 * (I * H // 2 + 2 * 2 * I * (H // 64))
     lora = U * 2 * I * cfg.rank * 2 + (U * 2 * cfg.rank * H * 2 if FUSED else 0)
+    if FUSED and T <= 2:
+        lora += U * cfg.rank * I * 2
     return base + lora + T * H * 2 + T * I * 2
 
 

@@ -31,7 +31,7 @@ def _run_mlp(hip, layer, xb, rings):
     return y.cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("cid,T", [(1, 1), (2, 1), (2, 8)])
+@pytest.mark.parametrize("cid,T", [(1, 1), (2, 1), (2, 2), (2, 8)])
 def test_mlp_decode_parity(hip, cid, T):
     xb, xf = W.activations(W.CONFIGS[cid], T)
     rings, _ = rings_for(cid, T)
