@@ -55,6 +55,7 @@ _SIGS = {
     "aoship_layer_set_stream": (C.c_int, [_P, _P]),
     "aoship_layer_set_profiling": (C.c_int, [_P, C.c_int]),
     "aoship_layer_kernel_stats": (C.c_int, [_P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
+    "aoship_layer_wait_timeouts": (C.c_int, [_P]),
     "aoship_layer_free": (None, [_P]),
     "aoship_mlp_forward": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "aoship_proj_forward": (C.c_int, [_P, C.c_char_p, _P, C.c_int, _P, _P]),
@@ -327,6 +328,13 @@ class Layer:
 
     def set_profiling(self, on: bool) -> None:
         _check(lib().aoship_layer_set_profiling(self.h, 1 if on else 0), "aoship_layer_set_profiling")
+
+    def wait_timeouts(self) -> int:
+        """1 if a fused decode launch's bounded wait gave up since the last call (then cleared)."""
+        r = lib().aoship_layer_wait_timeouts(self.h)
+        if r < 0:
+            raise AosError(last_error())
+        return r
 
     def kernel_stats(self) -> dict:
         out = {}

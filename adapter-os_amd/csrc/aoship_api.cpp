@@ -570,6 +570,7 @@ struct aoship_layer {
   ModTable tabs[AOS_MAX_MODULES];
   DevBuf bound, scale_all; /* [n] per bound adapter: 1 / alpha-over-rank */
   DevBuf zeros;            /* device zeros read by lanes without an adapter row */
+  DevBuf wait_flag;        /* set by a fused launch whose bounded wait gave up */
   DevBuf ws, counters;
   size_t ws_cap = 0, ctr_cap = 0;
   hipStream_t stream = nullptr;
@@ -592,7 +593,7 @@ extern "C" aoship_layer_t *aoship_layer_new(int layer_idx, int group_size, int b
   auto *l = new aoship_layer();
   l->layer_idx = layer_idx;
   for (int i = 0; i < KS_COUNT; ++i) l->stats[i].name = kStatNames[i];
-  if (l->zeros.alloc(256, true)) {
+  if (l->zeros.alloc(256, true) || l->wait_flag.alloc(256, true)) {
     delete l;
     return nullptr;
   }
@@ -783,6 +784,18 @@ extern "C" int aoship_layer_set_profiling(aoship_layer_t *l, int enable) {
     s.launches = 0;
   }
   return 0;
+}
+
+extern "C" int aoship_layer_wait_timeouts(aoship_layer_t *l) {
+  if (!l) return set_err("aoship_layer_wait_timeouts: null layer");
+  if (ensure_device()) return -1;
+  uint32_t v = 0;
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(&v, l->wait_flag.p, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess)
+    return set_err("aoship_layer_wait_timeouts: device error");
+  if (v && hipMemset(l->wait_flag.p, 0, sizeof(v)) != hipSuccess)
+    return set_err("aoship_layer_wait_timeouts: device error");
+  return v ? 1 : 0;
 }
 
 extern "C" int aoship_layer_kernel_stats(aoship_layer_t *l, int idx, const char **name,
@@ -1310,7 +1323,7 @@ static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_
       f.gp[i].sync = f.sync;
       f.gp[i].flags = f.flags + (size_t)end * 32;
       f.gp[i].sync_target = (uint32_t)f.n_pre;
-      f.gp[i].timeout = sync + 32;
+      f.gp[i].timeout = l->wait_flag.as<uint32_t>();
       end += gp[i].w0.RB * gp[i].ks;
     }
     f.wg_end[i] = end;

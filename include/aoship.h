@@ -225,6 +225,14 @@ int aoship_layer_set_profiling(aoship_layer_t *layer, int enable);
 int aoship_layer_kernel_stats(aoship_layer_t *layer, int idx, const char **name,
                               double *total_ms, int64_t *launches);
 
+/* Health of the layer's decode launches (part of the metrics surface, FusedKernels::get_metrics,
+ * crates/adapteros-lora-kernel-api/src/lib.rs:559): at decode each LoRA shrink runs in the first
+ * workgroups of the GEMV launch that reads its result, and the GEMV workgroups wait for it with a
+ * bounded wait (about a second). Returns 1 if such a wait gave up since the last call (the
+ * outputs of that forward are then invalid), else 0, and clears the flag; -1 on error.
+ * Synchronises the device. */
+int aoship_layer_wait_timeouts(aoship_layer_t *layer);
+
 void aoship_layer_free(aoship_layer_t *layer);
 
 /* SwiGLU MLP with LoRA on gate/up/down (mlx_cpp_wrapper_real.cpp:3509-3527):

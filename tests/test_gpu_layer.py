@@ -38,6 +38,7 @@ def test_mlp_decode_parity(hip, cid, T):
     layer, ads = gpu_layer(hip, cid)
     y1 = _run_mlp(hip, layer, xb, rings)
     y2 = _run_mlp(hip, layer, xb, rings)
+    assert layer.wait_timeouts() == 0
     assert np.array_equal(y1, y2), "run-to-run outputs differ"
     ref = oracle_mlp(cid, xf, rings)
     ratio = tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
