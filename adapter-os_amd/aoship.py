@@ -58,6 +58,7 @@ _SIGS = {
     "aoship_layer_wait_timeouts": (C.c_int, [_P]),
     "aoship_layer_free": (None, [_P]),
     "aoship_mlp_forward": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "aoship_route_mlp_forward": (C.c_int, [_P, _P, _P, C.c_int, _P, _P, C.c_int, _P, _P, _P]),
     "aoship_proj_forward": (C.c_int, [_P, C.c_char_p, _P, C.c_int, _P, _P]),
     "aoship_qkv_forward": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P]),
     "aoship_model_new": (_P, [_P]),
@@ -351,6 +352,14 @@ class Layer:
 
     def mlp_forward(self, x, rings, y) -> None:
         _check(lib().aoship_mlp_forward(self.h, _ptr(x), x.shape[0], _ptr(rings), _ptr(y)), "aoship_mlp_forward")
+
+    def route_mlp_forward(self, router, features, router_w, x, rings, y, status=None) -> None:
+        """Route the tokens from features (device float32 [T, d]) and run the MLP on them in one
+        call; rings (device uint8 [T * 40]) receive the decisions."""
+        T, d = features.shape
+        _check(lib().aoship_route_mlp_forward(router.h, _ptr(features), _ptr(router_w), d, self.h, _ptr(x), T,
+                                              _ptr(rings), None if status is None else _ptr(status), _ptr(y)),
+               "aoship_route_mlp_forward")
 
     def proj_forward(self, module: str, x, rings, y) -> None:
         _check(lib().aoship_proj_forward(self.h, module.encode(), _ptr(x), x.shape[0], _ptr(rings), _ptr(y)),

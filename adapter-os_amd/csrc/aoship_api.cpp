@@ -363,15 +363,10 @@ extern "C" int aoship_router_set_stream(aoship_router_t *r, void *stream) {
 
 extern "C" void aoship_router_free(aoship_router_t *r) { delete r; }
 
-static int route_common(aoship_router_t *r, const float *features, const float *router_w, int d,
-                        const float *priors_in, int T, aoship_ring_t *rings, float *priors_out,
-                        int32_t *status) {
-  if (!r) return set_err("aoship_route: null router");
-  if (T < 0 || T > (1 << 22)) return set_err("aoship_route: T out of range");
-  if (T == 0) return 0;
-  if (!rings) return set_err("aoship_route: null rings");
-  if (ensure_device()) return -1;
-  aos_route_params p;
+/* The launch parameters of a routing call (T >= 1), validated. */
+static int route_fill(aoship_router_t *r, const float *features, const float *router_w, int d,
+                      const float *priors_in, int T, aoship_ring_t *rings, float *priors_out, int32_t *status,
+                      aos_route_params &p) {
   memset(&p, 0, sizeof(p));
   p.n = r->n;
   p.d = d;
@@ -413,7 +408,20 @@ static int route_common(aoship_router_t *r, const float *features, const float *
   } else if (!priors_in) {
     return set_err("aoship_route: null priors");
   }
-  aos_launch_ctx ctx = {r->stream, nullptr, nullptr};
+  return 0;
+}
+
+static int route_common(aoship_router_t *r, const float *features, const float *router_w, int d,
+                        const float *priors_in, int T, aoship_ring_t *rings, float *priors_out,
+                        int32_t *status, hipStream_t stream) {
+  if (!r) return set_err("aoship_route: null router");
+  if (T < 0 || T > (1 << 22)) return set_err("aoship_route: T out of range");
+  if (T == 0) return 0;
+  if (!rings) return set_err("aoship_route: null rings");
+  if (ensure_device()) return -1;
+  aos_route_params p;
+  if (route_fill(r, features, router_w, d, priors_in, T, rings, priors_out, status, p)) return -1;
+  aos_launch_ctx ctx = {stream, nullptr, nullptr};
   int e = aos_launch_route(&p, &ctx);
   if (e != 0) return set_err(std::string("route launch: ") + hipGetErrorString((hipError_t)e));
   return 0;
@@ -421,14 +429,14 @@ static int route_common(aoship_router_t *r, const float *features, const float *
 
 extern "C" int aoship_route(aoship_router_t *r, const float *priors, int T, aoship_ring_t *rings,
                             int32_t *status) {
-  return route_common(r, nullptr, nullptr, 0, priors, T, rings, nullptr, status);
+  return route_common(r, nullptr, nullptr, 0, priors, T, rings, nullptr, status, r ? r->stream : nullptr);
 }
 
 extern "C" int aoship_route_features(aoship_router_t *r, const float *features,
                                      const float *router_w, int d, int T, aoship_ring_t *rings,
                                      float *priors_out, int32_t *status) {
   if (!features) return set_err("aoship_route_features: null features");
-  return route_common(r, features, router_w, d, nullptr, T, rings, priors_out, status);
+  return route_common(r, features, router_w, d, nullptr, T, rings, priors_out, status, r ? r->stream : nullptr);
 }
 
 /* ------------------------------------------------------------------------------------------ */
@@ -1014,6 +1022,7 @@ struct MlpPlan {
   aos_gemv_params gv1, gv2;
   uint32_t *sync1, *sync2; /* the fused launches' arrival counter, timeout flag and ready flags */
   float *hpart;            /* [RB of gate/up][T][s_stride of the down shrink]: the h shrink's partials */
+  uint32_t *route_done;    /* the combined route + gate/up launch's router arrivals */
   size_t bytes = 0, ctr = 0;
 };
 
@@ -1087,6 +1096,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.counters = cv.counters((size_t)Wd.RB);
 
   P.hpart = cv.b.take<float>((size_t)Wg.RB * T * s2.s_stride[0]);
+  P.route_done = cv.counter_lines(32);
   P.sync1 = cv.counter_lines(fused_sync_words(&g1, 1));
   P.sync2 = cv.counter_lines(fused_sync_words(&g2, 1));
   P.bytes = cv.b.off + 256;
@@ -1298,9 +1308,8 @@ static int shrink_wgs(const aos_shrink_params &sp) {
          sp.ks;
 }
 
-static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
-                        int swiglu, int slot, const char *what, const aos_hsum_params *hs = nullptr) {
-  aos_gemv_fused_params f;
+static void make_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
+                       const aos_hsum_params *hs, aos_gemv_fused_params &f) {
   memset(&f, 0, sizeof(f));
   if (hs) { /* the first workgroups sum the h shrink's partials instead of running a shrink */
     f.hsum = 1;
@@ -1329,8 +1338,93 @@ static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_
     f.wg_end[i] = end;
   }
   f.n_cons = (uint32_t)end;
+}
+
+static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
+                        int swiglu, int slot, const char *what, const aos_hsum_params *hs = nullptr) {
+  aos_gemv_fused_params f;
+  make_fused(l, sp, gp, n, sync, hs, f);
   aos_launch_ctx c = launch_ctx(l, slot);
   return launch_err(aos_launch_gemv_fused(&f, swiglu, &c), what);
+}
+
+/* One decode chunk (T <= 32 tokens) of the MLP. rp (may be NULL): the plain router's parameters
+ * for these tokens, which then run in the gate/up launch (rings written there); the caller has
+ * checked that the gate/up launch is fused. */
+static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const aoship_ring_t *rings, uint16_t *y,
+                            const aos_route_params *rp) {
+  MlpPlan P;
+  plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+  if (ws_reserve(l, P.bytes, P.ctr)) return -1;
+  plan_mlp(l, Tc, x, rings, y, l->ws.p, l->counters.p, P);
+  const bool fuse = fuse_shrinks();
+  const bool fuse_down = fuse && P.gv2.has_expand && P.sh.n_rb[0] > 0;
+  /* with both launches fused, the gate/up launch also forms the h shrink's partials over its
+   * row blocks, and the down launch only sums them */
+  const bool h_in_gu = fuse && P.gv1.has_expand && fuse_down && Tc <= 2; /* measured: slower at 8 tokens */
+  const bool route_in_gu = rp && fuse && P.gv1.has_expand && !P.sx.separate_plan;
+  if (rp && !route_in_gu) { /* route first, on the layer's stream */
+    aos_launch_ctx cr = {l->stream, nullptr, nullptr};
+    if (launch_err(aos_launch_route(rp, &cr), "route")) return -1;
+  }
+  if (route_in_gu) {
+    aos_gemv_params g1 = P.gv1;
+    if (h_in_gu) {
+      g1.htab = P.sh.tab[0];
+      g1.hpart = P.hpart;
+      g1.hstride = P.sh.s_stride[0];
+    }
+    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+    AOS_SKIP(&c0);
+    aos_route_gu_params q;
+    memset(&q, 0, sizeof(q));
+    q.rp = *rp;
+    make_fused(l, P.sx.sp, &g1, 1, P.sync1, nullptr, q.fp);
+    q.route_done = P.route_done;
+    aos_launch_ctx cg = launch_ctx(l, KS_GEMV_GU);
+    if (launch_err(aos_launch_route_gate_up(&q, &cg), "route + lora shrink + q4 gemv gate/up")) return -1;
+  } else if (fuse && P.gv1.has_expand) {
+    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+    if (P.sx.separate_plan) {
+      if (launch_err(aos_launch_shrink(&P.sx.plan_only, &c0), "adapter plan")) return -1;
+    } else {
+      AOS_SKIP(&c0);
+    }
+    aos_gemv_params g1 = P.gv1;
+    if (h_in_gu) {
+      g1.htab = P.sh.tab[0];
+      g1.hpart = P.hpart;
+      g1.hstride = P.sh.s_stride[0];
+    }
+    if (launch_fused(l, P.sx.sp, &g1, 1, P.sync1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up")) return -1;
+  } else {
+    if (launch_x_shrink(l, P.sx)) return -1;
+    aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
+    if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
+  }
+  if (fuse_down) {
+    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+    AOS_SKIP(&c3);
+    aos_hsum_params hs;
+    memset(&hs, 0, sizeof(hs));
+    hs.hpart = P.hpart;
+    hs.RB = P.gv1.w0.RB;
+    hs.T = Tc;
+    hs.stride = P.sh.s_stride[0];
+    hs.rpad = P.sh.tab[0].rpad;
+    hs.plan = P.sh.plan;
+    hs.S = P.sh.S[0];
+    hs.values_per_wg = AOS_HSUM_V;
+    if (launch_fused(l, P.sh, &P.gv2, 1, P.sync2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
+                     h_in_gu ? &hs : nullptr))
+      return -1;
+  } else {
+    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+    if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;
+    aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
+    if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
+  }
+  return 0;
 }
 
 extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int T,
@@ -1361,58 +1455,33 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
   }
   for (int t0 = 0; t0 < T; t0 += AOS_DECODE_MAX_T) {
     const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;
-    MlpPlan P;
-    plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
-    if (ws_reserve(l, P.bytes, P.ctr)) return -1;
-    plan_mlp(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, P);
-    const bool fuse = fuse_shrinks();
-    const bool fuse_down = fuse && P.gv2.has_expand && P.sh.n_rb[0] > 0;
-    /* with both launches fused, the gate/up launch also forms the h shrink's partials over its
-     * row blocks, and the down launch only sums them */
-    const bool h_in_gu = fuse && P.gv1.has_expand && fuse_down && Tc <= 2; /* measured: slower at 8 tokens */
-    if (fuse && P.gv1.has_expand) {
-      aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
-      if (P.sx.separate_plan) {
-        if (launch_err(aos_launch_shrink(&P.sx.plan_only, &c0), "adapter plan")) return -1;
-      } else {
-        AOS_SKIP(&c0);
-      }
-      aos_gemv_params g1 = P.gv1;
-      if (h_in_gu) {
-        g1.htab = P.sh.tab[0];
-        g1.hpart = P.hpart;
-        g1.hstride = P.sh.s_stride[0];
-      }
-      if (launch_fused(l, P.sx.sp, &g1, 1, P.sync1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up")) return -1;
-    } else {
-      if (launch_x_shrink(l, P.sx)) return -1;
-      aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
-      if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
-    }
-    if (fuse_down) {
-      aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
-      AOS_SKIP(&c3);
-      aos_hsum_params hs;
-      memset(&hs, 0, sizeof(hs));
-      hs.hpart = P.hpart;
-      hs.RB = P.gv1.w0.RB;
-      hs.T = Tc;
-      hs.stride = P.sh.s_stride[0];
-      hs.rpad = P.sh.tab[0].rpad;
-      hs.plan = P.sh.plan;
-      hs.S = P.sh.S[0];
-      hs.values_per_wg = AOS_HSUM_V;
-      if (launch_fused(l, P.sh, &P.gv2, 1, P.sync2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
-                       h_in_gu ? &hs : nullptr))
-        return -1;
-    } else {
-      aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
-      if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;
-      aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
-      if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
-    }
+    if (mlp_decode_chunk(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, nullptr)) return -1;
   }
   return 0;
+}
+
+/* Routing from features and the MLP of one layer in one call: at decode the router runs in the
+ * first workgroups of the gate/up launch, beside the x shrink and the weight stream. */
+extern "C" int aoship_route_mlp_forward(aoship_router_t *r, const float *features, const float *router_w, int d,
+                                        aoship_layer_t *l, const aoship_bf16_t *x, int T, aoship_ring_t *rings,
+                                        int32_t *status, aoship_bf16_t *y) {
+  if (!r || !features) return set_err("aoship_route_mlp_forward: null router or features");
+  if (check_common(l, x, T, rings, y)) return -1;
+  if (!l->mats[MOD_GATE].valid || !l->mats[MOD_UP].valid || !l->mats[MOD_DOWN].valid)
+    return set_err("aoship_route_mlp_forward: gate_proj, up_proj and down_proj must be set");
+  const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
+  if (Wu.in != Wg.in || Wu.out != Wg.out || Wd.in != Wg.out || Wd.out != Wg.in)
+    return set_err("aoship_route_mlp_forward: gate/up/down shapes are inconsistent");
+  if (ensure_device()) return -1;
+  aos_route_params rp;
+  if (route_fill(r, features, router_w, d, nullptr, T, rings, nullptr, status, rp)) return -1;
+  const bool plain = !(rp.scope || rp.tie_key || rp.post_allowed || rp.active_ids || rp.strengths || rp.hashes);
+  if (T > AOS_DECODE_MAX_T || !plain) { /* routing first, then the layer, both on the layer's stream */
+    aos_launch_ctx cr = {l->stream, nullptr, nullptr};
+    if (launch_err(aos_launch_route(&rp, &cr), "route")) return -1;
+    return aoship_mlp_forward(l, x, T, rings, y);
+  }
+  return mlp_decode_chunk(l, T, x, rings, y, &rp);
 }
 
 /* One or more projections sharing the input x. */

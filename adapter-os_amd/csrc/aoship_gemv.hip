@@ -24,496 +24,12 @@
  *     (waves through LDS, workgroups by the last one to finish), so results are bit-identical
  *     run to run with no floating-point atomics.
  */
-#include "aoship_device.h"
-#include "aoship_internal.h"
-#include "aoship_shrink.h"
+#include "aoship_gemv.h"
 #include <hip/hip_ext.h>
 
 namespace {
 
-constexpr int XE = 4; /* x staging: 16-byte loads per thread issued ahead of the weights */
-
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-/* Apply one group's scale and bias to the accumulators. Lanes whose token m >= T read a
- * clamped (valid) sum; their accumulators are never stored, so no branch is needed. */
-template <int NV>
-__device__ __forceinline__ void apply_group(const f32x16 &t, uint32_t sbv, const float *xs, int GR, int gl,
-                                            int T, int lane, float (&acc)[NV]) {
-  const float s = aos_f16_to_f32(sbv & 0xffffu);
-  const float b = aos_f16_to_f32(sbv >> 16);
-  const float bp = fmaf(-128.0f, s, b);
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    int m = aos_acc_m(v, lane);
-    m = m < T ? m : T - 1;
-    const float sx = xs[(m * GR + gl) * 2] + xs[(m * GR + gl) * 2 + 1];
-    acc[v] = fmaf(s, t[v], fmaf(bp, sx, acc[v]));
-  }
-}
-
-/* bf16 pair from two floats, round to nearest even */
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return (uint32_t)aos_f32_to_bf16(lo) | ((uint32_t)aos_f32_to_bf16(hi) << 16);
-}
-
-/* One LoRA expand step of a wave: union slot u = 16 q / rpad, rank rows j0 .. j0 + 15. The A
- * operand is coef(t, u) * S[t, col(u) + j0 + 8c ..], the B operand B_list[u][row, j0 + 8c ..]. */
-struct ExpandStep {
-  float4 s0, s1;
-  float cf;
-  u32x4 b;
-};
-
-/* coherent: S and the plan were stored by this launch (a fused launch) and are read with
- * device-scope loads, which see other workgroups' device-scope stores. */
-__device__ __forceinline__ float load_f(const float *a, bool coherent) {
-  return coherent ? __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *a;
-}
-
-__device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
-                                            int stride, int q, int row, int lane, ExpandStep &e,
-                                            bool coherent = false) {
-  const int i = lane & 31, c = lane >> 5;
-  const int ti = i < p.T ? i : 0;
-  const int rpad = tab.rpad;
-  const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
-  const int a = coherent ? (int)__hip_atomic_load(&p.plan->list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                         : (int)p.plan->list[u];
-  const int scol = (p.s_all ? a : u) * rpad + j0 + 8 * c;
-  const float *sp = S + (size_t)ti * stride + scol;
-  if (coherent) {
-    e.s0 = make_float4(load_f(sp, true), load_f(sp + 1, true), load_f(sp + 2, true), load_f(sp + 3, true));
-    e.s1 = make_float4(load_f(sp + 4, true), load_f(sp + 5, true), load_f(sp + 6, true), load_f(sp + 7, true));
-  } else {
-    e.s0 = *(const float4 *)sp;
-    e.s1 = *(const float4 *)(sp + 4);
-  }
-  e.cf = i < p.T ? load_f(&p.plan->coef[ti][u], coherent) : 0.0f;
-  const uint16_t *B = tab.B[a];
-  const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
-  e.b = *(const u32x4 *)bp;
-}
-
-__device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
-  u32x4 av;
-  av.x = pack_bf16(e.cf * e.s0.x, e.cf * e.s0.y);
-  av.y = pack_bf16(e.cf * e.s0.z, e.cf * e.s0.w);
-  av.z = pack_bf16(e.cf * e.s1.x, e.cf * e.s1.y);
-  av.w = pack_bf16(e.cf * e.s1.z, e.cf * e.s1.w);
-  f = aos_mfma32(av, e.b, f);
-}
-
-/* Row block rb, K split ksi of one matrix (or of the gate/up pair). */
-/* The down projection's LoRA shrink over the 32 rows of h this row block produced (wave 0 only,
- * after the SwiGLU): h goes through LDS as a [token][row] bf16 tile (the MFMA's token operand);
- * the union adapters' A_down rows at these 32 positions are the other operand, 32 union columns
- * per step; the partials land in hpart[rb][t][col]. The plan was produced by this launch, so it
- * is read with device-scope loads. */
-/* A_down fragments of union column block cb (32 columns, two 16-row K steps) at this row block */
-__device__ __forceinline__ void h_a_load(const aos_gemv_params &p, int rb, int lane, int U, int cb, u32x4 (&b)[2]) {
-  const int i = lane & 31, c = lane >> 5;
-  const int rpad = p.htab.rpad, in = p.w0.out;
-  const int col = cb * 32 + i;
-  const int u = col / rpad, j = col - u * rpad;
-  const uint16_t *arow = p.zero_row;
-  int step = 0;
-  if (u < U) {
-    const int aid = __hip_atomic_load(&p.plan->list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint16_t *A = p.htab.A[aid];
-    if (A) {
-      arow = A + (size_t)j * in + (size_t)rb * 32 + 8 * c;
-      step = 16;
-    }
-  }
-#pragma unroll
-  for (int k2 = 0; k2 < 2; ++k2) b[k2] = *(const u32x4 *)(arow + step * k2);
-}
-
-template <int NV>
-__device__ __forceinline__ void h_shrink_partial(const aos_gemv_params &p, int rb, int lane, const uint16_t (&hb)[NV],
-                                                 unsigned char *smem, int U, const u32x4 (&pre)[2][2]) {
-  const int T = p.T, i = lane & 31, c = lane >> 5;
-  uint32_t *hw = (uint32_t *)smem; /* [32 tokens][32 rows] bf16 */
-#pragma unroll
-  for (int e = 0; e < 8; ++e) hw[lane + 64 * e] = 0u;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-  uint16_t *hl = (uint16_t *)smem;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int m = aos_acc_m(v, lane);
-    if (m < T) hl[m * 32 + i] = hb[v];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-  u32x4 a[2];
-#pragma unroll
-  for (int k2 = 0; k2 < 2; ++k2) a[k2] = *(const u32x4 *)(hl + i * 32 + 16 * k2 + 8 * c);
-  const int cols = U * p.htab.rpad;
-  for (int cb = 0; cb * 32 < cols; ++cb) {
-    const int col = cb * 32 + i;
-    u32x4 b[2];
-    if (cb < 2) { /* loaded right after the wait for the plan */
-      b[0] = cb == 0 ? pre[0][0] : pre[1][0];
-      b[1] = cb == 0 ? pre[0][1] : pre[1][1];
-    } else {
-      h_a_load(p, rb, lane, U, cb, b);
-    }
-    f32x16 acc = {};
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) acc = aos_mfma32(a[k2], b[k2], acc);
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int m = aos_acc_m(v, lane);
-      if (m < T && col < cols) p.hpart[((size_t)rb * T + m) * p.hstride + col] = acc[v];
-    }
-  }
-}
-
-/* S[t][col] = sum over the row blocks, in order, of hpart[rb][t][col]: each thread sums row
- * blocks tid, tid + NT, ... in order, then a fixed pairwise tree over the threads. */
-constexpr int HSUM_V = AOS_HSUM_V;
-template <int NT>
-__device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, unsigned char *smem) {
-  float *red = (float *)smem; /* [HSUM_V][NT] */
-  const int tid = threadIdx.x;
-  const int U = __builtin_amdgcn_readfirstlane(__hip_atomic_load(&hs.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  const int cols = U * hs.rpad;
-  float sum[HSUM_V];
-  int t[HSUM_V], col[HSUM_V];
-#pragma unroll
-  for (int k = 0; k < HSUM_V; ++k) {
-    const int idx = b * HSUM_V + k;
-    t[k] = idx / hs.stride;
-    col[k] = idx - t[k] * hs.stride;
-    sum[k] = 0.0f;
-  }
-  for (int r0 = 0; r0 < hs.RB; r0 += 4 * NT) {
-    float v[4][HSUM_V];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = r0 + q * NT + tid;
-#pragma unroll
-      for (int k = 0; k < HSUM_V; ++k) {
-        const bool ok = r < hs.RB && t[k] < hs.T && col[k] < cols;
-        v[q][k] = ok ? hs.hpart[((size_t)r * hs.T + t[k]) * hs.stride + col[k]] : 0.0f;
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int k = 0; k < HSUM_V; ++k) sum[k] += v[q][k];
-  }
-#pragma unroll
-  for (int k = 0; k < HSUM_V; ++k) red[k * NT + tid] = sum[k];
-  __syncthreads();
-#pragma unroll
-  for (int w = NT / 2; w > 0; w >>= 1) {
-    if (tid < w) {
-#pragma unroll
-      for (int k = 0; k < HSUM_V; ++k) red[k * NT + tid] = red[k * NT + tid] + red[k * NT + tid + w];
-    }
-    __syncthreads();
-  }
-  if (tid < HSUM_V && t[tid] < hs.T && col[tid] < cols) aos_publish(&hs.S[(size_t)t[tid] * hs.stride + col[tid]], red[tid * NT]);
-}
-
-template <int NV, bool SW, int W, int D>
-__device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int ksi) {
-  constexpr int NA = SW ? 2 : 1;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: keeps the loop scalar */
-  const int G = p.w0.G, in = p.w0.in, T = p.T;
-  const int i = lane & 31, c = lane >> 5;
-  const int row = rb * 32 + i;
-  const uint32_t qmask = aos_q4_mask(), qexp = aos_q4_exp();
-
-  float acc0[NV], acc1[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    acc0[v] = 0.0f;
-    acc1[v] = 0.0f;
-  }
-
-  /* the expand: steps q of each module are dealt round-robin to the row block's ks workgroups
-   * and then to their waves (q = ksi + ks * (wave + W * j)); the SwiGLU kernel loads its first
-   * step's operands ahead of the K loop, the single-matrix kernel keeps its registers (and its
-   * occupancy) and loads them after the K loop */
-  const bool expands = p.has_expand != 0;
-  const bool fused = p.sync != nullptr; /* S and the plan are produced by this launch */
-  int hU = 0;
-  u32x4 hpre[2][2];
-  const int q_first = ksi + p.ks * wave, q_step = p.ks * W;
-  int nq0 = 0, nq1 = 0;
-  ExpandStep e0, e1;
-  if (expands && !fused) {
-    const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
-    nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
-    nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
-    if (SW && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
-    if (SW && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1);
-  }
-  {
-    const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
-    const int GR = gw1 - gw0;
-    const int ga = gw0 + wave * GR / W, gb = gw0 + (wave + 1) * GR / W, ng = gb - ga;
-
-    /* (1) first x staging loads, ahead of the weights. Loads are unconditional (addresses
-     * clamped into range) so no control flow separates them from their use and the compiler
-     * can wait for exactly the load it needs. */
-    const int xchunks = GR * 8; /* 16-byte chunks per token row */
-    const int nx = T * xchunks;
-    u32x4 xv[XE];
-#pragma unroll
-    for (int j = 0; j < XE; ++j) {
-      int idx = tid + j * 64 * W;
-      idx = idx < nx ? idx : nx - 1;
-      const int t = idx / xchunks, r = idx - t * xchunks;
-      xv[j] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
-    }
-
-    /* (2) the ring: groups ga .. ga+D-1 (every wave has at least one group) */
-    const u32x4 *q0 = (const u32x4 *)p.w0.qt + ((size_t)rb * G + ga) * 64 + lane;
-    const uint32_t *s0 = p.w0.sb + ((size_t)rb * G + ga) * 32 + i;
-    const u32x4 *q1 = SW ? (const u32x4 *)p.w1.qt + ((size_t)rb * G + ga) * 64 + lane : nullptr;
-    const uint32_t *s1 = SW ? p.w1.sb + ((size_t)rb * G + ga) * 32 + i : nullptr;
-    u32x4 wa[D], wb[D];
-    uint32_t sa[D], sb[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int jj = d < ng ? d : ng - 1;
-      wa[d] = q0[(size_t)jj * 64];
-      sa[d] = s0[(size_t)jj * 32];
-      if (SW) {
-        wb[d] = q1[(size_t)jj * 64];
-        sb[d] = s1[(size_t)jj * 32];
-      }
-    }
-
-    /* (3) x -> LDS (rest of the staging after the ring is in flight), group sums. LDS holds
-     * 128 zero bytes (read by lanes without a token), the T x rows, then the group sums. */
-    uint16_t *xl = (uint16_t *)(smem + 128);
-    float *xs = (float *)(smem + 128 + (size_t)T * GR * 128);
-    if (tid < 32) ((uint32_t *)smem)[tid] = 0u;
-    const int xstride = GR * 64;
-#pragma unroll
-    for (int j = 0; j < XE; ++j) {
-      const int idx = tid + j * 64 * W;
-      if (idx < nx) {
-        const int t = idx / xchunks, r = idx - t * xchunks;
-        *(u32x4 *)(xl + (size_t)t * xstride + r * 8) = xv[j];
-      }
-    }
-    for (int idx = tid + XE * 64 * W; idx < nx; idx += 64 * W) {
-      const int t = idx / xchunks, r = idx - t * xchunks;
-      *(u32x4 *)(xl + (size_t)t * xstride + r * 8) =
-          *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
-    }
-    lds_barrier();
-    for (int idx = tid; idx < T * GR * 2; idx += 64 * W) {
-      const int t = idx / (GR * 2), rem = idx - t * GR * 2;
-      const u32x4 *src = (const u32x4 *)(xl + (size_t)t * xstride + rem * 32);
-      const u32x4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-      const uint32_t w[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
-                              v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
-      float s = 0.0f; /* the 32 elements in order */
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s += __builtin_bit_cast(float, w[e] << 16);
-        s += __builtin_bit_cast(float, w[e] & 0xffff0000u);
-      }
-      xs[idx] = s;
-    }
-    lds_barrier();
-
-    /* (4) consume the ring, refilling each slot D groups ahead (refills past the end reload
-     * the last group and are never used). x fragment address: lanes with a token step through
-     * their row, the others stay on the zero block. */
-    const int xbase = i < T ? 128 + i * xstride * 2 + 64 * c : 0;
-    const int xmult = i < T ? 128 : 0;
-    for (int base = 0; base < ng; base += D) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const int j = base + d;
-        if (j < ng) {
-          const int gl = ga + j - gw0;
-          f32x16 t0 = {}, t1 = {};
-          u32x4 a[4];
-#pragma unroll
-          for (int st = 0; st < 4; ++st)
-            a[st] = *(const u32x4 *)(smem + xbase + (size_t)gl * xmult + 16 * st);
-#pragma unroll
-          for (int st = 0; st < 4; ++st) {
-            t0 = aos_mfma32(a[st], aos_q4_magic(wa[d][st], qmask, qexp), t0);
-            if (SW) t1 = aos_mfma32(a[st], aos_q4_magic(wb[d][st], qmask, qexp), t1);
-          }
-          apply_group<NV>(t0, sa[d], xs, GR, gl, T, lane, acc0);
-          if (SW) apply_group<NV>(t1, sb[d], xs, GR, gl, T, lane, acc1);
-        }
-        int jn = j + D;
-        jn = jn < ng ? jn : ng - 1;
-        wa[d] = q0[(size_t)jn * 64];
-        sa[d] = s0[(size_t)jn * 32];
-        if (SW) {
-          wb[d] = q1[(size_t)jn * 64];
-          sb[d] = s1[(size_t)jn * 32];
-        }
-      }
-    }
-  }
-
-  /* (4a) fused launch: wait for this workgroup's ready flag, raised once every shrink
-   * workgroup of the grid is done (they have the lowest workgroup ids, so they are dispatched
-   * before any GEMV workgroup, and they never wait), then clear it for the next launch. Each
-   * workgroup polls a line of its own. The wait is bounded: past about a second it gives up,
-   * sets p.timeout and finishes. */
-  if (fused) {
-    __shared__ uint32_t ok;
-    if (tid == 0) {
-      uint32_t *flag = p.flags + ((size_t)ksi * p.w0.RB + rb) * 32;
-      uint32_t spins = 0, done = 1;
-      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins > (1u << 24)) {
-          done = 0;
-          break;
-        }
-      }
-      ok = done;
-      __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    lds_barrier();
-    if (!ok && tid == 0 && p.timeout) *p.timeout = 1u;
-    if (expands) {
-      const int U = __builtin_amdgcn_readfirstlane(
-          __hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
-      nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
-      hU = U;
-    }
-    /* the h shrink's first A_down fragments (wave 0 forms the partials at the end) */
-    if (SW && p.hpart && wave == 0) {
-      h_a_load(p, rb, lane, hU, 0, hpre[0]);
-      h_a_load(p, rb, lane, hU, 1, hpre[1]);
-    }
-  }
-
-  /* (4b) the expand, added to the waves' accumulators */
-  if (expands) {
-    f32x16 f0 = {}, f1 = {};
-    if ((!SW || fused) && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0, fused);
-    if (SW && fused && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1, fused);
-    if (q_first < nq0) expand_apply(e0, f0);
-    if (SW && q_first < nq1) expand_apply(e1, f1);
-    for (int q = q_first + q_step; q < nq0; q += q_step) {
-      expand_load(p, p.tab0, p.S0, p.s_stride0, q, row, lane, e0, fused);
-      expand_apply(e0, f0);
-    }
-    if (SW)
-      for (int q = q_first + q_step; q < nq1; q += q_step) {
-        expand_load(p, p.tab1, p.S1, p.s_stride1, q, row, lane, e1, fused);
-        expand_apply(e1, f1);
-      }
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      acc0[v] += f0[v];
-      if (SW) acc1[v] += f1[v];
-    }
-  }
-
-  /* (5) fixed-order reduction over the waves (LDS reused once every wave is done with x) */
-  float *red = (float *)smem;
-  lds_barrier();
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    red[(wave * NA * NV + v) * 64 + lane] = acc0[v];
-    if (SW) red[(wave * NA * NV + NV + v) * 64 + lane] = acc1[v];
-  }
-  lds_barrier();
-  if (wave != 0) return;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float a0 = red[v * 64 + lane], a1 = SW ? red[(NV + v) * 64 + lane] : 0.0f;
-    for (int w = 1; w < W; ++w) {
-      a0 += red[(w * NA * NV + v) * 64 + lane];
-      if (SW) a1 += red[(w * NA * NV + NV + v) * 64 + lane];
-    }
-    acc0[v] = a0;
-    acc1[v] = a1;
-  }
-
-  /* (6) fixed-order reduction over the workgroups of this row block: the last one sums */
-  const int nsplit = p.ks;
-  if (nsplit > 1) {
-    float *part = p.part + ((size_t)rb * nsplit + ksi) * (NA * NV * 64);
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      aos_publish(part + v * 64 + lane, acc0[v]);
-      if (SW) aos_publish(part + (NV + v) * 64 + lane, acc1[v]);
-    }
-    uint32_t old = 0;
-    if (lane == 0) old = aos_arrive(&p.counters[rb]);
-    old = aos_shfl(old, 0);
-    if (old != (uint32_t)nsplit - 1u) return;
-    if (lane == 0) aos_reset(&p.counters[rb]);
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      acc0[v] = 0.0f;
-      acc1[v] = 0.0f;
-    }
-    /* partials are read 4 at a time (all loads in flight together) and summed in order */
-    for (int k0 = 0; k0 < nsplit; k0 += 4) {
-      float v0[4][NV], v1[4][NV];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int k = k0 + kk < nsplit ? k0 + kk : nsplit - 1;
-        const float *pp = p.part + ((size_t)rb * nsplit + k) * (NA * NV * 64);
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          v0[kk][v] = aos_collect(pp + v * 64 + lane);
-          v1[kk][v] = SW ? aos_collect(pp + (NV + v) * 64 + lane) : 0.0f;
-        }
-      }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        if (k0 + kk < nsplit) {
-#pragma unroll
-          for (int v = 0; v < NV; ++v) {
-            acc0[v] += v0[kk][v];
-            if (SW) acc1[v] += v1[kk][v];
-          }
-        }
-    }
-  }
-
-  /* (7) epilogue */
-  const int out = p.w0.out;
-  uint16_t hb[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int m = aos_acc_m(v, lane);
-    hb[v] = 0;
-    if (m >= T) continue;
-    if (!SW) {
-      if (p.yf) p.yf[(size_t)m * out + row] = acc0[v];
-      else p.y[(size_t)m * out + row] = aos_f32_to_bf16(acc0[v]);
-    } else {
-      const float gt = acc0[v], up = acc1[v];
-      const float sg = 1.0f / (1.0f + expf(-gt));
-      hb[v] = aos_f32_to_bf16((gt * sg) * up);
-      p.y[(size_t)m * out + row] = hb[v];
-    }
-  }
-  if (SW && p.hpart) h_shrink_partial<NV>(p, rb, lane, hb, smem, hU, hpre);
-}
+using namespace aos_gemv;
 
 template <int NV, bool SW, int W, int D>
 __global__ void __launch_bounds__(64 * W) aos_gemv_kernel(aos_gemv_params p) {
@@ -544,24 +60,7 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int b = blockIdx.x;
   if (b < fp.n_pre) {
-    __shared__ uint32_t last;
-    if (fp.hsum)
-      hsum_block<64 * W>(fp.hs, b, smem);
-    else
-      aos_shrink::shrink_block<NV, W, 4>(fp.sp, b % fp.pre_rows, b / fp.pre_rows, smem);
-    /* S and the plan went out as device-scope stores: wait for them, then count this
-     * workgroup in (no cache write-back is needed) */
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(fp.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = old == (uint32_t)fp.n_pre - 1u;
-      if (last) __hip_atomic_store(fp.sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (last) /* every shrink workgroup is done: raise the GEMV workgroups' flags */
-      for (uint32_t c = threadIdx.x; c < fp.n_cons; c += blockDim.x)
-        __hip_atomic_store(fp.flags + (size_t)c * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fused_producer<NV, W>(fp, b, smem, nullptr, 0);
     return;
   }
   const int r = b - fp.n_pre;

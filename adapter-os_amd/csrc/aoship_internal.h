@@ -182,6 +182,16 @@ typedef struct {
   uint32_t n_cons;    /* wg_end[n - 1] */
 } aos_gemv_fused_params;
 
+/* Routing from features and the fused gate/up launch in one grid: workgroups [0, rp.T) route
+ * one token each (the plain router), then fp's producers (the x shrink; its plan workgroup waits
+ * for route_done to reach rp.T before reading the rings) and fp.gp[0]'s gate/up GEMV
+ * workgroups. */
+typedef struct {
+  aos_route_params rp;
+  aos_gemv_fused_params fp;
+  uint32_t *route_done; /* zero between launches (the plan workgroup resets it) */
+} aos_route_gu_params;
+
 /* q, k and v (or any n <= 3 matrices with the same x, T and waves) in one launch: matrix i owns
  * workgroups [wg_end[i - 1], wg_end[i]) of a 1-D grid, wg_end[i] - wg_end[i - 1] = RB_i * ks_i;
  * entries past n repeat wg_end[n - 1]. */
@@ -366,6 +376,7 @@ int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_gemv3(const aos_gemv3_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv_fused(const aos_gemv_fused_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx);

@@ -25,6 +25,7 @@
 #include "aos_blake3.h"
 #include "aos_exp.h"
 #include "aoship_device.h"
+#include "aoship_gemv.h"
 #include "aoship_internal.h"
 #include <hip/hip_ext.h>
 
@@ -522,9 +523,7 @@ __global__ void __launch_bounds__(64) aos_route_kernel(aos_route_params p) {
 /* Routing from router features: one workgroup per token; wave w computes the priors of
  * adapters w, w + W, ... into LDS (and priors_out), then wave 0 routes. */
 template <bool X>
-__global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_params p) {
-  extern __shared__ float lds[]; /* features [d], then priors [n] */
-  const int t = blockIdx.x;
+__device__ __forceinline__ void route_features_block(const aos_route_params &p, int t, float *lds) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
@@ -543,7 +542,75 @@ __global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_para
   if (wave == 0) route_one<true, X>(p, lds_priors, t, lane);
 }
 
+template <bool X>
+__global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_params p) {
+  extern __shared__ float lds[]; /* features [d], then priors [n] */
+  route_features_block<X>(p, blockIdx.x, lds);
+}
+
+/* The router's workgroups (one per token, the plain router), then the x shrink and the gate/up
+ * GEMV of the layer those rings feed: the shrink does not depend on the rings, so it and the
+ * weight stream run while the tokens are routed; only the adapter plan, and through it the
+ * GEMV's LoRA expand, waits for them. */
+template <int NV>
+__global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int T = q.rp.T;
+  const int b = blockIdx.x;
+  if (b < T) {
+    route_features_block<false>(q.rp, b, (float *)smem);
+    /* the ring (plain stores of wave 0) is written again with device-scope stores, which the plan
+     * workgroup's device-scope loads see, then counted */
+    __syncthreads();
+    uint32_t *rw = (uint32_t *)(q.rp.rings + b);
+    if (threadIdx.x < 10) __hip_atomic_store(rw + threadIdx.x, rw[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(q.route_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int b2 = b - T;
+  if (b2 < q.fp.n_pre) {
+    aos_gemv::fused_producer<NV, 4>(q.fp, b2, smem, q.route_done, (uint32_t)T);
+    return;
+  }
+  const int r = b2 - q.fp.n_pre;
+  aos_gemv::gemv_body<NV, true, 4, 4>(q.fp.gp[0], r % q.fp.gp[0].w0.RB, r / q.fp.gp[0].w0.RB);
+}
+
+template <int NV>
+int launch_rgu(const aos_route_gu_params *q, const aos_launch_ctx *ctx) {
+  const int nwg = q->rp.T + q->fp.n_pre + (int)q->fp.n_cons;
+  size_t lds = (size_t)(q->rp.d + q->rp.n) * sizeof(float);
+  if ((size_t)q->fp.sp.lds_bytes > lds) lds = (size_t)q->fp.sp.lds_bytes;
+  if ((size_t)q->fp.gp[0].lds_bytes > lds) lds = (size_t)q->fp.gp[0].lds_bytes;
+  AOS_LAUNCH(ctx, aos_route_gu_kernel<NV>, dim3(nwg), dim3(256), lds, *q);
+  return (int)hipGetLastError();
+}
+
 }  // namespace
+
+static_assert(sizeof(aos_route_gu_params) <= 4096, "kernel arguments");
+
+extern "C" int aos_launch_route_gate_up(const aos_route_gu_params *q, const aos_launch_ctx *ctx) {
+  const aos_gemv_fused_params &fp = q->fp;
+  const int T = q->rp.T;
+  if (T < 1 || T > AOS_DECODE_MAX_T || !q->rp.features || !q->route_done) return (int)hipErrorInvalidValue;
+  if (q->rp.scope || q->rp.tie_key || q->rp.post_allowed || q->rp.active_ids || q->rp.strengths || q->rp.hashes)
+    return (int)hipErrorInvalidValue; /* the plain router only */
+  if (fp.n != 1 || fp.hsum || fp.gp[0].waves != 4 || fp.gp[0].T != T || fp.sp.T != T || !fp.sync || !fp.flags ||
+      fp.n_pre < 1 || fp.pre_rows < 1 || fp.n_pre % fp.pre_rows || fp.n_pre / fp.pre_rows != fp.sp.ks ||
+      !fp.sp.plan_build.plan || fp.n_cons != (uint32_t)(fp.gp[0].w0.RB * fp.gp[0].ks) ||
+      fp.wg_end[0] != (int)fp.n_cons || fp.gp[0].sync != fp.sync || fp.gp[0].flags != fp.flags ||
+      fp.gp[0].sync_target != (uint32_t)fp.n_pre)
+    return (int)hipErrorInvalidValue;
+  if ((size_t)(q->rp.d + q->rp.n) * sizeof(float) > 60 * 1024) return (int)hipErrorInvalidValue;
+  if (T <= 1) return launch_rgu<1>(q, ctx);
+  if (T <= 2) return launch_rgu<2>(q, ctx);
+  if (T <= 8) return launch_rgu<4>(q, ctx);
+  if (T <= 16) return launch_rgu<8>(q, ctx);
+  return launch_rgu<16>(q, ctx);
+}
 
 extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx) {
   const bool x = p->scope || p->tie_key || p->post_allowed || p->active_ids || p->strengths || p->hashes;

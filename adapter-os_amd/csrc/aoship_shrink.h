@@ -41,12 +41,16 @@ __device__ void build_plan(const aos_plan_params &pp) {
   __shared__ uint32_t bits[AOS_MAX_ADAPTERS / 32];
   __shared__ uint16_t list[AOS_PLAN_MAXU];
   __shared__ int cntU;
+  __shared__ aoship_ring_t rs[AOS_DECODE_MAX_T];
   const int tid = threadIdx.x, nt = blockDim.x;
   const int words = (pp.n + 31) >> 5;
   for (int w = tid; w < words; w += nt) bits[w] = 0u;
+  /* the rings, with device-scope loads (the router may have written them in this launch) */
+  for (int w = tid; w < pp.T * 10; w += nt)
+    ((uint32_t *)rs)[w] = __hip_atomic_load((const uint32_t *)pp.rings + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   for (int e = tid; e < pp.T * 8; e += nt) {
-    const aoship_ring_t &r = pp.rings[e >> 3];
+    const aoship_ring_t &r = rs[e >> 3];
     const int s = e & 7;
     const int a = r.adapter_indices[s];
     if (s < (int)r.top_k && r.gates_q15[s] > 0 && a < pp.n && pp.bound[a])
@@ -73,7 +77,7 @@ __device__ void build_plan(const aos_plan_params &pp) {
   for (int idx = tid; idx < pp.T * U; idx += nt) {
     const int t = idx / U, u = idx - t * U;
     const int a = list[u];
-    const aoship_ring_t &r = pp.rings[t];
+    const aoship_ring_t &r = rs[t];
     float c = 0.0f;
     for (int s = 0; s < 8; ++s) {
       if (s < (int)r.top_k && r.adapter_indices[s] == a && r.gates_q15[s] > 0) {

@@ -83,8 +83,14 @@ class MlpCase:
         else:
             self.priors = torch.from_numpy(W.priors(cfg, T)).cuda()
         self.i = 0
+        self.combined = False  # route and MLP in one call (aoship_route_mlp_forward)
 
     def step(self):
+        if self.combined and self.priors is None:
+            self.layers[self.i % self.n_layers].route_mlp_forward(self.router, self.f, self.w, self.x, self.rings,
+                                                                   self.y)
+            self.i += 1
+            return
         if self.priors is None:
             self.router.route_features(self.f, self.w, self.rings)
         else:
@@ -161,11 +167,13 @@ def gate_up_bytes(cfg, T: int, U: int) -> int:
     return base + lora + T * H * 2 + T * I * 2
 
 
-def launch_names(kt: dict) -> dict:
-    """Per-launch times keyed by what each launch runs (a fused shrink has no launch of its own)."""
+def launch_names(kt: dict, combined: bool = False) -> dict:
+    """Per-launch times keyed by what each launch runs (a fused shrink has no launch of its own;
+    with the combined call the router runs in the gate/up launch)."""
     if not FUSED:
         return dict(kt)
-    ren = {"q4_gemv_gate_up": "lora_shrink_x+q4_gemv_gate_up", "q4_gemv_down": "lora_shrink_h+q4_gemv_down"}
+    gu = ("route+" if combined else "") + "lora_shrink_x+q4_gemv_gate_up"
+    ren = {"q4_gemv_gate_up": gu, "q4_gemv_down": "lora_shrink_h+q4_gemv_down"}
     return {ren.get(k, k): v for k, v in kt.items() if k not in ("lora_shrink_x", "lora_shrink_h")}
 
 
@@ -179,6 +187,7 @@ def probe(aoship, W, torch, layers: int) -> int:
     steps of the headline workload, then one device copy of COPY_BYTES that calibrates the
     counters (it reads and writes exactly COPY_BYTES)."""
     dec = MlpCase(aoship, W, 2, 1, torch, layers)
+    dec.combined = FUSED
     for _ in range(50):
         dec.step()
     torch.cuda.synchronize()
@@ -420,15 +429,18 @@ def main() -> int:
     # ---- headline: 7B-shaped decode, one token ----
     T = 1
     dec = MlpCase(aoship, W, 2, T, torch, args.layers)
+    ms_sep = time_steps(dec, args.steps, args.warmup, torch)  # route, then the layer: two calls
+    dec.combined = FUSED  # one call: the router runs inside the gate/up launch
     ms = time_steps(dec, args.steps, args.warmup, torch)
     U = dec.distinct_adapters(aoship)
     kt = kernel_times(dec, max(20, args.steps // 4), torch)
     cfg = dec.cfg
     layer_bytes = W.algorithmic_bytes(cfg, T, U)
     gu_ms = kt["q4_gemv_gate_up"]
-    gu_bytes = gate_up_bytes(cfg, T, U)
+    # with the router in the launch: its weights and the token's features as well
+    gu_bytes = gate_up_bytes(cfg, T, U) + (cfg.n_adapters + T) * cfg.hidden * 4 * dec.combined
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-    kl = launch_names(kt)
+    kl = launch_names(kt, dec.combined)
     log(f"decode T=1: {ms * 1e3:.1f} us/step, launches (us): " +
         ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kl.items()))
     result = {
@@ -454,8 +466,8 @@ def main() -> int:
         "layer_hbm_gbps": layer_bytes / (ms * 1e-3) / 1e9,
         "roofline": {
             "bound": "hbm",
-            "kernel": ("lora_shrink_x+q4_gemv_gate_up (one launch: the LoRA x shrink in its first workgroups, "
-                       "then the int4 gate+up GEMV with the LoRA expand and SwiGLU)" if FUSED else
+            "kernel": ("route+lora_shrink_x+q4_gemv_gate_up (one launch: the router and the LoRA x shrink in its "
+                       "first workgroups, then the int4 gate+up GEMV with the LoRA expand and SwiGLU)" if FUSED else
                        "q4_gemv_gate_up (int4 gate+up GEMV, fused LoRA expand and SwiGLU)"),
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
@@ -466,12 +478,16 @@ def main() -> int:
             "avg_launch_us": gu_ms * 1e3,
         },
         "kernels_us": {k: v * 1e3 for k, v in kl.items()},
+        "decode_t1_separate_calls": {"ms_per_step": ms_sep, "tok_s": T / (ms_sep * 1e-3),
+                                     "note": "aoship_route_features then aoship_mlp_forward"},
     }
+    log(f"decode T=1 as two calls (route, then the layer): {ms_sep * 1e3:.1f} us/step")
     del dec
 
     # ---- 8-token decode batch ----
     T8 = 8
     d8 = MlpCase(aoship, W, 2, T8, torch, args.layers)
+    d8.combined = FUSED
     ms8 = time_steps(d8, args.steps, args.warmup, torch)
     U8 = d8.distinct_adapters(aoship)
     result["decode_t8"] = {

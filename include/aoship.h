@@ -245,6 +245,18 @@ void aoship_layer_free(aoship_layer_t *layer);
 int aoship_mlp_forward(aoship_layer_t *layer, const aoship_bf16_t *x, int T,
                        const aoship_ring_t *rings, aoship_bf16_t *y);
 
+/* One decode step of a layer's MLP with its tokens routed in the same call: the router's decision
+ * from features (aoship_route_features: Router::route_with_adapter_info_and_scope_with_ctx,
+ * router.rs:1567-1952, with the plain router settings) feeds the MLP (aoship_mlp_forward: the
+ * fused forward's MLP, mlx_cpp_wrapper_real.cpp:3509-3527). rings (and status, may be NULL)
+ * receive the decisions as aoship_route_features writes them; y equals aoship_mlp_forward's
+ * output for those rings. For T <= 32 with no router extras set, the router runs in the first
+ * workgroups of the gate/up launch, beside the LoRA shrink and the weight stream; otherwise the
+ * calls run one after the other. Everything runs on the layer's stream. Returns 0 / -1. */
+int aoship_route_mlp_forward(aoship_router_t *router, const float *features, const float *router_w, int d,
+                             aoship_layer_t *layer, const aoship_bf16_t *x, int T, aoship_ring_t *rings,
+                             int32_t *status, aoship_bf16_t *y);
+
 /* One projection with LoRA (mlx_cpp_wrapper_real.cpp:3445-3455 for q/k/v, 3499-3501 for o).
  *   x : device bf16[T * in];  y : device bf16[T * out]. Returns 0 / -1. */
 int aoship_proj_forward(aoship_layer_t *layer, const char *module, const aoship_bf16_t *x,
