@@ -1,7 +1,7 @@
 /*
  * aos_oracle.c — CPU restatement of adapterOS's router + int4 LoRA layer (test infrastructure).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never the product. See aos_oracle.h
+ * TEST INFRASTRUCTURE ONLY: the oracle the HIP path is tested against, never the product. See aos_oracle.h
  * for the reference file:line each function follows and for how each one is pinned.
  *
  * Built with -O2 -ffp-contract=off and without fast-math, so every float operation below is

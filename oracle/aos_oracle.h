@@ -1,8 +1,8 @@
 /*
  * aos_oracle.h — CPU restatement of adapterOS's adapter-augmented inference hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP implementation in
- * adapter-os_amd/. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle the HIP implementation in
+ * adapter-os_amd/ is tested against. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load it, and only to check or to time the CPU baseline. The product path never calls it.
  *
  * What it restates (reference paths are relative to the adapter-os tree):

@@ -1,6 +1,6 @@
 """ctypes wrapper of the CPU oracle (oracle/liborc.so).
 
-TEST INFRASTRUCTURE ONLY: the checker for the HIP path. Only tests/, __graft_entry__.smoke() and
+TEST INFRASTRUCTURE ONLY: the oracle the HIP path is tested against. Only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg use it. See aos_oracle.h for the reference file:line each function
 restates and how each is pinned.
 """
