@@ -139,3 +139,4 @@ def test_model_long_context_attention_splits(hip, hd):
     dm.reset_cache()
     third = [_run(hip, dm, ids[a:b], rg[a:b]) for a, b in spans]
     assert all(np.array_equal(x, y) for x, y in zip(again, third))
+    assert all(layer.wait_timeouts() == 0 for layer in dm.layers)
