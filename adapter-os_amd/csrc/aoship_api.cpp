@@ -1083,8 +1083,9 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.x = h;
   g2.T = T;
   /* the down GEMV streams beside the h shrink of its launch: more K splits (measured: 3 at the
-   * 7B shape) keep its tail short */
-  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, 2 * AOS_GEMV_WAVES);
+   * 7B shape) keep its tail short; at 1-2 tokens the launch only sums the shrink's partials, and
+   * 2 splits are faster (measured) */
+  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES);
   g2.tab0 = td;
   g2.S0 = s2.S[0];
   g2.s_stride0 = s2.s_stride[0];
