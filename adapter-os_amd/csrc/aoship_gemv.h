@@ -159,8 +159,9 @@ __device__ __forceinline__ void h_shrink_partial(const aos_gemv_params &p, int r
   }
 }
 
-/* S[t][col] = sum over the row blocks, in order, of hpart[rb][t][col]: each thread sums row
- * blocks tid, tid + NT, ... in order, then a fixed pairwise tree over the threads. */
+/* S[t][col] = sum over the row blocks of hpart[rb][t][col] in a fixed order: each thread sums
+ * row blocks tid, tid + NT, ... in order, then a butterfly within each wave, then the waves in
+ * order. */
 constexpr int HSUM_V = AOS_HSUM_V;
 template <int NT>
 __device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, unsigned char *smem) {
@@ -193,18 +194,23 @@ __device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, uns
 #pragma unroll
       for (int k = 0; k < HSUM_V; ++k) sum[k] += v[q][k];
   }
+  /* across each wave by a butterfly, then the NT / 64 wave sums in wave order */
+  const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
-  for (int k = 0; k < HSUM_V; ++k) red[k * NT + tid] = sum[k];
-  __syncthreads();
+  for (int k = 0; k < HSUM_V; ++k) {
 #pragma unroll
-  for (int w = NT / 2; w > 0; w >>= 1) {
-    if (tid < w) {
-#pragma unroll
-      for (int k = 0; k < HSUM_V; ++k) red[k * NT + tid] = red[k * NT + tid] + red[k * NT + tid + w];
-    }
-    __syncthreads();
+    for (int o = 32; o >= 1; o >>= 1) sum[k] = sum[k] + aos_shfl_f(sum[k], lane ^ o);
+    if (lane == 0) red[k * (NT / 64) + wave] = sum[k];
   }
-  if (tid < HSUM_V && t[tid] < hs.T && col[tid] < cols) aos_publish(&hs.S[(size_t)t[tid] * hs.stride + col[tid]], red[tid * NT]);
+  __syncthreads();
+  if (tid < HSUM_V) {
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) v += red[tid * (NT / 64) + w];
+    red[tid * (NT / 64)] = v;
+  }
+  if (tid < HSUM_V && t[tid] < hs.T && col[tid] < cols)
+    aos_publish(&hs.S[(size_t)t[tid] * hs.stride + col[tid]], red[tid * (NT / 64)]);
 }
 
 template <int NV, bool SW, int W, int D>
