@@ -8,6 +8,7 @@
  * (mlx_cpp_wrapper_real.cpp:3198-3199).
  */
 #include <hip/hip_runtime.h>
+#include <hip/hip_version.h>
 
 #include <algorithm>
 #include <cmath>
@@ -77,17 +78,24 @@ extern "C" int aoship_sync(void) {
   return 0;
 }
 
+/* The report in DeterminismReport's serialized form (attestation.rs:130-160): backend "Hip"
+ * (deterministic by design: fixed-order reductions, no floating-point atomics, no random draws on
+ * the device; adaptive tie-breaks come from the HKDF-seeded ChaCha20 stream on the host), the
+ * flags every kernel is built with, and this library's parity levels as extra fields. */
 extern "C" int aoship_attest_determinism(char *buf, int len) {
-  const char *js =
-      "{\"backend\":\"hip\",\"arch\":\"gfx950\","
-      "\"rng_seed_method\":\"none: kernels draw no random numbers\","
-      "\"floating_point_mode\":\"ieee; no fast-math; fp32 denormals preserved; "
-      "router compiled with -ffp-contract=off\","
+  char js[1024];
+  const int n = snprintf(
+      js, sizeof(js),
+      "{\"backend_type\":\"Hip\",\"metallib_hash\":null,\"metallib_verified\":false,\"manifest\":null,"
+      "\"rng_seed_method\":\"HkdfSeeded\",\"floating_point_mode\":\"Deterministic\","
+      "\"determinism_level\":\"bit_exact\","
+      "\"compiler_flags\":[\"-O3\",\"--offload-arch=gfx950\",\"-ffp-contract=off\",\"-fno-fast-math\","
+      "\"-fno-gpu-flush-denormals-to-zero\",\"-fhip-fp32-correctly-rounded-divide-sqrt\"],"
+      "\"deterministic\":true,\"runtime_version\":\"HIP %d.%d.%d\",\"device_id\":\"gfx950\","
       "\"reductions\":\"fixed order; no floating-point atomics\","
-      "\"router\":\"BitExact vs CPU (float64 softmax with correctly rounded exp)\","
-      "\"layer\":\"BitExact run-to-run; BoundedTolerance vs CPU (2e-2 relative, bf16)\","
-      "\"deterministic\":true}";
-  int n = (int)strlen(js);
+      "\"router\":\"bit_exact vs the CPU restatement (float64 softmax with correctly rounded exp)\","
+      "\"layer\":\"bit_exact run to run; bounded_tolerance vs the CPU restatement (2e-2 relative, bf16)\"}",
+      HIP_VERSION_MAJOR, HIP_VERSION_MINOR, HIP_VERSION_PATCH);
   if (buf && len > 0) snprintf(buf, (size_t)len, "%s", js);
   return n;
 }

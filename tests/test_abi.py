@@ -95,3 +95,21 @@ def test_ring_roundtrip_bytes():
     r[1]["gates_q15"][:2] = [20000, 12767]
     back = aoship.rings_from_bytes(r.view(np.uint8))
     assert back.tobytes() == r.tobytes()
+
+
+def test_attestation_is_a_valid_determinism_report():
+    """aoship_attest_determinism (no device needed) serializes DeterminismReport's fields and
+    passes the checks of DeterminismReport::validate (attestation.rs:160-214), restated."""
+    import json
+
+    import aoship
+
+    r = json.loads(aoship.attest_determinism())
+    for key in ("backend_type", "metallib_hash", "manifest", "rng_seed_method", "floating_point_mode",
+                "determinism_level", "compiler_flags", "deterministic"):
+        assert key in r, key
+    assert r["backend_type"] == "Hip" and r["deterministic"] is True
+    assert r["determinism_level"] in ("bit_exact", "bounded_tolerance")
+    assert r["rng_seed_method"] == "HkdfSeeded" or "FixedSeed" in r["rng_seed_method"]
+    assert r["floating_point_mode"] == "Deterministic"
+    assert not any(f in flag for flag in r["compiler_flags"] for f in ("-ffast-math", "-funsafe-math-optimizations"))
