@@ -435,6 +435,12 @@ class Router {
   float tau_, eps_, bias_ = 1.0f;
   int device_;
   aoship_router_t *h_ = nullptr;
+
+ public:
+  // The C-ABI router behind this object (for HipKernels::route_mlp_forward).
+  aoship_router_t *handle() const { return h_; }
+
+ private:
   std::vector<uint64_t> ids_;
   float *d_priors_ = nullptr;
   aoship_ring_t *d_ring_ = nullptr;
@@ -670,6 +676,21 @@ class HipKernels {
                    aoship_bf16_t *k, aoship_bf16_t *v) {
     detail::check(aoship_qkv_forward(layer_at(layer), x, T, rings, q, k, v), ErrorKind::Kernel,
                   "aoship_qkv_forward");
+  }
+  // Route T tokens from device features (float32 [T][d]) and run the layer's MLP on them in one
+  // call; rings and status (may be null) receive the decisions (aoship_route_mlp_forward).
+  void route_mlp_forward(const Router &router, const float *features, const float *router_w, int d, int layer,
+                         const aoship_bf16_t *x, int T, aoship_ring_t *rings, int32_t *status, aoship_bf16_t *y) {
+    detail::check(aoship_route_mlp_forward(router.handle(), features, router_w, d, layer_at(layer), x, T, rings,
+                                           status, y),
+                  ErrorKind::Kernel, "aoship_route_mlp_forward");
+  }
+  // True if a fused decode launch of the layer gave up a bounded wait since the last call
+  // (aoship_layer_wait_timeouts); clears the flag.
+  bool wait_timed_out(int layer) {
+    const int r = aoship_layer_wait_timeouts(layer_at(layer));
+    detail::check(r < 0 ? -1 : 0, ErrorKind::Kernel, "aoship_layer_wait_timeouts");
+    return r == 1;
   }
 
  private:
