@@ -110,8 +110,22 @@ def lib():
             f.argtypes = args
         L.aoship_internal_exp_cr.restype = C.c_double
         L.aoship_internal_exp_cr.argtypes = [C.c_double]
+        L.aoship_internal_layer_set_separate_shrinks.restype = C.c_int
+        L.aoship_internal_layer_set_separate_shrinks.argtypes = [_P, C.c_int]
+        L.aoship_internal_decode_geometry.restype = C.c_int
+        L.aoship_internal_decode_geometry.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
+                                                      C.POINTER(C.c_int), C.POINTER(C.c_int)]
         _lib = L
     return _lib
+
+
+def decode_geometry(kind: int, out: int, inp: int, T: int) -> tuple[int, int, int]:
+    """(waves, K splits, fewest K groups of any wave) of a decode launch shape (see
+    aoship_internal_decode_geometry)."""
+    w, k, g = C.c_int(), C.c_int(), C.c_int()
+    _check(lib().aoship_internal_decode_geometry(kind, out, inp, T, C.byref(w), C.byref(k), C.byref(g)),
+           "aoship_internal_decode_geometry")
+    return w.value, k.value, g.value
 
 
 def last_error() -> str:
@@ -330,8 +344,15 @@ class Layer:
     def set_profiling(self, on: bool) -> None:
         _check(lib().aoship_layer_set_profiling(self.h, 1 if on else 0), "aoship_layer_set_profiling")
 
+    def set_separate_shrinks(self, on: bool) -> None:
+        """Diagnostic: each decode LoRA shrink in a launch of its own (default: inside the GEMV
+        launch that reads it)."""
+        _check(lib().aoship_internal_layer_set_separate_shrinks(self.h, 1 if on else 0),
+               "aoship_internal_layer_set_separate_shrinks")
+
     def wait_timeouts(self) -> int:
-        """1 if a fused decode launch's bounded wait gave up since the last call (then cleared)."""
+        """1 if a fused decode launch's bounded wait gave up since the last call (the layer's
+        counters and flags are then reset)."""
         r = lib().aoship_layer_wait_timeouts(self.h)
         if r < 0:
             raise AosError(last_error())

@@ -586,9 +586,17 @@ struct aoship_layer {
   ModTable tabs[AOS_MAX_MODULES];
   DevBuf bound, scale_all; /* [n] per bound adapter: 1 / alpha-over-rank */
   DevBuf zeros;            /* device zeros read by lanes without an adapter row */
-  DevBuf wait_flag;        /* set by a fused launch whose bounded wait gave up */
-  DevBuf ws, counters;
-  size_t ws_cap = 0, ctr_cap = 0;
+  /* set by a fused launch whose bounded wait gave up: pinned host memory the kernels write
+   * through its device mapping, so a forward sees it without synchronising */
+  uint32_t *wait_host = nullptr;
+  uint32_t *wait_dev = nullptr;
+  /* workspace (partials, S, plan, h), arrival counters (zero at rest: each is reset by its last
+   * arriver) and generation-stamped ready flags, each grown on demand; counters and flags never
+   * share memory, since calls with other token counts lay them out differently */
+  DevBuf ws, counters, flags;
+  size_t ws_cap = 0, ctr_cap = 0, flag_cap = 0;
+  uint32_t gen = 0;        /* generation of the last fused launch (flags are raised to it) */
+  bool separate_shrinks = false; /* each decode shrink in a launch of its own (diagnostic) */
   hipStream_t stream = nullptr;
   bool profiling = false;
   KStat stats[KS_COUNT];
@@ -609,11 +617,33 @@ extern "C" aoship_layer_t *aoship_layer_new(int layer_idx, int group_size, int b
   auto *l = new aoship_layer();
   l->layer_idx = layer_idx;
   for (int i = 0; i < KS_COUNT; ++i) l->stats[i].name = kStatNames[i];
-  if (l->zeros.alloc(256, true) || l->wait_flag.alloc(256, true)) {
+  if (l->zeros.alloc(256, true)) {
     delete l;
     return nullptr;
   }
+  void *wh = nullptr;
+  if (hipHostMalloc(&wh, 256, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
+    set_err("aoship_layer_new: hipHostMalloc failed");
+    delete l;
+    return nullptr;
+  }
+  l->wait_host = (uint32_t *)wh;
+  *(volatile uint32_t *)l->wait_host = 0u;
+  void *wd = nullptr;
+  if (hipHostGetDevicePointer(&wd, wh, 0) != hipSuccess) {
+    set_err("aoship_layer_new: hipHostGetDevicePointer failed");
+    (void)hipHostFree(wh);
+    delete l;
+    return nullptr;
+  }
+  l->wait_dev = (uint32_t *)wd;
   return l;
+}
+
+/* The next generation number of a layer's fused launches (never 0: flags start at 0). */
+static uint32_t next_gen(uint32_t *g) {
+  *g = *g + 1u == 0u ? 1u : *g + 1u;
+  return *g;
 }
 
 static uint32_t shuffle_nibbles(uint32_t w) {
@@ -802,16 +832,39 @@ extern "C" int aoship_layer_set_profiling(aoship_layer_t *l, int enable) {
   return 0;
 }
 
+/* Reports (1) whether a fused launch of this layer gave up a bounded wait since the last call,
+ * and then resets the layer: once the device is idle, every arrival counter and ready flag of its
+ * workspace goes back to zero and the generation restarts, so the next forward starts clean. */
 extern "C" int aoship_layer_wait_timeouts(aoship_layer_t *l) {
   if (!l) return set_err("aoship_layer_wait_timeouts: null layer");
   if (ensure_device()) return -1;
-  uint32_t v = 0;
-  if (hipDeviceSynchronize() != hipSuccess ||
-      hipMemcpy(&v, l->wait_flag.p, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess)
+  if (hipDeviceSynchronize() != hipSuccess) return set_err("aoship_layer_wait_timeouts: device error");
+  const uint32_t v = *(volatile uint32_t *)l->wait_host;
+  if (!v) return 0;
+  if ((l->counters.p && hipMemset(l->counters.p, 0, l->ctr_cap) != hipSuccess) ||
+      (l->flags.p && hipMemset(l->flags.p, 0, l->flag_cap) != hipSuccess))
     return set_err("aoship_layer_wait_timeouts: device error");
-  if (v && hipMemset(l->wait_flag.p, 0, sizeof(v)) != hipSuccess)
-    return set_err("aoship_layer_wait_timeouts: device error");
-  return v ? 1 : 0;
+  if (hipDeviceSynchronize() != hipSuccess) return set_err("aoship_layer_wait_timeouts: device error");
+  l->gen = 0;
+  *(volatile uint32_t *)l->wait_host = 0u;
+  return 1;
+}
+
+/* A forward refuses to run while a given-up wait is pending: its counters may be inconsistent. */
+static int check_no_timeout(aoship_layer *l) {
+  if (*(volatile uint32_t *)l->wait_host)
+    return set_err("forward: a fused launch of this layer gave up a bounded wait; "
+                   "aoship_layer_wait_timeouts reports and resets it");
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): run each decode LoRA shrink in a launch of its
+ * own instead of in the first workgroups of the GEMV launch that reads it. Same results within
+ * the layer's tolerance; used to test the fused launches against separate ones. */
+extern "C" int aoship_internal_layer_set_separate_shrinks(aoship_layer_t *l, int on) {
+  if (!l) return set_err("aoship_internal_layer_set_separate_shrinks: null layer");
+  l->separate_shrinks = on != 0;
+  return 0;
 }
 
 extern "C" int aoship_layer_kernel_stats(aoship_layer_t *l, int idx, const char **name,
@@ -829,12 +882,12 @@ extern "C" int aoship_layer_kernel_stats(aoship_layer_t *l, int idx, const char 
 
 /* Launch context for one kernel of this layer: with profiling on, the dispatch records a pair
  * of events at kernel start and end, resolved lazily by aoship_layer_kernel_stats. */
-static aos_launch_ctx launch_ctx(aoship_layer *l, int slot) {
+static aos_launch_ctx launch_ctx(aoship_layer *l, int slot, bool events = true) {
   aos_launch_ctx c;
   c.stream = l->stream;
   c.ev_start = nullptr;
   c.ev_stop = nullptr;
-  if (l->profiling) {
+  if (l->profiling && events) {
     hipEvent_t a = get_event(l), b = get_event(l);
     if (a && b) {
       c.ev_start = a;
@@ -846,6 +899,18 @@ static aos_launch_ctx launch_ctx(aoship_layer *l, int slot) {
 }
 
 /* ---- workspace ---- */
+
+/* Where a decode forward's scratch memory lives: the layer's own workspace (grown on demand) or
+ * the device's static scratch (the allocation-free entry point). gen counts the generations of
+ * the flags in that memory; events says whether launches may record profiling events (that
+ * creates event objects, which the allocation-free entry point does not do). */
+struct Ws {
+  void *ws;
+  void *ctr;
+  void *flg;
+  uint32_t *gen;
+  bool events;
+};
 
 struct Bump {
   char *base;
@@ -860,7 +925,7 @@ struct Bump {
   }
 };
 
-static int ws_reserve(aoship_layer *l, size_t bytes, size_t ctr_words) {
+static int ws_reserve(aoship_layer *l, size_t bytes, size_t ctr_words, size_t flag_words = 0) {
   if (bytes > l->ws_cap) {
     HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (l->ws.alloc(bytes, false)) return -1;
@@ -870,6 +935,11 @@ static int ws_reserve(aoship_layer *l, size_t bytes, size_t ctr_words) {
     HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (l->counters.alloc(ctr_words * 4, true)) return -1;
     l->ctr_cap = ctr_words * 4;
+  }
+  if (flag_words * 4 > l->flag_cap) { /* zeroed: no generation is 0 */
+    HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (l->flags.alloc(flag_words * 4, true)) return -1;
+    l->flag_cap = flag_words * 4;
   }
   return 0;
 }
@@ -894,14 +964,25 @@ static int nv_for(int T) {
 #ifndef AOS_GEMV_W8_MIN_G
 #define AOS_GEMV_W8_MIN_G 128 /* single-matrix GEMVs with at least this many groups use 8 waves */
 #endif
-static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g,
-                          int waves_target = AOS_GEMV_WAVES) {
-  const int W = swiglu ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
+static int gemv_splits(int RB, int G, int T, int W, int waves_target) {
   int ks = ceil_div(waves_target, RB * W);
   int cap = G / W;
   if (cap < 1) cap = 1;
   if (ks > cap) ks = cap;
   while (ks < G && (size_t)T * ceil_div(G, ks) * 136 > AOS_GEMV_LDS_MAX) ++ks;
+  return ks;
+}
+
+/* Every wave of a K split must get at least one group (G / ks >= W): the 8-wave single-matrix
+ * kernel falls back to 4 waves when the LDS budget forces more splits (many tokens, long K). */
+static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g,
+                          int waves_target = AOS_GEMV_WAVES) {
+  int W = swiglu ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
+  int ks = gemv_splits(RB, G, T, W, waves_target);
+  if (G / ks < W && W == 8) {
+    W = 4;
+    ks = gemv_splits(RB, G, T, W, waves_target);
+  }
   const int NA = swiglu ? 2 : 1;
   size_t lds_x = 128 + (size_t)T * ceil_div(G, ks) * 136;
   size_t lds_r = (size_t)W * NA * nv_for(T) * 64 * 4;
@@ -932,13 +1013,48 @@ static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, i
   sp.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
 }
 
+/* Diagnostic (no counterpart in the reference): the decode geometry the forwards use, for a
+ * CPU-side check that every wave of every launch gets at least one K group. kind 0: the gate/up
+ * GEMV (out = intermediate, in = hidden); 1: the down GEMV (out = hidden, in = intermediate);
+ * 2: a projection GEMV (out = the row count of the matrices sharing x); 3: a shrink over `out`
+ * rank rows launched with 8 waves when in / 64 >= AOS_GEMV_W8_MIN_G, else 4 (the x shrink);
+ * 4: the same with 8 waves (the h shrink). Writes the waves, the K splits and the fewest groups
+ * any wave gets. */
+extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T, int *waves, int *ks,
+                                               int *min_groups) {
+  if (out < 32 || in < 64 || in % 64 || T < 1 || T > AOS_DECODE_MAX_T || !waves || !ks || !min_groups)
+    return set_err("aoship_internal_decode_geometry: bad arguments");
+  const int G = in / 64, RB = out / 32;
+  int W = 4, k = 1;
+  if (kind <= 2) {
+    aos_gemv_params g;
+    memset(&g, 0, sizeof(g));
+    const int target = kind == 1 ? (T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES) : AOS_GEMV_WAVES;
+    gemv_geometry(RB, G, T, kind == 0, true, g, target);
+    W = g.waves;
+    k = g.ks;
+  } else if (kind <= 4) {
+    aos_shrink_params sp;
+    memset(&sp, 0, sizeof(sp));
+    W = kind == 4 ? 8 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
+    shrink_geometry(RB, G, T, sp, W);
+    k = sp.ks;
+  } else {
+    return set_err("aoship_internal_decode_geometry: unknown kind");
+  }
+  *waves = W;
+  *ks = k;
+  *min_groups = (G / k) / W;
+  return 0;
+}
+
 /* One decode chunk (T <= 32 tokens) of a forward: the workspace carve-up and every launch's
  * parameters. The same code sizes the workspace (base == nullptr) and fills it. */
 struct Carve {
   Bump b;
-  uint32_t *cbase;
-  size_t coff = 0;
-  Carve(void *ws, void *ctr) : b(ws, 0), cbase((uint32_t *)ctr) {}
+  uint32_t *cbase, *fbase;
+  size_t coff = 0, foff = 0;
+  Carve(void *ws, void *ctr, void *flg = nullptr) : b(ws, 0), cbase((uint32_t *)ctr), fbase((uint32_t *)flg) {}
   uint32_t *counters(size_t n) {
     uint32_t *p = cbase ? cbase + coff : nullptr;
     coff += n;
@@ -948,6 +1064,13 @@ struct Carve {
   uint32_t *counter_lines(size_t n) {
     coff = (coff + 31) & ~(size_t)31;
     return counters(n);
+  }
+  /* generation-stamped flags, from a line of their own */
+  uint32_t *flag_lines(size_t n) {
+    foff = (foff + 31) & ~(size_t)31;
+    uint32_t *p = fbase ? fbase + foff : nullptr;
+    foff += n;
+    return p;
   }
 };
 
@@ -972,12 +1095,11 @@ struct XShrink {
   aos_shrink_params plan_only;
 };
 
-/* Counter words of a fused launch: the arrival counter and the timeout flag on lines of their
- * own, then one 128-byte line per GEMV workgroup for its ready flag. */
-static size_t fused_sync_words(const aos_gemv_params *gp, int n) {
+/* Flag words of a fused launch: one 128-byte line per GEMV workgroup for its ready flag. */
+static size_t fused_flag_words(const aos_gemv_params *gp, int n) {
   size_t c = 0;
   for (int i = 0; i < n; ++i) c += (size_t)gp[i].w0.RB * gp[i].ks;
-  return 64 + 32 * c;
+  return 32 * c;
 }
 
 static void plan_x_shrink(aoship_layer *l, Carve &cv, const uint16_t *x, int T, int in,
@@ -1028,14 +1150,17 @@ struct MlpPlan {
   XShrink sx;
   aos_shrink_params sh;
   aos_gemv_params gv1, gv2;
-  uint32_t *sync1, *sync2; /* the fused launches' arrival counter, timeout flag and ready flags */
-  float *hpart;            /* [RB of gate/up][T][s_stride of the down shrink]: the h shrink's partials */
+  uint32_t *sync1, *sync2;   /* the fused launches' arrival counters */
+  uint32_t *flags1, *flags2; /* ... and their ready flags */
+  float *hpart;            /* [RB of gate/up][T][s_stride of the down shrink]: the h shrink's partials
+                              (1-2 tokens only, else NULL) */
   uint32_t *route_done;    /* the combined route + gate/up launch's router arrivals */
-  size_t bytes = 0, ctr = 0;
+  uint32_t *route_flag;    /* ... and its routing flag */
+  size_t bytes = 0, ctr = 0, flg = 0;
 };
 
 static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_ring_t *rings,
-                     uint16_t *y, void *ws, void *ctr, MlpPlan &P) {
+                     uint16_t *y, void *ws, void *ctr, void *flg, MlpPlan &P) {
   const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
   const int H = Wg.in, I = Wg.out;
   aos_lora_tab tabs_gu[2] = {lora_tab(l, MOD_GATE, H, I), lora_tab(l, MOD_UP, H, I)};
@@ -1043,7 +1168,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   const int n = (int)l->table.size();
   int umax = n < 8 * T ? n : 8 * T;
   if (umax < 1) umax = 1;
-  Carve cv(ws, ctr);
+  Carve cv(ws, ctr, flg);
   aos_plan *plan = cv.b.take<aos_plan>(1);
   uint16_t *h = cv.b.take<uint16_t>((size_t)T * I);
   plan_x_shrink(l, cv, x, T, H, tabs_gu, 2, plan, rings, P.sx);
@@ -1104,12 +1229,16 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.part = cv.b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
   g2.counters = cv.counters((size_t)Wd.RB);
 
-  P.hpart = cv.b.take<float>((size_t)Wg.RB * T * s2.s_stride[0]);
+  P.hpart = T <= 2 ? cv.b.take<float>((size_t)Wg.RB * T * s2.s_stride[0]) : nullptr;
   P.route_done = cv.counter_lines(32);
-  P.sync1 = cv.counter_lines(fused_sync_words(&g1, 1));
-  P.sync2 = cv.counter_lines(fused_sync_words(&g2, 1));
+  P.route_flag = cv.flag_lines(32);
+  P.sync1 = cv.counter_lines(32);
+  P.flags1 = cv.flag_lines(fused_flag_words(&g1, 1));
+  P.sync2 = cv.counter_lines(32);
+  P.flags2 = cv.flag_lines(fused_flag_words(&g2, 1));
   P.bytes = cv.b.off + 256;
   P.ctr = cv.coff + 64;
+  P.flg = cv.foff + 64;
 }
 
 
@@ -1265,14 +1394,15 @@ extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
   if (!l) return set_err("aoship_layer_reserve: null layer");
   if (max_tokens < 1) return set_err("aoship_layer_reserve: max_tokens must be >= 1");
   if (ensure_device()) return -1;
-  size_t bytes = 0, ctr = 0;
+  size_t bytes = 0, ctr = 0, flg = 0;
   const bool mlp = l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid;
   for (int T = 1; T <= AOS_DECODE_MAX_T && T <= max_tokens; T *= 2) {
     if (mlp) {
       MlpPlan P;
-      plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+      plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, P);
       if (P.bytes > bytes) bytes = P.bytes;
       if (P.ctr > ctr) ctr = P.ctr;
+      if (P.flg > flg) flg = P.flg;
     }
   }
   if (mlp && max_tokens > AOS_DECODE_MAX_T) {
@@ -1281,7 +1411,7 @@ extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
     if (M.bytes > bytes) bytes = M.bytes;
     if (M.ctr > ctr) ctr = M.ctr;
   }
-  return ws_reserve(l, bytes, ctr);
+  return ws_reserve(l, bytes, ctr, flg);
 }
 
 static int check_common(aoship_layer *l, const void *x, int T, const aoship_ring_t *rings,
@@ -1290,6 +1420,7 @@ static int check_common(aoship_layer *l, const void *x, int T, const aoship_ring
   if (!x || !y || !rings) return set_err("forward: null device pointer");
   if (!aligned16(x) || !aligned16(y)) return set_err("forward: x and y must be 16-byte aligned");
   if (T < 0) return set_err("forward: negative token count");
+  if (check_no_timeout(l)) return -1;
   return ensure_device();
 }
 
@@ -1298,27 +1429,27 @@ static int launch_err(int e, const char *what) {
   return set_err(std::string(what) + ": " + hipGetErrorString((hipError_t)e));
 }
 
-static int launch_x_shrink(aoship_layer *l, XShrink &xs) {
+static int launch_x_shrink(aoship_layer *l, XShrink &xs, bool events = true) {
   if (xs.separate_plan) {
-    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, events);
     if (launch_err(aos_launch_shrink(&xs.plan_only, &c0), "adapter plan")) return -1;
   }
-  aos_launch_ctx c1 = launch_ctx(l, KS_SHRINK_X);
+  aos_launch_ctx c1 = launch_ctx(l, KS_SHRINK_X, events);
   return launch_err(aos_launch_shrink(&xs.sp, &c1), "lora shrink");
 }
 
 /* A decode shrink and the GEMV that reads its S fused into one launch (the shrink's workgroups
- * first). Off while AOSHIP_UNFUSED_SHRINK is set in the environment: separate launches of the
- * same device code, with the same results. */
-static bool fuse_shrinks() { return getenv("AOSHIP_UNFUSED_SHRINK") == nullptr; }
+ * first), unless the layer is set to separate launches of the same device code (same results
+ * within tolerance). */
+static bool fuse_shrinks(const aoship_layer *l) { return !l->separate_shrinks; }
 
 static int shrink_wgs(const aos_shrink_params &sp) {
   return (sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) + (sp.plan_build.plan ? 1 : 0)) *
          sp.ks;
 }
 
-static void make_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
-                       const aos_hsum_params *hs, aos_gemv_fused_params &f) {
+static void make_fused(aoship_layer *l, uint32_t *genc, const aos_shrink_params &sp, const aos_gemv_params *gp, int n,
+                       uint32_t *sync, uint32_t *flags, const aos_hsum_params *hs, aos_gemv_fused_params &f) {
   memset(&f, 0, sizeof(f));
   if (hs) { /* the first workgroups sum the h shrink's partials instead of running a shrink */
     f.hsum = 1;
@@ -1333,7 +1464,8 @@ static void make_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_g
   }
   f.n = n;
   f.sync = sync;          /* its own 128-byte line */
-  f.flags = sync + 64;    /* line 1 holds the timeout flag */
+  f.flags = flags;
+  f.gen = next_gen(genc);
   int end = 0;
   for (int i = 0; i < 3; ++i) {
     if (i < n) {
@@ -1341,7 +1473,8 @@ static void make_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_g
       f.gp[i].sync = f.sync;
       f.gp[i].flags = f.flags + (size_t)end * 32;
       f.gp[i].sync_target = (uint32_t)f.n_pre;
-      f.gp[i].timeout = l->wait_flag.as<uint32_t>();
+      f.gp[i].gen = f.gen;
+      f.gp[i].timeout = l->wait_dev;
       end += gp[i].w0.RB * gp[i].ks;
     }
     f.wg_end[i] = end;
@@ -1349,11 +1482,12 @@ static void make_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_g
   f.n_cons = (uint32_t)end;
 }
 
-static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_gemv_params *gp, int n, uint32_t *sync,
-                        int swiglu, int slot, const char *what, const aos_hsum_params *hs = nullptr) {
+static int launch_fused(aoship_layer *l, const Ws &w, const aos_shrink_params &sp, const aos_gemv_params *gp, int n,
+                        uint32_t *sync, uint32_t *flags, int swiglu, int slot, const char *what,
+                        const aos_hsum_params *hs = nullptr) {
   aos_gemv_fused_params f;
-  make_fused(l, sp, gp, n, sync, hs, f);
-  aos_launch_ctx c = launch_ctx(l, slot);
+  make_fused(l, w.gen, sp, gp, n, sync, flags, hs, f);
+  aos_launch_ctx c = launch_ctx(l, slot, w.events);
   return launch_err(aos_launch_gemv_fused(&f, swiglu, &c), what);
 }
 
@@ -1361,16 +1495,22 @@ static int launch_fused(aoship_layer *l, const aos_shrink_params &sp, const aos_
  * for these tokens, which then run in the gate/up launch (rings written there); the caller has
  * checked that the gate/up launch is fused. */
 static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const aoship_ring_t *rings, uint16_t *y,
-                            const aos_route_params *rp) {
+                            const aos_route_params *rp, const Ws *scratch = nullptr) {
   MlpPlan P;
-  plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, P);
-  if (ws_reserve(l, P.bytes, P.ctr)) return -1;
-  plan_mlp(l, Tc, x, rings, y, l->ws.p, l->counters.p, P);
-  const bool fuse = fuse_shrinks();
+  Ws w;
+  if (scratch) {
+    w = *scratch; /* the caller has checked the sizes */
+  } else {
+    plan_mlp(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+    if (ws_reserve(l, P.bytes, P.ctr, P.flg)) return -1;
+    w = {l->ws.p, l->counters.p, l->flags.p, &l->gen, true};
+  }
+  plan_mlp(l, Tc, x, rings, y, w.ws, w.ctr, w.flg, P);
+  const bool fuse = fuse_shrinks(l);
   const bool fuse_down = fuse && P.gv2.has_expand && P.sh.n_rb[0] > 0;
   /* with both launches fused, the gate/up launch also forms the h shrink's partials over its
    * row blocks, and the down launch only sums them */
-  const bool h_in_gu = fuse && P.gv1.has_expand && fuse_down && Tc <= 2; /* measured: slower at 8 tokens */
+  const bool h_in_gu = fuse && P.gv1.has_expand && fuse_down && P.hpart; /* 1-2 tokens (measured: slower at 8) */
   const bool route_in_gu = rp && fuse && P.gv1.has_expand && !P.sx.separate_plan;
   if (rp && !route_in_gu) { /* route first, on the layer's stream */
     aos_launch_ctx cr = {l->stream, nullptr, nullptr};
@@ -1383,17 +1523,18 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
       g1.hpart = P.hpart;
       g1.hstride = P.sh.s_stride[0];
     }
-    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, w.events);
     AOS_SKIP(&c0);
     aos_route_gu_params q;
     memset(&q, 0, sizeof(q));
     q.rp = *rp;
-    make_fused(l, P.sx.sp, &g1, 1, P.sync1, nullptr, q.fp);
+    make_fused(l, w.gen, P.sx.sp, &g1, 1, P.sync1, P.flags1, nullptr, q.fp);
     q.route_done = P.route_done;
-    aos_launch_ctx cg = launch_ctx(l, KS_GEMV_GU);
+    q.route_flag = P.route_flag;
+    aos_launch_ctx cg = launch_ctx(l, KS_GEMV_GU, w.events);
     if (launch_err(aos_launch_route_gate_up(&q, &cg), "route + lora shrink + q4 gemv gate/up")) return -1;
   } else if (fuse && P.gv1.has_expand) {
-    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, w.events);
     if (P.sx.separate_plan) {
       if (launch_err(aos_launch_shrink(&P.sx.plan_only, &c0), "adapter plan")) return -1;
     } else {
@@ -1405,14 +1546,15 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
       g1.hpart = P.hpart;
       g1.hstride = P.sh.s_stride[0];
     }
-    if (launch_fused(l, P.sx.sp, &g1, 1, P.sync1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up")) return -1;
+    if (launch_fused(l, w, P.sx.sp, &g1, 1, P.sync1, P.flags1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up"))
+      return -1;
   } else {
-    if (launch_x_shrink(l, P.sx)) return -1;
-    aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU);
+    if (launch_x_shrink(l, P.sx, w.events)) return -1;
+    aos_launch_ctx c2 = launch_ctx(l, KS_GEMV_GU, w.events);
     if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
   }
   if (fuse_down) {
-    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H, w.events);
     AOS_SKIP(&c3);
     aos_hsum_params hs;
     memset(&hs, 0, sizeof(hs));
@@ -1424,13 +1566,13 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
     hs.plan = P.sh.plan;
     hs.S = P.sh.S[0];
     hs.values_per_wg = AOS_HSUM_V;
-    if (launch_fused(l, P.sh, &P.gv2, 1, P.sync2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
+    if (launch_fused(l, w, P.sh, &P.gv2, 1, P.sync2, P.flags2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
                      h_in_gu ? &hs : nullptr))
       return -1;
   } else {
-    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H);
+    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H, w.events);
     if (launch_err(aos_launch_shrink(&P.sh, &c3), "lora shrink down")) return -1;
-    aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN);
+    aos_launch_ctx c4 = launch_ctx(l, KS_GEMV_DOWN, w.events);
     if (launch_err(aos_launch_gemv(&P.gv2, 0, &c4), "q4 gemv down")) return -1;
   }
   return 0;
@@ -1536,7 +1678,7 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
     aos_lora_tab tabs[3];
     for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
     for (int pass = 0; pass < 2; ++pass) {
-      Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr);
+      Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr, pass ? l->flags.p : nullptr);
       aos_plan *plan = cv.b.take<aos_plan>(1);
       XShrink xs;
       plan_x_shrink(l, cv, xc, Tc, in, tabs, nm, plan, rc, xs);
@@ -1562,21 +1704,23 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
         gp[i].counters = cv.counters((size_t)W.RB);
       }
-      uint32_t *sync = cv.counter_lines(fused_sync_words(gp, nm));
+      uint32_t *sync = cv.counter_lines(32);
+      uint32_t *flags = cv.flag_lines(fused_flag_words(gp, nm));
       if (pass == 0) {
-        if (ws_reserve(l, cv.b.off + 256, cv.coff + 64)) return -1;
+        if (ws_reserve(l, cv.b.off + 256, cv.coff + 64, cv.foff + 64)) return -1;
         continue;
       }
       bool expands = false;
       for (int i = 0; i < nm; ++i) expands = expands || gp[i].has_expand;
-      if (fuse_shrinks() && expands && shrink_wgs(xs.sp) > 0) {
+      if (fuse_shrinks(l) && expands && shrink_wgs(xs.sp) > 0) {
         aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
         if (xs.separate_plan) {
           if (launch_err(aos_launch_shrink(&xs.plan_only, &c0), "adapter plan")) return -1;
         } else {
           AOS_SKIP(&c0);
         }
-        if (launch_fused(l, xs.sp, gp, nm, sync, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
+        const Ws lw = {l->ws.p, l->counters.p, l->flags.p, &l->gen, true};
+        if (launch_fused(l, lw, xs.sp, gp, nm, sync, flags, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
         continue;
       }
       if (launch_x_shrink(l, xs)) return -1;
@@ -1623,6 +1767,7 @@ extern "C" void aoship_layer_free(aoship_layer_t *l) {
   resolve_events(l);
   for (auto e : l->event_pool) (void)hipEventDestroy(e);
   unbind_all(l);
+  if (l->wait_host) (void)hipHostFree(l->wait_host);
   delete l;
 }
 
@@ -1856,6 +2001,8 @@ extern "C" int aoship_model_forward(aoship_model_t *m, const int32_t *ids, int T
   if (position_offset + T > c.max_seq) return set_err("aoship_model_forward: the KV cache is full");
   if (!m->emb_set) return set_err("aoship_model_forward: embedding not set");
   if (!m->lm.valid) return set_err("aoship_model_forward: LM head not set");
+  for (auto *l : m->layers)
+    if (check_no_timeout(l)) return -1;
   if (ensure_device()) return -1;
   if (T > m->ws_T) {
     const size_t bytes = model_ws(m, T, nullptr).bytes;

@@ -83,12 +83,27 @@ __device__ __forceinline__ uint64_t aos_shfl64(uint64_t v, int src_lane) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-/* Cross-workgroup hand-over without cache flushes. A partial result is published with
- * device-coherent stores (agent-scope relaxed atomic stores: write-through past the per-XCD L2),
- * the storing wave waits until they are acknowledged, then counts its arrival with an
- * agent-scope atomic add; the workgroup that arrives last reads every partial back with
- * device-coherent loads, in a fixed order. An agent-scope fence would instead write back and
- * invalidate the whole L2 of the XCD on every arrival. */
+/* Cross-workgroup hand-over without cache flushes.
+ *
+ * Payload: every value another workgroup reads is stored with aos_publish (an agent-scope
+ * relaxed atomic store, global_store with sc1: it is written through the XCD's L2 to the
+ * device-coherent level) and read with aos_collect (agent-scope relaxed atomic load, sc1: it is
+ * not served from a possibly stale line of another XCD's L2).
+ *
+ * Ordering: the producing wave waits until its payload stores are acknowledged (s_waitcnt
+ * vmcnt(0), which on gfx9 counts stores as well) before the store or atomic that signals them;
+ * the consumer issues its payload loads only after the load that observed the signal has
+ * returned and been compared (a wave issues memory instructions in program order, and the
+ * loop's exit branch depends on that value). Both waits are volatile asm with a memory clobber,
+ * so the compiler moves no memory access across them either. Agent-scope release/acquire
+ * fences would give the same guarantee by writing back and invalidating the whole L2 of the
+ * XCD, which costs more than the hand-over itself.
+ *
+ * Signals are generation-stamped: a launch that hands over data gets a generation number
+ * (nonzero, new per call of its layer) and raises flags to that value; a consumer waits for
+ * equality, so a flag left over from an earlier call, or raised late by a producer whose
+ * consumer gave up, never satisfies a later call's wait. Arrival counters are reset by their
+ * last arriver. */
 __device__ __forceinline__ void aos_publish(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -97,16 +112,47 @@ __device__ __forceinline__ float aos_collect(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* Wait until this wave's earlier loads and stores are complete; a compiler barrier as well. */
+__device__ __forceinline__ void aos_mem_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+/* Compiler barrier only (no instruction). */
+__device__ __forceinline__ void aos_compiler_barrier() { asm volatile("" ::: "memory"); }
+
 /* Wait for this wave's published stores, then count the arrival (call from one lane).
  * Returns the previous count. */
 __device__ __forceinline__ uint32_t aos_arrive(uint32_t *ctr) {
-  __builtin_amdgcn_s_waitcnt(0);
-  return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  aos_mem_wait();
+  const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  aos_compiler_barrier();
+  return old;
 }
 
 /* Reset a counter for the next launch (the last arriver's job). */
 __device__ __forceinline__ void aos_reset(uint32_t *ctr) {
   __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Raise a generation flag once this wave's payload stores are complete. */
+__device__ __forceinline__ void aos_raise(uint32_t *flag, uint32_t gen) {
+  aos_mem_wait();
+  __hip_atomic_store(flag, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Bounded wait (one lane) until *flag == gen. Returns false when it gave up (after about a
+ * second). The payload loads that follow are not moved above the wait. */
+#define AOS_SPIN_LIMIT (1u << 24)
+__device__ __forceinline__ bool aos_wait_gen(const uint32_t *flag, uint32_t gen) {
+  uint32_t spins = 0;
+  bool ok = true;
+  while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) {
+    __builtin_amdgcn_s_sleep(2);
+    if (++spins > AOS_SPIN_LIMIT) {
+      ok = false;
+      break;
+    }
+  }
+  aos_compiler_barrier();
+  return ok;
 }
 
 #endif

@@ -167,7 +167,8 @@ template <int NT>
 __device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, unsigned char *smem) {
   float *red = (float *)smem; /* [HSUM_V][NT] */
   const int tid = threadIdx.x;
-  const int U = __builtin_amdgcn_readfirstlane(__hip_atomic_load(&hs.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  int U = __builtin_amdgcn_readfirstlane(__hip_atomic_load(&hs.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  U = U < AOS_PLAN_MAXU ? U : AOS_PLAN_MAXU;
   const int cols = U * hs.rpad;
   float sum[HSUM_V];
   int t[HSUM_V], col[HSUM_V];
@@ -268,7 +269,9 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
       xv[j] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
     }
 
-    /* (2) the ring: groups ga .. ga+D-1 (every wave has at least one group) */
+    /* (2) the ring: groups ga .. ga+D-1. The host sizes the splits so that every wave has at
+     * least one group; a wave without one still loads group ga (in range: ga < gw1 <= G) and
+     * never uses it. */
     const u32x4 *q0 = (const u32x4 *)p.w0.qt + ((size_t)rb * G + ga) * 64 + lane;
     const uint32_t *s0 = p.w0.sb + ((size_t)rb * G + ga) * 32 + i;
     const u32x4 *q1 = SW ? (const u32x4 *)p.w1.qt + ((size_t)rb * G + ga) * 64 + lane : nullptr;
@@ -277,7 +280,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     uint32_t sa[D], sb[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int jj = d < ng ? d : ng - 1;
+      const int jj = d < ng ? d : (ng > 0 ? ng - 1 : 0);
       wa[d] = q0[(size_t)jj * 64];
       sa[d] = s0[(size_t)jj * 32];
       if (SW) {
@@ -358,37 +361,31 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     }
   }
 
-  /* (4a) fused launch: wait for this workgroup's ready flag, raised once every shrink
-   * workgroup of the grid is done (they have the lowest workgroup ids, so they are dispatched
-   * before any GEMV workgroup, and they never wait), then clear it for the next launch. Each
-   * workgroup polls a line of its own. The wait is bounded: past about a second it gives up,
-   * sets p.timeout and finishes. */
+  /* (4a) fused launch: wait for this workgroup's ready flag, raised to this launch's generation
+   * once every producer workgroup of the grid is done (they have the lowest workgroup ids, so
+   * they are dispatched before any GEMV workgroup, and none of them waits on a GEMV workgroup).
+   * Each workgroup polls a line of its own. The wait is bounded: past about a second it gives up,
+   * sets p.timeout and finishes without the expand or the h shrink (reading neither S nor the
+   * plan); the call's output is then invalid and the layer reports the timeout. */
   if (fused) {
     __shared__ uint32_t ok;
     if (tid == 0) {
-      uint32_t *flag = p.flags + ((size_t)ksi * p.w0.RB + rb) * 32;
-      uint32_t spins = 0, done = 1;
-      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins > (1u << 24)) {
-          done = 0;
-          break;
-        }
-      }
-      ok = done;
-      __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t *flag = p.flags + ((size_t)ksi * p.w0.RB + rb) * 32;
+      const bool done = aos_wait_gen(flag, p.gen);
+      ok = done ? 1u : 0u;
+      if (!done && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     lds_barrier();
-    if (!ok && tid == 0 && p.timeout) *p.timeout = 1u;
-    if (expands) {
-      const int U = __builtin_amdgcn_readfirstlane(
+    if (ok && expands) {
+      int U = __builtin_amdgcn_readfirstlane(
           __hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      U = U < AOS_PLAN_MAXU ? U : AOS_PLAN_MAXU;
       nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
       nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
       hU = U;
     }
     /* the h shrink's first A_down fragments (wave 0 forms the partials at the end) */
-    if (SW && p.hpart && wave == 0) {
+    if (SW && p.hpart && wave == 0 && ok) {
       h_a_load(p, rb, lane, hU, 0, hpre[0]);
       h_a_load(p, rb, lane, hU, 1, hpre[1]);
     }
@@ -500,49 +497,51 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
       p.y[(size_t)m * out + row] = hb[v];
     }
   }
-  if (SW && p.hpart) h_shrink_partial<NV>(p, rb, lane, hb, smem, hU, hpre);
+  if (SW && p.hpart && hU > 0) h_shrink_partial<NV>(p, rb, lane, hb, smem, hU, hpre);
 }
 
 
 /* Producer workgroup b of a fused launch: a shrink workgroup (or, with fp.hsum, a sum of the h
  * shrink's partials), then the arrival count; the last producer raises every GEMV workgroup's
- * ready flag. route_done (may be NULL): the plan workgroup first waits, bounded, until route_done
- * reaches route_target (the router's workgroups of the same launch), then resets it and reads
- * the rings after an acquire fence. */
+ * ready flag to fp.gen. route_flag (may be NULL): the plan workgroup first waits, bounded, until
+ * the launch's routers have raised route_flag to fp.gen and only then reads the rings (with
+ * device-scope loads); if that wait gives up it publishes an empty plan instead. */
 template <int NV, int W>
 __device__ __forceinline__ void fused_producer(const aos_gemv_fused_params &fp, int b, unsigned char *smem,
-                                               uint32_t *route_done, uint32_t route_target) {
-  __shared__ uint32_t last;
+                                               const uint32_t *route_flag) {
+  __shared__ uint32_t last, routed;
   if (fp.hsum) {
     hsum_block<64 * W>(fp.hs, b, smem);
   } else {
     const int lrb = b % fp.pre_rows, ksi = b / fp.pre_rows;
-    if (route_done && fp.sp.plan_build.plan && lrb == fp.pre_rows - 1 && ksi == 0) {
+    bool run = true;
+    if (route_flag && fp.sp.plan_build.plan && lrb == fp.pre_rows - 1 && ksi == 0) {
       if (threadIdx.x == 0) {
-        uint32_t spins = 0;
-        while (__hip_atomic_load(route_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < route_target &&
-               ++spins < (1u << 24))
-          __builtin_amdgcn_s_sleep(2);
-        if (spins >= (1u << 24) && fp.gp[0].timeout) *fp.gp[0].timeout = 1u;
-        __hip_atomic_store(route_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool done = aos_wait_gen(route_flag, fp.gen);
+        routed = done ? 1u : 0u;
+        if (!done) {
+          if (fp.gp[0].timeout) __hip_atomic_store(fp.gp[0].timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          __hip_atomic_store(&fp.sp.plan_build.plan->U, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
-      __syncthreads(); /* build_plan reads the rings with device-scope loads */
+      __syncthreads();
+      run = routed != 0u;
     }
-    aos_shrink::shrink_block<NV, W, 4>(fp.sp, lrb, ksi, smem);
+    if (run) aos_shrink::shrink_block<NV, W, 4>(fp.sp, lrb, ksi, smem);
   }
   /* the partials, S and the plan went out as device-scope stores: wait for them, then count
    * this workgroup in (no cache write-back is needed) */
-  __builtin_amdgcn_s_waitcnt(0);
+  aos_mem_wait();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(fp.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t old = aos_arrive(fp.sync);
     last = old == (uint32_t)fp.n_pre - 1u;
-    if (last) __hip_atomic_store(fp.sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) aos_reset(fp.sync);
   }
   __syncthreads();
   if (last) /* every producer is done: raise the GEMV workgroups' flags */
     for (uint32_t c = threadIdx.x; c < fp.n_cons; c += blockDim.x)
-      __hip_atomic_store(fp.flags + (size_t)c * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(fp.flags + (size_t)c * 32, fp.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace aos_gemv

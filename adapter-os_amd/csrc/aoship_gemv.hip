@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int b = blockIdx.x;
   if (b < fp.n_pre) {
-    fused_producer<NV, W>(fp, b, smem, nullptr, 0);
+    fused_producer<NV, W>(fp, b, smem, nullptr);
     return;
   }
   const int r = b - fp.n_pre;
@@ -161,7 +161,7 @@ extern "C" int aos_launch_gemv_fused(const aos_gemv_fused_params *fp, int swiglu
   if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
   if (swiglu && waves != 4) return (int)hipErrorInvalidValue;
   if (T < 1 || T > AOS_DECODE_MAX_T || (fp->hsum ? fp->hs.T : fp->sp.T) != T) return (int)hipErrorInvalidValue;
-  if (!fp->sync || !fp->flags || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows)
+  if (!fp->sync || !fp->flags || !fp->gen || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows)
     return (int)hipErrorInvalidValue;
   if (fp->hsum ? (fp->pre_rows != fp->n_pre || !fp->hs.hpart || !fp->hs.S || fp->hs.values_per_wg != HSUM_V ||
                   (size_t)fp->n_pre * HSUM_V < (size_t)fp->hs.T * fp->hs.stride)
@@ -172,7 +172,7 @@ extern "C" int aos_launch_gemv_fused(const aos_gemv_fused_params *fp, int swiglu
     if (i < n) {
       const aos_gemv_params &p = fp->gp[i];
       if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1 || p.sync != fp->sync ||
-          p.flags != fp->flags + (size_t)end * 32 || p.sync_target != (uint32_t)fp->n_pre)
+          p.flags != fp->flags + (size_t)end * 32 || p.sync_target != (uint32_t)fp->n_pre || p.gen != fp->gen)
         return (int)hipErrorInvalidValue;
       end += p.w0.RB * p.ks;
     }

@@ -145,6 +145,7 @@ typedef struct {
   uint32_t *sync;     /* [1] producer arrivals; zero between launches */
   uint32_t *flags;    /* this matrix's ready flags [RB * ks * 32], one per 128-byte line */
   uint32_t sync_target;
+  uint32_t gen;       /* this launch's generation: a ready flag equal to it is raised */
   uint32_t *timeout;  /* set to 1 if a wait gave up (the launch still ends) */
   /* SwiGLU mode, fused launch: the down projection's LoRA shrink over this row block's 32 rows of
    * h, hpart[rb][t][col] = sum_r h[t][32 rb + r] A_down(col)[32 rb + r] for the plan's union
@@ -180,16 +181,18 @@ typedef struct {
   uint32_t *sync;     /* [1] producer arrivals */
   uint32_t *flags;    /* [n_cons * 32] */
   uint32_t n_cons;    /* wg_end[n - 1] */
+  uint32_t gen;       /* generation the last producer raises the flags to (nonzero) */
 } aos_gemv_fused_params;
 
 /* Routing from features and the fused gate/up launch in one grid: workgroups [0, rp.T) route
  * one token each (the plain router), then fp's producers (the x shrink; its plan workgroup waits
- * for route_done to reach rp.T before reading the rings) and fp.gp[0]'s gate/up GEMV
+ * for route_flag to equal fp.gen before reading the rings) and fp.gp[0]'s gate/up GEMV
  * workgroups. */
 typedef struct {
   aos_route_params rp;
   aos_gemv_fused_params fp;
-  uint32_t *route_done; /* zero between launches (the plan workgroup resets it) */
+  uint32_t *route_done; /* router arrivals, zero between launches (the last router resets it) */
+  uint32_t *route_flag; /* raised to fp.gen by the last router, on a line of its own */
 } aos_route_gu_params;
 
 /* q, k and v (or any n <= 3 matrices with the same x, T and waves) in one launch: matrix i owns

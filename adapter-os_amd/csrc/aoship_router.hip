@@ -564,14 +564,18 @@ __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q
     __syncthreads();
     uint32_t *rw = (uint32_t *)(q.rp.rings + b);
     if (threadIdx.x < 10) __hip_atomic_store(rw + threadIdx.x, rw[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
+    aos_mem_wait();
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(q.route_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    /* the last router to finish resets the count and raises the launch's routing flag */
+    if (threadIdx.x == 0 && aos_arrive(q.route_done) == (uint32_t)T - 1u) {
+      aos_reset(q.route_done);
+      aos_raise(q.route_flag, q.fp.gen);
+    }
     return;
   }
   const int b2 = b - T;
   if (b2 < q.fp.n_pre) {
-    aos_gemv::fused_producer<NV, 4>(q.fp, b2, smem, q.route_done, (uint32_t)T);
+    aos_gemv::fused_producer<NV, 4>(q.fp, b2, smem, q.route_flag);
     return;
   }
   const int r = b2 - q.fp.n_pre;
@@ -595,7 +599,8 @@ static_assert(sizeof(aos_route_gu_params) <= 4096, "kernel arguments");
 extern "C" int aos_launch_route_gate_up(const aos_route_gu_params *q, const aos_launch_ctx *ctx) {
   const aos_gemv_fused_params &fp = q->fp;
   const int T = q->rp.T;
-  if (T < 1 || T > AOS_DECODE_MAX_T || !q->rp.features || !q->route_done) return (int)hipErrorInvalidValue;
+  if (T < 1 || T > AOS_DECODE_MAX_T || !q->rp.features || !q->route_done || !q->route_flag || !q->fp.gen)
+    return (int)hipErrorInvalidValue;
   if (q->rp.scope || q->rp.tie_key || q->rp.post_allowed || q->rp.active_ids || q->rp.strengths || q->rp.hashes)
     return (int)hipErrorInvalidValue; /* the plain router only */
   if (fp.n != 1 || fp.hsum || fp.gp[0].waves != 4 || fp.gp[0].T != T || fp.sp.T != T || !fp.sync || !fp.flags ||

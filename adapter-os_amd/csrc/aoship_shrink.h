@@ -113,7 +113,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
   }
   const aos_lora_tab &tab = p.tab[m];
   const int rpad = tab.rpad;
-  const int nslots = p.all_mode ? tab.n : p.plan->U;
+  const int nslots = p.all_mode ? tab.n : (p.plan->U < AOS_PLAN_MAXU ? p.plan->U : AOS_PLAN_MAXU);
   /* uniform for every K split of this row block */
   if (rpad == 0 || lrb * 32 >= nslots * rpad) return;
 
@@ -147,14 +147,17 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
     const int t = idx / xchunks, r = idx - t * xchunks;
     xv[jx] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
   }
-  /* lane half c takes elements 32c + 8st .. +7 of each group, as the staged x fragments do */
-  const uint16_t *ap = valid ? arow + (size_t)ga * 64 + 32 * c : p.zero_row;
-  const int astep = valid ? 64 : 0;
-  const int sstep = valid ? 8 : 0;
+  /* lane half c takes elements 32c + 8st .. +7 of each group, as the staged x fragments do; a
+   * wave without a group (possible when the LDS budget forces more K splits than the geometry's
+   * groups per wave allow) reads the zero row and adds nothing */
+  const bool streams = valid && ng > 0;
+  const uint16_t *ap = streams ? arow + (size_t)ga * 64 + 32 * c : p.zero_row;
+  const int astep = streams ? 64 : 0;
+  const int sstep = streams ? 8 : 0;
   u32x4 ring[D][4];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    const int jj = d < ng ? d : ng - 1;
+    const int jj = d < ng ? d : (ng > 0 ? ng - 1 : 0);
 #pragma unroll
     for (int st = 0; st < 4; ++st) ring[d][st] = *(const u32x4 *)(ap + (size_t)jj * astep + sstep * st);
   }

@@ -312,12 +312,20 @@ struct TensorView {
   std::vector<size_t> shape;
   const uint8_t *data = nullptr;
   size_t nbytes = 0;
-  size_t numel() const {
+  size_t numel() const {  // the parser has checked that the product does not overflow
     size_t n = 1;
     for (size_t d : shape) n *= d;
     return n;
   }
 };
+
+// Element count of a shape, or false when it overflows size_t.
+inline bool checked_numel(const std::vector<size_t> &shape, size_t &n) {
+  n = 1;
+  for (size_t d : shape)
+    if (__builtin_mul_overflow(n, d, &n)) return false;
+  return true;
+}
 
 inline size_t dtype_size(const std::string &dt) {
   if (dt == "F64" || dt == "I64" || dt == "U64") return 8;
@@ -361,7 +369,8 @@ class SafeTensors {
       TensorView v;
       v.dtype = dt->str;
       for (const Json &d : sh->arr) {
-        if (d.type != Json::Type::Number || d.num < 0 || d.num != std::floor(d.num) || d.num > 9.0e15)
+        // dimensions are used as int extents downstream: larger ones are rejected here
+        if (d.type != Json::Type::Number || d.num < 0 || d.num != std::floor(d.num) || d.num > 2147483647.0)
           throw bad("tensor '" + kv.first + "' has a bad shape");
         v.shape.push_back((size_t)d.num);
       }
@@ -373,7 +382,10 @@ class SafeTensors {
       if (es == 0) throw bad("tensor '" + kv.first + "' has unsupported dtype " + v.dtype);
       v.data = buf + (size_t)b.num;
       v.nbytes = (size_t)e.num - (size_t)b.num;
-      if (v.nbytes != v.numel() * es) throw bad("tensor '" + kv.first + "' size does not match its shape");
+      size_t count = 0, want = 0;
+      if (!checked_numel(v.shape, count) || __builtin_mul_overflow(count, es, &want))
+        throw bad("tensor '" + kv.first + "' has a shape whose size overflows");
+      if (v.nbytes != want) throw bad("tensor '" + kv.first + "' size does not match its shape");
       if (st.tensors_.count(kv.first)) throw bad("duplicate tensor '" + kv.first + "'");
       st.tensors_[kv.first] = v;
       st.order_.push_back(kv.first);

@@ -98,6 +98,14 @@ class MlpCase:
         self.layers[self.i % self.n_layers].mlp_forward(self.x, self.rings, self.y)
         self.i += 1
 
+    def check_waits(self):
+        """A fused launch whose bounded wait gave up returns early with invalid output: a timed
+        block with one is not a valid measurement."""
+        self.torch.cuda.synchronize()
+        bad = [i for i, layer in enumerate(self.layers) if layer.wait_timeouts() != 0]
+        if bad:
+            raise RuntimeError(f"a fused launch gave up waiting on layer copies {bad}: the timing is invalid")
+
     def set_profiling(self, on: bool):
         for layer in self.layers:
             layer.set_profiling(on)
@@ -133,6 +141,7 @@ def time_steps(case, steps: int, warmup: int, torch) -> float:
         case.step()
     end.record()
     torch.cuda.synchronize()
+    case.check_waits()
     return start.elapsed_time(end) / steps
 
 
@@ -142,14 +151,14 @@ def kernel_times(case, steps: int, torch) -> dict:
     for _ in range(steps):
         case.step()
     torch.cuda.synchronize()
+    case.check_waits()
     st = case.kernel_stats()
     case.set_profiling(False)
     return {k: ms / n for k, (ms, n) in st.items() if n}
 
 
-# The decode shrinks run in the first workgroups of the GEMV launch that reads their S unless
-# AOSHIP_UNFUSED_SHRINK is set (then each is a launch of its own).
-FUSED = os.environ.get("AOSHIP_UNFUSED_SHRINK") is None
+# The decode shrinks run in the first workgroups of the GEMV launch that reads their S.
+FUSED = True
 
 
 def gate_up_bytes(cfg, T: int, U: int) -> int:
@@ -371,6 +380,8 @@ def model_decode(aoship, W, torch, n_layers: int, ctx: int, steps: int, warmup: 
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / steps
     assert bool(torch.isfinite(logits).all())
+    if any(layer.wait_timeouts() != 0 for layer in model.layers):
+        raise RuntimeError("a fused launch of the model gave up waiting: the timing is invalid")
     # per layer: int4 weights + f16 scales/biases and the K routed adapters' bf16 rows of all seven
     # projections, and the bf16 keys and values of the (average) context; then the LM head
     layer_w = W.algorithmic_bytes(mlp, 1, mlp.k) + W.algorithmic_bytes(attn, 1, attn.k)
@@ -466,9 +477,8 @@ def main() -> int:
         "layer_hbm_gbps": layer_bytes / (ms * 1e-3) / 1e9,
         "roofline": {
             "bound": "hbm",
-            "kernel": ("route+lora_shrink_x+q4_gemv_gate_up (one launch: the router and the LoRA x shrink in its "
-                       "first workgroups, then the int4 gate+up GEMV with the LoRA expand and SwiGLU)" if FUSED else
-                       "q4_gemv_gate_up (int4 gate+up GEMV, fused LoRA expand and SwiGLU)"),
+            "kernel": "lora_shrink_x+q4_gemv_gate_up (one launch: the LoRA x shrink in its first workgroups, "
+                      "then the int4 gate+up GEMV with the LoRA expand and SwiGLU)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

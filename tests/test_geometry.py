@@ -1,0 +1,54 @@
+"""Decode launch geometry (CPU): every wave of every GEMV launch gets at least one K group.
+
+The decode GEMVs split K over the waves of a workgroup and over ks workgroups per row block, and
+the LDS budget for the staged activations can force more splits than the waves per workgroup
+allow. The geometry then falls back to 4-wave workgroups; a wave with no group would otherwise
+prime its weight ring from before the matrix. This replays the library's own geometry (the same
+function the forwards call) for every workload shape at every decode token count.
+"""
+import pytest
+
+import aoship
+
+# (hidden, intermediate) of the MLP shapes: the 0.5B plumbing layer, the 7B layer, the 32B
+# stress layer; then projection row counts sharing one input (q+k+v, o) at their input widths.
+MLP_SHAPES = [(896, 4864), (3584, 18944), (5120, 27648)]
+PROJ_SHAPES = [(3072 + 1024 + 1024, 3072), (3072, 3072), (3584 + 512 + 512, 3584), (3584, 3584),
+               (152064, 3584)]
+# x-shrink rank rows (adapters x padded rank x modules) and h-shrink rows
+SHRINK_ROWS = [(8 * 16 * 2, 896), (16 * 16 * 2, 3584), (32 * 16 * 3, 3072), (64 * 64 * 2, 5120),
+               (16 * 48 * 2, 3584)]
+H_SHRINK_ROWS = [(8 * 16, 4864), (16 * 16, 18944), (64 * 64, 27648), (16 * 48, 18944)]
+
+
+@pytest.mark.parametrize("T", range(1, 33))
+def test_every_gemv_wave_gets_a_group(T):
+    for H, I in MLP_SHAPES:
+        for kind, out, inp in ((0, I, H), (1, H, I)):
+            w, ks, g = aoship.decode_geometry(kind, out, inp, T)
+            assert w in (4, 8) and 1 <= ks <= inp // 64
+            assert g >= 1, f"kind {kind} {out}x{inp} T={T}: waves {w}, splits {ks}"
+            assert T * -(-(inp // 64) // ks) * 136 <= 32 * 1024, "staged x exceeds the LDS budget"
+    for out, inp in PROJ_SHAPES:
+        w, ks, g = aoship.decode_geometry(2, out, inp, T)
+        assert g >= 1, f"projection {out}x{inp} T={T}: waves {w}, splits {ks}"
+
+
+@pytest.mark.parametrize("T", range(1, 33))
+def test_shrink_geometry_within_limits(T):
+    """Shrinks: the K splits stay within the groups and the LDS budget. A shrink wave may get no
+    group when its launch runs more waves per workgroup than its splits leave groups; it then
+    reads the zero row and adds nothing."""
+    for kind, shapes in ((3, SHRINK_ROWS), (4, H_SHRINK_ROWS)):
+        for rows, inp in shapes:
+            w, ks, g = aoship.decode_geometry(kind, rows, inp, T)
+            G = inp // 64
+            assert 1 <= ks <= G
+            assert 128 + T * -(-G // ks) * 128 <= 32 * 1024
+
+
+def test_geometry_rejects_bad_shapes():
+    with pytest.raises(aoship.AosError):
+        aoship.decode_geometry(0, 3584, 100, 1)
+    with pytest.raises(aoship.AosError):
+        aoship.decode_geometry(0, 3584, 3584, 33)

@@ -31,7 +31,7 @@ def _run_mlp(hip, layer, xb, rings):
     return y.cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("cid,T", [(1, 1), (2, 1), (2, 2), (2, 8)])
+@pytest.mark.parametrize("cid,T", [(1, 1), (2, 1), (2, 2), (2, 8), (2, 31), (2, 32)])
 def test_mlp_decode_parity(hip, cid, T):
     xb, xf = W.activations(W.CONFIGS[cid], T)
     rings, _ = rings_for(cid, T)
@@ -46,19 +46,19 @@ def test_mlp_decode_parity(hip, cid, T):
 
 
 @pytest.mark.parametrize("T", [1, 8])
-def test_mlp_decode_unfused_launches(hip, T, monkeypatch):
-    """The decode MLP with each shrink in a launch of its own (AOSHIP_UNFUSED_SHRINK) instead of
-    in the first workgroups of the GEMV launch that reads it: the same tolerance, bit-identical run
-    to run, and the fused path afterwards still matches its own earlier output."""
+def test_mlp_decode_unfused_launches(hip, T):
+    """The decode MLP with each shrink in a launch of its own instead of in the first workgroups
+    of the GEMV launch that reads it: the same tolerance, bit-identical run to run, and the fused
+    path afterwards still matches its own earlier output."""
     cid = 2
     xb, xf = W.activations(W.CONFIGS[cid], T)
     rings, _ = rings_for(cid, T)
     layer, ads = gpu_layer(hip, cid)
     fused = _run_mlp(hip, layer, xb, rings)
-    monkeypatch.setenv("AOSHIP_UNFUSED_SHRINK", "1")
+    layer.set_separate_shrinks(True)
     y1 = _run_mlp(hip, layer, xb, rings)
     y2 = _run_mlp(hip, layer, xb, rings)
-    monkeypatch.delenv("AOSHIP_UNFUSED_SHRINK")
+    layer.set_separate_shrinks(False)
     assert np.array_equal(y1, y2), "run-to-run outputs differ"
     ref = oracle_mlp(cid, xf, rings)
     assert tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref) <= REL_TOL
@@ -258,18 +258,17 @@ def test_lora_projection_known_answer(hip):
 
 @pytest.mark.parametrize("unfused", [False, True], ids=["fused", "unfused"])
 @pytest.mark.parametrize("T", [1, 32])
-def test_attention_projections_parity(hip, T, unfused, monkeypatch):
+def test_attention_projections_parity(hip, T, unfused):
     """q/k/v in one launch (with the x shrink in its first workgroups, or in a launch of its own)
     and o: each within tolerance of the oracle and bit-identical run to run."""
     import torch
 
-    if unfused:
-        monkeypatch.setenv("AOSHIP_UNFUSED_SHRINK", "1")
     cid = 4
     cfg = W.CONFIGS[cid]
     xb, xf = W.activations(cfg, T)
     rings, _ = rings_for(cid, T)
     layer, ads = gpu_layer(hip, cid)
+    layer.set_separate_shrinks(unfused)
     x = _dev(xb.view(np.int16))
     r = _dev(rings.view(np.uint8))
     q = torch.empty((T, cfg.q_out), dtype=torch.int16, device="cuda")

@@ -266,6 +266,10 @@ def test_safetensors_format_errors(tmp_path):
         "dtype": _raw_file({"a": {"dtype": "Q4", "shape": [2], "data_offsets": [0, 8]}}, bytes(8)),
         "json": struct.pack("<Q", 8) + b'{"a":1 }',
         "metadata_value": _raw_file({"__metadata__": {"k": 1}, **ok}, bytes(8)),
+        # a shape whose element count wraps to 0 in 64 bits must not pass the size check
+        "numel_overflow": _raw_file({"a": {"dtype": "F32", "shape": [2 ** 30, 2 ** 30, 16],
+                                           "data_offsets": [0, 0]}}, b""),
+        "dim_over_int": _raw_file({"a": {"dtype": "F32", "shape": [2 ** 32, 0], "data_offsets": [0, 0]}}, b""),
     }
     for name, raw in bad.items():
         out = _adapter(tmp_path, {}, raw=raw)
