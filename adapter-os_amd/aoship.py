@@ -58,6 +58,7 @@ _SIGS = {
     "aoship_layer_wait_timeouts": (C.c_int, [_P]),
     "aoship_layer_free": (None, [_P]),
     "aoship_mlp_forward": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "aoship_mlp_forward_noalloc": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "aoship_route_mlp_forward": (C.c_int, [_P, _P, _P, C.c_int, _P, _P, C.c_int, _P, _P, _P]),
     "aoship_proj_forward": (C.c_int, [_P, C.c_char_p, _P, C.c_int, _P, _P]),
     "aoship_qkv_forward": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P]),
@@ -373,6 +374,11 @@ class Layer:
 
     def mlp_forward(self, x, rings, y) -> None:
         _check(lib().aoship_mlp_forward(self.h, _ptr(x), x.shape[0], _ptr(rings), _ptr(y)), "aoship_mlp_forward")
+
+    def mlp_forward_noalloc(self, x, rings, y) -> None:
+        """The decode MLP with its workspace in the device's static scratch (no allocation)."""
+        _check(lib().aoship_mlp_forward_noalloc(self.h, _ptr(x), x.shape[0], _ptr(rings), _ptr(y)),
+               "aoship_mlp_forward_noalloc")
 
     def route_mlp_forward(self, router, features, router_w, x, rings, y, status=None) -> None:
         """Route the tokens from features (device float32 [T, d]) and run the MLP on them in one

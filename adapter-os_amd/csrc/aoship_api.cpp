@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -47,6 +48,40 @@ extern "C" double aoship_internal_exp_cr(double x) { return aos_exp_cr(x); }
 
 static int g_device = -1;
 
+/* ---- the allocation-free decode forward's scratch ----
+ * One static device array (each GPU holds its own copy, at its own address, until the process
+ * ends): arrival counters (zero at rest), generation-stamped ready flags (zero at first use),
+ * then the workspace. Host code never uses the array's name as an address: at set-up, with the
+ * device current, hipGetSymbolAddress gives this device's copy, kept per device. */
+#define AOS_SCRATCH_BYTES ((size_t)32 << 20)
+#define AOS_SCRATCH_CTR_BYTES ((size_t)256 << 10)
+#define AOS_SCRATCH_FLAG_BYTES ((size_t)2 << 20)
+#define AOS_SCRATCH_WS_BYTES (AOS_SCRATCH_BYTES - AOS_SCRATCH_CTR_BYTES - AOS_SCRATCH_FLAG_BYTES)
+#define AOS_MAX_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[AOS_SCRATCH_BYTES];
+
+struct ScratchDev {
+  unsigned char *ptr = nullptr; /* this device's copy of scratch */
+  uint32_t gen = 0;             /* generation of its flags */
+};
+static ScratchDev g_scratch[AOS_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+/* Once per device, with that device current: look up its copy of the array and clear the counter
+ * and flag regions (the workspace needs no initial contents). */
+static int scratch_setup(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (dev < 0 || dev >= AOS_MAX_DEVICES) return set_err("scratch: device index out of range");
+  if (g_scratch[dev].ptr) return 0;
+  void *p = nullptr;
+  HIP_OR_FAIL(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  HIP_OR_FAIL(hipMemset(p, 0, AOS_SCRATCH_CTR_BYTES + AOS_SCRATCH_FLAG_BYTES), "hipMemset(scratch)");
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  g_scratch[dev].ptr = (unsigned char *)p;
+  g_scratch[dev].gen = 0;
+  return 0;
+}
+
 static int ensure_device() {
   if (g_device < 0) return set_err("aoship_init() has not been called");
   HIP_OR_FAIL(hipSetDevice(g_device), "hipSetDevice");
@@ -60,6 +95,10 @@ extern "C" int aoship_init(int device) {
   if (device < 0 || device >= count) return set_err("device index out of range");
   HIP_OR_FAIL(hipSetDevice(device), "hipSetDevice");
   g_device = device;
+  /* the allocation-free forward's scratch; a failure here is reported again by that forward,
+   * which retries the set-up on its first call */
+  const std::string keep = g_last_error;
+  if (scratch_setup(device)) g_last_error = keep;
   return 0;
 }
 
@@ -844,6 +883,12 @@ extern "C" int aoship_layer_wait_timeouts(aoship_layer_t *l) {
   if ((l->counters.p && hipMemset(l->counters.p, 0, l->ctr_cap) != hipSuccess) ||
       (l->flags.p && hipMemset(l->flags.p, 0, l->flag_cap) != hipSuccess))
     return set_err("aoship_layer_wait_timeouts: device error");
+  /* the allocation-free forward on this device may have been the one that gave up */
+  if (g_device >= 0 && g_device < AOS_MAX_DEVICES && g_scratch[g_device].ptr) {
+    if (hipMemset(g_scratch[g_device].ptr, 0, AOS_SCRATCH_CTR_BYTES + AOS_SCRATCH_FLAG_BYTES) != hipSuccess)
+      return set_err("aoship_layer_wait_timeouts: device error");
+    g_scratch[g_device].gen = 0;
+  }
   if (hipDeviceSynchronize() != hipSuccess) return set_err("aoship_layer_wait_timeouts: device error");
   l->gen = 0;
   *(volatile uint32_t *)l->wait_host = 0u;
@@ -1609,6 +1654,37 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
     if (mlp_decode_chunk(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, nullptr)) return -1;
   }
   return 0;
+}
+
+/* The decode MLP forward without allocation: the same launches as aoship_mlp_forward for T <= 32
+ * tokens, with the workspace, counters and flags in the device's static scratch instead of the
+ * layer's workspace. No hipMalloc, hipFree, event or other allocating call is made; a call whose
+ * workspace does not fit is rejected. Calls that overlap on one GPU share the scratch and race. */
+extern "C" int aoship_mlp_forward_noalloc(aoship_layer_t *l, const aoship_bf16_t *x, int T,
+                                          const aoship_ring_t *rings, aoship_bf16_t *y) {
+  if (check_common(l, x, T, rings, y)) return -1;
+  if (!l->mats[MOD_GATE].valid || !l->mats[MOD_UP].valid || !l->mats[MOD_DOWN].valid)
+    return set_err("aoship_mlp_forward_noalloc: gate_proj, up_proj and down_proj must be set");
+  const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
+  if (Wu.in != Wg.in || Wu.out != Wg.out || Wd.in != Wg.out || Wd.out != Wg.in)
+    return set_err("aoship_mlp_forward_noalloc: gate/up/down shapes are inconsistent");
+  if (T < 1 || T > AOS_DECODE_MAX_T)
+    return set_err("aoship_mlp_forward_noalloc: T must be 1.." + std::to_string(AOS_DECODE_MAX_T) +
+                   " (decode batches)");
+  if (g_device >= AOS_MAX_DEVICES) return set_err("aoship_mlp_forward_noalloc: device index out of range");
+  ScratchDev &sd = g_scratch[g_device];
+  if (!sd.ptr && scratch_setup(g_device)) return -1;
+  MlpPlan P;
+  plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, P);
+  if (P.bytes > AOS_SCRATCH_WS_BYTES || P.ctr * 4 > AOS_SCRATCH_CTR_BYTES || P.flg * 4 > AOS_SCRATCH_FLAG_BYTES)
+    return set_err("aoship_mlp_forward_noalloc: this layer at " + std::to_string(T) + " tokens needs " +
+                   std::to_string(P.bytes) + " workspace bytes, " + std::to_string(P.ctr * 4) + " counter bytes and " +
+                   std::to_string(P.flg * 4) + " flag bytes; the scratch holds " +
+                   std::to_string(AOS_SCRATCH_WS_BYTES) + ", " + std::to_string(AOS_SCRATCH_CTR_BYTES) + " and " +
+                   std::to_string(AOS_SCRATCH_FLAG_BYTES));
+  const Ws w = {sd.ptr + AOS_SCRATCH_CTR_BYTES + AOS_SCRATCH_FLAG_BYTES, sd.ptr, sd.ptr + AOS_SCRATCH_CTR_BYTES,
+                &sd.gen, false};
+  return mlp_decode_chunk(l, T, x, rings, y, nullptr, &w);
 }
 
 /* Routing from features and the MLP of one layer in one call: at decode the router runs in the

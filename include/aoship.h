@@ -245,6 +245,17 @@ void aoship_layer_free(aoship_layer_t *layer);
 int aoship_mlp_forward(aoship_layer_t *layer, const aoship_bf16_t *x, int T,
                        const aoship_ring_t *rings, aoship_bf16_t *y);
 
+/* No counterpart in the reference: the decode MLP forward (aoship_mlp_forward's launches, T <= 32)
+ * for callers that cannot allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc). Its workspace, counters and flags live in a static device array
+ * of 32 MiB (about 29.75 MiB of workspace) that each GPU holds until the process ends; a layer and
+ * token count whose workspace does not fit is rejected with an error (-1), as is T > 32. Makes no
+ * hipMalloc, hipFree or other allocating call. The array keeps the last call's contents; calls that
+ * overlap on one GPU (on different streams) share it and race: serialise them. Output equals
+ * aoship_mlp_forward's bit for bit. Returns 0 / -1. */
+int aoship_mlp_forward_noalloc(aoship_layer_t *layer, const aoship_bf16_t *x, int T,
+                               const aoship_ring_t *rings, aoship_bf16_t *y);
+
 /* One decode step of a layer's MLP with its tokens routed in the same call: the router's decision
  * from features (aoship_route_features: Router::route_with_adapter_info_and_scope_with_ctx,
  * router.rs:1567-1952, with the plain router settings) feeds the MLP (aoship_mlp_forward: the
