@@ -113,6 +113,8 @@ def lib():
         L.aoship_internal_exp_cr.argtypes = [C.c_double]
         L.aoship_internal_layer_set_separate_shrinks.restype = C.c_int
         L.aoship_internal_layer_set_separate_shrinks.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_last_perm.restype = C.c_int
+        L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
         L.aoship_internal_decode_geometry.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                                       C.POINTER(C.c_int), C.POINTER(C.c_int)]
@@ -350,6 +352,14 @@ class Layer:
         launch that reads it)."""
         _check(lib().aoship_internal_layer_set_separate_shrinks(self.h, 1 if on else 0),
                "aoship_internal_layer_set_separate_shrinks")
+
+    def last_perm(self):
+        """Token order (sorted position -> token) of the last grouped MLP prefill chunk, or None."""
+        buf = np.zeros(4096, dtype=np.uint16)
+        n = lib().aoship_internal_layer_last_perm(self.h, buf.ctypes.data, buf.size)
+        if n < 0:
+            raise AosError(last_error())
+        return buf[:n].copy() if n else None
 
     def wait_timeouts(self) -> int:
         """1 if a fused decode launch's bounded wait gave up since the last call (the layer's

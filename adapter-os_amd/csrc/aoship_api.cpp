@@ -604,19 +604,16 @@ enum {
   KS_GEMV_PROJ,
   KS_PPLAN,
   KS_PSHRINK_X,
-  KS_PFINISH_X,
   KS_GEMM_GU,
   KS_PSHRINK_H,
-  KS_PFINISH_H,
   KS_GEMM_DOWN,
   KS_GEMM_PROJ,
   KS_COUNT
 };
 static const char *kStatNames[KS_COUNT] = {
     "route",         "lora_shrink_x",   "q4_gemv_gate_up", "lora_shrink_h",
-    "q4_gemv_down",  "q4_gemv_proj",    "prefill_plan",
-    "lora_pshrink_x", "lora_pfinish_x", "q4_gemm_gate_up", "lora_pshrink_h",
-    "lora_pfinish_h", "q4_gemm_down",   "q4_gemm_proj"};
+    "q4_gemv_down",  "q4_gemv_proj",    "prefill_group_plan",
+    "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -635,6 +632,8 @@ struct aoship_layer {
   DevBuf ws, counters, flags;
   size_t ws_cap = 0, ctr_cap = 0, flag_cap = 0;
   uint32_t gen = 0;        /* generation of the last fused launch (flags are raised to it) */
+  const uint16_t *last_perm = nullptr; /* token order of the last grouped prefill chunk (device) */
+  int last_perm_T = 0;
   bool separate_shrinks = false; /* each decode shrink in a launch of its own (diagnostic) */
   hipStream_t stream = nullptr;
   bool profiling = false;
@@ -903,6 +902,20 @@ static int check_no_timeout(aoship_layer *l) {
   return 0;
 }
 
+/* Diagnostic (no counterpart in the reference): the token order (sorted position -> token) of the
+ * layer's last grouped MLP prefill chunk, copied to perm[T] on the host after synchronising; valid
+ * until the layer's next forward. Returns the chunk's token count, 0 when it was not grouped (no
+ * adapters), -1 on error. */
+extern "C" int aoship_internal_layer_last_perm(aoship_layer_t *l, uint16_t *perm, int cap) {
+  if (!l || !perm) return set_err("aoship_internal_layer_last_perm: null argument");
+  if (ensure_device()) return -1;
+  if (!l->last_perm) return 0;
+  if (cap < l->last_perm_T) return set_err("aoship_internal_layer_last_perm: buffer too small");
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  HIP_OR_FAIL(hipMemcpy(perm, l->last_perm, (size_t)l->last_perm_T * 2, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  return l->last_perm_T;
+}
+
 /* Diagnostic (no counterpart in the reference): run each decode LoRA shrink in a launch of its
  * own instead of in the first workgroups of the GEMV launch that reads it. Same results within
  * the layer's tolerance; used to test the fused launches against separate ones. */
@@ -973,6 +986,8 @@ struct Bump {
 static int ws_reserve(aoship_layer *l, size_t bytes, size_t ctr_words, size_t flag_words = 0) {
   if (bytes > l->ws_cap) {
     HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    l->last_perm = nullptr;
+    l->last_perm_T = 0;
     if (l->ws.alloc(bytes, false)) return -1;
     l->ws_cap = bytes;
   }
@@ -1289,148 +1304,164 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
 
 /* ---- prefill (T > 32 tokens) ---- */
 
-/* Plan of one prefill chunk: the adapter union and coefficients, then per module set a shrink
- * (S over the union's rank rows, ks partial sums) and the GEMMs that consume it. */
+/* Plan of one prefill chunk: the group plan (token order, tile unions, coefficients, pointer
+ * tables), then per module set a tile shrink and the GEMMs that consume it. lora is false when no
+ * bound adapter has any of the call's modules: the GEMMs then run in token order with no plan. */
 struct PrefillPlan {
-  aos_pplan_params pp;
-  int umax = 1, mtiles = 0;
+  aos_gplan_params gp;
+  int mtiles = 0, tu_cap = 1;
+  bool lora = false;
 };
 
-/* Union plan of one prefill call; tabs are the modules (in the order of the call's GEMMs) whose
- * per-slot B pointers the plan tabulates. */
+/* Group plan of one prefill call; tabs are the modules (in the order of the call's GEMMs) whose
+ * A and B pointers the plan tabulates. */
 static void plan_prefill_common(aoship_layer *l, Carve &cv, const aoship_ring_t *rings, int T,
                                 const aos_lora_tab *tabs, int nm, PrefillPlan &P) {
   const int n = (int)l->table.size();
-  int umax = n < 8 * T ? n : 8 * T;
-  if (umax < 1) umax = 1;
-  P.umax = umax;
   P.mtiles = ceil_div(T, AOS_GEMM_BM);
-  aos_pplan_params &pp = P.pp;
-  memset(&pp, 0, sizeof(pp));
-  pp.rings = rings;
-  pp.T = T;
-  pp.n = n;
-  pp.bound = l->bound.as<uint8_t>();
-  pp.scale = l->scale_all.as<float>();
-  pp.plan = cv.b.take<aos_pplan>(1);
-  pp.cstride = umax;
-  pp.coef = cv.b.take<float>((size_t)T * umax);
-  pp.mwords = ceil_div(umax, 32);
-  pp.tile_mask = cv.b.take<uint32_t>((size_t)P.mtiles * pp.mwords);
-  pp.nmod = nm;
-  for (int i = 0; i < nm; ++i) pp.tab[i] = tabs[i];
-  pp.bp = cv.b.take<const uint16_t *>((size_t)nm * umax);
+  P.tu_cap = n < AOS_TILE_U_MAX ? (n > 0 ? n : 1) : AOS_TILE_U_MAX;
+  P.lora = false;
+  for (int i = 0; i < nm; ++i) P.lora = P.lora || (tabs[i].rpad > 0 && n > 0);
+  aos_gplan_params &gp = P.gp;
+  memset(&gp, 0, sizeof(gp));
+  if (!P.lora) return;
+  gp.rings = rings;
+  gp.T = T;
+  gp.n = n;
+  gp.bound = l->bound.as<uint8_t>();
+  gp.scale = l->scale_all.as<float>();
+  gp.tu_cap = P.tu_cap;
+  gp.perm = cv.b.take<uint16_t>((size_t)T);
+  gp.tu = cv.b.take<int>((size_t)P.mtiles);
+  gp.list = cv.b.take<uint16_t>((size_t)P.mtiles * P.tu_cap);
+  gp.coef = cv.b.take<float>((size_t)T * P.tu_cap);
+  gp.nmod = nm;
+  for (int i = 0; i < nm; ++i) gp.tab[i] = tabs[i];
+  gp.ap = cv.b.take<const uint16_t *>((size_t)nm * P.mtiles * P.tu_cap);
+  gp.bp = cv.b.take<const uint16_t *>((size_t)nm * P.mtiles * P.tu_cap);
 }
 
-/* Shrink over the union for nm modules sharing x: K splits so that the grid has about 512
- * workgroups, at least 4 groups per split and at most 16 splits. */
-static void plan_pshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const uint16_t *x, int T, int in,
-                         const aos_lora_tab *tabs, int nm, aos_pshrink_params &sp) {
+/* Tile shrink over modules [m0, m0 + nm) of the plan (sharing x, whose rows are read through perm,
+ * or in sorted order when perm is NULL). K slices: about 512 workgroups over the tiles, at least 8
+ * groups a slice, at most 16 slices, and the slices' partial sums within 128 MiB. */
+static void plan_tshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const uint16_t *x, const uint16_t *perm,
+                         int T, int in, int m0, int nm, aos_tshrink_params &sp) {
   memset(&sp, 0, sizeof(sp));
+  if (!P.lora) return;
   sp.x = x;
+  sp.perm = perm;
   sp.T = T;
   sp.in = in;
   sp.nmod = nm;
-  sp.plan = P.pp.plan;
-  sp.umax = P.umax;
-  sp.coef = P.pp.coef;
-  sp.cstride = P.pp.cstride;
-  sp.mtiles = P.mtiles;
-  sp.zero_row = l->zeros.as<uint16_t>();
-  int off = 0, cols_max = 0;
+  int cols = 0;
   for (int i = 0; i < nm; ++i) {
-    sp.tab[i] = tabs[i];
-    sp.s_off[i] = off;
-    const int c = P.umax * tabs[i].rpad;
-    off += c;
-    cols_max = c > cols_max ? c : cols_max;
+    sp.rpad[i] = P.gp.tab[m0 + i].rpad;
+    cols += P.tu_cap * sp.rpad[i];
   }
-  sp.s_stride = off > 0 ? off : 16;
-  sp.cblocks = ceil_div(cols_max, 128);
+  if (cols == 0) {
+    sp.nmod = 0; /* nothing to shrink: no launch */
+    return;
+  }
+  sp.tu = P.gp.tu;
+  sp.coef = P.gp.coef;
+  sp.tu_cap = P.tu_cap;
+  sp.ap = P.gp.ap ? P.gp.ap + (size_t)m0 * P.mtiles * P.tu_cap : nullptr;
+  sp.mtiles = P.mtiles;
+  sp.s_stride = ceil_div(cols, 64) * 64;
+  sp.csets = ceil_div(cols, 128);
   const int G = in / 64;
-  const int wg = P.mtiles * (sp.cblocks > 0 ? sp.cblocks : 1) * nm;
-  int ks = ceil_div(512, wg);
-  int cap = G / 4;
-  if (cap < 1) cap = 1;
-  if (cap > 16) cap = 16;
-  if (ks > cap) ks = cap;
+  int ks = ceil_div(512, P.mtiles);
+  if (ks > 16) ks = 16;
+  if (ks > G / 8) ks = G / 8;
   if (ks < 1) ks = 1;
-  sp.gpk = ceil_div(G, ks);
-  sp.ks = ceil_div(G, sp.gpk);
+  while (ks > 1 && (size_t)P.mtiles * ks * AOS_GEMM_BM * sp.s_stride * 4 > ((size_t)128 << 20)) --ks;
+  sp.ks = ks;
+  sp.part = cv.b.take<float>((size_t)P.mtiles * ks * AOS_GEMM_BM * sp.s_stride);
+  sp.counters = cv.counters((size_t)P.mtiles * sp.csets);
+  sp.flags = cv.flag_lines((size_t)P.mtiles * sp.csets * 32);
   sp.SA = cv.b.take<uint16_t>((size_t)T * sp.s_stride);
-  sp.part = sp.ks > 1 ? cv.b.take<float>((size_t)sp.ks * T * sp.s_stride) : nullptr;
+  sp.zero_row = l->zeros.as<uint16_t>();
+  sp.timeout = l->wait_dev;
 }
 
-/* GEMM of matrix W0 (module mi0 of the plan's tables) or, in SwiGLU mode, W0 and W1 (module
- * mi0 + 1). */
-static void plan_gemm(aoship_layer *l, const PrefillPlan &P, const aos_pshrink_params &sp, const Q4Mat &W0,
-                      const Q4Mat *W1, const uint16_t *x, int T, int mi0, const aos_lora_tab &t0, int off0,
-                      const aos_lora_tab *t1, int off1, uint16_t *y, aos_gemm_params &g) {
+/* GEMM of matrix W0 (module mod0 of the plan's tables) or, in SwiGLU mode, W0 and W1 (module
+ * mod0 + 1), its expand reading the shrink sp's columns: nbefore modules of sp come before mod0's. */
+static void plan_gemm(aoship_layer *l, const PrefillPlan &P, const aos_tshrink_params &sp, const Q4Mat &W0,
+                      const Q4Mat *W1, const uint16_t *x, const uint16_t *in_perm, const uint16_t *out_perm, int T,
+                      int mod0, int nbefore, uint16_t *y, aos_gemm_params &g) {
   memset(&g, 0, sizeof(g));
   g.w0 = W0.dev();
   if (W1) g.w1 = W1->dev();
   g.x = x;
   g.T = T;
-
-  g.tab0 = t0;
-  if (t1) g.tab1 = *t1;
+  g.y = y;
+  g.zero = l->zeros.as<uint16_t>();
+  g.mtiles = P.mtiles;
+  g.tu_cap = P.tu_cap;
+  if (!P.lora || sp.nmod == 0) return; /* token order, no expand */
+  g.in_perm = in_perm;
+  g.out_perm = out_perm;
+  g.rpad0 = P.gp.tab[mod0].rpad;
+  g.rpad1 = W1 ? P.gp.tab[mod0 + 1].rpad : 0;
+  g.mod0 = mod0;
+  g.tu = P.gp.tu;
+  g.bp = P.gp.bp;
   g.SA = sp.SA;
   g.sa_stride = sp.s_stride;
-  g.s_off0 = off0;
-  g.s_off1 = off1;
-  g.plan = P.pp.plan;
-  g.tile_mask = P.pp.tile_mask;
-  g.mwords = P.pp.mwords;
-  g.umax = P.umax;
-  g.bp0 = P.pp.bp ? P.pp.bp + (size_t)mi0 * P.umax : nullptr;
-  g.bp1 = P.pp.bp && t1 ? P.pp.bp + (size_t)(mi0 + 1) * P.umax : nullptr;
-  g.lsteps_max = aos_lstep_bound(P.umax, t0.rpad) + (t1 ? aos_lstep_bound(P.umax, t1->rpad) : 0);
-  g.zero = l->zeros.as<uint16_t>();
-  g.y = y;
+  g.sa_mod_before = nbefore;
+  for (int i = 0; i < nbefore && i < 2; ++i) g.rpad_before[i] = sp.rpad[i];
 }
 
 struct MlpPrefill {
   PrefillPlan P;
-  aos_pshrink_params sx, sh;
+  aos_tshrink_params sx, sh;
   aos_gemm_params g1, g2;
-  size_t bytes = 0, ctr = 0;
+  size_t bytes = 0, ctr = 0, flg = 0;
 };
 
 static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const aoship_ring_t *rings, uint16_t *y,
-                             void *ws, void *ctr, MlpPrefill &M) {
+                             void *ws, void *ctr, void *flg, MlpPrefill &M) {
   const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
   const int H = Wg.in, I = Wg.out;
-  aos_lora_tab tgu[2] = {lora_tab(l, MOD_GATE, H, I), lora_tab(l, MOD_UP, H, I)};
-  aos_lora_tab td = lora_tab(l, MOD_DOWN, I, H);
-  Carve cv(ws, ctr);
-  const aos_lora_tab tall[3] = {tgu[0], tgu[1], td};
+  Carve cv(ws, ctr, flg);
+  const aos_lora_tab tall[3] = {lora_tab(l, MOD_GATE, H, I), lora_tab(l, MOD_UP, H, I), lora_tab(l, MOD_DOWN, I, H)};
   plan_prefill_common(l, cv, rings, T, tall, 3, M.P);
-  uint16_t *h = cv.b.take<uint16_t>((size_t)T * I);
-  plan_pshrink(l, cv, M.P, x, T, H, tgu, 2, M.sx);
-  plan_gemm(l, M.P, M.sx, Wg, &Wu, x, T, 0, tgu[0], M.sx.s_off[0], &tgu[1], M.sx.s_off[1], h, M.g1);
-  plan_pshrink(l, cv, M.P, h, T, I, &td, 1, M.sh);
-  plan_gemm(l, M.P, M.sh, Wd, nullptr, h, T, 2, td, 0, nullptr, 0, y, M.g2);
+  uint16_t *h = cv.b.take<uint16_t>((size_t)T * I); /* sorted rows when grouped */
+  const uint16_t *perm = M.P.lora ? M.P.gp.perm : nullptr;
+  plan_tshrink(l, cv, M.P, x, perm, T, H, 0, 2, M.sx);
+  plan_gemm(l, M.P, M.sx, Wg, &Wu, x, perm, nullptr, T, 0, 0, h, M.g1);
+  plan_tshrink(l, cv, M.P, h, nullptr, T, I, 2, 1, M.sh);
+  plan_gemm(l, M.P, M.sh, Wd, nullptr, h, nullptr, perm, T, 2, 0, y, M.g2);
+  if (M.P.lora && M.sh.nmod == 0) M.g2.out_perm = perm; /* h is in sorted order even without a down expand */
+  if (M.P.lora && M.sx.nmod == 0) M.g1.in_perm = perm;
   M.bytes = cv.b.off + 256;
   M.ctr = cv.coff + 64;
+  M.flg = cv.foff + 64;
 }
 
 static int launch_err(int e, const char *what);
 
-/* Launch the prefill plan (union, coefficients, tile masks). */
-static int launch_pplan(aoship_layer *l, const aos_pplan_params &pp) {
+/* Launch the group plan (nothing without adapters). */
+static int launch_gplan(aoship_layer *l, const PrefillPlan &P) {
   aos_launch_ctx c0 = launch_ctx(l, KS_PPLAN);
-  return launch_err(aos_launch_pplan(&pp, &c0), "prefill plan");
+  if (!P.lora) {
+    AOS_SKIP(&c0);
+    return 0;
+  }
+  return launch_err(aos_launch_gplan(&P.gp, &c0), "prefill group plan");
 }
 
-/* Launch a prefill shrink and, with K splits, its finishing sum (nothing when no bound adapter
- * has these modules). */
-static int launch_pshrink(aoship_layer *l, const aos_pshrink_params &sp, int slot_shrink, int slot_finish) {
-  if (sp.cblocks == 0) return 0;
-  aos_launch_ctx c0 = launch_ctx(l, slot_shrink);
-  if (launch_err(aos_launch_pshrink(&sp, &c0), "lora shrink (prefill)")) return -1;
-  if (sp.ks == 1) return 0;
-  aos_launch_ctx c1 = launch_ctx(l, slot_finish);
-  return launch_err(aos_launch_pfinish(&sp, &c1), "lora shrink sum (prefill)");
+/* Launch a tile shrink (nothing when no bound adapter has its modules) with a new generation for
+ * its meeting flags. */
+static int launch_tshrink(aoship_layer *l, const aos_tshrink_params &sp, int slot) {
+  aos_launch_ctx c0 = launch_ctx(l, slot);
+  if (sp.nmod == 0) {
+    AOS_SKIP(&c0);
+    return 0;
+  }
+  aos_tshrink_params q = sp;
+  q.gen = next_gen(&l->gen);
+  return launch_err(aos_launch_tshrink(&q, &c0), "lora shrink (prefill)");
 }
 
 static int chunk_prefill_t(int T) { return T < AOS_PREFILL_MAX_T ? T : AOS_PREFILL_MAX_T; }
@@ -1452,9 +1483,10 @@ extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
   }
   if (mlp && max_tokens > AOS_DECODE_MAX_T) {
     MlpPrefill M;
-    plan_mlp_prefill(l, chunk_prefill_t(max_tokens), nullptr, nullptr, nullptr, nullptr, nullptr, M);
+    plan_mlp_prefill(l, chunk_prefill_t(max_tokens), nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M);
     if (M.bytes > bytes) bytes = M.bytes;
     if (M.ctr > ctr) ctr = M.ctr;
+    if (M.flg > flg) flg = M.flg;
   }
   return ws_reserve(l, bytes, ctr, flg);
 }
@@ -1636,14 +1668,17 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
     for (int t0 = 0; t0 < T; t0 += AOS_PREFILL_MAX_T) {
       const int Tc = chunk_prefill_t(T - t0);
       MlpPrefill M;
-      plan_mlp_prefill(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, M);
-      if (ws_reserve(l, M.bytes, M.ctr)) return -1;
-      plan_mlp_prefill(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p, M);
-      if (launch_pplan(l, M.P.pp)) return -1;
-      if (launch_pshrink(l, M.sx, KS_PSHRINK_X, KS_PFINISH_X)) return -1;
+      plan_mlp_prefill(l, Tc, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M);
+      if (ws_reserve(l, M.bytes, M.ctr, M.flg)) return -1;
+      plan_mlp_prefill(l, Tc, x + (size_t)t0 * H, rings + t0, y + (size_t)t0 * H, l->ws.p, l->counters.p,
+                       l->flags.p, M);
+      l->last_perm = M.P.lora ? M.P.gp.perm : nullptr;
+      l->last_perm_T = M.P.lora ? Tc : 0;
+      if (launch_gplan(l, M.P)) return -1;
+      if (launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
       aos_launch_ctx c2 = launch_ctx(l, KS_GEMM_GU);
       if (launch_err(aos_launch_gemm(&M.g1, 1, &c2), "q4 gemm gate/up")) return -1;
-      if (launch_pshrink(l, M.sh, KS_PSHRINK_H, KS_PFINISH_H)) return -1;
+      if (launch_tshrink(l, M.sh, KS_PSHRINK_H)) return -1;
       aos_launch_ctx c4 = launch_ctx(l, KS_GEMM_DOWN);
       if (launch_err(aos_launch_gemm(&M.g2, 0, &c4), "q4 gemm down")) return -1;
     }
@@ -1727,19 +1762,21 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
       aos_lora_tab tabs[3];
       for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
       PrefillPlan P;
-      aos_pshrink_params sp;
+      aos_tshrink_params sp;
       aos_gemm_params gp[3];
       for (int pass = 0; pass < 2; ++pass) {
-        Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr);
+        Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr, pass ? l->flags.p : nullptr);
         plan_prefill_common(l, cv, rings + t0, Tc, tabs, nm, P);
-        plan_pshrink(l, cv, P, xc, Tc, in, tabs, nm, sp);
-        for (int i = 0; i < nm; ++i)
-          plan_gemm(l, P, sp, l->mats[mods[i]], nullptr, xc, Tc, i, tabs[i], sp.s_off[i], nullptr, 0,
+        const uint16_t *perm = P.lora ? P.gp.perm : nullptr;
+        plan_tshrink(l, cv, P, xc, perm, Tc, in, 0, nm, sp);
+        for (int i = 0; i < nm; ++i) {
+          plan_gemm(l, P, sp, l->mats[mods[i]], nullptr, xc, perm, perm, Tc, i, i,
                     ys[i] + (size_t)t0 * l->mats[mods[i]].out, gp[i]);
-        if (pass == 0 && ws_reserve(l, cv.b.off + 256, cv.coff + 64)) return -1;
+        }
+        if (pass == 0 && ws_reserve(l, cv.b.off + 256, cv.coff + 64, cv.foff + 64)) return -1;
       }
-      if (launch_pplan(l, P.pp)) return -1;
-      if (launch_pshrink(l, sp, KS_PSHRINK_X, KS_PFINISH_X)) return -1;
+      if (launch_gplan(l, P)) return -1;
+      if (launch_tshrink(l, sp, KS_PSHRINK_X)) return -1;
       for (int i = 0; i < nm; ++i) {
         aos_launch_ctx cg = launch_ctx(l, KS_GEMM_PROJ);
         if (launch_err(aos_launch_gemm(&gp[i], 0, &cg), "q4 gemm")) return -1;

@@ -69,6 +69,18 @@ __device__ __forceinline__ u32x4 aos_q4_magic(uint32_t w, uint32_t smask, uint32
 __device__ __forceinline__ uint32_t aos_q4_mask() { return __builtin_amdgcn_readfirstlane(0x000F000Fu); }
 __device__ __forceinline__ uint32_t aos_q4_exp() { return 0x43004300u; }
 
+/* 16-byte load through the global address space. Pointers read from tables (adapter rows, the
+ * union's B pointers) are otherwise generic, and a generic (flat) load counts against the LDS
+ * counter as well: every later wait for an LDS access would then also wait for it. */
+__device__ __forceinline__ u32x4 aos_gld16(const void *p) {
+  return *(const __attribute__((address_space(1))) u32x4 *)p;
+}
+
+/* A pointer stored in global memory (a table), loaded through the global address space. */
+__device__ __forceinline__ const uint16_t *aos_gld_ptr(const void *p) {
+  return (const uint16_t *)*(const __attribute__((address_space(1))) uint64_t *)p;
+}
+
 __device__ __forceinline__ uint32_t aos_shfl(uint32_t v, int src_lane) {
   return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
 }

@@ -1,6 +1,7 @@
 /*
- * aoship_gemm.hip — prefill path (T > 32 tokens): adapter plan, LoRA shrink and the int4 GEMM
- * with fused LoRA expand (+ SwiGLU), all on the matrix cores.
+ * aoship_gemm.hip — prefill path (T > 32 tokens): token grouping by adapter set, the LoRA shrink
+ * over each tile's adapters, and the int4 GEMM with the fused LoRA expand (+ SwiGLU), all on the
+ * matrix cores.
  *
  * Computes the MLX forward's linear(x, W) + apply_lora(x) (mlx_cpp_wrapper_real.cpp:3372-3419)
  * for a block of tokens, and in SwiGLU mode h = (g * sigmoid(g)) * u (:3509-3522); the ring ->
@@ -8,25 +9,28 @@
  * (crates/adapteros-lora-mlx-ffi/src/backend.rs:398-428).
  *
  * Launch sequence of one call:
- *   1. pplan         (one per M tile) union of the adapters the tokens use (ascending), the
- *                                     tile's per-token coefficients over the union and the
- *                                     bitmask of union slots any of its 128 tokens uses;
- *   3. pshrink       S = x . A^T over the union's rank rows, float32, K split into ks partial
- *                                     sums; pfinish adds them in split order and applies each
- *                                     token's coefficient: SA = bf16(coef * S);
- *   4. gemm          int4 GEMM, the expand over the tile's union slots added to the same
- *                                     accumulators after the K loop.
+ *   1. gplan    group the tokens by their active adapter set (groups in the order of their first
+ *               token, tokens in index order: deterministic); for each 128-token tile of that order, the
+ *               union of the adapters its tokens use, the tokens' coefficients over it and the
+ *               union's A and B pointers;
+ *   2. tshrink  S = x . A^T over each tile's union columns, K split into slices; the last slice of
+ *               a tile to finish adds the slices in order and stores SA = bf16(coef * S);
+ *   3. gemm     int4 GEMM over the sorted tiles (x rows gathered through the permutation), the
+ *               expand over the tile's union columns added to the same accumulators after the
+ *               K loop, outputs stored in sorted order (h) or scattered back (y).
+ * Grouping makes a tile's union the one or two adapter sets of its tokens instead of every
+ * adapter the whole batch uses.
  *
  * GEMM tiling for gfx950 (v_mfma_f32_32x32x16_bf16, 64-wide waves):
- *   - a workgroup of 4 waves covers 32 * MT tokens; each wave owns NR 32-row blocks of weights
+ *   - a workgroup of WV waves covers 128 tokens; each wave owns a 32-row block of weights
  *     (SwiGLU: the same rows of gate and up) for all the tokens of the tile;
  *   - weights come straight from the q4-tile layout (one 16-byte load per lane per group and row
  *     block) into registers through a ring D groups deep and are dequantised there to bfloat16
  *     B fragments (w = s * q + b in float32, hardware round-to-nearest-even packing), so each
  *     weight is read and dequantised once per workgroup;
- *   - the token tile of each group (32 * MT rows x 64 bf16) is staged in LDS, double buffered,
+ *   - the token tile of each group (128 rows x 64 bf16) is staged in LDS, double buffered,
  *     with an XOR swizzle of its 16-byte chunks so that fragment reads are free of bank
- *     conflicts; the four waves share it;
+ *     conflicts; the waves share it;
  *   - workgroups are ordered so that the token tiles of one weight block run back to back on one
  *     XCD, whose L2 then serves the weight re-reads.
  */
@@ -37,6 +41,9 @@
 namespace {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int BM = AOS_GEMM_BM; /* tokens per tile */
+constexpr int SC1 = 16;         /* buffer cache policy: device-coherent (sc1) */
 
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -83,35 +90,27 @@ __device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float b) {
  * consecutive rows read one chunk each without a bank conflict. */
 __device__ __forceinline__ int tile_off(int r, int chunk) { return r * 128 + ((chunk ^ ((r >> 1) & 7)) << 4); }
 
-/* Stage the [BM x 64] bf16 slice of group g of the token rows m0... with NT threads. Rows past
- * the last token repeat it: they only feed accumulator rows that are never stored. */
-template <int BM, int NT = 256>
+/* Stages the [BM x 64] bf16 slice of group g of a tile's token rows with NT threads. Row r of
+ * the tile is token perm[m0 + r] (m0 + r without a permutation); rows past the last token repeat
+ * it: they only feed accumulator rows that are never stored. */
+template <int NT>
 struct Stager {
   static constexpr int CH = BM * 8 / NT; /* 16-byte chunks per thread */
   u32x4 v[CH];
-  __device__ __forceinline__ void load(const uint16_t *x, int in, int T, int m0, int g, int tid) {
+  int off[CH]; /* element offset of each chunk's row and column in group 0 */
+  __device__ __forceinline__ void rows(const uint16_t *perm, int in, int T, int m0, int tid) {
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
       const int idx = tid + k * NT;
       const int r = idx >> 3, ch = idx & 7;
-      const int tok = m0 + r < T ? m0 + r : T - 1;
-      v[k] = *(const u32x4 *)(x + (size_t)tok * in + (size_t)g * 64 + ch * 8);
+      const int ps = m0 + r < T ? m0 + r : T - 1;
+      const int tok = perm ? (int)perm[ps] : ps;
+      off[k] = tok * in + ch * 8;
     }
   }
-  /* 64 columns of the rows of a tile-based buffer (rows bytes apart, rows >= nrows repeat the
-   * last): byte columns cb .. cb + 127; chunks at or past lim bytes read as zeros (an offset
-   * past the buffer's end). */
-  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t rs, int row_bytes, int nrows, int cb, int lim,
-                                           int tid) {
+  __device__ __forceinline__ void load(const uint16_t *x, int g) {
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int idx = tid + k * NT;
-      const int r = idx >> 3, ch = idx & 7;
-      const int rr = r < nrows ? r : nrows - 1;
-      const int c = cb + ch * 16;
-      const int off = c < lim ? rr * row_bytes + c : (int)0x80000000;
-      v[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
-    }
+    for (int k = 0; k < CH; ++k) v[k] = *(const u32x4 *)(x + off[k] + g * 64);
   }
   __device__ __forceinline__ void store(unsigned char *buf, int tid) const {
 #pragma unroll
@@ -124,53 +123,305 @@ struct Stager {
 };
 
 /* ------------------------------------------------------------------------------------------ */
-/* plan                                                                                       */
+/* group plan                                                                                 */
 /* ------------------------------------------------------------------------------------------ */
 
-/* One workgroup per M tile of AOS_GEMM_BM tokens. Every workgroup scans all the rings and
- * derives the same union (workgroup 0 stores it); each then writes the coefficient rows of its
- * own tokens and its tile's slot mask. Every ring a thread scans, the bound flags and the
- * scales are loaded before anything waits, so the scan costs one memory round trip. */
-constexpr int PLAN_NT = 1024;
-constexpr int PLAN_RINGS = AOS_PREFILL_MAX_T / PLAN_NT; /* rings per thread */
-
-__global__ void __launch_bounds__(PLAN_NT) aos_pplan_kernel(aos_pplan_params p) {
-  __shared__ uint32_t bits[AOS_MAX_ADAPTERS / 32];
-  __shared__ uint32_t mask[AOS_MAX_ADAPTERS / 32];
-  __shared__ int base[AOS_MAX_ADAPTERS / 32 + 1];
-  __shared__ uint8_t bound_s[AOS_MAX_ADAPTERS];
-  __shared__ float scale_s[AOS_MAX_ADAPTERS];
-  const int tid = threadIdx.x;
-  const int words = (p.n + 31) >> 5;
-  u32x2 rw[PLAN_RINGS][5];
+/* A ring as ten 32-bit words (top_k, position, four words of adapter indices, four of gates). */
+struct RingWords {
+  uint32_t w[10];
+  __device__ __forceinline__ void load(const aoship_ring_t *r) {
+    const u32x2 *src = (const u32x2 *)r;
 #pragma unroll
-  for (int j = 0; j < PLAN_RINGS; ++j) {
-    const int t = tid + j * PLAN_NT;
-    const u32x2 *r = (const u32x2 *)(p.rings + (t < p.T ? t : p.T - 1));
-#pragma unroll
-    for (int w = 0; w < 5; ++w) rw[j][w] = r[w];
-  }
-  for (int a = tid; a < p.n; a += PLAN_NT) {
-    bound_s[a] = p.bound[a];
-    scale_s[a] = p.scale[a];
-  }
-  for (int w = tid; w < words; w += PLAN_NT) bits[w] = 0u;
-  for (int w = tid; w < p.mwords; w += PLAN_NT) mask[w] = 0u;
-  __syncthreads();
-  /* union over every token's active slots */
-#pragma unroll
-  for (int j = 0; j < PLAN_RINGS; ++j) {
-    if (tid + j * PLAN_NT >= p.T) continue;
-    const uint32_t k = rw[j][0].x;
-    const uint32_t idx[4] = {rw[j][1].x, rw[j][1].y, rw[j][2].x, rw[j][2].y}; /* adapter_indices */
-    const uint32_t gq[4] = {rw[j][3].x, rw[j][3].y, rw[j][4].x, rw[j][4].y};  /* gates_q15 */
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int a = (int)((idx[s >> 1] >> (16 * (s & 1))) & 0xffffu);
-      const int q = (int)(int16_t)((gq[s >> 1] >> (16 * (s & 1))) & 0xffffu);
-      if (s < (int)k && q > 0 && a < p.n && bound_s[a] && !((bits[a >> 5] >> (a & 31)) & 1u))
-        atomicOr(&bits[a >> 5], 1u << (a & 31));
+    for (int k = 0; k < 5; ++k) {
+      const u32x2 v = src[k];
+      w[2 * k] = v.x;
+      w[2 * k + 1] = v.y;
     }
+  }
+  __device__ __forceinline__ uint32_t top_k() const { return w[0]; }
+  __device__ __forceinline__ int adapter(int s) const { return (int)((w[2 + (s >> 1)] >> (16 * (s & 1))) & 0xffffu); }
+  __device__ __forceinline__ int gate(int s) const { return (int)(int16_t)((w[6 + (s >> 1)] >> (16 * (s & 1))) & 0xffffu); }
+};
+
+/* The active slots of a ring (prepare_lora_for_ring, backend.rs:409-425: slot s < top_k, gate
+ * q > 0, a bound adapter index < n), each adapter once (its first slot): bit s of the result.
+ * bound is the layer's bound flags in LDS. */
+__device__ __forceinline__ uint32_t ring_set(const RingWords &r, int n, const uint8_t *bound, uint16_t (&ids)[8]) {
+  uint32_t act = 0, mask = 0;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int a = r.adapter(s);
+    ids[s] = (uint16_t)a;
+    if (s < (int)r.top_k() && r.gate(s) > 0 && a < n && bound[a]) act |= 1u << s;
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    bool dup = false;
+#pragma unroll
+    for (int s2 = 0; s2 < s; ++s2) dup |= ((act >> s2) & 1u) && ids[s2] == ids[s];
+    if (((act >> s) & 1u) && !dup) mask |= 1u << s;
+  }
+  return mask;
+}
+
+/* 32-bit hash of an adapter set, independent of the slots' order (a sum of mixed ids, then a
+ * finaliser); the empty set hashes to 0 and every other set to a nonzero value, so tokens without
+ * adapters sort first. Equal sets hash equally; a collision between different sets only
+ * interleaves their tokens. */
+__device__ __forceinline__ uint32_t set_hash(const uint16_t (&ids)[8], uint32_t mask) {
+  if (!mask) return 0u;
+  uint32_t h = 0;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    if ((mask >> s) & 1u) {
+      uint32_t v = (uint32_t)ids[s] * 0x9E3779B1u + 0x7F4A7C15u;
+      v ^= v >> 16;
+      v *= 0x85EBCA6Bu;
+      v ^= v >> 13;
+      h += v;
+    }
+  h ^= h >> 15;
+  h *= 0x2c1b3c6du;
+  h ^= h >> 12;
+  return h ? h : 1u;
+}
+
+constexpr int GP_NT = 1024;
+constexpr int GP_HT = 2 * AOS_PREFILL_MAX_T; /* hash table slots (load factor <= 1/2) */
+constexpr int GP_BLK = AOS_PREFILL_MAX_T / 64; /* 64-token blocks: (pass, wave) in token order */
+constexpr int GP_SMALL = 64;                   /* groups ranked with ballots; more fall back to a sort */
+constexpr uint32_t GP_EMPTY = 0xffffffffu;
+
+/* Dynamic LDS of the plan kernel. */
+constexpr int GP_OFF_TABH = 0;
+constexpr int GP_OFF_TABF = GP_OFF_TABH + GP_HT * 4;
+constexpr int GP_OFF_BOUND = GP_OFF_TABF + GP_HT * 4;
+constexpr int GP_OFF_BLK = GP_OFF_BOUND + AOS_MAX_ADAPTERS;
+constexpr int GP_OFF_MISC = GP_OFF_BLK + GP_SMALL * GP_BLK * 4;
+constexpr int GP_LDS = GP_OFF_MISC + (AOS_MAX_ADAPTERS / 32) * 4 + (AOS_MAX_ADAPTERS / 32 + 1) * 4 +
+                       (GP_BLK + GP_SMALL + 2) * 4;
+
+/* Compare-exchange of a bitonic network between this lane's key and the key of lane ^ d: the
+ * lower lane keeps the smaller key of an ascending pair. */
+__device__ __forceinline__ uint64_t bitonic_lane(uint64_t a, int lane, int d, bool up) {
+  const uint64_t b = aos_shfl64(a, lane ^ d);
+  const bool lower = (lane & d) == 0;
+  const bool take_min = lower == up;
+  return take_min ? (a < b ? a : b) : (a > b ? a : b);
+}
+
+/* Bitonic sort of key[0, NP) in LDS by the workgroup (element i: thread i % GP_NT); stages whose
+ * partner lies in the same wave exchange through lane shuffles. */
+__device__ void gp_sort(uint64_t *key, int NP) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int k = 2; k <= NP; k <<= 1) {
+    int j = k >> 1;
+    for (; j >= 64; j >>= 1) {
+      for (int i = tid; i < NP; i += GP_NT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t a = key[i], b = key[ixj];
+          if (((i & k) == 0) ? (a > b) : (a < b)) {
+            key[i] = b;
+            key[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    for (int i0 = 0; i0 < NP; i0 += GP_NT) {
+      const int i = i0 + tid;
+      if (i < NP) { /* uniform per wave: NP and GP_NT are multiples of 64 */
+        uint64_t v = key[i];
+        const bool up = (i & k) == 0;
+        for (int d = j; d > 0; d >>= 1) v = bitonic_lane(v, lane, d, up);
+        key[i] = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+/* One workgroup per tile; every workgroup derives the same order of all the tokens, then writes
+ * its own tile's slice: perm, the tile union (ascending), the pointer tables and the coefficient
+ * rows.
+ *
+ * The order: tokens with equal adapter sets (equal set hashes) form a group; groups come in the
+ * order of their first token, tokens within a group in index order. Each token finds its group's
+ * first token through an LDS hash table (atomicMin per slot); the group index is the count of
+ * first tokens before it. With at most GP_SMALL groups a token's position is its group's start
+ * plus its rank among the group's tokens before it, counted with one ballot per (group, 64-token
+ * block); otherwise the (first token, token) keys are sorted. */
+__global__ void __launch_bounds__(GP_NT) aos_gplan_kernel(aos_gplan_params p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char gsm[];
+  uint32_t *tab_h = (uint32_t *)(gsm + GP_OFF_TABH);
+  uint32_t *tab_f = (uint32_t *)(gsm + GP_OFF_TABF);
+  uint8_t *bound_s = (uint8_t *)(gsm + GP_OFF_BOUND);
+  uint32_t *blk = (uint32_t *)(gsm + GP_OFF_BLK);               /* [GP_SMALL][GP_BLK] */
+  uint32_t *bits = (uint32_t *)(gsm + GP_OFF_MISC);            /* [AOS_MAX_ADAPTERS / 32] */
+  int *base = (int *)(bits + AOS_MAX_ADAPTERS / 32);           /* [.. + 1] */
+  uint32_t *wsum = (uint32_t *)(base + AOS_MAX_ADAPTERS / 32 + 1); /* [GP_BLK] */
+  uint32_t *gstart = wsum + GP_BLK;                            /* [GP_SMALL + 1] */
+  uint32_t *ngroups = gstart + GP_SMALL + 1;
+  uint16_t *tperm = (uint16_t *)tab_h; /* sorted position -> token, once the table is done */
+  uint64_t *key = (uint64_t *)tab_h;   /* sort keys of the fallback, likewise */
+  constexpr int RPT = AOS_PREFILL_MAX_T / GP_NT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, T = p.T, n = p.n;
+  const uint64_t lt = (1ull << lane) - 1ull;
+
+  for (int a = tid; a < n; a += GP_NT) bound_s[a] = p.bound[a];
+  for (int e = tid; e < GP_HT; e += GP_NT) {
+    tab_h[e] = GP_EMPTY;
+    tab_f[e] = GP_EMPTY;
+  }
+  RingWords rw[RPT];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) {
+    const int t = tid + q * GP_NT;
+    if (t < T) rw[q].load(p.rings + t);
+  }
+  __syncthreads();
+  /* group of each token: its set's hash, inserted into the table; the slot keeps the lowest token.
+   * Within a wave the lanes of one set elect their lowest lane (its token is the set's lowest in
+   * the wave), which alone touches the table: one pair of LDS atomics per set and wave. */
+  uint32_t slot[RPT];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) {
+    const int t = tid + q * GP_NT;
+    uint32_t h = 0;
+    if (t < T) {
+      uint16_t ids[8];
+      h = set_hash(ids, ring_set(rw[q], n, bound_s, ids));
+      h = h == GP_EMPTY ? GP_EMPTY - 1u : h;
+    }
+    slot[q] = 0;
+    uint64_t todo = __ballot(t < T);
+    while (todo) { /* uniform: todo is the same in every lane */
+      const int leader = __ffsll((long long)todo) - 1;
+      const uint32_t h0 = aos_shfl(h, leader);
+      const uint64_t same = __ballot(h == h0) & todo;
+      uint32_t sl = 0;
+      if (lane == leader) {
+        sl = (h0 * 0x9E3779B1u) >> 19; /* 13 bits: GP_HT slots */
+        for (;;) {
+          const uint32_t old = atomicCAS(&tab_h[sl], GP_EMPTY, h0);
+          if (old == GP_EMPTY || old == h0) break;
+          sl = (sl + 1) & (GP_HT - 1);
+        }
+        atomicMin(&tab_f[sl], (uint32_t)t);
+      }
+      sl = aos_shfl(sl, leader);
+      if ((same >> lane) & 1ull) slot[q] = sl;
+      todo &= ~same;
+    }
+  }
+  __syncthreads();
+  /* group index = number of first tokens before the group's first token: a scan over the
+   * 64-token blocks in token order */
+  uint32_t first[RPT];
+  uint64_t fb[RPT];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) {
+    const int t = tid + q * GP_NT;
+    first[q] = t < T ? tab_f[slot[q]] : GP_EMPTY;
+    fb[q] = __ballot(t < T && first[q] == (uint32_t)t);
+    if (lane == 0) wsum[q * (GP_NT / 64) + wave] = (uint32_t)__popcll(fb[q]);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t acc = 0;
+    for (int b = 0; b < GP_BLK; ++b) {
+      const uint32_t v = wsum[b];
+      wsum[b] = acc;
+      acc += v;
+    }
+    *ngroups = acc;
+  }
+  __syncthreads();
+  const uint32_t D = *ngroups;
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) {
+    const int t = tid + q * GP_NT;
+    if (t < T && first[q] == (uint32_t)t) tab_f[slot[q]] = wsum[q * (GP_NT / 64) + wave] + (uint32_t)__popcll(fb[q] & lt);
+  }
+  __syncthreads();
+  uint32_t gid[RPT];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) gid[q] = tid + q * GP_NT < T ? tab_f[slot[q]] : GP_EMPTY;
+  __syncthreads(); /* the table is no longer read: its memory takes the order */
+
+  if (D <= (uint32_t)GP_SMALL) {
+    uint32_t rank[RPT];
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) rank[q] = 0;
+    for (uint32_t g = 0; g < D; ++g) {
+#pragma unroll
+      for (int q = 0; q < RPT; ++q) {
+        const uint64_t b = __ballot(gid[q] == g);
+        if (lane == 0) blk[g * GP_BLK + q * (GP_NT / 64) + wave] = (uint32_t)__popcll(b);
+        if (gid[q] == g) rank[q] = (uint32_t)__popcll(b & lt);
+      }
+    }
+    __syncthreads();
+    if (tid < (int)D) { /* block prefix within group tid, and its size */
+      uint32_t acc = 0;
+      for (int b = 0; b < GP_BLK; ++b) {
+        const uint32_t v = blk[tid * GP_BLK + b];
+        blk[tid * GP_BLK + b] = acc;
+        acc += v;
+      }
+      gstart[tid + 1] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      gstart[0] = 0;
+      for (uint32_t g = 1; g <= D; ++g) gstart[g] += gstart[g - 1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int t = tid + q * GP_NT;
+      if (t < T) tperm[gstart[gid[q]] + blk[gid[q] * GP_BLK + q * (GP_NT / 64) + wave] + rank[q]] = (uint16_t)t;
+    }
+  } else {
+    int NP = 64;
+    while (NP < T) NP <<= 1;
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int t = tid + q * GP_NT;
+      if (t < NP) key[t] = t < T ? ((uint64_t)first[q] << 32) | (uint32_t)t : ~0ull;
+    }
+    __syncthreads();
+    gp_sort(key, NP);
+    /* keys -> tokens in place, a pass of GP_NT at a time: pass j writes bytes 2 i of tperm, which
+     * hold keys below (j + 1) * GP_NT / 4, all read by passes up to j */
+    for (int j = 0; j * GP_NT < T; ++j) {
+      const int i = j * GP_NT + tid;
+      const uint16_t t = i < T ? (uint16_t)(uint32_t)key[i] : 0;
+      __syncthreads();
+      if (i < T) tperm[i] = t;
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+
+  const int mt = blockIdx.x, p0 = mt * BM;
+  const int mtiles = (T + BM - 1) / BM;
+  const int tn = T - p0 < BM ? T - p0 : BM;
+  const int words = (n + 31) >> 5;
+  for (int w = tid; w < words; w += GP_NT) bits[w] = 0u;
+  __syncthreads();
+  uint16_t ids[8];
+  int tok = 0;
+  RingWords r;
+  if (tid < tn) {
+    tok = tperm[p0 + tid];
+    p.perm[p0 + tid] = (uint16_t)tok;
+    r.load(p.rings + tok);
+    const uint32_t set = ring_set(r, n, bound_s, ids);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if ((set >> q) & 1u) atomicOr(&bits[ids[q] >> 5], 1u << (ids[q] & 31));
   }
   __syncthreads();
   if (tid == 0) {
@@ -180,211 +431,256 @@ __global__ void __launch_bounds__(PLAN_NT) aos_pplan_kernel(aos_pplan_params p) 
       acc += __builtin_popcount(bits[w]);
     }
     base[words] = acc;
-    if (blockIdx.x == 0) p.plan->U = acc;
+    p.tu[mt] = acc;
   }
   __syncthreads();
-  if (blockIdx.x == 0) {
-    for (int a = tid; a < p.n; a += PLAN_NT) {
-      const uint32_t m = bits[a >> 5];
-      if ((m >> (a & 31)) & 1u) {
-        const int u = base[a >> 5] + __builtin_popcount(m & ((1u << (a & 31)) - 1u));
-        p.plan->list[u] = (uint16_t)a;
-        p.plan->slot[a] = (int16_t)u;
-        if (u < p.cstride)
-          for (int k = 0; k < p.nmod; ++k)
-            p.bp[(size_t)k * p.cstride + u] = p.tab[k].rpad && a < p.tab[k].n ? p.tab[k].B[a] : nullptr;
-      } else {
-        p.plan->slot[a] = -1;
+  const int U = base[words];
+  const size_t trow = (size_t)mt * p.tu_cap;
+  for (int a = tid; a < n; a += GP_NT) {
+    const uint32_t m = bits[a >> 5];
+    if ((m >> (a & 31)) & 1u) {
+      const int u = base[a >> 5] + __builtin_popcount(m & ((1u << (a & 31)) - 1u));
+      p.list[trow + u] = (uint16_t)a;
+      for (int k = 0; k < p.nmod; ++k) {
+        const aos_lora_tab &tb = p.tab[k];
+        const bool has = tb.rpad && a < tb.n;
+        p.ap[(size_t)k * mtiles * p.tu_cap + trow + u] = has ? tb.A[a] : nullptr;
+        p.bp[(size_t)k * mtiles * p.tu_cap + trow + u] = has ? tb.B[a] : nullptr;
       }
     }
-    for (int u = base[words] + tid; u < p.cstride; u += PLAN_NT)
-      for (int k = 0; k < p.nmod; ++k) p.bp[(size_t)k * p.cstride + u] = nullptr;
   }
-  /* this tile's coefficient rows: zero, then each token's slots by one thread, summed in ring
-   * order per union slot (a slot named twice adds up in order) */
-  const int t0 = blockIdx.x * AOS_GEMM_BM;
-  const int tn = (p.T - t0) < AOS_GEMM_BM ? (p.T - t0) : AOS_GEMM_BM;
-  const int cs = p.cstride;
-  for (int e = tid; e < tn * cs; e += PLAN_NT) p.coef[(size_t)t0 * cs + e] = 0.0f;
-  __syncthreads();
+  /* coefficient rows of the tile: each token's row by one thread, summed in ring order per union
+   * slot (an adapter named twice adds up in order), zeros elsewhere */
   if (tid < tn) {
-    const aoship_ring_t &r = p.rings[t0 + tid];
-    float *row = p.coef + (size_t)(t0 + tid) * cs;
+    float *row = p.coef + (size_t)(p0 + tid) * p.tu_cap;
     int us[8];
     float cv[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int a = r.adapter_indices[s];
-      const int q = r.gates_q15[s];
+      const int a = r.adapter(s);
+      const int q = r.gate(s);
       us[s] = -1;
       cv[s] = 0.0f;
-      if (s < (int)r.top_k && q > 0 && a < p.n && bound_s[a]) {
+      if (s < (int)r.top_k() && q > 0 && a < n && bound_s[a]) {
         const uint32_t m = bits[a >> 5];
         const int u = base[a >> 5] + __builtin_popcount(m & ((1u << (a & 31)) - 1u));
-        const float c = scale_s[a] * ((float)q / 32767.0f);
-        int first = s;
+        const float c = p.scale[a] * ((float)q / 32767.0f);
+        int first_s = s;
 #pragma unroll
         for (int s2 = 0; s2 < s; ++s2)
-          if (first == s && us[s2] == u) first = s2;
-        if (first == s) {
+          if (first_s == s && us[s2] == u) first_s = s2;
+        if (first_s == s) {
           us[s] = u;
           cv[s] = 0.0f + c;
         } else {
-          cv[first] += c;
+          cv[first_s] += c;
         }
-        if (!((mask[u >> 5] >> (u & 31)) & 1u)) atomicOr(&mask[u >> 5], 1u << (u & 31));
       }
     }
+    for (int u = 0; u < U; ++u) {
+      float v = 0.0f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      if (us[s] >= 0) row[us[s]] = cv[s];
+      for (int s = 0; s < 8; ++s)
+        if (us[s] == u) v = cv[s];
+      row[u] = v;
+    }
   }
-  __syncthreads();
-  for (int w = tid; w < p.mwords; w += PLAN_NT) p.tile_mask[(size_t)blockIdx.x * p.mwords + w] = mask[w];
 }
 
 /* ------------------------------------------------------------------------------------------ */
-/* shrink over the union, finished with the coefficients (bf16 SA)                            */
+/* tile shrink                                                                                */
 /* ------------------------------------------------------------------------------------------ */
 
-template <int MT>
-__global__ void __launch_bounds__(256) aos_pshrink_kernel(aos_pshrink_params p) {
-  constexpr int BM = 32 * MT;
-  constexpr int TILE = BM * 128;
+/* Union columns of tile mt for the shrink's modules: module i holds tu * rpad[i] columns after
+ * those of modules before it. */
+__device__ __forceinline__ int tile_cols(const aos_tshrink_params &p, int tu) {
+  int c = 0;
+  for (int i = 0; i < p.nmod; ++i) c += tu * p.rpad[i];
+  return c;
+}
+
+/* Workgroup (K slice kz, column set cs of 128 columns, tile mt), kz fastest; wave w takes the
+ * 32 columns cs * 128 + 32 w .., all 128 tokens (four 32-token sub-tiles). The slice's token
+ * tiles and A fragments are loaded two groups ahead. Once every slice of the (tile, column set)
+ * has published its partial sums (the ks workgroups are consecutive: dispatched together, none
+ * waits on a later one), slice kz sums rows kz * 128 / ks .. of them over the slices in order. */
+__global__ void __launch_bounds__(256) aos_tshrink_kernel(aos_tshrink_params p) {
+  constexpr int MT = BM / 32, TILE = BM * 128;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ uint32_t met;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, c = lane >> 5;
-  const int mi = blockIdx.z / p.ks, kz = blockIdx.z - mi * p.ks;
-  const aos_lora_tab &tab = p.tab[mi];
-  const int rpad = tab.rpad;
-  const int U = p.plan->U < p.umax ? p.plan->U : p.umax;
-  const int col0 = blockIdx.y * 128;
-  /* uniform over the workgroup and over the K splits of this tile: all of them leave together */
-  if (rpad == 0 || col0 >= U * rpad) return;
-  const int m0 = blockIdx.x * BM;
+  const int kz = blockIdx.x, cs = blockIdx.y, mt = blockIdx.z;
+  const int TU = __builtin_amdgcn_readfirstlane(p.tu[mt]);
+  const int C = tile_cols(p, TU);
+  const int csets = (C + 127) / 128;
+  if (cs >= csets) return; /* uniform; such workgroups take no part in the meeting below */
+  const int m0 = mt * BM;
+  const int tn = p.T - m0 < BM ? p.T - m0 : BM;
   const int G = p.in / 64;
-  const int g_lo = kz * p.gpk;
-  const int g_hi = (g_lo + p.gpk) < G ? (g_lo + p.gpk) : G;
+  const int g_lo = (int)((long)kz * G / p.ks), g_hi = (int)((long)(kz + 1) * G / p.ks);
 
-  /* this lane's A row: column col = col0 + 32 wave + i of module mi */
-  const int col = col0 + 32 * wave + i;
-  const int u = col / rpad, j = col - u * rpad;
+  /* this lane's A row: column col of the tile's union columns */
+  const int col = cs * 128 + 32 * wave + i;
   const uint16_t *arow = p.zero_row;
   size_t kstep = 0;
-  if (u < U) {
-    const uint16_t *A = tab.A[p.plan->list[u]];
+  if (col < C) {
+    int mi = 0, off = 0;
+    while (mi < p.nmod - 1 && col >= off + TU * p.rpad[mi]) {
+      off += TU * p.rpad[mi];
+      ++mi;
+    }
+    const int rp = p.rpad[mi];
+    const int u = (col - off) / rp, j = col - off - u * rp;
+    const uint16_t *A = p.ap[((size_t)mi * p.mtiles + mt) * p.tu_cap + u];
     if (A) {
       arow = A + (size_t)j * p.in;
       kstep = 1;
     }
   }
+  auto aload = [&](int g, u32x4 (&a)[4]) {
+    const int gc = g < g_hi ? g : g_hi - 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[s] = aos_gld16(arow + kstep * ((size_t)gc * 64 + 16 * s + 8 * c));
+  };
 
   f32x16 acc[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
-
-  Stager<BM> st;
-  u32x4 an[4];
-  st.load(p.x, p.in, p.T, m0, g_lo, tid);
-  st.store(smem, tid);
+  for (int s = 0; s < MT; ++s) acc[s] = f32x16{};
+  if (g_lo < g_hi) {
+    Stager<256> st0, st1;
+    st0.rows(p.perm, p.in, p.T, m0, tid);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) an[s] = *(const u32x4 *)(arow + kstep * ((size_t)g_lo * 64 + 16 * s + 8 * c));
-  lds_barrier();
-  for (int g = g_lo; g < g_hi; ++g) {
-    const unsigned char *tb = smem + ((g - g_lo) & 1) * TILE;
-    u32x4 a[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) a[s] = an[s];
-    const int gn = g + 1 < g_hi ? g + 1 : g_hi - 1;
-    st.load(p.x, p.in, p.T, m0, gn, tid);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) an[s] = *(const u32x4 *)(arow + kstep * ((size_t)gn * 64 + 16 * s + 8 * c));
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = mt * 32 + i;
-      u32x4 xv[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xv[s] = *(const u32x4 *)(tb + tile_off(r, 2 * s + c)); /* K 16 s + 8 c */
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc[mt] = aos_mfma32(xv[s], a[s], acc[mt]);
-    }
-    st.store(smem + (((g - g_lo) & 1) ^ 1) * TILE, tid);
+    for (int k = 0; k < Stager<256>::CH; ++k) st1.off[k] = st0.off[k];
+    u32x4 a0[4], a1[4];
+    st0.load(p.x, g_lo);
+    st1.load(p.x, g_lo + 1 < g_hi ? g_lo + 1 : g_hi - 1);
+    aload(g_lo, a0);
+    aload(g_lo + 1, a1);
+    st0.store(smem, tid);
     lds_barrier();
-  }
-
-  const int scol = p.s_off[mi] + col;
-  const bool col_live = col < U * rpad;
-  const int uc = col_live ? u : 0;
-  if (p.ks == 1) {
+    /* group g from LDS buffer (g - g_lo) & 1 with A fragments a; hold (group g + 1) goes to the
+     * other buffer, ld receives group g + 2 and a is refilled with group g + 2 after its MFMAs.
+     * Every load is unconditional (clamped to the slice), so no branch separates a load from its
+     * use and the compiler waits for exactly the loads each step needs. */
+    auto step = [&](int g, Stager<256> &hold, Stager<256> &ld, u32x4 (&a)[4]) {
+      const unsigned char *tb = smem + ((g - g_lo) & 1) * TILE;
+      ld.load(p.x, g + 2 < g_hi ? g + 2 : g_hi - 1);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int s = 0; s < MT; ++s) {
+        const int r = s * 32 + i;
+        u32x4 xv[4];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int tok = m0 + mt * 32 + aos_acc_m(v, lane);
-        if (col_live && tok < p.T)
-          p.SA[(size_t)tok * p.s_stride + scol] =
-              aos_f32_to_bf16(p.coef[(size_t)tok * p.cstride + uc] * acc[mt][v]);
+        for (int k = 0; k < 4; ++k) xv[k] = *(const u32x4 *)(tb + tile_off(r, 2 * k + c)); /* K 16 k + 8 c */
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[s] = aos_mfma32(xv[k], a[k], acc[s]);
       }
-    return;
-  }
-  /* K split: plain float32 partial sums, added in split order by aos_pfinish_kernel */
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int tok = m0 + mt * 32 + aos_acc_m(v, lane);
-      if (col_live && tok < p.T) p.part[((size_t)kz * p.T + tok) * p.s_stride + scol] = acc[mt][v];
+      aload(g + 2, a);
+      hold.store(smem + (((g - g_lo) & 1) ^ 1) * TILE, tid);
+      lds_barrier();
+    };
+    int g = g_lo;
+    for (; g + 1 < g_hi; g += 2) {
+      step(g, st1, st0, a0);
+      step(g + 1, st0, st1, a1);
     }
-}
-
-/* SA[t][col] = bf16(coef[t][u(col)] * sum_kz part[kz][t][col]), four columns per thread. */
-__global__ void __launch_bounds__(256) aos_pfinish_kernel(aos_pshrink_params p) {
-  const int q4 = p.s_stride / 4; /* s_stride is a multiple of 16 */
-  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= (size_t)p.T * q4) return;
-  const int t = (int)(e / q4);
-  const int col = (int)(e - (size_t)t * q4) * 4;
-  int mi = 0;
-  for (int k = 1; k < p.nmod; ++k)
-    if (col >= p.s_off[k]) mi = k;
-  const int rpad = p.tab[mi].rpad;
-  if (rpad == 0) return;
-  const int u = (col - p.s_off[mi]) / rpad;
-  const int U = p.plan->U < p.umax ? p.plan->U : p.umax;
-  if (u >= U) return;
-  const size_t kstride = (size_t)p.T * p.s_stride;
-  const float *pp = p.part + (size_t)t * p.s_stride + col;
-  float4 sum = *(const float4 *)pp;
-  for (int k = 1; k < p.ks; ++k) {
-    const float4 v = *(const float4 *)(pp + k * kstride);
-    sum.x += v.x;
-    sum.y += v.y;
-    sum.z += v.z;
-    sum.w += v.w;
+    if (g < g_hi) step(g, st1, st0, a0);
   }
-  const float cf = p.coef[(size_t)t * p.cstride + u];
-  u32x2 o;
-  o.x = (uint32_t)aos_f32_to_bf16(cf * sum.x) | ((uint32_t)aos_f32_to_bf16(cf * sum.y) << 16);
-  o.y = (uint32_t)aos_f32_to_bf16(cf * sum.z) | ((uint32_t)aos_f32_to_bf16(cf * sum.w) << 16);
-  *(u32x2 *)(p.SA + (size_t)t * p.s_stride + col) = o;
+
+  /* this slice's partial sums, device-coherent (the other slices read them), column-major:
+   * registers 4q .. 4q + 3 of a lane hold four consecutive rows of its column, one 16-byte store */
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(p.part + (size_t)mt * p.ks * p.s_stride * BM), (short)0, (int)((size_t)p.ks * p.s_stride * BM * 4),
+      0x00020000);
+  if (col < C) {
+    const int cbase = (kz * p.s_stride + col) * BM;
+#pragma unroll
+    for (int s = 0; s < MT; ++s)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 v = {acc[s][4 * q], acc[s][4 * q + 1], acc[s][4 * q + 2], acc[s][4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs,
+                                               (cbase + s * 32 + 8 * q + 4 * c) * 4, 0, SC1);
+      }
+  }
+  /* meet the other slices of this (tile, column set): the last to arrive resets the count and
+   * raises the flag to this launch's generation */
+  aos_mem_wait();
+  __syncthreads();
+  if (tid == 0) {
+    const size_t gi = (size_t)mt * p.csets + cs;
+    bool ok = true;
+    if (aos_arrive(&p.counters[gi]) == (uint32_t)p.ks - 1u) {
+      aos_reset(&p.counters[gi]);
+      aos_raise(p.flags + gi * 32, p.gen);
+    } else {
+      ok = aos_wait_gen(p.flags + gi * 32, p.gen);
+      if (!ok && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    met = ok ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!met) return;
+
+  /* this slice's share of the column set (blocks of 4 columns kz, kz + ks, ..., all the rows):
+   * SA = bf16(coef * sum of the slices in order) over blocks of 4 rows x 4 columns, the row block
+   * fastest across lanes so that each load reads consecutive rows of one column; every slice's
+   * loads of a block are in flight before the adds */
+  const int nrb = (tn + 3) / 4;
+  const int c0 = cs * 128, cn = C - c0 < 128 ? C - c0 : 128;
+  const int ncb = cn / 4; /* C is a multiple of 16 */
+  const int mycb = ncb > kz ? (ncb - kz + p.ks - 1) / p.ks : 0;
+  for (int e = tid; e < mycb * nrb; e += 256) {
+    const int r = (e % nrb) * 4, cc = c0 + (kz + (e / nrb) * p.ks) * 4;
+    f32x4 sum[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
+                    {0.0f, 0.0f, 0.0f, 0.0f}}; /* sum[j]: column cc + j, rows r .. r + 3 */
+    for (int k0 = 0; k0 < p.ks; k0 += 4) {
+      f32x4 v[4][4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int kk = k0 + k < p.ks ? k0 + k : p.ks - 1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          v[k][j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((kk * p.s_stride + cc + j) * BM + r) * 4, 0, SC1));
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k0 + k < p.ks) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sum[j] += v[k][j];
+        }
+    }
+    int mi = 0, off = 0;
+    while (mi < p.nmod - 1 && cc >= off + TU * p.rpad[mi]) {
+      off += TU * p.rpad[mi];
+      ++mi;
+    }
+    const int u = (cc - off) / p.rpad[mi];
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      if (r + e2 >= tn) break;
+      const float cf = p.coef[(size_t)(m0 + r + e2) * p.tu_cap + u];
+      u32x2 o;
+      o.x = (uint32_t)aos_f32_to_bf16(cf * sum[0][e2]) | ((uint32_t)aos_f32_to_bf16(cf * sum[1][e2]) << 16);
+      o.y = (uint32_t)aos_f32_to_bf16(cf * sum[2][e2]) | ((uint32_t)aos_f32_to_bf16(cf * sum[3][e2]) << 16);
+      *(u32x2 *)(p.SA + (size_t)(m0 + r + e2) * p.s_stride + cc) = o;
+    }
+  }
 }
 
 /* ------------------------------------------------------------------------------------------ */
 /* int4 GEMM + LoRA expand (+ SwiGLU)                                                          */
 /* ------------------------------------------------------------------------------------------ */
 
-/* Expand K steps: the LoRA expand of a token tile runs as extra K steps of 64 columns after the
- * weight groups. The token operand is SA (coefficient-scaled shrink of the union slots), the
- * weight operand the union adapters' B rows (bf16). A step is listed as (module << 15) | j, j =
- * index of its 64 columns among the module's union columns u * rpad + r; a tile lists only the
- * steps that hold a slot one of its tokens uses.
- *
- * LDS after the token tiles: 16 bytes of counts, the slot mask words of the BM / 128 plan tiles
- * the token tile spans, LBP B pointers per module (two modules), then the step list. */
+/* Expand K steps: the LoRA expand of a token tile runs as extra K steps of 64 union columns after
+ * the weight groups: module 0's ceil(TU * rpad0 / 64) steps, then module 1's (SwiGLU). The token
+ * operand is the tile's SA columns (coefficient-scaled shrink), the weight operand the union
+ * adapters' B rows (bf16). LDS after the token tiles: 16 bytes of counts, then up to LBP B
+ * pointers per module (loaded at kernel start while the tile union is small enough). */
 constexpr int LBP = 256;
-constexpr int MASK_WORDS = AOS_MAX_ADAPTERS / 32;
-__host__ __device__ constexpr int gemm_aux(int bm) { return 16 + 4 * MASK_WORDS * (bm / AOS_GEMM_BM) + 2 * LBP * 8; }
+__host__ __device__ constexpr int gemm_aux() { return 16 + 2 * LBP * 8; }
 
 /* Workgroup b of a grid of mb token tiles x nb weight blocks -> (token tile, weight block).
  * Workgroup b runs on XCD b % 8. With a multiple of 8 token tiles each XCD takes its own token
@@ -405,115 +701,61 @@ __device__ __forceinline__ void gemm_tile_of(int b, int mb, int nb, int &mbi, in
   }
 }
 
-/* The expand steps of one token tile (BM tokens, WV waves, NM modules). Each lane's B fragment
- * word w of a step holds union columns k = 64 j + koff[w] .. +7 of the lane's weight row:
+/* The expand steps of one token tile (WV waves, NM modules). Each lane's B fragment word w of a
+ * step holds union columns k = 64 j + koff[w] .. +7 of the lane's weight row:
  * B_{list[u]}[row][k - u * rpad .. +7] with u = k / rpad, zeros past the union or for an adapter
  * without the module (rpad is a multiple of 16, so 8 columns never straddle two slots). Words
  * w and w + 1 share a slot when NW / NP = 2 (koff 16-aligned for w even). */
-template <int BM, int WV, int NM, int NW, int NP>
+template <int WV, int NM, int NW, int NP>
 struct Expand {
-  static constexpr int MR = BM / AOS_GEMM_BM; /* plan tiles per token tile */
   static constexpr int TILE = BM * 128;
   const aos_gemm_params &p;
   unsigned char *smem;
-  int *ls_n;
-  uint32_t *mw;
   const uint16_t **lbp;
-  uint16_t *ls;
-  int wave, lane, m0, mbi, row, Ue;
-  bool lora, bp_lds;
+  const uint16_t *const *bpt[2];
+  int wave, lane, m0, row, TU, n0, nls, off[2], rp[2];
+  bool bp_lds;
 
   /* row: the lane's weight row (of every module) */
   __device__ Expand(const aos_gemm_params &p_, unsigned char *smem_, int ntile, int wave_, int lane_, int m0_,
-                    int mbi_, int row_)
-      : p(p_), smem(smem_), wave(wave_), lane(lane_), m0(m0_), mbi(mbi_), row(row_) {
-    unsigned char *aux = smem + ntile * TILE;
-    ls_n = (int *)aux;
-    mw = (uint32_t *)(aux + 16);
-    lbp = (const uint16_t **)(aux + 16 + 4 * MASK_WORDS * MR);
-    ls = (uint16_t *)(aux + gemm_aux(BM));
-    lora = (p.tab0.rpad | (NM == 2 ? p.tab1.rpad : 0)) != 0;
-    Ue = p.plan->U < p.umax ? p.plan->U : p.umax;
-    bp_lds = p.umax <= LBP;
+                    int mbi, int row_)
+      : p(p_), smem(smem_), wave(wave_), lane(lane_), m0(m0_), row(row_) {
+    lbp = (const uint16_t **)(smem + ntile * TILE + 16);
+    TU = (p.tu && (p.rpad0 | (NM == 2 ? p.rpad1 : 0))) ? __builtin_amdgcn_readfirstlane(p.tu[mbi]) : 0;
+    rp[0] = p.rpad0;
+    rp[1] = NM == 2 ? p.rpad1 : 0;
+    int before = 0;
+    for (int i = 0; i < p.sa_mod_before; ++i) before += TU * p.rpad_before[i];
+    off[0] = before;
+    off[1] = before + TU * rp[0];
+    n0 = rp[0] ? (TU * rp[0] + 63) >> 6 : 0;
+    nls = n0 + (rp[1] ? (TU * rp[1] + 63) >> 6 : 0);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) bpt[m] = p.bp + ((size_t)(p.mod0 + m) * p.mtiles + mbi) * p.tu_cap;
+    bp_lds = TU <= LBP;
   }
 
-  /* At kernel start: the tile's slot mask words and (union bound <= LBP) the union's B pointers
-   * go straight to LDS; their loads complete during the K loop. */
+  /* At kernel start: the union's B pointers go straight to LDS; their loads complete during the
+   * K loop. */
   __device__ void prefetch() {
-    if (!lora) return;
+    if (nls == 0 || !bp_lds) return;
     constexpr int NT = 64 * WV;
-    const int ptiles = (p.T + AOS_GEMM_BM - 1) / AOS_GEMM_BM;
-    const int pr0 = mbi * MR;
-    const int npr = ptiles - pr0 < MR ? ptiles - pr0 : MR;
-    const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.tile_mask + (size_t)pr0 * p.mwords), (short)0, npr * p.mwords * 4, 0x00020000);
 #pragma unroll
-    for (int r = 0; r < MR; ++r)
-      for (int w0 = wave * 64; w0 < p.mwords; w0 += NT)
+    for (int m = 0; m < NM; ++m) {
+      if (!rp[m]) continue;
+      const __amdgpu_buffer_rsrc_t rb =
+          __builtin_amdgcn_make_buffer_rsrc((void *)bpt[m], (short)0, TU * 8, 0x00020000);
+      for (int d0 = wave * 64; d0 < 2 * TU; d0 += NT)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rm, (__attribute__((address_space(3))) void *)(mw + r * MASK_WORDS + w0), 4,
-            r < npr ? (r * p.mwords + w0 + lane) * 4 : (int)0x80000000, 0, 0, 0);
-    if (bp_lds) {
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        const __amdgpu_buffer_rsrc_t rb =
-            __builtin_amdgcn_make_buffer_rsrc((void *)(m ? p.bp1 : p.bp0), (short)0, p.umax * 8, 0x00020000);
-        for (int d0 = wave * 64; d0 < 2 * p.umax; d0 += NT)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rb, (__attribute__((address_space(3))) void *)((uint32_t *)(lbp + m * LBP) + d0), 4,
-              (d0 + lane) * 4, 0, 0, 0);
-      }
+            rb, (__attribute__((address_space(3))) void *)((uint32_t *)(lbp + m * LBP) + d0), 4,
+            (d0 + lane) * 4, 0, 0, 0);
     }
   }
 
-  /* After the K loop (all waves): wave 0 lists the tile's steps, ascending module then column.
-   * Returns the step count; n0 receives the count of module 0's steps. */
-  __device__ int build(int &n0) {
-    n0 = 0;
-    if (!lora) return 0;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();
-    if (wave == 0) {
-      int n = 0;
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        if (m == 1 && lane == 0) ls_n[1] = n < p.lsteps_max ? n : p.lsteps_max;
-        const int rpad = m ? p.tab1.rpad : p.tab0.rpad;
-        const int nj = rpad ? (Ue * rpad + 63) >> 6 : 0;
-        for (int j0 = 0; j0 < nj; j0 += 64) {
-          const int j = j0 + lane;
-          bool act = false;
-          if (j < nj) {
-            const int ulo = (64 * j) / rpad;
-            int uhi = (64 * j + 63) / rpad;
-            uhi = uhi < Ue - 1 ? uhi : Ue - 1;
-            for (int u = ulo; u <= uhi; ++u) {
-              uint32_t wd = 0;
-#pragma unroll
-              for (int r = 0; r < MR; ++r) wd |= mw[r * MASK_WORDS + (u >> 5)];
-              act |= ((wd >> (u & 31)) & 1u) != 0;
-            }
-          }
-          const uint64_t bal = __ballot(act);
-          const int at = n + __popcll(bal & ((1ull << lane) - 1ull));
-          if (act && at < p.lsteps_max) ls[at] = (uint16_t)((m << 15) | j);
-          n += __popcll(bal);
-        }
-      }
-      if (lane == 0) ls_n[0] = n < p.lsteps_max ? n : p.lsteps_max;
-    }
-    lds_barrier();
-    const int nls = __builtin_amdgcn_readfirstlane(ls_n[0]);
-    n0 = NM == 2 ? __builtin_amdgcn_readfirstlane(ls_n[1]) : nls;
-    return nls;
-  }
-
-  __device__ void step_of(int l, int nls, int &m, int &j, int &rpad) const {
+  __device__ __forceinline__ void step_of(int l, int &m, int &j) const {
     l = l < nls ? l : nls - 1;
-    const int d = __builtin_amdgcn_readfirstlane((int)ls[l > 0 ? l : 0]);
-    m = d >> 15;
-    j = d & 0x7fff;
-    rpad = m ? p.tab1.rpad : p.tab0.rpad;
+    m = l < n0 ? 0 : 1;
+    j = l - (m ? n0 : 0);
   }
 
   /* Runs the nls steps in chunks of LC steps within one module. A chunk's token tiles (the
@@ -522,40 +764,46 @@ struct Expand {
    * registers; one wait per chunk, the next chunk's B pointers loading meanwhile. mma(m, n, bv)
    * adds the chunk's n steps of module m (token tile q at smem + q * TILE). */
   template <int LC, class Mma>
-  __device__ void run(int nls, int n0, const int (&koff)[NW], Mma &&mma) {
+  __device__ void run(const int (&koff)[NW], Mma &&mma) {
+    if (nls == 0) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier(); /* the prefetched pointers, and every wave past the K loop's last LDS reads */
     const int rows = p.T - m0 < BM ? p.T - m0 : BM;
     const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.SA + (size_t)m0 * p.sa_stride), (short)0, rows * p.sa_stride * 2, 0x00020000);
     auto load_ptrs = [&](int l, const uint16_t *(&pr)[NP]) {
-      int m, j, rpad;
-      step_of(l, nls, m, j, rpad);
-      const uint16_t *const *bp = m ? p.bp1 : p.bp0;
+      int m, j;
+      step_of(l, m, j);
 #pragma unroll
       for (int h = 0; h < NP; ++h) {
-        int u = (64 * j + koff[h * (NW / NP)]) / rpad;
-        u = u < Ue ? u : Ue - 1;
-        pr[h] = bp_lds ? lbp[m * LBP + u] : bp[u];
+        int u = (64 * j + koff[h * (NW / NP)]) / rp[m];
+        u = u < TU ? u : TU - 1;
+        /* two explicit loads (LDS, global) and a select of the value: a select of the two
+         * addresses would make one generic load */
+        const uint16_t *from_lds =
+            (const uint16_t *)((const __attribute__((address_space(3))) uint64_t *)lbp)[m * LBP + (u < LBP ? u : 0)];
+        pr[h] = bp_lds ? from_lds : aos_gld_ptr(bpt[m] + u);
       }
     };
     auto load_frags = [&](int l, const uint16_t *const (&pr)[NP], u32x4 (&bv)[NW]) {
-      int m, j, rpad;
-      step_of(l, nls, m, j, rpad);
+      int m, j;
+      step_of(l, m, j);
+      const int r = rp[m];
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         const uint16_t *b = pr[w / (NW / NP)];
         const int k = 64 * j + koff[w];
-        const int u = k / rpad;
-        const uint16_t *src = (u < Ue && b) ? b + (size_t)row * rpad + (k - u * rpad) : p.zero;
-        bv[w] = *(const u32x4 *)src;
+        const int u = k / r;
+        const uint16_t *src = (u < TU && b) ? b + (size_t)row * r + (k - u * r) : p.zero;
+        bv[w] = aos_gld16(src);
       }
     };
     /* token tile of step l into LDS region q: BM / 8 blocks of 8 rows (1 KB), lane l of a block
      * writing bytes 16 l, i.e. row 8 b + l / 8, slot l % 8, which holds chunk slot ^ ((r >> 1) & 7) */
     auto dma_tile = [&](int q, int l) {
-      int m, j, rpad;
-      step_of(l, nls, m, j, rpad);
-      const int off = m ? p.s_off1 : p.s_off0;
-      const int cb = (off + 64 * j) * 2, lim = (off + Ue * rpad) * 2, rb = p.sa_stride * 2;
+      int m, j;
+      step_of(l, m, j);
+      const int cb = (off[m] + 64 * j) * 2, lim = (off[m] + TU * rp[m]) * 2, rb = p.sa_stride * 2;
 #pragma unroll
       for (int k = 0; k < BM / 8 / WV; ++k) {
         const int bk = k * WV + wave;
@@ -598,17 +846,15 @@ struct Expand {
   }
 };
 
-/* Single-matrix kernel (and SwiGLU for short prefills) on v_mfma_f32_32x32x16_bf16.
+/* Single-matrix kernel (and SwiGLU) on v_mfma_f32_32x32x16_bf16.
  * SW: SwiGLU (gate and up rows of one 32-row block per wave) or a single matrix (one 32-row
- * block per wave); MT: 32-token sub-tiles (token tile of 32 MT rows, a multiple of the 128-token
- * plan tile); D: weight ring depth (divides the group count); DB: token tile loads two groups
+ * block per wave); D: weight ring depth (divides the group count); DB: token tile loads two groups
  * ahead (two register stages); APF: next sub-tile's LDS fragments loaded before the current
  * MFMAs; WV: waves per workgroup; OCC: waves per SIMD the registers are sized for; LC: expand
  * steps per chunk (their token tiles occupy LC LDS regions). */
-template <bool SW, int MT, int D, bool DBT, bool APF, int WV, int OCC, int LC>
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC>
 __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params p) {
-  static_assert(MT % 4 == 0, "token tiles are whole plan tiles");
-  constexpr int BM = 32 * MT;
+  constexpr int MT = BM / 32;
   constexpr int TILE = BM * 128;
   constexpr int NT = 64 * WV;
   constexpr int NTILE = LC > 2 ? LC : 2;
@@ -657,15 +903,20 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
    * flight. With D even, two register stages let the loads run two groups ahead of their LDS
    * store. */
   constexpr bool DB = DBT && (D % 2) == 0;
-  Stager<BM, NT> st0, st1;
-  st0.load(p.x, in, p.T, m0, 0, tid);
-  Expand<BM, WV, SW ? 2 : 1, 4, 2> ex(p, smem, NTILE, wave, lane, m0, mbi, row);
+  Stager<NT> st0, st1;
+  st0.rows(p.in_perm, in, p.T, m0, tid);
+  st0.load(p.x, 0);
+  if (DB) {
+#pragma unroll
+    for (int k = 0; k < Stager<NT>::CH; ++k) st1.off[k] = st0.off[k];
+  }
+  Expand<WV, SW ? 2 : 1, 4, 2> ex(p, smem, NTILE, wave, lane, m0, mbi, row);
   ex.prefetch();
   st0.store(smem, tid);
   lds_barrier();
 
   /* token tile of weight group gx (clamped: the tiles staged past the last group are not read) */
-  auto stage = [&](Stager<BM, NT> &st, const int gx) { st.load(p.x, in, p.T, m0, gx < G ? gx : G - 1, tid); };
+  auto stage = [&](Stager<NT> &st, const int gx) { st.load(p.x, gx < G ? gx : G - 1); };
   if (DB) stage(st1, 1);
 
   /* dequantise ring slot d into B fragments, then refill it with group gn */
@@ -690,7 +941,7 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
   };
 
   /* one K group: ld receives group g + 2 (g + 1 without DB), sto holds group g + 1 */
-  auto group = [&](const int g, const int d, Stager<BM, NT> &ld, Stager<BM, NT> &sto) {
+  auto group = [&](const int g, const int d, Stager<NT> &ld, Stager<NT> &sto) {
     const unsigned char *tb = smem + (g & 1) * TILE;
     /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
     u32x4 a[4];
@@ -738,10 +989,8 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
     }
   }
 
-  /* LoRA expand: word s of lane (i, c) covers step columns 32 c + 8 s .. +7 */
-  int n0;
-  const int nls = ex.build(n0);
-  if (nls > 0) {
+  /* LoRA expand over the tile union: word s of lane (i, c) covers step columns 32 c + 8 s .. +7 */
+  {
     const int koff[4] = {32 * c, 32 * c + 8, 32 * c + 16, 32 * c + 24};
     auto mma_into = [&](int n, const u32x4 (&bv)[LC][4], f32x16 (&acc)[MT]) {
 #pragma unroll
@@ -758,7 +1007,7 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
         }
       }
     };
-    ex.template run<LC>(nls, n0, koff, [&](int m, int n, const u32x4 (&bv)[LC][4]) {
+    ex.template run<LC>(koff, [&](int m, int n, const u32x4 (&bv)[LC][4]) {
       if (!SW || m == 0)
         mma_into(n, bv, acc0);
       else
@@ -766,15 +1015,16 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
     });
   }
 
-  /* epilogue */
+  /* epilogue: sorted row m0 + r goes to output row out_perm[m0 + r] (or m0 + r) */
   if (!live) return;
   const int out = p.w0.out;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int tok = m0 + mt * 32 + aos_acc_m(v, lane);
-      if (tok >= p.T) continue;
+      const int ps = m0 + mt * 32 + aos_acc_m(v, lane);
+      if (ps >= p.T) continue;
+      const int tok = p.out_perm ? (int)p.out_perm[ps] : ps;
       if (SW) {
         const float gt = acc0[mt][v], up = acc1[mt][v];
         const float sg = 1.0f / (1.0f + expf(-gt));
@@ -788,23 +1038,29 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
 
 }  // namespace
 
-extern "C" int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx) {
-  const int mtiles = (p->T + AOS_GEMM_BM - 1) / AOS_GEMM_BM;
-  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->n > AOS_MAX_ADAPTERS) return (int)hipErrorInvalidValue;
-  AOS_LAUNCH(ctx, aos_pplan_kernel, dim3(mtiles), dim3(PLAN_NT), 0, *p);
+extern "C" int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx) {
+  const int mtiles = (p->T + BM - 1) / BM;
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->n > AOS_MAX_ADAPTERS || p->nmod < 0 || p->nmod > 3)
+    return (int)hipErrorInvalidValue;
+  const int ucap = p->n < AOS_TILE_U_MAX ? p->n : AOS_TILE_U_MAX;
+  if (p->tu_cap < ucap || p->tu_cap < 1) return (int)hipErrorInvalidValue;
+  AOS_LAUNCH(ctx, aos_gplan_kernel, dim3(mtiles), dim3(GP_NT), GP_LDS, *p);
   return (int)hipGetLastError();
 }
 
-extern "C" int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx) {
-  constexpr int MT = AOS_GEMM_BM / 32;
-  dim3 grid(p->mtiles, p->cblocks, p->ks * p->nmod);
-  AOS_LAUNCH(ctx, aos_pshrink_kernel<MT>, grid, dim3(256), 2 * AOS_GEMM_BM * 128, *p);
-  return (int)hipGetLastError();
-}
-
-extern "C" int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx) {
-  const size_t n = (size_t)p->T * (p->s_stride / 4);
-  AOS_LAUNCH(ctx, aos_pfinish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, *p);
+extern "C" int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx) {
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->nmod < 1 || p->nmod > 3 || p->ks < 1 || p->csets < 1 ||
+      p->mtiles != (p->T + BM - 1) / BM || p->in % 64 || p->s_stride % 4)
+    return (int)hipErrorInvalidValue;
+  int cols = 0;
+  for (int i = 0; i < p->nmod; ++i) {
+    if (p->rpad[i] < 0 || p->rpad[i] % 16) return (int)hipErrorInvalidValue;
+    cols += p->tu_cap * p->rpad[i];
+  }
+  if (cols > p->s_stride || (cols + 127) / 128 > p->csets) return (int)hipErrorInvalidValue;
+  if (!p->counters || !p->flags || !p->gen) return (int)hipErrorInvalidValue;
+  dim3 grid(p->ks, p->csets, p->mtiles);
+  AOS_LAUNCH(ctx, aos_tshrink_kernel, grid, dim3(256), 2 * BM * 128, *p);
   return (int)hipGetLastError();
 }
 
@@ -812,27 +1068,30 @@ extern "C" int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_
  * per SIMD, so that one wave's dequantisation overlaps the other's matrix-core work; SwiGLU with
  * a shallow ring and single staging in 4-wave workgroups (two per CU), the single-matrix kernel
  * with the deep pipeline in 8-wave workgroups. */
-template <bool SW, int MT, int D, bool DBT, bool APF, int WV, int OCC, int LC>
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC>
 static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
-  constexpr int BM = 32 * MT, NTILE = LC > 2 ? LC : 2;
+  constexpr int NTILE = LC > 2 ? LC : 2;
   aos_gemm_params q = *p;
   q.mb = (q.T + BM - 1) / BM;
   q.nb = (q.w0.RB + WV - 1) / WV;
-  const size_t lds = (size_t)NTILE * BM * 128 + gemm_aux(BM) + ((size_t)q.lsteps_max * 2 + 15) / 16 * 16;
+  const size_t lds = (size_t)NTILE * BM * 128 + gemm_aux();
   const dim3 grid(q.mb * q.nb), block(64 * WV);
   const int G = q.w0.G;
   if (G % D == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, D, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, D, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
   else if (G % 2 == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 2, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 2, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
   else
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, MT, 1, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 1, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
 }
 
 extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx) {
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->mtiles != (p->T + BM - 1) / BM || (p->sa_mod_before < 0) ||
+      p->sa_mod_before > 2 || p->rpad0 % 16 || p->rpad1 % 16 || (swiglu && (!p->w1.qt || p->w1.RB != p->w0.RB)))
+    return (int)hipErrorInvalidValue;
   if (swiglu)
-    launch_gemm_cfg<true, 4, 2, false, false, 4, 2, 2>(p, ctx);
+    launch_gemm_cfg<true, 2, false, false, 4, 2, 2>(p, ctx);
   else
-    launch_gemm_cfg<false, 4, 4, true, true, 8, 2, 4>(p, ctx);
+    launch_gemm_cfg<false, 4, true, true, 8, 2, 4>(p, ctx);
   return (int)hipGetLastError();
 }

@@ -78,7 +78,7 @@ __device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_
   e.cf = i < p.T ? load_f(&p.plan->coef[ti][u], coherent) : 0.0f;
   const uint16_t *B = tab.B[a];
   const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
-  e.b = *(const u32x4 *)bp;
+  e.b = aos_gld16(bp);
 }
 
 __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
@@ -113,7 +113,7 @@ __device__ __forceinline__ void h_a_load(const aos_gemv_params &p, int rb, int l
     }
   }
 #pragma unroll
-  for (int k2 = 0; k2 < 2; ++k2) b[k2] = *(const u32x4 *)(arow + step * k2);
+  for (int k2 = 0; k2 < 2; ++k2) b[k2] = aos_gld16(arow + step * k2);
 }
 
 template <int NV>

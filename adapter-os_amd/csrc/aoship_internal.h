@@ -205,88 +205,83 @@ typedef struct {
 } aos_gemv3_params;
 
 /* ---- prefill path (T > 32 tokens) ----
- * The call's adapter union: list[u] = adapter of union slot u (ascending), slot[a] = u or -1.
- * coef[t][u] = sum over token t's active ring slots of adapter list[u] of scale * q / 32767;
- * tile_mask[mt][w] bit b = some token of M tile mt has a nonzero coefficient for slot 32 w + b. */
+ * Tokens are grouped by adapter set before the GEMMs: a stable sort by a hash of each token's
+ * active adapter set (ties by token index) gives perm[p] = the token at sorted position p. The
+ * GEMMs run over 128-token tiles of the sorted order; each tile's LoRA work covers only the
+ * adapters its own tokens use (the tile union, ascending adapter index). */
 #define AOS_PREFILL_MAX_T 4096
-#define AOS_GEMM_BM 128 /* tokens per M tile */
-typedef struct {
-  int U;
-  int pad[3];
-  uint16_t list[AOS_MAX_ADAPTERS];
-  int16_t slot[AOS_MAX_ADAPTERS];
-} aos_pplan;
+#define AOS_GEMM_BM 128 /* tokens per tile */
+#define AOS_TILE_U_MAX 1024 /* a tile's union: at most 128 tokens x 8 ring slots */
 
+/* Group plan: the sort, then for each tile mt its union tu[mt] <= tu_cap, list[mt][u], the
+ * coefficients coef[p][u] = sum over sorted token p's active ring slots naming list[mt][u] of
+ * scale * q / 32767 (ring order), and per module the union's A and B pointers (NULL for an adapter
+ * without the module). */
 typedef struct {
   const aoship_ring_t *rings;
   int T, n;
-  const uint8_t *bound;
-  const float *scale;
-  aos_pplan *plan;
-  float *coef;          /* [T][cstride] */
-  int cstride;          /* >= union size bound */
-  uint32_t *tile_mask;  /* [mtiles][mwords] */
-  int mwords;
-  int nmod;             /* modules whose B tables bp receives */
-  aos_lora_tab tab[3];
-  const uint16_t **bp;  /* [nmod][cstride]: B of union slot u, NULL when absent or u >= U */
-} aos_pplan_params;
-
-/* Shrink over the union for T tokens, finished with the coefficients:
- *   SA[t][s_off[i] + u * rpad_i + j] = bf16(coef[t][u] * sum_i x[t][i] A_{list[u]}[j][i])
- * for module i. K is split over ks workgroups; with ks > 1 their float32 partials go to
- * part[kz][t][...] and a second kernel adds them in split order. */
-typedef struct {
-  const uint16_t *x; /* [T][in] */
-  int T, in;
+  const uint8_t *bound;    /* [n] */
+  const float *scale;      /* [n] */
+  int tu_cap;              /* slots tabulated per tile (>= min(n, AOS_TILE_U_MAX)) */
+  uint16_t *perm;          /* [T] */
+  int *tu;                 /* [mtiles] */
+  uint16_t *list;          /* [mtiles][tu_cap] */
+  float *coef;             /* [T][tu_cap], rows in sorted order */
   int nmod;
   aos_lora_tab tab[3];
-  int s_off[3];
-  const aos_pplan *plan;
-  int umax;             /* union slots covered by the grid */
-  const float *coef;    /* [T][cstride] */
-  int cstride;
-  uint16_t *SA;         /* [T][s_stride] bf16 */
-  float *part;          /* [ks][T][s_stride] float32 (ks > 1) */
-  int s_stride;
-  int ks;               /* K splits */
-  int gpk;              /* groups per K split */
-  int mtiles, cblocks;  /* grid extents (column blocks of 128) */
-  const uint16_t *zero_row;
-} aos_pshrink_params;
+  const uint16_t **ap, **bp; /* [nmod][mtiles][tu_cap] */
+} aos_gplan_params;
 
-/* int4 GEMM with LoRA expand: y[t][o] = sum_i x[t][i] w[o][i] +
- * sum_u SA[t][s_off + u * rpad + j] . B_{list[u]}[o][j] over the union slots u used by the token
- * tile, the expand taken as extra K steps of 64 union columns (those holding a slot the tile
- * uses). SwiGLU mode computes gate (w0) and up (w1) and writes (g * sigmoid(g)) * u. */
+/* Tile shrink: for module i of a tile, S[p][c] = sum_k x[perm[p]][k] A_{list[u]}[j][k] over the
+ * tile's union columns c = u * rpad_i + j, K split into ks slices; once every slice of a (tile,
+ * column set) has stored its partial sums, each slice sums its share of the rows over the slices
+ * in order and stores SA[p][off_i(mt) + c] = bf16(coef[p][u] * S) with off_i(mt) = sum over
+ * modules i' < i of tu[mt] * rpad_i'. One workgroup per (K slice, set of four 32-column blocks,
+ * tile), the K slice fastest: the slices that meet are consecutive workgroups. */
+typedef struct {
+  const uint16_t *x;       /* [T][in] activations in token order, or sorted order when !perm */
+  const uint16_t *perm;    /* [T] or NULL (rows already in sorted order) */
+  int T, in;
+  int nmod;
+  int rpad[3];
+  const int *tu;
+  const float *coef;
+  int tu_cap;
+  const uint16_t *const *ap; /* [nmod][mtiles][tu_cap] */
+  int mtiles, csets, ks;   /* grid: mtiles x csets x ks */
+  float *part;             /* [mtiles][ks][128][s_stride] float32 */
+  uint32_t *counters;      /* [mtiles * csets], zero at rest */
+  uint32_t *flags;         /* [mtiles * csets] lines of 32 words: the slices' meeting point */
+  uint32_t gen;            /* raised to by the last slice of a (tile, column set) */
+  uint32_t *timeout;       /* set when a wait gave up */
+  uint16_t *SA;            /* [T][s_stride] bf16, sorted rows */
+  int s_stride;            /* >= sum over modules of tu_cap * rpad_i, multiple of 64 */
+  const uint16_t *zero_row;
+} aos_tshrink_params;
+
+/* int4 GEMM with the LoRA expand over the tile union: y[p][o] = sum_k x[p][k] w[o][k] +
+ * sum_c SA[p][off + c] B_{list[u]}[o][c - u * rpad] (the expand as extra K steps of 64 union
+ * columns), for the sorted rows p of each tile; SwiGLU mode computes gate (w0) and up (w1) and
+ * writes (g * sigmoid(g)) * u. x rows are read through in_perm (NULL: sorted order) and y rows
+ * written through out_perm (NULL: sorted order). */
 typedef struct {
   aos_q4_dev w0, w1;
   const uint16_t *x;  /* [T][in] */
+  const uint16_t *in_perm, *out_perm;
   int T;
   int mb, nb;         /* token tiles, weight blocks (set by the launcher for its kernel shape) */
-  aos_lora_tab tab0, tab1;
+  int rpad0, rpad1;   /* modules of w0 / w1 (0: no adapter has it) */
+  int mod0;           /* module index of w0 in the plan's tables (w1: mod0 + 1) */
+  const int *tu;
+  const uint16_t *const *bp; /* [nmod][mtiles][tu_cap] */
+  int tu_cap, mtiles;
   const uint16_t *SA; /* [T][sa_stride] bf16 */
-  int sa_stride, s_off0, s_off1;
-  const aos_pplan *plan;
-  const uint32_t *tile_mask;
-  int mwords;
-  const uint16_t *const *bp0, *const *bp1; /* [umax] B per union slot (plan table rows) */
-  int umax;
-  int lsteps_max;     /* bound on the expand K steps of a tile (LDS list length) */
-  const uint16_t *zero; /* 16 zero bytes: source of SA chunks past the union */
+  int sa_stride;
+  int sa_mod_before;  /* modules of the shrink before mod0 (their columns come first) */
+  int rpad_before[2]; /* their padded ranks */
+  const uint16_t *zero; /* 16 zero bytes */
   uint16_t *y;        /* [T][out] */
 } aos_gemm_params;
-
-/* Bound on the expand K steps of one GEMM token tile (at most AOS_GEMM_TILE_MAX tokens) for a
- * module: all the 64-column steps of its union columns, and at most 8 slots per token, each
- * spanning at most rpad / 64 + 2 steps. */
-#define AOS_GEMM_TILE_MAX 256
-static inline int aos_lstep_bound(int umax, int rpad) {
-  if (rpad == 0) return 0;
-  const int all = (umax * rpad + 63) / 64;
-  const int used = AOS_GEMM_TILE_MAX * 8 * (rpad / 64 + 2);
-  return all < used ? all : used;
-}
 
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
  * records at kernel start and end (hipExtLaunchKernelGGL). */
@@ -380,9 +375,8 @@ int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *
 int aos_launch_gemv3(const aos_gemv3_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv_fused(const aos_gemv_fused_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx *ctx);
-int aos_launch_pplan(const aos_pplan_params *p, const aos_launch_ctx *ctx);
-int aos_launch_pshrink(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
-int aos_launch_pfinish(const aos_pshrink_params *p, const aos_launch_ctx *ctx);
+int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
+int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 #ifdef __cplusplus
 }

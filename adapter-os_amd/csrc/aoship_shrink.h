@@ -159,7 +159,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
   for (int d = 0; d < D; ++d) {
     const int jj = d < ng ? d : (ng > 0 ? ng - 1 : 0);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) ring[d][st] = *(const u32x4 *)(ap + (size_t)jj * astep + sstep * st);
+    for (int st = 0; st < 4; ++st) ring[d][st] = aos_gld16(ap + (size_t)jj * astep + sstep * st);
   }
   uint16_t *xl = (uint16_t *)(smem + 128);
   const int xstride = GR * 64;
@@ -197,7 +197,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
       int jn = jg + D;
       jn = jn < ng ? jn : ng - 1;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) ring[d][st] = *(const u32x4 *)(ap + (size_t)jn * astep + sstep * st);
+      for (int st = 0; st < 4; ++st) ring[d][st] = aos_gld16(ap + (size_t)jn * astep + sstep * st);
     }
   }
 

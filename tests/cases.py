@@ -20,6 +20,56 @@ def tol_ratio(y, ref) -> float:
     return float(np.max(np.abs(y - ref) / (np.abs(ref) + rms)))
 
 
+def norm_rel_err(y, ref) -> float:
+    """||y - ref|| / ||ref|| over all elements (float64)."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-300))
+
+
+def report(name: str, y, ref) -> float:
+    """Prints the achieved tolerance ratio (max over elements of |y - ref| / (|ref| + rms(ref)),
+    which must stay <= REL_TOL) and the norm-wise relative error; returns the ratio."""
+    ratio = tol_ratio(y, ref)
+    print(f"[parity] {name}: worst tolerance ratio {ratio:.4g} (limit {REL_TOL}), "
+          f"norm-wise relative error {norm_rel_err(y, ref):.3g}", flush=True)
+    return ratio
+
+
+def tile_sample(perm, T: int, tile: int = 128):
+    """Tokens at the first, middle and last sorted position of every tile of the grouped order."""
+    pos = []
+    for t0 in range(0, T, tile):
+        last = min(t0 + tile, T) - 1
+        pos += [t0, (t0 + last) // 2, last]
+    return np.unique(np.asarray(perm)[np.asarray(pos)])
+
+
+def adapter_sets(rings, n_adapters: int):
+    """Each token's active adapter set (prepare_lora_for_ring's rule: slot < top_k, q > 0, index
+    < n), as a frozenset."""
+    out = []
+    for r in rings:
+        k = int(r["top_k"])
+        out.append(frozenset(int(r["adapter_indices"][s]) for s in range(min(k, 8))
+                             if r["gates_q15"][s] > 0 and r["adapter_indices"][s] < n_adapters))
+    return out
+
+
+def check_grouping(perm, rings, n_adapters: int):
+    """The grouped order is a permutation in which the tokens of each adapter set are contiguous
+    and ascending (the sort's tie-break)."""
+    T = len(rings)
+    assert sorted(int(t) for t in perm) == list(range(T)), "not a permutation"
+    sets = adapter_sets(rings, n_adapters)
+    seq = [sets[int(t)] for t in perm]
+    runs = 1 + sum(1 for a, b in zip(seq, seq[1:]) if a != b)
+    assert runs == len(set(sets)), f"{len(set(sets))} adapter sets in {runs} runs"
+    for a, b in zip(perm, perm[1:]):
+        if sets[int(a)] == sets[int(b)]:
+            assert int(a) < int(b), "tokens of one set out of order"
+
+
 @functools.lru_cache(maxsize=4)
 def base(cid: int):
     cfg = W.CONFIGS[cid]

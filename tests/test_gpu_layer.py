@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import workloads as W
-from cases import REL_TOL, gpu_layer, oracle_mlp, oracle_proj, rings_for, tol_ratio
+from cases import REL_TOL, check_grouping, gpu_layer, oracle_mlp, oracle_proj, report, rings_for, tile_sample, tol_ratio
 
 pytestmark = pytest.mark.gpu
 
@@ -91,19 +91,24 @@ def test_mlp_without_bound_adapters(hip, T):
 
 
 def test_mlp_prefill_shape_parity(hip):
-    """2048-token prefill of the 7B-shaped layer (matrix-core GEMM path), checked on a sample
-    of tokens across tile boundaries, and bit-identical run to run."""
+    """2048-token prefill of the 7B-shaped layer (matrix-core GEMM path): the tokens are grouped by
+    adapter set (each set contiguous, ascending within it); the first, middle and last token of
+    every 128-token tile of the grouped order, and the first and last tokens, are checked against
+    the oracle; bit-identical run to run."""
     cid, T = 3, 2048
     xb, xf = W.activations(W.CONFIGS[cid], T)
     rings, _ = rings_for(cid, T)
     layer, ads = gpu_layer(hip, cid)
     y = _run_mlp(hip, layer, xb, rings)
+    perm = layer.last_perm()
     y2 = _run_mlp(hip, layer, xb, rings)
     assert np.array_equal(y, y2), "run-to-run outputs differ"
-    sample = np.array([0, 1, 2, 31, 32, 33, 127, 128, 511, 1024, 1500, 2046, 2047])
+    check_grouping(perm, rings, W.CONFIGS[cid].n_adapters)
+    sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
+    assert len(np.unique(np.argsort(perm)[sample] // 128)) == T // 128  # a token of every tile
     ref = oracle_mlp(cid, xf[sample], rings[sample])
     got = W.bf16_bits_to_f32(y.reshape(T, -1)[sample])
-    assert tol_ratio(got, ref) <= REL_TOL
+    assert report(f"C3 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref) <= REL_TOL
 
 
 def test_mlp_stress_32b_prefill(hip):
@@ -127,13 +132,15 @@ def test_mlp_stress_32b_prefill(hip):
     y1 = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
     y2 = torch.empty_like(y1)
     layer.mlp_forward(x, rdev, y1)
+    perm = layer.last_perm()
     layer.mlp_forward(x, rdev, y2)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2), "run-to-run outputs differ"
-    sample = np.array([0, 1, 127, 128, 1000, 2047, 2048, 3001, 4094, 4095])
+    check_grouping(perm, rings, cfg.n_adapters)
+    sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
     ref = oracle_mlp(cid, xf[sample], rings[sample])
     got = W.bf16_bits_to_f32(y1.cpu().numpy().view(np.uint16)[sample])
-    ratio = tol_ratio(got, ref)
+    ratio = report(f"C5 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
 
 
