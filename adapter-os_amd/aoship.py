@@ -113,6 +113,8 @@ def lib():
         L.aoship_internal_exp_cr.argtypes = [C.c_double]
         L.aoship_internal_layer_set_separate_shrinks.restype = C.c_int
         L.aoship_internal_layer_set_separate_shrinks.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_set_decode_handoff.restype = C.c_int
+        L.aoship_internal_layer_set_decode_handoff.argtypes = [_P, C.c_int, C.c_int]
         L.aoship_internal_layer_last_perm.restype = C.c_int
         L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
@@ -352,6 +354,12 @@ class Layer:
         launch that reads it)."""
         _check(lib().aoship_internal_layer_set_separate_shrinks(self.h, 1 if on else 0),
                "aoship_internal_layer_set_separate_shrinks")
+
+    def set_decode_handoff(self, one_launch: bool, lines: bool) -> None:
+        """Diagnostic: the 1-2 token MLP as one launch (default two), and per-producer lines in the
+        fused launches (default) instead of an arrival count with one flag per consumer."""
+        _check(lib().aoship_internal_layer_set_decode_handoff(self.h, 1 if one_launch else 0, 1 if lines else 0),
+               "aoship_internal_layer_set_decode_handoff")
 
     def last_perm(self):
         """Token order (sorted position -> token) of the last grouped MLP prefill chunk, or None."""

@@ -608,12 +608,14 @@ enum {
   KS_PSHRINK_H,
   KS_GEMM_DOWN,
   KS_GEMM_PROJ,
+  KS_DECODE_MLP,
   KS_COUNT
 };
 static const char *kStatNames[KS_COUNT] = {
     "route",         "lora_shrink_x",   "q4_gemv_gate_up", "lora_shrink_h",
     "q4_gemv_down",  "q4_gemv_proj",    "prefill_group_plan",
-    "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj"};
+    "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj",
+    "decode_mlp"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -635,6 +637,8 @@ struct aoship_layer {
   const uint16_t *last_perm = nullptr; /* token order of the last grouped prefill chunk (device) */
   int last_perm_T = 0;
   bool separate_shrinks = false; /* each decode shrink in a launch of its own (diagnostic) */
+  bool one_launch_mlp = false;   /* 1-2 token MLP in one launch */
+  bool producer_lines = true;    /* fused launches hand over through per-producer lines */
   hipStream_t stream = nullptr;
   bool profiling = false;
   KStat stats[KS_COUNT];
@@ -925,6 +929,17 @@ extern "C" int aoship_internal_layer_set_separate_shrinks(aoship_layer_t *l, int
   return 0;
 }
 
+/* Diagnostic (no counterpart in the reference): how the decode launches hand over within a
+ * launch. one_launch: the 1-2 token MLP runs as one launch instead of two; lines: the producers of
+ * a fused launch each raise a line of their own, polled by every consumer, instead of counting in
+ * and raising one flag per consumer. Same results either way. */
+extern "C" int aoship_internal_layer_set_decode_handoff(aoship_layer_t *l, int one_launch, int lines) {
+  if (!l) return set_err("aoship_internal_layer_set_decode_handoff: null layer");
+  l->one_launch_mlp = one_launch != 0;
+  l->producer_lines = lines != 0;
+  return 0;
+}
+
 extern "C" int aoship_layer_kernel_stats(aoship_layer_t *l, int idx, const char **name,
                                          double *total_ms, int64_t *launches) {
   if (!l) return set_err("aoship_layer_kernel_stats: null layer");
@@ -1036,8 +1051,8 @@ static int gemv_splits(int RB, int G, int T, int W, int waves_target) {
 /* Every wave of a K split must get at least one group (G / ks >= W): the 8-wave single-matrix
  * kernel falls back to 4 waves when the LDS budget forces more splits (many tokens, long K). */
 static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g,
-                          int waves_target = AOS_GEMV_WAVES) {
-  int W = swiglu ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
+                          int waves_target = AOS_GEMV_WAVES, bool four_waves = false) {
+  int W = (swiglu || four_waves) ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
   int ks = gemv_splits(RB, G, T, W, waves_target);
   if (G / ks < W && W == 8) {
     W = 4;
@@ -1090,7 +1105,7 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
     aos_gemv_params g;
     memset(&g, 0, sizeof(g));
     const int target = kind == 1 ? (T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES) : AOS_GEMV_WAVES;
-    gemv_geometry(RB, G, T, kind == 0, true, g, target);
+    gemv_geometry(RB, G, T, kind == 0, true, g, target, kind == 1 && T <= 2);
     W = g.waves;
     k = g.ks;
   } else if (kind <= 4) {
@@ -1155,6 +1170,38 @@ struct XShrink {
   aos_shrink_params plan_only;
 };
 
+static int shrink_wgs(const aos_shrink_params &sp) {
+  return (sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) + (sp.plan_build.plan ? 1 : 0)) *
+         sp.ks;
+}
+
+/* Producer lines of a shrink: its row blocks and the plan workgroup (counted whether or not the
+ * shrink builds the plan: a sizing pass has no plan pointer). */
+static size_t shrink_lines(const aos_shrink_params &sp) {
+  return (size_t)(sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) + 1);
+}
+
+/* Arrival counter words for a shrink's workgroups, counting the plan workgroup whether or not
+ * the shrink builds the plan (a sizing pass has no plan pointer). */
+static size_t shrink_arrive_words(const aos_shrink_params &sp) {
+  const int rows = sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) + 1;
+  return AOS_ARRIVE_WORDS(rows * sp.ks);
+}
+
+/* The hand-off memory of a fused launch: the arrival counter and the consumers' ready flags
+ * (counted hand-off), and the producers' lines (per-producer hand-off). */
+struct Handoff {
+  uint32_t *sync = nullptr, *flags = nullptr, *lines = nullptr;
+};
+
+static Handoff carve_handoff(Carve &cv, size_t arrive_words, size_t flag_words, size_t n_lines) {
+  Handoff h;
+  h.sync = cv.counter_lines(arrive_words);
+  h.flags = cv.flag_lines(flag_words);
+  h.lines = cv.flag_lines(32 * n_lines);
+  return h;
+}
+
 /* Flag words of a fused launch: one 128-byte line per GEMV workgroup for its ready flag. */
 static size_t fused_flag_words(const aos_gemv_params *gp, int n) {
   size_t c = 0;
@@ -1210,10 +1257,12 @@ struct MlpPlan {
   XShrink sx;
   aos_shrink_params sh;
   aos_gemv_params gv1, gv2;
-  uint32_t *sync1, *sync2;   /* the fused launches' arrival counters */
-  uint32_t *flags1, *flags2; /* ... and their ready flags */
+  Handoff ho1, ho2;          /* the fused launches' hand-off memory */
   float *hpart;            /* [RB of gate/up][T][s_stride of the down shrink]: the h shrink's partials
                               (1-2 tokens only, else NULL) */
+  uint32_t *hdone;         /* one-launch MLP (1-2 tokens): gate/up row blocks done */
+  uint32_t *hflags;        /* ... and the lines raised when h is complete */
+  int hsum_wgs = 0;        /* workgroups summing the h shrink's partials */
   uint32_t *route_done;    /* the combined route + gate/up launch's router arrivals */
   uint32_t *route_flag;    /* ... and its routing flag */
   size_t bytes = 0, ctr = 0, flg = 0;
@@ -1276,9 +1325,9 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.x = h;
   g2.T = T;
   /* the down GEMV streams beside the h shrink of its launch: more K splits (measured: 3 at the
-   * 7B shape) keep its tail short; at 1-2 tokens the launch only sums the shrink's partials, and
-   * 2 splits are faster (measured) */
-  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES);
+   * 7B shape) keep its tail short; at 1-2 tokens it runs in the gate/up launch's grid, in
+   * 4-wave workgroups like the rest of that grid */
+  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES, T <= 2);
   g2.tab0 = td;
   g2.S0 = s2.S[0];
   g2.s_stride0 = s2.s_stride[0];
@@ -1290,12 +1339,18 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.counters = cv.counters((size_t)Wd.RB);
 
   P.hpart = T <= 2 ? cv.b.take<float>((size_t)Wg.RB * T * s2.s_stride[0]) : nullptr;
+  P.hsum_wgs = ceil_div(T * s2.s_stride[0], AOS_HSUM_V);
+  P.hdone = cv.counter_lines(AOS_ARRIVE_WORDS(Wg.RB));
+  P.hflags = cv.flag_lines(((size_t)P.hsum_wgs + (size_t)Wd.RB * g2.ks) * 32);
   P.route_done = cv.counter_lines(32);
   P.route_flag = cv.flag_lines(32);
-  P.sync1 = cv.counter_lines(32);
-  P.flags1 = cv.flag_lines(fused_flag_words(&g1, 1));
-  P.sync2 = cv.counter_lines(32);
-  P.flags2 = cv.flag_lines(fused_flag_words(&g2, 1));
+  P.ho1 = carve_handoff(cv, shrink_arrive_words(P.sx.sp), fused_flag_words(&g1, 1), shrink_lines(P.sx.sp));
+  {
+    /* the h shrink's or the h sum's workgroups */
+    const size_t w_sh = shrink_arrive_words(s2), w_hs = AOS_ARRIVE_WORDS(P.hsum_wgs);
+    const size_t l_sh = shrink_lines(s2), l_hs = (size_t)P.hsum_wgs;
+    P.ho2 = carve_handoff(cv, w_sh > w_hs ? w_sh : w_hs, fused_flag_words(&g2, 1), l_sh > l_hs ? l_sh : l_hs);
+  }
   P.bytes = cv.b.off + 256;
   P.ctr = cv.coff + 64;
   P.flg = cv.foff + 64;
@@ -1443,22 +1498,16 @@ static int launch_err(int e, const char *what);
 
 /* Launch the group plan (nothing without adapters). */
 static int launch_gplan(aoship_layer *l, const PrefillPlan &P) {
+  if (!P.lora) return 0;
   aos_launch_ctx c0 = launch_ctx(l, KS_PPLAN);
-  if (!P.lora) {
-    AOS_SKIP(&c0);
-    return 0;
-  }
   return launch_err(aos_launch_gplan(&P.gp, &c0), "prefill group plan");
 }
 
 /* Launch a tile shrink (nothing when no bound adapter has its modules) with a new generation for
  * its meeting flags. */
 static int launch_tshrink(aoship_layer *l, const aos_tshrink_params &sp, int slot) {
+  if (sp.nmod == 0) return 0;
   aos_launch_ctx c0 = launch_ctx(l, slot);
-  if (sp.nmod == 0) {
-    AOS_SKIP(&c0);
-    return 0;
-  }
   aos_tshrink_params q = sp;
   q.gen = next_gen(&l->gen);
   return launch_err(aos_launch_tshrink(&q, &c0), "lora shrink (prefill)");
@@ -1520,13 +1569,14 @@ static int launch_x_shrink(aoship_layer *l, XShrink &xs, bool events = true) {
  * within tolerance). */
 static bool fuse_shrinks(const aoship_layer *l) { return !l->separate_shrinks; }
 
-static int shrink_wgs(const aos_shrink_params &sp) {
-  return (sp.n_rb[0] + (sp.nmod > 1 ? sp.n_rb[1] : 0) + (sp.nmod > 2 ? sp.n_rb[2] : 0) + (sp.plan_build.plan ? 1 : 0)) *
-         sp.ks;
-}
+
+/* Producers of a fused launch hand over through a line each (polled by every consumer) up to this
+ * many lines, else through an arrival count and one ready flag per consumer. */
+#define AOS_LINES_MAX 512
 
 static void make_fused(aoship_layer *l, uint32_t *genc, const aos_shrink_params &sp, const aos_gemv_params *gp, int n,
-                       uint32_t *sync, uint32_t *flags, const aos_hsum_params *hs, aos_gemv_fused_params &f) {
+                       const Handoff &ho, const aos_hsum_params *hs, aos_gemv_fused_params &f) {
+  uint32_t *sync = ho.sync, *flags = ho.flags;
   memset(&f, 0, sizeof(f));
   if (hs) { /* the first workgroups sum the h shrink's partials instead of running a shrink */
     f.hsum = 1;
@@ -1540,7 +1590,7 @@ static void make_fused(aoship_layer *l, uint32_t *genc, const aos_shrink_params 
     f.n_pre = f.pre_rows * sp.ks;
   }
   f.n = n;
-  f.sync = sync;          /* its own 128-byte line */
+  f.sync = sync;          /* AOS_ARRIVE_WORDS(n_pre) words from a line of their own */
   f.flags = flags;
   f.gen = next_gen(genc);
   int end = 0;
@@ -1557,13 +1607,36 @@ static void make_fused(aoship_layer *l, uint32_t *genc, const aos_shrink_params 
     f.wg_end[i] = end;
   }
   f.n_cons = (uint32_t)end;
+  const int n_lines = hs ? f.n_pre : f.pre_rows;
+  if (ho.lines && l->producer_lines && n_lines <= AOS_LINES_MAX) { /* per-producer lines instead of the count */
+    f.lines = ho.lines;
+    f.n_lines = n_lines;
+    f.sync = nullptr;
+    f.flags = nullptr;
+    if (hs) {
+      f.hs.lines = ho.lines;
+      f.hs.gen = f.gen;
+    } else {
+      f.sp.lines = ho.lines;
+      f.sp.gen = f.gen;
+    }
+    const int plan_line = (!hs && sp.plan_build.plan) ? f.pre_rows - 1 : -1;
+    for (int i = 0; i < n; ++i) {
+      f.gp[i].sync = nullptr;
+      f.gp[i].flags = nullptr;
+      f.gp[i].sync_target = 0;
+      f.gp[i].pre_lines = ho.lines;
+      f.gp[i].n_pre_lines = n_lines;
+      f.gp[i].plan_line = plan_line;
+    }
+  }
 }
 
 static int launch_fused(aoship_layer *l, const Ws &w, const aos_shrink_params &sp, const aos_gemv_params *gp, int n,
-                        uint32_t *sync, uint32_t *flags, int swiglu, int slot, const char *what,
+                        const Handoff &ho, int swiglu, int slot, const char *what,
                         const aos_hsum_params *hs = nullptr) {
   aos_gemv_fused_params f;
-  make_fused(l, w.gen, sp, gp, n, sync, flags, hs, f);
+  make_fused(l, w.gen, sp, gp, n, ho, hs, f);
   aos_launch_ctx c = launch_ctx(l, slot, w.events);
   return launch_err(aos_launch_gemv_fused(&f, swiglu, &c), what);
 }
@@ -1589,6 +1662,39 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
    * row blocks, and the down launch only sums them */
   const bool h_in_gu = fuse && P.gv1.has_expand && fuse_down && P.hpart; /* 1-2 tokens (measured: slower at 8) */
   const bool route_in_gu = rp && fuse && P.gv1.has_expand && !P.sx.separate_plan;
+  if (h_in_gu && !rp && l->one_launch_mlp) { /* 1-2 tokens: the whole MLP in one launch */
+    if (P.sx.separate_plan) {
+      aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, w.events);
+      if (launch_err(aos_launch_shrink(&P.sx.plan_only, &c0), "adapter plan")) return -1;
+    }
+    aos_gemv_params g1 = P.gv1;
+    g1.htab = P.sh.tab[0];
+    g1.hpart = P.hpart;
+    g1.hstride = P.sh.s_stride[0];
+    g1.hdone = P.hdone;
+    g1.hflags = P.hflags;
+    g1.n_hflags = (uint32_t)(P.hsum_wgs + P.gv2.w0.RB * P.gv2.ks);
+    aos_hsum_params hs;
+    memset(&hs, 0, sizeof(hs));
+    hs.hpart = P.hpart;
+    hs.RB = P.gv1.w0.RB;
+    hs.T = Tc;
+    hs.stride = P.sh.s_stride[0];
+    hs.rpad = P.sh.tab[0].rpad;
+    hs.plan = P.sh.plan;
+    hs.S = P.sh.S[0];
+    hs.values_per_wg = AOS_HSUM_V;
+    hs.coherent = 1;
+    aos_decode_mlp_params mp;
+    memset(&mp, 0, sizeof(mp));
+    make_fused(l, w.gen, P.sx.sp, &g1, 1, P.ho1, nullptr, mp.gu);
+    make_fused(l, w.gen, P.sh, &P.gv2, 1, P.ho2, &hs, mp.dn);
+    mp.dn.gen = mp.dn.gp[0].gen = mp.gu.gen; /* one generation for the launch */
+    if (mp.dn.lines) mp.dn.hs.gen = mp.gu.gen;
+    mp.hflags = P.hflags;
+    aos_launch_ctx cm = launch_ctx(l, KS_DECODE_MLP, w.events);
+    return launch_err(aos_launch_decode_mlp(&mp, &cm), "decode mlp (lora shrink + q4 gemv gate/up + down)");
+  }
   if (rp && !route_in_gu) { /* route first, on the layer's stream */
     aos_launch_ctx cr = {l->stream, nullptr, nullptr};
     if (launch_err(aos_launch_route(rp, &cr), "route")) return -1;
@@ -1600,22 +1706,18 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
       g1.hpart = P.hpart;
       g1.hstride = P.sh.s_stride[0];
     }
-    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, w.events);
-    AOS_SKIP(&c0);
     aos_route_gu_params q;
     memset(&q, 0, sizeof(q));
     q.rp = *rp;
-    make_fused(l, w.gen, P.sx.sp, &g1, 1, P.sync1, P.flags1, nullptr, q.fp);
+    make_fused(l, w.gen, P.sx.sp, &g1, 1, P.ho1, nullptr, q.fp);
     q.route_done = P.route_done;
     q.route_flag = P.route_flag;
     aos_launch_ctx cg = launch_ctx(l, KS_GEMV_GU, w.events);
     if (launch_err(aos_launch_route_gate_up(&q, &cg), "route + lora shrink + q4 gemv gate/up")) return -1;
   } else if (fuse && P.gv1.has_expand) {
-    aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, w.events);
     if (P.sx.separate_plan) {
+      aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X, w.events);
       if (launch_err(aos_launch_shrink(&P.sx.plan_only, &c0), "adapter plan")) return -1;
-    } else {
-      AOS_SKIP(&c0);
     }
     aos_gemv_params g1 = P.gv1;
     if (h_in_gu) {
@@ -1623,7 +1725,7 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
       g1.hpart = P.hpart;
       g1.hstride = P.sh.s_stride[0];
     }
-    if (launch_fused(l, w, P.sx.sp, &g1, 1, P.sync1, P.flags1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up"))
+    if (launch_fused(l, w, P.sx.sp, &g1, 1, P.ho1, 1, KS_GEMV_GU, "lora shrink + q4 gemv gate/up"))
       return -1;
   } else {
     if (launch_x_shrink(l, P.sx, w.events)) return -1;
@@ -1631,8 +1733,6 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
     if (launch_err(aos_launch_gemv(&P.gv1, 1, &c2), "q4 gemv gate/up")) return -1;
   }
   if (fuse_down) {
-    aos_launch_ctx c3 = launch_ctx(l, KS_SHRINK_H, w.events);
-    AOS_SKIP(&c3);
     aos_hsum_params hs;
     memset(&hs, 0, sizeof(hs));
     hs.hpart = P.hpart;
@@ -1643,7 +1743,7 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
     hs.plan = P.sh.plan;
     hs.S = P.sh.S[0];
     hs.values_per_wg = AOS_HSUM_V;
-    if (launch_fused(l, w, P.sh, &P.gv2, 1, P.sync2, P.flags2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
+    if (launch_fused(l, w, P.sh, &P.gv2, 1, P.ho2, 0, KS_GEMV_DOWN, "lora shrink + q4 gemv down",
                      h_in_gu ? &hs : nullptr))
       return -1;
   } else {
@@ -1817,8 +1917,7 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
         gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
         gp[i].counters = cv.counters((size_t)W.RB);
       }
-      uint32_t *sync = cv.counter_lines(32);
-      uint32_t *flags = cv.flag_lines(fused_flag_words(gp, nm));
+      const Handoff ho = carve_handoff(cv, shrink_arrive_words(xs.sp), fused_flag_words(gp, nm), shrink_lines(xs.sp));
       if (pass == 0) {
         if (ws_reserve(l, cv.b.off + 256, cv.coff + 64, cv.foff + 64)) return -1;
         continue;
@@ -1826,14 +1925,12 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
       bool expands = false;
       for (int i = 0; i < nm; ++i) expands = expands || gp[i].has_expand;
       if (fuse_shrinks(l) && expands && shrink_wgs(xs.sp) > 0) {
-        aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
         if (xs.separate_plan) {
+          aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
           if (launch_err(aos_launch_shrink(&xs.plan_only, &c0), "adapter plan")) return -1;
-        } else {
-          AOS_SKIP(&c0);
         }
         const Ws lw = {l->ws.p, l->counters.p, l->flags.p, &l->gen, true};
-        if (launch_fused(l, lw, xs.sp, gp, nm, sync, flags, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
+        if (launch_fused(l, lw, xs.sp, gp, nm, ho, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
         continue;
       }
       if (launch_x_shrink(l, xs)) return -1;

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "aoship_internal.h"
+
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -144,6 +146,26 @@ __device__ __forceinline__ void aos_reset(uint32_t *ctr) {
   __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* Arrival idx of n (one lane per workgroup) on the counter lines ctr (AOS_ARRIVE_WORDS(n) words,
+ * zero between launches): true for the last of the n, which has then reset every counter. Each
+ * arrival first waits for its wave's stores, so when the last returns, the payload of all n is
+ * complete. */
+__device__ __forceinline__ bool aos_arrive_tree(uint32_t *ctr, uint32_t idx, uint32_t n) {
+  if (n <= AOS_ARRIVE_GROUP) {
+    if (aos_arrive(ctr) != n - 1u) return false;
+    aos_reset(ctr);
+    return true;
+  }
+  const uint32_t g = idx / AOS_ARRIVE_GROUP, ng = (n + AOS_ARRIVE_GROUP - 1u) / AOS_ARRIVE_GROUP;
+  const uint32_t gsize = n - g * AOS_ARRIVE_GROUP < AOS_ARRIVE_GROUP ? n - g * AOS_ARRIVE_GROUP : AOS_ARRIVE_GROUP;
+  uint32_t *gc = ctr + (size_t)(1u + g) * AOS_ARRIVE_STRIDE;
+  if (aos_arrive(gc) != gsize - 1u) return false;
+  aos_reset(gc);
+  if (aos_arrive(ctr) != ng - 1u) return false;
+  aos_reset(ctr);
+  return true;
+}
+
 /* Raise a generation flag once this wave's payload stores are complete. */
 __device__ __forceinline__ void aos_raise(uint32_t *flag, uint32_t gen) {
   aos_mem_wait();
@@ -165,6 +187,28 @@ __device__ __forceinline__ bool aos_wait_gen(const uint32_t *flag, uint32_t gen)
   }
   aos_compiler_barrier();
   return ok;
+}
+
+/* Bounded wait by one wave until each of the n flag lines (32 words apart) equals gen: lane l
+ * polls lines l, l + 64, ... Returns false (uniformly) when it gave up. The loads that follow
+ * are not moved above the wait. */
+__device__ __forceinline__ bool aos_wait_lines(const uint32_t *lines, int n, uint32_t gen, int lane) {
+  uint32_t spins = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const uint32_t *f = lines + (size_t)(i < n ? i : 0) * 32;
+    while (true) {
+      const uint32_t v = i < n ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : gen;
+      if (__ballot(v != gen) == 0ull) break;
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > AOS_SPIN_LIMIT) {
+        aos_compiler_barrier();
+        return false;
+      }
+    }
+  }
+  aos_compiler_barrier();
+  return true;
 }
 
 #endif

@@ -49,6 +49,7 @@ struct ExpandStep {
   float4 s0, s1;
   float cf;
   u32x4 b;
+  int a; /* the union slot's adapter */
 };
 
 /* coherent: S and the plan were stored by this launch (a fused launch) and are read with
@@ -57,16 +58,31 @@ __device__ __forceinline__ float load_f(const float *a, bool coherent) {
   return coherent ? __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *a;
 }
 
-__device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
-                                            int stride, int q, int row, int lane, ExpandStep &e,
-                                            bool coherent = false) {
+/* The plan's part of step q: the adapter of union slot u, the token's coefficient and the B
+ * fragment (needs the plan only). */
+__device__ __forceinline__ void expand_load_b(const aos_gemv_params &p, const aos_lora_tab &tab, int q, int row,
+                                              int lane, ExpandStep &e, bool coherent) {
   const int i = lane & 31, c = lane >> 5;
   const int ti = i < p.T ? i : 0;
   const int rpad = tab.rpad;
   const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
   const int a = coherent ? (int)__hip_atomic_load(&p.plan->list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                          : (int)p.plan->list[u];
-  const int scol = (p.s_all ? a : u) * rpad + j0 + 8 * c;
+  e.a = a;
+  e.cf = i < p.T ? load_f(&p.plan->coef[ti][u], coherent) : 0.0f;
+  const uint16_t *B = aos_gld_ptr(&tab.B[a]);
+  const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
+  e.b = aos_gld16(bp);
+}
+
+/* The shrink's part of step q: the 8 values of S the lane's half of the A operand scales. */
+__device__ __forceinline__ void expand_load_s(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
+                                              int stride, int q, int lane, ExpandStep &e, bool coherent) {
+  const int i = lane & 31, c = lane >> 5;
+  const int ti = i < p.T ? i : 0;
+  const int rpad = tab.rpad;
+  const int colq = 16 * q, u = colq / rpad, j0 = colq - u * rpad;
+  const int scol = (p.s_all ? e.a : u) * rpad + j0 + 8 * c;
   const float *sp = S + (size_t)ti * stride + scol;
   if (coherent) {
     e.s0 = make_float4(load_f(sp, true), load_f(sp + 1, true), load_f(sp + 2, true), load_f(sp + 3, true));
@@ -75,10 +91,13 @@ __device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_
     e.s0 = *(const float4 *)sp;
     e.s1 = *(const float4 *)(sp + 4);
   }
-  e.cf = i < p.T ? load_f(&p.plan->coef[ti][u], coherent) : 0.0f;
-  const uint16_t *B = tab.B[a];
-  const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
-  e.b = aos_gld16(bp);
+}
+
+__device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
+                                            int stride, int q, int row, int lane, ExpandStep &e,
+                                            bool coherent = false) {
+  expand_load_b(p, tab, q, row, lane, e, coherent);
+  expand_load_s(p, tab, S, stride, q, lane, e, coherent);
 }
 
 __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
@@ -154,7 +173,11 @@ __device__ __forceinline__ void h_shrink_partial(const aos_gemv_params &p, int r
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int m = aos_acc_m(v, lane);
-      if (m < T && col < cols) p.hpart[((size_t)rb * T + m) * p.hstride + col] = acc[v];
+      if (m < T && col < cols) {
+        float *dst = p.hpart + ((size_t)rb * T + m) * p.hstride + col;
+        if (p.hdone) aos_publish(dst, acc[v]); /* read by this launch's sum workgroups */
+        else *dst = acc[v];
+      }
     }
   }
 }
@@ -187,7 +210,8 @@ __device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, uns
 #pragma unroll
       for (int k = 0; k < HSUM_V; ++k) {
         const bool ok = r < hs.RB && t[k] < hs.T && col[k] < cols;
-        v[q][k] = ok ? hs.hpart[((size_t)r * hs.T + t[k]) * hs.stride + col[k]] : 0.0f;
+        const float *src = hs.hpart + ((size_t)(ok ? r : 0) * hs.T + (ok ? t[k] : 0)) * hs.stride + (ok ? col[k] : 0);
+        v[q][k] = ok ? (hs.coherent ? aos_collect(src) : *src) : 0.0f;
       }
     }
 #pragma unroll
@@ -214,8 +238,18 @@ __device__ __forceinline__ void hsum_block(const aos_hsum_params &hs, int b, uns
     aos_publish(&hs.S[(size_t)t[tid] * hs.stride + col[tid]], red[tid * (NT / 64)]);
 }
 
-template <int NV, bool SW, int W, int D>
-__device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int ksi) {
+/* x staging loads: plain, or device-coherent (sc1) when x was written by this launch. */
+template <bool XL>
+__device__ __forceinline__ u32x4 x_load(const uint16_t *x, size_t elem, __amdgpu_buffer_rsrc_t rs) {
+  if (XL) return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(elem * 2), 0, 16));
+  return *(const u32x4 *)(x + elem);
+}
+
+/* Row block rb, K split ksi of one matrix (or of the gate/up pair). XL: x is written by earlier
+ * workgroups of this launch; the weight ring is primed first, then the workgroup waits (bounded)
+ * for its line of xflag to reach p.gen and stages x with device-coherent loads. */
+template <int NV, bool SW, int W, int D, bool XL = false>
+__device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int ksi, const uint32_t *xflag = nullptr) {
   constexpr int NA = SW ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -237,7 +271,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
    * step's operands ahead of the K loop, the single-matrix kernel keeps its registers (and its
    * occupancy) and loads them after the K loop */
   const bool expands = p.has_expand != 0;
-  const bool fused = p.sync != nullptr; /* S and the plan are produced by this launch */
+  const bool fused = p.sync != nullptr || p.pre_lines != nullptr; /* S (and the plan) are produced by this launch */
   int hU = 0;
   u32x4 hpre[2][2];
   const int q_first = ksi + p.ks * wave, q_step = p.ks * W;
@@ -260,14 +294,20 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
      * can wait for exactly the load it needs. */
     const int xchunks = GR * 8; /* 16-byte chunks per token row */
     const int nx = T * xchunks;
+    const __amdgpu_buffer_rsrc_t xrs = /* unused (and removed) unless XL */
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.x, (short)0, T * in * 2, 0x00020000);
     u32x4 xv[XE];
+    auto x_first = [&]() {
 #pragma unroll
-    for (int j = 0; j < XE; ++j) {
-      int idx = tid + j * 64 * W;
-      idx = idx < nx ? idx : nx - 1;
-      const int t = idx / xchunks, r = idx - t * xchunks;
-      xv[j] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
-    }
+      for (int j = 0; j < XE; ++j) {
+        int idx = tid + j * 64 * W;
+        idx = idx < nx ? idx : idx % nx; /* surplus lanes re-read chunks spread over x (a single
+                                        * clamped chunk would be one cache line hit by every lane) */
+        const int t = idx / xchunks, r = idx - t * xchunks;
+        xv[j] = x_load<XL>(p.x, (size_t)t * in + (size_t)gw0 * 64 + r * 8, xrs);
+      }
+    };
+    if (!XL) x_first();
 
     /* (2) the ring: groups ga .. ga+D-1. The host sizes the splits so that every wave has at
      * least one group; a wave without one still loads group ga (in range: ga < gw1 <= G) and
@@ -289,6 +329,14 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
       }
     }
 
+    if (XL) { /* x is being produced by this launch: wait for it with the weights in flight (if
+               * the wait gives up, the call is reported as timed out and its output is invalid) */
+      if (tid == 0 && !aos_wait_gen(xflag, p.gen) && p.timeout)
+        __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      lds_barrier();
+      x_first();
+    }
+
     /* (3) x -> LDS (rest of the staging after the ring is in flight), group sums. LDS holds
      * 128 zero bytes (read by lanes without a token), the T x rows, then the group sums. */
     uint16_t *xl = (uint16_t *)(smem + 128);
@@ -305,8 +353,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     }
     for (int idx = tid + XE * 64 * W; idx < nx; idx += 64 * W) {
       const int t = idx / xchunks, r = idx - t * xchunks;
-      *(u32x4 *)(xl + (size_t)t * xstride + r * 8) =
-          *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
+      *(u32x4 *)(xl + (size_t)t * xstride + r * 8) = x_load<XL>(p.x, (size_t)t * in + (size_t)gw0 * 64 + r * 8, xrs);
     }
     lds_barrier();
     for (int idx = tid; idx < T * GR * 2; idx += 64 * W) {
@@ -361,19 +408,28 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     }
   }
 
-  /* (4a) fused launch: wait for this workgroup's ready flag, raised to this launch's generation
-   * once every producer workgroup of the grid is done (they have the lowest workgroup ids, so
-   * they are dispatched before any GEMV workgroup, and none of them waits on a GEMV workgroup).
-   * Each workgroup polls a line of its own. The wait is bounded: past about a second it gives up,
-   * sets p.timeout and finishes without the expand or the h shrink (reading neither S nor the
-   * plan); the call's output is then invalid and the layer reports the timeout. */
+  /* (4a) fused launch. The producers have the lowest workgroup ids, so they are dispatched before
+   * any GEMV workgroup, and none of them waits on a GEMV workgroup. With per-producer lines, wave 0
+   * first waits for the plan's line (when the plan is built in this launch), the first expand
+   * step's B fragments are loaded, then wave 0 waits for every producer's line before S is read;
+   * otherwise it waits for this workgroup's own ready flag, raised once every producer is done.
+   * The waits are bounded: past about a second they give up, set p.timeout and the workgroup
+   * finishes without the expand or the h shrink; the call's output is then invalid and the layer
+   * reports the timeout. */
   if (fused) {
-    __shared__ uint32_t ok;
-    if (tid == 0) {
-      const uint32_t *flag = p.flags + ((size_t)ksi * p.w0.RB + rb) * 32;
-      const bool done = aos_wait_gen(flag, p.gen);
-      ok = done ? 1u : 0u;
-      if (!done && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __shared__ uint32_t ok, ok2;
+    const bool lines = p.pre_lines != nullptr;
+    if (wave == 0) {
+      bool done = true;
+      if (lines) {
+        if (p.plan_line >= 0) done = aos_wait_lines(p.pre_lines + (size_t)p.plan_line * 32, 1, p.gen, lane);
+      } else if (lane == 0) {
+        done = aos_wait_gen(p.flags + ((size_t)ksi * p.w0.RB + rb) * 32, p.gen);
+      }
+      if (lane == 0) {
+        ok = done ? 1u : 0u;
+        if (!done && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
     }
     lds_barrier();
     if (ok && expands) {
@@ -384,18 +440,40 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
       nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
       hU = U;
     }
-    /* the h shrink's first A_down fragments (wave 0 forms the partials at the end) */
+    /* the h shrink's first A_down fragments (wave 0 forms the partials at the end), and the first
+     * expand step's plan part */
     if (SW && p.hpart && wave == 0 && ok) {
       h_a_load(p, rb, lane, hU, 0, hpre[0]);
       h_a_load(p, rb, lane, hU, 1, hpre[1]);
+    }
+    if (q_first < nq0) expand_load_b(p, p.tab0, q_first, row, lane, e0, true);
+    if (SW && q_first < nq1) expand_load_b(p, p.tab1, q_first, row, lane, e1, true);
+    if (lines) {
+      if (wave == 0) {
+        const bool done = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
+        if (lane == 0) {
+          ok2 = done ? 1u : 0u;
+          if (!done && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+      }
+      lds_barrier();
+      if (!ok2) {
+        nq0 = 0;
+        nq1 = 0;
+        hU = 0;
+      }
     }
   }
 
   /* (4b) the expand, added to the waves' accumulators */
   if (expands) {
     f32x16 f0 = {}, f1 = {};
-    if ((!SW || fused) && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0, fused);
-    if (SW && fused && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1, fused);
+    if (fused) {
+      if (q_first < nq0) expand_load_s(p, p.tab0, p.S0, p.s_stride0, q_first, lane, e0, true);
+      if (SW && q_first < nq1) expand_load_s(p, p.tab1, p.S1, p.s_stride1, q_first, lane, e1, true);
+    } else if (!SW && q_first < nq0) {
+      expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
+    }
     if (q_first < nq0) expand_apply(e0, f0);
     if (SW && q_first < nq1) expand_apply(e1, f1);
     for (int q = q_first + q_step; q < nq0; q += q_step) {
@@ -494,24 +572,51 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
       const float gt = acc0[v], up = acc1[v];
       const float sg = 1.0f / (1.0f + expf(-gt));
       hb[v] = aos_f32_to_bf16((gt * sg) * up);
-      p.y[(size_t)m * out + row] = hb[v];
+      if (p.hdone) /* read by this launch's down workgroups */
+        __hip_atomic_store(p.y + (size_t)m * out + row, hb[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        p.y[(size_t)m * out + row] = hb[v];
     }
   }
   if (SW && p.hpart && hU > 0) h_shrink_partial<NV>(p, rb, lane, hb, smem, hU, hpre);
+  /* one-launch decode: this row block of h (and its partials) is out; the last row block raises
+   * the lines of every workgroup that reads h */
+  if (SW && p.hdone) {
+    uint32_t last = 0;
+    if (lane == 0) last = aos_arrive_tree(p.hdone, (uint32_t)rb, (uint32_t)p.w0.RB) ? 1u : 0u;
+    last = aos_shfl(last, 0);
+    if (last) {
+      for (uint32_t c2 = lane; c2 < p.n_hflags; c2 += 64)
+        __hip_atomic_store(p.hflags + (size_t)c2 * 32, p.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 
 /* Producer workgroup b of a fused launch: a shrink workgroup (or, with fp.hsum, a sum of the h
- * shrink's partials), then the arrival count; the last producer raises every GEMV workgroup's
- * ready flag to fp.gen. route_flag (may be NULL): the plan workgroup first waits, bounded, until
- * the launch's routers have raised route_flag to fp.gen and only then reads the rings (with
- * device-scope loads); if that wait gives up it publishes an empty plan instead. */
+ * shrink's partials). Then, with per-producer lines, the workgroup that completed a row block of
+ * the shrink (or the plan, or a sum) raises that producer's line to fp.gen; otherwise every
+ * producer counts itself in and the last one raises every GEMV workgroup's ready flag to fp.gen.
+ * route_flag (may be NULL): the plan workgroup first waits, bounded, until the launch's routers
+ * have raised route_flag to fp.gen and only then reads the rings (with device-scope loads); if
+ * that wait gives up it publishes an empty plan instead. start_flag (may be NULL): the producer's
+ * inputs are written by earlier workgroups of this launch, which raise start_flag to fp.gen. */
 template <int NV, int W>
 __device__ __forceinline__ void fused_producer(const aos_gemv_fused_params &fp, int b, unsigned char *smem,
-                                               const uint32_t *route_flag) {
-  __shared__ uint32_t last, routed;
+                                               const uint32_t *route_flag, const uint32_t *start_flag = nullptr) {
+  __shared__ uint32_t last, routed, started;
+  if (start_flag) { /* the inputs come from earlier workgroups of this launch */
+    if (threadIdx.x == 0) {
+      const bool done = aos_wait_gen(start_flag, fp.gen);
+      started = done ? 1u : 0u;
+      if (!done && fp.gp[0].timeout)
+        __hip_atomic_store(fp.gp[0].timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __syncthreads();
+  }
+  bool done_here = true; /* this workgroup completes its producer (shrink: see shrink_block) */
   if (fp.hsum) {
-    hsum_block<64 * W>(fp.hs, b, smem);
+    if (!start_flag || started) hsum_block<64 * W>(fp.hs, b, smem);
   } else {
     const int lrb = b % fp.pre_rows, ksi = b / fp.pre_rows;
     bool run = true;
@@ -527,17 +632,17 @@ __device__ __forceinline__ void fused_producer(const aos_gemv_fused_params &fp, 
       __syncthreads();
       run = routed != 0u;
     }
-    if (run) aos_shrink::shrink_block<NV, W, 4>(fp.sp, lrb, ksi, smem);
+    done_here = run ? aos_shrink::shrink_block<NV, W, 4>(fp.sp, lrb, ksi, smem) : true;
   }
   /* the partials, S and the plan went out as device-scope stores: wait for them, then count
    * this workgroup in (no cache write-back is needed) */
   aos_mem_wait();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = aos_arrive(fp.sync);
-    last = old == (uint32_t)fp.n_pre - 1u;
-    if (last) aos_reset(fp.sync);
+  if (fp.lines) { /* per-producer lines: thread 0 (in wave 0, which decided) raises this one's */
+    if (threadIdx.x == 0 && done_here) aos_raise(fp.lines + (size_t)(fp.hsum ? b : b % fp.pre_rows) * 32, fp.gen);
+    return;
   }
+  if (threadIdx.x == 0) last = aos_arrive_tree(fp.sync, (uint32_t)b, (uint32_t)fp.n_pre) ? 1u : 0u;
   __syncthreads();
   if (last) /* every producer is done: raise the GEMV workgroups' flags */
     for (uint32_t c = threadIdx.x; c < fp.n_cons; c += blockDim.x)

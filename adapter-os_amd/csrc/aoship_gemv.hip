@@ -75,6 +75,56 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
   }
 }
 
+/* The decode MLP of 1-2 tokens in one launch (4-wave workgroups throughout):
+ *   [0, gu.n_pre)             the x shrink and the plan (gate/up's producers);
+ *   next gu.n_cons            the gate/up GEMV with its expand; h and the h shrink's partials go
+ *                             out device-coherent, and the last row block raises hflags;
+ *   next dn.n_pre             the sum of those partials (each waits for its line of hflags);
+ *   last dn.n_cons            the down GEMV: weights first, then h once its line of hflags is
+ *                             raised, then the expand once the sums are out (dn's flags).
+ * Every wait is for workgroups with lower ids: those are dispatched first and wait on none of
+ * the later ones, so the grid drains whatever the residency. */
+#ifndef AOS_MLP_GU_RING
+#define AOS_MLP_GU_RING 4 /* groups in flight per wave: gate/up GEMV of the one-launch MLP */
+#endif
+#ifndef AOS_MLP_DN_RING
+#define AOS_MLP_DN_RING 12 /* ... and its down GEMV */
+#endif
+template <int NV>
+__global__ void __launch_bounds__(256) aos_decode_mlp_kernel(aos_decode_mlp_params mp) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const aos_gemv_fused_params &gu = mp.gu, &dn = mp.dn;
+  int b = blockIdx.x;
+  if (b < gu.n_pre) {
+    fused_producer<NV, 4>(gu, b, smem, nullptr);
+    return;
+  }
+  b -= gu.n_pre;
+  if (b < (int)gu.n_cons) {
+    gemv_body<NV, true, 4, AOS_MLP_GU_RING>(gu.gp[0], b % gu.gp[0].w0.RB, b / gu.gp[0].w0.RB);
+    return;
+  }
+  b -= (int)gu.n_cons;
+  if (b < dn.n_pre) {
+    fused_producer<NV, 4>(dn, b, smem, nullptr, mp.hflags + (size_t)b * 32);
+    return;
+  }
+  b -= dn.n_pre;
+  gemv_body<NV, false, 4, AOS_MLP_DN_RING, true>(dn.gp[0], b % dn.gp[0].w0.RB, b / dn.gp[0].w0.RB,
+                                    mp.hflags + (size_t)(dn.n_pre + b) * 32);
+}
+
+template <int NV>
+int launch_mlp_nv(const aos_decode_mlp_params *mp, const aos_launch_ctx *ctx) {
+  const int nwg = mp->gu.n_pre + (int)mp->gu.n_cons + mp->dn.n_pre + (int)mp->dn.n_cons;
+  size_t lds = (size_t)mp->gu.sp.lds_bytes;
+  const size_t l_hs = (size_t)HSUM_V * 64 * 4 * 4;
+  const size_t roles[3] = {(size_t)mp->gu.gp[0].lds_bytes, l_hs, (size_t)mp->dn.gp[0].lds_bytes};
+  for (size_t r : roles) lds = lds > r ? lds : r;
+  AOS_LAUNCH(ctx, aos_decode_mlp_kernel<NV>, dim3(nwg), dim3(256), lds, *mp);
+  return (int)hipGetLastError();
+}
+
 template <int NV>
 int launchf_nv(const aos_gemv_fused_params *fp, int swiglu, const aos_launch_ctx *ctx) {
   const int nwg = fp->n_pre + (int)fp->n_cons;
@@ -155,33 +205,70 @@ extern "C" int aos_launch_gemv3(const aos_gemv3_params *mp, const aos_launch_ctx
 }
 
 extern "C" int aos_launch_gemv_fused(const aos_gemv_fused_params *fp, int swiglu, const aos_launch_ctx *st) {
-  const int n = fp->n;
-  if (n < 1 || n > 3 || (swiglu && n != 1)) return (int)hipErrorInvalidValue;
-  const int waves = fp->gp[0].waves, T = fp->gp[0].T;
-  if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
-  if (swiglu && waves != 4) return (int)hipErrorInvalidValue;
-  if (T < 1 || T > AOS_DECODE_MAX_T || (fp->hsum ? fp->hs.T : fp->sp.T) != T) return (int)hipErrorInvalidValue;
-  if (!fp->sync || !fp->flags || !fp->gen || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows)
-    return (int)hipErrorInvalidValue;
-  if (fp->hsum ? (fp->pre_rows != fp->n_pre || !fp->hs.hpart || !fp->hs.S || fp->hs.values_per_wg != HSUM_V ||
-                  (size_t)fp->n_pre * HSUM_V < (size_t)fp->hs.T * fp->hs.stride)
-               : fp->n_pre / fp->pre_rows != fp->sp.ks)
-    return (int)hipErrorInvalidValue;
-  int end = 0;
-  for (int i = 0; i < 3; ++i) {
-    if (i < n) {
-      const aos_gemv_params &p = fp->gp[i];
-      if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1 || p.sync != fp->sync ||
-          p.flags != fp->flags + (size_t)end * 32 || p.sync_target != (uint32_t)fp->n_pre || p.gen != fp->gen)
-        return (int)hipErrorInvalidValue;
-      end += p.w0.RB * p.ks;
-    }
-    if (fp->wg_end[i] != end) return (int)hipErrorInvalidValue;
-  }
-  if (fp->n_cons != (uint32_t)end) return (int)hipErrorInvalidValue;
+  if (!aos_fused_params_ok(fp, swiglu)) return (int)hipErrorInvalidValue;
+  const int T = fp->gp[0].T;
   if (T <= 1) return launchf_nv<1>(fp, swiglu, st);
   if (T <= 2) return launchf_nv<2>(fp, swiglu, st);
   if (T <= 8) return launchf_nv<4>(fp, swiglu, st);
   if (T <= 16) return launchf_nv<8>(fp, swiglu, st);
   return launchf_nv<16>(fp, swiglu, st);
+}
+
+/* Checks of one fused parameter block's own consistency (shared by the fused, the route + gate/up
+ * and the one-launch MLP launchers). */
+extern "C" int aos_fused_params_ok(const aos_gemv_fused_params *fp, int swiglu) {
+  const int n = fp->n;
+  if (n < 1 || n > 3 || (swiglu && n != 1)) return false;
+  const int waves = fp->gp[0].waves, T = fp->gp[0].T;
+  if (waves != 4 && waves != 8) return false;
+  if (swiglu && waves != 4) return false;
+  if (T < 1 || T > AOS_DECODE_MAX_T || (fp->hsum ? fp->hs.T : fp->sp.T) != T) return false;
+  if (!fp->gen || fp->n_pre < 1 || fp->pre_rows < 1 || fp->n_pre % fp->pre_rows) return false;
+  const bool lines = fp->lines != nullptr;
+  /* per-producer lines: one per row block of the shrink (and the plan) or per sum workgroup;
+   * the plan's line is the last when the shrink builds the plan */
+  const int plan_line = (!fp->hsum && fp->sp.plan_build.plan) ? fp->pre_rows - 1 : -1;
+  if (lines) {
+    if (fp->n_lines != (fp->hsum ? fp->n_pre : fp->pre_rows)) return false;
+    if (fp->hsum ? (fp->hs.lines != fp->lines || fp->hs.gen != fp->gen)
+                 : (fp->sp.lines != fp->lines || fp->sp.gen != fp->gen))
+      return false;
+  } else if (!fp->sync || !fp->flags || (fp->hsum ? fp->hs.lines != nullptr : fp->sp.lines != nullptr)) {
+    return false;
+  }
+  if (fp->hsum ? (fp->pre_rows != fp->n_pre || !fp->hs.hpart || !fp->hs.S || fp->hs.values_per_wg != HSUM_V ||
+                  (size_t)fp->n_pre * HSUM_V < (size_t)fp->hs.T * fp->hs.stride)
+               : fp->n_pre / fp->pre_rows != fp->sp.ks)
+    return false;
+  int end = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (i < n) {
+      const aos_gemv_params &p = fp->gp[i];
+      if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1 || p.gen != fp->gen) return false;
+      if (lines ? (p.pre_lines != fp->lines || p.n_pre_lines != fp->n_lines || p.plan_line != plan_line ||
+                   p.sync != nullptr)
+                : (p.sync != fp->sync || p.flags != fp->flags + (size_t)end * 32 ||
+                   p.sync_target != (uint32_t)fp->n_pre || p.pre_lines != nullptr))
+        return false;
+      end += p.w0.RB * p.ks;
+    }
+    if (fp->wg_end[i] != end) return false;
+  }
+  return fp->n_cons == (uint32_t)end;
+}
+
+extern "C" int aos_launch_decode_mlp(const aos_decode_mlp_params *mp, const aos_launch_ctx *st) {
+  const aos_gemv_fused_params &gu = mp->gu, &dn = mp->dn;
+  if (!aos_fused_params_ok(&gu, 1) || !aos_fused_params_ok(&dn, 0)) return (int)hipErrorInvalidValue;
+  const aos_gemv_params &g1 = gu.gp[0], &g2 = dn.gp[0];
+  const int T = g1.T;
+  /* 1-2 tokens, 4-wave workgroups in every role, one generation, the h shrink formed by gate/up
+   * and summed by dn's producers, h handed over through hdone and hflags */
+  if (T > 2 || g2.T != T || g2.waves != 4 || dn.n != 1 || gu.hsum || !dn.hsum || !dn.hs.coherent) return (int)hipErrorInvalidValue;
+  if (dn.gen != gu.gen || g1.x == nullptr || g2.x != g1.y || !g1.hpart || g1.hpart != dn.hs.hpart ||
+      dn.hs.RB != g1.w0.RB || g1.hstride != dn.hs.stride || !g1.hdone || !mp->hflags || g1.hflags != mp->hflags ||
+      g1.n_hflags != (uint32_t)dn.n_pre + dn.n_cons || g2.w0.in != g1.w0.out)
+    return (int)hipErrorInvalidValue;
+  if (T <= 1) return launch_mlp_nv<1>(mp, st);
+  return launch_mlp_nv<2>(mp, st);
 }

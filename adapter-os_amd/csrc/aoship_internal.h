@@ -35,6 +35,18 @@ enum { MOD_Q = 0, MOD_K, MOD_V, MOD_O, MOD_GATE, MOD_UP, MOD_DOWN };
 #endif
 #define AOS_SHRINK_GROUPS_PER_WAVE 2
 
+/* Arrival counting over n workgroups in two levels: groups of AOS_ARRIVE_GROUP arrivals count
+ * into a counter of their own, and the last of each group into the top counter (same-address
+ * device-scope atomics are performed one after another). Counter words for n arrivals: the top
+ * line and one line per group, 32 words (128 bytes) a line. */
+#define AOS_ARRIVE_GROUP 32u
+#ifndef AOS_ARRIVE_STRIDE
+#define AOS_ARRIVE_STRIDE 32u /* words between counters */
+#endif
+#define AOS_ARRIVE_WORDS(n)                                                                             \
+  (AOS_ARRIVE_STRIDE *                                                                                    \
+   ((uint32_t)(n) <= AOS_ARRIVE_GROUP ? 1u : 1u + ((uint32_t)(n) + AOS_ARRIVE_GROUP - 1u) / AOS_ARRIVE_GROUP))
+
 typedef struct {
   int out, in, G, RB;
   const uint32_t *qt;
@@ -115,6 +127,11 @@ typedef struct {
   uint32_t *counters;/* [rb_total] zero between launches */
   aos_plan_params plan_build; /* used when plan_build.plan != NULL */
   const uint16_t *zero_row;   /* device zeros, read by lanes without an adapter row */
+  /* fused launch, per-producer lines: once row block r's S is stored, its finishing workgroup
+   * raises lines[32 r] to gen; the plan workgroup raises lines[32 rb_total] once the plan is
+   * stored (NULL: no lines) */
+  uint32_t *lines;
+  uint32_t gen;
 } aos_shrink_params;
 
 /* ---- decode GEMV ---- */
@@ -139,10 +156,16 @@ typedef struct {
   float *part;        /* [RB][ks][NA * NV * 64] */
   uint32_t *counters; /* [RB] zero between launches */
   /* fused launch (aos_launch_gemv_fused): the shrink that produces S0 / S1 (and the plan) runs
-   * in the first workgroups of the same grid. The last of its sync_target workgroups to finish
-   * raises one ready flag per GEMV workgroup; each GEMV workgroup waits for its own flag (and
-   * clears it) before its expand. NULL sync: S and the plan come from earlier launches. */
-  uint32_t *sync;     /* [1] producer arrivals; zero between launches */
+   * in the first workgroups of the same grid. Either every producer raises a line of its own
+   * (pre_lines: n_pre_lines lines; the plan's is line plan_line, -1 when the plan comes from an
+   * earlier launch) and each GEMV workgroup waits for the plan's line before loading its expand's
+   * B rows and for every line before loading S; or (sync) the last of the sync_target producers
+   * to finish raises one ready flag per GEMV workgroup, which waits for its own flag before its
+   * expand. NULL sync and pre_lines: S and the plan come from earlier launches. */
+  const uint32_t *pre_lines;
+  int n_pre_lines;
+  int plan_line;
+  uint32_t *sync;     /* producer arrivals, AOS_ARRIVE_WORDS(sync_target) words; zero between launches */
   uint32_t *flags;    /* this matrix's ready flags [RB * ks * 32], one per 128-byte line */
   uint32_t sync_target;
   uint32_t gen;       /* this launch's generation: a ready flag equal to it is raised */
@@ -153,6 +176,13 @@ typedef struct {
   aos_lora_tab htab;
   float *hpart;
   int hstride;
+  /* one-launch decode, gate/up: h and its shrink partials go out device-coherent, and each row
+   * block's finisher counts itself into hdone (AOS_ARRIVE_WORDS(RB) words); the last of the RB
+   * raises n_hflags flag lines
+   * (hflags, one per later workgroup that reads h) to gen */
+  uint32_t *hdone;
+  uint32_t *hflags;
+  uint32_t n_hflags;
 } aos_gemv_params;
 
 /* The sum of those partials over the row blocks, in row-block order: S[t][col] for col <
@@ -164,6 +194,10 @@ typedef struct {
   const aos_plan *plan;
   float *S;           /* [T][stride] */
   int values_per_wg;
+  int coherent;       /* 1: hpart was written by this launch (device-scope loads) */
+  uint32_t *lines;    /* fused launch, per-producer lines: workgroup b raises lines[32 b] to gen once
+                         its sums are stored (NULL: no lines) */
+  uint32_t gen;
 } aos_hsum_params;
 
 /* A shrink and the GEMVs that consume its S in one launch: workgroups [0, n_pre) run the shrink
@@ -178,11 +212,26 @@ typedef struct {
   int n_pre, pre_rows;
   int hsum;           /* 1: the first workgroups run hs (pre_rows = n_pre) instead of the shrink sp */
   aos_hsum_params hs;
-  uint32_t *sync;     /* [1] producer arrivals */
-  uint32_t *flags;    /* [n_cons * 32] */
+  uint32_t *sync;     /* producer arrivals, AOS_ARRIVE_WORDS(n_pre) words (counted hand-off) */
+  uint32_t *flags;    /* [n_cons * 32] (counted hand-off) */
   uint32_t n_cons;    /* wg_end[n - 1] */
-  uint32_t gen;       /* generation the last producer raises the flags to (nonzero) */
+  uint32_t gen;       /* generation the producers raise their lines / the flags to (nonzero) */
+  uint32_t *lines;    /* per-producer hand-off: n_lines lines (pre_rows for a shrink, n_pre for the
+                         sums), the same as sp.lines / hs.lines and every gp[i].pre_lines; NULL:
+                         counted hand-off through sync and flags */
+  int n_lines;
 } aos_gemv_fused_params;
+
+/* The decode MLP (1-2 tokens) in one launch: workgroups [0, gu.n_pre) run the x shrink and the
+ * plan, the next gu.n_cons the gate/up GEMV (h and the h shrink's partials, device-coherent), the
+ * next dn.n_pre sum those partials once every row block of h is done (their line of hflags), and
+ * the last dn.n_cons run the down GEMV, which stream their weights first and stage h once it is
+ * complete (their line of hflags), then wait for the h shrink's S as any fused consumer does.
+ * gu.gen == dn.gen: the launch's generation. */
+typedef struct {
+  aos_gemv_fused_params gu, dn;
+  uint32_t *hflags; /* [dn.n_pre + dn.n_cons] lines of 32 words */
+} aos_decode_mlp_params;
 
 /* Routing from features and the fused gate/up launch in one grid: workgroups [0, rp.T) route
  * one token each (the plain router), then fp's producers (the x shrink; its plan workgroup waits
@@ -374,6 +423,9 @@ int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_gemv3(const aos_gemv3_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv_fused(const aos_gemv_fused_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_launch_decode_mlp(const aos_decode_mlp_params *p, const aos_launch_ctx *ctx);
+/* consistency of a fused parameter block (sizes, generations, hand-off pointers) */
+int aos_fused_params_ok(const aos_gemv_fused_params *fp, int swiglu); /* 1: consistent */
 int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);

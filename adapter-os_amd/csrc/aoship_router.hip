@@ -603,11 +603,7 @@ extern "C" int aos_launch_route_gate_up(const aos_route_gu_params *q, const aos_
     return (int)hipErrorInvalidValue;
   if (q->rp.scope || q->rp.tie_key || q->rp.post_allowed || q->rp.active_ids || q->rp.strengths || q->rp.hashes)
     return (int)hipErrorInvalidValue; /* the plain router only */
-  if (fp.n != 1 || fp.hsum || fp.gp[0].waves != 4 || fp.gp[0].T != T || fp.sp.T != T || !fp.sync || !fp.flags ||
-      fp.n_pre < 1 || fp.pre_rows < 1 || fp.n_pre % fp.pre_rows || fp.n_pre / fp.pre_rows != fp.sp.ks ||
-      !fp.sp.plan_build.plan || fp.n_cons != (uint32_t)(fp.gp[0].w0.RB * fp.gp[0].ks) ||
-      fp.wg_end[0] != (int)fp.n_cons || fp.gp[0].sync != fp.sync || fp.gp[0].flags != fp.flags ||
-      fp.gp[0].sync_target != (uint32_t)fp.n_pre)
+  if (!aos_fused_params_ok(&fp, 1) || fp.hsum || fp.gp[0].T != T || !fp.sp.plan_build.plan)
     return (int)hipErrorInvalidValue;
   if ((size_t)(q->rp.d + q->rp.n) * sizeof(float) > 60 * 1024) return (int)hipErrorInvalidValue;
   if (T <= 1) return launch_rgu<1>(q, ctx);

@@ -95,15 +95,17 @@ __device__ __forceinline__ int shrink_rows(const aos_shrink_params &p) {
 }
 
 /* One workgroup of the shrink: row block lrb (lrb == shrink_rows(p): the plan workgroup, when
- * plan_build is set), K split ksi. */
+ * plan_build is set), K split ksi. Returns true in wave 0 of the workgroup that completes the row
+ * block (the one that stored its S, or split 0 of a row block with nothing to compute, or of the
+ * plan), false elsewhere. */
 template <int NV, int W, int D>
-__device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsigned char *smem) {
+__device__ bool shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsigned char *smem) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rb_total = shrink_rows(p);
   if (lrb == rb_total) {
     if (ksi == 0 && p.plan_build.plan) build_plan(p.plan_build);
-    return;
+    return ksi == 0;
   }
   const int rb_global = lrb;
   int m = 0;
@@ -115,7 +117,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
   const int rpad = tab.rpad;
   const int nslots = p.all_mode ? tab.n : (p.plan->U < AOS_PLAN_MAXU ? p.plan->U : AOS_PLAN_MAXU);
   /* uniform for every K split of this row block */
-  if (rpad == 0 || lrb * 32 >= nslots * rpad) return;
+  if (rpad == 0 || lrb * 32 >= nslots * rpad) return ksi == 0;
 
   const int T = p.T, in = p.in, G = in >> 6;
   const int i = lane & 31, c = lane >> 5;
@@ -143,7 +145,8 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
 #pragma unroll
   for (int jx = 0; jx < XE; ++jx) {
     int idx = tid + jx * 64 * W;
-    idx = idx < nx ? idx : nx - 1;
+    idx = idx < nx ? idx : idx % nx; /* surplus lanes re-read chunks spread over x (a single
+                                      * clamped chunk would be one cache line hit by every lane) */
     const int t = idx / xchunks, r = idx - t * xchunks;
     xv[jx] = *(const u32x4 *)(p.x + (size_t)t * in + (size_t)gw0 * 64 + r * 8);
   }
@@ -207,7 +210,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
 #pragma unroll
   for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc[v];
   lds_barrier();
-  if (wave != 0) return;
+  if (wave != 0) return false;
   float tot[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -222,7 +225,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
     uint32_t old = 0;
     if (lane == 0) old = aos_arrive(&p.counters[rb_global]);
     old = aos_shfl(old, 0);
-    if (old != (uint32_t)p.ks - 1u) return;
+    if (old != (uint32_t)p.ks - 1u) return false;
     if (lane == 0) aos_reset(&p.counters[rb_global]);
 #pragma unroll
     for (int v = 0; v < NV; ++v) tot[v] = 0.0f;
@@ -254,6 +257,7 @@ __device__ void shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsig
       if (mt < T) aos_publish(&S[(size_t)mt * stride + col], valid ? tot[v] : 0.0f);
     }
   }
+  return true;
 }
 
 }  // namespace aos_shrink

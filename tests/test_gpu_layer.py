@@ -65,6 +65,30 @@ def test_mlp_decode_unfused_launches(hip, T):
     assert np.array_equal(_run_mlp(hip, layer, xb, rings), fused)
 
 
+@pytest.mark.parametrize("one_launch,lines", [(True, True), (True, False), (False, False)])
+@pytest.mark.parametrize("T", [1, 2, 8])
+def test_mlp_decode_handoff_variants(hip, T, one_launch, lines):
+    """The decode MLP with the other in-launch hand-offs: the 1-2 token MLP as one launch (gate/up
+    row blocks hand h to the down GEMV workgroups of the same grid), and the counted hand-off (the
+    producers count in, the last raises one flag per consumer) instead of per-producer lines. Each
+    is bit-identical run to run, within the tolerance, and leaves no timed-out wait; the default
+    afterwards reproduces its own earlier output."""
+    cid = 2
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    default = _run_mlp(hip, layer, xb, rings)
+    layer.set_decode_handoff(one_launch, lines)
+    y1 = _run_mlp(hip, layer, xb, rings)
+    y2 = _run_mlp(hip, layer, xb, rings)
+    layer.set_decode_handoff(False, True)
+    assert layer.wait_timeouts() == 0
+    assert np.array_equal(y1, y2), "run-to-run outputs differ"
+    ref = oracle_mlp(cid, xf, rings)
+    assert tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref) <= REL_TOL
+    assert np.array_equal(_run_mlp(hip, layer, xb, rings), default)
+
+
 def test_mlp_no_adapters_matches_base(hip):
     """Zero gates / empty rings: the layer is the plain int4 SwiGLU MLP."""
     cid, T = 1, 4
