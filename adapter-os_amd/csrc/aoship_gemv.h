@@ -109,6 +109,58 @@ __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
   f = aos_mfma32(av, e.b, f);
 }
 
+/* Steps q0, q0 + qs, ... (< nq) of one module, up to EB at a time: the loads of a batch go out
+ * phase by phase (plan list, then B row pointers, then B fragments, S and coefficients), so a
+ * batch costs three memory round trips rather than three per step. Steps past nq load nothing
+ * (the branches are uniform). */
+template <int EB>
+__device__ __forceinline__ void expand_rest(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
+                                            int stride, int q0, int qs, int nq, int row, int lane, bool coherent,
+                                            f32x16 &f) {
+  const int i = lane & 31, c = lane >> 5;
+  const int ti = i < p.T ? i : 0;
+  const int rpad = tab.rpad;
+  for (int qb = q0; qb < nq; qb += EB * qs) {
+    int u[EB], j0[EB], a[EB];
+    const uint16_t *bptr[EB];
+    ExpandStep e[EB];
+#pragma unroll
+    for (int k = 0; k < EB; ++k) {
+      const int q = qb + k * qs;
+      u[k] = 16 * q / rpad;
+      j0[k] = 16 * q - u[k] * rpad;
+      a[k] = 0;
+      if (q < nq)
+        a[k] = coherent ? (int)__hip_atomic_load(&p.plan->list[u[k]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : (int)p.plan->list[u[k]];
+    }
+#pragma unroll
+    for (int k = 0; k < EB; ++k) {
+      bptr[k] = nullptr;
+      if (qb + k * qs < nq) bptr[k] = aos_gld_ptr(&tab.B[a[k]]);
+    }
+#pragma unroll
+    for (int k = 0; k < EB; ++k) {
+      if (qb + k * qs >= nq) continue;
+      e[k].a = a[k];
+      e[k].cf = i < p.T ? load_f(&p.plan->coef[ti][u[k]], coherent) : 0.0f;
+      e[k].b = aos_gld16(bptr[k] ? bptr[k] + (size_t)row * rpad + j0[k] + 8 * c : p.zero_row);
+      const float *sp = S + (size_t)ti * stride + (p.s_all ? a[k] : u[k]) * rpad + j0[k] + 8 * c;
+      if (coherent) {
+        e[k].s0 = make_float4(load_f(sp, true), load_f(sp + 1, true), load_f(sp + 2, true), load_f(sp + 3, true));
+        e[k].s1 = make_float4(load_f(sp + 4, true), load_f(sp + 5, true), load_f(sp + 6, true), load_f(sp + 7, true));
+      } else {
+        e[k].s0 = *(const float4 *)sp;
+        e[k].s1 = *(const float4 *)(sp + 4);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < EB; ++k)
+      if (qb + k * qs < nq) expand_apply(e[k], f);
+  }
+}
+
+
 /* Row block rb, K split ksi of one matrix (or of the gate/up pair). */
 /* The down projection's LoRA shrink over the 32 rows of h this row block produced (wave 0 only,
  * after the SwiGLU): h goes through LDS as a [token][row] bf16 tile (the MFMA's token operand);
@@ -476,15 +528,10 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     }
     if (q_first < nq0) expand_apply(e0, f0);
     if (SW && q_first < nq1) expand_apply(e1, f1);
-    for (int q = q_first + q_step; q < nq0; q += q_step) {
-      expand_load(p, p.tab0, p.S0, p.s_stride0, q, row, lane, e0, fused);
-      expand_apply(e0, f0);
-    }
-    if (SW)
-      for (int q = q_first + q_step; q < nq1; q += q_step) {
-        expand_load(p, p.tab1, p.S1, p.s_stride1, q, row, lane, e1, fused);
-        expand_apply(e1, f1);
-      }
+    if (q_first + q_step < nq0)
+      expand_rest<4>(p, p.tab0, p.S0, p.s_stride0, q_first + q_step, q_step, nq0, row, lane, fused, f0);
+    if (SW && q_first + q_step < nq1)
+      expand_rest<4>(p, p.tab1, p.S1, p.s_stride1, q_first + q_step, q_step, nq1, row, lane, fused, f1);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       acc0[v] += f0[v];

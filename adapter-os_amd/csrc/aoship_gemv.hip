@@ -125,17 +125,23 @@ int launch_mlp_nv(const aos_decode_mlp_params *mp, const aos_launch_ctx *ctx) {
   return (int)hipGetLastError();
 }
 
+#ifndef AOS_GU_RING
+#define AOS_GU_RING 4 /* groups in flight per wave: gate/up GEMV */
+#endif
+#ifndef AOS_ONE_RING
+#define AOS_ONE_RING 4 /* ... single-matrix GEMVs (measured: 12 in flight lengthen every dependent round trip) */
+#endif
 template <int NV>
 int launchf_nv(const aos_gemv_fused_params *fp, int swiglu, const aos_launch_ctx *ctx) {
   const int nwg = fp->n_pre + (int)fp->n_cons;
   size_t lds = fp->hsum ? (size_t)HSUM_V * 64 * (fp->gp[0].waves) * 4 : (size_t)fp->sp.lds_bytes;
   for (int i = 0; i < fp->n; ++i) lds = lds > (size_t)fp->gp[i].lds_bytes ? lds : (size_t)fp->gp[i].lds_bytes;
   if (swiglu) {
-    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, true, 4, 4>), dim3(nwg), dim3(256), lds, *fp);
+    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, true, 4, AOS_GU_RING>), dim3(nwg), dim3(256), lds, *fp);
   } else if (fp->gp[0].waves == 4) {
-    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, false, 4, 12>), dim3(nwg), dim3(256), lds, *fp);
+    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, false, 4, AOS_ONE_RING>), dim3(nwg), dim3(256), lds, *fp);
   } else {
-    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, false, 8, 12>), dim3(nwg), dim3(512), lds, *fp);
+    AOS_LAUNCH(ctx, (aos_gemv_fused_kernel<NV, false, 8, AOS_ONE_RING>), dim3(nwg), dim3(512), lds, *fp);
   }
   return (int)hipGetLastError();
 }

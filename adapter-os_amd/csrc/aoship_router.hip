@@ -215,10 +215,29 @@ __device__ __forceinline__ int scale_gate(int q, float strength) {
   return (int)r;
 }
 
+/* Per-adapter inputs of the selection besides the prior: the allowed mask, the scope hint and
+ * the tie-break key (stable_id, or the adaptive mode's rank). */
+struct RouteMeta {
+  int allowed, in_scope;
+  uint64_t sid;
+};
+
+template <bool X>
+__device__ __forceinline__ RouteMeta route_meta(const aos_route_params &p, int i) {
+  RouteMeta m = {1, 1, 0ull};
+  if (i >= p.n) return m;
+  if (p.allowed) m.allowed = p.allowed[i];
+  if (X && p.scope) m.in_scope = p.scope[i];
+  m.sid = (X && p.tie_key) ? p.tie_key[i] : (p.stable_id ? p.stable_id[i] : 0ull);
+  return m;
+}
+
 /* X: the extras (scope, adaptive keys, decision policy, ring mapping, decision hashes) are
- * compiled in; the X = false instance is the plain router, launched when none is set. */
+ * compiled in; the X = false instance is the plain router, launched when none is set. first: the
+ * lane's RouteMeta for adapter `lane`, loaded ahead (NULL: loaded here). */
 template <bool LDS, bool X>
-__device__ __forceinline__ void route_one(const aos_route_params &p, const float *priors, int t, int lane) {
+__device__ __forceinline__ void route_one(const aos_route_params &p, const float *priors, int t, int lane,
+                                          const RouteMeta *first = nullptr) {
   const int n = p.n;
   const uint8_t *scope = X ? p.scope : nullptr;
   const uint64_t *tie_key = X ? p.tie_key : nullptr;
@@ -231,28 +250,28 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
   bool bad = false;
   uint64_t ka = ~0ull, kb = ~0ull;
   int m_allowed = 0;
-  auto load_key = [&](int i, uint64_t &a, uint64_t &b) -> bool {
+  auto load_key = [&](int i, uint64_t &a, uint64_t &b, const RouteMeta &m) -> bool {
     a = ~0ull;
     b = ~0ull;
     if (i >= n) return false;
     const float raw = priors[i];
     if (!__builtin_isfinite(raw)) bad = true;
-    if (p.allowed && !p.allowed[i]) return false;
+    if (!m.allowed) return false;
     /* scope hint (router.rs:1587-1602): adapters outside the scope score from -1e9 */
-    const float prior = (scope && !scope[i]) ? -1.0e9f : raw;
+    const float prior = (scope && !m.in_scope) ? -1.0e9f : raw;
     float sim = (prior + 0.0f) - 0.0f;
     float score = sim * p.bias;
     score = score * 1.0f;
     if (!__builtin_isfinite(score)) bad = true;
     /* adaptive mode (sort_scores_adaptive, router.rs:265-306): the rank of (breaker, stable_id,
      * index) stands in for stable_id, which orders equal scores exactly as those three keys do */
-    uint64_t sid = tie_key ? tie_key[i] : (p.stable_id ? p.stable_id[i] : 0ull);
+    const uint64_t sid = m.sid;
     a = ((uint64_t)score_key_desc(score) << 32) | (sid >> 32);
     b = ((sid & 0xffffffffull) << 32) | (uint64_t)(uint32_t)i;
     return true;
   };
   {
-    bool v = load_key(lane, ka, kb);
+    bool v = load_key(lane, ka, kb, first ? *first : route_meta<X>(p, lane));
     m_allowed += __popcll(__ballot(v));
     if (n <= AOS_WAVE) {
       /* n <= 64: rank selection. Keys are unique (they end in the index), so lane i's rank is
@@ -285,7 +304,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     bool v = false;
     if (lane >= 8) {
       uint64_t a, b;
-      v = load_key(base + lane - 8, a, b);
+      v = load_key(base + lane - 8, a, b, route_meta<X>(p, base + lane - 8));
       ka = a;
       kb = b;
     }
@@ -304,103 +323,77 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     return;
   }
 
-  /* Gather the top entries into every lane (uniform from here on). */
-  float sc[8];
-  uint32_t skey[8], sidx[8];
-  uint64_t ssid[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    uint64_t a = aos_shfl64(ka, s), b = aos_shfl64(kb, s);
-    skey[s] = (uint32_t)(a >> 32);
-    sc[s] = score_from_key(skey[s]);
-    ssid[s] = ((a & 0xffffffffull) << 32) | (b >> 32);
-    sidx[s] = (uint32_t)b;
-  }
-  if (tie_key) {
-    /* the canonical re-sort keeps stable_id in adaptive mode (router.rs:1305-1325) */
-#pragma unroll
-    for (int s = 0; s < 8; ++s) ssid[s] = (s < kk && p.stable_id) ? p.stable_id[sidx[s]] : 0ull;
-  }
+  /* Lane l works on top-K entry e = l % 8 (lanes 8 and up repeat lanes 0..7); what every lane
+   * needs of the other entries comes through shuffles. Each entry's arithmetic is the serial
+   * loop's, and the sums run over the entries in top-K order, so the results are the serial
+   * code's. */
+  const int e = lane & 7;
+  const uint64_t ea = aos_shfl64(ka, e), eb = aos_shfl64(kb, e);
+  const uint32_t e_key = (uint32_t)(ea >> 32), e_idx = (uint32_t)eb;
+  const float e_sc = score_from_key(e_key);
+  uint64_t e_sid = ((ea & 0xffffffffull) << 32) | (eb >> 32);
+  /* the canonical re-sort keeps stable_id in adaptive mode (router.rs:1305-1325) */
+  if (tie_key) e_sid = (e < kk && p.stable_id) ? p.stable_id[e_idx] : 0ull;
 
   /* deterministic_softmax (router.rs:1340-1411); tau > 0 after sanitising. */
   double mx = -__builtin_inf();
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    if (s < kk) mx = rust_f64_max(mx, (double)sc[s]);
-  /* lane s evaluates exp for top-K entry s (the same value the serial loop would produce), then
-   * every lane gathers the K values and runs the Kahan summation in top-K order */
-  double my_e;
-  {
-    const int s = lane & 7;
-    float my_sc = sc[0];
-#pragma unroll
-    for (int q = 1; q < 8; ++q)
-      if (s == q) my_sc = sc[q];
-    my_e = aos_exp_cr(((double)my_sc - mx) / (double)p.tau);
+  for (int s = 0; s < 8; ++s) {
+    const float v = aos_shfl_f(e_sc, s);
+    if (s < kk) mx = rust_f64_max(mx, (double)v);
   }
-  double e[8];
+  const double e_exp = aos_exp_cr(((double)e_sc - mx) / (double)p.tau);
   double sum = 0.0, comp = 0.0;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    const uint64_t bits = __builtin_bit_cast(uint64_t, my_e);
-    const double ex = __builtin_bit_cast(double, aos_shfl64(bits, s));
+    const double ex = __builtin_bit_cast(double, aos_shfl64(__builtin_bit_cast(uint64_t, e_exp), s));
     if (s < kk) {
       double y = ex - comp;
       double tt = sum + y;
       comp = (tt - sum) - y;
       sum = tt;
-      e[s] = ex;
-    } else {
-      e[s] = 0.0;
     }
   }
-  float g[8];
-  float uni = 1.0f / (float)kk;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) g[s] = (sum == 0.0) ? uni : (float)(e[s] / sum);
-  float min_gate = p.eps / (float)kk;
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-    if (s < kk) g[s] = rust_f32_max(g[s], min_gate);
+  float g = (sum == 0.0) ? 1.0f / (float)kk : (float)(e_exp / sum);
+  g = rust_f32_max(g, p.eps / (float)kk);
   float S = 0.0f;
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    if (s < kk) S += g[s];
+  for (int s = 0; s < 8; ++s) {
+    const float gs = aos_shfl_f(g, s);
+    if (s < kk) S += gs;
+  }
   if (!(S > 0.0f)) {
     ring_empty(ring, p.status, t, lane, policy ? -2 : 0);
     hash_empty(hashes, t, lane);
     return;
   }
-  int q[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) q[s] = (s < kk) ? quantize_q15(g[s] / S) : 0;
+  const int e_q = e < kk ? quantize_q15(g / S) : 0;
 
-  /* Canonical order (router.rs:1310-1325): rank of each candidate. */
-  int rank[8];
+  /* Canonical order (router.rs:1310-1325): entry e's rank among the kk entries. */
+  int rank = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int r = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j == i || j >= kk) continue;
-      bool before = q[j] > q[i] ||
-                    (q[j] == q[i] &&
-                     (skey[j] < skey[i] ||
-                      (skey[j] == skey[i] &&
-                       (ssid[j] < ssid[i] || (ssid[j] == ssid[i] && sidx[j] < sidx[i])))));
-      r += before ? 1 : 0;
-    }
-    rank[i] = r;
+  for (int j = 0; j < 8; ++j) {
+    const int qj = (int)aos_shfl((uint32_t)e_q, j);
+    const uint32_t kj = aos_shfl(e_key, j), ij = aos_shfl(e_idx, j);
+    const uint64_t sj = aos_shfl64(e_sid, j);
+    const bool before =
+        qj > e_q ||
+        (qj == e_q && (kj < e_key || (kj == e_key && (sj < e_sid || (sj == e_sid && ij < e_idx)))));
+    rank += (j != e && j < kk && before) ? 1 : 0;
   }
   /* lane s < kk holds decision entry s (canonical order) */
   uint32_t my_i = 0;
   int my_q = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < kk && rank[i] == lane) {
-      my_i = sidx[i];
-      my_q = q[i];
+  for (int i = 0; i < 8; ++i) {
+    const int ri = (int)aos_shfl((uint32_t)rank, i);
+    const int qi = (int)aos_shfl((uint32_t)e_q, i);
+    const uint32_t ii = aos_shfl(e_idx, i);
+    if (i < kk && ri == lane) {
+      my_i = ii;
+      my_q = qi;
     }
+  }
   if (X && hashes) {
     /* the decision hash belongs to the router's decision, before any policy filter: kk indices
      * (u16 LE) then kk gates (i16 LE), packed two halves to a word */
@@ -476,37 +469,47 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
 
 /* Dot products of router features (staged in LDS) with router weight rows: lane l sums elements
  * 256k + 4l + e (k ascending, e = 0..3) with fused multiply-adds, then a xor butterfly over the
- * 64 lanes. Up to 16 chunks of 256 weights are loaded before any arithmetic. */
-__device__ __forceinline__ float router_dot(const float *f_lds, const float *w, int d, int lane) {
-  const float4 *f4 = (const float4 *)f_lds;
+ * 64 lanes. 16 chunks of 256 weights are loaded (dot_load) before their arithmetic (dot_use). */
+__device__ __forceinline__ void dot_load(const float *w, int k0, int nk, int lane, float4 (&wv)[16]) {
   const float4 *w4 = (const float4 *)w;
-  const int nk = d >> 8;    /* full 256-element chunks */
-  const int tail = d & 255; /* multiple of 4 */
-  float acc = 0.0f;
-  for (int k0 = 0; k0 < nk; k0 += 16) {
-    float4 wv[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int k = k0 + j < nk ? k0 + j : nk - 1;
-      wv[j] = w4[k * 64 + lane];
-    }
+  for (int j = 0; j < 16; ++j) {
+    const int k = k0 + j < nk ? k0 + j : nk - 1;
+    wv[j] = w4[k * 64 + lane];
+  }
+}
+
+__device__ __forceinline__ void dot_use(const float *f_lds, const float4 (&wv)[16], int k0, int nk, int lane,
+                                        float &acc) {
+  const float4 *f4 = (const float4 *)f_lds;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (k0 + j < nk) {
-        const float4 fv = f4[(k0 + j) * 64 + lane];
-        acc = fmaf(wv[j].x, fv.x, acc);
-        acc = fmaf(wv[j].y, fv.y, acc);
-        acc = fmaf(wv[j].z, fv.z, acc);
-        acc = fmaf(wv[j].w, fv.w, acc);
-      }
+  for (int j = 0; j < 16; ++j) {
+    if (k0 + j < nk) {
+      const float4 fv = f4[(k0 + j) * 64 + lane];
+      acc = fmaf(wv[j].x, fv.x, acc);
+      acc = fmaf(wv[j].y, fv.y, acc);
+      acc = fmaf(wv[j].z, fv.z, acc);
+      acc = fmaf(wv[j].w, fv.w, acc);
     }
   }
+}
+
+/* The rest of a dot product whose first 16 chunks are in wv: the remaining chunks, the tail
+ * (d % 256 elements, a multiple of 4), then the butterfly. */
+__device__ __forceinline__ float dot_finish(const float *f_lds, const float *w, int d, int lane, float4 (&wv)[16]) {
+  const int nk = d >> 8, tail = d & 255;
+  float acc = 0.0f;
+  if (nk > 0) dot_use(f_lds, wv, 0, nk, lane, acc);
+  for (int k0 = 16; k0 < nk; k0 += 16) {
+    dot_load(w, k0, nk, lane, wv);
+    dot_use(f_lds, wv, k0, nk, lane, acc);
+  }
   if (4 * lane < tail) {
-    const float4 fv = f4[nk * 64 + lane], wv = w4[nk * 64 + lane];
-    acc = fmaf(wv.x, fv.x, acc);
-    acc = fmaf(wv.y, fv.y, acc);
-    acc = fmaf(wv.z, fv.z, acc);
-    acc = fmaf(wv.w, fv.w, acc);
+    const float4 fv = ((const float4 *)f_lds)[nk * 64 + lane], wt = ((const float4 *)w)[nk * 64 + lane];
+    acc = fmaf(wt.x, fv.x, acc);
+    acc = fmaf(wt.y, fv.y, acc);
+    acc = fmaf(wt.z, fv.z, acc);
+    acc = fmaf(wt.w, fv.w, acc);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) acc = acc + aos_shfl_f(acc, lane ^ o);
@@ -528,18 +531,27 @@ __device__ __forceinline__ void route_features_block(const aos_route_params &p, 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   float *lds_f = lds, *lds_priors = lds + p.d;
+  /* the loads of the wave's first weight row and, in wave 0, of the selection's per-adapter
+   * inputs go out before the features are staged */
+  const int nk = p.d >> 8;
+  float4 wv[16];
+  if (nk > 0 && wave < p.n) dot_load(p.router_w + (size_t)wave * p.d, 0, nk, lane, wv);
+  RouteMeta meta = {1, 1, 0ull};
+  if (wave == 0) meta = route_meta<X>(p, lane);
   const float4 *f4 = (const float4 *)(p.features + (size_t)t * p.d);
   for (int e = threadIdx.x; e < p.d / 4; e += blockDim.x) ((float4 *)lds_f)[e] = f4[e];
   __syncthreads();
   for (int a = wave; a < p.n; a += nw) {
-    const float v = router_dot(lds_f, p.router_w + (size_t)a * p.d, p.d, lane);
+    const float *wr = p.router_w + (size_t)a * p.d;
+    if (a != wave && nk > 0) dot_load(wr, 0, nk, lane, wv);
+    const float v = dot_finish(lds_f, wr, p.d, lane, wv);
     if (lane == 0) {
       lds_priors[a] = v;
       if (p.priors_out) p.priors_out[(size_t)t * p.n + a] = v;
     }
   }
   __syncthreads();
-  if (wave == 0) route_one<true, X>(p, lds_priors, t, lane);
+  if (wave == 0) route_one<true, X>(p, lds_priors, t, lane, &meta);
 }
 
 template <bool X>
