@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -130,6 +131,66 @@ class MlpCase:
         return len(used)
 
 
+class ProjCase:
+    """Device-resident attention projections (q, k, v, o) of a workload for T concurrent decode
+    streams, each token with its own routed adapter set: n_layers distinct copies of the layer
+    (own int4 weights and LoRA weights) are cycled step by step so the weights stream from HBM.
+    A step routes the T tokens from their features, then runs q/k/v in one call and o in another;
+    with route=False the rings of the first routing are reused (the projections alone)."""
+
+    def __init__(self, aoship, W, cid: int, T: int, torch, n_layers: int):
+        self.cfg = cfg = W.CONFIGS[cid]
+        self.T, self.torch, self.n_layers = T, torch, n_layers
+        base = {m: W.base_weights(cfg, m) for m in cfg.modules}
+        self.adapters = []
+        for a in range(cfg.n_adapters):
+            ad = aoship.LoraAdapter(a, n_layers, W.lora_scale(cfg))
+            for m in cfg.modules:
+                A, B = W.lora_weights(cfg, a, m)
+                for li in range(n_layers):
+                    ad.set_module(li, m, A, B)
+            self.adapters.append(ad)
+        self.layers = []
+        for li in range(n_layers):
+            layer = aoship.Layer(li)
+            for m in cfg.modules:
+                p, sc, b = base[m]
+                layer.set_base(m, p, sc, b)
+            layer.set_adapters(self.adapters)
+            layer.reserve(T)
+            self.layers.append(layer)
+        del base
+        sid = np.arange(cfg.n_adapters, dtype=np.uint64)
+        self.router = aoship.Router(cfg.n_adapters, cfg.k, cfg.tau, cfg.eps, 1.0, sid)
+        xb, _ = W.activations(cfg, T)
+        self.x = torch.from_numpy(xb.view(np.int16)).cuda()
+        self.xo = torch.from_numpy(W.activations(cfg, T, cfg.q_out)[0].view(np.int16)).cuda()
+        self.q = torch.empty((T, cfg.q_out), dtype=torch.int16, device="cuda")
+        self.k = torch.empty((T, cfg.kv_out), dtype=torch.int16, device="cuda")
+        self.v = torch.empty((T, cfg.kv_out), dtype=torch.int16, device="cuda")
+        self.o = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
+        self.rings = torch.zeros(T * 40, dtype=torch.uint8, device="cuda")
+        f, w = W.router_inputs(cfg, T)
+        self.f = torch.from_numpy(f).cuda()
+        self.w = torch.from_numpy(w).cuda()
+        self.router.route_features(self.f, self.w, self.rings)
+        self.route = True
+        self.i = 0
+
+    def step(self):
+        if self.route:
+            self.router.route_features(self.f, self.w, self.rings)
+        layer = self.layers[self.i % self.n_layers]
+        layer.qkv_forward(self.x, self.rings, self.q, self.k, self.v)
+        layer.proj_forward("o_proj", self.xo, self.rings, self.o)
+        self.i += 1
+
+    check_waits = MlpCase.check_waits
+    set_profiling = MlpCase.set_profiling
+    kernel_stats = MlpCase.kernel_stats
+    distinct_adapters = MlpCase.distinct_adapters
+
+
 def time_steps(case, steps: int, warmup: int, torch) -> float:
     """Milliseconds per step over `steps` steps, events on the launch stream (the null stream)."""
     for _ in range(warmup):
@@ -159,6 +220,19 @@ def kernel_times(case, steps: int, torch) -> dict:
 
 # The decode shrinks run in the first workgroups of the GEMV launch that reads their S.
 FUSED = True
+
+
+def c4_bytes(cfg, T: int, U: int) -> int:
+    """Algorithmic HBM bytes of one C4 step's projections: the int4 q/k/v/o matrices with their f16
+    scales and biases, the bf16 LoRA A and B rows of the U distinct adapters on all four, and the
+    bf16 activations (x in, q/k/v out, o's input in, o out)."""
+    base = lora = 0
+    for m in cfg.modules:
+        out, inp = cfg.shape(m)
+        base += out * inp // 2 + 2 * 2 * out * (inp // 64)
+        lora += cfg.rank * (inp + out) * 2
+    acts = T * cfg.hidden * 2 + T * (cfg.q_out + 2 * cfg.kv_out) * 2 + T * cfg.q_out * 2 + T * cfg.hidden * 2
+    return base + U * lora + acts
 
 
 def gate_up_bytes(cfg, T: int, U: int) -> int:
@@ -242,9 +316,32 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(W, T: int = 1) -> dict:
-    """The C oracle (float32, dequantising on the fly, OpenMP over output rows) on this host: a
-    bounded sample of the decode workload, routing included."""
+def host_cpu_info() -> dict:
+    """The host's CPU topology (lscpu), the logical CPUs the OS reports (nproc) and the CPUs this
+    process may run on (its affinity mask)."""
+    info = {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        out = ""
+    keys = {"Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket", "Thread(s) per core": "threads_per_core",
+            "Model name": "model"}
+    for line in out.splitlines():
+        k, _, v = line.partition(":")
+        k = k.strip()
+        if k in keys:
+            v = v.strip()
+            info[keys[k]] = int(v) if v.isdigit() else v
+    if all(k in info for k in ("sockets", "cores_per_socket")):
+        info["physical_cores"] = info["sockets"] * info["cores_per_socket"]
+    return info
+
+
+def cpu_baseline(W, T: int = 1, runs: int = 20) -> dict:
+    """The C oracle (float32, dequantising on the fly, OpenMP over output rows) on this host, on the
+    7B-shaped decode workload: the router (priors from features, then routing) and the layer (int4
+    SwiGLU MLP with the K=4 LoRA deltas) timed separately, each the median of `runs` timed calls
+    after warm-up, once on every CPU this job may use and once on one thread."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
@@ -255,34 +352,54 @@ def cpu_baseline(W, T: int = 1) -> dict:
     f, w = W.router_inputs(cfg, T)
     _, xf = W.activations(cfg, T)
     sid = np.arange(cfg.n_adapters, dtype=np.uint64)
+    rings = None
 
-    def one():
+    def router():
+        nonlocal rings
         pri = oracle.priors(f, w)
         rings = oracle.route_batch(pri, cfg.k, cfg.tau, cfg.eps, 1.0, sid)
+
+    def layer():
         oracle.mlp_forward(xf, bw["gate_proj"], bw["up_proj"], bw["down_proj"], lora, scales, cfg.rank, rings)
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    threads = min(threads, 16)
-    oracle.set_threads(threads)
-    one()
-    n, t0 = 0, time.perf_counter()
-    while n < 3 or (time.perf_counter() - t0 < 8.0 and n < 200):
-        one()
-        n += 1
-    per = (time.perf_counter() - t0) / n
-    oracle.set_threads(1)
-    t1 = time.perf_counter()
-    one()
-    per1 = time.perf_counter() - t1
+    def median_ms(fn) -> float:
+        for _ in range(2):
+            fn()
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)) * 1e3
+
+    host = host_cpu_info()
+    # the CPUs this job may use: its affinity mask, or fewer when the job is given a thread budget
+    # (OMP_NUM_THREADS; a GPU job here is allotted a share of the host's cores)
+    threads = host["affinity_cpus"]
+    budget = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    if budget > 0:
+        threads = min(threads, budget)
+    figures = {}
+    for name, nt in (("all", threads), ("one", 1)):
+        oracle.set_threads(nt)
+        r_ms = median_ms(router)
+        l_ms = median_ms(layer)
+        figures[name] = {"threads": nt, "router_ms": r_ms, "layer_ms": l_ms, "tok_s": T / ((r_ms + l_ms) * 1e-3)}
     oracle.set_threads(threads)
     return {
-        "value": T / per,
+        "value": figures["all"]["tok_s"],
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"7B-shaped decode step (route + int4 SwiGLU MLP + K=4 LoRA), T={T}, {n} steps on "
-                  f"{threads} threads; 1 thread: {T / per1:.3f} tok/s",
-        "single_thread_tok_s": T / per1,
+        "sample": f"7B-shaped decode step, T={T}: router (features -> priors -> rings) and layer (int4 SwiGLU "
+                  f"MLP + K=4 LoRA) each the median of {runs} timed calls after 2 warm-up calls; tok/s = T / "
+                  f"(router + layer); on {threads} threads and on 1",
+        "router_ms": figures["all"]["router_ms"],
+        "layer_ms": figures["all"]["layer_ms"],
+        "single_thread": figures["one"],
+        "host": host,
+        "threads_note": "threads = the CPUs in this process's affinity mask, capped by OMP_NUM_THREADS when set "
+                        "(the CPU share a one-GPU job is given on a shared host)",
     }
 
 
@@ -410,6 +527,8 @@ def main() -> int:
     ap.add_argument("--probe-prefill", action="store_true",
                     help="run the prefill hardware-counter workload only (see probe_prefill())")
     ap.add_argument("--skip-model", action="store_true", help="skip the full-model decode line")
+    ap.add_argument("--skip-c4", action="store_true", help="skip the multi-tenant projection line (C4)")
+    ap.add_argument("--skip-c5", action="store_true", help="skip the 32B stress prefill line (C5)")
     ap.add_argument("--probe-model", action="store_true",
                     help="run the full-model decode only (--model-layers layers) and print its figures")
     ap.add_argument("--model-layers", type=int, default=28)
@@ -544,6 +663,54 @@ def main() -> int:
         log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s; kernels (us): " +
             ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kp.items()))
         del pf
+
+    # ---- C4: attention projections of a 3B-shaped layer for 32 concurrent decode streams ----
+    if not args.skip_c4:
+        c4 = ProjCase(aoship, W, 4, 32, torch, 24)
+        c4.route = False  # the projections alone (rings of the first routing): the roofline figure
+        ms_p = time_steps(c4, args.steps, args.warmup, torch)
+        kt4 = kernel_times(c4, max(20, args.steps // 4), torch)
+        c4.route = True
+        ms_s = time_steps(c4, args.steps, args.warmup, torch)
+        U4 = c4.distinct_adapters(aoship)
+        b4 = c4_bytes(c4.cfg, 32, U4)
+        ach = b4 / (ms_p * 1e-3) / 1e9
+        result["c4_projections"] = {
+            "workload": "Llama-3.2-3B-shaped q/k/v/o projections (3072 -> 3072/1024/1024, o 3072 -> 3072), int4 g64, "
+                        "32 rank-16 adapters on all four, 32 decode streams each routed to its own K=4 set from its "
+                        "features; 24 distinct layer copies cycled",
+            "streams": 32, "distinct_adapters": U4,
+            "ms_per_step": ms_s, "tok_s": 32 / (ms_s * 1e-3),
+            "projections_ms": ms_p,
+            "kernels_us": {k: v * 1e3 for k, v in kt4.items()},
+            "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": ach / HBM_PEAK_GBPS, "algorithmic_bytes": b4,
+                         "note": "q/k/v launch + o launch per step (rings given), bytes = int4 base with scales and "
+                                 "biases + the U distinct adapters' bf16 LoRA rows + bf16 activations"},
+        }
+        log(f"C4 projections, 32 streams: {ms_p * 1e3:.1f} us (projections), {ms_s * 1e3:.1f} us with routing; "
+            f"{ach:.0f} GB/s; launches (us): " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kt4.items()))
+        del c4
+
+    # ---- C5: 32B-shaped MLP, 4096-token prefill, 64 rank-64 adapters, K=8, adversarial routing ----
+    if not args.skip_c5:
+        c5 = MlpCase(aoship, W, 5, 4096, torch, 1)
+        ms5 = time_steps(c5, max(3, args.steps // 40), 2, torch)
+        kt5 = kernel_times(c5, 3, torch)
+        f5 = W.algorithmic_flops(c5.cfg, 4096)
+        tf5 = f5 / (ms5 * 1e-3) / 1e12
+        result["c5_stress"] = {
+            "workload": "Qwen2.5-32B-shaped int4 (g64) SwiGLU MLP (5120 / 27648), 64 rank-64 adapters, K=8, "
+                        "adversarial priors (exact ties, gates rounding to 0 or 1 in Q15), prefill of 4096 tokens",
+            "tokens": 4096, "ms_per_step": ms5, "tok_s": 4096 / (ms5 * 1e-3),
+            "kernels_us": {k: v * 1e3 for k, v in kt5.items()},
+            "roofline": {"bound": "mfma", "achieved": tf5, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf5 / BF16_PEAK_TFLOPS, "algorithmic_flop": f5,
+                         "note": "route + MLP per step; FLOP = base GEMMs + the K active adapters' shrink and expand"},
+        }
+        log(f"C5 stress prefill T=4096: {ms5:.3f} ms/step, {tf5:.1f} TFLOP/s; kernels (us): " +
+            ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kt5.items()))
+        del c5
 
     # ---- the whole decoder, token by token ----
     if not args.skip_model:
