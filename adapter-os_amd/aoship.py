@@ -58,6 +58,7 @@ _SIGS = {
     "aoship_layer_wait_timeouts": (C.c_int, [_P]),
     "aoship_layer_free": (None, [_P]),
     "aoship_mlp_forward": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "aoship_liquid_blend_and_forward": (C.c_int, [_P, C.c_int, _P, C.c_int, _P, C.c_int, _P, C.c_int, _P, _P]),
     "aoship_mlp_forward_noalloc": (C.c_int, [_P, _P, C.c_int, _P, _P]),
     "aoship_route_mlp_forward": (C.c_int, [_P, _P, _P, C.c_int, _P, _P, C.c_int, _P, _P, _P]),
     "aoship_proj_forward": (C.c_int, [_P, C.c_char_p, _P, C.c_int, _P, _P]),
@@ -418,6 +419,48 @@ class Layer:
         if getattr(self, "h", None) and _lib is not None and getattr(self, "owned", True):
             _lib.aoship_layer_free(self.h)
         self.h = None
+
+
+class _LiquidTensor(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("bf16", C.c_int), ("rows", C.c_int), ("cols", C.c_int), ("len", C.c_size_t)]
+
+
+class _LiquidAdapter(C.Structure):
+    _fields_ = [("id", C.c_uint16), ("down", _LiquidTensor), ("up", _LiquidTensor), ("alpha", C.c_float)]
+
+
+def _liquid_tensor(t, rows: int | None = None, cols: int | None = None) -> _LiquidTensor:
+    """A device tensor (float32, or int16/uint16 holding bfloat16 bits) as a LiquidTensor; rows and
+    cols default to its 2-D shape (pass them to describe a buffer whose shape does not match)."""
+    import torch
+
+    bf16 = t.dtype in (torch.int16, torch.uint16, torch.bfloat16)
+    r = rows if rows is not None else t.shape[0]
+    c = cols if cols is not None else (t.shape[1] if t.dim() > 1 else 1)
+    return _LiquidTensor(t.data_ptr() if t.numel() else None, 1 if bf16 else 0, r, c, t.numel())
+
+
+def liquid_blend_and_forward(adapters, coefficients, x, out, stream=None) -> int:
+    """LiquidKernel::blend_and_forward: adapters is a list of (down, up, alpha[, id]) with down / up
+    device tensors (float32, or bfloat16 bits) or already-built (down, up) LiquidTensor pairs;
+    coefficients a host sequence; x and out device float32 vectors. Returns the precision (0 =
+    float32, 1 = bfloat16)."""
+    n = len(adapters)
+    arr = (_LiquidAdapter * max(n, 1))()
+    for i, a in enumerate(adapters):
+        down, up, alpha = a[0], a[1], a[2]
+        aid = a[3] if len(a) > 3 else i
+        arr[i].id = aid
+        arr[i].down = down if isinstance(down, _LiquidTensor) else _liquid_tensor(down)
+        arr[i].up = up if isinstance(up, _LiquidTensor) else _liquid_tensor(up)
+        arr[i].alpha = alpha
+    cf = np.ascontiguousarray(np.asarray(coefficients, dtype=np.float32))
+    prec = C.c_int(-1)
+    _check(lib().aoship_liquid_blend_and_forward(C.cast(arr, C.c_void_p), n, cf.ctypes.data if cf.size else None,
+                                                 cf.size, _ptr(x), x.numel(), _ptr(out), out.numel(),
+                                                 C.byref(prec), stream),
+           "aoship_liquid_blend_and_forward")
+    return prec.value
 
 
 def exp_cr(x: float) -> float:

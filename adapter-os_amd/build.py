@@ -48,6 +48,7 @@ SOURCES = [
     "aoship_gemv.hip",
     "aoship_gemm.hip",
     "aoship_model.hip",
+    "aoship_liquid.hip",
     "aoship_api.cpp",
 ]
 

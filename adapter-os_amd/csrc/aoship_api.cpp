@@ -2326,3 +2326,82 @@ extern "C" int aoship_model_forward(aoship_model_t *m, const int32_t *ids, int T
   m->cache_len += T;
   return 0;
 }
+
+/* ---- Liquid blend ---- */
+
+/* LiquidKernel::blend_and_forward (crates/adapteros-lora-kernel-api/src/liquid.rs:147-160),
+ * checked as blend_and_forward_reference checks (liquid.rs:163-219), in its order and with its
+ * messages. */
+extern "C" int aoship_liquid_blend_and_forward(const aoship_liquid_adapter_t *adapters, int n_adapters,
+                                               const float *coefficients, int n_coefficients, const float *input,
+                                               int in_len, float *output, int out_len, int *precision, void *stream) {
+  if (n_adapters <= 0) return set_err("Liquid blend requested with zero adapters");
+  if (n_adapters > AOSHIP_LIQUID_MAX_ADAPTERS)
+    return set_err("Liquid blend exceeds max adapters (" + std::to_string(n_adapters) + " > " +
+                   std::to_string(AOSHIP_LIQUID_MAX_ADAPTERS) + ")");
+  if (n_adapters != n_coefficients)
+    return set_err("Liquid blend coefficient mismatch: " + std::to_string(n_adapters) + " adapters vs " +
+                   std::to_string(n_coefficients) + " coefficients");
+  if (!adapters || !coefficients) return set_err("aoship_liquid_blend_and_forward: null adapters or coefficients");
+  if (in_len < 0 || out_len < 0) return set_err("aoship_liquid_blend_and_forward: negative length");
+  int prec = 0;
+  for (int i = 0; i < n_adapters; ++i) {
+    const aoship_liquid_adapter_t &a = adapters[i];
+    const struct {
+      const aoship_liquid_tensor_t *t;
+      const char *label;
+    } ts[2] = {{&a.down, "down"}, {&a.up, "up"}};
+    for (const auto &e : ts) {
+      const aoship_liquid_tensor_t &t = *e.t;
+      if (t.rows < 0 || t.cols < 0 || (size_t)t.rows * (size_t)t.cols != t.len)
+        return set_err(std::string("Liquid tensor ") + e.label + " has inconsistent shape: rows*cols=" +
+                       std::to_string((long long)t.rows * t.cols) + " != len=" + std::to_string(t.len));
+    }
+    if (a.down.cols != in_len)
+      return set_err("Liquid adapter " + std::to_string(i) + " input mismatch: down.cols=" +
+                     std::to_string(a.down.cols) + " vs input len=" + std::to_string(in_len));
+    if (a.up.rows > out_len)
+      return set_err("Liquid adapter " + std::to_string(i) + " output mismatch: up.rows=" +
+                     std::to_string(a.up.rows) + " vs output len=" + std::to_string(out_len));
+    if (a.up.cols != a.down.rows)
+      return set_err("Liquid adapter " + std::to_string(i) + " rank mismatch: up.cols=" +
+                     std::to_string(a.up.cols) + " vs down.rows=" + std::to_string(a.down.rows));
+    if (a.down.bf16 || a.up.bf16) prec = 1;
+  }
+  /* this backend's own limits */
+  aos_liquid_params p;
+  memset(&p, 0, sizeof(p));
+  p.n = n_adapters;
+  p.in = in_len;
+  p.out_len = out_len;
+  p.x = input;
+  p.y = output;
+  for (int i = 0; i < n_adapters; ++i) {
+    const aoship_liquid_adapter_t &a = adapters[i];
+    const int rank = a.down.rows;
+    if (rank > AOSHIP_LIQUID_MAX_RANK)
+      return set_err("aoship_liquid_blend_and_forward: adapter " + std::to_string(i) + " rank " +
+                     std::to_string(rank) + " exceeds " + std::to_string(AOSHIP_LIQUID_MAX_RANK));
+    const size_t align_d = a.down.bf16 ? 2 : 4, align_u = a.up.bf16 ? 2 : 4;
+    if ((a.down.len && (!a.down.data || (uintptr_t)a.down.data % align_d)) ||
+        (a.up.len && (!a.up.data || (uintptr_t)a.up.data % align_u)))
+      return set_err("aoship_liquid_blend_and_forward: adapter " + std::to_string(i) +
+                     " weights must be non-NULL and aligned to their element size");
+    p.down[i] = a.down.data;
+    p.up[i] = a.up.data;
+    p.down_bf16[i] = a.down.bf16 ? 1 : 0;
+    p.up_bf16[i] = a.up.bf16 ? 1 : 0;
+    p.rank[i] = rank;
+    p.up_rows[i] = a.up.rows;
+    p.coef[i] = coefficients[i];
+    p.scaling[i] = a.alpha / (float)rank; /* liquid.rs:228 */
+  }
+  if ((in_len > 0 && (!input || (uintptr_t)input % 4)) || (out_len > 0 && (!output || (uintptr_t)output % 4)))
+    return set_err("aoship_liquid_blend_and_forward: input and output must be non-NULL, 4-byte aligned device "
+                   "float arrays");
+  if (ensure_device()) return -1;
+  if (precision) *precision = prec;
+  if (out_len == 0) return 0;
+  aos_launch_ctx c = {stream, nullptr, nullptr};
+  return launch_err(aos_launch_liquid(&p, &c), "liquid blend");
+}

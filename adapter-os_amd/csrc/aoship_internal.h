@@ -410,6 +410,21 @@ typedef struct {
     }                                                                                             \
   } while (0)
 
+/* ---- Liquid blend: up to AOS_LIQUID_MAX adapters' deltas on one activation vector ----
+ * down[a] = A [rank[a] x in], up[a] = B [up_rows[a] x rank[a]], row-major, float32 or bfloat16
+ * (the *_bf16 flags); scaling[a] = alpha / rank. Entries past n have rank 0. */
+#define AOS_LIQUID_MAX 3
+#define AOS_LIQUID_RANK_MAX 1024
+typedef struct {
+  int n, in, out_len;
+  const void *down[AOS_LIQUID_MAX], *up[AOS_LIQUID_MAX];
+  int down_bf16[AOS_LIQUID_MAX], up_bf16[AOS_LIQUID_MAX];
+  int rank[AOS_LIQUID_MAX], up_rows[AOS_LIQUID_MAX];
+  float coef[AOS_LIQUID_MAX], scaling[AOS_LIQUID_MAX];
+  const float *x; /* [in] */
+  float *y;       /* [out_len] */
+} aos_liquid_params;
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -425,6 +440,7 @@ int aos_launch_gemv3(const aos_gemv3_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemv_fused(const aos_gemv_fused_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_decode_mlp(const aos_decode_mlp_params *p, const aos_launch_ctx *ctx);
 /* consistency of a fused parameter block (sizes, generations, hand-off pointers) */
+int aos_launch_liquid(const aos_liquid_params *p, const aos_launch_ctx *ctx);
 int aos_fused_params_ok(const aos_gemv_fused_params *fp, int swiglu); /* 1: consistent */
 int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);

@@ -340,6 +340,43 @@ int aoship_model_cache_len(const aoship_model_t *model);
 int aoship_model_forward(aoship_model_t *model, const int32_t *ids, int T, int position_offset,
                          const aoship_ring_t *rings, float *logits);
 
+/* ---- Liquid blend (crates/adapteros-lora-kernel-api/src/liquid.rs) ------------------------ */
+
+#define AOSHIP_LIQUID_MAX_ADAPTERS 3 /* liquid.rs:12 (LIQUID_MAX_ADAPTERS) */
+#define AOSHIP_LIQUID_MAX_RANK 1024  /* per adapter, this backend's limit */
+
+/* LiquidTensor (liquid.rs:66-104): a row-major device matrix of float32 (bf16 == 0) or bfloat16
+ * bit patterns (bf16 == 1); len is the buffer's element count, which rows * cols must equal. */
+typedef struct {
+  const void *data;
+  int bf16;
+  int rows, cols;
+  size_t len;
+} aoship_liquid_tensor_t;
+
+/* LiquidAdapterRef (liquid.rs:106-116): down = A [rank x in_features], up = B [out_features x
+ * rank], alpha. */
+typedef struct {
+  uint16_t id;
+  aoship_liquid_tensor_t down, up;
+  float alpha;
+} aoship_liquid_adapter_t;
+
+/* LiquidKernel::blend_and_forward (liquid.rs:147-160) with the result of
+ * blend_and_forward_reference (liquid.rs:163-257): output[0 .. out_len) = 0; then for each adapter
+ * in order whose coefficient is not 0, rank_buf = down . input and, for o < up.rows,
+ * output[o] += coefficient * (up[o, :] . rank_buf) * (alpha / rank), in float32. The checks are
+ * the reference's, in its order (at least one and at most AOSHIP_LIQUID_MAX_ADAPTERS adapters, one
+ * coefficient per adapter, rows * cols == len for each tensor, down.cols == in_len,
+ * up.rows <= out_len, up.cols == down.rows), plus rank <= AOSHIP_LIQUID_MAX_RANK and non-NULL,
+ * aligned device pointers. *precision (may be NULL) receives LiquidBlendStats::precision: 0
+ * (float32) or 1 (some tensor is bfloat16). Weights, input and output are device memory; adapters
+ * and coefficients are host arrays. Runs asynchronously on stream (hipStream_t; NULL = the null
+ * stream) and allocates nothing. Returns 0 / -1 (aoship_last_error). */
+int aoship_liquid_blend_and_forward(const aoship_liquid_adapter_t *adapters, int n_adapters,
+                                    const float *coefficients, int n_coefficients, const float *input,
+                                    int in_len, float *output, int out_len, int *precision, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,13 +7,15 @@ restates and how each is pinned.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "liborc.so"
+# AOS_ORACLE_LIB selects another build of the same source (the sanitizer build, oracle/_asan)
+LIB = Path(os.environ["AOS_ORACLE_LIB"]) if os.environ.get("AOS_ORACLE_LIB") else HERE / "liborc.so"
 
 RING_DTYPE = np.dtype(
     [("top_k", "<u4"), ("current_pos", "<u4"), ("adapter_indices", "<u2", (8,)), ("gates_q15", "<i2", (8,))]

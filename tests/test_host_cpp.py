@@ -3,6 +3,7 @@ tests/cpp/aos_host_test, built by __graft_entry__.build() (make -C tests/cpp).""
 import hashlib
 import hmac
 import json
+import os
 import subprocess
 from pathlib import Path
 
@@ -10,7 +11,8 @@ import pytest
 
 import oracle
 
-EXE = Path(__file__).resolve().parent / "cpp" / "aos_host_test"
+# AOS_HOST_TEST selects another build of the program (the sanitizer build, aos_host_test_asan)
+EXE = Path(os.environ.get("AOS_HOST_TEST") or Path(__file__).resolve().parent / "cpp" / "aos_host_test")
 
 
 def _run(mode: str) -> None:

@@ -8,6 +8,7 @@ as tables of cases; the first test restates the reference's own
 test_load_adapter_with_metadata_overrides_inferred_defaults (backend.rs:1566-1586). Expected
 float16 scales come from numpy's float32 -> float16 conversion (round to nearest even)."""
 import json
+import os
 import struct
 import subprocess
 from pathlib import Path
@@ -17,7 +18,8 @@ import pytest
 import torch
 from safetensors.torch import save
 
-EXE = Path(__file__).resolve().parent / "cpp" / "aos_host_test"
+# AOS_HOST_TEST selects another build of the program (the sanitizer build, aos_host_test_asan)
+EXE = Path(os.environ.get("AOS_HOST_TEST") or Path(__file__).resolve().parent / "cpp" / "aos_host_test")
 
 
 def _exe() -> str:
