@@ -191,6 +191,23 @@ class ProjCase:
     distinct_adapters = MlpCase.distinct_adapters
 
 
+class RouteOnly:
+    """A case's router launch alone (priors or features, as the case routes)."""
+
+    def __init__(self, case):
+        self.case = case
+
+    def step(self):
+        c = self.case
+        if c.priors is None:
+            c.router.route_features(c.f, c.w, c.rings)
+        else:
+            c.router.route(c.priors, c.rings)
+
+    def check_waits(self):
+        pass
+
+
 def time_steps(case, steps: int, warmup: int, torch) -> float:
     """Milliseconds per step over `steps` steps, events on the launch stream (the null stream)."""
     for _ in range(warmup):
@@ -660,7 +677,12 @@ def main() -> int:
             "gemm_gate_up_tflops": gu_flops / (kp["q4_gemm_gate_up"] * 1e-3) / 1e12 if "q4_gemm_gate_up" in kp else None,
             "library_bf16_gemm": library_gemm_reference(torch, 2048, H, I),
         }
-        log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s; kernels (us): " +
+        # what the step holds besides the layer's launches: the router's launch, and the rest
+        # (launch gaps, host-side planning)
+        route_ms = time_steps(RouteOnly(pf), 20, 3, torch)
+        result["prefill"]["route_us"] = route_ms * 1e3
+        result["prefill"]["step_minus_route_and_launches_us"] = (msp - route_ms - sum(kp.values())) * 1e3
+        log(f"prefill T=2048: {msp:.3f} ms/step, {tflops:.1f} TFLOP/s; route {route_ms * 1e3:.1f} us; kernels (us): " +
             ", ".join(f"{k} {v * 1e3:.1f}" for k, v in kp.items()))
         del pf
 
