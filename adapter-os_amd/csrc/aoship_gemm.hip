@@ -851,13 +851,35 @@ struct Expand {
  * block per wave); D: weight ring depth (divides the group count); DB: token tile loads two groups
  * ahead (two register stages); APF: next sub-tile's LDS fragments loaded before the current
  * MFMAs; WV: waves per workgroup; OCC: waves per SIMD the registers are sized for; LC: expand
- * steps per chunk (their token tiles occupy LC LDS regions). */
-template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC>
+ * steps per chunk (their token tiles occupy LC LDS regions); NS: 0, or the token tiles go straight
+ * from memory to an NS-stage LDS ring, NS - 1 groups ahead of their use (no staging registers). */
+template <int NS, int LC>
+__host__ __device__ constexpr int gemm_ntile() { return NS > (LC > 2 ? LC : 2) ? NS : (LC > 2 ? LC : 2); }
+
+/* Group gx of a token tile straight to LDS (the DMA of the NS-stage ring): the wave's n (<= 4)
+ * blocks of 8 rows, block k at stage + (k * wv + wave) * 1024; v[k] is the lane's byte offset in x
+ * of its chunk in group 0. A device function of its own, not a template: the buffer resource type
+ * exists only on the device, and the kernel's lambdas are compiled for the host as well. */
+__device__ __forceinline__ void tile_dma(const uint16_t *x, int T, int in, unsigned char *stage, int wave, int wv,
+                                         int n, int v0, int v1, int v2, int v3, int gx) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, T * in * 2, 0x00020000);
+  const int v[4] = {v0, v1, v2, v3};
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (k < n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void *)(stage + (k * wv + wave) * 1024), 16, v[k], gx * 128, 0, 0);
+}
+
+/* Wait until at most n of this wave's memory instructions are outstanding (n a constant). */
+#define AOS_VM_WAIT_LE(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS = 0>
 __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params p) {
   constexpr int MT = BM / 32;
   constexpr int TILE = BM * 128;
   constexpr int NT = 64 * WV;
-  constexpr int NTILE = LC > 2 ? LC : 2;
+  constexpr int NTILE = gemm_ntile<NS, LC>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -899,25 +921,54 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
       ws1[d] = s1p[(size_t)d * 32];
     }
   }
-  /* Token tiles: LDS holds groups g and g + 1 (double buffer); registers hold the loads in
-   * flight. With D even, two register stages let the loads run two groups ahead of their LDS
-   * store. */
-  constexpr bool DB = DBT && (D % 2) == 0;
+  /* Token tiles, NS == 0: LDS holds groups g and g + 1 (double buffer); registers hold the loads
+   * in flight. With D even, two register stages let the loads run two groups ahead of their LDS
+   * store. NS > 0: tile g goes straight to LDS stage g % NS: block k of 8 rows (1 KB) by wave
+   * k % WV, lane l writing bytes 16 l (row 8 k + l / 8, slot l % 8, which holds chunk
+   * slot ^ ((row >> 1) & 7): the layout tile_off reads). */
+  constexpr bool DB = NS == 0 && DBT && (D % 2) == 0;
+  constexpr int DMA_N = BM / 8 / WV; /* 1 KB blocks per wave per tile */
+  static_assert(NS == 0 || DMA_N <= 4, "tile DMA: at most 4 blocks per wave");
   Stager<NT> st0, st1;
-  st0.rows(p.in_perm, in, p.T, m0, tid);
-  st0.load(p.x, 0);
-  if (DB) {
+  int voff[4] = {0, 0, 0, 0};
+  auto dma = [&](int stage, int gx) {
+    /* tiles past the last group repeat it and are never read */
+    tile_dma(p.x, p.T, in, smem + stage * TILE, wave, WV, DMA_N, voff[0], voff[1], voff[2], voff[3],
+             gx < G ? gx : G - 1);
+  };
+  if (NS) {
 #pragma unroll
-    for (int k = 0; k < Stager<NT>::CH; ++k) st1.off[k] = st0.off[k];
+    for (int k = 0; k < DMA_N; ++k) {
+      const int r = (k * WV + wave) * 8 + (lane >> 3);
+      const int ch = (lane & 7) ^ ((r >> 1) & 7);
+      const int ps = m0 + r < p.T ? m0 + r : p.T - 1;
+      const int tok = p.in_perm ? (int)p.in_perm[ps] : ps;
+      voff[k] = (tok * in + ch * 8) * 2;
+    }
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) dma(s, s);
+  } else {
+    st0.rows(p.in_perm, in, p.T, m0, tid);
+    st0.load(p.x, 0);
+    if (DB) {
+#pragma unroll
+      for (int k = 0; k < Stager<NT>::CH; ++k) st1.off[k] = st0.off[k];
+    }
   }
   Expand<WV, SW ? 2 : 1, 4, 2> ex(p, smem, NTILE, wave, lane, m0, mbi, row);
   ex.prefetch();
-  st0.store(smem, tid);
-  lds_barrier();
+  if (!NS) {
+    st0.store(smem, tid);
+    lds_barrier();
+  }
 
   /* token tile of weight group gx (clamped: the tiles staged past the last group are not read) */
   auto stage = [&](Stager<NT> &st, const int gx) { st.load(p.x, gx < G ? gx : G - 1); };
   if (DB) stage(st1, 1);
+  /* NS > 0: memory instructions a wave issues per group (the tile's DMA, then the ring refill);
+   * waiting until no more than VM_AFTER are outstanding completes the DMA issued NS - 1 groups
+   * earlier (at least that many were issued after it) */
+  constexpr int VM_AFTER = NS >= 2 ? (DMA_N + (SW ? 4 : 2)) * (NS - 2) : 0;
 
   /* dequantise ring slot d into B fragments, then refill it with group gn */
   auto dequant_slot = [&](const int d, const int gn, u32x4 (&f0)[4], u32x4 (&f1)[4]) {
@@ -942,12 +993,17 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
 
   /* one K group: ld receives group g + 2 (g + 1 without DB), sto holds group g + 1 */
   auto group = [&](const int g, const int d, Stager<NT> &ld, Stager<NT> &sto) {
-    const unsigned char *tb = smem + (g & 1) * TILE;
+    if (NS) { /* tile g is in LDS once this wave's DMA of it completes and every wave has waited */
+      AOS_VM_WAIT_LE(VM_AFTER);
+      lds_barrier(); /* also: every wave is past its reads of the stage refilled next */
+      dma((g + NS - 1) % NS, g + NS - 1);
+    }
+    const unsigned char *tb = smem + (NS ? (g % (NS ? NS : 1)) : (g & 1)) * TILE;
     /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
     u32x4 a[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(i, 4 * c + s));
-    stage(ld, g + (DB ? 2 : 1));
+    if (!NS) stage(ld, g + (DB ? 2 : 1));
     u32x4 f0[4], f1[4];
     dequant_slot(d, g + D, f0, f1);
 #pragma unroll
@@ -972,8 +1028,10 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
         for (int s = 0; s < 4; ++s) a[s] = an[s];
       }
     }
-    sto.store(smem + ((g & 1) ^ 1) * TILE, tid);
-    lds_barrier();
+    if (!NS) {
+      sto.store(smem + ((g & 1) ^ 1) * TILE, tid);
+      lds_barrier();
+    }
   };
 
   for (int g0 = 0; g0 < G; g0 += D) {
@@ -1068,9 +1126,9 @@ extern "C" int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_
  * per SIMD, so that one wave's dequantisation overlaps the other's matrix-core work; SwiGLU with
  * a shallow ring and single staging in 4-wave workgroups (two per CU), the single-matrix kernel
  * with the deep pipeline in 8-wave workgroups. */
-template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC>
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS>
 static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
-  constexpr int NTILE = LC > 2 ? LC : 2;
+  constexpr int NTILE = gemm_ntile<NS, LC>();
   aos_gemm_params q = *p;
   q.mb = (q.T + BM - 1) / BM;
   q.nb = (q.w0.RB + WV - 1) / WV;
@@ -1078,20 +1136,27 @@ static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx)
   const dim3 grid(q.mb * q.nb), block(64 * WV);
   const int G = q.w0.G;
   if (G % D == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, D, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, D, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
   else if (G % 2 == 0)
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 2, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 2, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
   else
-    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 1, DBT, APF, WV, OCC, LC>), grid, block, lds, q);
+    AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 1, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
 }
+
+#ifndef AOS_GEMM_NS_SW
+#define AOS_GEMM_NS_SW 4 /* token-tile LDS stages, SwiGLU GEMM (0: register staging) */
+#endif
+#ifndef AOS_GEMM_NS_ONE
+#define AOS_GEMM_NS_ONE 4 /* ... single-matrix GEMM */
+#endif
 
 extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx) {
   if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->mtiles != (p->T + BM - 1) / BM || (p->sa_mod_before < 0) ||
       p->sa_mod_before > 2 || p->rpad0 % 16 || p->rpad1 % 16 || (swiglu && (!p->w1.qt || p->w1.RB != p->w0.RB)))
     return (int)hipErrorInvalidValue;
   if (swiglu)
-    launch_gemm_cfg<true, 2, false, false, 4, 2, 2>(p, ctx);
+    launch_gemm_cfg<true, 2, false, false, 4, 2, 2, AOS_GEMM_NS_SW>(p, ctx);
   else
-    launch_gemm_cfg<false, 4, true, true, 8, 2, 4>(p, ctx);
+    launch_gemm_cfg<false, 4, true, true, 8, 2, 4, AOS_GEMM_NS_ONE>(p, ctx);
   return (int)hipGetLastError();
 }
