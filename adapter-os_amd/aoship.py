@@ -116,6 +116,8 @@ def lib():
         L.aoship_internal_layer_set_separate_shrinks.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_set_decode_handoff.restype = C.c_int
         L.aoship_internal_layer_set_decode_handoff.argtypes = [_P, C.c_int, C.c_int]
+        L.aoship_internal_layer_set_prefill_shrink.restype = C.c_int
+        L.aoship_internal_layer_set_prefill_shrink.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_last_perm.restype = C.c_int
         L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
@@ -361,6 +363,12 @@ class Layer:
         fused launches (default) instead of an arrival count with one flag per consumer."""
         _check(lib().aoship_internal_layer_set_decode_handoff(self.h, 1 if one_launch else 0, 1 if lines else 0),
                "aoship_internal_layer_set_decode_handoff")
+
+    def set_prefill_shrink(self, fused: bool) -> None:
+        """Diagnostic: the prefill MLP's LoRA shrinks in the GEMM launches that consume them
+        (default) or in launches of their own."""
+        _check(lib().aoship_internal_layer_set_prefill_shrink(self.h, 1 if fused else 0),
+               "aoship_internal_layer_set_prefill_shrink")
 
     def last_perm(self):
         """Token order (sorted position -> token) of the last grouped MLP prefill chunk, or None."""

@@ -639,6 +639,7 @@ struct aoship_layer {
   bool separate_shrinks = false; /* each decode shrink in a launch of its own (diagnostic) */
   bool one_launch_mlp = false;   /* 1-2 token MLP in one launch */
   bool producer_lines = true;    /* fused launches hand over through per-producer lines */
+  bool prefill_fused_shrink = true; /* prefill MLP: the LoRA shrinks run in the GEMM launches */
   hipStream_t stream = nullptr;
   bool profiling = false;
   KStat stats[KS_COUNT];
@@ -937,6 +938,15 @@ extern "C" int aoship_internal_layer_set_decode_handoff(aoship_layer_t *l, int o
   if (!l) return set_err("aoship_internal_layer_set_decode_handoff: null layer");
   l->one_launch_mlp = one_launch != 0;
   l->producer_lines = lines != 0;
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): whether the prefill MLP's LoRA shrinks run as
+ * the first workgroups of the GEMM launches that consume them (fused) or as launches of their
+ * own with K split into slices. Results agree within float32 summation order. */
+extern "C" int aoship_internal_layer_set_prefill_shrink(aoship_layer_t *l, int fused) {
+  if (!l) return set_err("aoship_internal_layer_set_prefill_shrink: null layer");
+  l->prefill_fused_shrink = fused != 0;
   return 0;
 }
 
@@ -1398,9 +1408,11 @@ static void plan_prefill_common(aoship_layer *l, Carve &cv, const aoship_ring_t 
 
 /* Tile shrink over modules [m0, m0 + nm) of the plan (sharing x, whose rows are read through perm,
  * or in sorted order when perm is NULL). K slices: about 512 workgroups over the tiles, at least 8
- * groups a slice, at most 16 slices, and the slices' partial sums within 128 MiB. */
+ * groups a slice, at most 16 slices, and the slices' partial sums within 128 MiB. fused: the
+ * shrink runs in the consuming GEMM launch instead (see fuse_shrink): only the SA layout and
+ * buffer are planned. */
 static void plan_tshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const uint16_t *x, const uint16_t *perm,
-                         int T, int in, int m0, int nm, aos_tshrink_params &sp) {
+                         int T, int in, int m0, int nm, aos_tshrink_params &sp, bool fused = false) {
   memset(&sp, 0, sizeof(sp));
   if (!P.lora) return;
   sp.x = x;
@@ -1424,6 +1436,12 @@ static void plan_tshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const
   sp.mtiles = P.mtiles;
   sp.s_stride = ceil_div(cols, 64) * 64;
   sp.csets = ceil_div(cols, 128);
+  if (fused) {
+    sp.SA = cv.b.take<uint16_t>((size_t)T * sp.s_stride);
+    sp.zero_row = l->zeros.as<uint16_t>();
+    sp.timeout = l->wait_dev;
+    return;
+  }
   const int G = in / 64;
   int ks = ceil_div(512, P.mtiles);
   if (ks > 16) ks = 16;
@@ -1467,10 +1485,27 @@ static void plan_gemm(aoship_layer *l, const PrefillPlan &P, const aos_tshrink_p
   for (int i = 0; i < nbefore && i < 2; ++i) g.rpad_before[i] = sp.rpad[i];
 }
 
+/* The shrink sp (planned with fused = true) as the first workgroups of GEMM g, over g's modules
+ * (mod0, and mod0 + 1 in SwiGLU mode, the first modules of sp). */
+static void fuse_shrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const aos_tshrink_params &sp,
+                        aos_gemm_params &g) {
+  if (!P.lora || sp.nmod == 0) return;
+  const int c0 = P.tu_cap * g.rpad0, c1 = P.tu_cap * g.rpad1;
+  g.s_cols = c0 > c1 ? c0 : c1;
+  if (g.s_cols == 0) return;
+  g.ap = P.gp.ap;
+  g.coef = P.gp.coef;
+  g.sa_out = sp.SA;
+  g.sa_ctr = cv.counters((size_t)P.mtiles);
+  g.sa_lines = cv.flag_lines((size_t)P.mtiles * 32);
+  g.timeout = l->wait_dev;
+}
+
 struct MlpPrefill {
   PrefillPlan P;
   aos_tshrink_params sx, sh;
   aos_gemm_params g1, g2;
+  bool fused_x = false, fused_h = false; /* the x / h shrink runs in the GEMM launch */
   size_t bytes = 0, ctr = 0, flg = 0;
 };
 
@@ -1483,10 +1518,20 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
   plan_prefill_common(l, cv, rings, T, tall, 3, M.P);
   uint16_t *h = cv.b.take<uint16_t>((size_t)T * I); /* sorted rows when grouped */
   const uint16_t *perm = M.P.lora ? M.P.gp.perm : nullptr;
-  plan_tshrink(l, cv, M.P, x, perm, T, H, 0, 2, M.sx);
+  /* each shrink in its GEMM's launch when its workgroups fit in the idle slots of that grid's
+   * last round, else a launch of its own (K split into slices) */
+  M.fused_x = M.fused_h = false;
+  if (M.P.lora && l->prefill_fused_shrink) {
+    const int tc = M.P.tu_cap, rg = tall[0].rpad, ru = tall[1].rpad, rd = tall[2].rpad;
+    M.fused_x = aos_gemm_shrink_fits(T, Wg.RB, tc * (rg > ru ? rg : ru), 1) != 0;
+    M.fused_h = aos_gemm_shrink_fits(T, Wd.RB, tc * rd, 0) != 0;
+  }
+  plan_tshrink(l, cv, M.P, x, perm, T, H, 0, 2, M.sx, M.fused_x);
   plan_gemm(l, M.P, M.sx, Wg, &Wu, x, perm, nullptr, T, 0, 0, h, M.g1);
-  plan_tshrink(l, cv, M.P, h, nullptr, T, I, 2, 1, M.sh);
+  plan_tshrink(l, cv, M.P, h, nullptr, T, I, 2, 1, M.sh, M.fused_h);
   plan_gemm(l, M.P, M.sh, Wd, nullptr, h, nullptr, perm, T, 2, 0, y, M.g2);
+  if (M.fused_x) fuse_shrink(l, cv, M.P, M.sx, M.g1);
+  if (M.fused_h) fuse_shrink(l, cv, M.P, M.sh, M.g2);
   if (M.P.lora && M.sh.nmod == 0) M.g2.out_perm = perm; /* h is in sorted order even without a down expand */
   if (M.P.lora && M.sx.nmod == 0) M.g1.in_perm = perm;
   M.bytes = cv.b.off + 256;
@@ -1775,10 +1820,12 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       l->last_perm = M.P.lora ? M.P.gp.perm : nullptr;
       l->last_perm_T = M.P.lora ? Tc : 0;
       if (launch_gplan(l, M.P)) return -1;
-      if (launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
+      if (!M.fused_x && launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
+      if (M.g1.s_cols) M.g1.gen = next_gen(&l->gen);
       aos_launch_ctx c2 = launch_ctx(l, KS_GEMM_GU);
       if (launch_err(aos_launch_gemm(&M.g1, 1, &c2), "q4 gemm gate/up")) return -1;
-      if (launch_tshrink(l, M.sh, KS_PSHRINK_H)) return -1;
+      if (!M.fused_h && launch_tshrink(l, M.sh, KS_PSHRINK_H)) return -1;
+      if (M.g2.s_cols) M.g2.gen = next_gen(&l->gen);
       aos_launch_ctx c4 = launch_ctx(l, KS_GEMM_DOWN);
       if (launch_err(aos_launch_gemm(&M.g2, 0, &c4), "q4 gemm down")) return -1;
     }

@@ -51,6 +51,14 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+/* Workgroup barrier for a ring whose LDS writes come from buffer loads straight to LDS, whose
+ * completion each wave has already waited for with a counted vmcnt: this wave's LDS reads have
+ * returned (lgkmcnt 0), then s_barrier; the asm's memory clobber keeps the compiler from moving
+ * memory accesses across it. (A release fence here would make the compiler drain every
+ * outstanding memory load, the ring's later loads included: LDS DMA writes count as vector
+ * memory operations.) */
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 /* Two floats -> packed bfloat16 pair (round to nearest even, v_cvt_pk_bf16_f32). */
 __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   bf16x2_t v;
@@ -713,13 +721,13 @@ struct Expand {
   unsigned char *smem;
   const uint16_t **lbp;
   const uint16_t *const *bpt[2];
-  int wave, lane, m0, row, TU, n0, nls, off[2], rp[2];
+  int wave, lane, m0, mbi, row, TU, n0, nls, off[2], rp[2];
   bool bp_lds;
 
   /* row: the lane's weight row (of every module) */
   __device__ Expand(const aos_gemm_params &p_, unsigned char *smem_, int ntile, int wave_, int lane_, int m0_,
-                    int mbi, int row_)
-      : p(p_), smem(smem_), wave(wave_), lane(lane_), m0(m0_), row(row_) {
+                    int mbi_, int row_)
+      : p(p_), smem(smem_), wave(wave_), lane(lane_), m0(m0_), mbi(mbi_), row(row_) {
     lbp = (const uint16_t **)(smem + ntile * TILE + 16);
     TU = (p.tu && (p.rpad0 | (NM == 2 ? p.rpad1 : 0))) ? __builtin_amdgcn_readfirstlane(p.tu[mbi]) : 0;
     rp[0] = p.rpad0;
@@ -766,8 +774,13 @@ struct Expand {
   template <int LC, class Mma>
   __device__ void run(const int (&koff)[NW], Mma &&mma) {
     if (nls == 0) return;
+    if (p.nbs && threadIdx.x == 0) { /* SA comes from this launch's shrink workgroups */
+      if (!aos_wait_gen(p.sa_lines + (size_t)mbi * 32, p.gen) && p.timeout)
+        __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier(); /* the prefetched pointers, and every wave past the K loop's last LDS reads */
+    lds_barrier(); /* the prefetched pointers, the tile's SA line, and every wave past the K loop's
+                    * last LDS reads */
     const int rows = p.T - m0 < BM ? p.T - m0 : BM;
     const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.SA + (size_t)m0 * p.sa_stride), (short)0, rows * p.sa_stride * 2, 0x00020000);
@@ -812,8 +825,13 @@ struct Expand {
         const int rr = r < rows ? r : rows - 1;
         const int col = cb + ch * 16;
         const int vo = col < lim ? rr * rb + col : (int)0x80000000;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, 0);
+        /* SA stored in this launch (by a workgroup maybe on another XCD): device-coherent (sc1) */
+        if (p.nbs)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, SC1);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, 0);
       }
     };
     const uint16_t *pr[LC][NP];
@@ -874,6 +892,121 @@ __device__ __forceinline__ void tile_dma(const uint16_t *x, int T, int in, unsig
 /* Wait until at most n of this wave's memory instructions are outstanding (n a constant). */
 #define AOS_VM_WAIT_LE(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 
+/* Shrink workgroup sb of token tile mbi (a GEMM launch's first workgroups): for module
+ * m = sb % nmg of the nmg modules the launch's expand consumes (SwiGLU: gate, up), S = x . A^T over
+ * the tile's union columns c = 32 WV (sb / nmg) + 32 w + i (wave w, lane i % 32), with the token
+ * tiles through the same NS-stage LDS ring as the GEMM workgroups and the A rows (bf16) as the
+ * weight operand through a 4-deep register ring; then SA[p][off_m + c] = bf16(coef[p][u] * S)
+ * with u = c / rpad_m, stored device-coherently, and an arrival on the tile's counter: the last of
+ * the tile's nbs workgroups raises its line. A workgroup whose columns are all past the tile's
+ * union only arrives. Column c reads union slot u = c / rpad, row c - u * rpad of its A (zeros for
+ * an adapter without the module). */
+template <int WV, int NS>
+__device__ __forceinline__ void tile_shrink_rows(const aos_gemm_params &p, unsigned char *smem, int mbi, int sb,
+                                                 int nmg, int wave, int lane) {
+  constexpr int MT = BM / 32, TILE = BM * 128, DMA_N = BM / 8 / WV, D = 4;
+  const int i = lane & 31, c = lane >> 5;
+  const int m0 = mbi * BM, G = p.w0.G, in = p.w0.in;
+  const int tn = p.T - m0 < BM ? p.T - m0 : BM;
+  const int TU = __builtin_amdgcn_readfirstlane(p.tu[mbi]);
+  const int m = sb % nmg, cb = sb / nmg;
+  const int rp = m == 0 ? p.rpad0 : p.rpad1;
+  int off = m == 0 ? 0 : TU * p.rpad0;
+  for (int k = 0; k < p.sa_mod_before; ++k) off += TU * p.rpad_before[k];
+  const int C = TU * rp;
+  const int col = cb * 32 * WV + 32 * wave + i;
+  if (cb * 32 * WV < C) { /* uniform */
+    const uint16_t *arow = p.zero;
+    size_t kst = 0;
+    if (col < C) {
+      const int u = col / rp, j = col - u * rp;
+      const uint16_t *A = aos_gld_ptr(p.ap + ((size_t)(p.mod0 + m) * p.mtiles + mbi) * p.tu_cap + u);
+      if (A) {
+        arow = A + (size_t)j * in;
+        kst = 1;
+      }
+    }
+    /* word s of lane (i, c): K elements 32 c + 8 s .. +7 of group g (the GEMM's fragment layout) */
+    auto bload = [&](int g, u32x4 (&b)[4]) {
+      const int gc = g < G ? g : G - 1;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[s] = aos_gld16(arow + kst * ((size_t)gc * 64 + 32 * c + 8 * s));
+    };
+    int voff[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < DMA_N; ++k) {
+      const int r = (k * WV + wave) * 8 + (lane >> 3);
+      const int ch = (lane & 7) ^ ((r >> 1) & 7);
+      const int ps = m0 + r < p.T ? m0 + r : p.T - 1;
+      const int tok = p.in_perm ? (int)p.in_perm[ps] : ps;
+      voff[k] = (tok * in + ch * 8) * 2;
+    }
+    auto dma = [&](int stage, int gx) {
+      tile_dma(p.x, p.T, in, smem + stage * TILE, wave, WV, DMA_N, voff[0], voff[1], voff[2], voff[3],
+               gx < G ? gx : G - 1);
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) dma(s, s);
+    u32x4 b[D][4];
+#pragma unroll
+    for (int d = 0; d < D; ++d) bload(d, b[d]);
+    /* the prologue's tiles are complete: the counted wait below covers the later ones */
+    AOS_VM_WAIT_LE(0);
+    /* memory instructions per group: the DMA of a tile, then the A rows of the group D ahead. At
+     * the top of group g >= NS - 1 the DMA of tile g was issued NS - 1 groups earlier and followed
+     * by that group's A loads and NS - 2 full groups: at most VM_AFTER outstanding means it is
+     * complete */
+    constexpr int VM_AFTER = 4 + (NS - 2) * (DMA_N + 4);
+    f32x16 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+    /* group g: tile g is in LDS once each wave's DMA of it is complete and all have passed the
+     * barrier, which also puts every wave past its reads of the stage the next DMA refills */
+    auto grp = [&](int g, u32x4 (&bb)[4]) {
+      AOS_VM_WAIT_LE(VM_AFTER);
+      ring_barrier();
+      dma((g + NS - 1) % NS, g + NS - 1);
+      const unsigned char *tb = smem + (g % NS) * TILE;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 a[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[mt] = aos_mfma32(a[s], bb[s], acc[mt]);
+      }
+      bload(g + D, bb);
+    };
+    for (int g = 0; g < G; g += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (g + d < G) grp(g + d, b[d]);
+    }
+    aos_mem_wait(); /* the rings' trailing loads (past the last group) land before the workgroup ends */
+    if (col < C) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(p.sa_out + (size_t)m0 * p.sa_stride), (short)0, tn * p.sa_stride * 2, 0x00020000);
+      const int u = col / rp;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = mt * 32 + aos_acc_m(v, lane);
+          if (r >= tn) continue;
+          const float cf = p.coef[(size_t)(m0 + r) * p.tu_cap + u];
+          __builtin_amdgcn_raw_buffer_store_b16(aos_f32_to_bf16(cf * acc[mt][v]), rs,
+                                                (r * p.sa_stride + off + col) * 2, 0, SC1);
+        }
+    }
+  }
+  aos_mem_wait();
+  __syncthreads();
+  if (threadIdx.x == 0 && aos_arrive(p.sa_ctr + mbi) == (uint32_t)p.nbs - 1u) {
+    aos_reset(p.sa_ctr + mbi);
+    aos_raise(p.sa_lines + (size_t)mbi * 32, p.gen);
+  }
+}
+
 template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS = 0>
 __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params p) {
   constexpr int MT = BM / 32;
@@ -884,8 +1017,16 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, c = lane >> 5;
+  /* The launch's first mb * nbs workgroups are shrink workgroups (tile fastest): dispatched before
+   * every GEMM workgroup, which waits for them only after its K loop, so none waits on a
+   * workgroup that cannot start. */
+  const int nsh = p.mb * p.nbs;
+  if (NS > 0 && (int)blockIdx.x < nsh) { /* uniform */
+    tile_shrink_rows<WV, (NS > 0 ? NS : 2)>(p, smem, blockIdx.x % p.mb, blockIdx.x / p.mb, SW ? 2 : 1, wave, lane);
+    return;
+  }
   int mbi, nbk;
-  gemm_tile_of(blockIdx.x, p.mb, p.nb, mbi, nbk);
+  gemm_tile_of(blockIdx.x - nsh, p.mb, p.nb, mbi, nbk);
   const int m0 = mbi * BM;
   const int G = p.w0.G, in = p.w0.in, RB = p.w0.RB;
 
@@ -1127,13 +1268,16 @@ extern "C" int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_
  * a shallow ring and single staging in 4-wave workgroups (two per CU), the single-matrix kernel
  * with the deep pipeline in 8-wave workgroups. */
 template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS>
-static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
+static int launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx) {
   constexpr int NTILE = gemm_ntile<NS, LC>();
   aos_gemm_params q = *p;
   q.mb = (q.T + BM - 1) / BM;
   q.nb = (q.w0.RB + WV - 1) / WV;
+  /* shrink workgroups: one module, 32 columns per wave (they use the LDS ring: NS > 0) */
+  q.nbs = q.s_cols > 0 ? (SW ? 2 : 1) * ((q.s_cols + 32 * WV - 1) / (32 * WV)) : 0;
+  if (q.nbs && NS == 0) return (int)hipErrorInvalidValue;
   const size_t lds = (size_t)NTILE * BM * 128 + gemm_aux();
-  const dim3 grid(q.mb * q.nb), block(64 * WV);
+  const dim3 grid(q.mb * (q.nbs + q.nb)), block(64 * WV);
   const int G = q.w0.G;
   if (G % D == 0)
     AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, D, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
@@ -1141,6 +1285,7 @@ static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx)
     AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 2, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
   else
     AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, 1, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
+  return (int)hipGetLastError();
 }
 
 #ifndef AOS_GEMM_NS_SW
@@ -1150,13 +1295,40 @@ static void launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx)
 #define AOS_GEMM_NS_ONE 4 /* ... single-matrix GEMM */
 #endif
 
+/* Whether a GEMM's shrink workgroups (s_cols columns per module at the widest union) fit in the
+ * idle slots of its grid's last round on the current device: then the launch takes no longer with
+ * them. Workgroups resident per CU: the waves the kernel's registers allow, and its LDS. */
+template <bool SW, int WV, int OCC, int LC, int NS>
+static int shrink_fits_cfg(int T, int RB, int s_cols) {
+  if (NS == 0 || s_cols <= 0) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus < 1)
+    return 0;
+  const size_t lds = (size_t)gemm_ntile<NS, LC>() * BM * 128 + gemm_aux();
+  int per_cu = 4 * OCC / WV;
+  const int by_lds = (int)(((size_t)160 << 10) / lds);
+  if (by_lds < per_cu) per_cu = by_lds;
+  if (per_cu < 1) per_cu = 1;
+  const long slots = (long)cus * per_cu;
+  const long n = (long)((T + BM - 1) / BM) * ((RB + WV - 1) / WV);
+  const long slack = (n + slots - 1) / slots * slots - n;
+  const long nsh = (long)((T + BM - 1) / BM) * (SW ? 2 : 1) * ((s_cols + 32 * WV - 1) / (32 * WV));
+  return nsh <= slack ? 1 : 0;
+}
+
+extern "C" int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu) {
+  if (swiglu) return shrink_fits_cfg<true, 4, 2, 2, AOS_GEMM_NS_SW>(T, RB, s_cols);
+  return shrink_fits_cfg<false, 8, 2, 4, AOS_GEMM_NS_ONE>(T, RB, s_cols);
+}
+
 extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx) {
   if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->mtiles != (p->T + BM - 1) / BM || (p->sa_mod_before < 0) ||
       p->sa_mod_before > 2 || p->rpad0 % 16 || p->rpad1 % 16 || (swiglu && (!p->w1.qt || p->w1.RB != p->w0.RB)))
     return (int)hipErrorInvalidValue;
-  if (swiglu)
-    launch_gemm_cfg<true, 2, false, false, 4, 2, 2, AOS_GEMM_NS_SW>(p, ctx);
-  else
-    launch_gemm_cfg<false, 4, true, true, 8, 2, 4, AOS_GEMM_NS_ONE>(p, ctx);
-  return (int)hipGetLastError();
+  if (p->s_cols < 0 || (p->s_cols > 0 && (!p->ap || !p->coef || !p->sa_out || p->sa_out != p->SA || !p->sa_ctr ||
+                                          !p->sa_lines || !p->gen || !p->tu || p->s_cols > p->tu_cap * 1024)))
+    return (int)hipErrorInvalidValue;
+  if (swiglu) return launch_gemm_cfg<true, 2, false, false, 4, 2, 2, AOS_GEMM_NS_SW>(p, ctx);
+  return launch_gemm_cfg<false, 4, true, true, 8, 2, 4, AOS_GEMM_NS_ONE>(p, ctx);
 }

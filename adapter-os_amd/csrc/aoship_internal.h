@@ -330,6 +330,19 @@ typedef struct {
   int rpad_before[2]; /* their padded ranks */
   const uint16_t *zero; /* 16 zero bytes */
   uint16_t *y;        /* [T][out] */
+  /* The LoRA shrink in the same launch (s_cols > 0): the launch's first mb * nbs workgroups
+   * compute SA = bf16(coef * x . A^T) over each tile's union columns of module mod0 (and mod0 + 1
+   * in SwiGLU mode) from the same token tiles, store it device-coherently and raise the tile's
+   * line; the tile's GEMM workgroups wait for that line before their expand. s_cols is the larger
+   * module's column count at the widest union (tu_cap * rpad); nbs is set by the launcher. */
+  int s_cols, nbs;
+  const uint16_t *const *ap; /* [nmod][mtiles][tu_cap] A pointers of the plan */
+  const float *coef;         /* [T][tu_cap], sorted rows */
+  uint16_t *sa_out;          /* == SA */
+  uint32_t *sa_ctr;          /* [mtiles] arrival counters, zero at rest */
+  uint32_t *sa_lines;        /* [mtiles] lines of 32 words, raised to gen */
+  uint32_t gen;
+  uint32_t *timeout;         /* set when a wait gave up */
 } aos_gemm_params;
 
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
@@ -446,6 +459,7 @@ int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx 
 int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);
 #ifdef __cplusplus
 }
 #endif

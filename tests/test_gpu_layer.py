@@ -168,6 +168,32 @@ def test_mlp_stress_32b_prefill(hip):
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
 
 
+@pytest.mark.parametrize("cid,T", [(1, 300), (3, 2048)])
+def test_mlp_prefill_shrink_modes(hip, cid, T):
+    """The prefill LoRA shrinks as the first workgroups of the GEMM launches (default) and as
+    launches of their own with K split into slices: both within tolerance of the oracle, each
+    bit-identical run to run, and equal to each other up to float32 summation order."""
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    out = {}
+    for fused in (True, False):
+        layer.set_prefill_shrink(fused)
+        y = _run_mlp(hip, layer, xb, rings)
+        assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), f"fused={fused}: run-to-run outputs differ"
+        out[fused] = W.bf16_bits_to_f32(y).reshape(T, -1)
+    layer.set_prefill_shrink(True)
+    perm = layer.last_perm()
+    sample = np.arange(T) if T <= 300 else np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
+    ref = oracle_mlp(cid, xf[sample], rings[sample])
+    for fused in (True, False):
+        ratio = report(f"C{cid} prefill T={T} shrink fused={fused}", out[fused][sample], ref)
+        assert ratio <= REL_TOL, f"fused={fused}: max tolerance ratio {ratio:.4g}"
+    # float32 order changes flip some bf16 roundings of SA and h: a small fraction of the
+    # tolerance (a wrong column or adapter would give ratios near 1)
+    assert tol_ratio(out[True], out[False]) <= REL_TOL / 2
+
+
 @pytest.mark.parametrize("T", [33, 100, 128, 129, 300])
 def test_mlp_prefill_ragged_full_parity(hip, T):
     """Prefill path at token counts around the 128-token tile (0.5B-shaped layer, every token
