@@ -122,18 +122,20 @@ def lib():
         L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
         L.aoship_internal_decode_geometry.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
-                                                      C.POINTER(C.c_int), C.POINTER(C.c_int)]
+                                                      C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        L.aoship_internal_layer_set_gemv_geometry.restype = C.c_int
+        L.aoship_internal_layer_set_gemv_geometry.argtypes = [_P, C.c_int, C.c_int, C.c_int]
         _lib = L
     return _lib
 
 
-def decode_geometry(kind: int, out: int, inp: int, T: int) -> tuple[int, int, int]:
-    """(waves, K splits, fewest K groups of any wave) of a decode launch shape (see
-    aoship_internal_decode_geometry)."""
-    w, k, g = C.c_int(), C.c_int(), C.c_int()
-    _check(lib().aoship_internal_decode_geometry(kind, out, inp, T, C.byref(w), C.byref(k), C.byref(g)),
+def decode_geometry(kind: int, out: int, inp: int, T: int) -> tuple[int, int, int, int]:
+    """(waves, K splits, row blocks per workgroup, fewest K groups of any wave) of a decode launch
+    shape (see aoship_internal_decode_geometry)."""
+    w, k, r, g = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+    _check(lib().aoship_internal_decode_geometry(kind, out, inp, T, C.byref(w), C.byref(k), C.byref(r), C.byref(g)),
            "aoship_internal_decode_geometry")
-    return w.value, k.value, g.value
+    return w.value, k.value, r.value, g.value
 
 
 def last_error() -> str:
@@ -363,6 +365,12 @@ class Layer:
         fused launches (default) instead of an arrival count with one flag per consumer."""
         _check(lib().aoship_internal_layer_set_decode_handoff(self.h, 1 if one_launch else 0, 1 if lines else 0),
                "aoship_internal_layer_set_decode_handoff")
+
+    def set_gemv_geometry(self, kind: int, wr: int = 0, ks: int = 0) -> None:
+        """Diagnostic: pin the decode GEMV geometry of launch kind 0 (gate/up), 1 (down) or 2
+        (projections) to wr row blocks per workgroup and ks K splits (0: automatic)."""
+        _check(lib().aoship_internal_layer_set_gemv_geometry(self.h, kind, wr, ks),
+               "aoship_internal_layer_set_gemv_geometry")
 
     def set_prefill_shrink(self, fused: bool) -> None:
         """Diagnostic: the prefill MLP's LoRA shrinks in the GEMM launches that consume them

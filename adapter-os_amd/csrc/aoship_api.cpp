@@ -640,6 +640,9 @@ struct aoship_layer {
   bool one_launch_mlp = false;   /* 1-2 token MLP in one launch */
   bool producer_lines = true;    /* fused launches hand over through per-producer lines */
   bool prefill_fused_shrink = true; /* prefill MLP: the LoRA shrinks run in the GEMM launches */
+  /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
+   * workgroup and K splits, 0 = chosen by the geometry (diagnostic) */
+  int geo_wr[3] = {0, 0, 0}, geo_ks[3] = {0, 0, 0};
   hipStream_t stream = nullptr;
   bool profiling = false;
   KStat stats[KS_COUNT];
@@ -1058,21 +1061,86 @@ static int gemv_splits(int RB, int G, int T, int W, int waves_target) {
   return ks;
 }
 
+/* Staged x (T rows of the split's groups, their group sums and 128 zero bytes) and the wave
+ * reduction's LDS. */
+static size_t gemv_lds_x(int T, int G, int ks) { return 128 + (size_t)T * ceil_div(G, ks) * 136; }
+
+/* Row-split geometry (3 or more tokens): the waves of a workgroup take different row blocks over
+ * one K split, so the x slice staged in LDS serves WR row blocks instead of one (x staged over a
+ * whole launch scales with RB / WR). The rules below are the best of sweeps over (WR, ks) on
+ * MI355X (the 7B MLP at 4, 8 and 32 tokens, the 3B projections at 32): the fewest K splits that
+ * keep x within an LDS budget while each wave streams at most a given number of K groups - fewer
+ * splits leave too few workgroups to fill the GPU, more add partial sums and x staging per byte
+ * of weights.
+ *   gate/up (SwiGLU, 4 waves): 4 row blocks per workgroup, 32 KiB of x, 14 groups of both matrices;
+ *   one long matrix (8 waves: K >= 128 groups): 8 row blocks, 64 KiB of x, 40 groups;
+ *   one short matrix (4 waves): 4 row blocks, 32 KiB of x, 6 groups.
+ * wr_force / ks_force (> 0) pin either choice (diagnostic: up to 64 KiB of x); a pinned shape that
+ * does not fit falls back to a row block per wave and the fewest splits that fit 32 KiB. */
+#ifndef AOS_GEMV_LDS_MAX_ROWS
+#define AOS_GEMV_LDS_MAX_ROWS (64 * 1024) /* staged x of a row-split shape, at most */
+#endif
+static void gemv_geometry_rows(int RB, int G, int T, bool swiglu, int W, aos_gemv_params &g, int wr_force,
+                               int ks_force) {
+  const int NA = swiglu ? 2 : 1;
+  int wr_auto = 4, gmax = 6;
+  size_t budget = AOS_GEMV_LDS_MAX;
+  if (swiglu) {
+    gmax = 14;
+  } else if (W == 8) {
+    wr_auto = 8;
+    gmax = 40;
+    budget = AOS_GEMV_LDS_MAX_ROWS;
+  }
+  int WR = wr_force > 0 ? wr_force : wr_auto;
+  if (WR > W) WR = W;
+  const int WK = W / WR;
+  auto fits = [&](int ks, size_t b) { return ks <= G && G / ks >= WK && gemv_lds_x(T, G, ks) <= b; };
+  int ks = 0;
+  if (ks_force > 0) {
+    if (fits(ks_force, AOS_GEMV_LDS_MAX_ROWS)) ks = ks_force;
+  } else {
+    for (int k = 1; k <= G && !ks; ++k)
+      if (fits(k, budget) && ceil_div(ceil_div(G, k), WK) <= gmax) ks = k;
+    for (int k = 1; k <= G && !ks; ++k) /* no split within the stream limit: the fewest that fit */
+      if (fits(k, budget)) ks = k;
+  }
+  if (ks == 0) { /* nothing fits what was asked: a row block per wave, the fewest splits that fit */
+    WR = W;
+    ks = 1;
+    while (ks < G && gemv_lds_x(T, G, ks) > AOS_GEMV_LDS_MAX) ++ks;
+  }
+  (void)RB;
+  (void)NA;
+  g.wr = WR;
+  g.ks = ks;
+}
+
 /* Every wave of a K split must get at least one group (G / ks >= W): the 8-wave single-matrix
- * kernel falls back to 4 waves when the LDS budget forces more splits (many tokens, long K). */
+ * kernel falls back to 4 waves when the LDS budget forces more splits (many tokens, long K).
+ * From 3 tokens on, the row-split geometry above. */
 static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv_params &g,
-                          int waves_target = AOS_GEMV_WAVES, bool four_waves = false) {
+                          int waves_target = AOS_GEMV_WAVES, bool four_waves = false, int wr_force = 0,
+                          int ks_force = 0) {
   int W = (swiglu || four_waves) ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
-  int ks = gemv_splits(RB, G, T, W, waves_target);
-  if (G / ks < W && W == 8) {
-    W = 4;
+  int ks = 1;
+  g.wr = 1;
+  if (T > 2 || wr_force > 0 || ks_force > 0) {
+    gemv_geometry_rows(RB, G, T, swiglu, W, g, wr_force, ks_force);
+    ks = g.ks;
+  } else {
     ks = gemv_splits(RB, G, T, W, waves_target);
+    if (G / ks < W && W == 8) {
+      W = 4;
+      ks = gemv_splits(RB, G, T, W, waves_target);
+    }
   }
   const int NA = swiglu ? 2 : 1;
-  size_t lds_x = 128 + (size_t)T * ceil_div(G, ks) * 136;
+  size_t lds_x = gemv_lds_x(T, G, ks);
   size_t lds_r = (size_t)W * NA * nv_for(T) * 64 * 4;
   g.waves = W;
   g.ks = ks;
+  g.nrbg = g.w0.RB > 0 ? ceil_div(g.w0.RB, g.wr) : 0;
   g.has_expand = lora ? 1 : 0;
   g.lds_bytes = (int)(lds_x > lds_r ? lds_x : lds_r);
 }
@@ -1103,14 +1171,14 @@ static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, i
  * GEMV (out = intermediate, in = hidden); 1: the down GEMV (out = hidden, in = intermediate);
  * 2: a projection GEMV (out = the row count of the matrices sharing x); 3: a shrink over `out`
  * rank rows launched with 8 waves when in / 64 >= AOS_GEMV_W8_MIN_G, else 4 (the x shrink);
- * 4: the same with 8 waves (the h shrink). Writes the waves, the K splits and the fewest groups
- * any wave gets. */
-extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T, int *waves, int *ks,
+ * 4: the same with 8 waves (the h shrink). Writes the waves, the K splits, the row blocks per
+ * workgroup (GEMVs; 1 for a shrink) and the fewest groups any wave gets. */
+extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T, int *waves, int *ks, int *wr,
                                                int *min_groups) {
-  if (out < 32 || in < 64 || in % 64 || T < 1 || T > AOS_DECODE_MAX_T || !waves || !ks || !min_groups)
+  if (out < 32 || in < 64 || in % 64 || T < 1 || T > AOS_DECODE_MAX_T || !waves || !ks || !wr || !min_groups)
     return set_err("aoship_internal_decode_geometry: bad arguments");
   const int G = in / 64, RB = out / 32;
-  int W = 4, k = 1;
+  int W = 4, k = 1, r = 1;
   if (kind <= 2) {
     aos_gemv_params g;
     memset(&g, 0, sizeof(g));
@@ -1118,6 +1186,7 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
     gemv_geometry(RB, G, T, kind == 0, true, g, target, kind == 1 && T <= 2);
     W = g.waves;
     k = g.ks;
+    r = g.wr;
   } else if (kind <= 4) {
     aos_shrink_params sp;
     memset(&sp, 0, sizeof(sp));
@@ -1129,7 +1198,21 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
   }
   *waves = W;
   *ks = k;
-  *min_groups = (G / k) / W;
+  *wr = r;
+  *min_groups = (G / k) / (W / r);
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): pin the decode GEMV geometry of one launch kind
+ * of this layer (0: gate/up, 1: down, 2: projections) to wr row blocks per workgroup and ks K
+ * splits (0: the geometry's own choice), for measurement sweeps. A pinned shape that leaves a
+ * wave without a K group or exceeds the LDS budget is rejected at the next forward. */
+extern "C" int aoship_internal_layer_set_gemv_geometry(aoship_layer_t *l, int kind, int wr, int ks) {
+  if (!l) return set_err("aoship_internal_layer_set_gemv_geometry: null layer");
+  if (kind < 0 || kind > 2 || wr < 0 || wr > 8 || (wr & (wr - 1)) || ks < 0 || ks > 64)
+    return set_err("aoship_internal_layer_set_gemv_geometry: bad arguments");
+  l->geo_wr[kind] = wr;
+  l->geo_ks[kind] = ks;
   return 0;
 }
 
@@ -1215,7 +1298,7 @@ static Handoff carve_handoff(Carve &cv, size_t arrive_words, size_t flag_words, 
 /* Flag words of a fused launch: one 128-byte line per GEMV workgroup for its ready flag. */
 static size_t fused_flag_words(const aos_gemv_params *gp, int n) {
   size_t c = 0;
-  for (int i = 0; i < n; ++i) c += (size_t)gp[i].w0.RB * gp[i].ks;
+  for (int i = 0; i < n; ++i) c += (size_t)gp[i].nrbg * gp[i].ks;
   return 32 * c;
 }
 
@@ -1298,7 +1381,8 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g1.w1 = Wu.dev();
   g1.x = x;
   g1.T = T;
-  gemv_geometry(Wg.RB, Wg.G, T, true, tabs_gu[0].rpad > 0 || tabs_gu[1].rpad > 0, g1);
+  gemv_geometry(Wg.RB, Wg.G, T, true, tabs_gu[0].rpad > 0 || tabs_gu[1].rpad > 0, g1, AOS_GEMV_WAVES, false,
+                l->geo_wr[0], l->geo_ks[0]);
   g1.tab0 = tabs_gu[0];
   g1.tab1 = tabs_gu[1];
   g1.S0 = P.sx.sp.S[0];
@@ -1337,7 +1421,8 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   /* the down GEMV streams beside the h shrink of its launch: more K splits (measured: 3 at the
    * 7B shape) keep its tail short; at 1-2 tokens it runs in the gate/up launch's grid, in
    * 4-wave workgroups like the rest of that grid */
-  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES, T <= 2);
+  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES, T <= 2,
+                l->geo_wr[1], l->geo_ks[1]);
   g2.tab0 = td;
   g2.S0 = s2.S[0];
   g2.s_stride0 = s2.s_stride[0];
@@ -1351,7 +1436,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   P.hpart = T <= 2 ? cv.b.take<float>((size_t)Wg.RB * T * s2.s_stride[0]) : nullptr;
   P.hsum_wgs = ceil_div(T * s2.s_stride[0], AOS_HSUM_V);
   P.hdone = cv.counter_lines(AOS_ARRIVE_WORDS(Wg.RB));
-  P.hflags = cv.flag_lines(((size_t)P.hsum_wgs + (size_t)Wd.RB * g2.ks) * 32);
+  P.hflags = cv.flag_lines(((size_t)P.hsum_wgs + (size_t)g2.nrbg * g2.ks) * 32);
   P.route_done = cv.counter_lines(32);
   P.route_flag = cv.flag_lines(32);
   P.ho1 = carve_handoff(cv, shrink_arrive_words(P.sx.sp), fused_flag_words(&g1, 1), shrink_lines(P.sx.sp));
@@ -1560,13 +1645,16 @@ static int launch_tshrink(aoship_layer *l, const aos_tshrink_params &sp, int slo
 
 static int chunk_prefill_t(int T) { return T < AOS_PREFILL_MAX_T ? T : AOS_PREFILL_MAX_T; }
 
+static void size_proj(aoship_layer *l, const int *mods, int nm, int max_tokens, size_t &bytes, size_t &ctr,
+                      size_t &flg);
+
 extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
   if (!l) return set_err("aoship_layer_reserve: null layer");
   if (max_tokens < 1) return set_err("aoship_layer_reserve: max_tokens must be >= 1");
   if (ensure_device()) return -1;
   size_t bytes = 0, ctr = 0, flg = 0;
   const bool mlp = l->mats[MOD_GATE].valid && l->mats[MOD_UP].valid && l->mats[MOD_DOWN].valid;
-  for (int T = 1; T <= AOS_DECODE_MAX_T && T <= max_tokens; T *= 2) {
+  for (int T = 1; T <= AOS_DECODE_MAX_T && T <= max_tokens; ++T) {
     if (mlp) {
       MlpPlan P;
       plan_mlp(l, T, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, P);
@@ -1582,6 +1670,13 @@ extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
     if (M.ctr > ctr) ctr = M.ctr;
     if (M.flg > flg) flg = M.flg;
   }
+  /* the projections: q, k and v together (aoship_qkv_forward) and each one alone */
+  const int qkv[3] = {MOD_Q, MOD_K, MOD_V};
+  if (l->mats[MOD_Q].valid && l->mats[MOD_K].valid && l->mats[MOD_V].valid && l->mats[MOD_K].in == l->mats[MOD_Q].in &&
+      l->mats[MOD_V].in == l->mats[MOD_Q].in)
+    size_proj(l, qkv, 3, max_tokens, bytes, ctr, flg);
+  for (int m = MOD_Q; m <= MOD_O; ++m)
+    if (l->mats[m].valid) size_proj(l, &m, 1, max_tokens, bytes, ctr, flg);
   return ws_reserve(l, bytes, ctr, flg);
 }
 
@@ -1647,7 +1742,7 @@ static void make_fused(aoship_layer *l, uint32_t *genc, const aos_shrink_params 
       f.gp[i].sync_target = (uint32_t)f.n_pre;
       f.gp[i].gen = f.gen;
       f.gp[i].timeout = l->wait_dev;
-      end += gp[i].w0.RB * gp[i].ks;
+      end += gp[i].nrbg * gp[i].ks;
     }
     f.wg_end[i] = end;
   }
@@ -1718,7 +1813,7 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
     g1.hstride = P.sh.s_stride[0];
     g1.hdone = P.hdone;
     g1.hflags = P.hflags;
-    g1.n_hflags = (uint32_t)(P.hsum_wgs + P.gv2.w0.RB * P.gv2.ks);
+    g1.n_hflags = (uint32_t)(P.hsum_wgs + P.gv2.nrbg * P.gv2.ks);
     aos_hsum_params hs;
     memset(&hs, 0, sizeof(hs));
     hs.hpart = P.hpart;
@@ -1893,6 +1988,88 @@ extern "C" int aoship_route_mlp_forward(aoship_router_t *r, const float *feature
   return mlp_decode_chunk(l, T, x, rings, y, &rp);
 }
 
+/* Prefill chunk of projections sharing x: the group plan, one tile shrink over every module, one
+ * GEMM per matrix. The same code sizes the workspace (a Carve over nullptr) and fills it. */
+struct ProjPrefill {
+  PrefillPlan P;
+  aos_tshrink_params sp;
+  aos_gemm_params gp[3];
+};
+
+static void plan_proj_prefill(aoship_layer *l, Carve &cv, const int *mods, int nm, const uint16_t *xc, int Tc,
+                              const aoship_ring_t *rc, uint16_t *const *yc, ProjPrefill &Q) {
+  const int in = l->mats[mods[0]].in;
+  aos_lora_tab tabs[3];
+  for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
+  plan_prefill_common(l, cv, rc, Tc, tabs, nm, Q.P);
+  const uint16_t *perm = Q.P.lora ? Q.P.gp.perm : nullptr;
+  plan_tshrink(l, cv, Q.P, xc, perm, Tc, in, 0, nm, Q.sp);
+  for (int i = 0; i < nm; ++i)
+    plan_gemm(l, Q.P, Q.sp, l->mats[mods[i]], nullptr, xc, perm, perm, Tc, i, i, yc ? yc[i] : nullptr, Q.gp[i]);
+}
+
+/* Decode chunk (T <= 32) of projections sharing x: the x shrink (and plan) and the GEMVs, whose
+ * K split is sized for their rows together so that they run in one launch. */
+struct ProjDecode {
+  XShrink xs;
+  aos_gemv3_params g3;
+  Handoff ho;
+};
+
+static void plan_proj_decode(aoship_layer *l, Carve &cv, const int *mods, int nm, const uint16_t *xc, int Tc,
+                             const aoship_ring_t *rc, uint16_t *const *yc, ProjDecode &Q) {
+  const int in = l->mats[mods[0]].in;
+  aos_lora_tab tabs[3];
+  for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
+  aos_plan *plan = cv.b.take<aos_plan>(1);
+  plan_x_shrink(l, cv, xc, Tc, in, tabs, nm, plan, rc, Q.xs);
+  memset(&Q.g3, 0, sizeof(Q.g3));
+  aos_gemv_params *gp = Q.g3.p;
+  int rb_all = 0;
+  for (int i = 0; i < nm; ++i) rb_all += l->mats[mods[i]].RB;
+  for (int i = 0; i < nm; ++i) {
+    const Q4Mat &W = l->mats[mods[i]];
+    gp[i].w0 = W.dev();
+    gp[i].x = xc;
+    gp[i].T = Tc;
+    gemv_geometry(rb_all, W.G, Tc, false, tabs[i].rpad > 0, gp[i], AOS_GEMV_WAVES, false, l->geo_wr[2],
+                  l->geo_ks[2]);
+    gp[i].tab0 = tabs[i];
+    gp[i].S0 = Q.xs.sp.S[i];
+    gp[i].s_stride0 = Q.xs.sp.s_stride[i];
+    gp[i].s_all = Q.xs.sp.all_mode;
+    gp[i].plan = plan;
+    gp[i].zero_row = l->zeros.as<uint16_t>();
+    gp[i].y = yc ? yc[i] : nullptr;
+    gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
+    gp[i].counters = cv.counters((size_t)W.RB);
+  }
+  Q.ho = carve_handoff(cv, shrink_arrive_words(Q.xs.sp), fused_flag_words(gp, nm), shrink_lines(Q.xs.sp));
+}
+
+/* Workspace of projections sharing x for calls of up to max_tokens tokens (decode chunks at every
+ * power of two up to 32 tokens, and the largest prefill chunk). */
+static void size_proj(aoship_layer *l, const int *mods, int nm, int max_tokens, size_t &bytes, size_t &ctr,
+                      size_t &flg) {
+  auto take = [&](const Carve &cv) {
+    bytes = std::max(bytes, cv.b.off + 256);
+    ctr = std::max(ctr, cv.coff + 64);
+    flg = std::max(flg, cv.foff + 64);
+  };
+  for (int T = 1; T <= AOS_DECODE_MAX_T && T <= max_tokens; ++T) {
+    Carve cv(nullptr, nullptr, nullptr);
+    ProjDecode Q;
+    plan_proj_decode(l, cv, mods, nm, nullptr, T, nullptr, nullptr, Q);
+    take(cv);
+  }
+  if (max_tokens > AOS_DECODE_MAX_T) {
+    Carve cv(nullptr, nullptr, nullptr);
+    ProjPrefill Q;
+    plan_proj_prefill(l, cv, mods, nm, nullptr, chunk_prefill_t(max_tokens), nullptr, nullptr, Q);
+    take(cv);
+  }
+}
+
 /* One or more projections sharing the input x. */
 static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *x, int T,
                       const aoship_ring_t *rings, uint16_t *const *ys) {
@@ -1905,28 +2082,21 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
   if (T > AOS_DECODE_MAX_T) {
     for (int t0 = 0; t0 < T; t0 += AOS_PREFILL_MAX_T) {
       const int Tc = chunk_prefill_t(T - t0);
-      const uint16_t *xc = x + (size_t)t0 * in;
-      aos_lora_tab tabs[3];
-      for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
-      PrefillPlan P;
-      aos_tshrink_params sp;
-      aos_gemm_params gp[3];
-      for (int pass = 0; pass < 2; ++pass) {
-        Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr, pass ? l->flags.p : nullptr);
-        plan_prefill_common(l, cv, rings + t0, Tc, tabs, nm, P);
-        const uint16_t *perm = P.lora ? P.gp.perm : nullptr;
-        plan_tshrink(l, cv, P, xc, perm, Tc, in, 0, nm, sp);
-        for (int i = 0; i < nm; ++i) {
-          plan_gemm(l, P, sp, l->mats[mods[i]], nullptr, xc, perm, perm, Tc, i, i,
-                    ys[i] + (size_t)t0 * l->mats[mods[i]].out, gp[i]);
-        }
-        if (pass == 0 && ws_reserve(l, cv.b.off + 256, cv.coff + 64, cv.foff + 64)) return -1;
+      uint16_t *yc[3];
+      for (int i = 0; i < nm; ++i) yc[i] = ys[i] + (size_t)t0 * l->mats[mods[i]].out;
+      ProjPrefill Q;
+      {
+        Carve c0(nullptr, nullptr, nullptr);
+        plan_proj_prefill(l, c0, mods, nm, x + (size_t)t0 * in, Tc, rings + t0, yc, Q);
+        if (ws_reserve(l, c0.b.off + 256, c0.coff + 64, c0.foff + 64)) return -1;
       }
-      if (launch_gplan(l, P)) return -1;
-      if (launch_tshrink(l, sp, KS_PSHRINK_X)) return -1;
+      Carve cv(l->ws.p, l->counters.p, l->flags.p);
+      plan_proj_prefill(l, cv, mods, nm, x + (size_t)t0 * in, Tc, rings + t0, yc, Q);
+      if (launch_gplan(l, Q.P)) return -1;
+      if (launch_tshrink(l, Q.sp, KS_PSHRINK_X)) return -1;
       for (int i = 0; i < nm; ++i) {
         aos_launch_ctx cg = launch_ctx(l, KS_GEMM_PROJ);
-        if (launch_err(aos_launch_gemm(&gp[i], 0, &cg), "q4 gemm")) return -1;
+        if (launch_err(aos_launch_gemm(&Q.gp[i], 0, &cg), "q4 gemm")) return -1;
       }
     }
     return 0;
@@ -1934,65 +2104,40 @@ static int proj_multi(aoship_layer *l, const int *mods, int nm, const uint16_t *
   for (int t0 = 0; t0 < T; t0 += AOS_DECODE_MAX_T) {
     const int Tc = (T - t0) < AOS_DECODE_MAX_T ? (T - t0) : AOS_DECODE_MAX_T;
     const uint16_t *xc = x + (size_t)t0 * in;
-    const aoship_ring_t *rc = rings + t0;
-    aos_lora_tab tabs[3];
-    for (int i = 0; i < nm; ++i) tabs[i] = lora_tab(l, mods[i], in, l->mats[mods[i]].out);
-    for (int pass = 0; pass < 2; ++pass) {
-      Carve cv(pass ? l->ws.p : nullptr, pass ? l->counters.p : nullptr, pass ? l->flags.p : nullptr);
-      aos_plan *plan = cv.b.take<aos_plan>(1);
-      XShrink xs;
-      plan_x_shrink(l, cv, xc, Tc, in, tabs, nm, plan, rc, xs);
-      /* matrices sharing x run in one launch, with a K split sized for their rows together */
-      aos_gemv3_params g3;
-      memset(&g3, 0, sizeof(g3));
-      aos_gemv_params *gp = g3.p;
-      int rb_all = 0;
-      for (int i = 0; i < nm; ++i) rb_all += l->mats[mods[i]].RB;
-      for (int i = 0; i < nm; ++i) {
-        const Q4Mat &W = l->mats[mods[i]];
-        gp[i].w0 = W.dev();
-        gp[i].x = xc;
-        gp[i].T = Tc;
-        gemv_geometry(rb_all, W.G, Tc, false, tabs[i].rpad > 0, gp[i]);
-        gp[i].tab0 = tabs[i];
-        gp[i].S0 = xs.sp.S[i];
-        gp[i].s_stride0 = xs.sp.s_stride[i];
-        gp[i].s_all = xs.sp.all_mode;
-        gp[i].plan = plan;
-        gp[i].zero_row = l->zeros.as<uint16_t>();
-        gp[i].y = ys[i] + (size_t)t0 * W.out;
-        gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);
-        gp[i].counters = cv.counters((size_t)W.RB);
+    uint16_t *yc[3];
+    for (int i = 0; i < nm; ++i) yc[i] = ys[i] + (size_t)t0 * l->mats[mods[i]].out;
+    ProjDecode Q;
+    {
+      Carve c0(nullptr, nullptr, nullptr);
+      plan_proj_decode(l, c0, mods, nm, xc, Tc, rings + t0, yc, Q);
+      if (ws_reserve(l, c0.b.off + 256, c0.coff + 64, c0.foff + 64)) return -1;
+    }
+    Carve cv(l->ws.p, l->counters.p, l->flags.p);
+    plan_proj_decode(l, cv, mods, nm, xc, Tc, rings + t0, yc, Q);
+    aos_gemv_params *gp = Q.g3.p;
+    bool expands = false;
+    for (int i = 0; i < nm; ++i) expands = expands || gp[i].has_expand;
+    if (fuse_shrinks(l) && expands && shrink_wgs(Q.xs.sp) > 0) {
+      if (Q.xs.separate_plan) {
+        aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
+        if (launch_err(aos_launch_shrink(&Q.xs.plan_only, &c0), "adapter plan")) return -1;
       }
-      const Handoff ho = carve_handoff(cv, shrink_arrive_words(xs.sp), fused_flag_words(gp, nm), shrink_lines(xs.sp));
-      if (pass == 0) {
-        if (ws_reserve(l, cv.b.off + 256, cv.coff + 64, cv.foff + 64)) return -1;
-        continue;
+      const Ws lw = {l->ws.p, l->counters.p, l->flags.p, &l->gen, true};
+      if (launch_fused(l, lw, Q.xs.sp, gp, nm, Q.ho, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
+      continue;
+    }
+    if (launch_x_shrink(l, Q.xs)) return -1;
+    aos_launch_ctx cg = launch_ctx(l, KS_GEMV_PROJ);
+    if (nm == 1) {
+      if (launch_err(aos_launch_gemv(&gp[0], 0, &cg), "q4 gemv")) return -1;
+    } else {
+      Q.g3.n = nm;
+      int end = 0;
+      for (int i = 0; i < 3; ++i) {
+        if (i < nm) end += gp[i].nrbg * gp[i].ks;
+        Q.g3.wg_end[i] = end;
       }
-      bool expands = false;
-      for (int i = 0; i < nm; ++i) expands = expands || gp[i].has_expand;
-      if (fuse_shrinks(l) && expands && shrink_wgs(xs.sp) > 0) {
-        if (xs.separate_plan) {
-          aos_launch_ctx c0 = launch_ctx(l, KS_SHRINK_X);
-          if (launch_err(aos_launch_shrink(&xs.plan_only, &c0), "adapter plan")) return -1;
-        }
-        const Ws lw = {l->ws.p, l->counters.p, l->flags.p, &l->gen, true};
-        if (launch_fused(l, lw, xs.sp, gp, nm, ho, 0, KS_GEMV_PROJ, "lora shrink + q4 gemv")) return -1;
-        continue;
-      }
-      if (launch_x_shrink(l, xs)) return -1;
-      aos_launch_ctx cg = launch_ctx(l, KS_GEMV_PROJ);
-      if (nm == 1) {
-        if (launch_err(aos_launch_gemv(&gp[0], 0, &cg), "q4 gemv")) return -1;
-      } else {
-        g3.n = nm;
-        int end = 0;
-        for (int i = 0; i < 3; ++i) {
-          if (i < nm) end += gp[i].w0.RB * gp[i].ks;
-          g3.wg_end[i] = end;
-        }
-        if (launch_err(aos_launch_gemv3(&g3, &cg), "q4 gemv")) return -1;
-      }
+      if (launch_err(aos_launch_gemv3(&Q.g3, &cg), "q4 gemv")) return -1;
     }
   }
   return 0;

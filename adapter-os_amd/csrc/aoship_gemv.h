@@ -297,17 +297,25 @@ __device__ __forceinline__ u32x4 x_load(const uint16_t *x, size_t elem, __amdgpu
   return *(const u32x4 *)(x + elem);
 }
 
-/* Row block rb, K split ksi of one matrix (or of the gate/up pair). XL: x is written by earlier
- * workgroups of this launch; the weight ring is primed first, then the workgroup waits (bounded)
- * for its line of xflag to reach p.gen and stages x with device-coherent loads. */
+/* Row-block group rbg, K split ksi of one matrix (or of the gate/up pair): the workgroup's waves
+ * cover p.wr row blocks (wave w: row block p.wr * rbg + w % p.wr, K piece w / p.wr of the split),
+ * all reading the one x slice staged for the split. Waves of a row block past the matrix (the
+ * last group of a matrix whose row blocks wr does not divide) read the last row block and store
+ * nothing. XL: x is written by earlier workgroups of this launch; the weight ring is primed
+ * first, then the workgroup waits (bounded) for its line of xflag to reach p.gen and stages x
+ * with device-coherent loads. */
 template <int NV, bool SW, int W, int D, bool XL = false>
-__device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int ksi, const uint32_t *xflag = nullptr) {
+__device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int ksi, const uint32_t *xflag = nullptr) {
   constexpr int NA = SW ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: keeps the loop scalar */
   const int G = p.w0.G, in = p.w0.in, T = p.T;
   const int i = lane & 31, c = lane >> 5;
+  const int WR = p.wr, WK = W / WR;
+  const int wr = wave % WR, wk = wave / WR;
+  const bool live = rbg * WR + wr < p.w0.RB;
+  const int rb = live ? rbg * WR + wr : p.w0.RB - 1;
   const int row = rb * 32 + i;
   const uint32_t qmask = aos_q4_mask(), qexp = aos_q4_exp();
 
@@ -319,14 +327,14 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
   }
 
   /* the expand: steps q of each module are dealt round-robin to the row block's ks workgroups
-   * and then to their waves (q = ksi + ks * (wave + W * j)); the SwiGLU kernel loads its first
-   * step's operands ahead of the K loop, the single-matrix kernel keeps its registers (and its
-   * occupancy) and loads them after the K loop */
+   * and then to the waves of its K pieces (q = ksi + ks * (wk + WK * j)); the SwiGLU kernel loads
+   * its first step's operands ahead of the K loop, the single-matrix kernel keeps its registers
+   * (and its occupancy) and loads them after the K loop */
   const bool expands = p.has_expand != 0;
   const bool fused = p.sync != nullptr || p.pre_lines != nullptr; /* S (and the plan) are produced by this launch */
   int hU = 0;
   u32x4 hpre[2][2];
-  const int q_first = ksi + p.ks * wave, q_step = p.ks * W;
+  const int q_first = ksi + p.ks * wk, q_step = p.ks * WK;
   int nq0 = 0, nq1 = 0;
   ExpandStep e0, e1;
   if (expands && !fused) {
@@ -339,7 +347,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
   {
     const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
     const int GR = gw1 - gw0;
-    const int ga = gw0 + wave * GR / W, gb = gw0 + (wave + 1) * GR / W, ng = gb - ga;
+    const int ga = gw0 + wk * GR / WK, gb = gw0 + (wk + 1) * GR / WK, ng = gb - ga;
 
     /* (1) first x staging loads, ahead of the weights. Loads are unconditional (addresses
      * clamped into range) so no control flow separates them from their use and the compiler
@@ -476,7 +484,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
       if (lines) {
         if (p.plan_line >= 0) done = aos_wait_lines(p.pre_lines + (size_t)p.plan_line * 32, 1, p.gen, lane);
       } else if (lane == 0) {
-        done = aos_wait_gen(p.flags + ((size_t)ksi * p.w0.RB + rb) * 32, p.gen);
+        done = aos_wait_gen(p.flags + ((size_t)ksi * p.nrbg + rbg) * 32, p.gen);
       }
       if (lane == 0) {
         ok = done ? 1u : 0u;
@@ -539,26 +547,33 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rb, int 
     }
   }
 
-  /* (5) fixed-order reduction over the waves (LDS reused once every wave is done with x) */
+  /* (5) fixed-order reduction over the K pieces of each row block (LDS reused once every wave is
+   * done with x): wave wr sums the pieces k = 0 .. WK - 1 (waves wr + WR k) in order */
   float *red = (float *)smem;
   lds_barrier();
+  if (WK > 1) {
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    red[(wave * NA * NV + v) * 64 + lane] = acc0[v];
-    if (SW) red[(wave * NA * NV + NV + v) * 64 + lane] = acc1[v];
+    for (int v = 0; v < NV; ++v) {
+      red[(wave * NA * NV + v) * 64 + lane] = acc0[v];
+      if (SW) red[(wave * NA * NV + NV + v) * 64 + lane] = acc1[v];
+    }
   }
   lds_barrier();
-  if (wave != 0) return;
+  if (wk != 0) return;
+  if (WK > 1) {
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float a0 = red[v * 64 + lane], a1 = SW ? red[(NV + v) * 64 + lane] : 0.0f;
-    for (int w = 1; w < W; ++w) {
-      a0 += red[(w * NA * NV + v) * 64 + lane];
-      if (SW) a1 += red[(w * NA * NV + NV + v) * 64 + lane];
+    for (int v = 0; v < NV; ++v) {
+      float a0 = red[(wr * NA * NV + v) * 64 + lane], a1 = SW ? red[(wr * NA * NV + NV + v) * 64 + lane] : 0.0f;
+      for (int k = 1; k < WK; ++k) {
+        const int w = wr + WR * k;
+        a0 += red[(w * NA * NV + v) * 64 + lane];
+        if (SW) a1 += red[(w * NA * NV + NV + v) * 64 + lane];
+      }
+      acc0[v] = a0;
+      acc1[v] = a1;
     }
-    acc0[v] = a0;
-    acc1[v] = a1;
   }
+  if (!live) return;
 
   /* (6) fixed-order reduction over the workgroups of this row block: the last one sums */
   const int nsplit = p.ks;

@@ -42,13 +42,13 @@ template <int NV, int W, int D>
 __global__ void __launch_bounds__(64 * W) aos_gemv3_kernel(aos_gemv3_params mp) {
   const int b = blockIdx.x;
   if (b < mp.wg_end[0]) {
-    gemv_body<NV, false, W, D>(mp.p[0], b % mp.p[0].w0.RB, b / mp.p[0].w0.RB);
+    gemv_body<NV, false, W, D>(mp.p[0], b % mp.p[0].nrbg, b / mp.p[0].nrbg);
   } else if (b < mp.wg_end[1]) {
     const int r = b - mp.wg_end[0];
-    gemv_body<NV, false, W, D>(mp.p[1], r % mp.p[1].w0.RB, r / mp.p[1].w0.RB);
+    gemv_body<NV, false, W, D>(mp.p[1], r % mp.p[1].nrbg, r / mp.p[1].nrbg);
   } else {
     const int r = b - mp.wg_end[1];
-    gemv_body<NV, false, W, D>(mp.p[2], r % mp.p[2].w0.RB, r / mp.p[2].w0.RB);
+    gemv_body<NV, false, W, D>(mp.p[2], r % mp.p[2].nrbg, r / mp.p[2].nrbg);
   }
 }
 
@@ -65,13 +65,13 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
   }
   const int r = b - fp.n_pre;
   if (SW || r < fp.wg_end[0]) {
-    gemv_body<NV, SW, W, D>(fp.gp[0], r % fp.gp[0].w0.RB, r / fp.gp[0].w0.RB);
+    gemv_body<NV, SW, W, D>(fp.gp[0], r % fp.gp[0].nrbg, r / fp.gp[0].nrbg);
   } else if (r < fp.wg_end[1]) {
     const int r1 = r - fp.wg_end[0];
-    gemv_body<NV, false, W, D>(fp.gp[1], r1 % fp.gp[1].w0.RB, r1 / fp.gp[1].w0.RB);
+    gemv_body<NV, false, W, D>(fp.gp[1], r1 % fp.gp[1].nrbg, r1 / fp.gp[1].nrbg);
   } else {
     const int r2 = r - fp.wg_end[1];
-    gemv_body<NV, false, W, D>(fp.gp[2], r2 % fp.gp[2].w0.RB, r2 / fp.gp[2].w0.RB);
+    gemv_body<NV, false, W, D>(fp.gp[2], r2 % fp.gp[2].nrbg, r2 / fp.gp[2].nrbg);
   }
 }
 
@@ -101,7 +101,7 @@ __global__ void __launch_bounds__(256) aos_decode_mlp_kernel(aos_decode_mlp_para
   }
   b -= gu.n_pre;
   if (b < (int)gu.n_cons) {
-    gemv_body<NV, true, 4, AOS_MLP_GU_RING>(gu.gp[0], b % gu.gp[0].w0.RB, b / gu.gp[0].w0.RB);
+    gemv_body<NV, true, 4, AOS_MLP_GU_RING>(gu.gp[0], b % gu.gp[0].nrbg, b / gu.gp[0].nrbg);
     return;
   }
   b -= (int)gu.n_cons;
@@ -110,7 +110,7 @@ __global__ void __launch_bounds__(256) aos_decode_mlp_kernel(aos_decode_mlp_para
     return;
   }
   b -= dn.n_pre;
-  gemv_body<NV, false, 4, AOS_MLP_DN_RING, true>(dn.gp[0], b % dn.gp[0].w0.RB, b / dn.gp[0].w0.RB,
+  gemv_body<NV, false, 4, AOS_MLP_DN_RING, true>(dn.gp[0], b % dn.gp[0].nrbg, b / dn.gp[0].nrbg,
                                     mp.hflags + (size_t)(dn.n_pre + b) * 32);
 }
 
@@ -161,7 +161,7 @@ int launch3_nv(const aos_gemv3_params *mp, const aos_launch_ctx *ctx) {
 
 template <int NV>
 int launch_nv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx) {
-  dim3 grid(p->w0.RB, p->ks);
+  dim3 grid(p->nrbg, p->ks);
   const size_t lds = p->lds_bytes;
   if (swiglu) {
     AOS_LAUNCH(ctx, (aos_gemv_kernel<NV, true, 4, 4>), grid, dim3(256), lds, *p);
@@ -175,9 +175,17 @@ int launch_nv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *ctx) {
 
 }  // namespace
 
+/* Row-block groups of a GEMV: wr divides the waves, nrbg = ceil(RB / wr), and the h shrink and
+ * the one-launch hand-off (which use the workgroup's LDS per row block) only with wr == 1. */
+static bool rbg_ok(const aos_gemv_params &p) {
+  if (p.wr < 1 || p.waves % p.wr || p.w0.RB < 1 || p.nrbg != (p.w0.RB + p.wr - 1) / p.wr) return false;
+  return p.wr == 1 || (!p.hpart && !p.hdone);
+}
+
 extern "C" int aos_launch_gemv(const aos_gemv_params *p, int swiglu, const aos_launch_ctx *st) {
   const int waves = p->waves;
   if (waves != 4 && waves != 8) return (int)hipErrorInvalidValue;
+  if (!rbg_ok(*p)) return (int)hipErrorInvalidValue;
   if (swiglu && waves != 4) return (int)hipErrorInvalidValue;
   const int T = p->T;
   if (T < 1 || T > AOS_DECODE_MAX_T) return (int)hipErrorInvalidValue;
@@ -198,8 +206,8 @@ extern "C" int aos_launch_gemv3(const aos_gemv3_params *mp, const aos_launch_ctx
   for (int i = 0; i < 3; ++i) {
     if (i < n) {
       const aos_gemv_params &p = mp->p[i];
-      if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1) return (int)hipErrorInvalidValue;
-      end += p.w0.RB * p.ks;
+      if (p.waves != waves || p.T != T || !rbg_ok(p) || p.ks < 1) return (int)hipErrorInvalidValue;
+      end += p.nrbg * p.ks;
     }
     if (mp->wg_end[i] != end) return (int)hipErrorInvalidValue;
   }
@@ -250,13 +258,13 @@ extern "C" int aos_fused_params_ok(const aos_gemv_fused_params *fp, int swiglu) 
   for (int i = 0; i < 3; ++i) {
     if (i < n) {
       const aos_gemv_params &p = fp->gp[i];
-      if (p.waves != waves || p.T != T || p.w0.RB < 1 || p.ks < 1 || p.gen != fp->gen) return false;
+      if (p.waves != waves || p.T != T || !rbg_ok(p) || p.ks < 1 || p.gen != fp->gen) return false;
       if (lines ? (p.pre_lines != fp->lines || p.n_pre_lines != fp->n_lines || p.plan_line != plan_line ||
                    p.sync != nullptr)
                 : (p.sync != fp->sync || p.flags != fp->flags + (size_t)end * 32 ||
                    p.sync_target != (uint32_t)fp->n_pre || p.pre_lines != nullptr))
         return false;
-      end += p.w0.RB * p.ks;
+      end += p.nrbg * p.ks;
     }
     if (fp->wg_end[i] != end) return false;
   }

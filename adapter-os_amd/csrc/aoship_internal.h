@@ -141,6 +141,10 @@ typedef struct {
   int T;
   int ks;             /* workgroups per row block (split K) */
   int waves;          /* waves per workgroup: 4 or 8 */
+  int wr;             /* row blocks per workgroup (divides waves): wave w takes row block
+                         wr * rbg + w % wr of the workgroup's row-block group rbg and K piece
+                         w / wr of the workgroup's K split; all of them share the staged x */
+  int nrbg;           /* row-block groups: ceil(RB / wr); workgroup (rbg, ksi) of the grid */
   int lds_bytes;      /* dynamic LDS: x staging + group sums, or the wave reduction */
   int has_expand;     /* 1: the K-split workgroups of each row block add the LoRA expand */
   /* LoRA expand: coef(t, u) * S[t][col(u) + j] . B_list[u][row][j] over the plan's union */
@@ -166,17 +170,17 @@ typedef struct {
   int n_pre_lines;
   int plan_line;
   uint32_t *sync;     /* producer arrivals, AOS_ARRIVE_WORDS(sync_target) words; zero between launches */
-  uint32_t *flags;    /* this matrix's ready flags [RB * ks * 32], one per 128-byte line */
+  uint32_t *flags;    /* this matrix's ready flags [nrbg * ks * 32], one per workgroup and 128-byte line */
   uint32_t sync_target;
   uint32_t gen;       /* this launch's generation: a ready flag equal to it is raised */
   uint32_t *timeout;  /* set to 1 if a wait gave up (the launch still ends) */
-  /* SwiGLU mode, fused launch: the down projection's LoRA shrink over this row block's 32 rows of
-   * h, hpart[rb][t][col] = sum_r h[t][32 rb + r] A_down(col)[32 rb + r] for the plan's union
+  /* SwiGLU mode, fused launch (wr == 1): the down projection's LoRA shrink over this row block's
+   * 32 rows of h, hpart[rb][t][col] = sum_r h[t][32 rb + r] A_down(col)[32 rb + r] for the plan's union
    * columns col < U * htab.rpad (NULL: not formed) */
   aos_lora_tab htab;
   float *hpart;
   int hstride;
-  /* one-launch decode, gate/up: h and its shrink partials go out device-coherent, and each row
+  /* one-launch decode, gate/up (wr == 1): h and its shrink partials go out device-coherent, and each row
    * block's finisher counts itself into hdone (AOS_ARRIVE_WORDS(RB) words); the last of the RB
    * raises n_hflags flag lines
    * (hflags, one per later workgroup that reads h) to gen */

@@ -209,8 +209,9 @@ class RouteOnly:
 
 
 def time_steps(case, steps: int, warmup: int, torch) -> float:
-    """Milliseconds per step over `steps` steps, events on the launch stream (the null stream)."""
-    for _ in range(warmup):
+    """Milliseconds per step over `steps` steps, events on the launch stream (the null stream). The
+    warm-up covers every layer copy a case cycles through at least once."""
+    for _ in range(max(warmup, getattr(case, "n_layers", 0))):
         case.step()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -210,7 +210,9 @@ int aoship_layer_set_base(aoship_layer_t *layer, const char *module, int out_fea
  * backend.rs:398-428). All adapters bound for one module must share its rank. Returns 0 / -1. */
 int aoship_layer_set_adapters(aoship_layer_t *layer, aoship_lora_adapter_t *const *table, int n);
 
-/* Size the device workspace for up to max_tokens tokens per call. Returns 0 / -1. */
+/* Size the device workspace for calls of up to max_tokens tokens: the MLP when gate, up and down
+ * are set, q/k/v together and every projection alone. Forwards within that size allocate
+ * nothing. Returns 0 / -1. */
 int aoship_layer_reserve(aoship_layer_t *layer, int max_tokens);
 
 /* Stream (hipStream_t) for this layer's launches; NULL = null stream. Returns 0 / -1. */

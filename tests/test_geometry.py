@@ -25,13 +25,17 @@ H_SHRINK_ROWS = [(8 * 16, 4864), (16 * 16, 18944), (64 * 64, 27648), (16 * 48, 1
 def test_every_gemv_wave_gets_a_group(T):
     for H, I in MLP_SHAPES:
         for kind, out, inp in ((0, I, H), (1, H, I)):
-            w, ks, g = aoship.decode_geometry(kind, out, inp, T)
-            assert w in (4, 8) and 1 <= ks <= inp // 64
-            assert g >= 1, f"kind {kind} {out}x{inp} T={T}: waves {w}, splits {ks}"
-            assert T * -(-(inp // 64) // ks) * 136 <= 32 * 1024, "staged x exceeds the LDS budget"
+            w, ks, wr, g = aoship.decode_geometry(kind, out, inp, T)
+            assert w in (4, 8) and 1 <= ks <= inp // 64 and wr in (1, 2, 4, 8) and w % wr == 0
+            assert wr == 1 or T > 2, "1-2 tokens keep one row block per workgroup (the h shrink needs it)"
+            assert g >= 1, f"kind {kind} {out}x{inp} T={T}: waves {w}, splits {ks}, rows {wr}"
+            budget = 64 * 1024 if (kind == 1 and w == 8 and T > 2) else 32 * 1024
+            assert 128 + T * -(-(inp // 64) // ks) * 136 <= budget, "staged x exceeds the LDS budget"
     for out, inp in PROJ_SHAPES:
-        w, ks, g = aoship.decode_geometry(2, out, inp, T)
-        assert g >= 1, f"projection {out}x{inp} T={T}: waves {w}, splits {ks}"
+        w, ks, wr, g = aoship.decode_geometry(2, out, inp, T)
+        assert g >= 1, f"projection {out}x{inp} T={T}: waves {w}, splits {ks}, rows {wr}"
+        budget = 64 * 1024 if (w == 8 and T > 2) else 32 * 1024
+        assert 128 + T * -(-(inp // 64) // ks) * 136 <= budget, "staged x exceeds the LDS budget"
 
 
 @pytest.mark.parametrize("T", range(1, 33))
@@ -41,7 +45,7 @@ def test_shrink_geometry_within_limits(T):
     reads the zero row and adds nothing."""
     for kind, shapes in ((3, SHRINK_ROWS), (4, H_SHRINK_ROWS)):
         for rows, inp in shapes:
-            w, ks, g = aoship.decode_geometry(kind, rows, inp, T)
+            w, ks, _, g = aoship.decode_geometry(kind, rows, inp, T)
             G = inp // 64
             assert 1 <= ks <= G
             assert 128 + T * -(-G // ks) * 128 <= 32 * 1024
