@@ -53,22 +53,45 @@ SOURCES = [
 ]
 
 
-def _run(cmd: list[str]) -> None:
+# Kernels whose workgroups hand data to each other within the launch (the fused decode launches)
+# must compile without a private stack: a non-inlined device function call in one of them (which
+# forced a stack frame and one wave per SIMD) gave wrong one-token results even where the call
+# was never taken. The build fails if one of them gets private memory.
+NO_SCRATCH = ("aos_gemv_fused_kernel", "aos_route_gu_kernel", "aos_decode_mlp_kernel")
+RESOURCE_REMARKS = ["-Rpass-analysis=kernel-resource-usage"]
+
+
+def _check_resources(src: str, text: str) -> None:
+    kernel = None
+    for line in text.splitlines():
+        if "Function Name:" in line:
+            kernel = line.split("Function Name:", 1)[1].split("[-Rpass", 1)[0].strip()
+        elif "ScratchSize [bytes/lane]:" in line and kernel and any(k in kernel for k in NO_SCRATCH):
+            size = int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0])
+            if size:
+                raise SystemExit(f"build failed: {kernel} in {src} uses {size} bytes of private memory per lane")
+
+
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(" ".join(cmd) + "\n" + proc.stdout + proc.stderr)
         raise SystemExit(f"build failed: {cmd[-1]}")
-    # keep real warnings visible, drop the host pass's note about the GPU-only feature flag
-    noise = ("packed-fp32-ops", "warning generated", "warnings generated")
+    # keep real warnings visible; drop the host pass's note about the GPU-only feature flag and
+    # the resource-usage remarks (checked by _check_resources)
+    noise = ("packed-fp32-ops", "warning generated", "warnings generated", "remark", "^", "|")
     for line in (proc.stdout + proc.stderr).splitlines():
         if line.strip() and not any(n in line for n in noise):
             sys.stderr.write(line + "\n")
+    return proc.stdout + proc.stderr
 
 
 def compile_one(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
     lang = ["-x", "hip"]
-    _run([HIPCC, *lang, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    remarks = RESOURCE_REMARKS if src.endswith(".hip") else []
+    out = _run([HIPCC, *lang, *HIP_FLAGS, *remarks, "-c", str(CSRC / src), "-o", str(obj)])
+    _check_resources(src, out)
     return obj
 
 

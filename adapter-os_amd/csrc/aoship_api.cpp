@@ -1358,6 +1358,8 @@ struct MlpPlan {
   int hsum_wgs = 0;        /* workgroups summing the h shrink's partials */
   uint32_t *route_done;    /* the combined route + gate/up launch's router arrivals */
   uint32_t *route_flag;    /* ... and its routing flag */
+  uint32_t *rpart_ctr;     /* ... its per-token counts of prior workgroups */
+  float *rpri;             /* ... and the priors they hand over */
   size_t bytes = 0, ctr = 0, flg = 0;
 };
 
@@ -1439,6 +1441,8 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   P.hflags = cv.flag_lines(((size_t)P.hsum_wgs + (size_t)g2.nrbg * g2.ks) * 32);
   P.route_done = cv.counter_lines(32);
   P.route_flag = cv.flag_lines(32);
+  P.rpart_ctr = cv.counter_lines((size_t)32 * T);
+  P.rpri = cv.b.take<float>((size_t)T * AOS_ROUTE_PARTS_MAXN);
   P.ho1 = carve_handoff(cv, shrink_arrive_words(P.sx.sp), fused_flag_words(&g1, 1), shrink_lines(P.sx.sp));
   {
     /* the h shrink's or the h sum's workgroups */
@@ -1852,6 +1856,11 @@ static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const ao
     make_fused(l, w.gen, P.sx.sp, &g1, 1, P.ho1, nullptr, q.fp);
     q.route_done = P.route_done;
     q.route_flag = P.route_flag;
+    /* with up to 64 adapters each token's priors are spread over a workgroup per four adapters */
+    q.rparts = rp->n <= AOS_ROUTE_PARTS_MAXN ? (rp->n + 3) / 4 : 1;
+    if (q.rparts < 1) q.rparts = 1;
+    q.rpart_ctr = P.rpart_ctr;
+    q.rpri = P.rpri;
     aos_launch_ctx cg = launch_ctx(l, KS_GEMV_GU, w.events);
     if (launch_err(aos_launch_route_gate_up(&q, &cg), "route + lora shrink + q4 gemv gate/up")) return -1;
   } else if (fuse && P.gv1.has_expand) {

@@ -1197,12 +1197,12 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
         if (q >= n) continue;
         const unsigned char *tb = smem + q * TILE;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          u32x4 a[4];
+        for (int s = 0; s < 4; ++s) {
+          u32x4 a[MT];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) a[s] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
+          for (int mt = 0; mt < MT; ++mt) a[mt] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
 #pragma unroll
-          for (int s = 0; s < 4; ++s) acc[mt] = aos_mfma32(a[s], bv[q][s], acc[mt]);
+          for (int mt = 0; mt < MT; ++mt) acc[mt] = aos_mfma32(a[mt], bv[q][s], acc[mt]);
         }
       }
     };

@@ -344,6 +344,19 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
     if (SW && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
     if (SW && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1);
   }
+  /* a fused launch whose plan comes from an earlier launch (only S is produced here): the plan and
+   * the first step's B fragments load before the K loop, so that after it only S is waited for.
+   * Not with XL: the one-launch MLP's down GEMV reads a plan built earlier in its own launch. */
+  const bool plan_early = !XL && expands && fused && p.pre_lines != nullptr && p.plan_line < 0;
+  if (plan_early) {
+    int U = __builtin_amdgcn_readfirstlane(p.plan->U);
+    U = U < AOS_PLAN_MAXU ? U : AOS_PLAN_MAXU;
+    nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
+    nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
+    hU = U;
+    if (q_first < nq0) expand_load_b(p, p.tab0, q_first, row, lane, e0, false);
+    if (SW && q_first < nq1) expand_load_b(p, p.tab1, q_first, row, lane, e1, false);
+  }
   {
     const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
     const int GR = gw1 - gw0;
@@ -492,7 +505,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
       }
     }
     lds_barrier();
-    if (ok && expands) {
+    if (ok && expands && !plan_early) {
       int U = __builtin_amdgcn_readfirstlane(
           __hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
       U = U < AOS_PLAN_MAXU ? U : AOS_PLAN_MAXU;
@@ -506,8 +519,10 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
       h_a_load(p, rb, lane, hU, 0, hpre[0]);
       h_a_load(p, rb, lane, hU, 1, hpre[1]);
     }
-    if (q_first < nq0) expand_load_b(p, p.tab0, q_first, row, lane, e0, true);
-    if (SW && q_first < nq1) expand_load_b(p, p.tab1, q_first, row, lane, e1, true);
+    if (!plan_early) {
+      if (q_first < nq0) expand_load_b(p, p.tab0, q_first, row, lane, e0, true);
+      if (SW && q_first < nq1) expand_load_b(p, p.tab1, q_first, row, lane, e1, true);
+    }
     if (lines) {
       if (wave == 0) {
         const bool done = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);

@@ -241,11 +241,19 @@ typedef struct {
  * one token each (the plain router), then fp's producers (the x shrink; its plan workgroup waits
  * for route_flag to equal fp.gen before reading the rings) and fp.gp[0]'s gate/up GEMV
  * workgroups. */
+#define AOS_ROUTE_PARTS_MAXN 64 /* adapters up to which a token's priors are split over workgroups */
 typedef struct {
   aos_route_params rp;
   aos_gemv_fused_params fp;
   uint32_t *route_done; /* router arrivals, zero between launches (the last router resets it) */
   uint32_t *route_flag; /* raised to fp.gen by the last router, on a line of its own */
+  /* rparts > 1 (rp.n <= AOS_ROUTE_PARTS_MAXN): each token's priors are computed by rparts
+   * workgroups, one wave per adapter (workgroup r: adapters 4 r .. 4 r + 3), stored to rpri[t][a]
+   * device-coherently and counted on the token's line of rpart_ctr; the last of them routes the
+   * token. rparts == 1: one workgroup per token computes every prior and routes. */
+  int rparts;
+  uint32_t *rpart_ctr;  /* [T] lines of 32 words, zero between launches */
+  float *rpri;          /* [T][AOS_ROUTE_PARTS_MAXN] */
 } aos_route_gu_params;
 
 /* q, k and v (or any n <= 3 matrices with the same x, T and waves) in one launch: matrix i owns

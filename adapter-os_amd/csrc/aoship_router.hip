@@ -564,17 +564,68 @@ __global__ void __launch_bounds__(1024) aos_route_features_kernel(aos_route_para
  * GEMV of the layer those rings feed: the shrink does not depend on the rings, so it and the
  * weight stream run while the tokens are routed; only the adapter plan, and through it the
  * GEMV's LoRA expand, waits for them. */
+/* Part r of token t's routing in the route + gate/up launch (rparts > 1, 4 waves): wave w computes
+ * the priors of adapters 4 r + w, 4 (r + rparts) + w, ... exactly as route_features_block does
+ * (same loads, order and butterfly), stores them device-coherently and counts the workgroup in on
+ * the token's line; the last part loads the token's priors into LDS and routes it. Returns true in
+ * the workgroup that routed the token. */
+__device__ __forceinline__ bool route_part_block(const aos_route_gu_params &q, int t, int r, float *lds) {
+  const aos_route_params &p = q.rp;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int R = q.rparts;
+  float *lds_f = lds, *lds_priors = lds + p.d;
+  const int nk = p.d >> 8;
+  const int a0 = 4 * r + wave;
+  float4 wv[16];
+  if (nk > 0 && a0 < p.n) dot_load(p.router_w + (size_t)a0 * p.d, 0, nk, lane, wv);
+  RouteMeta meta = {1, 1, 0ull};
+  if (wave == 0) meta = route_meta<false>(p, lane);
+  const float4 *f4 = (const float4 *)(p.features + (size_t)t * p.d);
+  for (int e = threadIdx.x; e < p.d / 4; e += blockDim.x) ((float4 *)lds_f)[e] = f4[e];
+  __syncthreads();
+  float *pri = q.rpri + (size_t)t * AOS_ROUTE_PARTS_MAXN;
+  for (int a = a0; a < p.n; a += 4 * R) {
+    const float *wr = p.router_w + (size_t)a * p.d;
+    if (a != a0 && nk > 0) dot_load(wr, 0, nk, lane, wv);
+    const float v = dot_finish(lds_f, wr, p.d, lane, wv);
+    if (lane == 0) {
+      aos_publish(pri + a, v);
+      if (p.priors_out) p.priors_out[(size_t)t * p.n + a] = v;
+    }
+  }
+  aos_mem_wait();
+  __syncthreads();
+  uint32_t *last = (uint32_t *)(lds_priors + p.n); /* the LDS word after the priors */
+  uint32_t *ctr = q.rpart_ctr + (size_t)t * 32;
+  if (threadIdx.x == 0) {
+    *last = aos_arrive(ctr) == (uint32_t)R - 1u ? 1u : 0u;
+    if (*last) aos_reset(ctr);
+  }
+  __syncthreads();
+  if (!*last) return false;
+  for (int a = threadIdx.x; a < p.n; a += blockDim.x) lds_priors[a] = aos_collect(pri + a);
+  __syncthreads();
+  if (wave == 0) route_one<true, false>(p, lds_priors, t, lane, &meta);
+  return true;
+}
+
 template <int NV>
 __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int T = q.rp.T;
+  const int T = q.rp.T, R = q.rparts;
   const int b = blockIdx.x;
-  if (b < T) {
-    route_features_block<false>(q.rp, b, (float *)smem);
+  if (b < T * R) {
+    const int t = b / R;
+    if (R > 1) {
+      if (!route_part_block(q, t, b - t * R, (float *)smem)) return;
+    } else {
+      route_features_block<false>(q.rp, t, (float *)smem);
+    }
     /* the ring (plain stores of wave 0) is written again with device-scope stores, which the plan
      * workgroup's device-scope loads see, then counted */
     __syncthreads();
-    uint32_t *rw = (uint32_t *)(q.rp.rings + b);
+    uint32_t *rw = (uint32_t *)(q.rp.rings + t);
     if (threadIdx.x < 10) __hip_atomic_store(rw + threadIdx.x, rw[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     aos_mem_wait();
     __syncthreads();
@@ -585,7 +636,7 @@ __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q
     }
     return;
   }
-  const int b2 = b - T;
+  const int b2 = b - T * R;
   if (b2 < q.fp.n_pre) {
     aos_gemv::fused_producer<NV, 4>(q.fp, b2, smem, q.route_flag);
     return;
@@ -596,8 +647,8 @@ __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q
 
 template <int NV>
 int launch_rgu(const aos_route_gu_params *q, const aos_launch_ctx *ctx) {
-  const int nwg = q->rp.T + q->fp.n_pre + (int)q->fp.n_cons;
-  size_t lds = (size_t)(q->rp.d + q->rp.n) * sizeof(float);
+  const int nwg = q->rp.T * q->rparts + q->fp.n_pre + (int)q->fp.n_cons;
+  size_t lds = (size_t)(q->rp.d + q->rp.n + 4) * sizeof(float);
   if ((size_t)q->fp.sp.lds_bytes > lds) lds = (size_t)q->fp.sp.lds_bytes;
   if ((size_t)q->fp.gp[0].lds_bytes > lds) lds = (size_t)q->fp.gp[0].lds_bytes;
   AOS_LAUNCH(ctx, aos_route_gu_kernel<NV>, dim3(nwg), dim3(256), lds, *q);
@@ -618,6 +669,9 @@ extern "C" int aos_launch_route_gate_up(const aos_route_gu_params *q, const aos_
   if (!aos_fused_params_ok(&fp, 1) || fp.hsum || fp.gp[0].T != T || !fp.sp.plan_build.plan)
     return (int)hipErrorInvalidValue;
   if ((size_t)(q->rp.d + q->rp.n) * sizeof(float) > 60 * 1024) return (int)hipErrorInvalidValue;
+  if (q->rparts < 1 || q->rparts > 16 || (q->rparts > 1 && (q->rp.n > AOS_ROUTE_PARTS_MAXN ||
+                                                           4 * q->rparts < q->rp.n || !q->rpart_ctr || !q->rpri)))
+    return (int)hipErrorInvalidValue;
   if (T <= 1) return launch_rgu<1>(q, ctx);
   if (T <= 2) return launch_rgu<2>(q, ctx);
   if (T <= 8) return launch_rgu<4>(q, ctx);
