@@ -285,12 +285,22 @@ COPY_BYTES = 512 << 20
 
 def probe(aoship, W, torch, layers: int) -> int:
     """Workload for the hardware-counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): 50 decode
-    steps of the headline workload, then one device copy of COPY_BYTES that calibrates the
-    counters (it reads and writes exactly COPY_BYTES)."""
-    dec = MlpCase(aoship, W, 2, 1, torch, layers)
-    for _ in range(50):
-        dec.step()
+    steps of the headline workload (1 token), 50 of the 8-token batch, 48 steps of the C4
+    projections (32 streams, rings given), then one device copy of COPY_BYTES that calibrates the
+    counters (it reads and writes exactly COPY_BYTES). Each workload's launches have kernel
+    instances or grids of their own."""
+    for T in (1, 8):
+        dec = MlpCase(aoship, W, 2, T, torch, layers)
+        for _ in range(50):
+            dec.step()
+        torch.cuda.synchronize()
+        del dec
+    c4 = ProjCase(aoship, W, 4, 32, torch, 24)
+    c4.route = False
+    for _ in range(48):
+        c4.step()
     torch.cuda.synchronize()
+    del c4
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     dst.copy_(src)
