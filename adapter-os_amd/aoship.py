@@ -116,6 +116,8 @@ def lib():
         L.aoship_internal_layer_set_separate_shrinks.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_set_decode_handoff.restype = C.c_int
         L.aoship_internal_layer_set_decode_handoff.argtypes = [_P, C.c_int, C.c_int]
+        L.aoship_internal_layer_set_plan_pointers.restype = C.c_int
+        L.aoship_internal_layer_set_plan_pointers.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_set_prefill_shrink.restype = C.c_int
         L.aoship_internal_layer_set_prefill_shrink.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_last_perm.restype = C.c_int
@@ -365,6 +367,12 @@ class Layer:
         fused launches (default) instead of an arrival count with one flag per consumer."""
         _check(lib().aoship_internal_layer_set_decode_handoff(self.h, 1 if one_launch else 0, 1 if lines else 0),
                "aoship_internal_layer_set_decode_handoff")
+
+    def set_plan_pointers(self, on: bool) -> None:
+        """Diagnostic: decode plans list the LoRA tables' row pointers for their readers (default)
+        or the readers look them up through the plan's list; outputs are identical."""
+        _check(lib().aoship_internal_layer_set_plan_pointers(self.h, 1 if on else 0),
+               "aoship_internal_layer_set_plan_pointers")
 
     def set_gemv_geometry(self, kind: int, wr: int = 0, ks: int = 0) -> None:
         """Diagnostic: pin the decode GEMV geometry of launch kind 0 (gate/up), 1 (down) or 2

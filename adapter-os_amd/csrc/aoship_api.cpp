@@ -639,6 +639,7 @@ struct aoship_layer {
   bool separate_shrinks = false; /* each decode shrink in a launch of its own (diagnostic) */
   bool one_launch_mlp = false;   /* 1-2 token MLP in one launch */
   bool producer_lines = true;    /* fused launches hand over through per-producer lines */
+  bool plan_ptrs = true;         /* decode plans list the LoRA tables' row pointers */
   bool prefill_fused_shrink = true; /* prefill MLP: the LoRA shrinks run in the GEMM launches */
   /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
    * workgroup and K splits, 0 = chosen by the geometry (diagnostic) */
@@ -941,6 +942,16 @@ extern "C" int aoship_internal_layer_set_decode_handoff(aoship_layer_t *l, int o
   if (!l) return set_err("aoship_internal_layer_set_decode_handoff: null layer");
   l->one_launch_mlp = one_launch != 0;
   l->producer_lines = lines != 0;
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): whether a decode plan also lists the union's
+ * row pointers in the LoRA tables its GEMV readers use (default on: a reader then needs one load
+ * for a pointer rather than two, and a fused launch's first expand step two round trips after its
+ * wait). The loads change, the arithmetic does not: outputs are identical either way. */
+extern "C" int aoship_internal_layer_set_plan_pointers(aoship_layer_t *l, int on) {
+  if (!l) return set_err("aoship_internal_layer_set_plan_pointers: null layer");
+  l->plan_ptrs = on != 0;
   return 0;
 }
 
@@ -1345,6 +1356,18 @@ static void plan_x_shrink(aoship_layer *l, Carve &cv, const uint16_t *x, int T, 
   }
 }
 
+/* The plan build of an x shrink (in its launch, or in a launch of its own), and the tables whose
+ * row pointers the plan lists for its readers (k: the table's slot; the readers' pk = k + 1). */
+static aos_plan_params &plan_build_of(XShrink &xs) {
+  return xs.separate_plan ? xs.plan_only.plan_build : xs.sp.plan_build;
+}
+
+static int plan_list_table(const aoship_layer *l, XShrink &xs, int k, const uint16_t *const *table) {
+  if (!l->plan_ptrs) table = nullptr;
+  plan_build_of(xs).ptab[k] = table;
+  return table ? k + 1 : 0;
+}
+
 /* Plan of one decode chunk of the SwiGLU MLP. */
 struct MlpPlan {
   XShrink sx;
@@ -1393,6 +1416,9 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g1.s_stride1 = P.sx.sp.s_stride[1];
   g1.s_all = P.sx.sp.all_mode;
   g1.plan = plan;
+  g1.pk0 = plan_list_table(l, P.sx, 0, tabs_gu[0].B);
+  g1.pk1 = plan_list_table(l, P.sx, 1, tabs_gu[1].B);
+  g1.pkh = plan_list_table(l, P.sx, 2, td.A);
   g1.zero_row = l->zeros.as<uint16_t>();
   g1.y = h;
   g1.part = cv.b.take<float>((size_t)Wg.RB * g1.ks * 2 * nv_for(T) * 64);
@@ -1430,6 +1456,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   g2.s_stride0 = s2.s_stride[0];
   g2.s_all = 0;
   g2.plan = plan;
+  g2.pk0 = plan_list_table(l, P.sx, 3, td.B);
   g2.zero_row = l->zeros.as<uint16_t>();
   g2.y = y;
   g2.part = cv.b.take<float>((size_t)Wd.RB * g2.ks * nv_for(T) * 64);
@@ -2048,6 +2075,7 @@ static void plan_proj_decode(aoship_layer *l, Carve &cv, const int *mods, int nm
     gp[i].s_stride0 = Q.xs.sp.s_stride[i];
     gp[i].s_all = Q.xs.sp.all_mode;
     gp[i].plan = plan;
+    gp[i].pk0 = plan_list_table(l, Q.xs, i, tabs[i].B);
     gp[i].zero_row = l->zeros.as<uint16_t>();
     gp[i].y = yc ? yc[i] : nullptr;
     gp[i].part = cv.b.take<float>((size_t)W.RB * gp[i].ks * nv_for(Tc) * 64);

@@ -58,9 +58,22 @@ __device__ __forceinline__ float load_f(const float *a, bool coherent) {
   return coherent ? __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *a;
 }
 
+/* Row pointer of union slot u in a table the plan lists (pk = 1 + its pointer table). */
+__device__ __forceinline__ const uint16_t *plan_ptr(const aos_gemv_params &p, int pk, int u, bool coherent) {
+  const uint64_t *a = &p.plan->ptr[pk - 1][u];
+  return (const uint16_t *)(coherent ? __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *a);
+}
+
+/* Row pointer of union slot u in table T: from the plan's pointer table when it lists T (a load
+ * beside the list entry's), else through the list entry a (a load after it). */
+__device__ __forceinline__ const uint16_t *slot_ptr(const aos_gemv_params &p, const uint16_t *const *T, int pk, int u,
+                                                    int a, bool coherent) {
+  return pk ? plan_ptr(p, pk, u, coherent) : aos_gld_ptr(&T[a]);
+}
+
 /* The plan's part of step q: the adapter of union slot u, the token's coefficient and the B
- * fragment (needs the plan only). */
-__device__ __forceinline__ void expand_load_b(const aos_gemv_params &p, const aos_lora_tab &tab, int q, int row,
+ * fragment (needs the plan only). pk: the plan's pointer table of tab.B (0: none). */
+__device__ __forceinline__ void expand_load_b(const aos_gemv_params &p, const aos_lora_tab &tab, int pk, int q, int row,
                                               int lane, ExpandStep &e, bool coherent) {
   const int i = lane & 31, c = lane >> 5;
   const int ti = i < p.T ? i : 0;
@@ -70,7 +83,7 @@ __device__ __forceinline__ void expand_load_b(const aos_gemv_params &p, const ao
                          : (int)p.plan->list[u];
   e.a = a;
   e.cf = i < p.T ? load_f(&p.plan->coef[ti][u], coherent) : 0.0f;
-  const uint16_t *B = aos_gld_ptr(&tab.B[a]);
+  const uint16_t *B = slot_ptr(p, tab.B, pk, u, a, coherent);
   const uint16_t *bp = B ? B + (size_t)row * rpad + j0 + 8 * c : p.zero_row;
   e.b = aos_gld16(bp);
 }
@@ -93,11 +106,52 @@ __device__ __forceinline__ void expand_load_s(const aos_gemv_params &p, const ao
   }
 }
 
-__device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
+__device__ __forceinline__ void expand_load(const aos_gemv_params &p, const aos_lora_tab &tab, int pk, const float *S,
                                             int stride, int q, int row, int lane, ExpandStep &e,
                                             bool coherent = false) {
-  expand_load_b(p, tab, q, row, lane, e, coherent);
+  expand_load_b(p, tab, pk, q, row, lane, e, coherent);
   expand_load_s(p, tab, S, stride, q, lane, e, coherent);
+}
+
+/* Step q of a fused launch whose plan lists the B table's row pointers (pk). The table's padded
+ * rank rpad is passed by value: a reference to one of two tables of the kernel's arguments would
+ * make the compiler copy the arguments to private memory. Three parts, so that loads of one
+ * round trip go out together: the plan's part (list entry, coefficient, row pointer; slot clamped
+ * into the plan, so it loads before U is known), then the B fragment and S, which read the zero
+ * row and S's first column unless the step lies in the union (in = q < nq). */
+struct PlanPart {
+  const uint16_t *B;
+  int u, j0;
+};
+
+__device__ __forceinline__ PlanPart expand_plan_part(const aos_gemv_params &p, int rpad, int pk, int q, int lane,
+                                                     ExpandStep &e) {
+  const int i = lane & 31;
+  const int ti = i < p.T ? i : 0;
+  const int colq = 16 * q, u0 = colq / rpad;
+  PlanPart r;
+  r.j0 = colq - u0 * rpad;
+  r.u = u0 < AOS_PLAN_MAXU ? u0 : AOS_PLAN_MAXU - 1;
+  e.a = (int)__hip_atomic_load(&p.plan->list[r.u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float cf = load_f(&p.plan->coef[ti][r.u], true);
+  e.cf = i < p.T ? cf : 0.0f;
+  r.B = plan_ptr(p, pk, r.u, true);
+  return r;
+}
+
+__device__ __forceinline__ void expand_b_of(const aos_gemv_params &p, int rpad, const PlanPart &pp, bool in, int row,
+                                            int lane, ExpandStep &e) {
+  const int c = lane >> 5;
+  e.b = aos_gld16(in && pp.B ? pp.B + (size_t)row * rpad + pp.j0 + 8 * c : p.zero_row);
+}
+
+__device__ __forceinline__ void expand_s_of(const aos_gemv_params &p, int rpad, const PlanPart &pp, bool in,
+                                            const float *S, int stride, int lane, ExpandStep &e) {
+  const int i = lane & 31, c = lane >> 5;
+  const int ti = i < p.T ? i : 0;
+  const float *sp = S + (in ? (size_t)ti * stride + (p.s_all ? e.a : pp.u) * rpad + pp.j0 + 8 * c : 0);
+  e.s0 = make_float4(load_f(sp, true), load_f(sp + 1, true), load_f(sp + 2, true), load_f(sp + 3, true));
+  e.s1 = make_float4(load_f(sp + 4, true), load_f(sp + 5, true), load_f(sp + 6, true), load_f(sp + 7, true));
 }
 
 __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
@@ -111,10 +165,10 @@ __device__ __forceinline__ void expand_apply(const ExpandStep &e, f32x16 &f) {
 
 /* Steps q0, q0 + qs, ... (< nq) of one module, up to EB at a time: the loads of a batch go out
  * phase by phase (plan list, then B row pointers, then B fragments, S and coefficients), so a
- * batch costs three memory round trips rather than three per step. Steps past nq load nothing
- * (the branches are uniform). */
+ * batch costs three memory round trips rather than three per step (two when the plan lists the
+ * row pointers). Steps past nq load nothing (the branches are uniform). */
 template <int EB>
-__device__ __forceinline__ void expand_rest(const aos_gemv_params &p, const aos_lora_tab &tab, const float *S,
+__device__ __forceinline__ void expand_rest(const aos_gemv_params &p, const aos_lora_tab &tab, int pk, const float *S,
                                             int stride, int q0, int qs, int nq, int row, int lane, bool coherent,
                                             f32x16 &f) {
   const int i = lane & 31, c = lane >> 5;
@@ -137,7 +191,7 @@ __device__ __forceinline__ void expand_rest(const aos_gemv_params &p, const aos_
 #pragma unroll
     for (int k = 0; k < EB; ++k) {
       bptr[k] = nullptr;
-      if (qb + k * qs < nq) bptr[k] = aos_gld_ptr(&tab.B[a[k]]);
+      if (qb + k * qs < nq) bptr[k] = slot_ptr(p, tab.B, pk, u[k], a[k], coherent);
     }
 #pragma unroll
     for (int k = 0; k < EB; ++k) {
@@ -175,7 +229,13 @@ __device__ __forceinline__ void h_a_load(const aos_gemv_params &p, int rb, int l
   const int u = col / rpad, j = col - u * rpad;
   const uint16_t *arow = p.zero_row;
   int step = 0;
-  if (u < U) {
+  if (p.pkh) { /* the row pointer straight from the plan (slot clamped; used only below U) */
+    const uint16_t *A = plan_ptr(p, p.pkh, u < AOS_PLAN_MAXU ? u : AOS_PLAN_MAXU - 1, true);
+    if (u < U && A) {
+      arow = A + (size_t)j * in + (size_t)rb * 32 + 8 * c;
+      step = 16;
+    }
+  } else if (u < U) {
     const int aid = __hip_atomic_load(&p.plan->list[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint16_t *A = p.htab.A[aid];
     if (A) {
@@ -303,8 +363,10 @@ __device__ __forceinline__ u32x4 x_load(const uint16_t *x, size_t elem, __amdgpu
  * last group of a matrix whose row blocks wr does not divide) read the last row block and store
  * nothing. XL: x is written by earlier workgroups of this launch; the weight ring is primed
  * first, then the workgroup waits (bounded) for its line of xflag to reach p.gen and stages x
- * with device-coherent loads. */
-template <int NV, bool SW, int W, int D, bool XL = false>
+ * with device-coherent loads. DP: the direct expand loads (see (4a)) are allowed; the one-launch
+ * MLP turns them off, since in its kernel they cost the compiler's promotion of the kernel
+ * arguments to registers (the arguments would be copied to private memory). */
+template <int NV, bool SW, int W, int D, bool XL = false, bool DP = true>
 __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int ksi, const uint32_t *xflag = nullptr) {
   constexpr int NA = SW ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -341,21 +403,39 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
     const int U = __builtin_amdgcn_readfirstlane(p.plan->U);
     nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
     nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
-    if (SW && q_first < nq0) expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
-    if (SW && q_first < nq1) expand_load(p, p.tab1, p.S1, p.s_stride1, q_first, row, lane, e1);
+    if (SW && q_first < nq0) expand_load(p, p.tab0, p.pk0, p.S0, p.s_stride0, q_first, row, lane, e0);
+    if (SW && q_first < nq1) expand_load(p, p.tab1, p.pk1, p.S1, p.s_stride1, q_first, row, lane, e1);
   }
   /* a fused launch whose plan comes from an earlier launch (only S is produced here): the plan and
    * the first step's B fragments load before the K loop, so that after it only S is waited for.
    * Not with XL: the one-launch MLP's down GEMV reads a plan built earlier in its own launch. */
   const bool plan_early = !XL && expands && fused && p.pre_lines != nullptr && p.plan_line < 0;
+  /* direct: the plan lists the row pointers of every table read through it, so wave 0 waits for
+   * every producer's line at once, and the first expand step then costs two round trips (the
+   * plan's part with U, then the B fragments and S) rather than five. (Measured and not kept:
+   * waiting for the plan before the K loop, when the plan is built from rings already in memory,
+   * delays the loop by more than it saves after it.) */
+  const bool direct = DP && fused && !XL && expands && p.pre_lines != nullptr && p.pk0 != 0 &&
+                      (!SW || p.tab1.rpad == 0 || p.pk1 != 0) && (!SW || p.hpart == nullptr || p.pkh != 0);
+  /* early: this wave saw every producer's line raised during its last ring round and issued the
+   * first expand step's plan part and U (pe0, pe1, Ue) or, with the plan from an earlier launch,
+   * its S, so that after the loop it neither waits nor makes that round trip */
+  bool early = false;
+  PlanPart pe0 = {}, pe1 = {};
+  int Ue = 0;
+  /* single-matrix kernels with the direct loads: the wave's next NB steps (q_first + k q_step,
+   * k = 1 .. NB) load with its first, so that its first NB + 1 steps cost the round trips of one */
+  constexpr int NB = SW ? 0 : 3;
+  ExpandStep er[NB > 0 ? NB : 1];
+  PlanPart pr[NB > 0 ? NB : 1];
   if (plan_early) {
     int U = __builtin_amdgcn_readfirstlane(p.plan->U);
     U = U < AOS_PLAN_MAXU ? U : AOS_PLAN_MAXU;
     nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
     nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
     hU = U;
-    if (q_first < nq0) expand_load_b(p, p.tab0, q_first, row, lane, e0, false);
-    if (SW && q_first < nq1) expand_load_b(p, p.tab1, q_first, row, lane, e1, false);
+    if (q_first < nq0) expand_load_b(p, p.tab0, p.pk0, q_first, row, lane, e0, false);
+    if (SW && q_first < nq1) expand_load_b(p, p.tab1, p.pk1, q_first, row, lane, e1, false);
   }
   {
     const int gw0 = (int)((long)ksi * G / p.ks), gw1 = (int)((long)(ksi + 1) * G / p.ks);
@@ -450,7 +530,30 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
      * their row, the others stay on the zero block. */
     const int xbase = i < T ? 128 + i * xstride * 2 + 64 * c : 0;
     const int xmult = i < T ? 128 : 0;
+    /* direct: one poll of the producers' lines at the top of the second-to-last ring round, read
+     * at the top of the last (by then it has returned); if every line is raised, the first
+     * expand step's first round trip goes out during the last round */
+    const int last_base = ng > 0 ? ((ng - 1) / D) * D : 0;
+    constexpr bool EARLY_OK = !SW || NV == 1; /* its registers cost the SwiGLU kernels of 2-4 tokens a wave per SIMD */
+    const bool try_early = EARLY_OK && direct && p.n_pre_lines <= 64 && last_base >= D;
+    uint32_t pv = p.gen;
     for (int base = 0; base < ng; base += D) {
+      if (try_early && base == last_base - D)
+        pv = lane < p.n_pre_lines
+                 ? __hip_atomic_load(p.pre_lines + (size_t)lane * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                 : p.gen;
+      if (try_early && base == last_base && __ballot(pv != p.gen) == 0ull) {
+        aos_compiler_barrier();
+        early = true;
+        if (!plan_early) {
+          if (p.tab0.rpad) pe0 = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first, lane, e0);
+          if (SW && p.tab1.rpad) pe1 = expand_plan_part(p, p.tab1.rpad, p.pk1, q_first, lane, e1);
+          Ue = (int)__hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          if (q_first < nq0) expand_load_s(p, p.tab0, p.S0, p.s_stride0, q_first, lane, e0, true);
+          if (SW && q_first < nq1) expand_load_s(p, p.tab1, p.S1, p.s_stride1, q_first, lane, e1, true);
+        }
+      }
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         const int j = base + d;
@@ -489,7 +592,79 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
    * The waits are bounded: past about a second they give up, set p.timeout and the workgroup
    * finishes without the expand or the h shrink; the call's output is then invalid and the layer
    * reports the timeout. */
-  if (fused) {
+  if (fused && direct) {
+    /* each wave on its own: the wait (unless it saw the lines during its last round), then the
+     * loads after it */
+    bool ready = early;
+    if (!ready) {
+      ready = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
+      if (!ready && lane == 0 && p.timeout)
+        __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    if (!ready) {
+      nq0 = 0;
+      nq1 = 0;
+      hU = 0;
+    } else if (!plan_early) {
+      /* round trip 1 (unless issued early): the plan's parts and U (kept per lane, so that nothing
+       * waits for it before the other loads go out); round trip 2: the B fragments, S, and the
+       * h shrink's A_down pointers and fragments */
+      if (!early) {
+        if (p.tab0.rpad) pe0 = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first, lane, e0);
+        if (SW && p.tab1.rpad) pe1 = expand_plan_part(p, p.tab1.rpad, p.pk1, q_first, lane, e1);
+        Ue = (int)__hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (p.tab0.rpad)
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+          pr[k] = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first + (k + 1) * q_step, lane, er[k]);
+      const int Uv = Ue < AOS_PLAN_MAXU ? Ue : AOS_PLAN_MAXU;
+      if (SW && p.hpart && wave == 0) {
+        h_a_load(p, rb, lane, Uv, 0, hpre[0]);
+        h_a_load(p, rb, lane, Uv, 1, hpre[1]);
+      }
+      if (p.tab0.rpad) {
+        const int nq = Uv * p.tab0.rpad / 16;
+        expand_b_of(p, p.tab0.rpad, pe0, q_first < nq, row, lane, e0);
+        expand_s_of(p, p.tab0.rpad, pe0, q_first < nq, p.S0, p.s_stride0, lane, e0);
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+          const bool in = q_first + (k + 1) * q_step < nq;
+          expand_b_of(p, p.tab0.rpad, pr[k], in, row, lane, er[k]);
+          expand_s_of(p, p.tab0.rpad, pr[k], in, p.S0, p.s_stride0, lane, er[k]);
+        }
+      }
+      if (SW && p.tab1.rpad) {
+        const bool in = q_first < Uv * p.tab1.rpad / 16;
+        expand_b_of(p, p.tab1.rpad, pe1, in, row, lane, e1);
+        expand_s_of(p, p.tab1.rpad, pe1, in, p.S1, p.s_stride1, lane, e1);
+      }
+      const int U = __builtin_amdgcn_readfirstlane(Uv);
+      nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
+      nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
+      hU = U;
+    } else { /* plan and B fragments loaded before the K loop */
+      if (SW && p.hpart && wave == 0) {
+        h_a_load(p, rb, lane, hU, 0, hpre[0]);
+        h_a_load(p, rb, lane, hU, 1, hpre[1]);
+      }
+      if (!early) {
+        if (q_first < nq0) expand_load_s(p, p.tab0, p.S0, p.s_stride0, q_first, lane, e0, true);
+        if (SW && q_first < nq1) expand_load_s(p, p.tab1, p.S1, p.s_stride1, q_first, lane, e1, true);
+      }
+      if (p.tab0.rpad && q_first + q_step < nq0) { /* the next steps: plan parts, then B and S */
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+          pr[k] = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first + (k + 1) * q_step, lane, er[k]);
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+          const bool in = q_first + (k + 1) * q_step < nq0;
+          expand_b_of(p, p.tab0.rpad, pr[k], in, row, lane, er[k]);
+          expand_s_of(p, p.tab0.rpad, pr[k], in, p.S0, p.s_stride0, lane, er[k]);
+        }
+      }
+    }
+  } else if (fused) {
     __shared__ uint32_t ok, ok2;
     const bool lines = p.pre_lines != nullptr;
     if (wave == 0) {
@@ -520,8 +695,8 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
       h_a_load(p, rb, lane, hU, 1, hpre[1]);
     }
     if (!plan_early) {
-      if (q_first < nq0) expand_load_b(p, p.tab0, q_first, row, lane, e0, true);
-      if (SW && q_first < nq1) expand_load_b(p, p.tab1, q_first, row, lane, e1, true);
+      if (q_first < nq0) expand_load_b(p, p.tab0, p.pk0, q_first, row, lane, e0, true);
+      if (SW && q_first < nq1) expand_load_b(p, p.tab1, p.pk1, q_first, row, lane, e1, true);
     }
     if (lines) {
       if (wave == 0) {
@@ -543,18 +718,25 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
   /* (4b) the expand, added to the waves' accumulators */
   if (expands) {
     f32x16 f0 = {}, f1 = {};
-    if (fused) {
+    if (direct) {
+      /* loaded above */
+    } else if (fused) {
       if (q_first < nq0) expand_load_s(p, p.tab0, p.S0, p.s_stride0, q_first, lane, e0, true);
       if (SW && q_first < nq1) expand_load_s(p, p.tab1, p.S1, p.s_stride1, q_first, lane, e1, true);
     } else if (!SW && q_first < nq0) {
-      expand_load(p, p.tab0, p.S0, p.s_stride0, q_first, row, lane, e0);
+      expand_load(p, p.tab0, p.pk0, p.S0, p.s_stride0, q_first, row, lane, e0);
     }
     if (q_first < nq0) expand_apply(e0, f0);
     if (SW && q_first < nq1) expand_apply(e1, f1);
-    if (q_first + q_step < nq0)
-      expand_rest<4>(p, p.tab0, p.S0, p.s_stride0, q_first + q_step, q_step, nq0, row, lane, fused, f0);
+    const int nb = direct ? NB : 0; /* steps after the first already loaded */
+#pragma unroll
+    for (int k = 0; k < NB; ++k)
+      if (k < nb && q_first + (k + 1) * q_step < nq0) expand_apply(er[k], f0);
+    if (q_first + (nb + 1) * q_step < nq0)
+      expand_rest<4>(p, p.tab0, p.pk0, p.S0, p.s_stride0, q_first + (nb + 1) * q_step, q_step, nq0, row, lane, fused,
+                     f0);
     if (SW && q_first + q_step < nq1)
-      expand_rest<4>(p, p.tab1, p.S1, p.s_stride1, q_first + q_step, q_step, nq1, row, lane, fused, f1);
+      expand_rest<4>(p, p.tab1, p.pk1, p.S1, p.s_stride1, q_first + q_step, q_step, nq1, row, lane, fused, f1);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       acc0[v] += f0[v];

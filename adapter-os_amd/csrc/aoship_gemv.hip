@@ -63,16 +63,17 @@ __global__ void __launch_bounds__(64 * W) aos_gemv_fused_kernel(aos_gemv_fused_p
     fused_producer<NV, W>(fp, b, smem, nullptr);
     return;
   }
-  const int r = b - fp.n_pre;
-  if (SW || r < fp.wg_end[0]) {
-    gemv_body<NV, SW, W, D>(fp.gp[0], r % fp.gp[0].nrbg, r / fp.gp[0].nrbg);
-  } else if (r < fp.wg_end[1]) {
-    const int r1 = r - fp.wg_end[0];
-    gemv_body<NV, false, W, D>(fp.gp[1], r1 % fp.gp[1].nrbg, r1 / fp.gp[1].nrbg);
-  } else {
-    const int r2 = r - fp.wg_end[1];
-    gemv_body<NV, false, W, D>(fp.gp[2], r2 % fp.gp[2].nrbg, r2 / fp.gp[2].nrbg);
+  int r = b - fp.n_pre, m = 0;
+  if (!SW && r >= fp.wg_end[0]) {
+    m = r < fp.wg_end[1] ? 1 : 2;
+    r -= fp.wg_end[m - 1];
   }
+  /* matrix m's parameters read in place from the argument segment (fp is its first and only
+   * argument): one call site for the three matrices */
+  const aos_gemv_params &g = *(const aos_gemv_params *)((const char *)__builtin_amdgcn_kernarg_segment_ptr() +
+                                                        offsetof(aos_gemv_fused_params, gp) +
+                                                        (size_t)m * sizeof(aos_gemv_params));
+  gemv_body<NV, SW, W, D>(g, r % g.nrbg, r / g.nrbg);
 }
 
 /* The decode MLP of 1-2 tokens in one launch (4-wave workgroups throughout):
@@ -101,7 +102,7 @@ __global__ void __launch_bounds__(256) aos_decode_mlp_kernel(aos_decode_mlp_para
   }
   b -= gu.n_pre;
   if (b < (int)gu.n_cons) {
-    gemv_body<NV, true, 4, AOS_MLP_GU_RING>(gu.gp[0], b % gu.gp[0].nrbg, b / gu.gp[0].nrbg);
+    gemv_body<NV, true, 4, AOS_MLP_GU_RING, false, false>(gu.gp[0], b % gu.gp[0].nrbg, b / gu.gp[0].nrbg);
     return;
   }
   b -= (int)gu.n_cons;

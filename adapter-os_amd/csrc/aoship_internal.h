@@ -63,14 +63,19 @@ typedef struct {
 } aos_lora_tab;
 
 /* Adapter plan of one layer call (T <= 32 tokens), built once from the rings:
- * the union of adapters used by the tokens (ascending index) and each token's coefficient
- * scale * q / 32767 for each adapter of the union (0 when the token does not use it). */
+ * the union of adapters used by the tokens (ascending index), each token's coefficient
+ * scale * q / 32767 for each adapter of the union (0 when the token does not use it), and, for
+ * up to AOS_PLAN_NPTR pointer tables named at the build, the union's row pointers in each
+ * (ptr[k][u] = table_k[list[u]], so that a reader needs one load rather than two dependent ones).
+ * Entries at u >= U are stale. */
 #define AOS_PLAN_MAXU 256
+#define AOS_PLAN_NPTR 4
 typedef struct {
   int U;
   int pad[3];
   uint16_t list[AOS_PLAN_MAXU];
   float coef[AOS_DECODE_MAX_T][AOS_PLAN_MAXU];
+  uint64_t ptr[AOS_PLAN_NPTR][AOS_PLAN_MAXU];
 } aos_plan;
 
 typedef struct {
@@ -80,6 +85,8 @@ typedef struct {
   const uint8_t *bound;  /* [n] 1 = adapter bound for this layer */
   const float *scale;    /* [n] */
   aos_plan *plan;
+  const uint16_t *const *ptab[AOS_PLAN_NPTR]; /* device pointer tables [n] listed per union slot
+                                                 into plan->ptr (NULL: not listed) */
 } aos_plan_params;
 
 /* ---- router ---- */
@@ -153,6 +160,8 @@ typedef struct {
   int s_stride0, s_stride1;
   int s_all;              /* 1: S columns indexed by adapter, 0: by union slot */
   const aos_plan *plan;
+  int pk0, pk1, pkh;      /* 1 + the plan's pointer table listing tab0.B, tab1.B, htab.A rows
+                           * (0: looked up through plan->list and the table) */
   const uint16_t *zero_row;
   /* outputs */
   uint16_t *y;        /* [T][out] bf16 (plain) or h (SwiGLU) */

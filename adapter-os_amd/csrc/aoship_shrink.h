@@ -37,7 +37,7 @@ __device__ __forceinline__ void lds_barrier() {
  * (backend.rs:409-425 skips q <= 0 and unknown handles). coef[t][u] = sum over such slots of
  * scale[a] * (float(q) / 32767.0f), the product mod.scale * blend_weights[i] of the MLX
  * forward. */
-__device__ void build_plan(const aos_plan_params &pp) {
+__device__ __forceinline__ void build_plan(const aos_plan_params &pp) {
   __shared__ uint32_t bits[AOS_MAX_ADAPTERS / 32];
   __shared__ uint16_t list[AOS_PLAN_MAXU];
   __shared__ int cntU;
@@ -74,6 +74,16 @@ __device__ void build_plan(const aos_plan_params &pp) {
   }
   __syncthreads();
   const int U = cntU;
+  /* the union's row pointers in the listed tables: thread tid's entries (slot tid of each
+   * table) load here and are stored after the coefficients; slots past the threads loop at the
+   * end. Tables are indexed by constants only (a variable index would copy the kernel's
+   * arguments to private memory). */
+  uint64_t pv[AOS_PLAN_NPTR];
+#pragma unroll
+  for (int k = 0; k < AOS_PLAN_NPTR; ++k) {
+    pv[k] = 0;
+    if (tid < U && pp.ptab[k]) pv[k] = (uint64_t)aos_gld_ptr(pp.ptab[k] + list[tid]);
+  }
   for (int idx = tid; idx < pp.T * U; idx += nt) {
     const int t = idx / U, u = idx - t * U;
     const int a = list[u];
@@ -87,6 +97,14 @@ __device__ void build_plan(const aos_plan_params &pp) {
     }
     aos_publish(&pp.plan->coef[t][u], c);
   }
+#pragma unroll
+  for (int k = 0; k < AOS_PLAN_NPTR; ++k) {
+    if (!pp.ptab[k]) continue;
+    if (tid < U) __hip_atomic_store(&pp.plan->ptr[k][tid], pv[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int u = tid + nt; u < U; u += nt)
+      __hip_atomic_store(&pp.plan->ptr[k][u], (uint64_t)aos_gld_ptr(pp.ptab[k] + list[u]), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 /* Row blocks of 32 over the modules' rank rows. */
@@ -99,7 +117,7 @@ __device__ __forceinline__ int shrink_rows(const aos_shrink_params &p) {
  * block (the one that stored its S, or split 0 of a row block with nothing to compute, or of the
  * plan), false elsewhere. */
 template <int NV, int W, int D>
-__device__ bool shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsigned char *smem) {
+__device__ __forceinline__ bool shrink_block(const aos_shrink_params &p, int lrb, int ksi, unsigned char *smem) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rb_total = shrink_rows(p);

@@ -89,6 +89,54 @@ def test_mlp_decode_handoff_variants(hip, T, one_launch, lines):
     assert np.array_equal(_run_mlp(hip, layer, xb, rings), default)
 
 
+@pytest.mark.parametrize("T", [1, 2, 8, 32])
+def test_decode_plan_pointer_lists(hip, T):
+    """The decode plan lists the union's row pointers in the LoRA tables (default), so a fused
+    launch's first expand step loads in two round trips after its wait; without the lists each
+    reader looks the pointers up through the plan's adapter list. Only the order of the loads
+    changes: the MLP and the q/k/v and o projections are identical either way, within tolerance of
+    the oracle, and leave no timed-out wait."""
+    import torch
+
+    cid = 2
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    on = _run_mlp(hip, layer, xb, rings)
+    layer.set_plan_pointers(False)
+    off = _run_mlp(hip, layer, xb, rings)
+    layer.set_plan_pointers(True)
+    assert layer.wait_timeouts() == 0
+    assert np.array_equal(on, off), "MLP outputs differ with and without the plan's pointer lists"
+    ref = oracle_mlp(cid, xf, rings)
+    assert tol_ratio(W.bf16_bits_to_f32(on).reshape(ref.shape), ref) <= REL_TOL
+
+    cid = 4
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    x = _dev(xb.view(np.int16))
+    r = _dev(rings.view(np.uint8))
+    outs = []
+    for lists in (True, False):
+        layer.set_plan_pointers(lists)
+        q = torch.empty((T, cfg.q_out), dtype=torch.int16, device="cuda")
+        k = torch.empty((T, cfg.kv_out), dtype=torch.int16, device="cuda")
+        v = torch.empty((T, cfg.kv_out), dtype=torch.int16, device="cuda")
+        o = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
+        layer.qkv_forward(x, r, q, k, v)
+        layer.proj_forward("o_proj", x, r, o)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy().view(np.uint16) for t in (q, k, v, o)])
+    layer.set_plan_pointers(True)
+    assert layer.wait_timeouts() == 0
+    for name, a, b in zip(cfg.modules, outs[0], outs[1]):
+        assert np.array_equal(a, b), f"{name}: outputs differ with and without the plan's pointer lists"
+        ref = oracle_proj(cid, name, xf, rings)
+        assert tol_ratio(W.bf16_bits_to_f32(a).reshape(ref.shape), ref) <= REL_TOL, name
+
+
 def test_mlp_no_adapters_matches_base(hip):
     """Zero gates / empty rings: the layer is the plain int4 SwiGLU MLP."""
     cid, T = 1, 4
