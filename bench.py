@@ -285,12 +285,14 @@ COPY_BYTES = 512 << 20
 
 def probe(aoship, W, torch, layers: int) -> int:
     """Workload for the hardware-counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): 50 decode
-    steps of the headline workload (1 token), 50 of the 8-token batch, 48 steps of the C4
+    steps of the headline workload (1 token, one aoship_route_mlp_forward call per step), 50 of the
+    same token as two calls (route, then the MLP), 50 of the 8-token batch, 48 steps of the C4
     projections (32 streams, rings given), then one device copy of COPY_BYTES that calibrates the
     counters (it reads and writes exactly COPY_BYTES). Each workload's launches have kernel
     instances or grids of their own."""
-    for T in (1, 8):
+    for T, combined in ((1, True), (1, False), (8, False)):
         dec = MlpCase(aoship, W, 2, T, torch, layers)
+        dec.combined = combined
         for _ in range(50):
             dec.step()
         torch.cuda.synchronize()
@@ -586,9 +588,10 @@ def main() -> int:
     # ---- headline: 7B-shaped decode, one token ----
     T = 1
     dec = MlpCase(aoship, W, 2, T, torch, args.layers)
-    dec.combined = FUSED  # one call: the router runs inside the gate/up launch
-    ms_comb = time_steps(dec, args.steps, args.warmup, torch)
-    dec.combined = False  # route, then the layer: two calls (the headline; its launches are profiled)
+    dec.combined = False  # route, then the layer: two calls
+    ms_two = time_steps(dec, args.steps, args.warmup, torch)
+    kt_two = kernel_times(dec, max(20, args.steps // 4), torch)
+    dec.combined = FUSED  # the headline: one call, the router inside the gate/up launch
     ms = time_steps(dec, args.steps, args.warmup, torch)
     U = dec.distinct_adapters(aoship)
     kt = kernel_times(dec, max(20, args.steps // 4), torch)
@@ -605,7 +608,10 @@ def main() -> int:
         gu_ms = kt["q4_gemv_gate_up"]
         # with the router in the launch: its weights and the token's features as well
         gu_bytes = gate_up_bytes(cfg, T, U) + (cfg.n_adapters + T) * cfg.hidden * 4 * dec.combined
-        rl_kernel = ("lora_shrink_x+q4_gemv_gate_up (one launch: the LoRA x shrink in its first workgroups, "
+        rl_kernel = ("route+lora_shrink_x+q4_gemv_gate_up (one launch: the router's workgroups, the adapter plan "
+                     "and the LoRA x shrink in its first workgroups, then the int4 gate+up GEMV with the LoRA "
+                     "expand and SwiGLU)" if dec.combined else
+                     "lora_shrink_x+q4_gemv_gate_up (one launch: the LoRA x shrink in its first workgroups, "
                      "then the int4 gate+up GEMV with the LoRA expand and SwiGLU)")
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
     kl = launch_names(kt, dec.combined)
@@ -627,7 +633,8 @@ def main() -> int:
         "config": {
             "workload": "Qwen2.5-7B-shaped int4 (g64) SwiGLU MLP, 16 rank-16 LoRA adapters on gate/up/down, "
                         "K=4 Q15 router over 3584-dim features, decode of 1 token; each step routes the token "
-                        "and runs the next of %d distinct layer copies" % args.layers,
+                        "and runs the next of %d distinct layer copies, both in one aoship_route_mlp_forward "
+                        "call" % args.layers,
             "hidden": cfg.hidden, "intermediate": cfg.inter, "tokens": T, "adapters": cfg.n_adapters,
             "rank": cfg.rank, "k": cfg.k, "layers_cycled": args.layers,
         },
@@ -644,10 +651,11 @@ def main() -> int:
             "avg_launch_us": gu_ms * 1e3,
         },
         "kernels_us": {k: v * 1e3 for k, v in kl.items()},
-        "decode_t1_one_call": {"ms_per_step": ms_comb, "tok_s": T / (ms_comb * 1e-3),
-                               "note": "aoship_route_mlp_forward: the router inside the gate/up launch"},
+        "decode_t1_two_calls": {"ms_per_step": ms_two, "tok_s": T / (ms_two * 1e-3),
+                                "kernels_us": {k: v * 1e3 for k, v in launch_names(kt_two).items()},
+                                "note": "the router's launch, then aoship_mlp_forward"},
     }
-    log(f"decode T=1 as one call (aoship_route_mlp_forward): {ms_comb * 1e3:.1f} us/step")
+    log(f"decode T=1 as two calls (route, then aoship_mlp_forward): {ms_two * 1e3:.1f} us/step")
     del dec
 
     # ---- 8-token decode batch ----
