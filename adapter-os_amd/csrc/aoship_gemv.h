@@ -357,6 +357,19 @@ __device__ __forceinline__ u32x4 x_load(const uint16_t *x, size_t elem, __amdgpu
   return *(const u32x4 *)(x + elem);
 }
 
+/* One poll of n producer lines (lane l reads lines l, l + 64, ...): true if every line equals gen.
+ * Loads issued after it (and depending on its result) are not moved above it. */
+__device__ __forceinline__ bool poll_lines_once(const uint32_t *lines, int n, uint32_t gen, int lane) {
+  bool all = true;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const uint32_t v = i < n ? __hip_atomic_load(lines + (size_t)i * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : gen;
+    all = all && __ballot(v != gen) == 0ull;
+  }
+  aos_compiler_barrier();
+  return all;
+}
+
 /* Row-block group rbg, K split ksi of one matrix (or of the gate/up pair): the workgroup's waves
  * cover p.wr row blocks (wave w: row block p.wr * rbg + w % p.wr, K piece w / p.wr of the split),
  * all reading the one x slice staged for the split. Waves of a row block past the matrix (the
@@ -417,15 +430,9 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
    * delays the loop by more than it saves after it.) */
   const bool direct = DP && fused && !XL && expands && p.pre_lines != nullptr && p.pk0 != 0 &&
                       (!SW || p.tab1.rpad == 0 || p.pk1 != 0) && (!SW || p.hpart == nullptr || p.pkh != 0);
-  /* early: this wave saw every producer's line raised during its last ring round and issued the
-   * first expand step's plan part and U (pe0, pe1, Ue) or, with the plan from an earlier launch,
-   * its S, so that after the loop it neither waits nor makes that round trip */
-  bool early = false;
-  PlanPart pe0 = {}, pe1 = {};
-  int Ue = 0;
   /* single-matrix kernels with the direct loads: the wave's next NB steps (q_first + k q_step,
    * k = 1 .. NB) load with its first, so that its first NB + 1 steps cost the round trips of one */
-  constexpr int NB = SW ? 0 : 3;
+  constexpr int NB = (SW || NV == 1) ? 0 : 3;
   ExpandStep er[NB > 0 ? NB : 1];
   PlanPart pr[NB > 0 ? NB : 1];
   if (plan_early) {
@@ -530,30 +537,7 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
      * their row, the others stay on the zero block. */
     const int xbase = i < T ? 128 + i * xstride * 2 + 64 * c : 0;
     const int xmult = i < T ? 128 : 0;
-    /* direct: one poll of the producers' lines at the top of the second-to-last ring round, read
-     * at the top of the last (by then it has returned); if every line is raised, the first
-     * expand step's first round trip goes out during the last round */
-    const int last_base = ng > 0 ? ((ng - 1) / D) * D : 0;
-    constexpr bool EARLY_OK = !SW || NV == 1; /* its registers cost the SwiGLU kernels of 2-4 tokens a wave per SIMD */
-    const bool try_early = EARLY_OK && direct && p.n_pre_lines <= 64 && last_base >= D;
-    uint32_t pv = p.gen;
     for (int base = 0; base < ng; base += D) {
-      if (try_early && base == last_base - D)
-        pv = lane < p.n_pre_lines
-                 ? __hip_atomic_load(p.pre_lines + (size_t)lane * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                 : p.gen;
-      if (try_early && base == last_base && __ballot(pv != p.gen) == 0ull) {
-        aos_compiler_barrier();
-        early = true;
-        if (!plan_early) {
-          if (p.tab0.rpad) pe0 = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first, lane, e0);
-          if (SW && p.tab1.rpad) pe1 = expand_plan_part(p, p.tab1.rpad, p.pk1, q_first, lane, e1);
-          Ue = (int)__hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          if (q_first < nq0) expand_load_s(p, p.tab0, p.S0, p.s_stride0, q_first, lane, e0, true);
-          if (SW && q_first < nq1) expand_load_s(p, p.tab1, p.S1, p.s_stride1, q_first, lane, e1, true);
-        }
-      }
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         const int j = base + d;
@@ -593,74 +577,85 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
    * finishes without the expand or the h shrink; the call's output is then invalid and the layer
    * reports the timeout. */
   if (fused && direct) {
-    /* each wave on its own: the wait (unless it saw the lines during its last round), then the
-     * loads after it */
-    bool ready = early;
-    if (!ready) {
-      ready = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
-      if (!ready && lane == 0 && p.timeout)
-        __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    if (!ready) {
-      nq0 = 0;
-      nq1 = 0;
-      hU = 0;
-    } else if (!plan_early) {
-      /* round trip 1 (unless issued early): the plan's parts and U (kept per lane, so that nothing
-       * waits for it before the other loads go out); round trip 2: the B fragments, S, and the
-       * h shrink's A_down pointers and fragments */
-      if (!early) {
-        if (p.tab0.rpad) pe0 = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first, lane, e0);
+    /* each wave on its own. Plan built by this launch: one poll of every producer line; if all are
+     * up, round trip 1 (the plan's parts and U, kept per lane so that nothing waits for it before
+     * the other loads go out) and round trip 2 (the B fragments, S, the h shrink's A_down pointers
+     * and fragments) follow at once; if not, the wave waits for the plan's line, loads the plan's
+     * parts and the B fragments, and only then waits for the other lines and loads S (the B loads
+     * then overlap the shrink's tail). Plan from an earlier launch: wait, then S. */
+    if (!plan_early) {
+      const bool all_up = poll_lines_once(p.pre_lines, p.n_pre_lines, p.gen, lane);
+      bool ready = all_up || aos_wait_lines(p.pre_lines + (size_t)p.plan_line * 32, 1, p.gen, lane);
+      PlanPart pe0 = {}, pe1 = {};
+      int Ue = 0;
+      if (ready) {
+        if (p.tab0.rpad) {
+          pe0 = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first, lane, e0);
+#pragma unroll
+          for (int k = 0; k < NB; ++k)
+            pr[k] = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first + (k + 1) * q_step, lane, er[k]);
+        }
         if (SW && p.tab1.rpad) pe1 = expand_plan_part(p, p.tab1.rpad, p.pk1, q_first, lane, e1);
         Ue = (int)__hip_atomic_load(&p.plan->U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (p.tab0.rpad)
-#pragma unroll
-        for (int k = 0; k < NB; ++k)
-          pr[k] = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first + (k + 1) * q_step, lane, er[k]);
-      const int Uv = Ue < AOS_PLAN_MAXU ? Ue : AOS_PLAN_MAXU;
-      if (SW && p.hpart && wave == 0) {
-        h_a_load(p, rb, lane, Uv, 0, hpre[0]);
-        h_a_load(p, rb, lane, Uv, 1, hpre[1]);
-      }
-      if (p.tab0.rpad) {
-        const int nq = Uv * p.tab0.rpad / 16;
-        expand_b_of(p, p.tab0.rpad, pe0, q_first < nq, row, lane, e0);
-        expand_s_of(p, p.tab0.rpad, pe0, q_first < nq, p.S0, p.s_stride0, lane, e0);
-#pragma unroll
-        for (int k = 0; k < NB; ++k) {
-          const bool in = q_first + (k + 1) * q_step < nq;
-          expand_b_of(p, p.tab0.rpad, pr[k], in, row, lane, er[k]);
-          expand_s_of(p, p.tab0.rpad, pr[k], in, p.S0, p.s_stride0, lane, er[k]);
+        Ue = Ue < AOS_PLAN_MAXU ? Ue : AOS_PLAN_MAXU;
+        if (SW && p.hpart && wave == 0) {
+          h_a_load(p, rb, lane, Ue, 0, hpre[0]);
+          h_a_load(p, rb, lane, Ue, 1, hpre[1]);
         }
+        if (p.tab0.rpad) {
+          const int nq = Ue * p.tab0.rpad / 16;
+          expand_b_of(p, p.tab0.rpad, pe0, q_first < nq, row, lane, e0);
+#pragma unroll
+          for (int k = 0; k < NB; ++k)
+            expand_b_of(p, p.tab0.rpad, pr[k], q_first + (k + 1) * q_step < nq, row, lane, er[k]);
+        }
+        if (SW && p.tab1.rpad) expand_b_of(p, p.tab1.rpad, pe1, q_first < Ue * p.tab1.rpad / 16, row, lane, e1);
+        if (!all_up) ready = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
       }
-      if (SW && p.tab1.rpad) {
-        const bool in = q_first < Uv * p.tab1.rpad / 16;
-        expand_b_of(p, p.tab1.rpad, pe1, in, row, lane, e1);
-        expand_s_of(p, p.tab1.rpad, pe1, in, p.S1, p.s_stride1, lane, e1);
+      if (ready) {
+        if (p.tab0.rpad) {
+          const int nq = Ue * p.tab0.rpad / 16;
+          expand_s_of(p, p.tab0.rpad, pe0, q_first < nq, p.S0, p.s_stride0, lane, e0);
+#pragma unroll
+          for (int k = 0; k < NB; ++k)
+            expand_s_of(p, p.tab0.rpad, pr[k], q_first + (k + 1) * q_step < nq, p.S0, p.s_stride0, lane, er[k]);
+        }
+        if (SW && p.tab1.rpad)
+          expand_s_of(p, p.tab1.rpad, pe1, q_first < Ue * p.tab1.rpad / 16, p.S1, p.s_stride1, lane, e1);
+        const int U = __builtin_amdgcn_readfirstlane(Ue);
+        nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
+        nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
+        hU = U;
+      } else {
+        if (lane == 0 && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        nq0 = 0;
+        nq1 = 0;
+        hU = 0;
       }
-      const int U = __builtin_amdgcn_readfirstlane(Uv);
-      nq0 = p.tab0.rpad ? U * p.tab0.rpad / 16 : 0;
-      nq1 = (SW && p.tab1.rpad) ? U * p.tab1.rpad / 16 : 0;
-      hU = U;
-    } else { /* plan and B fragments loaded before the K loop */
-      if (SW && p.hpart && wave == 0) {
-        h_a_load(p, rb, lane, hU, 0, hpre[0]);
-        h_a_load(p, rb, lane, hU, 1, hpre[1]);
-      }
-      if (!early) {
+    } else { /* plan and the first step's B fragments loaded before the K loop */
+      const bool ready = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
+      if (!ready) {
+        if (lane == 0 && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        nq0 = 0;
+        nq1 = 0;
+        hU = 0;
+      } else {
+        if (SW && p.hpart && wave == 0) {
+          h_a_load(p, rb, lane, hU, 0, hpre[0]);
+          h_a_load(p, rb, lane, hU, 1, hpre[1]);
+        }
         if (q_first < nq0) expand_load_s(p, p.tab0, p.S0, p.s_stride0, q_first, lane, e0, true);
         if (SW && q_first < nq1) expand_load_s(p, p.tab1, p.S1, p.s_stride1, q_first, lane, e1, true);
-      }
-      if (p.tab0.rpad && q_first + q_step < nq0) { /* the next steps: plan parts, then B and S */
+        if (p.tab0.rpad && q_first + q_step < nq0) { /* the next steps: plan parts, then B and S */
 #pragma unroll
-        for (int k = 0; k < NB; ++k)
-          pr[k] = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first + (k + 1) * q_step, lane, er[k]);
+          for (int k = 0; k < NB; ++k)
+            pr[k] = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first + (k + 1) * q_step, lane, er[k]);
 #pragma unroll
-        for (int k = 0; k < NB; ++k) {
-          const bool in = q_first + (k + 1) * q_step < nq0;
-          expand_b_of(p, p.tab0.rpad, pr[k], in, row, lane, er[k]);
-          expand_s_of(p, p.tab0.rpad, pr[k], in, p.S0, p.s_stride0, lane, er[k]);
+          for (int k = 0; k < NB; ++k) {
+            const bool in = q_first + (k + 1) * q_step < nq0;
+            expand_b_of(p, p.tab0.rpad, pr[k], in, row, lane, er[k]);
+            expand_s_of(p, p.tab0.rpad, pr[k], in, p.S0, p.s_stride0, lane, er[k]);
+          }
         }
       }
     }
