@@ -610,34 +610,64 @@ __device__ __forceinline__ bool route_part_block(const aos_route_gu_params &q, i
   return true;
 }
 
+/* LDS offset of the plan's staged tables in a router workgroup: after the features, the priors and
+ * the arrival word */
+__host__ __device__ constexpr size_t rgu_tabs_off(int d, int n) { return ((size_t)(d + n + 4) * 4 + 15) & ~(size_t)15; }
+
 template <int NV>
 __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int T = q.rp.T, R = q.rparts;
   const int b = blockIdx.x;
+  /* with per-producer lines and at most AOS_PLAN_TABS_N adapters (the split router), the router
+   * that finishes the last token builds the plan itself and raises the plan workgroup's line; the
+   * plan workgroup then stands aside */
+  const bool plan_by_router = q.fp.lines != nullptr && q.fp.sp.plan_build.plan != nullptr && R > 1 &&
+                              q.rp.n <= AOS_PLAN_TABS_N;
   if (b < T * R) {
     const int t = b / R;
+    aos_shrink::PlanTabs *lt = (aos_shrink::PlanTabs *)(smem + rgu_tabs_off(q.rp.d, q.rp.n));
+    aos_shrink::PlanTabRegs tr = {};
+    if (plan_by_router) tr = aos_shrink::plan_tabs_fetch(q.fp.sp.plan_build);
     if (R > 1) {
       if (!route_part_block(q, t, b - t * R, (float *)smem)) return;
     } else {
       route_features_block<false>(q.rp, t, (float *)smem);
     }
-    /* the ring (plain stores of wave 0) is written again with device-scope stores, which the plan
-     * workgroup's device-scope loads see, then counted */
+    if (plan_by_router) aos_shrink::plan_tabs_store(q.fp.sp.plan_build, tr, lt); /* read after the barriers below */
+    /* one token whose router builds the plan: from its own ring, which no other workgroup reads.
+     * Otherwise the ring (plain stores of wave 0) is written again with device-scope stores, which
+     * the plan's device-scope loads see, and the routers count in. */
+    const bool solo = plan_by_router && T == 1;
     __syncthreads();
-    uint32_t *rw = (uint32_t *)(q.rp.rings + t);
-    if (threadIdx.x < 10) __hip_atomic_store(rw + threadIdx.x, rw[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    aos_mem_wait();
-    __syncthreads();
-    /* the last router to finish resets the count and raises the launch's routing flag */
-    if (threadIdx.x == 0 && aos_arrive(q.route_done) == (uint32_t)T - 1u) {
-      aos_reset(q.route_done);
-      aos_raise(q.route_flag, q.fp.gen);
+    if (!solo) {
+      uint32_t *rw = (uint32_t *)(q.rp.rings + t);
+      if (threadIdx.x < 10)
+        __hip_atomic_store(rw + threadIdx.x, rw[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      aos_mem_wait();
     }
+    __shared__ uint32_t last_router;
+    __syncthreads();
+    /* the last router to finish resets the count, builds the plan (or has the plan workgroup build
+     * it) and raises the launch's routing flag */
+    if (threadIdx.x == 0) {
+      last_router = solo ? 1u : (aos_arrive(q.route_done) == (uint32_t)T - 1u ? 1u : 0u);
+      if (last_router && !solo) aos_reset(q.route_done);
+    }
+    __syncthreads();
+    if (!last_router) return;
+    if (plan_by_router) {
+      aos_shrink::build_plan(q.fp.sp.plan_build, lt, solo);
+      aos_mem_wait();
+      __syncthreads();
+      if (threadIdx.x == 0) aos_raise(q.fp.lines + (size_t)(q.fp.pre_rows - 1) * 32, q.fp.gen);
+    }
+    if (threadIdx.x == 0) aos_raise(q.route_flag, q.fp.gen);
     return;
   }
   const int b2 = b - T * R;
   if (b2 < q.fp.n_pre) {
+    if (plan_by_router && b2 % q.fp.pre_rows == q.fp.pre_rows - 1) return; /* the plan workgroup */
     aos_gemv::fused_producer<NV, 4>(q.fp, b2, smem, q.route_flag);
     return;
   }
@@ -648,7 +678,7 @@ __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q
 template <int NV>
 int launch_rgu(const aos_route_gu_params *q, const aos_launch_ctx *ctx) {
   const int nwg = q->rp.T * q->rparts + q->fp.n_pre + (int)q->fp.n_cons;
-  size_t lds = (size_t)(q->rp.d + q->rp.n + 4) * sizeof(float);
+  size_t lds = rgu_tabs_off(q->rp.d, q->rp.n) + sizeof(aos_shrink::PlanTabs);
   if ((size_t)q->fp.sp.lds_bytes > lds) lds = (size_t)q->fp.sp.lds_bytes;
   if ((size_t)q->fp.gp[0].lds_bytes > lds) lds = (size_t)q->fp.gp[0].lds_bytes;
   AOS_LAUNCH(ctx, aos_route_gu_kernel<NV>, dim3(nwg), dim3(256), lds, *q);

@@ -32,12 +32,58 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+/* The plan's per-adapter inputs (bound flags, scales, the listed pointer tables) staged in LDS by
+ * a workgroup that builds the plan right after routing (at most AOS_PLAN_TABS_N adapters): it loads
+ * them before it routes, so that building the plan afterwards needs only the rings. */
+#define AOS_PLAN_TABS_N 64
+struct PlanTabs {
+  uint32_t bound[AOS_PLAN_TABS_N];
+  float scale[AOS_PLAN_TABS_N];
+  uint64_t ptr[AOS_PLAN_NPTR][AOS_PLAN_TABS_N];
+};
+
+/* Thread a's entries (a < n): loaded into registers first (relaxed atomic loads, which the compiler
+ * does not move down to their use), stored to LDS later, so that the loads overlap other work. */
+struct PlanTabRegs {
+  uint32_t bound;
+  float scale;
+  uint64_t ptr[AOS_PLAN_NPTR];
+};
+
+__device__ __forceinline__ PlanTabRegs plan_tabs_fetch(const aos_plan_params &pp) {
+  PlanTabRegs r = {};
+  const int a = threadIdx.x;
+  if (a < pp.n && a < AOS_PLAN_TABS_N) {
+    r.bound = __hip_atomic_load(pp.bound + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    r.scale = __hip_atomic_load(pp.scale + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int k = 0; k < AOS_PLAN_NPTR; ++k)
+      if (pp.ptab[k])
+        r.ptr[k] = __hip_atomic_load((const uint64_t *)(pp.ptab[k] + a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return r;
+}
+
+__device__ __forceinline__ void plan_tabs_store(const aos_plan_params &pp, const PlanTabRegs &r, PlanTabs *lt) {
+  const int a = threadIdx.x;
+  if (a < pp.n && a < AOS_PLAN_TABS_N) {
+    lt->bound[a] = r.bound;
+    lt->scale[a] = r.scale;
+#pragma unroll
+    for (int k = 0; k < AOS_PLAN_NPTR; ++k) lt->ptr[k][a] = r.ptr[k];
+  }
+}
+
 /* Plan of one call, built by a whole workgroup: ring slot s of token t contributes adapter
  * a = adapter_indices[s] when s < top_k, its gate q > 0 and the adapter is bound
  * (backend.rs:409-425 skips q <= 0 and unknown handles). coef[t][u] = sum over such slots of
  * scale[a] * (float(q) / 32767.0f), the product mod.scale * blend_weights[i] of the MLX
  * forward. */
-__device__ __forceinline__ void build_plan(const aos_plan_params &pp) {
+/* lt: the per-adapter inputs staged in LDS (NULL: read from memory). own_rings: the rings were written
+ * by this workgroup (plain loads see them after its barriers); otherwise they are read with
+ * device-scope loads. */
+__device__ __forceinline__ void build_plan(const aos_plan_params &pp, const PlanTabs *lt = nullptr,
+                                           bool own_rings = false) {
   __shared__ uint32_t bits[AOS_MAX_ADAPTERS / 32];
   __shared__ uint16_t list[AOS_PLAN_MAXU];
   __shared__ int cntU;
@@ -47,13 +93,15 @@ __device__ __forceinline__ void build_plan(const aos_plan_params &pp) {
   for (int w = tid; w < words; w += nt) bits[w] = 0u;
   /* the rings, with device-scope loads (the router may have written them in this launch) */
   for (int w = tid; w < pp.T * 10; w += nt)
-    ((uint32_t *)rs)[w] = __hip_atomic_load((const uint32_t *)pp.rings + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ((uint32_t *)rs)[w] = own_rings ? ((const uint32_t *)pp.rings)[w]
+                                    : __hip_atomic_load((const uint32_t *)pp.rings + w, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   for (int e = tid; e < pp.T * 8; e += nt) {
     const aoship_ring_t &r = rs[e >> 3];
     const int s = e & 7;
     const int a = r.adapter_indices[s];
-    if (s < (int)r.top_k && r.gates_q15[s] > 0 && a < pp.n && pp.bound[a])
+    if (s < (int)r.top_k && r.gates_q15[s] > 0 && a < pp.n && (lt ? lt->bound[a] != 0u : pp.bound[a] != 0))
       atomicOr(&bits[a >> 5], 1u << (a & 31));
   }
   __syncthreads();
@@ -82,7 +130,7 @@ __device__ __forceinline__ void build_plan(const aos_plan_params &pp) {
 #pragma unroll
   for (int k = 0; k < AOS_PLAN_NPTR; ++k) {
     pv[k] = 0;
-    if (tid < U && pp.ptab[k]) pv[k] = (uint64_t)aos_gld_ptr(pp.ptab[k] + list[tid]);
+    if (tid < U && pp.ptab[k]) pv[k] = lt ? lt->ptr[k][list[tid]] : (uint64_t)aos_gld_ptr(pp.ptab[k] + list[tid]);
   }
   for (int idx = tid; idx < pp.T * U; idx += nt) {
     const int t = idx / U, u = idx - t * U;
@@ -92,7 +140,7 @@ __device__ __forceinline__ void build_plan(const aos_plan_params &pp) {
     for (int s = 0; s < 8; ++s) {
       if (s < (int)r.top_k && r.adapter_indices[s] == a && r.gates_q15[s] > 0) {
         const float blend = (float)r.gates_q15[s] / 32767.0f;
-        c += pp.scale[a] * blend;
+        c += (lt ? lt->scale[a] : pp.scale[a]) * blend;
       }
     }
     aos_publish(&pp.plan->coef[t][u], c);
