@@ -378,8 +378,10 @@ __device__ __forceinline__ bool poll_lines_once(const uint32_t *lines, int n, ui
  * first, then the workgroup waits (bounded) for its line of xflag to reach p.gen and stages x
  * with device-coherent loads. DP: the direct expand loads (see (4a)) are allowed; the one-launch
  * MLP turns them off, since in its kernel they cost the compiler's promotion of the kernel
- * arguments to registers (the arguments would be copied to private memory). */
-template <int NV, bool SW, int W, int D, bool XL = false, bool DP = true>
+ * arguments to registers (the arguments would be copied to private memory). PP: when the plan
+ * arrives after the K loop, poll the other producers with the plan's parts (the launch with the
+ * router, whose plan comes last; elsewhere the extra loads measured slower). */
+template <int NV, bool SW, int W, int D, bool XL = false, bool DP = true, bool PP = false>
 __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int ksi, const uint32_t *xflag = nullptr) {
   constexpr int NA = SW ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -589,6 +591,11 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
       PlanPart pe0 = {}, pe1 = {};
       int Ue = 0;
       if (ready) {
+        /* with the plan's parts, one more poll of the lines (their values are read once the parts
+         * have arrived, so it costs no round trip of its own) */
+        uint32_t pv = p.gen;
+        if (PP && !all_up && p.n_pre_lines <= 64 && lane < p.n_pre_lines)
+          pv = __hip_atomic_load(p.pre_lines + (size_t)lane * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (p.tab0.rpad) {
           pe0 = expand_plan_part(p, p.tab0.rpad, p.pk0, q_first, lane, e0);
 #pragma unroll
@@ -610,7 +617,9 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
             expand_b_of(p, p.tab0.rpad, pr[k], q_first + (k + 1) * q_step < nq, row, lane, er[k]);
         }
         if (SW && p.tab1.rpad) expand_b_of(p, p.tab1.rpad, pe1, q_first < Ue * p.tab1.rpad / 16, row, lane, e1);
-        if (!all_up) ready = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
+        if (!all_up && !(PP && p.n_pre_lines <= 64 && __ballot(pv != p.gen) == 0ull))
+          ready = aos_wait_lines(p.pre_lines, p.n_pre_lines, p.gen, lane);
+        aos_compiler_barrier();
       }
       if (ready) {
         if (p.tab0.rpad) {

@@ -672,7 +672,7 @@ __global__ void __launch_bounds__(256) aos_route_gu_kernel(aos_route_gu_params q
     return;
   }
   const int r = b2 - q.fp.n_pre;
-  aos_gemv::gemv_body<NV, true, 4, 4>(q.fp.gp[0], r % q.fp.gp[0].nrbg, r / q.fp.gp[0].nrbg);
+  aos_gemv::gemv_body<NV, true, 4, 4, false, true, true>(q.fp.gp[0], r % q.fp.gp[0].nrbg, r / q.fp.gp[0].nrbg);
 }
 
 template <int NV>
