@@ -215,6 +215,78 @@ __device__ __forceinline__ void expand_rest(const aos_gemv_params &p, const aos_
 }
 
 
+/* The rest of both SwiGLU modules' steps in the same batches (EB of each), whose loads go out phase
+ * by phase together (plan list and row pointers, then B fragments, S and coefficients): both
+ * modules' steps cost the round trips of one module's. Each module's steps are added in its own
+ * order, as expand_rest adds them, so the sums are the same. */
+template <int EB>
+__device__ __forceinline__ void expand_rest2(const aos_gemv_params &p, int qa, int na, int qb, int nb, int qs, int row,
+                                             int lane, bool coherent, f32x16 &f0, f32x16 &f1) {
+  const int i = lane & 31, c = lane >> 5;
+  const int ti = i < p.T ? i : 0;
+  while (qa < na || qb < nb) {
+    int u[2][EB], j0[2][EB], a[2][EB];
+    bool on[2][EB];
+    const uint16_t *bptr[2][EB];
+    ExpandStep e[2][EB];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int rpad = m ? p.tab1.rpad : p.tab0.rpad;
+      const int pk = m ? p.pk1 : p.pk0;
+#pragma unroll
+      for (int k = 0; k < EB; ++k) {
+        const int q = (m ? qb : qa) + k * qs;
+        on[m][k] = q < (m ? nb : na);
+        u[m][k] = on[m][k] ? 16 * q / rpad : 0;
+        j0[m][k] = on[m][k] ? 16 * q - u[m][k] * rpad : 0;
+        a[m][k] = 0;
+        bptr[m][k] = nullptr;
+        if (on[m][k]) {
+          a[m][k] = coherent ? (int)__hip_atomic_load(&p.plan->list[u[m][k]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : (int)p.plan->list[u[m][k]];
+          if (pk) bptr[m][k] = plan_ptr(p, pk, u[m][k], coherent);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int pk = m ? p.pk1 : p.pk0;
+#pragma unroll
+      for (int k = 0; k < EB; ++k)
+        if (on[m][k] && !pk) bptr[m][k] = aos_gld_ptr(&(m ? p.tab1.B : p.tab0.B)[a[m][k]]);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int rpad = m ? p.tab1.rpad : p.tab0.rpad;
+      const float *S = m ? p.S1 : p.S0;
+      const int stride = m ? p.s_stride1 : p.s_stride0;
+#pragma unroll
+      for (int k = 0; k < EB; ++k) {
+        if (!on[m][k]) continue;
+        e[m][k].a = a[m][k];
+        e[m][k].cf = i < p.T ? load_f(&p.plan->coef[ti][u[m][k]], coherent) : 0.0f;
+        e[m][k].b = aos_gld16(bptr[m][k] ? bptr[m][k] + (size_t)row * rpad + j0[m][k] + 8 * c : p.zero_row);
+        const float *sp = S + (size_t)ti * stride + (p.s_all ? a[m][k] : u[m][k]) * rpad + j0[m][k] + 8 * c;
+        if (coherent) {
+          e[m][k].s0 = make_float4(load_f(sp, true), load_f(sp + 1, true), load_f(sp + 2, true), load_f(sp + 3, true));
+          e[m][k].s1 = make_float4(load_f(sp + 4, true), load_f(sp + 5, true), load_f(sp + 6, true), load_f(sp + 7, true));
+        } else {
+          e[m][k].s0 = *(const float4 *)sp;
+          e[m][k].s1 = *(const float4 *)(sp + 4);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < EB; ++k)
+      if (on[0][k]) expand_apply(e[0][k], f0);
+#pragma unroll
+    for (int k = 0; k < EB; ++k)
+      if (on[1][k]) expand_apply(e[1][k], f1);
+    qa += EB * qs;
+    qb += EB * qs;
+  }
+}
+
 /* Row block rb, K split ksi of one matrix (or of the gate/up pair). */
 /* The down projection's LoRA shrink over the 32 rows of h this row block produced (wave 0 only,
  * after the SwiGLU): h goes through LDS as a [token][row] bf16 tile (the MFMA's token operand);
@@ -736,11 +808,16 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
 #pragma unroll
     for (int k = 0; k < NB; ++k)
       if (k < nb && q_first + (k + 1) * q_step < nq0) expand_apply(er[k], f0);
-    if (q_first + (nb + 1) * q_step < nq0)
-      expand_rest<4>(p, p.tab0, p.pk0, p.S0, p.s_stride0, q_first + (nb + 1) * q_step, q_step, nq0, row, lane, fused,
-                     f0);
-    if (SW && q_first + q_step < nq1)
-      expand_rest<4>(p, p.tab1, p.pk1, p.S1, p.s_stride1, q_first + q_step, q_step, nq1, row, lane, fused, f1);
+    if (SW && NV > 1) { /* several steps per module per wave (8 tokens and up): both rests together */
+      if (q_first + q_step < nq0 || q_first + q_step < nq1)
+        expand_rest2<2>(p, q_first + q_step, nq0, q_first + q_step, nq1, q_step, row, lane, fused, f0, f1);
+    } else {
+      if (q_first + (nb + 1) * q_step < nq0)
+        expand_rest<4>(p, p.tab0, p.pk0, p.S0, p.s_stride0, q_first + (nb + 1) * q_step, q_step, nq0, row, lane, fused,
+                       f0);
+      if (SW && q_first + q_step < nq1)
+        expand_rest<4>(p, p.tab1, p.pk1, p.S1, p.s_stride1, q_first + q_step, q_step, nq1, row, lane, fused, f1);
+    }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       acc0[v] += f0[v];
