@@ -1163,14 +1163,22 @@ static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv
 #ifndef AOS_SHRINK_WGS
 #define AOS_SHRINK_WGS 256
 #endif
-static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, int waves = 4) {
+/* The x shrink's budget for staged x above 16 tokens: those fused launches run two waves per SIMD
+ * (their registers), so 64 KB of LDS per workgroup costs them no residency, and fewer K splits
+ * keep the launch within one round of resident workgroups (the 32-stream projections: 336 shrink
+ * workgroups at 32 KB, 192 at 64 KB). */
+#define AOS_XSHRINK_LDS_MAX_T32 (64 * 1024)
+static size_t x_shrink_lds_max(int T) { return T > 16 ? AOS_XSHRINK_LDS_MAX_T32 : AOS_GEMV_LDS_MAX; }
+
+static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, int waves = 4,
+                            size_t lds_max = AOS_GEMV_LDS_MAX) {
   const int target = waves == 8 ? AOS_SHRINK_WGS : AOS_SHRINK_WGS / 2;
   int ks = ceil_div(target, rb_total > 0 ? rb_total : 1);
   int cap = G / waves; /* every wave of a workgroup gets at least one group */
   if (cap < 1) cap = 1;
   if (cap > 16) cap = 16;
   if (ks > cap) ks = cap;
-  while (ks < G && 128 + (size_t)T * ceil_div(G, ks) * 128 > AOS_GEMV_LDS_MAX) ++ks;
+  while (ks < G && 128 + (size_t)T * ceil_div(G, ks) * 128 > lds_max) ++ks;
   size_t lds_x = 128 + (size_t)T * ceil_div(G, ks) * 128;
   size_t lds_r = (size_t)waves * nv_for(T) * 64 * 4;
   sp.ks = ks;
@@ -1202,7 +1210,7 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
     aos_shrink_params sp;
     memset(&sp, 0, sizeof(sp));
     W = kind == 4 ? 8 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
-    shrink_geometry(RB, G, T, sp, W);
+    shrink_geometry(RB, G, T, sp, W, kind == 3 ? x_shrink_lds_max(T) : AOS_GEMV_LDS_MAX);
     k = sp.ks;
   } else {
     return set_err("aoship_internal_decode_geometry: unknown kind");
@@ -1340,7 +1348,7 @@ static void plan_x_shrink(aoship_layer *l, Carve &cv, const uint16_t *x, int T, 
     rb_total += sp.n_rb[i];
   }
   /* sized for the waves of the GEMV it may be fused with (valid for the 4-wave launch too) */
-  shrink_geometry(rb_total, in / 64, T, sp, in / 64 >= AOS_GEMV_W8_MIN_G ? 8 : 4);
+  shrink_geometry(rb_total, in / 64, T, sp, in / 64 >= AOS_GEMV_W8_MIN_G ? 8 : 4, x_shrink_lds_max(T));
   sp.part = cv.b.take<float>((size_t)rb_total * sp.ks * nv_for(T) * 64);
   sp.counters = cv.counters((size_t)rb_total + 1);
   xs.separate_plan = !all;

@@ -40,7 +40,8 @@ def test_every_gemv_wave_gets_a_group(T):
 
 @pytest.mark.parametrize("T", range(1, 33))
 def test_shrink_geometry_within_limits(T):
-    """Shrinks: the K splits stay within the groups and the LDS budget. A shrink wave may get no
+    """Shrinks: the K splits stay within the groups and the LDS budget (64 KB for the x shrink above
+    16 tokens, else 32 KB). A shrink wave may get no
     group when its launch runs more waves per workgroup than its splits leave groups; it then
     reads the zero row and adds nothing."""
     for kind, shapes in ((3, SHRINK_ROWS), (4, H_SHRINK_ROWS)):
@@ -48,7 +49,10 @@ def test_shrink_geometry_within_limits(T):
             w, ks, _, g = aoship.decode_geometry(kind, rows, inp, T)
             G = inp // 64
             assert 1 <= ks <= G
-            assert 128 + T * -(-G // ks) * 128 <= 32 * 1024
+            # the x shrink above 16 tokens runs in launches held to two waves per SIMD by their
+            # registers: 64 KB of staged x costs them no residency
+            budget = 64 * 1024 if (kind == 3 and T > 16) else 32 * 1024
+            assert 128 + T * -(-G // ks) * 128 <= budget
 
 
 def test_geometry_rejects_bad_shapes():
