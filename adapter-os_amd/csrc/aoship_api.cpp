@@ -1059,6 +1059,9 @@ static int nv_for(int T) {
  * any bound adapter has this module. */
 #ifndef AOS_GEMV_WAVES
 #define AOS_GEMV_WAVES 1024 /* waves streaming one matrix (measured best at decode) */
+#define AOS_GEMV_WAVES_DOWN12 1536 /* ... the 1-2 token down GEMV, whose plan and first B fragments load
+                                    * before its K loop (measured on two boxes: 4 splits of the 7B
+                                    * shape against 3, the launch 0.5-1 us shorter) */
 #endif
 #ifndef AOS_GEMV_W8_MIN_G
 #define AOS_GEMV_W8_MIN_G 128 /* single-matrix GEMVs with at least this many groups use 8 waves */
@@ -1201,7 +1204,7 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
   if (kind <= 2) {
     aos_gemv_params g;
     memset(&g, 0, sizeof(g));
-    const int target = kind == 1 ? (T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES) : AOS_GEMV_WAVES;
+    const int target = kind == 1 ? (T <= 2 ? AOS_GEMV_WAVES_DOWN12 : 2 * AOS_GEMV_WAVES) : AOS_GEMV_WAVES;
     gemv_geometry(RB, G, T, kind == 0, true, g, target, kind == 1 && T <= 2);
     W = g.waves;
     k = g.ks;
@@ -1457,7 +1460,7 @@ static void plan_mlp(aoship_layer *l, int T, const uint16_t *x, const aoship_rin
   /* the down GEMV streams beside the h shrink of its launch: more K splits (measured: 3 at the
    * 7B shape) keep its tail short; at 1-2 tokens it runs in the gate/up launch's grid, in
    * 4-wave workgroups like the rest of that grid */
-  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES : 2 * AOS_GEMV_WAVES, T <= 2,
+  gemv_geometry(Wd.RB, Wd.G, T, false, td.rpad > 0, g2, T <= 2 ? AOS_GEMV_WAVES_DOWN12 : 2 * AOS_GEMV_WAVES, T <= 2,
                 l->geo_wr[1], l->geo_ks[1]);
   g2.tab0 = td;
   g2.S0 = s2.S[0];
