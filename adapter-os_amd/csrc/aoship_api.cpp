@@ -1062,6 +1062,9 @@ static int nv_for(int T) {
 #define AOS_GEMV_WAVES_DOWN12 1536 /* ... the 1-2 token down GEMV, whose plan and first B fragments load
                                     * before its K loop (measured on two boxes: 4 splits of the 7B
                                     * shape against 3, the launch 0.5-1 us shorter) */
+#define AOS_GEMV_WAVES_PROJ12 256 /* ... the 1-2 token projections: one K split from 64 row blocks on
+                                   * (the 7B q/k/v and o launches each 3-4 us shorter without the split
+                                   * reduction's round trip: model decode 2.65 -> 2.56 ms/token) */
 #endif
 #ifndef AOS_GEMV_W8_MIN_G
 #define AOS_GEMV_W8_MIN_G 128 /* single-matrix GEMVs with at least this many groups use 8 waves */
@@ -1204,7 +1207,9 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
   if (kind <= 2) {
     aos_gemv_params g;
     memset(&g, 0, sizeof(g));
-    const int target = kind == 1 ? (T <= 2 ? AOS_GEMV_WAVES_DOWN12 : 2 * AOS_GEMV_WAVES) : AOS_GEMV_WAVES;
+    const int target = kind == 1   ? (T <= 2 ? AOS_GEMV_WAVES_DOWN12 : 2 * AOS_GEMV_WAVES)
+                       : kind == 2 ? (T <= 2 ? AOS_GEMV_WAVES_PROJ12 : AOS_GEMV_WAVES)
+                                   : AOS_GEMV_WAVES;
     gemv_geometry(RB, G, T, kind == 0, true, g, target, kind == 1 && T <= 2);
     W = g.waves;
     k = g.ks;
@@ -2079,8 +2084,8 @@ static void plan_proj_decode(aoship_layer *l, Carve &cv, const int *mods, int nm
     gp[i].w0 = W.dev();
     gp[i].x = xc;
     gp[i].T = Tc;
-    gemv_geometry(rb_all, W.G, Tc, false, tabs[i].rpad > 0, gp[i], AOS_GEMV_WAVES, false, l->geo_wr[2],
-                  l->geo_ks[2]);
+    gemv_geometry(rb_all, W.G, Tc, false, tabs[i].rpad > 0, gp[i], Tc <= 2 ? AOS_GEMV_WAVES_PROJ12 : AOS_GEMV_WAVES,
+                  false, l->geo_wr[2], l->geo_ks[2]);
     gp[i].tab0 = tabs[i];
     gp[i].S0 = Q.xs.sp.S[i];
     gp[i].s_stride0 = Q.xs.sp.s_stride[i];
