@@ -229,6 +229,42 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
     const int w = lane + 64 * jw;
     wi[jw] = w < hw ? w : 0;
   }
+  /* rope_fused: the token's query pairs (and, in the split holding its position, its key pairs
+   * and value words) with their biases and frequencies are loaded first, so that they share the
+   * memory round trip of the first block's key and value rows; pair w = lane + 64 jw */
+  float cq1[NW], cq2[NW], cf[NW], ck1[NW], ck2[NW], cv0[NW], cv1[NW];
+  if (p.rope_fused) {
+    const uint16_t *qb = p.qb + (size_t)h * hd;
+    const uint16_t *kb = p.kb + (size_t)kvh * hd;
+    const uint32_t *vb = (const uint32_t *)(p.vb + (size_t)kvh * hd);
+#pragma unroll
+    for (int jw = 0; jw < NW; ++jw) {
+      const int w = wi[jw];
+      cq1[jw] = aos_bf16_to_f32(qb[w]);
+      cq2[jw] = aos_bf16_to_f32(qb[w + hw]);
+      if (p.bq) {
+        cq1[jw] = cq1[jw] + p.bq[h * hd + w];
+        cq2[jw] = cq2[jw] + p.bq[h * hd + w + hw];
+      }
+      cf[jw] = p.inv_freq[w];
+      ck1[jw] = ck2[jw] = cv0[jw] = cv1[jw] = 0.0f;
+      if (has_cur) {
+        ck1[jw] = aos_bf16_to_f32(kb[w]);
+        ck2[jw] = aos_bf16_to_f32(kb[w + hw]);
+        if (p.bk) {
+          ck1[jw] = ck1[jw] + p.bk[kvh * hd + w];
+          ck2[jw] = ck2[jw] + p.bk[kvh * hd + w + hw];
+        }
+        const uint32_t pr = vb[w];
+        cv0[jw] = __builtin_bit_cast(float, pr << 16);
+        cv1[jw] = __builtin_bit_cast(float, pr & 0xffff0000u);
+        if (p.bv) {
+          cv0[jw] = cv0[jw] + p.bv[kvh * hd + 2 * w];
+          cv1[jw] = cv1[jw] + p.bv[kvh * hd + 2 * w + 1];
+        }
+      }
+    }
+  }
   for (int base = beg; base < end; base += 64) {
     const int pos = base + lane;
     const bool valid = pos < end;
@@ -249,49 +285,30 @@ __global__ void __launch_bounds__(64) aos_attn_kernel(aos_attn_params p) {
     if (base == beg) {
       if (p.rope_fused) {
         const float fpos = (float)cur;
-        const uint16_t *qb = p.qb + (size_t)h * hd;
-        for (int i = lane; i < hw; i += 64) {
-          float x1 = aos_bf16_to_f32(qb[i]), x2 = aos_bf16_to_f32(qb[i + hw]);
-          if (p.bq) {
-            x1 = x1 + p.bq[h * hd + i];
-            x2 = x2 + p.bq[h * hd + i + hw];
-          }
-          rope_pair(x1, x2, fpos, p.inv_freq[i], qs[i], qs[i + hw]);
-        }
-        if (has_cur) {
-          /* the key and value as the cache holds them (bf16); the first head of the group
-           * appends them */
-          const bool writer = h % (p.nh / p.nkv) == 0;
-          const uint16_t *kb = p.kb + (size_t)kvh * hd;
-          uint16_t *kdst = p.kc + ((size_t)kvh * p.max_seq + cur) * hd;
-          for (int i = lane; i < hw; i += 64) {
-            float x1 = aos_bf16_to_f32(kb[i]), x2 = aos_bf16_to_f32(kb[i + hw]);
-            if (p.bk) {
-              x1 = x1 + p.bk[kvh * hd + i];
-              x2 = x2 + p.bk[kvh * hd + i + hw];
+        /* the key and value as the cache holds them (bf16); the first head of the group
+         * appends them */
+        const bool writer = has_cur && h % (p.nh / p.nkv) == 0;
+        uint16_t *kdst = p.kc + ((size_t)kvh * p.max_seq + cur) * hd;
+        uint32_t *vdst = (uint32_t *)(p.vc + ((size_t)kvh * p.max_seq + cur) * hd);
+#pragma unroll
+        for (int jw = 0; jw < NW; ++jw) {
+          const int i = lane + 64 * jw;
+          if (i < hw) {
+            rope_pair(cq1[jw], cq2[jw], fpos, cf[jw], qs[i], qs[i + hw]);
+            if (has_cur) {
+              float r1, r2;
+              rope_pair(ck1[jw], ck2[jw], fpos, cf[jw], r1, r2);
+              const uint16_t b1 = aos_f32_to_bf16(r1), b2 = aos_f32_to_bf16(r2);
+              ((uint16_t *)kcur)[i] = b1;
+              ((uint16_t *)kcur)[i + hw] = b2;
+              const uint32_t o = (uint32_t)aos_f32_to_bf16(cv0[jw]) | ((uint32_t)aos_f32_to_bf16(cv1[jw]) << 16);
+              vcur[i] = o;
+              if (writer) {
+                kdst[i] = b1;
+                kdst[i + hw] = b2;
+                vdst[i] = o;
+              }
             }
-            float r1, r2;
-            rope_pair(x1, x2, fpos, p.inv_freq[i], r1, r2);
-            const uint16_t b1 = aos_f32_to_bf16(r1), b2 = aos_f32_to_bf16(r2);
-            ((uint16_t *)kcur)[i] = b1;
-            ((uint16_t *)kcur)[i + hw] = b2;
-            if (writer) {
-              kdst[i] = b1;
-              kdst[i + hw] = b2;
-            }
-          }
-          const uint32_t *vb = (const uint32_t *)(p.vb + (size_t)kvh * hd);
-          uint32_t *vdst = (uint32_t *)(p.vc + ((size_t)kvh * p.max_seq + cur) * hd);
-          for (int w = lane; w < hw; w += 64) {
-            const uint32_t pr = vb[w];
-            float v0 = __builtin_bit_cast(float, pr << 16), v1 = __builtin_bit_cast(float, pr & 0xffff0000u);
-            if (p.bv) {
-              v0 = v0 + p.bv[kvh * hd + 2 * w];
-              v1 = v1 + p.bv[kvh * hd + 2 * w + 1];
-            }
-            const uint32_t o = (uint32_t)aos_f32_to_bf16(v0) | ((uint32_t)aos_f32_to_bf16(v1) << 16);
-            vcur[w] = o;
-            if (writer) vdst[w] = o;
           }
         }
       } else {
