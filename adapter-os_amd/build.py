@@ -1,5 +1,6 @@
 """Build the gfx950 library (libaoship.so), the synthetic-input helper (libaos_synth.so) and the
-matrix-core peak probe the bench reports beside the datasheet peak (libaos_peak.so).
+probes the bench reports beside the datasheet peaks (libaos_peak.so: the matrix-core peak and the
+one-launch HBM stream).
 
 Every HIP translation unit is compiled for gfx950 only, with IEEE float semantics: no fast-math,
 no floating-point contraction, float32 denormals kept, and packed-FP32 instruction selection
@@ -111,7 +112,7 @@ def build(jobs: int = 4) -> None:
     os.replace(tmp, SYNTH)
     tmp = PEAK.with_suffix(".so.tmp")
     _run([HIPCC, "-x", "hip", *HIP_FLAGS, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          str(PKG / "probe" / "aos_mfma_peak.hip")])
+          str(PKG / "probe" / "aos_mfma_peak.hip"), str(PKG / "probe" / "aos_hbm_stream.hip")])
     os.replace(tmp, PEAK)
 
 

@@ -336,6 +336,51 @@ def measured_mfma_peak() -> float | None:
     return tf if tf > 0 else None
 
 
+def hbm_stream_probe(gate_up_b: int, down_b: int) -> dict | None:
+    """What one launch can read from HBM here (the probe library's stream kernel: the decode GEMVs'
+    pattern of contiguous 1 KiB chunks per wave, 4-wave workgroups, each timed launch after a 1 GiB
+    read that evicts the caches; median of 7 launches). Reports the ceiling (1 GiB, best of the
+    workgroup counts and ring depths tried) and, for the byte counts of the decode launches, the
+    best one-launch time and the time at the decode grids' workgroup counts; None when absent."""
+    import ctypes
+
+    path = ROOT / "adapter-os_amd" / "libaos_peak.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    fn = lib.aos_hbm_stream_us
+    fn.restype = ctypes.c_double
+    fn.argtypes = [ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+
+    def best(nbytes: int, wgs_list, depths=(4, 8)) -> dict:
+        nbytes -= nbytes % 1024
+        out = None
+        for wgs in wgs_list:
+            for d in depths:
+                us = fn(nbytes, wgs, d, 7)
+                if us <= 0:
+                    raise RuntimeError("HBM stream probe failed")
+                if out is None or us < out["us"]:
+                    out = {"us": us, "tbps": nbytes / (us * 1e-6) / 1e12, "workgroups": wgs, "depth": d}
+        out["bytes"] = nbytes
+        return out
+
+    grids = (256, 512, 768, 1024, 1536, 2048)
+    res = {
+        "ceiling": best(1 << 30, (1024, 2048, 4096, 8192)),
+        "gate_up_bytes": best(gate_up_b, grids),
+        "down_bytes": best(down_b, grids),
+        "gate_up_bytes_at_592_workgroups": best(gate_up_b, (592,), (4,)),
+        "down_bytes_at_448_workgroups": best(down_b, (448,), (4,)),
+    }
+    lib.aos_hbm_stream_free()
+    res["two_launch_floor_us"] = res["gate_up_bytes"]["us"] + res["down_bytes"]["us"]
+    res["note"] = ("plain streaming kernels, no compute: a lower bound for one launch per matrix; the "
+                   "592- and 448-workgroup lines read the same bytes with the decode grids' workgroup "
+                   "counts (592 row blocks of gate/up; 448 down workgroups)")
+    return res
+
+
 def measured_traffic():
     """HBM bytes per launch of the gate/up GEMV from the committed counter summary, or None."""
     if not TRAFFIC_FILE.exists():
@@ -657,6 +702,15 @@ def main() -> int:
     }
     log(f"decode T=1 as two calls (route, then aoship_mlp_forward): {ms_two * 1e3:.1f} us/step")
     del dec
+    hp = hbm_stream_probe(gu_bytes, layer_bytes - gate_up_bytes(cfg, T, U))
+    if hp:
+        result["decode_hbm_probe"] = hp
+        log("HBM stream probe: ceiling %.2f TB/s; one launch of %.1f MB %.1f us (%.2f TB/s), %.1f MB %.1f us "
+            "(%.2f TB/s); at the decode grids %.1f / %.1f us" % (
+                hp["ceiling"]["tbps"], hp["gate_up_bytes"]["bytes"] / 1e6, hp["gate_up_bytes"]["us"],
+                hp["gate_up_bytes"]["tbps"], hp["down_bytes"]["bytes"] / 1e6, hp["down_bytes"]["us"],
+                hp["down_bytes"]["tbps"], hp["gate_up_bytes_at_592_workgroups"]["us"],
+                hp["down_bytes_at_448_workgroups"]["us"]))
 
     # ---- 8-token decode batch ----
     T8 = 8
