@@ -125,19 +125,34 @@ def lib():
         L.aoship_internal_decode_geometry.restype = C.c_int
         L.aoship_internal_decode_geometry.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int),
                                                       C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        L.aoship_internal_decode_geometry_pinned.restype = C.c_int
+        L.aoship_internal_decode_geometry_pinned.argtypes = [C.c_int] * 6 + [C.POINTER(C.c_int)] * 4
         L.aoship_internal_layer_set_gemv_geometry.restype = C.c_int
         L.aoship_internal_layer_set_gemv_geometry.argtypes = [_P, C.c_int, C.c_int, C.c_int]
+        L.aoship_internal_set_spin_limit.restype = C.c_int
+        L.aoship_internal_set_spin_limit.argtypes = [C.c_uint32]
         _lib = L
     return _lib
 
 
-def decode_geometry(kind: int, out: int, inp: int, T: int) -> tuple[int, int, int, int]:
+def decode_geometry(kind: int, out: int, inp: int, T: int, wr_pin: int = 0, ks_pin: int = 0) -> tuple[int, int, int, int]:
     """(waves, K splits, row blocks per workgroup, fewest K groups of any wave) of a decode launch
-    shape (see aoship_internal_decode_geometry)."""
+    shape (see aoship_internal_decode_geometry), optionally with a GEMV shape pinned as
+    Layer.set_gemv_geometry pins it."""
     w, k, r, g = C.c_int(), C.c_int(), C.c_int(), C.c_int()
-    _check(lib().aoship_internal_decode_geometry(kind, out, inp, T, C.byref(w), C.byref(k), C.byref(r), C.byref(g)),
+    _check(lib().aoship_internal_decode_geometry_pinned(kind, out, inp, T, wr_pin, ks_pin, C.byref(w), C.byref(k),
+                                                        C.byref(r), C.byref(g)),
            "aoship_internal_decode_geometry")
     return w.value, k.value, r.value, g.value
+
+
+SPIN_LIMIT_DEFAULT = 1 << 24
+
+
+def set_spin_limit(polls: int) -> None:
+    """Diagnostic: the bound (in polls) of every in-launch wait on the current device; 0 makes every
+    wait give up at once (each kernel still ends normally and the layer reports the timeout)."""
+    _check(lib().aoship_internal_set_spin_limit(polls), "aoship_internal_set_spin_limit")
 
 
 def last_error() -> str:

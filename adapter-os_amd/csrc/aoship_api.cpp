@@ -903,6 +903,22 @@ extern "C" int aoship_layer_wait_timeouts(aoship_layer_t *l) {
   return 1;
 }
 
+/* Diagnostic (no counterpart in the reference): the bound of every in-launch wait of this
+ * library's kernels on the current device, in polls (the default, 2^24, is about a second). With
+ * 0 every wait gives up before its first poll: each kernel still runs to its end, skips what it
+ * waited for and reports the timeout, so tests can drive the give-up paths. Synchronises the
+ * device first. */
+extern "C" int aoship_internal_set_spin_limit(uint32_t polls) {
+  if (ensure_device()) return -1;
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  int (*const setters[])(uint32_t) = {aos_spin_setter_router, aos_spin_setter_lora, aos_spin_setter_gemv,
+                                      aos_spin_setter_gemm,   aos_spin_setter_model, aos_spin_setter_liquid};
+  for (auto *f : setters)
+    if (f(polls) != (int)hipSuccess) return set_err("aoship_internal_set_spin_limit: hipMemcpyToSymbol failed");
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return 0;
+}
+
 /* A forward refuses to run while a given-up wait is pending: its counters may be inconsistent. */
 static int check_no_timeout(aoship_layer *l) {
   if (*(volatile uint32_t *)l->wait_host)
@@ -1142,7 +1158,16 @@ static void gemv_geometry(int RB, int G, int T, bool swiglu, bool lora, aos_gemv
   int W = (swiglu || four_waves) ? 4 : (G >= AOS_GEMV_W8_MIN_G ? 8 : 4);
   int ks = 1;
   g.wr = 1;
-  if (T > 2 || wr_force > 0 || ks_force > 0) {
+  /* at 1-2 tokens the SwiGLU launch forms the h shrink's partials, one row block per workgroup
+   * (wave 0 of the workgroup forms them): a pinned shape keeps one row block per workgroup, and
+   * a pinned split count that leaves a wave without a K group or exceeds the LDS budget is not
+   * applied */
+  const bool one_rb = swiglu && T <= 2;
+  if (one_rb && ks_force > 0 && (ks_force > G || G / ks_force < W || gemv_lds_x(T, G, ks_force) > AOS_GEMV_LDS_MAX))
+    ks_force = 0;
+  if (one_rb && ks_force > 0) {
+    ks = ks_force;
+  } else if (!one_rb && (T > 2 || wr_force > 0 || ks_force > 0)) {
     gemv_geometry_rows(RB, G, T, swiglu, W, g, wr_force, ks_force);
     ks = g.ks;
   } else {
@@ -1198,9 +1223,21 @@ static void shrink_geometry(int rb_total, int G, int T, aos_shrink_params &sp, i
  * rank rows launched with 8 waves when in / 64 >= AOS_GEMV_W8_MIN_G, else 4 (the x shrink);
  * 4: the same with 8 waves (the h shrink). Writes the waves, the K splits, the row blocks per
  * workgroup (GEMVs; 1 for a shrink) and the fewest groups any wave gets. */
+extern "C" int aoship_internal_decode_geometry_pinned(int kind, int out, int in, int T, int wr_pin, int ks_pin,
+                                                      int *waves, int *ks, int *wr, int *min_groups);
+
 extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T, int *waves, int *ks, int *wr,
                                                int *min_groups) {
-  if (out < 32 || in < 64 || in % 64 || T < 1 || T > AOS_DECODE_MAX_T || !waves || !ks || !wr || !min_groups)
+  return aoship_internal_decode_geometry_pinned(kind, out, in, T, 0, 0, waves, ks, wr, min_groups);
+}
+
+/* The same with a GEMV shape pinned as aoship_internal_layer_set_gemv_geometry pins it (wr_pin row
+ * blocks per workgroup, ks_pin K splits; 0: the geometry's own choice; GEMV kinds only). */
+extern "C" int aoship_internal_decode_geometry_pinned(int kind, int out, int in, int T, int wr_pin, int ks_pin,
+                                                      int *waves, int *ks, int *wr, int *min_groups) {
+  if (out < 32 || in < 64 || in % 64 || T < 1 || T > AOS_DECODE_MAX_T || !waves || !ks || !wr || !min_groups ||
+      wr_pin < 0 || wr_pin > 8 || (wr_pin & (wr_pin - 1)) || ks_pin < 0 || ks_pin > 64 ||
+      (kind > 2 && (wr_pin || ks_pin)))
     return set_err("aoship_internal_decode_geometry: bad arguments");
   const int G = in / 64, RB = out / 32;
   int W = 4, k = 1, r = 1;
@@ -1210,7 +1247,7 @@ extern "C" int aoship_internal_decode_geometry(int kind, int out, int in, int T,
     const int target = kind == 1   ? (T <= 2 ? AOS_GEMV_WAVES_DOWN12 : 2 * AOS_GEMV_WAVES)
                        : kind == 2 ? (T <= 2 ? AOS_GEMV_WAVES_PROJ12 : AOS_GEMV_WAVES)
                                    : AOS_GEMV_WAVES;
-    gemv_geometry(RB, G, T, kind == 0, true, g, target, kind == 1 && T <= 2);
+    gemv_geometry(RB, G, T, kind == 0, true, g, target, kind == 1 && T <= 2, wr_pin, ks_pin);
     W = g.waves;
     k = g.ks;
     r = g.wr;

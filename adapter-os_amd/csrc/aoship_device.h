@@ -172,18 +172,33 @@ __device__ __forceinline__ void aos_raise(uint32_t *flag, uint32_t gen) {
   __hip_atomic_store(flag, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* The bound of every wait below, in polls: 2^24 (about a second) unless the host sets another
+ * value (aoship_internal_set_spin_limit, per device). With 0 every wait gives up before its first
+ * poll, so that a test can drive every give-up path while every kernel still ends normally. Each
+ * translation unit holds its own copy of the variable (internal linkage) and defines a host setter
+ * for it with AOS_DEFINE_SPIN_SETTER; the library's setter calls all of them. */
+#define AOS_SPIN_LIMIT_DEFAULT (1u << 24)
+static __device__ uint32_t aos_spin_limit_dev = AOS_SPIN_LIMIT_DEFAULT;
+#define AOS_DEFINE_SPIN_SETTER(name)                                                        \
+  extern "C" int name(uint32_t polls) {                                                     \
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(aos_spin_limit_dev), &polls, sizeof(polls)); \
+  }
+
+__device__ __forceinline__ uint32_t aos_spin_limit() { return aos_spin_limit_dev; }
+
 /* Bounded wait (one lane) until *flag == gen. Returns false when it gave up (after about a
- * second). The payload loads that follow are not moved above the wait. */
-#define AOS_SPIN_LIMIT (1u << 24)
+ * second at the default bound). The payload loads that follow are not moved above the wait. */
 __device__ __forceinline__ bool aos_wait_gen(const uint32_t *flag, uint32_t gen) {
+  const uint32_t limit = aos_spin_limit();
   uint32_t spins = 0;
   bool ok = true;
-  while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) {
-    __builtin_amdgcn_s_sleep(2);
-    if (++spins > AOS_SPIN_LIMIT) {
+  while (true) {
+    if (spins++ >= limit) {
       ok = false;
       break;
     }
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) break;
+    __builtin_amdgcn_s_sleep(2);
   }
   aos_compiler_barrier();
   return ok;
@@ -193,18 +208,19 @@ __device__ __forceinline__ bool aos_wait_gen(const uint32_t *flag, uint32_t gen)
  * polls lines l, l + 64, ... Returns false (uniformly) when it gave up. The loads that follow
  * are not moved above the wait. */
 __device__ __forceinline__ bool aos_wait_lines(const uint32_t *lines, int n, uint32_t gen, int lane) {
+  const uint32_t limit = aos_spin_limit();
   uint32_t spins = 0;
   for (int base = 0; base < n; base += 64) {
     const int i = base + lane;
     const uint32_t *f = lines + (size_t)(i < n ? i : 0) * 32;
     while (true) {
-      const uint32_t v = i < n ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : gen;
-      if (__ballot(v != gen) == 0ull) break;
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > AOS_SPIN_LIMIT) {
+      if (spins++ >= limit) {
         aos_compiler_barrier();
         return false;
       }
+      const uint32_t v = i < n ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : gen;
+      if (__ballot(v != gen) == 0ull) break;
+      __builtin_amdgcn_s_sleep(2);
     }
   }
   aos_compiler_barrier();

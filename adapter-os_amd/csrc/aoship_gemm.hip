@@ -1332,3 +1332,5 @@ extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_l
   if (swiglu) return launch_gemm_cfg<true, 2, false, false, 4, 2, 2, AOS_GEMM_NS_SW>(p, ctx);
   return launch_gemm_cfg<false, 4, true, true, 8, 2, 4, AOS_GEMM_NS_ONE>(p, ctx);
 }
+
+AOS_DEFINE_SPIN_SETTER(aos_spin_setter_gemm)

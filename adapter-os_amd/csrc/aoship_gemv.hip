@@ -287,3 +287,5 @@ extern "C" int aos_launch_decode_mlp(const aos_decode_mlp_params *mp, const aos_
   if (T <= 1) return launch_mlp_nv<1>(mp, st);
   return launch_mlp_nv<2>(mp, st);
 }
+
+AOS_DEFINE_SPIN_SETTER(aos_spin_setter_gemv)

@@ -481,6 +481,13 @@ int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);
+/* The wait bound of each translation unit's kernels on the current device (polls; hipError_t). */
+int aos_spin_setter_router(uint32_t polls);
+int aos_spin_setter_lora(uint32_t polls);
+int aos_spin_setter_gemv(uint32_t polls);
+int aos_spin_setter_gemm(uint32_t polls);
+int aos_spin_setter_model(uint32_t polls);
+int aos_spin_setter_liquid(uint32_t polls);
 #ifdef __cplusplus
 }
 #endif

@@ -77,3 +77,5 @@ extern "C" int aos_launch_liquid(const aos_liquid_params *p, const aos_launch_ct
   AOS_LAUNCH(ctx, aos_liquid_kernel, dim3(grid), dim3(LQ_NT), 0, *p);
   return (int)hipGetLastError();
 }
+
+AOS_DEFINE_SPIN_SETTER(aos_spin_setter_liquid)

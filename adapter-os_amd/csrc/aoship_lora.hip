@@ -40,3 +40,5 @@ extern "C" int aos_launch_shrink(const aos_shrink_params *p, const aos_launch_ct
   if (T <= 16) return launch_nv<8>(p, ctx);
   return launch_nv<16>(p, ctx);
 }
+
+AOS_DEFINE_SPIN_SETTER(aos_spin_setter_lora)

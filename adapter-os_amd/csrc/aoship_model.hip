@@ -533,3 +533,5 @@ extern "C" int aos_launch_attention(const aos_attn_params *p, const aos_launch_c
   if (p->hd <= 128) return launch_attn<2>(p, ctx);
   return launch_attn<4>(p, ctx);
 }
+
+AOS_DEFINE_SPIN_SETTER(aos_spin_setter_model)

@@ -722,3 +722,5 @@ extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx 
   }
   return (int)hipGetLastError();
 }
+
+AOS_DEFINE_SPIN_SETTER(aos_spin_setter_router)

@@ -55,6 +55,21 @@ def test_shrink_geometry_within_limits(T):
             assert 128 + T * -(-G // ks) * 128 <= budget
 
 
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("wr", [1, 2, 4])
+@pytest.mark.parametrize("ks", [0, 1, 2, 4])
+def test_pinned_gate_up_keeps_one_row_block_at_one_or_two_tokens(T, wr, ks):
+    """A pinned row-split shape is not applied to the 1-2 token gate/up launch, whose wave 0 forms
+    the h shrink's partials for the workgroup's one row block; other launches take the pin."""
+    for H, I in MLP_SHAPES:
+        w, k, r, g = aoship.decode_geometry(0, I, H, T, wr, ks)
+        assert r == 1 and g >= 1
+        if ks and (H // 64) // ks >= w:  # a pin that leaves a wave without a K group is not applied
+            assert k == ks
+    w, k, r, g = aoship.decode_geometry(0, 18944, 3584, 3, 4, 0)
+    assert r == 4
+
+
 def test_geometry_rejects_bad_shapes():
     with pytest.raises(aoship.AosError):
         aoship.decode_geometry(0, 3584, 100, 1)
