@@ -129,6 +129,8 @@ def lib():
         L.aoship_internal_decode_geometry_pinned.argtypes = [C.c_int] * 6 + [C.POINTER(C.c_int)] * 4
         L.aoship_internal_layer_set_gemv_geometry.restype = C.c_int
         L.aoship_internal_layer_set_gemv_geometry.argtypes = [_P, C.c_int, C.c_int, C.c_int]
+        L.aoship_internal_layer_set_mlp1.restype = C.c_int
+        L.aoship_internal_layer_set_mlp1.argtypes = [_P, C.c_int]
         L.aoship_internal_set_spin_limit.restype = C.c_int
         L.aoship_internal_set_spin_limit.argtypes = [C.c_uint32]
         _lib = L
@@ -394,6 +396,12 @@ class Layer:
         (projections) to wr row blocks per workgroup and ks K splits (0: automatic)."""
         _check(lib().aoship_internal_layer_set_gemv_geometry(self.h, kind, wr, ks),
                "aoship_internal_layer_set_gemv_geometry")
+
+    def set_mlp1(self, on: bool) -> None:
+        """Diagnostic: one token's MLP (and its routing) in one launch with the down matrix held in
+        LDS, where the layer's shape fits (off by default: the two-launch decode path is faster so
+        far)."""
+        _check(lib().aoship_internal_layer_set_mlp1(self.h, 1 if on else 0), "aoship_internal_layer_set_mlp1")
 
     def set_prefill_shrink(self, fused: bool) -> None:
         """Diagnostic: the prefill MLP's LoRA shrinks in the GEMM launches that consume them

@@ -50,6 +50,7 @@ SOURCES = [
     "aoship_gemm.hip",
     "aoship_model.hip",
     "aoship_liquid.hip",
+    "aoship_mlp1.hip",
     "aoship_api.cpp",
 ]
 
@@ -58,7 +59,7 @@ SOURCES = [
 # must compile without a private stack: a non-inlined device function call in one of them (which
 # forced a stack frame and one wave per SIMD) gave wrong one-token results even where the call
 # was never taken. The build fails if one of them gets private memory.
-NO_SCRATCH = ("aos_gemv_fused_kernel", "aos_route_gu_kernel", "aos_decode_mlp_kernel")
+NO_SCRATCH = ("aos_gemv_fused_kernel", "aos_route_gu_kernel", "aos_decode_mlp_kernel", "aos_mlp1_kernel")
 RESOURCE_REMARKS = ["-Rpass-analysis=kernel-resource-usage"]
 
 

@@ -55,7 +55,7 @@ static int g_device = -1;
  * device current, hipGetSymbolAddress gives this device's copy, kept per device. */
 #define AOS_SCRATCH_BYTES ((size_t)32 << 20)
 #define AOS_SCRATCH_CTR_BYTES ((size_t)256 << 10)
-#define AOS_SCRATCH_FLAG_BYTES ((size_t)2 << 20)
+#define AOS_SCRATCH_FLAG_BYTES ((size_t)4 << 20)
 #define AOS_SCRATCH_WS_BYTES (AOS_SCRATCH_BYTES - AOS_SCRATCH_CTR_BYTES - AOS_SCRATCH_FLAG_BYTES)
 #define AOS_MAX_DEVICES 64
 static __device__ __align__(256) unsigned char scratch[AOS_SCRATCH_BYTES];
@@ -609,13 +609,14 @@ enum {
   KS_GEMM_DOWN,
   KS_GEMM_PROJ,
   KS_DECODE_MLP,
+  KS_MLP1,
   KS_COUNT
 };
 static const char *kStatNames[KS_COUNT] = {
     "route",         "lora_shrink_x",   "q4_gemv_gate_up", "lora_shrink_h",
     "q4_gemv_down",  "q4_gemv_proj",    "prefill_group_plan",
     "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj",
-    "decode_mlp"};
+    "decode_mlp", "mlp1"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -641,6 +642,8 @@ struct aoship_layer {
   bool producer_lines = true;    /* fused launches hand over through per-producer lines */
   bool plan_ptrs = true;         /* decode plans list the LoRA tables' row pointers */
   bool prefill_fused_shrink = true; /* prefill MLP: the LoRA shrinks run in the GEMM launches */
+  bool mlp1 = false;             /* one token: the MLP (and its routing) in one launch, down in LDS
+                                  * (opt-in: slower than the two launches so far) */
   /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
    * workgroup and K splits, 0 = chosen by the geometry (diagnostic) */
   int geo_wr[3] = {0, 0, 0}, geo_ks[3] = {0, 0, 0};
@@ -911,8 +914,9 @@ extern "C" int aoship_layer_wait_timeouts(aoship_layer_t *l) {
 extern "C" int aoship_internal_set_spin_limit(uint32_t polls) {
   if (ensure_device()) return -1;
   HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
-  int (*const setters[])(uint32_t) = {aos_spin_setter_router, aos_spin_setter_lora, aos_spin_setter_gemv,
-                                      aos_spin_setter_gemm,   aos_spin_setter_model, aos_spin_setter_liquid};
+  int (*const setters[])(uint32_t) = {aos_spin_setter_router, aos_spin_setter_lora,   aos_spin_setter_gemv,
+                                      aos_spin_setter_gemm,   aos_spin_setter_model,  aos_spin_setter_liquid,
+                                      aos_spin_setter_mlp1};
   for (auto *f : setters)
     if (f(polls) != (int)hipSuccess) return set_err("aoship_internal_set_spin_limit: hipMemcpyToSymbol failed");
   HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -965,6 +969,28 @@ extern "C" int aoship_internal_layer_set_decode_handoff(aoship_layer_t *l, int o
  * row pointers in the LoRA tables its GEMV readers use (default on: a reader then needs one load
  * for a pointer rather than two, and a fused launch's first expand step two round trips after its
  * wait). The loads change, the arithmetic does not: outputs are identical either way. */
+/* Diagnostic (no counterpart in the reference): copies bytes [offset, offset + bytes) of the layer's
+ * flag memory (where the one-token launch keeps its tagged exchange words) to dst on the host, after
+ * synchronising the device. Returns the flag memory's size, or -1. */
+extern "C" long aoship_internal_layer_read_flags(aoship_layer_t *l, size_t offset, size_t bytes, void *dst) {
+  if (!l) return set_err("aoship_internal_layer_read_flags: null layer");
+  if (ensure_device()) return -1;
+  HIP_OR_FAIL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  if (bytes) {
+    if (!dst || offset + bytes > l->flag_cap) return set_err("aoship_internal_layer_read_flags: out of range");
+    HIP_OR_FAIL(hipMemcpy(dst, (char *)l->flags.p + offset, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  }
+  return (long)l->flag_cap;
+}
+
+/* Diagnostic (no counterpart in the reference): the one-token MLP as one launch with the down
+ * matrix in LDS (default on where the layer's shape fits) or the two-launch path. */
+extern "C" int aoship_internal_layer_set_mlp1(aoship_layer_t *l, int on) {
+  if (!l) return set_err("aoship_internal_layer_set_mlp1: null layer");
+  l->mlp1 = on != 0;
+  return 0;
+}
+
 extern "C" int aoship_internal_layer_set_plan_pointers(aoship_layer_t *l, int on) {
   if (!l) return set_err("aoship_internal_layer_set_plan_pointers: null layer");
   l->plan_ptrs = on != 0;
@@ -1732,6 +1758,8 @@ static int chunk_prefill_t(int T) { return T < AOS_PREFILL_MAX_T ? T : AOS_PREFI
 static void size_proj(aoship_layer *l, const int *mods, int nm, int max_tokens, size_t &bytes, size_t &ctr,
                       size_t &flg);
 
+static size_t mlp1_flag_words(aoship_layer *l);
+
 extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
   if (!l) return set_err("aoship_layer_reserve: null layer");
   if (max_tokens < 1) return set_err("aoship_layer_reserve: max_tokens must be >= 1");
@@ -1746,6 +1774,10 @@ extern "C" int aoship_layer_reserve(aoship_layer_t *l, int max_tokens) {
       if (P.ctr > ctr) ctr = P.ctr;
       if (P.flg > flg) flg = P.flg;
     }
+  }
+  if (mlp) { /* the one-token launch's tagged words */
+    const size_t fw = mlp1_flag_words(l);
+    if (fw > flg) flg = fw;
   }
   if (mlp && max_tokens > AOS_DECODE_MAX_T) {
     MlpPrefill M;
@@ -1865,11 +1897,153 @@ static int launch_fused(aoship_layer *l, const Ws &w, const aos_shrink_params &s
   return launch_err(aos_launch_gemv_fused(&f, swiglu, &c), what);
 }
 
+/* ---- the one-token MLP launch (aoship_mlp1.hip) ---- */
+
+static int g_cu_count[AOS_MAX_DEVICES];
+
+static int device_cus() {
+  if (g_device < 0 || g_device >= AOS_MAX_DEVICES) return 0;
+  if (!g_cu_count[g_device]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, g_device) != hipSuccess) return 0;
+    g_cu_count[g_device] = n;
+  }
+  return g_cu_count[g_device];
+}
+
+#define AOS_MLP1_STATIC_LDS 2048 /* the kernel's static LDS (the router's selection arrays, flags), at most */
+
+/* Whether the one-token launch applies to this layer (its shape fits the LDS of two workgroups per
+ * CU, at most AOS_MLP1_MAXN adapters of rank <= AOS_MLP1_MAXR, the plain router when rp is set) and
+ * its parameters; flags == nullptr sizes its tagged words (flag_words, 32-bit words of the layer's
+ * flag memory). */
+static bool plan_mlp1(aoship_layer *l, const aos_route_params *rp, const uint16_t *x, const aoship_ring_t *ring,
+                      uint16_t *y, void *flags, aos_mlp1_params &q, size_t &flag_words) {
+  memset(&q, 0, sizeof(q));
+  flag_words = 0;
+  if (!l->mlp1 || l->separate_shrinks || l->one_launch_mlp || !l->producer_lines) return false;
+  const Q4Mat &Wg = l->mats[MOD_GATE], &Wu = l->mats[MOD_UP], &Wd = l->mats[MOD_DOWN];
+  const int H = Wg.in, I = Wg.out;
+  const int cus = device_cus();
+  if (cus <= 0) return false;
+  const int nwg = 2 * cus;
+  const long UG = (long)Wg.RB * Wg.G, UD = (long)Wd.RB * Wd.G;
+  /* the kernel forms unit indices and share bounds (units x waves) in 32 bits */
+  if (UG * 4L * nwg >= (1L << 32) || UD * (long)nwg >= (1L << 32)) return false;
+  if ((UG + 4L * nwg - 1) / (4L * nwg) > Wg.G) return false; /* a G wave spans at most two row blocks */
+  const int dmax = (int)((UD + nwg - 1) / nwg);
+  const int dwave = (dmax + 3) / 4;
+  if (dwave > AOS_MLP1_MAX_DU || dwave > Wd.G) return false;
+  const int slots = Wg.G > dmax ? Wg.G : dmax;
+  const int doff = ((128 + slots * 136) + 255) & ~255;
+  const int lds = doff + dmax * 1024;
+  if (lds + AOS_MLP1_STATIC_LDS > AOS_MLP1_LDS_MAX) return false;
+  const int n = (int)l->table.size();
+  const aos_lora_tab tg = lora_tab(l, MOD_GATE, H, I), tu = lora_tab(l, MOD_UP, H, I), td = lora_tab(l, MOD_DOWN, I, H);
+  if (n > AOS_MLP1_MAXN || tg.rpad > AOS_MLP1_MAXR || tu.rpad > AOS_MLP1_MAXR || td.rpad > AOS_MLP1_MAXR) return false;
+  if (rp && (rp->T != 1 || rp->n < 1 || rp->n > AOS_MLP1_MAXN || rp->d < 4 || rp->d % 4 || rp->scope || rp->tie_key ||
+             rp->post_allowed || rp->active_ids || rp->strengths || rp->hashes))
+    return false;
+  const int tiles_g = (n * tg.rpad + 31) / 32, tiles_u = (n * tu.rpad + 31) / 32;
+  const int rw4 = rp ? (rp->n + 3) / 4 * 4 : 0;
+  const int avail = 4 * nwg - rw4, tiles = tiles_g + tiles_u;
+  /* K pieces per x-shrink tile: at most two groups per wave (one round of loads), at most half the
+   * D waves (the rest expand gate/up row blocks) */
+  int ks = tiles ? avail / 2 / tiles : 1;
+  if (ks > (Wg.G + 1) / 2) ks = (Wg.G + 1) / 2;
+  if (ks < 1) return false;
+  if (4 * nwg - rw4 - tiles * ks < Wg.RB) return false; /* one D wave per gate/up row block's expand */
+  const int hc = 8 * td.rpad;
+  if (hc > nwg) return false;
+  Bump b(flags, (size_t)-1);
+  q.gpart = b.take<uint64_t>((size_t)4 * nwg * 64);
+  q.dpart = b.take<uint64_t>((size_t)4 * nwg * 32);
+  q.htag = b.take<uint64_t>((size_t)I);
+  q.hpart = b.take<uint64_t>((size_t)Wg.RB * (hc ? hc : 1));
+  q.ex = b.take<uint64_t>((size_t)Wg.RB * 64);
+  q.sh = b.take<uint64_t>((size_t)(hc ? hc : 1));
+  q.spart = b.take<uint64_t>((size_t)(tiles ? tiles : 1) * ks * 32);
+  q.sx = b.take<uint64_t>((size_t)(n ? n : 1) * (tg.rpad + tu.rpad + 1));
+  q.pri = b.take<uint64_t>(AOS_MLP1_MAXN);
+  q.ringt = b.take<uint64_t>(16);
+  flag_words = (b.off + 255) / 4;
+  q.wg = Wg.dev();
+  q.wu = Wu.dev();
+  q.wd = Wd.dev();
+  q.x = x;
+  q.y = y;
+  q.ring_in = ring;
+  if (rp) {
+    q.route = 1;
+    q.rp = *rp;
+  }
+  q.n = n;
+  q.bound = l->bound.as<const uint8_t>();
+  q.scale = l->scale_all.as<const float>();
+  q.tg = tg;
+  q.tu = tu;
+  q.td = td;
+  q.zero_row = l->zeros.as<uint16_t>();
+  q.nwg = nwg;
+  q.d_units_max = dmax;
+  q.doff = doff;
+  q.lds_bytes = lds;
+  q.x_tiles_g = tiles_g;
+  q.x_tiles_u = tiles_u;
+  q.x_ks = ks;
+  q.hc = hc;
+  q.timeout = l->wait_dev;
+  return true;
+}
+
+static size_t mlp1_flag_words(aoship_layer *l) {
+  aos_mlp1_params q;
+  size_t fw = 0;
+  aos_route_params rp;
+  memset(&rp, 0, sizeof(rp));
+  rp.T = 1;
+  rp.n = AOS_MLP1_MAXN;
+  rp.d = 4;
+  /* the largest size: with the router's waves taken */
+  if (!plan_mlp1(l, &rp, nullptr, nullptr, nullptr, nullptr, q, fw)) plan_mlp1(l, nullptr, nullptr, nullptr, nullptr, nullptr, q, fw);
+  return fw;
+}
+
+/* One token through the one-launch MLP, when it applies: 1 launched, 0 not applicable, -1 error.
+ * scratch: the allocation-free forward's memory (its tagged words in the scratch's flag region,
+ * which must hold them; no profiling events), else the layer's own flag memory. */
+static int mlp1_forward(aoship_layer *l, const uint16_t *x, const aoship_ring_t *ring, uint16_t *y,
+                        const aos_route_params *rp, const Ws *scratch) {
+  aos_mlp1_params q;
+  size_t fw = 0;
+  if (!plan_mlp1(l, rp, nullptr, nullptr, nullptr, nullptr, q, fw)) return 0;
+  void *flags = nullptr;
+  uint32_t *genc = &l->gen;
+  if (scratch) {
+    if (fw * 4 > AOS_SCRATCH_FLAG_BYTES) return 0;
+    flags = scratch->flg;
+    genc = scratch->gen;
+  } else {
+    if (ws_reserve(l, 0, 0, fw)) return -1;
+    flags = l->flags.p;
+  }
+  plan_mlp1(l, rp, x, ring, y, flags, q, fw);
+  q.gen = next_gen(genc);
+  aos_launch_ctx c = launch_ctx(l, KS_MLP1, !scratch);
+  if (launch_err(aos_launch_mlp1(&q, &c), rp ? "route + decode mlp (one launch)" : "decode mlp (one launch)"))
+    return -1;
+  return 1;
+}
+
 /* One decode chunk (T <= 32 tokens) of the MLP. rp (may be NULL): the plain router's parameters
  * for these tokens, which then run in the gate/up launch (rings written there); the caller has
  * checked that the gate/up launch is fused. */
 static int mlp_decode_chunk(aoship_layer *l, int Tc, const uint16_t *x, const aoship_ring_t *rings, uint16_t *y,
                             const aos_route_params *rp, const Ws *scratch = nullptr) {
+  if (Tc == 1 && l->mats[MOD_GATE].valid) {
+    const int r = mlp1_forward(l, x, rings, y, rp, scratch);
+    if (r) return r < 0 ? -1 : 0;
+  }
   MlpPlan P;
   Ws w;
   if (scratch) {

@@ -27,6 +27,32 @@ __device__ __forceinline__ f32x16 aos_mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+/* MFMA register lifetimes. An MFMA reads its A and B operands and writes all 16 result registers
+ * some cycles after it issues, later still when other waves' MFMAs occupy the SIMD's matrix core.
+ * The compiler (ROCm 7.2, gfx950) does not always allow for that: measured in the one-token MLP
+ * launch, (1) a VALU write into a result register of an in-flight 32x32x16 MFMA that the kernel
+ * never reads (at one token only register 0 of the 16 holds a token) was overwritten by the MFMA's
+ * write-back, and (2) a VALU write into the A operand registers of the MFMA issued just before it
+ * reached that MFMA; both gave deterministic wrong outputs only when other waves issued MFMAs on the
+ * same SIMD, and correct ones when the same code ran alone. The rule kept here: the registers of an
+ * MFMA's operands and of its whole result stay reserved until an instruction has read the result
+ * (which waits for the MFMA to complete). aos_mfma_hold(t), placed after the instructions that
+ * consume t, reads t[0] and passes all 16 registers to an empty asm statement; aos_mfma_done(t, a,
+ * b) does the same and keeps the operands a and b as well. Result holds cost no registers and are
+ * used wherever fewer than 16 result registers are read. Operand holds are used in the one-token
+ * MLP launch, where (2) was measured; in the streaming GEMV and shrink loops they would keep 32-48
+ * more registers live (three waves per SIMD to two, the 7B gate/up GEMV 25 to 34 us), and those
+ * kernels' outputs are checked run to run and against the oracle by the GPU tests instead. */
+__device__ __forceinline__ void aos_mfma_hold(const f32x16 &t) {
+  float u = t[0];
+  asm volatile("" : "+v"(u) : "v"(t));
+}
+
+__device__ __forceinline__ void aos_mfma_done(const f32x16 &t, const u32x4 &a, const u32x4 &b) {
+  float u = t[0];
+  asm volatile("" : "+v"(u) : "v"(t), "v"(a), "v"(b));
+}
+
 /* Token (row of the MFMA M dimension) held by accumulator register v in lane l. */
 __device__ __forceinline__ int aos_acc_m(int v, int lane) {
   return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
@@ -178,7 +204,9 @@ __device__ __forceinline__ void aos_raise(uint32_t *flag, uint32_t gen) {
  * translation unit holds its own copy of the variable (internal linkage) and defines a host setter
  * for it with AOS_DEFINE_SPIN_SETTER; the library's setter calls all of them. */
 #define AOS_SPIN_LIMIT_DEFAULT (1u << 24)
-static __device__ uint32_t aos_spin_limit_dev = AOS_SPIN_LIMIT_DEFAULT;
+/* constant memory: waits read it with a scalar load through the constant cache, not with a vector
+ * load that would queue behind the launch's streaming loads before every wait */
+static __constant__ uint32_t aos_spin_limit_dev = AOS_SPIN_LIMIT_DEFAULT;
 #define AOS_DEFINE_SPIN_SETTER(name)                                                        \
   extern "C" int name(uint32_t polls) {                                                     \
     return (int)hipMemcpyToSymbol(HIP_SYMBOL(aos_spin_limit_dev), &polls, sizeof(polls)); \

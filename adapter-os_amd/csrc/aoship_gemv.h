@@ -36,6 +36,7 @@ __device__ __forceinline__ void apply_group(const f32x16 &t, uint32_t sbv, const
     const float sx = xs[(m * GR + gl) * 2] + xs[(m * GR + gl) * 2 + 1];
     acc[v] = fmaf(s, t[v], fmaf(bp, sx, acc[v]));
   }
+  if (NV < 16) aos_mfma_hold(t);
 }
 
 /* bf16 pair from two floats, round to nearest even */
@@ -363,6 +364,7 @@ __device__ __forceinline__ void h_shrink_partial(const aos_gemv_params &p, int r
         else *dst = acc[v];
       }
     }
+    if (NV < 16) aos_mfma_hold(acc);
   }
 }
 
@@ -822,6 +824,10 @@ __device__ __forceinline__ void gemv_body(const aos_gemv_params &p, int rbg, int
     for (int v = 0; v < NV; ++v) {
       acc0[v] += f0[v];
       if (SW) acc1[v] += f1[v];
+    }
+    if (NV < 16) {
+      aos_mfma_hold(f0);
+      if (SW) aos_mfma_hold(f1);
     }
   }
 

@@ -265,6 +265,58 @@ typedef struct {
   float *rpri;          /* [T][AOS_ROUTE_PARTS_MAXN] */
 } aos_route_gu_params;
 
+/* The decode MLP of one token, with its routing when rp is set, in one launch (aoship_mlp1.hip).
+ * nwg = two workgroups per CU, all resident at once (LDS holds at most two), 8 waves each.
+ * Waves 0-3 stream an even share of the gate/up units (row block rb, group g; unit rb * G + g, in
+ * order) over all 4 nwg of them; waves 4-7 load their workgroup's share of the down matrix's
+ * units into LDS at the start and multiply it with h once h is complete. The first of waves 4-7
+ * also route the token (one wave per adapter's prior, the last of them routes) and form the x
+ * shrink S for every adapter (a wave per 32-column tile and K piece). Every value one wave hands
+ * to another is a 64-bit word (payload | gen << 32) stored device-coherently: the reader loads
+ * it until the stamp equals this launch's generation, so no producer waits for its stores. A row
+ * block's partial sums (gate/up or down) are summed by the wave holding its last unit (its
+ * owner), over the waves before it in order; the owner adds the LoRA expand (for gate/up formed
+ * ahead by otherwise idle waves, ex), and a gate/up owner forms h and its rows' part of the down
+ * shrink (hpart). The down shrink S_h is summed over the
+ * gate/up row blocks by one wave per column. The tagged buffers sit in the layer's flag memory
+ * (zero at rest, cleared when a given-up wait is reset). */
+#define AOS_MLP1_MAXN 64 /* adapters in the layer's table */
+#define AOS_MLP1_MAXR 64 /* padded rank of each module */
+#define AOS_MLP1_MAX_DU 20 /* down units per wave */
+#define AOS_MLP1_LDS_MAX (80 * 1024) /* two workgroups per CU */
+typedef struct {
+  aos_q4_dev wg, wu, wd;     /* gate, up, down */
+  const uint16_t *x;         /* [H] bf16 */
+  uint16_t *y;               /* [H] bf16 */
+  const aoship_ring_t *ring_in; /* the token's ring, when it is not routed in this launch */
+  int route;                 /* 1: routed in this launch by rp (the plain router, one token) */
+  aos_route_params rp;
+  int n;                     /* adapter table length */
+  const uint8_t *bound;      /* [n] */
+  const float *scale;        /* [n] */
+  aos_lora_tab tg, tu, td;   /* LoRA tables of gate, up, down */
+  const uint16_t *zero_row;  /* >= 256 zero bytes */
+  int nwg;
+  int d_units_max;           /* most down units one workgroup holds */
+  int doff;                  /* LDS offset of the down units */
+  int lds_bytes;
+  int x_tiles_g, x_tiles_u, x_ks; /* x shrink: 32-column tiles of gate and of up, K pieces */
+  int hc;                    /* h-shrink columns per gate/up row block in hpart (8 * td.rpad) */
+  /* tagged exchange words */
+  uint64_t *gpart;           /* [4 nwg][64] gate (lanes 0-31) / up (32-63) partials handed on */
+  uint64_t *dpart;           /* [4 nwg][32] down partials handed on */
+  uint64_t *htag;            /* [I] h (bf16 in the payload) */
+  uint64_t *hpart;           /* [RB_gate][hc] */
+  uint64_t *ex;              /* [RB_gate][64] LoRA expand of gate (words 0-31) and up (32-63) */
+  uint64_t *sh;              /* [hc] S_h */
+  uint64_t *spart;           /* [(x_tiles_g + x_tiles_u) x_ks][32] */
+  uint64_t *sx;              /* [n tg.rpad + n tu.rpad] S of every adapter: gate's, then up's */
+  uint64_t *pri;             /* [n] priors */
+  uint64_t *ringt;           /* [10] the ring's words */
+  uint32_t gen;
+  uint32_t *timeout;         /* set to 1 if a wait gave up (the launch still ends) */
+} aos_mlp1_params;
+
 /* q, k and v (or any n <= 3 matrices with the same x, T and waves) in one launch: matrix i owns
  * workgroups [wg_end[i - 1], wg_end[i]) of a 1-D grid, wg_end[i] - wg_end[i - 1] = RB_i * ks_i;
  * entries past n repeat wg_end[n - 1]. */
@@ -481,6 +533,8 @@ int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);
+int aos_launch_mlp1(const aos_mlp1_params *p, const aos_launch_ctx *ctx);
+int aos_spin_setter_mlp1(uint32_t polls);
 /* The wait bound of each translation unit's kernels on the current device (polls; hipError_t). */
 int aos_spin_setter_router(uint32_t polls);
 int aos_spin_setter_lora(uint32_t polls);

@@ -275,6 +275,7 @@ __device__ __forceinline__ bool shrink_block(const aos_shrink_params &p, int lrb
   lds_barrier();
 #pragma unroll
   for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc[v];
+  if (NV < 16) aos_mfma_hold(acc);
   lds_barrier();
   if (wave != 0) return false;
   float tot[NV];

@@ -274,12 +274,14 @@ def launch_names(kt: dict, combined: bool = False) -> dict:
     if not FUSED:
         return dict(kt)
     gu = ("route+" if combined else "") + "lora_shrink_x+q4_gemv_gate_up"
-    ren = {"q4_gemv_gate_up": gu, "q4_gemv_down": "lora_shrink_h+q4_gemv_down"}
+    ren = {"q4_gemv_gate_up": gu, "q4_gemv_down": "lora_shrink_h+q4_gemv_down",
+           "mlp1": ("route+" if combined else "") + "mlp1"}
     return {ren.get(k, k): v for k, v in kt.items() if k not in ("lora_shrink_x", "lora_shrink_h")}
 
 
 PROFILES = ROOT / "profiles"
 TRAFFIC_FILE = PROFILES / "q4_gemv_gate_up__qwen7b_decode_t1__hbm_traffic.md"
+MLP1_TRAFFIC_FILE = PROFILES / "mlp1__qwen7b_decode_t1__hbm_traffic.md"
 COPY_BYTES = 512 << 20
 
 
@@ -336,7 +338,7 @@ def measured_mfma_peak() -> float | None:
     return tf if tf > 0 else None
 
 
-def hbm_stream_probe(gate_up_b: int, down_b: int) -> dict | None:
+def hbm_stream_probe(gate_up_b: int, down_b: int, layer_b: int) -> dict | None:
     """What one launch can read from HBM here (the probe library's stream kernel: the decode GEMVs'
     pattern of contiguous 1 KiB chunks per wave, 4-wave workgroups, each timed launch after a 1 GiB
     read that evicts the caches; median of 7 launches). Reports the ceiling (1 GiB, best of the
@@ -372,20 +374,22 @@ def hbm_stream_probe(gate_up_b: int, down_b: int) -> dict | None:
         "down_bytes": best(down_b, grids),
         "gate_up_bytes_at_592_workgroups": best(gate_up_b, (592,), (4,)),
         "down_bytes_at_448_workgroups": best(down_b, (448,), (4,)),
+        "layer_bytes": best(layer_b, grids),
     }
     lib.aos_hbm_stream_free()
     res["two_launch_floor_us"] = res["gate_up_bytes"]["us"] + res["down_bytes"]["us"]
     res["note"] = ("plain streaming kernels, no compute: a lower bound for one launch per matrix; the "
                    "592- and 448-workgroup lines read the same bytes with the decode grids' workgroup "
-                   "counts (592 row blocks of gate/up; 448 down workgroups)")
+                   "counts (592 row blocks of gate/up; 448 down workgroups); layer_bytes: the whole "
+                   "layer's algorithmic bytes in one launch, the floor of the one-token launch")
     return res
 
 
-def measured_traffic():
-    """HBM bytes per launch of the gate/up GEMV from the committed counter summary, or None."""
-    if not TRAFFIC_FILE.exists():
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch of the headline kernel from its committed counter summary, or None."""
+    if not path.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
@@ -643,7 +647,14 @@ def main() -> int:
     cfg = dec.cfg
     layer_bytes = W.algorithmic_bytes(cfg, T, U)
     one_launch = "decode_mlp" in kt  # 1-2 tokens: the whole MLP is one launch
-    if one_launch:
+    if "mlp1" in kt:  # one token: the whole layer (and the router) in one launch, down matrix in LDS
+        gu_ms = kt["mlp1"]
+        gu_bytes = layer_bytes + (cfg.n_adapters + T) * cfg.hidden * 4 * dec.combined
+        rl_kernel = (("route+" if dec.combined else "") + "mlp1 (one launch: " +
+                     ("the router in the first waves, " if dec.combined else "") +
+                     "the LoRA x shrink, the int4 gate+up GEMV with the LoRA expand and SwiGLU, the down "
+                     "shrink, and the int4 down GEMV from LDS with its expand)")
+    elif one_launch:
         gu_ms = kt["decode_mlp"]
         gu_bytes = layer_bytes
         rl_kernel = ("decode_mlp (one launch: the LoRA x shrink and adapter plan, the int4 gate+up GEMV with "
@@ -691,7 +702,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": measured_traffic(),
+            "traffic": measured_traffic(MLP1_TRAFFIC_FILE if "mlp1" in kt else TRAFFIC_FILE),
             "algorithmic_bytes": gu_bytes,
             "avg_launch_us": gu_ms * 1e3,
         },
@@ -702,7 +713,8 @@ def main() -> int:
     }
     log(f"decode T=1 as two calls (route, then aoship_mlp_forward): {ms_two * 1e3:.1f} us/step")
     del dec
-    hp = hbm_stream_probe(gu_bytes, layer_bytes - gate_up_bytes(cfg, T, U))
+    hp = hbm_stream_probe(gate_up_bytes(cfg, T, U), layer_bytes - gate_up_bytes(cfg, T, U),
+                          layer_bytes + (cfg.n_adapters + T) * cfg.hidden * 4 * dec.combined)
     if hp:
         result["decode_hbm_probe"] = hp
         log("HBM stream probe: ceiling %.2f TB/s; one launch of %.1f MB %.1f us (%.2f TB/s), %.1f MB %.1f us "
@@ -711,6 +723,8 @@ def main() -> int:
                 hp["gate_up_bytes"]["tbps"], hp["down_bytes"]["bytes"] / 1e6, hp["down_bytes"]["us"],
                 hp["down_bytes"]["tbps"], hp["gate_up_bytes_at_592_workgroups"]["us"],
                 hp["down_bytes_at_448_workgroups"]["us"]))
+        log("HBM stream probe: the one-token launch's %.1f MB in one launch %.1f us" % (
+            hp["layer_bytes"]["bytes"] / 1e6, hp["layer_bytes"]["us"]))
 
     # ---- 8-token decode batch ----
     T8 = 8

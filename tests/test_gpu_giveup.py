@@ -1,8 +1,9 @@
 """GPU: the give-up path of the in-launch hand-offs. With the wait bound set to 0 polls
 (aoship_internal_set_spin_limit) every bounded wait of every launch gives up before its first poll,
 so each kernel skips what it waited for and still runs to its end. For each fused path (the
-two-launch decode MLP with per-producer lines and with the counted hand-off, the one-launch MLP, the
-router inside the gate/up launch, the allocation-free MLP, the q/k/v projections and the prefill
+two-launch decode MLP with per-producer lines and with the counted hand-off, the one-launch MLP of 1-2
+tokens, the one-token launch with the down matrix in LDS (plain and routed), the router inside the
+gate/up launch, the allocation-free MLP, the q/k/v projections and the prefill
 GEMMs with their tile shrinks): the forward that gave up is reported, the next forward on the layer
 is refused (-1), aoship_layer_wait_timeouts reports 1 and resets the layer (then 0), and a forward
 with the default bound equals the output from before the give-up bit for bit."""
@@ -97,16 +98,13 @@ def test_giveup_prefill(hip, T):
     _give_up(hip, layer, _mlp_runner(layer, 1, T))
 
 
-@pytest.mark.parametrize("T", [1, 8])
-def test_giveup_route_mlp(hip, T):
+def _route_mlp_runner(hip, layer, cid, T):
     import torch
 
-    cid = 2
     cfg = W.CONFIGS[cid]
     f, w = W.router_inputs(cfg, T)
     fd, wd, x = torch.from_numpy(f).cuda(), torch.from_numpy(w).cuda(), _x(cid, T)
     router = hip.Router(cfg.n_adapters, cfg.k, cfg.tau, cfg.eps, 1.0, np.arange(cfg.n_adapters, dtype=np.uint64))
-    layer, _ = gpu_layer(hip, cid)
 
     def run():
         rings = torch.zeros(T * 40, dtype=torch.uint8, device="cuda")
@@ -115,7 +113,20 @@ def test_giveup_route_mlp(hip, T):
         torch.cuda.synchronize()
         return np.concatenate([rings.cpu().numpy().view(np.uint8), y.cpu().numpy().view(np.uint8).ravel()])
 
-    _give_up(hip, layer, run)
+    return run
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_giveup_route_mlp(hip, T):
+    layer, _ = gpu_layer(hip, 2)
+    _give_up(hip, layer, _route_mlp_runner(hip, layer, 2, T))
+
+
+@pytest.mark.parametrize("routed", [False, True])
+def test_giveup_mlp1(hip, routed):
+    layer, _ = gpu_layer(hip, 2)
+    layer.set_mlp1(True)
+    _give_up(hip, layer, _route_mlp_runner(hip, layer, 2, 1) if routed else _mlp_runner(layer, 2, 1))
 
 
 @pytest.mark.parametrize("T", [2, 32])
