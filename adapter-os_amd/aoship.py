@@ -20,6 +20,13 @@ RING_DTYPE = np.dtype(
 )
 assert RING_DTYPE.itemsize == 40
 
+# aoship_decision_t: a Decision's entropy and candidates (decision order)
+DECISION_DTYPE = np.dtype(
+    [("entropy", "<f4"), ("n_candidates", "<u4"), ("adapter_idx", "<u2", (8,)), ("gate_q15", "<i2", (8,)),
+     ("raw_score", "<f4", (8,))]
+)
+assert DECISION_DTYPE.itemsize == 72
+
 MODULES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
 # name -> (restype, argtypes)
@@ -41,6 +48,7 @@ _SIGS = {
     "aoship_router_set_decision_policy": (C.c_int, [_P, _P, C.c_int]),
     "aoship_router_set_ring_mapping": (C.c_int, [_P, _P, _P]),
     "aoship_router_set_decision_hashing": (C.c_int, [_P, _P, C.c_int, _P, _P]),
+    "aoship_router_set_decision_output": (C.c_int, [_P, _P, C.c_int]),
     "aoship_blake3": (C.c_int, [_P, C.c_size_t, _P]),
     "aoship_router_free": (None, [_P]),
     "aoship_route": (C.c_int, [_P, _P, C.c_int, _P, _P]),
@@ -294,6 +302,14 @@ class Router:
         self._hashes = hashes  # keep the buffer alive while the router may write it
         _check(lib().aoship_router_set_decision_hashing(self.h, _ptr(hashes), cap, _hptr(r), _hptr(b)),
                "aoship_router_set_decision_hashing")
+
+    def set_decision_output(self, decisions) -> None:
+        """Each token's Decision entropy and candidates into decisions (a device uint8 tensor of
+        DECISION_DTYPE.itemsize bytes per token, read back with .view(DECISION_DTYPE); None = off)."""
+        cap = 0 if decisions is None else decisions.numel() * decisions.element_size() // DECISION_DTYPE.itemsize
+        self._decisions = decisions  # keep the buffer alive while the router may write it
+        _check(lib().aoship_router_set_decision_output(self.h, _ptr(decisions), cap),
+               "aoship_router_set_decision_output")
 
     def route(self, priors, rings, status=None) -> None:
         T = priors.shape[0]

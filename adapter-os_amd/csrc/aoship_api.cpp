@@ -224,6 +224,8 @@ struct aoship_router {
   int hash_max_tokens = 0;
   DevBuf hash_extra;         /* reasoning hash words 0-7, backend identity hash words 8-15 */
   int hash_reasoning = 0, hash_backend = 0;
+  aoship_decision_t *decisions = nullptr; /* caller's device buffer, [dec_max_tokens] */
+  int dec_max_tokens = 0;
   hipStream_t stream = nullptr;
 };
 
@@ -381,6 +383,14 @@ extern "C" int aoship_router_set_decision_hashing(aoship_router_t *r, uint8_t *h
   return 0;
 }
 
+extern "C" int aoship_router_set_decision_output(aoship_router_t *r, aoship_decision_t *decisions, int max_tokens) {
+  if (!r) return set_err("aoship_router_set_decision_output: null router");
+  if (decisions && max_tokens < 1) return set_err("aoship_router_set_decision_output: max_tokens must be >= 1");
+  r->decisions = decisions;
+  r->dec_max_tokens = decisions ? max_tokens : 0;
+  return 0;
+}
+
 extern "C" int aoship_router_set_ring_mapping(aoship_router_t *r, const uint16_t *active_ids,
                                               const float *strengths) {
   if (!r) return set_err("aoship_router_set_ring_mapping: null router");
@@ -441,6 +451,12 @@ static int route_fill(aoship_router_t *r, const float *features, const float *ro
     p.hash_extra = r->hash_extra.as<uint32_t>();
     p.hash_reasoning = r->hash_reasoning;
     p.hash_backend = r->hash_backend;
+  }
+  if (r->decisions) {
+    if (T > r->dec_max_tokens)
+      return set_err("aoship_route: T exceeds the decision-output buffer (" + std::to_string(r->dec_max_tokens) +
+                     " tokens)");
+    p.decisions = r->decisions;
   }
   if (features) {
     if (!router_w || d <= 0 || d % 4 != 0)
@@ -1942,7 +1958,7 @@ static bool plan_mlp1(aoship_layer *l, const aos_route_params *rp, const uint16_
   const aos_lora_tab tg = lora_tab(l, MOD_GATE, H, I), tu = lora_tab(l, MOD_UP, H, I), td = lora_tab(l, MOD_DOWN, I, H);
   if (n > AOS_MLP1_MAXN || tg.rpad > AOS_MLP1_MAXR || tu.rpad > AOS_MLP1_MAXR || td.rpad > AOS_MLP1_MAXR) return false;
   if (rp && (rp->T != 1 || rp->n < 1 || rp->n > AOS_MLP1_MAXN || rp->d < 4 || rp->d % 4 || rp->scope || rp->tie_key ||
-             rp->post_allowed || rp->active_ids || rp->strengths || rp->hashes))
+             rp->post_allowed || rp->active_ids || rp->strengths || rp->hashes || rp->decisions))
     return false;
   const int tiles_g = (n * tg.rpad + 31) / 32, tiles_u = (n * tu.rpad + 31) / 32;
   const int rw4 = rp ? (rp->n + 3) / 4 * 4 : 0;
@@ -2242,7 +2258,8 @@ extern "C" int aoship_route_mlp_forward(aoship_router_t *r, const float *feature
   if (ensure_device()) return -1;
   aos_route_params rp;
   if (route_fill(r, features, router_w, d, nullptr, T, rings, nullptr, status, rp)) return -1;
-  const bool plain = !(rp.scope || rp.tie_key || rp.post_allowed || rp.active_ids || rp.strengths || rp.hashes);
+  const bool plain =
+      !(rp.scope || rp.tie_key || rp.post_allowed || rp.active_ids || rp.strengths || rp.hashes || rp.decisions);
   if (T > AOS_DECODE_MAX_T || !plain) { /* routing first, then the layer, both on the layer's stream */
     aos_launch_ctx cr = {l->stream, nullptr, nullptr};
     if (launch_err(aos_launch_route(&rp, &cr), "route")) return -1;

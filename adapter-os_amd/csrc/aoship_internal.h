@@ -111,6 +111,7 @@ typedef struct {
   uint8_t *hashes;             /* [T][96] decision hashes (input, output, combined) */
   const uint32_t *hash_extra;  /* [16] reasoning hash words 0-7, backend identity hash words 8-15 */
   int hash_reasoning, hash_backend;
+  aoship_decision_t *decisions; /* [T] entropy and candidates */
 } aos_route_params;
 
 /* ---- LoRA shrink for T <= 32 tokens: S[t][col] = sum_i A_row(col)[i] x[t][i], float32 ----

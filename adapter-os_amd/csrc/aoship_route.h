@@ -215,6 +215,21 @@ __device__ __forceinline__ RouteMeta route_meta(const aos_route_params &p, int i
   return m;
 }
 
+/* An empty Decision record (entropy 0, no candidates) for token t. */
+__device__ __forceinline__ void decision_empty(aoship_decision_t *decisions, int t, int lane) {
+  if (!decisions) return;
+  aoship_decision_t *d = decisions + t;
+  if (lane < 8) {
+    d->adapter_idx[lane] = 0;
+    d->gate_q15[lane] = 0;
+    d->raw_score[lane] = 0.0f;
+  }
+  if (lane == 0) {
+    d->entropy = 0.0f;
+    d->n_candidates = 0u;
+  }
+}
+
 /* X: the extras (scope, adaptive keys, decision policy, ring mapping, decision hashes) are
  * compiled in; the X = false instance is the plain router, launched when none is set. first: the
  * lane's RouteMeta for adapter `lane`, loaded ahead (NULL: loaded here). */
@@ -228,6 +243,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
   const uint16_t *active_ids = X ? p.active_ids : nullptr;
   const float *strengths = X ? p.strengths : nullptr;
   uint8_t *hashes = X ? p.hashes : nullptr;
+  aoship_decision_t *decisions = X ? p.decisions : nullptr;
   /* every prior is checked for finiteness, allowed or not (validate_router_inputs); the chunked
    * passes below visit each index exactly once */
   bool bad = false;
@@ -303,6 +319,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     /* an empty decision under a decision policy is a PolicyViolation (policy_mask.rs:330-337) */
     ring_empty(ring, p.status, t, lane, any_bad ? -1 : (policy ? -2 : 0));
     hash_empty(hashes, t, lane);
+    decision_empty(decisions, t, lane);
     return;
   }
 
@@ -348,9 +365,22 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
   if (!(S > 0.0f)) {
     ring_empty(ring, p.status, t, lane, policy ? -2 : 0);
     hash_empty(hashes, t, lane);
+    decision_empty(decisions, t, lane);
     return;
   }
   const int e_q = e < kk ? quantize_q15(g / S) : 0;
+  /* compute_entropy (router.rs:1287-1293) of the renormalised gates g / S: -g log2(g) for g > 0,
+   * summed in float32 in top-K order; log2 in double precision, rounded to float */
+  float entropy = 0.0f;
+  if (decisions) {
+    const float gn = g / S;
+    const float term = gn > 0.0f ? -gn * (float)log2((double)gn) : 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float ts = aos_shfl_f(term, s), gs = aos_shfl_f(gn, s);
+      if (s < kk && gs > 0.0f) entropy += ts;
+    }
+  }
 
   /* Canonical order (router.rs:1310-1325): entry e's rank among the kk entries. */
   int rank = 0;
@@ -367,14 +397,17 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
   /* lane s < kk holds decision entry s (canonical order) */
   uint32_t my_i = 0;
   int my_q = 0;
+  float my_raw = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int ri = (int)aos_shfl((uint32_t)rank, i);
     const int qi = (int)aos_shfl((uint32_t)e_q, i);
     const uint32_t ii = aos_shfl(e_idx, i);
+    const float ri_sc = aos_shfl_f(e_sc, i);
     if (i < kk && ri == lane) {
       my_i = ii;
       my_q = qi;
+      my_raw = ri_sc;
     }
   }
   if (X && hashes) {
@@ -398,6 +431,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
                   hw[8] | hw[9] << 16, hw[10] | hw[11] << 16, hw[12] | hw[13] << 16, hw[14] | hw[15] << 16);
   }
   int m = kk;
+  int cand_q = my_q; /* a candidate keeps its gate from before a policy's renormalisation */
   if (X && policy) {
     /* filter_decision_by_policy (policy_mask.rs:221-355): passing entries keep decision order,
      * capped at max_adapters_per_token; anything removed renormalises the gates */
@@ -407,6 +441,7 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     if (p.post_max >= 0 && kept > p.post_max) kept = p.post_max;
     if (kept == 0) {
       ring_empty(ring, p.status, t, lane, -2);
+      decision_empty(decisions, t, lane);
       return;
     }
     /* slot s takes the s-th passing entry */
@@ -420,12 +455,27 @@ __device__ __forceinline__ void route_one(const aos_route_params &p, const float
     }
     my_i = aos_shfl(my_i, src);
     my_q = (int)aos_shfl((uint32_t)my_q, src);
+    my_raw = aos_shfl_f(my_raw, src);
     if (lane >= kept) {
       my_i = 0;
       my_q = 0;
     }
+    cand_q = my_q;
     if (kept < kk) my_q = renormalize_q15_lane(my_q, kept, lane);
     m = kept;
+  }
+  if (decisions) {
+    /* the Decision's candidates (types.rs:669-674) in decision order, and its entropy */
+    aoship_decision_t *d = decisions + t;
+    if (lane < 8) {
+      d->adapter_idx[lane] = (uint16_t)(lane < m ? my_i : 0u);
+      d->gate_q15[lane] = (int16_t)(lane < m ? cand_q : 0);
+      d->raw_score[lane] = lane < m ? my_raw : 0.0f;
+    }
+    if (lane == 0) {
+      d->entropy = entropy;
+      d->n_candidates = (uint32_t)m;
+    }
   }
   /* decision_to_router_ring_with_active_ids_and_strengths (router_bridge.rs:137-186) */
   uint32_t oi = my_i;

@@ -208,7 +208,8 @@ extern "C" int aos_launch_route_gate_up(const aos_route_gu_params *q, const aos_
   const int T = q->rp.T;
   if (T < 1 || T > AOS_DECODE_MAX_T || !q->rp.features || !q->route_done || !q->route_flag || !q->fp.gen)
     return (int)hipErrorInvalidValue;
-  if (q->rp.scope || q->rp.tie_key || q->rp.post_allowed || q->rp.active_ids || q->rp.strengths || q->rp.hashes)
+  if (q->rp.scope || q->rp.tie_key || q->rp.post_allowed || q->rp.active_ids || q->rp.strengths || q->rp.hashes ||
+      q->rp.decisions)
     return (int)hipErrorInvalidValue; /* the plain router only */
   if (!aos_fused_params_ok(&fp, 1) || fp.hsum || fp.gp[0].T != T || !fp.sp.plan_build.plan)
     return (int)hipErrorInvalidValue;
@@ -224,7 +225,8 @@ extern "C" int aos_launch_route_gate_up(const aos_route_gu_params *q, const aos_
 }
 
 extern "C" int aos_launch_route(const aos_route_params *p, const aos_launch_ctx *ctx) {
-  const bool x = p->scope || p->tie_key || p->post_allowed || p->active_ids || p->strengths || p->hashes;
+  const bool x =
+      p->scope || p->tie_key || p->post_allowed || p->active_ids || p->strengths || p->hashes || p->decisions;
   if (p->features) {
     const int waves = p->n < 16 ? p->n : 16;
     const size_t lds = (size_t)(p->d + p->n) * sizeof(float);

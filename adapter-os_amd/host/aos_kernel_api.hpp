@@ -168,9 +168,20 @@ struct RouterDeterminismConfig {
   bool enable_decision_hashing = true;
 };
 
+// DecisionCandidate (types.rs:669-674): a routed adapter with its raw score and Q15 gate.
+struct DecisionCandidate {
+  uint16_t adapter_idx = 0;
+  float raw_score = 0.0f;
+  int16_t gate_q15 = 0;
+};
+
+// Decision (types.rs:676-687): entropy is Router::compute_entropy of the renormalised gates
+// (router.rs:1287-1293), candidates are in decision order (after a policy: those that passed).
 struct Decision {
   std::vector<uint16_t> indices;
   std::vector<int16_t> gates_q15;
+  float entropy = 0.0f;
+  std::vector<DecisionCandidate> candidates;
   std::optional<DecisionHash> decision_hash;
 
   std::vector<float> gates_f32() const {
@@ -310,6 +321,8 @@ class Router {
     detail::check(aoship_router_set_decision_hashing(h_, config_.enable_decision_hashing ? d_hash_ : nullptr, 1,
                                                      nullptr, nullptr),
                   ErrorKind::Validation, "aoship_router_set_decision_hashing");
+    detail::check(aoship_router_set_decision_output(h_, d_dec_, 1), ErrorKind::Validation,
+                  "aoship_router_set_decision_output");
     const size_t n = info.size();
     detail::hip_check(hipMemcpy(d_priors_, priors.data(), n * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
     detail::check(aoship_route(h_, d_priors_, 1, d_ring_, d_status_), ErrorKind::Routing, "aoship_route");
@@ -320,6 +333,8 @@ class Router {
     detail::hip_check(hipMemcpy(&status, d_status_, sizeof(status), hipMemcpyDeviceToHost), "hipMemcpy");
     if (config_.enable_decision_hashing)
       detail::hip_check(hipMemcpy(hashes, d_hash_, 96, hipMemcpyDeviceToHost), "hipMemcpy");
+    aoship_decision_t rec;
+    detail::hip_check(hipMemcpy(&rec, d_dec_, sizeof(rec), hipMemcpyDeviceToHost), "hipMemcpy");
     if (status == -1) throw AosError(ErrorKind::DeterminismViolation, "non-finite prior or score");
     if (status == -2) throw AosError(ErrorKind::PolicyViolation, "Routing policy denied all adapters for this token");
     Decision d;
@@ -327,6 +342,9 @@ class Router {
       d.indices.push_back(ring.adapter_indices[i]);
       d.gates_q15.push_back(ring.gates_q15[i]);
     }
+    d.entropy = rec.entropy;
+    for (uint32_t i = 0; i < rec.n_candidates && i < 8; ++i)
+      d.candidates.push_back(DecisionCandidate{rec.adapter_idx[i], rec.raw_score[i], rec.gate_q15[i]});
     if (config_.enable_decision_hashing && ring.top_k > 0) {
       DecisionHash h;
       h.input_hash = det::B3Hash::hex(hashes, 8);
@@ -382,6 +400,7 @@ class Router {
     detail::hip_check(hipMalloc(&d_ring_, sizeof(aoship_ring_t)), "hipMalloc");
     detail::hip_check(hipMalloc(&d_status_, sizeof(int32_t)), "hipMalloc");
     detail::hip_check(hipMalloc(&d_hash_, 96), "hipMalloc");
+    detail::hip_check(hipMalloc(&d_dec_, sizeof(aoship_decision_t)), "hipMalloc");
     seed_.reset();
   }
   // Router::new sanitises tau and eps (router.rs:146-187); DecisionHash reports them.
@@ -425,6 +444,8 @@ class Router {
     if (d_status_) (void)hipFree(d_status_);
     if (d_hash_) (void)hipFree(d_hash_);
     d_hash_ = nullptr;
+    if (d_dec_) (void)hipFree(d_dec_);
+    d_dec_ = nullptr;
     d_priors_ = nullptr;
     d_ring_ = nullptr;
     d_status_ = nullptr;
@@ -446,6 +467,7 @@ class Router {
   aoship_ring_t *d_ring_ = nullptr;
   int32_t *d_status_ = nullptr;
   uint8_t *d_hash_ = nullptr;
+  aoship_decision_t *d_dec_ = nullptr;
   bool adaptive_ = false;
   RouterDeterminismConfig config_;
   std::optional<det::Bytes32> seed_;

@@ -147,6 +147,26 @@ int aoship_router_set_decision_hashing(aoship_router_t *router, uint8_t *hashes,
                                        const uint8_t *reasoning_hash,
                                        const uint8_t *backend_identity_hash);
 
+/* The Decision beyond its ring (types.rs:676-687): the Shannon entropy of the renormalised gates
+ * (Router::compute_entropy, router.rs:1287-1293, applied at :1844) and the candidates
+ * (DecisionCandidate: adapter index, raw score, Q15 gate), in decision order. After a decision
+ * policy the candidates are those that passed, with their gates from before the renormalisation,
+ * and the entropy is the router's (filter_decision_by_policy, policy_mask.rs:221-355). A token
+ * without a decision has entropy 0 and no candidates. */
+typedef struct {
+  float entropy;
+  uint32_t n_candidates;
+  uint16_t adapter_idx[8];
+  int16_t gate_q15[8];
+  float raw_score[8];
+} aoship_decision_t;
+
+/* With decisions != NULL, each later route call writes token t's Decision details to
+ * decisions[t] (device buffer of max_tokens entries, used until this is called again). The
+ * entropy's log2 is computed in double precision and rounded to float; the products and the sum
+ * are float32 in top-K order, as the reference's. decisions == NULL turns this off. Returns 0 / -1. */
+int aoship_router_set_decision_output(aoship_router_t *router, aoship_decision_t *decisions, int max_tokens);
+
 /* Stream (hipStream_t) for this router's launches; NULL = null stream. Returns 0 / -1. */
 int aoship_router_set_stream(aoship_router_t *router, void *stream);
 

@@ -185,10 +185,26 @@ int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const u
 int orc_route_one_ex(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
                      const uint8_t *scope, const uint64_t *breakers, int k, float tau, float eps,
                      float routing_bias, uint16_t idx_out[8], int16_t q15_out[8]) {
+  return orc_route_one_detail(priors, n, stable_id, allowed, scope, breakers, k, tau, eps, routing_bias, idx_out,
+                              q15_out, NULL, NULL);
+}
+
+/* orc_route_one_ex that also returns the decision's entropy and its candidates' raw scores (in
+ * decision order; the candidates' indices and Q15 gates are idx_out / q15_out). The entropy is
+ * Router::compute_entropy (router.rs:1287-1293) of the renormalised f32 gates, applied at
+ * router.rs:1844: the sum over gates g > 0, in top-K (score) order, of -g * log2(g) in f32, with
+ * the C library's log2f (what Rust's f32::log2 calls on this platform). An empty decision has
+ * entropy 0 (router.rs:2070). entropy_out / raw_out may be NULL. */
+int orc_route_one_detail(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
+                         const uint8_t *scope, const uint64_t *breakers, int k, float tau, float eps,
+                         float routing_bias, uint16_t idx_out[8], int16_t q15_out[8], float *entropy_out,
+                         float raw_out[8]) {
   for (int i = 0; i < 8; ++i) {
     idx_out[i] = 0;
     q15_out[i] = 0;
+    if (raw_out) raw_out[i] = 0.0f;
   }
+  if (entropy_out) *entropy_out = 0.0f;
   /* Router::new rejects k > MAX_K (router.rs:769-777); sanitize_k lifts 0 to 1 (:127-142). */
   if (k > ORC_MAX_K || n < 0) return -1;
   if (k < 1) k = 1;
@@ -261,6 +277,12 @@ int orc_route_one_ex(const float *priors, int n, const uint64_t *stable_id, cons
     return 0;
   }
   for (int i = 0; i < kk; ++i) g[i] /= s;
+  if (entropy_out) {
+    float h = 0.0f;
+    for (int i = 0; i < kk; ++i)
+      if (g[i] > 0.0f) h += -g[i] * log2f(g[i]);
+    *entropy_out = h;
+  }
 
   orc_final_t f[ORC_MAX_K];
   for (int i = 0; i < kk; ++i) {
@@ -274,6 +296,7 @@ int orc_route_one_ex(const float *priors, int n, const uint64_t *stable_id, cons
   for (int i = 0; i < kk; ++i) {
     idx_out[i] = (uint16_t)f[i].idx;
     q15_out[i] = f[i].q;
+    if (raw_out) raw_out[i] = f[i].raw;
   }
   return kk;
 }

@@ -96,6 +96,10 @@ int orc_route_one(const float *priors, int n, const uint64_t *stable_id, const u
 int orc_route_one_ex(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
                      const uint8_t *scope, const uint64_t *breakers, int k, float tau, float eps,
                      float routing_bias, uint16_t idx_out[8], int16_t q15_out[8]);
+int orc_route_one_detail(const float *priors, int n, const uint64_t *stable_id, const uint8_t *allowed,
+                         const uint8_t *scope, const uint64_t *breakers, int k, float tau, float eps,
+                         float routing_bias, uint16_t idx_out[8], int16_t q15_out[8], float *entropy_out,
+                         float raw_out[8]);
 
 /* renormalize_gates_q15 (policy_mask.rs:164-213): out[n]. */
 void orc_renormalize_q15(const int16_t *q, int n, int16_t *out);

@@ -53,6 +53,9 @@ def lib():
         L.orc_route_batch.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
         L.orc_route_one_ex.restype = C.c_int
         L.orc_route_one_ex.argtypes = [P, C.c_int, P, P, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P]
+        L.orc_route_one_detail.restype = C.c_int
+        L.orc_route_one_detail.argtypes = [P, C.c_int, P, P, P, P, C.c_int, C.c_float, C.c_float, C.c_float, P, P,
+                                           P, P]
         L.orc_renormalize_q15.restype = None
         L.orc_renormalize_q15.argtypes = [P, C.c_int, P]
         L.orc_filter_decision.restype = C.c_int
@@ -164,6 +167,23 @@ def route_one_ex(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None
     if kk < 0:
         raise ValueError("routing error (non-finite prior/score or k > 8)")
     return idx[:kk].tolist(), q[:kk].tolist()
+
+
+def route_one_detail(priors, k, tau=1.0, eps=0.02, routing_bias=1.0, stable_ids=None, allowed=None,
+                     scope=None, breakers=None):
+    """route_one_ex with the Decision's entropy and candidates: (indices, gates, raw_scores,
+    entropy), the candidates in decision order (aos_oracle.c: orc_route_one_detail)."""
+    p = _c(priors, np.float32)
+    arrs = [_opt(stable_ids, np.uint64), _opt(allowed, np.uint8), _opt(scope, np.uint8), _opt(breakers, np.uint64)]
+    idx = np.zeros(8, np.uint16)
+    q = np.zeros(8, np.int16)
+    raw = np.zeros(8, np.float32)
+    ent = np.zeros(1, np.float32)
+    kk = lib().orc_route_one_detail(p.ctypes.data, p.shape[0], *[_ptr(a) for a in arrs], k, tau, eps, routing_bias,
+                                    idx.ctypes.data, q.ctypes.data, ent.ctypes.data, raw.ctypes.data)
+    if kk < 0:
+        raise ValueError("routing error (non-finite prior/score or k > 8)")
+    return idx[:kk].tolist(), q[:kk].tolist(), raw[:kk].copy(), np.float32(ent[0])
 
 
 def renormalize_q15(gates) -> list[int]:

@@ -183,6 +183,29 @@ void gpu_tests() {
     Decision d3 = router2.route_with_adapter_info({}, priors, info, mask);
     CHECK(d1.indices == d3.indices && d1.gates_q15 == d3.gates_q15);
   });
+  run("test_entropy_computation", [] {  // router/tests/abstain_edge_cases.rs:121-162
+    Router router(3, 1.0f, 0.01f);
+    auto info = infos({0, 0, 0});
+    auto mask = PolicyMask::allow_all(3);
+    Decision d1 = router.route_with_adapter_info({}, {0.33f, 0.33f, 0.34f}, info, mask);
+    Decision d2 = router.route_with_adapter_info({}, {2.0f, 0.1f, 0.1f}, info, mask);
+    CHECK(d1.entropy > d2.entropy);
+    CHECK(d1.indices.size() == 3 && d2.indices.size() == 3);
+    CHECK(d1.candidates.size() == 3 && d1.candidates[0].adapter_idx == d1.indices[0]);
+    CHECK(d2.candidates[0].raw_score == 2.0f && d2.candidates[0].gate_q15 == d2.gates_q15[0]);
+  });
+  run("test_entropy_uniform_four", [] {  // compute_entropy of four equal gates: log2(4)
+    Router router(4, 1.0f, 0.02f);
+    Decision d = router.route_with_adapter_info({}, {0.5f, 0.5f, 0.5f, 0.5f}, infos({1, 2, 3, 4}),
+                                                PolicyMask::allow_all(4));
+    CHECK(d.entropy == 2.0f && d.candidates.size() == 4 && d.candidates[3].raw_score == 0.5f);
+  });
+  run("test_empty_decision_zero_entropy", [] {  // abstain_edge_cases.rs:60-76
+    Router router(2, 1.0f, 0.02f);
+    std::vector<AdapterInfo> info{{"adapter-1", 0}, {"adapter-2", 0}};
+    Decision d = router.route_with_adapter_info({}, {1.0f, 1.0f}, info, PolicyMask::deny(info, {"adapter-1", "adapter-2"}));
+    CHECK(d.indices.empty() && d.entropy == 0.0f && d.candidates.empty());
+  });
   run("test_score_sorting_descending_with_stable_id_tiebreak", [] {  // determinism.rs:537-574
     Router router(3, 1.0f, 0.01f);
     auto info = infos({10, 200, 100, 300, 400});

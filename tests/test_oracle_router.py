@@ -319,3 +319,82 @@ def test_exp_pinning():
         finally:
             oracle.set_exp(None)
         assert a.tobytes() == b.tobytes()
+
+
+# ---- the Decision's entropy and candidates (router.rs:1287-1293, 1844-1860; types.rs:669-687) ----
+
+def _softmax_entropy64(scores, tau=1.0):
+    """Entropy (bits) of softmax(scores / tau) in float64: the closed form the float32 result must
+    approach when the entropy floor is inactive."""
+    s = np.asarray(scores, np.float64) / tau
+    e = np.exp(s - s.max())
+    g = e / e.sum()
+    return float(-(g * np.log2(g)).sum())
+
+
+def test_entropy_uniform_is_log2_k():
+    for k in (1, 2, 4, 8):
+        idx, q, raw, h = oracle.route_one_detail(np.ones(k, np.float32), k)
+        assert len(idx) == k
+        assert h == np.float32(np.log2(k)), (k, h)  # g = 1/k exactly for these k
+        assert np.array_equal(raw, np.ones(k, np.float32))
+
+
+def test_entropy_three_equal_within_rounding_of_log2_3():
+    idx, q, raw, h = oracle.route_one_detail(np.zeros(3, np.float32), 3, eps=0.0)
+    assert abs(float(h) - np.log2(3.0)) < 4e-7
+
+
+def test_entropy_single_candidate_is_zero():
+    idx, q, raw, h = oracle.route_one_detail(np.array([3.0, -1.0, 0.5], np.float32), 1)
+    assert idx == [0] and q == [32767] and float(h) == 0.0 and raw.tolist() == [3.0]
+
+
+@pytest.mark.parametrize("d", [0.1, 0.7, 2.5, 6.0])
+def test_entropy_two_gates_matches_binary_entropy(d):
+    idx, q, raw, h = oracle.route_one_detail(np.array([d, 0.0, -50.0], np.float32), 2, eps=1e-6)
+    assert idx == [0, 1]
+    assert abs(float(h) - _softmax_entropy64([d, 0.0])) < 2e-6
+
+
+def test_entropy_random_softmax_matches_float64():
+    rng = np.random.default_rng(7)
+    for _ in range(50):
+        n = int(rng.integers(8, 40))
+        p = rng.standard_normal(n).astype(np.float32)
+        k = int(rng.integers(2, 9))
+        tau = float(rng.choice([0.5, 1.0, 2.0]))
+        idx, q, raw, h = oracle.route_one_detail(p, k, tau=tau, eps=1e-7)
+        top = np.sort(p)[::-1][:k]
+        assert abs(float(h) - _softmax_entropy64(top, tau)) < 4e-6 * max(1.0, float(h))
+
+
+def test_entropy_reference_uniform_above_skewed():
+    """abstain_edge_cases.rs:121-162: uniform priors give a higher entropy than skewed ones."""
+    _, _, _, h1 = oracle.route_one_detail(np.array([0.33, 0.33, 0.34], np.float32), 3, eps=0.01)
+    _, _, _, h2 = oracle.route_one_detail(np.array([2.0, 0.1, 0.1], np.float32), 3, eps=0.01)
+    assert h1 > h2
+
+
+def test_empty_decision_has_zero_entropy_and_no_candidates():
+    """abstain_edge_cases.rs:164-186 (and :60-76): no adapter, or none allowed."""
+    idx, q, raw, h = oracle.route_one_detail(np.zeros(0, np.float32), 3)
+    assert idx == [] and float(h) == 0.0 and raw.size == 0
+    idx, q, raw, h = oracle.route_one_detail(np.ones(4, np.float32), 3, allowed=np.zeros(4, np.uint8))
+    assert idx == [] and float(h) == 0.0
+
+
+def test_candidates_are_the_decision_with_raw_scores():
+    """router.rs:1848-1860: the candidates carry the top-K raw scores (scope and bias applied) in
+    the decision's order; the decision's indices and gates are the candidates'."""
+    rng = np.random.default_rng(3)
+    for _ in range(30):
+        n = int(rng.integers(4, 30))
+        p = rng.standard_normal(n).astype(np.float32)
+        scope = (rng.random(n) < 0.7).astype(np.uint8)
+        bias = float(rng.choice([1.0, 2.0, 0.5]))
+        idx, q, raw, h = oracle.route_one_detail(p, 4, routing_bias=bias, scope=scope)
+        i2, q2 = oracle.route_one_ex(p, 4, routing_bias=bias, scope=scope)
+        assert (idx, q) == (i2, q2)
+        want = np.where(scope[idx] != 0, p[idx], np.float32(-1.0e9)) * np.float32(bias)
+        assert np.array_equal(raw, want.astype(np.float32))
