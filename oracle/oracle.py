@@ -430,6 +430,40 @@ def attention(q, k, v, offset, mode=0):
     return out
 
 
+def _lora_coefs(rings, n_adapters, has):
+    """coef[t][a] = sum over token t's ring slots s < top_k naming adapter a (q > 0, a < n, the
+    module present) of q / 32767: add_lora_for_ring's rule (aos_oracle.c) as one matrix."""
+    rg = np.ascontiguousarray(rings, dtype=RING_DTYPE)
+    T = rg.shape[0]
+    coef = np.zeros((T, n_adapters), np.float32)
+    for t in range(T):
+        kk = min(int(rg[t]["top_k"]), 8)
+        for sl in range(kk):
+            q = int(rg[t]["gates_q15"][sl])
+            a = int(rg[t]["adapter_indices"][sl])
+            if q > 0 and a < n_adapters and has[a]:
+                coef[t, a] += np.float32(q) / np.float32(32767.0)
+    return coef
+
+
+def proj_forward_fast(x, w_deq, module, lora, scales, rings):
+    """proj_forward in float32 BLAS: x @ W^T with W dequantised once, plus each token's LoRA delta
+    scale[a] * coef[t][a] * B_a (A_a x_t) summed over the adapters. The same arithmetic as the C
+    oracle's, in another summation order (pinned against it by the oracle's own tests)."""
+    x = _c(x, np.float32)
+    y = x @ w_deq.T
+    n = len(lora)
+    has = [lora[a] is not None and lora[a].get(module) is not None for a in range(n)]
+    coef = _lora_coefs(rings, n, has)
+    for a in range(n):
+        if not has[a] or not coef[:, a].any():
+            continue
+        A, B = lora[a][module]
+        c = coef[:, a] * np.float32(scales[a])
+        y += ((x @ np.asarray(A, np.float32).T) @ np.asarray(B, np.float32).T) * c[:, None]
+    return y
+
+
 class ModelOracle:
     """mlx_model_forward_with_cache_and_lora (mlx_cpp_wrapper_real.cpp:3339-3527) on the CPU with its
     KV cache: embedding, per layer RMSNorm -> q/k/v (+bias, +LoRA) -> RoPE -> cache -> causal GQA
@@ -441,12 +475,19 @@ class ModelOracle:
     rope_theta, rms_eps. w: {"embed": (packed, scales, biases) or "embed_bf16": uint16 rows,
     "lm_head": (packed, scales, biases), "norm": [H], "layers": [{"input_norm", "post_norm",
     "q_proj" .. "down_proj": (packed, scales, biases), "bias": {"q_proj": [out] or None, ..}}]}.
-    lora[layer][a] = {module: (A, B)} for n adapters of one rank; scales[a] = alpha / rank."""
+    lora[layer][a] = {module: (A, B)} for n adapters of one rank; scales[a] = alpha / rank.
+
+    fast=True computes the projections and the MLP with the weights dequantised once and float32
+    BLAS products (proj_forward_fast) instead of the C loops; the rest (norms, RoPE, attention,
+    the LM head) is the same code. For model shapes where the C loops would take minutes."""
 
     ATTN = ("q_proj", "k_proj", "v_proj", "o_proj")
+    MODS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
-    def __init__(self, cfg, w, lora, scales, rank):
+    def __init__(self, cfg, w, lora, scales, rank, fast=False):
         self.cfg, self.w, self.lora, self.scales, self.rank = cfg, w, lora, scales, rank
+        self.fast = fast
+        self.deq = [{m: dequant(*lw[m]) for m in self.MODS} for lw in w["layers"]] if fast else None
         if "embed" in w:
             self.embed = dequant(*w["embed"])
         else:
@@ -469,7 +510,8 @@ class ModelOracle:
             normed = rmsnorm(x, lw["input_norm"], eps, mode)
             qkv = []
             for m in ("q_proj", "k_proj", "v_proj"):
-                y = proj_forward(normed, lw[m], m, self.ATTN, lo, self.scales, self.rank, rings, mode)
+                y = (proj_forward_fast(normed, self.deq[li][m], m, lo, self.scales, rings) if self.fast else
+                     proj_forward(normed, lw[m], m, self.ATTN, lo, self.scales, self.rank, rings, mode))
                 b = lw.get("bias", {}).get(m)
                 qkv.append(y + np.asarray(b, np.float32) if b is not None else y)
             q = rope(qkv[0].reshape(T, nh, hd), offset, c["rope_theta"])
@@ -478,6 +520,14 @@ class ModelOracle:
             self.kc[li] = np.concatenate([self.kc[li], k])
             self.vc[li] = np.concatenate([self.vc[li], v])
             a = attention(q, self.kc[li], self.vc[li], offset, mode).reshape(T, nh * hd)
+            if self.fast:
+                x = x + proj_forward_fast(a, self.deq[li]["o_proj"], "o_proj", lo, self.scales, rings)
+                normed = rmsnorm(x, lw["post_norm"], eps, mode)
+                g = proj_forward_fast(normed, self.deq[li]["gate_proj"], "gate_proj", lo, self.scales, rings)
+                u = proj_forward_fast(normed, self.deq[li]["up_proj"], "up_proj", lo, self.scales, rings)
+                h = (g * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g)))) * u
+                x = x + proj_forward_fast(h, self.deq[li]["down_proj"], "down_proj", lo, self.scales, rings)
+                continue
             x = x + proj_forward(a, lw["o_proj"], "o_proj", self.ATTN, lo, self.scales, self.rank, rings, mode)
             normed = rmsnorm(x, lw["post_norm"], eps, mode)
             x = x + mlp_forward(normed, lw["gate_proj"], lw["up_proj"], lw["down_proj"], lo, self.scales,

@@ -36,6 +36,24 @@ def report(name: str, y, ref) -> float:
     return ratio
 
 
+# ... and the norm-wise relative error ||y - ref|| / ||ref|| must stay within 2e-2 as well
+NORM_TOL = 2e-2
+
+
+def assert_parity(name: str, y, ref, rel_tol: float = REL_TOL, norm_tol: float = NORM_TOL) -> float:
+    """Prints both figures for this case and asserts them (finite outputs, the worst tolerance
+    ratio <= rel_tol, the norm-wise relative error <= norm_tol); returns the ratio."""
+    y = np.asarray(y, np.float64)
+    ratio = tol_ratio(y, ref)
+    ne = norm_rel_err(y, ref)
+    print(f"[parity] {name}: worst tolerance ratio {ratio:.4g} (limit {rel_tol}), "
+          f"norm-wise relative error {ne:.3g} (limit {norm_tol})", flush=True)
+    assert np.isfinite(y).all(), f"{name}: non-finite outputs"
+    assert ratio <= rel_tol, f"{name}: worst tolerance ratio {ratio:.4g}"
+    assert ne <= norm_tol, f"{name}: norm-wise relative error {ne:.3g}"
+    return ratio
+
+
 def tile_sample(perm, T: int, tile: int = 128):
     """Tokens at the first, middle and last sorted position of every tile of the grouped order."""
     pos = []

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import workloads as W
-from cases import REL_TOL, gpu_layer, oracle_mlp, oracle_proj, rings_for, tol_ratio
+from cases import REL_TOL, assert_parity, gpu_layer, oracle_mlp, oracle_proj, rings_for, tol_ratio
 
 pytestmark = pytest.mark.gpu
 
@@ -50,7 +50,7 @@ def test_mlp_decode_pinned_geometries(hip, cid, T):
         y2 = _mlp(layer, x, r, T, cfg.hidden)
         assert layer.wait_timeouts() == 0
         assert np.array_equal(y1, y2), f"gate/up {gu}, down {dn}: run-to-run outputs differ"
-        ratio = tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
+        ratio = assert_parity(f"test_mlp_decode_pinned_geometries cid={cid} T={T} gu={gu} dn={dn}", W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
         assert ratio <= REL_TOL, f"gate/up {gu}, down {dn}: tolerance ratio {ratio:.4g}"
 
 
@@ -82,5 +82,5 @@ def test_projections_pinned_geometries(hip, T):
                     assert np.array_equal(outs[m], cur[m]), f"wr {wr} ks {ks} {m}: run-to-run outputs differ"
             outs = cur
         for m in cfg.modules:
-            ratio = tol_ratio(W.bf16_bits_to_f32(outs[m]).reshape(refs[m].shape), refs[m])
+            ratio = assert_parity(f"test_projections_pinned_geometries T={T} wr={wr} ks={ks} {m}", W.bf16_bits_to_f32(outs[m]).reshape(refs[m].shape), refs[m])
             assert ratio <= REL_TOL, f"wr {wr} ks {ks} {m}: tolerance ratio {ratio:.4g}"

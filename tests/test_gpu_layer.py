@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import workloads as W
-from cases import REL_TOL, check_grouping, gpu_layer, oracle_mlp, oracle_proj, report, rings_for, tile_sample, tol_ratio
+from cases import REL_TOL, assert_parity, check_grouping, gpu_layer, oracle_mlp, oracle_proj, report, rings_for, tile_sample, tol_ratio
 
 pytestmark = pytest.mark.gpu
 
@@ -41,7 +41,7 @@ def test_mlp_decode_parity(hip, cid, T):
     assert layer.wait_timeouts() == 0
     assert np.array_equal(y1, y2), "run-to-run outputs differ"
     ref = oracle_mlp(cid, xf, rings)
-    ratio = tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
+    ratio = assert_parity(f"test_mlp_decode_parity cid={cid} T={T}", W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
 
 
@@ -61,7 +61,7 @@ def test_mlp_decode_unfused_launches(hip, T):
     layer.set_separate_shrinks(False)
     assert np.array_equal(y1, y2), "run-to-run outputs differ"
     ref = oracle_mlp(cid, xf, rings)
-    assert tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_mlp_decode_unfused_launches T={T}", W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
     assert np.array_equal(_run_mlp(hip, layer, xb, rings), fused)
 
 
@@ -85,7 +85,7 @@ def test_mlp_decode_handoff_variants(hip, T, one_launch, lines):
     assert layer.wait_timeouts() == 0
     assert np.array_equal(y1, y2), "run-to-run outputs differ"
     ref = oracle_mlp(cid, xf, rings)
-    assert tol_ratio(W.bf16_bits_to_f32(y1).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_mlp_decode_handoff_variants T={T} one_launch={one_launch} lines={lines}", W.bf16_bits_to_f32(y1).reshape(ref.shape), ref)
     assert np.array_equal(_run_mlp(hip, layer, xb, rings), default)
 
 
@@ -109,7 +109,7 @@ def test_decode_plan_pointer_lists(hip, T):
     assert layer.wait_timeouts() == 0
     assert np.array_equal(on, off), "MLP outputs differ with and without the plan's pointer lists"
     ref = oracle_mlp(cid, xf, rings)
-    assert tol_ratio(W.bf16_bits_to_f32(on).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_decode_plan_pointer_lists T={T}", W.bf16_bits_to_f32(on).reshape(ref.shape), ref)
 
     cid = 4
     cfg = W.CONFIGS[cid]
@@ -134,7 +134,7 @@ def test_decode_plan_pointer_lists(hip, T):
     for name, a, b in zip(cfg.modules, outs[0], outs[1]):
         assert np.array_equal(a, b), f"{name}: outputs differ with and without the plan's pointer lists"
         ref = oracle_proj(cid, name, xf, rings)
-        assert tol_ratio(W.bf16_bits_to_f32(a).reshape(ref.shape), ref) <= REL_TOL, name
+        assert_parity(f"test_decode_plan_pointer_lists T={T} {name}", W.bf16_bits_to_f32(a).reshape(ref.shape), ref)
 
 
 def test_mlp_no_adapters_matches_base(hip):
@@ -145,7 +145,7 @@ def test_mlp_no_adapters_matches_base(hip):
     layer, ads = gpu_layer(hip, cid)
     y = _run_mlp(hip, layer, xb, rings)
     ref = oracle_mlp(cid, xf, rings)
-    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_mlp_no_adapters_matches_base", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
 
 
 @pytest.mark.parametrize("T", [1, 8, 40])
@@ -159,7 +159,7 @@ def test_mlp_without_bound_adapters(hip, T):
     layer.set_adapters([])
     y = _run_mlp(hip, layer, xb, rings)
     ref = oracle_mlp(cid, xf, np.zeros(T, dtype=hip.RING_DTYPE))
-    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_mlp_without_bound_adapters T={T}", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
 
 
 def test_mlp_prefill_shape_parity(hip):
@@ -180,7 +180,7 @@ def test_mlp_prefill_shape_parity(hip):
     assert len(np.unique(np.argsort(perm)[sample] // 128)) == T // 128  # a token of every tile
     ref = oracle_mlp(cid, xf[sample], rings[sample])
     got = W.bf16_bits_to_f32(y.reshape(T, -1)[sample])
-    assert report(f"C3 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref) <= REL_TOL
+    assert_parity(f"C3 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref)
 
 
 def test_mlp_stress_32b_prefill(hip):
@@ -212,7 +212,7 @@ def test_mlp_stress_32b_prefill(hip):
     sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
     ref = oracle_mlp(cid, xf[sample], rings[sample])
     got = W.bf16_bits_to_f32(y1.cpu().numpy().view(np.uint16)[sample])
-    ratio = report(f"C5 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref)
+    ratio = assert_parity(f"C5 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
 
 
@@ -235,7 +235,7 @@ def test_mlp_prefill_shrink_modes(hip, cid, T):
     sample = np.arange(T) if T <= 300 else np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
     ref = oracle_mlp(cid, xf[sample], rings[sample])
     for fused in (True, False):
-        ratio = report(f"C{cid} prefill T={T} shrink fused={fused}", out[fused][sample], ref)
+        ratio = assert_parity(f"C{cid} prefill T={T} shrink fused={fused}", out[fused][sample], ref)
         assert ratio <= REL_TOL, f"fused={fused}: max tolerance ratio {ratio:.4g}"
     # float32 order changes flip some bf16 roundings of SA and h: a small fraction of the
     # tolerance (a wrong column or adapter would give ratios near 1)
@@ -252,7 +252,7 @@ def test_mlp_prefill_ragged_full_parity(hip, T):
     layer, ads = gpu_layer(hip, cid)
     y = _run_mlp(hip, layer, xb, rings)
     ref = oracle_mlp(cid, xf, rings)
-    ratio = tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
+    ratio = assert_parity(f"test_mlp_prefill_ragged_full_parity T={T}", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
 
 
@@ -270,7 +270,7 @@ def test_mlp_prefill_mixed_rings(hip):
     layer, ads = gpu_layer(hip, cid)
     y = _run_mlp(hip, layer, xb, rings)
     ref = oracle_mlp(cid, xf, rings)
-    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_mlp_prefill_mixed_rings", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
 
 
 @pytest.mark.parametrize("T", [5, 160])
@@ -291,7 +291,7 @@ def test_mlp_rings_naming_an_adapter_twice(hip, T):
     layer, ads = gpu_layer(hip, cid)
     y = _run_mlp(hip, layer, xb, rings)
     ref = oracle_mlp(cid, xf, rings)
-    assert tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref) <= REL_TOL
+    assert_parity(f"test_mlp_rings_naming_an_adapter_twice T={T}", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
 
 
 def test_projections_prefill_parity(hip):
@@ -315,7 +315,7 @@ def test_projections_prefill_parity(hip):
     for name, dev in (("q_proj", q), ("k_proj", k), ("v_proj", v), ("o_proj", o)):
         got = W.bf16_bits_to_f32(dev.cpu().numpy().view(np.uint16))
         ref = oracle_proj(cid, name, xf, rings)
-        ratio = tol_ratio(got.reshape(ref.shape), ref)
+        ratio = assert_parity(f"test_projections_prefill_parity {name}", got.reshape(ref.shape), ref)
         assert ratio <= REL_TOL, f"{name}: {ratio:.4g}"
 
 
@@ -392,7 +392,7 @@ def test_attention_projections_parity(hip, T, unfused):
     for name, dev in (("q_proj", q), ("k_proj", k), ("v_proj", v), ("o_proj", o)):
         got = W.bf16_bits_to_f32(dev.cpu().numpy().view(np.uint16))
         ref = oracle_proj(cid, name, xf, rings)
-        ratio = tol_ratio(got.reshape(ref.shape), ref)
+        ratio = assert_parity(f"test_attention_projections_parity T={T} unfused={unfused} {name}", got.reshape(ref.shape), ref)
         assert ratio <= REL_TOL, f"{name}: {ratio:.4g}"
 
 
@@ -429,5 +429,5 @@ def test_mlp_rank_not_multiple_of_16_and_missing_modules(hip, T):
     scales = np.full(cfg.n_adapters, W.lora_scale(cfg), np.float32)
     ref = oracle.mlp_forward(xf, base["gate_proj"], base["up_proj"], base["down_proj"], lora, scales, cfg.rank,
                              rings)
-    ratio = tol_ratio(W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
+    ratio = assert_parity(f"test_mlp_rank_not_multiple_of_16_and_missing_modules T={T}", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"

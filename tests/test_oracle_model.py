@@ -153,3 +153,24 @@ def test_model_oracle_cache_equals_full_prefill():
     full = m.forward(ids, rg)
     assert np.allclose(inc, full, rtol=1e-5, atol=1e-5)
     assert np.isfinite(full).all() and full.std() > 0.1
+
+
+def test_model_oracle_fast_path_equals_c_loops():
+    """ModelOracle(fast=True) (dequantised weights, float32 BLAS, per-adapter LoRA coefficients)
+    against the C loops on the same model: a prefill, decode steps and a continuation, rings
+    naming an adapter twice included; float32 with other summation orders."""
+    cfg, w, lora, scales, rank = tiny_model(seed=5, n_adapters=3)
+    rng = np.random.default_rng(11)
+    n = 30
+    ids = rng.integers(0, cfg["vocab"], n)
+    rg = rings(rng, n, len(scales))
+    rg[4]["top_k"] = 3
+    rg[4]["adapter_indices"][:3] = [1, 1, 2]
+    rg[4]["gates_q15"][:3] = [9000, 12000, 3000]
+    slow = oracle.ModelOracle(cfg, w, lora, scales, rank)
+    fast = oracle.ModelOracle(cfg, w, lora, scales, rank, fast=True)
+    for a, b in [(0, 9), (9, 10), (10, 11), (11, 30)]:
+        r0 = slow.forward(ids[a:b], rg[a:b])
+        r1 = fast.forward(ids[a:b], rg[a:b])
+        err = np.max(np.abs(r1 - r0)) / np.max(np.abs(r0))
+        assert err < 2e-5, (a, b, err)
