@@ -128,6 +128,10 @@ def lib():
         L.aoship_internal_layer_set_plan_pointers.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_set_prefill_shrink.restype = C.c_int
         L.aoship_internal_layer_set_prefill_shrink.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_set_prefill_sk.restype = C.c_int
+        L.aoship_internal_layer_set_prefill_sk.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_last_stream_k.restype = C.c_int
+        L.aoship_internal_layer_last_stream_k.argtypes = [_P]
         L.aoship_internal_layer_last_perm.restype = C.c_int
         L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
@@ -418,6 +422,22 @@ class Layer:
         LDS, where the layer's shape fits (off by default: the two-launch decode path is faster so
         far)."""
         _check(lib().aoship_internal_layer_set_mlp1(self.h, 1 if on else 0), "aoship_internal_layer_set_mlp1")
+
+    def set_prefill_sk(self, mask) -> None:
+        """Diagnostic: which prefill GEMMs may run as stream-K over the device's resident
+        workgroups (bit 0 gate/up, bit 1 down; True = both, the default) where the plan finds it
+        pays (no shrink workgroups in the launch, an idle tail in the plain grid), instead of one
+        workgroup per task."""
+        m = 3 if mask is True else (0 if mask is False else int(mask))
+        _check(lib().aoship_internal_layer_set_prefill_sk(self.h, m), "aoship_internal_layer_set_prefill_sk")
+
+    def last_stream_k(self) -> int:
+        """Diagnostic: the prefill GEMMs that ran as stream-K in the last prefill MLP (bit 0
+        gate/up, bit 1 down)."""
+        r = lib().aoship_internal_layer_last_stream_k(self.h)
+        if r < 0:
+            raise AosError(last_error())
+        return r
 
     def set_prefill_shrink(self, fused: bool) -> None:
         """Diagnostic: the prefill MLP's LoRA shrinks in the GEMM launches that consume them

@@ -658,6 +658,8 @@ struct aoship_layer {
   bool producer_lines = true;    /* fused launches hand over through per-producer lines */
   bool plan_ptrs = true;         /* decode plans list the LoRA tables' row pointers */
   bool prefill_fused_shrink = true; /* prefill MLP: the LoRA shrinks run in the GEMM launches */
+  int prefill_sk = 3;               /* prefill GEMMs as stream-K: bit 0 gate/up, bit 1 down */
+  int last_sk = 0;                  /* the GEMMs the last prefill MLP ran as stream-K (same bits) */
   bool mlp1 = false;             /* one token: the MLP (and its routing) in one launch, down in LDS
                                   * (opt-in: slower than the two launches so far) */
   /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
@@ -1011,6 +1013,23 @@ extern "C" int aoship_internal_layer_set_plan_pointers(aoship_layer_t *l, int on
   if (!l) return set_err("aoship_internal_layer_set_plan_pointers: null layer");
   l->plan_ptrs = on != 0;
   return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): which prefill GEMMs may run as stream-K over the
+ * device's resident workgroups (bit 0 gate/up, bit 1 down; both by default) where the plan finds
+ * it pays, instead of one workgroup per (token tile, row block) task. Results agree within
+ * float32 summation order; each form is deterministic run to run. */
+extern "C" int aoship_internal_layer_set_prefill_sk(aoship_layer_t *l, int mask) {
+  if (!l) return set_err("aoship_internal_layer_set_prefill_sk: null layer");
+  l->prefill_sk = mask & 3;
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): the prefill GEMMs that ran as stream-K in the
+ * layer's last prefill MLP (bit 0 gate/up, bit 1 down; of its last chunk of tokens). */
+extern "C" int aoship_internal_layer_last_stream_k(aoship_layer_t *l) {
+  if (!l) return set_err("aoship_internal_layer_last_stream_k: null layer");
+  return l->last_sk;
 }
 
 /* Diagnostic (no counterpart in the reference): whether the prefill MLP's LoRA shrinks run as
@@ -1712,6 +1731,31 @@ static void fuse_shrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const 
   g.timeout = l->wait_dev;
 }
 
+/* Stream-K for GEMM g (planned): its partial-sum slots and lines from the workspace, when
+ *  - the launch carries no shrink workgroups: those fill the plain grid's last round, and stream-K
+ *    over the slots they leave was slower (7B-shaped layer, 2048 tokens: gate/up 643 us against
+ *    562 us, down 323 us against 309 us);
+ *  - the plain grid's last round leaves at least a tenth of the resident set idle (what stream-K
+ *    wins back: 4096 tokens, gate/up 5.53 ms against 5.68 ms, down 1.59 ms against 1.67 ms);
+ *  - every workgroup gets at least AOS_SK_MIN_GROUPS K groups. */
+#define AOS_SK_MIN_GROUPS 16
+static void plan_sk(aoship_layer *l, Carve &cv, aos_gemm_params &g, bool swiglu) {
+  g.sk_nwg = 0;
+  if (!(l->prefill_sk & (swiglu ? 1 : 2)) || g.s_cols > 0) return;
+  const int wv = swiglu ? 4 : 8; /* the kernel shape's waves per workgroup */
+  const int slots = aos_gemm_sk_slots(swiglu ? 1 : 0) & ~7; /* one share per XCD */
+  if (slots <= 0) return;
+  const uint64_t tasks = (uint64_t)((g.T + AOS_GEMM_BM - 1) / AOS_GEMM_BM) * ((g.w0.RB + wv - 1) / wv);
+  const uint64_t last = tasks % (uint64_t)slots; /* workgroups of the plain grid's last round */
+  if (last == 0 || last * 10 >= (uint64_t)slots * 9) return;
+  const uint64_t total = tasks * (uint64_t)g.w0.G;
+  if (total / (uint64_t)slots < AOS_SK_MIN_GROUPS || total * (uint64_t)slots >= (1ull << 32)) return;
+  g.sk_nwg = slots;
+  g.sk_part = cv.b.take<float>((size_t)slots * aos_gemm_sk_slot_floats(swiglu ? 1 : 0));
+  g.sk_lines = cv.flag_lines((size_t)slots * 32);
+  g.timeout = l->wait_dev;
+}
+
 struct MlpPrefill {
   PrefillPlan P;
   aos_tshrink_params sx, sh;
@@ -1743,6 +1787,8 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
   plan_gemm(l, M.P, M.sh, Wd, nullptr, h, nullptr, perm, T, 2, 0, y, M.g2);
   if (M.fused_x) fuse_shrink(l, cv, M.P, M.sx, M.g1);
   if (M.fused_h) fuse_shrink(l, cv, M.P, M.sh, M.g2);
+  plan_sk(l, cv, M.g1, true);
+  plan_sk(l, cv, M.g2, false);
   if (M.P.lora && M.sh.nmod == 0) M.g2.out_perm = perm; /* h is in sorted order even without a down expand */
   if (M.P.lora && M.sx.nmod == 0) M.g1.in_perm = perm;
   M.bytes = cv.b.off + 256;
@@ -2195,11 +2241,12 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       l->last_perm_T = M.P.lora ? Tc : 0;
       if (launch_gplan(l, M.P)) return -1;
       if (!M.fused_x && launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
-      if (M.g1.s_cols) M.g1.gen = next_gen(&l->gen);
+      l->last_sk = (M.g1.sk_nwg ? 1 : 0) | (M.g2.sk_nwg ? 2 : 0);
+      if (M.g1.s_cols || M.g1.sk_nwg) M.g1.gen = next_gen(&l->gen);
       aos_launch_ctx c2 = launch_ctx(l, KS_GEMM_GU);
       if (launch_err(aos_launch_gemm(&M.g1, 1, &c2), "q4 gemm gate/up")) return -1;
       if (!M.fused_h && launch_tshrink(l, M.sh, KS_PSHRINK_H)) return -1;
-      if (M.g2.s_cols) M.g2.gen = next_gen(&l->gen);
+      if (M.g2.s_cols || M.g2.sk_nwg) M.g2.gen = next_gen(&l->gen);
       aos_launch_ctx c4 = launch_ctx(l, KS_GEMM_DOWN);
       if (launch_err(aos_launch_gemm(&M.g2, 0, &c4), "q4 gemm down")) return -1;
     }

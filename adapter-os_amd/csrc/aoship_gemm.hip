@@ -685,8 +685,10 @@ __global__ void __launch_bounds__(256) aos_tshrink_kernel(aos_tshrink_params p) 
 /* Expand K steps: the LoRA expand of a token tile runs as extra K steps of 64 union columns after
  * the weight groups: module 0's ceil(TU * rpad0 / 64) steps, then module 1's (SwiGLU). The token
  * operand is the tile's SA columns (coefficient-scaled shrink), the weight operand the union
- * adapters' B rows (bf16). LDS after the token tiles: 16 bytes of counts, then up to LBP B
- * pointers per module (loaded at kernel start while the tile union is small enough). */
+ * adapters' B rows (bf16). LDS after the token tiles: 16 bytes of flags (word 0: the stream-K
+ * owner's "every partial arrived"), then up to LBP B pointers per module (loaded at kernel start
+ * while the tile union is small enough). The GEMM kernels declare no static LDS: their dynamic
+ * area then starts at LDS address 0, where the token-tile DMA (M0-based) and the reads agree. */
 constexpr int LBP = 256;
 __host__ __device__ constexpr int gemm_aux() { return 16 + 2 * LBP * 8; }
 
@@ -1007,26 +1009,29 @@ __device__ __forceinline__ void tile_shrink_rows(const aos_gemm_params &p, unsig
   }
 }
 
-template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS = 0>
-__global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params p) {
+/* Roles of a piece [ga, gb) of a task's K groups: the whole task; the owner of a task split over
+ * workgroups (it holds group 0, adds the other pieces' partial sums, then runs the expand and the
+ * epilogue); a partial piece (its sums go to the workspace for the owner). */
+enum { GEMM_WHOLE = 0, GEMM_OWNER = 1, GEMM_PART = 2 };
+
+/* Stream-K: the task's pieces after the owner's, which hold its partial sums, and where they go. */
+struct SkCtx {
+  uint32_t v;          /* this workgroup's slot (its place in the launch's iteration order) */
+  uint32_t v_first;    /* owner: first contributing slot (v + 1) */
+  uint32_t v_last;     /* owner: last contributing slot */
+};
+
+/* One task (token tile mbi, weight block nbk) over K groups [ga, gb). */
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS>
+__device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned char *smem, int mbi, int nbk, int ga,
+                                          int gb, int role, const SkCtx &sk) {
   constexpr int MT = BM / 32;
   constexpr int TILE = BM * 128;
   constexpr int NT = 64 * WV;
   constexpr int NTILE = gemm_ntile<NS, LC>();
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, c = lane >> 5;
-  /* The launch's first mb * nbs workgroups are shrink workgroups (tile fastest): dispatched before
-   * every GEMM workgroup, which waits for them only after its K loop, so none waits on a
-   * workgroup that cannot start. */
-  const int nsh = p.mb * p.nbs;
-  if (NS > 0 && (int)blockIdx.x < nsh) { /* uniform */
-    tile_shrink_rows<WV, (NS > 0 ? NS : 2)>(p, smem, blockIdx.x % p.mb, blockIdx.x / p.mb, SW ? 2 : 1, wave, lane);
-    return;
-  }
-  int mbi, nbk;
-  gemm_tile_of(blockIdx.x - nsh, p.mb, p.nb, mbi, nbk);
   const int m0 = mbi * BM;
   const int G = p.w0.G, in = p.w0.in, RB = p.w0.RB;
 
@@ -1042,6 +1047,7 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
   const uint32_t *s0p = W0.sb + (size_t)r0 * G * 32 + i;
   const uint32_t *s1p = W1.sb + (size_t)r0 * G * 32 + i;
   const int row = r0 * 32 + i;
+  const int glast = gb - 1; /* groups past the piece are clamped to its last (never read) */
 
   f32x16 acc0[MT], acc1[MT];
 #pragma unroll
@@ -1050,16 +1056,18 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
     acc1[mt] = f32x16{};
   }
 
-  /* prologue: weight ring D groups deep (D divides G), first token tile */
+  /* prologue: weight ring D groups deep (slot d holds group ga + d, ga + d + D, ...), first
+   * token tile */
   u32x4 wq0[D], wq1[D];
   uint32_t ws0[D], ws1[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    wq0[d] = q0[(size_t)d * 64];
-    ws0[d] = s0p[(size_t)d * 32];
+    const int gd = ga + d < gb ? ga + d : glast;
+    wq0[d] = q0[(size_t)gd * 64];
+    ws0[d] = s0p[(size_t)gd * 32];
     if (SW) {
-      wq1[d] = q1[(size_t)d * 64];
-      ws1[d] = s1p[(size_t)d * 32];
+      wq1[d] = q1[(size_t)gd * 64];
+      ws1[d] = s1p[(size_t)gd * 32];
     }
   }
   /* Token tiles, NS == 0: LDS holds groups g and g + 1 (double buffer); registers hold the loads
@@ -1073,9 +1081,9 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
   Stager<NT> st0, st1;
   int voff[4] = {0, 0, 0, 0};
   auto dma = [&](int stage, int gx) {
-    /* tiles past the last group repeat it and are never read */
+    /* tiles past the piece's last group repeat it and are never read */
     tile_dma(p.x, p.T, in, smem + stage * TILE, wave, WV, DMA_N, voff[0], voff[1], voff[2], voff[3],
-             gx < G ? gx : G - 1);
+             gx < gb ? gx : glast);
   };
   if (NS) {
 #pragma unroll
@@ -1087,25 +1095,26 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
       voff[k] = (tok * in + ch * 8) * 2;
     }
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) dma(s, s);
+    for (int s = 0; s < NS - 1; ++s) dma((ga + s) % (NS ? NS : 1), ga + s);
   } else {
     st0.rows(p.in_perm, in, p.T, m0, tid);
-    st0.load(p.x, 0);
+    st0.load(p.x, ga);
     if (DB) {
 #pragma unroll
       for (int k = 0; k < Stager<NT>::CH; ++k) st1.off[k] = st0.off[k];
     }
   }
+  const bool expand = role != GEMM_PART;
   Expand<WV, SW ? 2 : 1, 4, 2> ex(p, smem, NTILE, wave, lane, m0, mbi, row);
-  ex.prefetch();
+  if (expand) ex.prefetch();
   if (!NS) {
-    st0.store(smem, tid);
+    st0.store(smem + (ga & 1) * TILE, tid);
     lds_barrier();
   }
 
-  /* token tile of weight group gx (clamped: the tiles staged past the last group are not read) */
-  auto stage = [&](Stager<NT> &st, const int gx) { st.load(p.x, gx < G ? gx : G - 1); };
-  if (DB) stage(st1, 1);
+  /* token tile of weight group gx (clamped: the tiles staged past the piece are not read) */
+  auto stage = [&](Stager<NT> &st, const int gx) { st.load(p.x, gx < gb ? gx : glast); };
+  if (DB) stage(st1, ga + 1);
   /* NS > 0: memory instructions a wave issues per group (the tile's DMA, then the ring refill);
    * waiting until no more than VM_AFTER are outstanding completes the DMA issued NS - 1 groups
    * earlier (at least that many were issued after it) */
@@ -1123,7 +1132,7 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
 #pragma unroll
       for (int s = 0; s < 4; ++s) f1[s] = dequant_word(wq1[d][s], sc, bi);
     }
-    const int gc = gn < G ? gn : G - 1;
+    const int gc = gn < gb ? gn : glast;
     wq0[d] = q0[(size_t)gc * 64];
     ws0[d] = s0p[(size_t)gc * 32];
     if (SW) {
@@ -1134,10 +1143,15 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
 
   /* one K group: ld receives group g + 2 (g + 1 without DB), sto holds group g + 1 */
   auto group = [&](const int g, const int d, Stager<NT> &ld, Stager<NT> &sto) {
-    if (NS) { /* tile g is in LDS once this wave's DMA of it completes and every wave has waited */
-      AOS_VM_WAIT_LE(VM_AFTER);
+    if (NS) { /* tile g is in LDS once this wave's DMA of it completes and every wave has waited;
+               * the piece's first group waits for every load (fewer than VM_AFTER may follow its
+               * tile's DMA there) */
+      if (g == ga)
+        AOS_VM_WAIT_LE(0);
+      else
+        AOS_VM_WAIT_LE(VM_AFTER);
       lds_barrier(); /* also: every wave is past its reads of the stage refilled next */
-      dma((g + NS - 1) % NS, g + NS - 1);
+      dma((g + NS - 1) % (NS ? NS : 1), g + NS - 1);
     }
     const unsigned char *tb = smem + (NS ? (g % (NS ? NS : 1)) : (g & 1)) * TILE;
     /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
@@ -1175,16 +1189,84 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
     }
   };
 
-  for (int g0 = 0; g0 < G; g0 += D) {
+  for (int g0 = ga; g0 < gb; g0 += D) {
     if (DB) {
 #pragma unroll
       for (int d = 0; d < D; d += 2) {
-        group(g0 + d, d, st0, st1);
-        group(g0 + d + 1, d + 1, st1, st0);
+        if (g0 + d < gb) group(g0 + d, d, st0, st1);
+        if (g0 + d + 1 < gb) group(g0 + d + 1, d + 1, st1, st0);
       }
     } else {
 #pragma unroll
-      for (int d = 0; d < D; ++d) group(g0 + d, d, st0, st0);
+      for (int d = 0; d < D; ++d)
+        if (g0 + d < gb) group(g0 + d, d, st0, st0);
+    }
+  }
+
+  constexpr int NMAT = SW ? 2 : 1;
+  if (role != GEMM_WHOLE) {
+    /* the pieces meet through the workspace: slot v holds [WV waves][NMAT][MT][4 quads][64 lanes]
+     * 16-byte words, stored and loaded device-coherently (the slots' workgroups sit on other XCDs) */
+    constexpr int PW = NMAT * MT * 4; /* 16-byte words per lane per wave */
+    const size_t slot_words = (size_t)WV * PW * 64;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.sk_part, (short)0, 0x7fffffff, 0x00020000);
+    if (role == GEMM_PART) {
+      const uint32_t base = (uint32_t)(sk.v * slot_words + (size_t)wave * PW * 64 + lane) * 16u;
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16 &a = m ? acc1[mt] : acc0[mt];
+            f32x4 w4 = {a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w4), rs,
+                                                   base + (uint32_t)(((m * MT + mt) * 4 + q) * 64 * 16), 0, SC1);
+          }
+      aos_mem_wait();
+      __syncthreads();
+      if (tid == 0) aos_raise(p.sk_lines + (size_t)sk.v * 32, p.gen);
+      return;
+    }
+    /* owner: the other pieces' sums, in slot order, added to this piece's */
+    volatile uint32_t *sk_ok = (volatile uint32_t *)(smem + NTILE * TILE); /* aux word 0 */
+    if (tid == 0) {
+      bool ok = true;
+      for (uint32_t u = sk.v_first; u <= sk.v_last && ok; ++u) ok = aos_wait_gen(p.sk_lines + (size_t)u * 32, p.gen);
+      if (!ok && p.timeout) __hip_atomic_store(p.timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      *sk_ok = ok ? 1u : 0u;
+    }
+    __syncthreads();
+    if (*sk_ok) {
+      for (uint32_t u = sk.v_first; u <= sk.v_last; ++u) {
+        const uint32_t base = (uint32_t)(u * slot_words + (size_t)wave * PW * 64 + lane) * 16u;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+          /* one matrix's words in flight together, then added; through __builtin_bit_cast: this
+           * compiler turns an ext_vector initialised straight from the builtin's result into
+           * element 0 for every element (one dword load) */
+          f32x4 w4[MT][4];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              w4[mt][q] = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                             rs, base + (uint32_t)(((m * MT + mt) * 4 + q) * 64 * 16), 0, SC1));
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            f32x16 &a = m ? acc1[mt] : acc0[mt];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              a[4 * q] += w4[mt][q].x;
+              a[4 * q + 1] += w4[mt][q].y;
+              a[4 * q + 2] += w4[mt][q].z;
+              a[4 * q + 3] += w4[mt][q].w;
+            }
+          }
+        }
+      }
     }
   }
 
@@ -1235,6 +1317,68 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params 
   }
 }
 
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS = 0>
+__global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_kernel(aos_gemm_params p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  /* The launch's first mb * nbs workgroups are shrink workgroups (tile fastest): dispatched before
+   * every GEMM workgroup, which waits for them only after its K loop, so none waits on a
+   * workgroup that cannot start. */
+  const int nsh = p.mb * p.nbs;
+  if (NS > 0 && (int)blockIdx.x < nsh) { /* uniform */
+    tile_shrink_rows<WV, (NS > 0 ? NS : 2)>(p, smem, blockIdx.x % p.mb, blockIdx.x / p.mb, SW ? 2 : 1, wave, lane);
+    return;
+  }
+  int mbi, nbk;
+  gemm_tile_of(blockIdx.x - nsh, p.mb, p.nb, mbi, nbk);
+  gemm_task<SW, D, DBT, APF, WV, OCC, LC, NS>(p, smem, mbi, nbk, 0, p.w0.G, GEMM_WHOLE, SkCtx{0u, 0u, 0u});
+}
+
+/* Stream-K form of the same GEMM: sk_nwg workgroups (as many as the device holds at once) share
+ * the launch's mb * nb tasks x G groups evenly, in an order where a task's groups are consecutive
+ * and the tasks run token tile fastest; the slots of one XCD (workgroup w runs on XCD w % 8) take
+ * consecutive ranges, so each XCD streams its own share of the weights. A workgroup's range cuts
+ * at most its first and last tasks: it hands the first one's sums on (partial) when the task
+ * started in an earlier slot, and owns its last one when that continues in later slots (the
+ * partial pieces of a range run first, so the owner, which finishes its range with that task,
+ * rarely waits). */
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS>
+__global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_sk_kernel(aos_gemm_params p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  static_assert(NS > 0, "stream-K needs the LDS-DMA token tiles");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int nsh = p.mb * p.nbs;
+  if ((int)blockIdx.x < nsh) { /* uniform */
+    tile_shrink_rows<WV, NS>(p, smem, blockIdx.x % p.mb, blockIdx.x / p.mb, SW ? 2 : 1, wave, lane);
+    return;
+  }
+  const uint32_t nw = (uint32_t)p.sk_nwg, w = blockIdx.x - nsh;
+  const uint32_t v = nw % 8 == 0 ? (w & 7u) * (nw / 8) + (w >> 3) : w;
+  const uint32_t G = (uint32_t)p.w0.G, total = (uint32_t)(p.mb * p.nb) * G; /* the host keeps total * nw < 2^32 */
+  auto slot_lo = [&](uint32_t s) { return s * total / nw; };
+  auto slot_of = [&](uint32_t it) { return ((it + 1) * nw - 1) / total; };
+  const uint32_t lo = slot_lo(v), hi = slot_lo(v + 1);
+  for (uint32_t it = lo; it < hi;) {
+    const uint32_t t = it / G, ga = it - t * G;
+    const uint32_t gb = hi - it < G - ga ? ga + (hi - it) : G;
+    int role = GEMM_WHOLE;
+    SkCtx sk{v, v + 1, v};
+    if (ga > 0) {
+      role = GEMM_PART;
+    } else if (gb < G) {
+      role = GEMM_OWNER;
+      sk.v_last = slot_of(t * G + G - 1);
+    }
+    if (it > lo) { /* the previous piece's loads (LDS DMA included) are complete before reuse */
+      aos_mem_wait();
+      __syncthreads();
+    }
+    gemm_task<SW, D, DBT, APF, WV, OCC, LC, NS>(p, smem, (int)(t % (uint32_t)p.mb), (int)(t / (uint32_t)p.mb), (int)ga,
+                                                (int)gb, role, sk);
+    it += gb - ga;
+  }
+}
+
 }  // namespace
 
 extern "C" int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx) {
@@ -1279,6 +1423,19 @@ static int launch_gemm_cfg(const aos_gemm_params *p, const aos_launch_ctx *ctx) 
   const size_t lds = (size_t)NTILE * BM * 128 + gemm_aux();
   const dim3 grid(q.mb * (q.nbs + q.nb)), block(64 * WV);
   const int G = q.w0.G;
+  if (q.sk_nwg > 0) {
+    if (NS == 0 || !q.sk_part || !q.sk_lines || !q.gen ||
+        (uint64_t)q.mb * q.nb * G * (uint64_t)q.sk_nwg >= (1ull << 32))
+      return (int)hipErrorInvalidValue;
+    const dim3 skg(q.mb * q.nbs + q.sk_nwg);
+    if (G % D == 0)
+      AOS_LAUNCH(ctx, (aos_gemm_sk_kernel<SW, D, DBT, APF, WV, OCC, LC, (NS > 0 ? NS : 2)>), skg, block, lds, q);
+    else if (G % 2 == 0)
+      AOS_LAUNCH(ctx, (aos_gemm_sk_kernel<SW, 2, DBT, APF, WV, OCC, LC, (NS > 0 ? NS : 2)>), skg, block, lds, q);
+    else
+      AOS_LAUNCH(ctx, (aos_gemm_sk_kernel<SW, 1, DBT, APF, WV, OCC, LC, (NS > 0 ? NS : 2)>), skg, block, lds, q);
+    return (int)hipGetLastError();
+  }
   if (G % D == 0)
     AOS_LAUNCH(ctx, (aos_gemm_kernel<SW, D, DBT, APF, WV, OCC, LC, NS>), grid, block, lds, q);
   else if (G % 2 == 0)
@@ -1321,6 +1478,27 @@ extern "C" int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu) {
   if (swiglu) return shrink_fits_cfg<true, 4, 2, 2, AOS_GEMM_NS_SW>(T, RB, s_cols);
   return shrink_fits_cfg<false, 8, 2, 4, AOS_GEMM_NS_ONE>(T, RB, s_cols);
 }
+
+/* Workgroups of one kernel shape resident at once on the current device (registers and LDS). */
+template <bool SW, int D, bool DBT, bool APF, int WV, int OCC, int LC, int NS>
+static int sk_slots_cfg() {
+  int dev = 0, cus = 0, per_cu = 0;
+  const size_t lds = (size_t)gemm_ntile<NS, LC>() * BM * 128 + gemm_aux();
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus < 1)
+    return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, aos_gemm_sk_kernel<SW, D, DBT, APF, WV, OCC, LC, NS>,
+                                                   64 * WV, lds) != hipSuccess || per_cu < 1)
+    return 0;
+  return cus * per_cu;
+}
+
+extern "C" int aos_gemm_sk_slots(int swiglu) {
+  if (swiglu) return sk_slots_cfg<true, 2, false, false, 4, 2, 2, AOS_GEMM_NS_SW>();
+  return sk_slots_cfg<false, 4, true, true, 8, 2, 4, AOS_GEMM_NS_ONE>();
+}
+
+extern "C" int aos_gemm_sk_slot_floats(int swiglu) { return (swiglu ? 4 * 2 : 8) * (BM / 32) * 16 * 64; }
 
 extern "C" int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx) {
   if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->mtiles != (p->T + BM - 1) / BM || (p->sa_mod_before < 0) ||

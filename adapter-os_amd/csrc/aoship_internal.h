@@ -417,6 +417,12 @@ typedef struct {
   uint32_t *sa_lines;        /* [mtiles] lines of 32 words, raised to gen */
   uint32_t gen;
   uint32_t *timeout;         /* set when a wait gave up */
+  /* Stream-K (sk_nwg > 0): sk_nwg workgroups, the device's resident capacity for the kernel shape,
+   * share the tasks' K groups evenly (aos_gemm_sk_slots); sk_part holds one slot of partial sums
+   * per workgroup (aos_gemm_sk_slot_floats floats), sk_lines one line of 32 words per workgroup. */
+  int sk_nwg;
+  float *sk_part;
+  uint32_t *sk_lines;
 } aos_gemm_params;
 
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
@@ -535,6 +541,10 @@ int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);
 int aos_launch_mlp1(const aos_mlp1_params *p, const aos_launch_ctx *ctx);
+/* The prefill GEMM's stream-K shape on the current device (swiglu: the gate/up kernel, else the
+ * single-matrix one): workgroups resident at once, and floats of partial sums per workgroup. */
+int aos_gemm_sk_slots(int swiglu);
+int aos_gemm_sk_slot_floats(int swiglu);
 int aos_spin_setter_mlp1(uint32_t polls);
 /* The wait bound of each translation unit's kernels on the current device (polls; hipError_t). */
 int aos_spin_setter_router(uint32_t polls);

@@ -3,8 +3,8 @@
 so each kernel skips what it waited for and still runs to its end. For each fused path (the
 two-launch decode MLP with per-producer lines and with the counted hand-off, the one-launch MLP of 1-2
 tokens, the one-token launch with the down matrix in LDS (plain and routed), the router inside the
-gate/up launch, the allocation-free MLP, the q/k/v projections and the prefill
-GEMMs with their tile shrinks): the forward that gave up is reported, the next forward on the layer
+gate/up launch, the allocation-free MLP, the q/k/v projections, the prefill
+GEMMs with their tile shrinks, and the stream-K prefill GEMMs): the forward that gave up is reported, the next forward on the layer
 is refused (-1), aoship_layer_wait_timeouts reports 1 and resets the layer (then 0), and a forward
 with the default bound equals the output from before the give-up bit for bit."""
 import numpy as np
@@ -96,6 +96,17 @@ def test_giveup_noalloc(hip):
 def test_giveup_prefill(hip, T):
     layer, _ = gpu_layer(hip, 1)
     _give_up(hip, layer, _mlp_runner(layer, 1, T))
+
+
+def test_giveup_prefill_stream_k(hip):
+    """The stream-K prefill GEMMs (7B-shaped layer, 1000 tokens, shrinks in launches of their
+    own): owners that give up waiting for the other pieces' partial sums still end."""
+    layer, _ = gpu_layer(hip, 3)
+    layer.set_prefill_shrink(False)
+    run = _mlp_runner(layer, 3, 1000)
+    run()
+    assert layer.last_stream_k() == 3
+    _give_up(hip, layer, run)
 
 
 def _route_mlp_runner(hip, layer, cid, T):

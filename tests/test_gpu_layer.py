@@ -242,6 +242,43 @@ def test_mlp_prefill_shrink_modes(hip, cid, T):
     assert tol_ratio(out[True], out[False]) <= REL_TOL / 2
 
 
+@pytest.mark.parametrize("case", ["unfused_shrink", "ragged", "no_adapters"])
+def test_mlp_prefill_stream_k(hip, case):
+    """The prefill GEMMs as stream-K: the device's resident workgroups share the (token tile, row
+    block) tasks' K groups evenly; a task cut between workgroups is finished by its owner, which
+    adds the other pieces' partial sums in order. 7B-shaped layer with the shrinks in launches of
+    their own at 2048 and 1000 tokens, and without adapters at 2048 (both GEMMs then run as
+    stream-K by default): both GEMMs ran as stream-K, the outputs are bit-identical run to run,
+    within tolerance of the oracle on every tile, no wait timed out, and equal to the one-task-per-
+    workgroup GEMMs up to float32 summation order."""
+    cid = 3
+    T = 1000 if case == "ragged" else 2048
+    xb, xf = W.activations(W.CONFIGS[cid], T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    if case == "no_adapters":
+        layer.set_adapters([])
+        rings_ref = np.zeros(T, dtype=hip.RING_DTYPE)
+    else:
+        layer.set_prefill_shrink(False)
+        rings_ref = rings
+    y = _run_mlp(hip, layer, xb, rings)
+    assert layer.last_stream_k() == 3, "the prefill GEMMs did not run as stream-K"
+    assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), "run-to-run outputs differ"
+    assert layer.wait_timeouts() == 0
+    perm = layer.last_perm() if case != "no_adapters" else np.arange(T)
+    layer.set_prefill_sk(False)
+    y_plain = _run_mlp(hip, layer, xb, rings)
+    assert layer.last_stream_k() == 0
+    layer.set_prefill_sk(True)
+    sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
+    ref = oracle_mlp(cid, xf[sample], rings_ref[sample])
+    got = W.bf16_bits_to_f32(y.reshape(T, -1)[sample])
+    assert_parity(f"C3 prefill stream-K {case} T={T}, {len(sample)} tokens", got, ref)
+    a, b = W.bf16_bits_to_f32(y).reshape(T, -1), W.bf16_bits_to_f32(y_plain).reshape(T, -1)
+    assert tol_ratio(a, b) <= REL_TOL / 2
+
+
 @pytest.mark.parametrize("T", [33, 100, 128, 129, 300])
 def test_mlp_prefill_ragged_full_parity(hip, T):
     """Prefill path at token counts around the 128-token tile (0.5B-shaped layer, every token
