@@ -712,9 +712,10 @@ def main() -> int:
                                 "note": "the router's launch, then aoship_mlp_forward"},
     }
     log(f"decode T=1 as two calls (route, then aoship_mlp_forward): {ms_two * 1e3:.1f} us/step")
+    # the step's bytes, with the router's fp32 weights and features when it routes in the call
+    step_bytes = layer_bytes + (cfg.n_adapters + T) * cfg.hidden * 4 * int(bool(dec.combined))
     del dec
-    hp = hbm_stream_probe(gate_up_bytes(cfg, T, U), layer_bytes - gate_up_bytes(cfg, T, U),
-                          layer_bytes + (cfg.n_adapters + T) * cfg.hidden * 4 * dec.combined)
+    hp = hbm_stream_probe(gate_up_bytes(cfg, T, U), layer_bytes - gate_up_bytes(cfg, T, U), step_bytes)
     if hp:
         result["decode_hbm_probe"] = hp
         log("HBM stream probe: ceiling %.2f TB/s; one launch of %.1f MB %.1f us (%.2f TB/s), %.1f MB %.1f us "
