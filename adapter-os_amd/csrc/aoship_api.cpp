@@ -1002,7 +1002,7 @@ extern "C" long aoship_internal_layer_read_flags(aoship_layer_t *l, size_t offse
 }
 
 /* Diagnostic (no counterpart in the reference): the one-token MLP as one launch with the down
- * matrix in LDS (default on where the layer's shape fits) or the two-launch path. */
+ * matrix in LDS where the layer's shape fits (off by default: the two-launch path is faster). */
 extern "C" int aoship_internal_layer_set_mlp1(aoship_layer_t *l, int on) {
   if (!l) return set_err("aoship_internal_layer_set_mlp1: null layer");
   l->mlp1 = on != 0;
