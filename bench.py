@@ -314,11 +314,15 @@ def probe(aoship, W, torch, layers: int) -> int:
 
 
 def probe_prefill(aoship, W, torch) -> int:
-    """Workload for the prefill counter runs: 6 steps of the 2048-token prefill."""
-    pf = MlpCase(aoship, W, 3, 2048, torch, 1)
-    for _ in range(6):
-        pf.step()
-    torch.cuda.synchronize()
+    """Workload for the prefill counter runs: 6 steps of the 2048-token prefill (C3), then 3 of the
+    4096-token stress prefill (C5, whose GEMMs run as stream-K and whose tile shrinks are launches of
+    their own, so its launches are told apart by kernel and grid)."""
+    for cid, T, n in ((3, 2048, 6), (5, 4096, 3)):
+        pf = MlpCase(aoship, W, cid, T, torch, 1)
+        for _ in range(n):
+            pf.step()
+        torch.cuda.synchronize()
+        del pf
     log("prefill probe done")
     return 0
 
