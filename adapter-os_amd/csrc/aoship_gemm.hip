@@ -768,13 +768,17 @@ struct Expand {
     j = l - (m ? n0 : 0);
   }
 
-  /* Runs the nls steps in chunks of LC steps within one module. A chunk's token tiles (the
-   * steps' SA columns, through a buffer resource over the tile's rows; chunks past the union
-   * read as zeros) go straight from memory to LDS regions 0 .. LC - 1, its B fragments to
-   * registers; one wait per chunk, the next chunk's B pointers loading meanwhile. mma(m, n, bv)
-   * adds the chunk's n steps of module m (token tile q at smem + q * TILE). */
-  template <int LC, class Mma>
-  __device__ void run(const int (&koff)[NW], Mma &&mma) {
+  /* Runs the nls steps. With the union's B pointers in LDS: pipelined over the NT token-tile
+   * stages, as the weight groups are: step l's token tile (its SA columns, through a buffer resource
+   * over the tile's rows; columns past the union read as zeros) goes straight from memory to stage
+   * l % NT, NT - 1 steps ahead of its use, its B fragments to a register ring NT - 1 deep, and each
+   * step waits only for its own loads (a counted vmcnt: steps past the last re-load the last
+   * step's operands, so that the count holds to the end), one pipeline per module. mma1(mc, tile,
+   * bv) adds one step of module mc (a std::integral_constant). Otherwise in chunks of LC steps within one module with one wait per chunk, the next
+   * chunk's B pointers loading meanwhile: mma(m, n, bv) adds the chunk's n steps of module m (token
+   * tile q at smem + q * TILE). */
+  template <int LC, int NT, class Mma, class Mma1>
+  __device__ void run(const int (&koff)[NW], Mma &&mma, Mma1 &&mma1) {
     if (nls == 0) return;
     if (p.nbs && threadIdx.x == 0) { /* SA comes from this launch's shrink workgroups */
       if (!aos_wait_gen(p.sa_lines + (size_t)mbi * 32, p.gen) && p.timeout)
@@ -836,6 +840,44 @@ struct Expand {
               rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, 0);
       }
     };
+    if constexpr (NT >= 3) if (bp_lds) {
+      constexpr int VMS = BM / 8 / WV + NW; /* memory instructions a wave issues per step */
+      /* one pipeline per module (its steps lo .. hi - 1), the module a constant in each */
+      auto pipe = [&](auto mc, int lo, int hi) {
+        if (lo >= hi) return;
+        u32x4 bq[NT - 1][NW];
+        const uint16_t *pq[NP];
+#pragma unroll
+        for (int k = 0; k < NT - 1; ++k) {
+          dma_tile(k, lo + k);
+          load_ptrs(lo + k, pq);
+          load_frags(lo + k, pq, bq[k]);
+        }
+        for (int base = 0; base < hi - lo; base += NT - 1) {
+#pragma unroll
+          for (int d = 0; d < NT - 1; ++d) {
+            const int k = base + d;
+            if (k < hi - lo) {
+              /* step k's tile and fragments are in (this wave's loads, then every wave's after
+               * the barrier); every wave is past its reads of step k - 1's stage, refilled next */
+              asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VMS * (NT - 2)) : "memory");
+              lds_barrier();
+              const int kn = k + NT - 1;
+              dma_tile(kn % NT, lo + kn);
+              load_ptrs(lo + kn, pq);
+              mma1(mc, smem + (k % NT) * TILE, bq[d]);
+              load_frags(lo + kn, pq, bq[d]);
+            }
+          }
+        }
+        /* the loads past the last step land before the LDS is used again */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+      };
+      pipe(std::integral_constant<int, 0>{}, 0, n0);
+      if (NM > 1) pipe(std::integral_constant<int, 1>{}, n0, nls);
+      return;
+    }
     const uint16_t *pr[LC][NP];
     auto chunk_ptrs = [&](int l) {
       const int e = l < n0 ? n0 : nls;
@@ -1288,12 +1330,30 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
         }
       }
     };
-    ex.template run<LC>(koff, [&](int m, int n, const u32x4 (&bv)[LC][4]) {
-      if (!SW || m == 0)
-        mma_into(n, bv, acc0);
-      else
-        mma_into(n, bv, acc1);
-    });
+    auto mma_step = [&](const unsigned char *tb, const u32x4 (&bv)[4], f32x16 (&acc)[MT]) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4 a[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) a[mt] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = aos_mfma32(a[mt], bv[s], acc[mt]);
+      }
+    };
+    ex.template run<LC, (SW ? 0 : NTILE)>(
+        koff,
+        [&](int m, int n, const u32x4 (&bv)[LC][4]) {
+          if (!SW || m == 0)
+            mma_into(n, bv, acc0);
+          else
+            mma_into(n, bv, acc1);
+        },
+        [&](auto mc, const unsigned char *tb, const u32x4 (&bv)[4]) {
+          if constexpr (!SW || decltype(mc)::value == 0)
+            mma_step(tb, bv, acc0);
+          else
+            mma_step(tb, bv, acc1);
+        });
   }
 
   /* epilogue: sorted row m0 + r goes to output row out_perm[m0 + r] (or m0 + r) */
