@@ -510,6 +510,7 @@ struct LoraModule {
   bool valid = false;
   int rank = 0, rpad = 0, in = 0, out = 0;
   DevBuf A, B; /* bf16 [rpad][in], [out][rpad] */
+  DevBuf Bf;   /* B in fragment order [out / 32][rpad / 8][32][8] (the prefill GEMMs') */
 };
 
 struct aoship_lora_adapter {
@@ -562,9 +563,14 @@ extern "C" int aoship_lora_adapter_set_module(aoship_lora_adapter_t *a, int laye
   for (int o = 0; o < out_features; ++o)
     for (int j = 0; j < rank; ++j)
       B[(size_t)o * rpad + j] = f32_to_bf16(lora_b[(size_t)o * rank + j]);
+  std::vector<uint16_t> Bf(B.size(), 0);
+  for (int o = 0; o < out_features; ++o)
+    for (int j = 0; j < rpad; ++j)
+      Bf[((size_t)(o / 32) * (rpad / 8) + j / 8) * 256 + (o % 32) * 8 + j % 8] = B[(size_t)o * rpad + j];
   LoraModule &lm = a->mods[(size_t)layer_idx * AOS_MAX_MODULES + m];
   if (lm.A.upload(A.data(), A.size() * 2)) return -1;
   if (lm.B.upload(B.data(), B.size() * 2)) return -1;
+  if (lm.Bf.upload(Bf.data(), Bf.size() * 2)) return -1;
   lm.valid = true;
   lm.rank = rank;
   lm.rpad = rpad;
@@ -597,7 +603,7 @@ struct Q4Mat {
 
 struct ModTable {
   int rpad = 0, in = 0, out = 0;
-  DevBuf A, B, scale;
+  DevBuf A, B, Bf, scale;
 };
 
 struct KStat {
@@ -778,6 +784,7 @@ static void unbind_all(aoship_layer *l) {
   for (auto &t : l->tabs) {
     t.A.release();
     t.B.release();
+    t.Bf.release();
     t.scale.release();
     t.rpad = 0;
   }
@@ -811,7 +818,7 @@ extern "C" int aoship_layer_set_adapters(aoship_layer_t *l, aoship_lora_adapter_
     ModTable &t = l->tabs[m];
     t.rpad = rp[m];
     if (rp[m] == 0 || n == 0) continue;
-    std::vector<const void *> A((size_t)n, nullptr), B((size_t)n, nullptr);
+    std::vector<const void *> A((size_t)n, nullptr), B((size_t)n, nullptr), Bf((size_t)n, nullptr);
     std::vector<float> sc((size_t)n, 0.0f);
     for (int a = 0; a < n; ++a) {
       aoship_lora_adapter *ad = table[a];
@@ -820,12 +827,14 @@ extern "C" int aoship_layer_set_adapters(aoship_layer_t *l, aoship_lora_adapter_
       if (!lm.valid) continue;
       A[a] = lm.A.p;
       B[a] = lm.B.p;
+      Bf[a] = lm.Bf.p;
       sc[a] = ad->scale;
       t.in = lm.in;
       t.out = lm.out;
     }
     if (t.A.upload(A.data(), A.size() * sizeof(void *))) return -1;
     if (t.B.upload(B.data(), B.size() * sizeof(void *))) return -1;
+    if (t.Bf.upload(Bf.data(), Bf.size() * sizeof(void *))) return -1;
     if (t.scale.upload(sc.data(), sc.size() * sizeof(float))) return -1;
   }
   std::vector<uint8_t> bd((size_t)(n > 0 ? n : 1), 0);
@@ -858,6 +867,7 @@ static aos_lora_tab lora_tab(const aoship_layer *l, int m, int in, int out) {
   t.rpad = mt.rpad;
   t.A = mt.A.as<const uint16_t *const>();
   t.B = mt.B.as<const uint16_t *const>();
+  t.Bf = mt.Bf.as<const uint16_t *const>();
   t.scale = mt.scale.as<const float>();
   return t;
 }
@@ -1745,7 +1755,12 @@ static void plan_sk(aoship_layer *l, Carve &cv, aos_gemm_params &g, bool swiglu)
   const int wv = swiglu ? 4 : 8; /* the kernel shape's waves per workgroup */
   const int slots = aos_gemm_sk_slots(swiglu ? 1 : 0) & ~7; /* one share per XCD */
   if (slots <= 0) return;
-  const uint64_t tasks = (uint64_t)((g.T + AOS_GEMM_BM - 1) / AOS_GEMM_BM) * ((g.w0.RB + wv - 1) / wv);
+  const int mb = (g.T + AOS_GEMM_BM - 1) / AOS_GEMM_BM;
+  /* with a multiple of 8 token tiles the plain grid gives each XCD its own tiles (interleaved),
+   * which balances tiles whose adapter unions differ in size; stream-K's equal shares of K groups
+   * do not (a tile's expand steps fall to whichever workgroup ends its tasks) */
+  if (mb % 8 == 0) return;
+  const uint64_t tasks = (uint64_t)mb * ((g.w0.RB + wv - 1) / wv);
   const uint64_t last = tasks % (uint64_t)slots; /* workgroups of the plain grid's last round */
   if (last == 0 || last * 10 >= (uint64_t)slots * 9) return;
   const uint64_t total = tasks * (uint64_t)g.w0.G;

@@ -453,7 +453,7 @@ __global__ void __launch_bounds__(GP_NT) aos_gplan_kernel(aos_gplan_params p) {
         const aos_lora_tab &tb = p.tab[k];
         const bool has = tb.rpad && a < tb.n;
         p.ap[(size_t)k * mtiles * p.tu_cap + trow + u] = has ? tb.A[a] : nullptr;
-        p.bp[(size_t)k * mtiles * p.tu_cap + trow + u] = has ? tb.B[a] : nullptr;
+        p.bp[(size_t)k * mtiles * p.tu_cap + trow + u] = has ? tb.Bf[a] : nullptr;
       }
     }
   }
@@ -694,13 +694,15 @@ __host__ __device__ constexpr int gemm_aux() { return 16 + 2 * LBP * 8; }
 
 /* Workgroup b of a grid of mb token tiles x nb weight blocks -> (token tile, weight block).
  * Workgroup b runs on XCD b % 8. With a multiple of 8 token tiles each XCD takes its own token
- * tiles against every weight block (its L2 keeps those token rows while the weights stream);
- * otherwise each XCD takes a contiguous range of tiles (token tile fastest), so a weight block's
- * token tiles share its L2. */
+ * tiles against every weight block (its L2 keeps those token rows while the weights stream):
+ * XCD x the tiles x, x + 8, x + 16, ..., so that a run of consecutive tiles with large adapter
+ * unions (the grouped order puts the tokens of rare adapter sets last) spreads over the XCDs
+ * instead of landing on one; otherwise each XCD takes a contiguous range of tiles (token tile
+ * fastest), so a weight block's token tiles share its L2. */
 __device__ __forceinline__ void gemm_tile_of(int b, int mb, int nb, int &mbi, int &nbk) {
   if (mb % 8 == 0) {
     const int mpx = mb / 8, k = b >> 3;
-    mbi = (b & 7) * mpx + k % mpx;
+    mbi = (k % mpx) * 8 + (b & 7);
     nbk = k / mpx;
   } else {
     const int nt = mb * nb;
@@ -713,7 +715,8 @@ __device__ __forceinline__ void gemm_tile_of(int b, int mb, int nb, int &mbi, in
 
 /* The expand steps of one token tile (WV waves, NM modules). Each lane's B fragment word w of a
  * step holds union columns k = 64 j + koff[w] .. +7 of the lane's weight row:
- * B_{list[u]}[row][k - u * rpad .. +7] with u = k / rpad, zeros past the union or for an adapter
+ * B_{list[u]}[row][k - u * rpad .. +7] with u = k / rpad (read from the fragment-order copy, where
+ * the 32 rows of a wave's word are contiguous), zeros past the union or for an adapter
  * without the module (rpad is a multiple of 16, so 8 columns never straddle two slots). Words
  * w and w + 1 share a slot when NW / NP = 2 (koff 16-aligned for w even). */
 template <int WV, int NM, int NW, int NP>
@@ -813,7 +816,9 @@ struct Expand {
         const uint16_t *b = pr[w / (NW / NP)];
         const int k = 64 * j + koff[w];
         const int u = k / r;
-        const uint16_t *src = (u < TU && b) ? b + (size_t)row * r + (k - u * r) : p.zero;
+        /* B in fragment order: the 8 columns of 32 consecutive rows are 512 contiguous bytes */
+        const uint16_t *src =
+            (u < TU && b) ? b + ((size_t)(row >> 5) * (r >> 3) + ((k - u * r) >> 3)) * 256 + (row & 31) * 8 : p.zero;
         bv[w] = aos_gld16(src);
       }
     };

@@ -14,7 +14,10 @@
  *     sb[(rb * G + g) * 32 + n] = f16 scale | f16 bias << 16 for row rb*32+n, group g.
  *
  *   LoRA module: A[rpad][in] and B[out][rpad] bfloat16 row-major, rank zero-padded to rpad, a
- *   multiple of 16.
+ *   multiple of 16. The prefill GEMMs read a second copy of B in fragment order,
+ *   Bf[out / 32][rpad / 8][32][8]: element (o, j) at ((o / 32) * (rpad / 8) + j / 8) * 256 +
+ *   (o % 32) * 8 + j % 8, so that the 8 columns j0 .. j0 + 7 of 32 consecutive rows are one
+ *   contiguous 512-byte run (one MFMA operand load of 32 lanes) instead of 32 rows' slices.
  *
  *   Activations: bfloat16 [T][features] row-major.
  */
@@ -59,6 +62,7 @@ typedef struct {
   int rpad;     /* padded rank (multiple of 16), 0 if no adapter has this module */
   const uint16_t *const *A; /* device array [n] of device pointers (NULL = absent) */
   const uint16_t *const *B;
+  const uint16_t *const *Bf; /* B in fragment order (the prefill GEMMs' copy) */
   const float *scale;       /* device [n] alpha / rank */
 } aos_lora_tab;
 

@@ -99,11 +99,12 @@ def test_giveup_prefill(hip, T):
 
 
 def test_giveup_prefill_stream_k(hip):
-    """The stream-K prefill GEMMs (7B-shaped layer, 1000 tokens, shrinks in launches of their
-    own): owners that give up waiting for the other pieces' partial sums still end."""
+    """The stream-K prefill GEMMs (7B-shaped layer, 1100 tokens in 9 token tiles, shrinks in
+    launches of their own): owners that give up waiting for the other pieces' partial sums still
+    end."""
     layer, _ = gpu_layer(hip, 3)
     layer.set_prefill_shrink(False)
-    run = _mlp_runner(layer, 3, 1000)
+    run = _mlp_runner(layer, 3, 1100)
     run()
     assert layer.last_stream_k() == 3
     _give_up(hip, layer, run)

@@ -247,12 +247,13 @@ def test_mlp_prefill_stream_k(hip, case):
     """The prefill GEMMs as stream-K: the device's resident workgroups share the (token tile, row
     block) tasks' K groups evenly; a task cut between workgroups is finished by its owner, which
     adds the other pieces' partial sums in order. 7B-shaped layer with the shrinks in launches of
-    their own at 2048 and 1000 tokens, and without adapters at 2048 (both GEMMs then run as
-    stream-K by default): both GEMMs ran as stream-K, the outputs are bit-identical run to run,
+    their own at 1500 and 1100 tokens, and without adapters at 1500 (12 and 9 token tiles: not a
+    multiple of 8, so both GEMMs then run as stream-K by default; the last round of the plain grid
+    would be partly idle): both GEMMs ran as stream-K, the outputs are bit-identical run to run,
     within tolerance of the oracle on every tile, no wait timed out, and equal to the one-task-per-
     workgroup GEMMs up to float32 summation order."""
     cid = 3
-    T = 1000 if case == "ragged" else 2048
+    T = 1100 if case == "ragged" else 1500
     xb, xf = W.activations(W.CONFIGS[cid], T)
     rings, _ = rings_for(cid, T)
     layer, ads = gpu_layer(hip, cid)
