@@ -132,6 +132,10 @@ def lib():
         L.aoship_internal_layer_set_prefill_sk.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_last_stream_k.restype = C.c_int
         L.aoship_internal_layer_last_stream_k.argtypes = [_P]
+        L.aoship_internal_layer_set_prefill_expand.restype = C.c_int
+        L.aoship_internal_layer_set_prefill_expand.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_last_expand.restype = C.c_int
+        L.aoship_internal_layer_last_expand.argtypes = [_P]
         L.aoship_internal_layer_last_perm.restype = C.c_int
         L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
@@ -435,6 +439,20 @@ class Layer:
         """Diagnostic: the prefill GEMMs that ran as stream-K in the last prefill MLP (bit 0
         gate/up, bit 1 down)."""
         r = lib().aoship_internal_layer_last_stream_k(self.h)
+        if r < 0:
+            raise AosError(last_error())
+        return r
+
+    def set_prefill_expand(self, cols: int = -1) -> None:
+        """Diagnostic: the union width (columns of a tile's wider module) from which the prefill
+        MLP's gate/up LoRA expand of a tile runs in an expand launch of its own instead of in the
+        SwiGLU GEMM (0: never; negative: the default, 512)."""
+        _check(lib().aoship_internal_layer_set_prefill_expand(self.h, int(cols)),
+               "aoship_internal_layer_set_prefill_expand")
+
+    def last_expand(self) -> int:
+        """Diagnostic: 1 when the last prefill MLP ran the gate/up expand launch."""
+        r = lib().aoship_internal_layer_last_expand(self.h)
         if r < 0:
             raise AosError(last_error())
         return r

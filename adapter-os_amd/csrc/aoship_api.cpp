@@ -632,13 +632,14 @@ enum {
   KS_GEMM_PROJ,
   KS_DECODE_MLP,
   KS_MLP1,
+  KS_PXEXP,
   KS_COUNT
 };
 static const char *kStatNames[KS_COUNT] = {
     "route",         "lora_shrink_x",   "q4_gemv_gate_up", "lora_shrink_h",
     "q4_gemv_down",  "q4_gemv_proj",    "prefill_group_plan",
     "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj",
-    "decode_mlp", "mlp1"};
+    "decode_mlp", "mlp1", "lora_tile_expand_gate_up"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -666,6 +667,9 @@ struct aoship_layer {
   bool prefill_fused_shrink = true; /* prefill MLP: the LoRA shrinks run in the GEMM launches */
   int prefill_sk = 3;               /* prefill GEMMs as stream-K: bit 0 gate/up, bit 1 down */
   int last_sk = 0;                  /* the GEMMs the last prefill MLP ran as stream-K (same bits) */
+  int prefill_xe_cols = AOS_XE_COLS; /* union columns from which a tile's gate/up expand runs in the
+                                        expand launch (0: never) */
+  int last_xe = 0;                  /* the last prefill MLP ran the expand launch */
   bool mlp1 = false;             /* one token: the MLP (and its routing) in one launch, down in LDS
                                   * (opt-in: slower than the two launches so far) */
   /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
@@ -1040,6 +1044,24 @@ extern "C" int aoship_internal_layer_set_prefill_sk(aoship_layer_t *l, int mask)
 extern "C" int aoship_internal_layer_last_stream_k(aoship_layer_t *l) {
   if (!l) return set_err("aoship_internal_layer_last_stream_k: null layer");
   return l->last_sk;
+}
+
+/* Diagnostic (no counterpart in the reference): the union width (columns of a tile's wider module,
+ * tu * max(rpad_gate, rpad_up)) from which the prefill MLP's gate/up LoRA expand of a tile runs in
+ * an expand launch of its own, whose sums the SwiGLU GEMM adds before the activation, instead of in
+ * the GEMM (cols 0: never; negative: the default, AOS_XE_COLS). Results agree within float32
+ * summation order; each form is deterministic run to run. */
+extern "C" int aoship_internal_layer_set_prefill_expand(aoship_layer_t *l, int cols) {
+  if (!l) return set_err("aoship_internal_layer_set_prefill_expand: null layer");
+  l->prefill_xe_cols = cols < 0 ? AOS_XE_COLS : cols;
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): 1 when the layer's last prefill MLP (its last
+ * chunk of tokens) ran the gate/up expand launch, else 0. */
+extern "C" int aoship_internal_layer_last_expand(aoship_layer_t *l) {
+  if (!l) return set_err("aoship_internal_layer_last_expand: null layer");
+  return l->last_xe;
 }
 
 /* Diagnostic (no counterpart in the reference): whether the prefill MLP's LoRA shrinks run as
@@ -1775,7 +1797,9 @@ struct MlpPrefill {
   PrefillPlan P;
   aos_tshrink_params sx, sh;
   aos_gemm_params g1, g2;
+  aos_xexp_params xe;
   bool fused_x = false, fused_h = false; /* the x / h shrink runs in the GEMM launch */
+  bool use_xe = false;                   /* the gate/up expand launch runs (wide unions) */
   size_t bytes = 0, ctr = 0, flg = 0;
 };
 
@@ -1806,6 +1830,32 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
   plan_sk(l, cv, M.g2, false);
   if (M.P.lora && M.sh.nmod == 0) M.g2.out_perm = perm; /* h is in sorted order even without a down expand */
   if (M.P.lora && M.sx.nmod == 0) M.g1.in_perm = perm;
+  /* the gate/up expand of wide tile unions in a launch of its own (the SwiGLU GEMM holds both
+   * modules' accumulators, which leaves no registers to pipeline an expand step's B fragments; the
+   * expand launch, one module per wave, runs the pipelined expand), when some tile could reach
+   * the width and the x shrink is a launch of its own (the expand reads its SA) */
+  M.use_xe = false;
+  const int rxe = M.g1.rpad0 > M.g1.rpad1 ? M.g1.rpad0 : M.g1.rpad1;
+  if (M.P.lora && !M.fused_x && M.sx.nmod && rxe > 0 && l->prefill_xe_cols > 0 &&
+      M.P.tu_cap * rxe >= l->prefill_xe_cols) {
+    float *xd = cv.b.take<float>((size_t)2 * M.P.mtiles * Wg.RB * AOS_GEMM_BM * 32);
+    M.g1.xd = xd;
+    M.g1.xe_cols = l->prefill_xe_cols;
+    aos_xexp_params &X = M.xe;
+    memset(&X, 0, sizeof(X));
+    X.g[0] = M.g1;
+    X.g[0].rpad1 = 0;
+    X.g[1] = M.g1;
+    X.g[1].mod0 = M.g1.mod0 + 1;
+    X.g[1].rpad0 = M.g1.rpad1;
+    X.g[1].rpad1 = 0;
+    X.g[1].sa_mod_before = M.g1.sa_mod_before + 1;
+    if (M.g1.sa_mod_before < 2) X.g[1].rpad_before[M.g1.sa_mod_before] = M.g1.rpad0;
+    X.xd = xd;
+    X.xe_cols = l->prefill_xe_cols;
+    X.rmax = rxe;
+    M.use_xe = true;
+  }
   M.bytes = cv.b.off + 256;
   M.ctr = cv.coff + 64;
   M.flg = cv.foff + 64;
@@ -2256,6 +2306,11 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       l->last_perm_T = M.P.lora ? Tc : 0;
       if (launch_gplan(l, M.P)) return -1;
       if (!M.fused_x && launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
+      l->last_xe = M.use_xe ? 1 : 0;
+      if (M.use_xe) {
+        aos_launch_ctx cx = launch_ctx(l, KS_PXEXP);
+        if (launch_err(aos_launch_xexp(&M.xe, &cx), "lora tile expand gate/up")) return -1;
+      }
       l->last_sk = (M.g1.sk_nwg ? 1 : 0) | (M.g2.sk_nwg ? 2 : 0);
       if (M.g1.s_cols || M.g1.sk_nwg) M.g1.gen = next_gen(&l->gen);
       aos_launch_ctx c2 = launch_ctx(l, KS_GEMM_GU);

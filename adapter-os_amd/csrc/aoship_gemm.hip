@@ -98,6 +98,59 @@ __device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float b) {
  * consecutive rows read one chunk each without a bank conflict. */
 __device__ __forceinline__ int tile_off(int r, int chunk) { return r * 128 + ((chunk ^ ((r >> 1) & 7)) << 4); }
 
+/* Loads whose waits the kernel places itself. The compiler's wait insertion (ROCm 7.2, gfx950)
+ * cannot follow the K loop's rings: it cannot tell which LDS a buffer load to LDS writes, so it
+ * waits for all of them before any LDS read (or at a release fence), and at the loop's back edge
+ * it loses which load fills which ring register; either way every group waited for every load in
+ * flight, the ring's later stages included. These loads and LDS reads are single instructions in
+ * asm statements, which the compiler does not track; the kernel completes each with a counted
+ * s_waitcnt whose asm statement also takes the loaded registers as operands, so nothing reads
+ * them before it. Loads complete in issue order per counter (scalar loads in flight only make an
+ * lgkmcnt wait longer). */
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_rd16(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF));
+  return v;
+}
+/* completes this wave's LDS reads but the last N issued; v's values are usable after it */
+template <int N>
+__device__ __forceinline__ void lds_wait4(u32x4 (&v)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "n"(N));
+}
+__device__ __forceinline__ u32x4 gld16_untracked(const void *p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+  return v;
+}
+__device__ __forceinline__ uint32_t gld4_untracked(const void *p) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p));
+  return v;
+}
+/* completes this wave's vector memory loads but the last N issued; the operands' values are usable
+ * after it */
+template <int N>
+__device__ __forceinline__ void vm_wait2(u32x4 &a, uint32_t &b) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait4(u32x4 &a, uint32_t &b, u32x4 &c, uint32_t &d) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+
+/* f(std::integral_constant<int, k>) for k = B .. E - 1 */
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 /* Stages the [BM x 64] bf16 slice of group g of a tile's token rows with NT threads. Row r of
  * the tile is token perm[m0 + r] (m0 + r without a permutation); rows past the last token repeat
  * it: they only feed accumulator rows that are never stored. */
@@ -728,11 +781,19 @@ struct Expand {
   const uint16_t *const *bpt[2];
   int wave, lane, m0, mbi, row, TU, n0, nls, off[2], rp[2];
   bool bp_lds;
+  /* parameters the steps read, held in registers: a read of the kernel's arguments after an
+   * asm statement with a memory clobber (the waits, the barriers) is a scalar load again, and its
+   * wait also waits for the LDS reads in flight */
+  const uint16_t *zero;
+  int sa_stride, nbs;
 
   /* row: the lane's weight row (of every module) */
   __device__ Expand(const aos_gemm_params &p_, unsigned char *smem_, int ntile, int wave_, int lane_, int m0_,
                     int mbi_, int row_)
       : p(p_), smem(smem_), wave(wave_), lane(lane_), m0(m0_), mbi(mbi_), row(row_) {
+    zero = p.zero;
+    sa_stride = p.sa_stride;
+    nbs = p.nbs;
     lbp = (const uint16_t **)(smem + ntile * TILE + 16);
     TU = (p.tu && (p.rpad0 | (NM == 2 ? p.rpad1 : 0))) ? __builtin_amdgcn_readfirstlane(p.tu[mbi]) : 0;
     rp[0] = p.rpad0;
@@ -818,7 +879,7 @@ struct Expand {
         const int u = k / r;
         /* B in fragment order: the 8 columns of 32 consecutive rows are 512 contiguous bytes */
         const uint16_t *src =
-            (u < TU && b) ? b + ((size_t)(row >> 5) * (r >> 3) + ((k - u * r) >> 3)) * 256 + (row & 31) * 8 : p.zero;
+            (u < TU && b) ? b + ((size_t)(row >> 5) * (r >> 3) + ((k - u * r) >> 3)) * 256 + (row & 31) * 8 : zero;
         bv[w] = aos_gld16(src);
       }
     };
@@ -827,7 +888,7 @@ struct Expand {
     auto dma_tile = [&](int q, int l) {
       int m, j;
       step_of(l, m, j);
-      const int cb = (off[m] + 64 * j) * 2, lim = (off[m] + TU * rp[m]) * 2, rb = p.sa_stride * 2;
+      const int cb = (off[m] + 64 * j) * 2, lim = (off[m] + TU * rp[m]) * 2, rb = sa_stride * 2;
 #pragma unroll
       for (int k = 0; k < BM / 8 / WV; ++k) {
         const int bk = k * WV + wave;
@@ -837,7 +898,7 @@ struct Expand {
         const int col = cb + ch * 16;
         const int vo = col < lim ? rr * rb + col : (int)0x80000000;
         /* SA stored in this launch (by a workgroup maybe on another XCD): device-coherent (sc1) */
-        if (p.nbs)
+        if (nbs)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               rsa, (__attribute__((address_space(3))) void *)(smem + q * TILE + bk * 1024), 16, vo, 0, 0, SC1);
         else
@@ -1095,6 +1156,9 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
   const uint32_t *s1p = W1.sb + (size_t)r0 * G * 32 + i;
   const int row = r0 * 32 + i;
   const int glast = gb - 1; /* groups past the piece are clamped to its last (never read) */
+  uint32_t aoff[4]; /* the lane's token fragment s of a 32-row sub-tile: chunk 4 c + s of row i */
+#pragma unroll
+  for (int s = 0; s < 4; ++s) aoff[s] = (uint32_t)tile_off(i, 4 * c + s);
 
   f32x16 acc0[MT], acc1[MT];
 #pragma unroll
@@ -1110,11 +1174,20 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     const int gd = ga + d < gb ? ga + d : glast;
-    wq0[d] = q0[(size_t)gd * 64];
-    ws0[d] = s0p[(size_t)gd * 32];
-    if (SW) {
-      wq1[d] = q1[(size_t)gd * 64];
-      ws1[d] = s1p[(size_t)gd * 32];
+    if constexpr (NS > 0) { /* completed by the piece's first wait (vmcnt 0) or dequant_slot */
+      wq0[d] = gld16_untracked(q0 + (size_t)gd * 64);
+      ws0[d] = gld4_untracked(s0p + (size_t)gd * 32);
+      if (SW) {
+        wq1[d] = gld16_untracked(q1 + (size_t)gd * 64);
+        ws1[d] = gld4_untracked(s1p + (size_t)gd * 32);
+      }
+    } else {
+      wq0[d] = q0[(size_t)gd * 64];
+      ws0[d] = s0p[(size_t)gd * 32];
+      if (SW) {
+        wq1[d] = q1[(size_t)gd * 64];
+        ws1[d] = s1p[(size_t)gd * 32];
+      }
     }
   }
   /* Token tiles, NS == 0: LDS holds groups g and g + 1 (double buffer); registers hold the loads
@@ -1127,9 +1200,11 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
   static_assert(NS == 0 || DMA_N <= 4, "tile DMA: at most 4 blocks per wave");
   Stager<NT> st0, st1;
   int voff[4] = {0, 0, 0, 0};
+  const uint16_t *const xg = p.x; /* in registers: see Expand */
+  const int Tg = p.T;
   auto dma = [&](int stage, int gx) {
     /* tiles past the piece's last group repeat it and are never read */
-    tile_dma(p.x, p.T, in, smem + stage * TILE, wave, WV, DMA_N, voff[0], voff[1], voff[2], voff[3],
+    tile_dma(xg, Tg, in, smem + stage * TILE, wave, WV, DMA_N, voff[0], voff[1], voff[2], voff[3],
              gx < gb ? gx : glast);
   };
   if (NS) {
@@ -1153,6 +1228,9 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
   }
   const bool expand = role != GEMM_PART;
   Expand<WV, SW ? 2 : 1, 4, 2> ex(p, smem, NTILE, wave, lane, m0, mbi, row);
+  /* a tile whose expand ran in the expand launch: its sums are added in the epilogue */
+  const bool xe = SW && p.xd && ex.TU * (p.rpad0 > p.rpad1 ? p.rpad0 : p.rpad1) >= p.xe_cols;
+  if (xe) ex.nls = 0;
   if (expand) ex.prefetch();
   if (!NS) {
     st0.store(smem + (ga & 1) * TILE, tid);
@@ -1168,7 +1246,18 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
   constexpr int VM_AFTER = NS >= 2 ? (DMA_N + (SW ? 4 : 2)) * (NS - 2) : 0;
 
   /* dequantise ring slot d into B fragments, then refill it with group gn */
+  /* NS > 0: a group issues the tile DMA (DMA_N loads), then refills its ring slot (NWL loads);
+   * slot d's loads for group g went out in group g - D, followed by the rest of that group's, D - 1
+   * whole groups' and group g's DMA */
+  constexpr int NWL = SW ? 4 : 2;
+  constexpr int VM_W = (D - 1) * (DMA_N + NWL) + DMA_N;
   auto dequant_slot = [&](const int d, const int gn, u32x4 (&f0)[4], u32x4 (&f1)[4]) {
+    if constexpr (NS > 0) {
+      if constexpr (SW)
+        vm_wait4<VM_W>(wq0[d], ws0[d], wq1[d], ws1[d]);
+      else
+        vm_wait2<VM_W>(wq0[d], ws0[d]);
+    }
     {
       const float sc = aos_f16_to_f32(ws0[d] & 0xffffu), bi = aos_f16_to_f32(ws0[d] >> 16);
 #pragma unroll
@@ -1180,11 +1269,20 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
       for (int s = 0; s < 4; ++s) f1[s] = dequant_word(wq1[d][s], sc, bi);
     }
     const int gc = gn < gb ? gn : glast;
-    wq0[d] = q0[(size_t)gc * 64];
-    ws0[d] = s0p[(size_t)gc * 32];
-    if (SW) {
-      wq1[d] = q1[(size_t)gc * 64];
-      ws1[d] = s1p[(size_t)gc * 32];
+    if constexpr (NS > 0) {
+      wq0[d] = gld16_untracked(q0 + (size_t)gc * 64);
+      ws0[d] = gld4_untracked(s0p + (size_t)gc * 32);
+      if (SW) {
+        wq1[d] = gld16_untracked(q1 + (size_t)gc * 64);
+        ws1[d] = gld4_untracked(s1p + (size_t)gc * 32);
+      }
+    } else {
+      wq0[d] = q0[(size_t)gc * 64];
+      ws0[d] = s0p[(size_t)gc * 32];
+      if (SW) {
+        wq1[d] = q1[(size_t)gc * 64];
+        ws1[d] = s1p[(size_t)gc * 32];
+      }
     }
   };
 
@@ -1197,10 +1295,42 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
         AOS_VM_WAIT_LE(0);
       else
         AOS_VM_WAIT_LE(VM_AFTER);
-      lds_barrier(); /* also: every wave is past its reads of the stage refilled next */
+      ring_barrier(); /* also: every wave is past its reads of the stage refilled next */
       dma((g + NS - 1) % (NS ? NS : 1), g + NS - 1);
     }
     const unsigned char *tb = smem + (NS ? (g % (NS ? NS : 1)) : (g & 1)) * TILE;
+    if constexpr (NS > 0) {
+      /* token fragments out of the compiler's sight: sub-tile mt's in register set mt & 1 with APF
+       * (read while the previous sub-tile's MFMAs run), else in one set */
+      const uint32_t tba = lds_addr(tb);
+      u32x4 a[APF ? 2 : 1][4];
+      auto rd = [&](auto mc, u32x4 (&v)[4]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) v[s] = lds_rd16<decltype(mc)::value * 4096>(tba + aoff[s]);
+      };
+      /* the first sub-tile's LDS latency overlaps the dequantisation */
+      rd(std::integral_constant<int, 0>{}, a[0]);
+      u32x4 f0[4], f1[4];
+      dequant_slot(d, g + D, f0, f1);
+      static_for<0, MT>([&](auto mc) {
+        constexpr int mt = decltype(mc)::value;
+        constexpr int q = APF ? (mt & 1) : 0;
+        if constexpr (APF && mt + 1 < MT) {
+          rd(std::integral_constant<int, mt + 1>{}, a[(mt + 1) & 1]);
+          lds_wait4<4>(a[q]);
+        } else {
+          if constexpr (!APF && mt > 0) rd(mc, a[0]);
+          lds_wait4<0>(a[q]);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          /* word s of lane (i, c) covers K elements 32 c + 8 s .. +7: chunk 4 c + s */
+          acc0[mt] = aos_mfma32(a[q][s], f0[s], acc0[mt]);
+          if (SW) acc1[mt] = aos_mfma32(a[q][s], f1[s], acc1[mt]);
+        }
+      });
+      return;
+    }
     /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
     u32x4 a[4];
 #pragma unroll
@@ -1363,6 +1493,26 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
 
   /* epilogue: sorted row m0 + r goes to output row out_perm[m0 + r] (or m0 + r) */
   if (!live) return;
+  if (SW && xe) { /* the expand launch's gate and up sums, in accumulator order */
+    const size_t plane = (size_t)p.mtiles * RB * MT * 256; /* f32x4 words per module */
+    const f32x4 *d0 = (const f32x4 *)p.xd + ((size_t)mbi * RB + r0) * MT * 256 + lane;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 g4[4], u4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        g4[q] = d0[(mt * 4 + q) * 64];
+        u4[q] = d0[plane + (mt * 4 + q) * 64];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc0[mt][4 * q + e] += g4[q][e];
+          acc1[mt][4 * q + e] += u4[q][e];
+        }
+    }
+  }
   const int out = p.w0.out;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -1444,7 +1594,80 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_sk_kernel(aos_gemm_para
   }
 }
 
+/* The expand launch of a SwiGLU GEMM (aos_xexp_params): workgroup (module m, token tile mbi,
+ * block nbk of XW * 32 rows), the tiles mapped to XCDs as the GEMM's plain grid maps them. Each
+ * wave expands its 32 rows of module m over the tile's union with the pipelined expand (token tiles
+ * through an LDS ring, B fragments in a register ring) into one accumulator set and stores it in
+ * accumulator order. Tiles the GEMM expands itself (tu * rmax < xe_cols) exit at once. */
+constexpr int XW = 8;  /* waves per expand workgroup */
+constexpr int XNT = 4; /* LDS ring stages */
+__global__ void __launch_bounds__(64 * XW, 2) aos_xexp_kernel(aos_xexp_params p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int MT = BM / 32;
+  constexpr int TILE = BM * 128;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 31, c = lane >> 5;
+  const aos_gemm_params &g0 = p.g[0];
+  const int mb = g0.mb, nb = g0.nb, RB = g0.w0.RB;
+  const int m = (int)blockIdx.x / (mb * nb);
+  int mbi, nbk;
+  gemm_tile_of((int)blockIdx.x - m * mb * nb, mb, nb, mbi, nbk);
+  const int TU = __builtin_amdgcn_readfirstlane(g0.tu[mbi]);
+  if (TU * p.rmax < p.xe_cols) return; /* uniform: the GEMM expands this tile */
+  const aos_gemm_params &q = p.g[m];
+  const int rb = nbk * XW + wave;
+  const bool live = rb < RB;
+  const int r0 = live ? rb : RB - 1;
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+  Expand<XW, 1, 4, 2> ex(q, smem, XNT, wave, lane, mbi * BM, mbi, r0 * 32 + i);
+  ex.prefetch();
+  const int koff[4] = {32 * c, 32 * c + 8, 32 * c + 16, 32 * c + 24};
+  auto mma_step = [&](const unsigned char *tb, const u32x4 (&bv)[4]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4 a[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[mt] = *(const u32x4 *)(tb + tile_off(mt * 32 + i, 4 * c + s));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = aos_mfma32(a[mt], bv[s], acc[mt]);
+    }
+  };
+  ex.template run<XNT, XNT>(
+      koff,
+      [&](int, int n, const u32x4 (&bv)[XNT][4]) {
+#pragma unroll
+        for (int k = 0; k < XNT; ++k)
+          if (k < n) mma_step(smem + k * TILE, bv[k]);
+      },
+      [&](auto, const unsigned char *tb, const u32x4 (&bv)[4]) { mma_step(tb, bv); });
+  if (!live) return;
+  f32x4 *d = (f32x4 *)p.xd + (((size_t)m * g0.mtiles + mbi) * RB + r0) * MT * 256 + lane;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      d[(mt * 4 + k) * 64] = f32x4{acc[mt][4 * k], acc[mt][4 * k + 1], acc[mt][4 * k + 2], acc[mt][4 * k + 3]};
+}
+
 }  // namespace
+
+extern "C" int aos_launch_xexp(const aos_xexp_params *p, const aos_launch_ctx *ctx) {
+  aos_xexp_params q = *p;
+  const aos_gemm_params &g = q.g[0];
+  if (!q.xd || q.xe_cols < 1 || q.rmax < 1 || !g.tu || !g.bp || !g.SA || g.T < 1 || g.T > AOS_PREFILL_MAX_T ||
+      g.w0.RB < 1 || q.g[1].w0.RB != g.w0.RB || g.mtiles != (g.T + BM - 1) / BM)
+    return (int)hipErrorInvalidValue;
+  for (int m = 0; m < 2; ++m) {
+    q.g[m].mb = g.mtiles;
+    q.g[m].nb = (g.w0.RB + XW - 1) / XW;
+    q.g[m].nbs = 0;
+  }
+  const size_t lds = (size_t)XNT * BM * 128 + gemm_aux();
+  AOS_LAUNCH(ctx, aos_xexp_kernel, dim3(2 * q.g[0].mb * q.g[0].nb), dim3(64 * XW), lds, q);
+  return (int)hipGetLastError();
+}
 
 extern "C" int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx) {
   const int mtiles = (p->T + BM - 1) / BM;

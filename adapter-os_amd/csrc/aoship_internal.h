@@ -339,6 +339,7 @@ typedef struct {
 #define AOS_PREFILL_MAX_T 4096
 #define AOS_GEMM_BM 128 /* tokens per tile */
 #define AOS_TILE_U_MAX 1024 /* a tile's union: at most 128 tokens x 8 ring slots */
+#define AOS_XE_COLS 512     /* union columns from which a tile's gate/up expand runs in the expand launch */
 
 /* Group plan: the sort, then for each tile mt its union tu[mt] <= tu_cap, list[mt][u], the
  * coefficients coef[p][u] = sum over sorted token p's active ring slots naming list[mt][u] of
@@ -427,7 +428,23 @@ typedef struct {
   int sk_nwg;
   float *sk_part;
   uint32_t *sk_lines;
+  /* SwiGLU mode: the LoRA expand of each tile whose union spans xe_cols or more columns of its
+   * wider module (tu * max(rpad0, rpad1)) ran in an expand launch of its own (aos_xexp_params),
+   * whose gate and up sums this launch adds before the activation instead of expanding itself.
+   * xd: [2][mtiles][RB][4 sub-tiles][4][64 lanes][4] float32 (module, tile, 32-row block, the
+   * accumulator's registers 4 q .. 4 q + 3 of each lane); NULL: every tile expands here. */
+  const float *xd;
+  int xe_cols;
 } aos_gemm_params;
+
+/* The expand launch of a SwiGLU prefill GEMM: for each tile with tu * rmax >= xe_cols and each
+ * module m (0 gate, 1 up), xd[m] = SA . B^T over the tile's union columns of that module (g[m]
+ * describes module m as the only module of a single-matrix expand), in the layout the GEMM reads. */
+typedef struct {
+  aos_gemm_params g[2];
+  float *xd;
+  int xe_cols, rmax;
+} aos_xexp_params;
 
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
  * records at kernel start and end (hipExtLaunchKernelGGL). */
@@ -543,6 +560,7 @@ int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx 
 int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
+int aos_launch_xexp(const aos_xexp_params *p, const aos_launch_ctx *ctx);
 int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);
 int aos_launch_mlp1(const aos_mlp1_params *p, const aos_launch_ctx *ctx);
 /* The prefill GEMM's stream-K shape on the current device (swiglu: the gate/up kernel, else the

@@ -205,6 +205,7 @@ def test_mlp_stress_32b_prefill(hip):
     y2 = torch.empty_like(y1)
     layer.mlp_forward(x, rdev, y1)
     perm = layer.last_perm()
+    assert layer.last_expand() == 1, "the wide unions' gate/up expand did not run as its own launch"
     layer.mlp_forward(x, rdev, y2)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2), "run-to-run outputs differ"
@@ -214,6 +215,40 @@ def test_mlp_stress_32b_prefill(hip):
     got = W.bf16_bits_to_f32(y1.cpu().numpy().view(np.uint16)[sample])
     ratio = assert_parity(f"C5 prefill T={T}, {len(sample)} tokens over {T // 128} tiles", got, ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
+
+
+@pytest.mark.parametrize("T", [1024, 1100])
+def test_mlp_prefill_expand_launch(hip, T):
+    """The gate/up LoRA expand of wide tile unions as a launch of its own, whose sums the SwiGLU
+    GEMM adds before the activation (32B-shaped stress layer, 64 rank-64 adapters, K = 8,
+    adversarial routing; 1024 tokens in 8 tiles, and 1100 in 9 with a ragged last tile and the
+    GEMMs as stream-K): for every tile (the default width, 512 columns), for none (0), and for
+    the tiles of 50 adapters or more (3200 columns: the tiles of tokens with random adapter sets
+    hold 63-64, the others 31-42, so that both forms meet in one GEMM launch).
+    Each form is bit-identical run to run and within tolerance of the oracle on every tile; the
+    forms agree with each other up to float32 summation order."""
+    cid = 5
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    layer.set_prefill_shrink(False)
+    out = {}
+    for cols in (-1, 0, 50 * cfg.rank):
+        layer.set_prefill_expand(cols)
+        y = _run_mlp(hip, layer, xb, rings)
+        assert layer.last_expand() == (0 if cols == 0 else 1), f"cols={cols}: expand launch state"
+        assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), f"cols={cols}: run-to-run outputs differ"
+        out[cols] = W.bf16_bits_to_f32(y).reshape(T, -1)
+    layer.set_prefill_expand(-1)
+    perm = layer.last_perm()
+    sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
+    ref = oracle_mlp(cid, xf[sample], rings[sample])
+    for cols, y in out.items():
+        ratio = assert_parity(f"C5 prefill T={T} expand width {cols}", y[sample], ref)
+        assert ratio <= REL_TOL, f"cols={cols}: max tolerance ratio {ratio:.4g}"
+    assert tol_ratio(out[-1], out[0]) <= REL_TOL / 2
+    assert tol_ratio(out[50 * cfg.rank], out[0]) <= REL_TOL / 2
 
 
 @pytest.mark.parametrize("cid,T", [(1, 300), (3, 2048)])
