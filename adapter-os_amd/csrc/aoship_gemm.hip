@@ -98,59 +98,6 @@ __device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float b) {
  * consecutive rows read one chunk each without a bank conflict. */
 __device__ __forceinline__ int tile_off(int r, int chunk) { return r * 128 + ((chunk ^ ((r >> 1) & 7)) << 4); }
 
-/* Loads whose waits the kernel places itself. The compiler's wait insertion (ROCm 7.2, gfx950)
- * cannot follow the K loop's rings: it cannot tell which LDS a buffer load to LDS writes, so it
- * waits for all of them before any LDS read (or at a release fence), and at the loop's back edge
- * it loses which load fills which ring register; either way every group waited for every load in
- * flight, the ring's later stages included. These loads and LDS reads are single instructions in
- * asm statements, which the compiler does not track; the kernel completes each with a counted
- * s_waitcnt whose asm statement also takes the loaded registers as operands, so nothing reads
- * them before it. Loads complete in issue order per counter (scalar loads in flight only make an
- * lgkmcnt wait longer). */
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-template <int OFF>
-__device__ __forceinline__ u32x4 lds_rd16(uint32_t a) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF));
-  return v;
-}
-/* completes this wave's LDS reads but the last N issued; v's values are usable after it */
-template <int N>
-__device__ __forceinline__ void lds_wait4(u32x4 (&v)[4]) {
-  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "n"(N));
-}
-__device__ __forceinline__ u32x4 gld16_untracked(const void *p) {
-  u32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
-  return v;
-}
-__device__ __forceinline__ uint32_t gld4_untracked(const void *p) {
-  uint32_t v;
-  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p));
-  return v;
-}
-/* completes this wave's vector memory loads but the last N issued; the operands' values are usable
- * after it */
-template <int N>
-__device__ __forceinline__ void vm_wait2(u32x4 &a, uint32_t &b) {
-  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void vm_wait4(u32x4 &a, uint32_t &b, u32x4 &c, uint32_t &d) {
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
-}
-
-/* f(std::integral_constant<int, k>) for k = B .. E - 1 */
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
 /* Stages the [BM x 64] bf16 slice of group g of a tile's token rows with NT threads. Row r of
  * the tile is token perm[m0 + r] (m0 + r without a permutation); rows past the last token repeat
  * it: they only feed accumulator rows that are never stored. */
@@ -1156,9 +1103,6 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
   const uint32_t *s1p = W1.sb + (size_t)r0 * G * 32 + i;
   const int row = r0 * 32 + i;
   const int glast = gb - 1; /* groups past the piece are clamped to its last (never read) */
-  uint32_t aoff[4]; /* the lane's token fragment s of a 32-row sub-tile: chunk 4 c + s of row i */
-#pragma unroll
-  for (int s = 0; s < 4; ++s) aoff[s] = (uint32_t)tile_off(i, 4 * c + s);
 
   f32x16 acc0[MT], acc1[MT];
 #pragma unroll
@@ -1174,20 +1118,11 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     const int gd = ga + d < gb ? ga + d : glast;
-    if constexpr (NS > 0) { /* completed by the piece's first wait (vmcnt 0) or dequant_slot */
-      wq0[d] = gld16_untracked(q0 + (size_t)gd * 64);
-      ws0[d] = gld4_untracked(s0p + (size_t)gd * 32);
-      if (SW) {
-        wq1[d] = gld16_untracked(q1 + (size_t)gd * 64);
-        ws1[d] = gld4_untracked(s1p + (size_t)gd * 32);
-      }
-    } else {
-      wq0[d] = q0[(size_t)gd * 64];
-      ws0[d] = s0p[(size_t)gd * 32];
-      if (SW) {
-        wq1[d] = q1[(size_t)gd * 64];
-        ws1[d] = s1p[(size_t)gd * 32];
-      }
+    wq0[d] = q0[(size_t)gd * 64];
+    ws0[d] = s0p[(size_t)gd * 32];
+    if (SW) {
+      wq1[d] = q1[(size_t)gd * 64];
+      ws1[d] = s1p[(size_t)gd * 32];
     }
   }
   /* Token tiles, NS == 0: LDS holds groups g and g + 1 (double buffer); registers hold the loads
@@ -1246,18 +1181,7 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
   constexpr int VM_AFTER = NS >= 2 ? (DMA_N + (SW ? 4 : 2)) * (NS - 2) : 0;
 
   /* dequantise ring slot d into B fragments, then refill it with group gn */
-  /* NS > 0: a group issues the tile DMA (DMA_N loads), then refills its ring slot (NWL loads);
-   * slot d's loads for group g went out in group g - D, followed by the rest of that group's, D - 1
-   * whole groups' and group g's DMA */
-  constexpr int NWL = SW ? 4 : 2;
-  constexpr int VM_W = (D - 1) * (DMA_N + NWL) + DMA_N;
   auto dequant_slot = [&](const int d, const int gn, u32x4 (&f0)[4], u32x4 (&f1)[4]) {
-    if constexpr (NS > 0) {
-      if constexpr (SW)
-        vm_wait4<VM_W>(wq0[d], ws0[d], wq1[d], ws1[d]);
-      else
-        vm_wait2<VM_W>(wq0[d], ws0[d]);
-    }
     {
       const float sc = aos_f16_to_f32(ws0[d] & 0xffffu), bi = aos_f16_to_f32(ws0[d] >> 16);
 #pragma unroll
@@ -1269,20 +1193,11 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
       for (int s = 0; s < 4; ++s) f1[s] = dequant_word(wq1[d][s], sc, bi);
     }
     const int gc = gn < gb ? gn : glast;
-    if constexpr (NS > 0) {
-      wq0[d] = gld16_untracked(q0 + (size_t)gc * 64);
-      ws0[d] = gld4_untracked(s0p + (size_t)gc * 32);
-      if (SW) {
-        wq1[d] = gld16_untracked(q1 + (size_t)gc * 64);
-        ws1[d] = gld4_untracked(s1p + (size_t)gc * 32);
-      }
-    } else {
-      wq0[d] = q0[(size_t)gc * 64];
-      ws0[d] = s0p[(size_t)gc * 32];
-      if (SW) {
-        wq1[d] = q1[(size_t)gc * 64];
-        ws1[d] = s1p[(size_t)gc * 32];
-      }
+    wq0[d] = q0[(size_t)gc * 64];
+    ws0[d] = s0p[(size_t)gc * 32];
+    if (SW) {
+      wq1[d] = q1[(size_t)gc * 64];
+      ws1[d] = s1p[(size_t)gc * 32];
     }
   };
 
@@ -1295,42 +1210,10 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
         AOS_VM_WAIT_LE(0);
       else
         AOS_VM_WAIT_LE(VM_AFTER);
-      ring_barrier(); /* also: every wave is past its reads of the stage refilled next */
+      lds_barrier(); /* also: every wave is past its reads of the stage refilled next */
       dma((g + NS - 1) % (NS ? NS : 1), g + NS - 1);
     }
     const unsigned char *tb = smem + (NS ? (g % (NS ? NS : 1)) : (g & 1)) * TILE;
-    if constexpr (NS > 0) {
-      /* token fragments out of the compiler's sight: sub-tile mt's in register set mt & 1 with APF
-       * (read while the previous sub-tile's MFMAs run), else in one set */
-      const uint32_t tba = lds_addr(tb);
-      u32x4 a[APF ? 2 : 1][4];
-      auto rd = [&](auto mc, u32x4 (&v)[4]) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) v[s] = lds_rd16<decltype(mc)::value * 4096>(tba + aoff[s]);
-      };
-      /* the first sub-tile's LDS latency overlaps the dequantisation */
-      rd(std::integral_constant<int, 0>{}, a[0]);
-      u32x4 f0[4], f1[4];
-      dequant_slot(d, g + D, f0, f1);
-      static_for<0, MT>([&](auto mc) {
-        constexpr int mt = decltype(mc)::value;
-        constexpr int q = APF ? (mt & 1) : 0;
-        if constexpr (APF && mt + 1 < MT) {
-          rd(std::integral_constant<int, mt + 1>{}, a[(mt + 1) & 1]);
-          lds_wait4<4>(a[q]);
-        } else {
-          if constexpr (!APF && mt > 0) rd(mc, a[0]);
-          lds_wait4<0>(a[q]);
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          /* word s of lane (i, c) covers K elements 32 c + 8 s .. +7: chunk 4 c + s */
-          acc0[mt] = aos_mfma32(a[q][s], f0[s], acc0[mt]);
-          if (SW) acc1[mt] = aos_mfma32(a[q][s], f1[s], acc1[mt]);
-        }
-      });
-      return;
-    }
     /* token fragments of the first sub-tile: their LDS latency overlaps the dequantisation */
     u32x4 a[4];
 #pragma unroll
@@ -1379,7 +1262,6 @@ __device__ __forceinline__ void gemm_task(const aos_gemm_params &p, unsigned cha
         if (g0 + d < gb) group(g0 + d, d, st0, st0);
     }
   }
-
   constexpr int NMAT = SW ? 2 : 1;
   if (role != GEMM_WHOLE) {
     /* the pieces meet through the workspace: slot v holds [WV waves][NMAT][MT][4 quads][64 lanes]
@@ -1598,10 +1480,13 @@ __global__ void __launch_bounds__(64 * WV, OCC) aos_gemm_sk_kernel(aos_gemm_para
  * block nbk of XW * 32 rows), the tiles mapped to XCDs as the GEMM's plain grid maps them. Each
  * wave expands its 32 rows of module m over the tile's union with the pipelined expand (token tiles
  * through an LDS ring, B fragments in a register ring) into one accumulator set and stores it in
- * accumulator order. Tiles the GEMM expands itself (tu * rmax < xe_cols) exit at once. */
-constexpr int XW = 8;  /* waves per expand workgroup */
-constexpr int XNT = 4; /* LDS ring stages */
-__global__ void __launch_bounds__(64 * XW, 2) aos_xexp_kernel(aos_xexp_params p) {
+ * accumulator order. Tiles the GEMM expands itself (tu * rmax < xe_cols) exit at once. Shape: 4-wave
+ * workgroups with a 3-stage ring (52 KB of LDS, 162 VGPRs), three per CU; 8-wave workgroups with 4
+ * stages (one per CU) and 4-wave ones with 4 stages (two per CU) measured 17% slower on the 32B-shaped
+ * stress prefill: the steps wait on their loads, and more resident waves cover more of it. */
+constexpr int XW = 4;  /* waves per expand workgroup */
+constexpr int XNT = 3; /* LDS ring stages */
+__global__ void __launch_bounds__(64 * XW, 3) aos_xexp_kernel(aos_xexp_params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int MT = BM / 32;
   constexpr int TILE = BM * 128;
