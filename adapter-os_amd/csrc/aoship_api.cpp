@@ -1709,7 +1709,11 @@ static void plan_tshrink(aoship_layer *l, Carve &cv, const PrefillPlan &P, const
   if (ks > 16) ks = 16;
   if (ks > G / 8) ks = G / 8;
   if (ks < 1) ks = 1;
-  while (ks > 1 && (size_t)P.mtiles * ks * AOS_GEMM_BM * sp.s_stride * 4 > ((size_t)128 << 20)) --ks;
+  /* the slices' partial sums (sized for the widest union on every tile) within 512 MB: on the
+   * 32B-shaped layer at 4096 tokens (64 rank-64 adapters) the h shrink takes 8 slices (0.94 ms;
+   * 2 slices under a 128 MB bound, 1.1 ms; 16 slices, 1.13 ms: the partials' own traffic) and the
+   * x shrink 4 (no change against 1; 8 slices, 0.64 against 0.42 ms) */
+  while (ks > 1 && (size_t)P.mtiles * ks * AOS_GEMM_BM * sp.s_stride * 4 > ((size_t)512 << 20)) --ks;
   sp.ks = ks;
   sp.part = cv.b.take<float>((size_t)P.mtiles * ks * AOS_GEMM_BM * sp.s_stride);
   sp.counters = cv.counters((size_t)P.mtiles * sp.csets);
