@@ -136,6 +136,10 @@ def lib():
         L.aoship_internal_layer_set_prefill_expand.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_last_expand.restype = C.c_int
         L.aoship_internal_layer_last_expand.argtypes = [_P]
+        L.aoship_internal_layer_set_prefill_adapter_major.restype = C.c_int
+        L.aoship_internal_layer_set_prefill_adapter_major.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_last_adapter_major.restype = C.c_int
+        L.aoship_internal_layer_last_adapter_major.argtypes = [_P]
         L.aoship_internal_layer_last_perm.restype = C.c_int
         L.aoship_internal_layer_last_perm.argtypes = [_P, _P, C.c_int]
         L.aoship_internal_decode_geometry.restype = C.c_int
@@ -453,6 +457,20 @@ class Layer:
     def last_expand(self) -> int:
         """Diagnostic: 1 when the last prefill MLP ran the gate/up expand launch."""
         r = lib().aoship_internal_layer_last_expand(self.h)
+        if r < 0:
+            raise AosError(last_error())
+        return r
+
+    def set_prefill_adapter_major(self, tu: int = -1) -> None:
+        """Diagnostic: the union size (adapters) from which a prefill tile's LoRA shrinks run
+        adapter-major, each adapter's users gathered into tiles of their own (0: never; negative:
+        the default)."""
+        _check(lib().aoship_internal_layer_set_prefill_adapter_major(self.h, int(tu)),
+               "aoship_internal_layer_set_prefill_adapter_major")
+
+    def last_adapter_major(self) -> int:
+        """Diagnostic: the last prefill MLP's adapter-major shrinks (bit 0 x, bit 1 h)."""
+        r = lib().aoship_internal_layer_last_adapter_major(self.h)
         if r < 0:
             raise AosError(last_error())
         return r

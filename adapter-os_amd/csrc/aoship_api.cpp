@@ -633,13 +633,19 @@ enum {
   KS_DECODE_MLP,
   KS_MLP1,
   KS_PXEXP,
+  KS_PAMPLAN,
+  KS_PAMX,
+  KS_PAMXR,
+  KS_PAMH,
+  KS_PAMHR,
   KS_COUNT
 };
 static const char *kStatNames[KS_COUNT] = {
     "route",         "lora_shrink_x",   "q4_gemv_gate_up", "lora_shrink_h",
     "q4_gemv_down",  "q4_gemv_proj",    "prefill_group_plan",
     "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj",
-    "decode_mlp", "mlp1", "lora_tile_expand_gate_up"};
+    "decode_mlp", "mlp1", "lora_tile_expand_gate_up", "lora_adapter_plan", "lora_adapter_shrink_x",
+    "lora_adapter_reduce_x", "lora_adapter_shrink_h", "lora_adapter_reduce_h"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -670,6 +676,9 @@ struct aoship_layer {
   int prefill_xe_cols = AOS_XE_COLS; /* union columns from which a tile's gate/up expand runs in the
                                         expand launch (0: never) */
   int last_xe = 0;                  /* the last prefill MLP ran the expand launch */
+  int prefill_am_tu = AOS_AM_TU;    /* union adapters from which a tile's shrinks run adapter-major
+                                       (0: never) */
+  int last_am = 0;                  /* the last prefill MLP's adapter-major shrinks: bit 0 x, bit 1 h */
   bool mlp1 = false;             /* one token: the MLP (and its routing) in one launch, down in LDS
                                   * (opt-in: slower than the two launches so far) */
   /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
@@ -1062,6 +1071,24 @@ extern "C" int aoship_internal_layer_set_prefill_expand(aoship_layer_t *l, int c
 extern "C" int aoship_internal_layer_last_expand(aoship_layer_t *l) {
   if (!l) return set_err("aoship_internal_layer_last_expand: null layer");
   return l->last_xe;
+}
+
+/* Diagnostic (no counterpart in the reference): the union size (adapters) from which a tile's
+ * prefill MLP LoRA shrinks run adapter-major (each adapter's users gathered into tiles of their
+ * own) instead of over the tile's union (tu 0: never; negative: the default, AOS_AM_TU). Applies to
+ * the shrinks that run in launches of their own. Results agree within float32 summation order;
+ * each form is deterministic run to run. */
+extern "C" int aoship_internal_layer_set_prefill_adapter_major(aoship_layer_t *l, int tu) {
+  if (!l) return set_err("aoship_internal_layer_set_prefill_adapter_major: null layer");
+  l->prefill_am_tu = tu < 0 ? AOS_AM_TU : tu;
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): the adapter-major shrinks of the layer's last
+ * prefill MLP (its last chunk of tokens): bit 0 the x shrink, bit 1 the h shrink. */
+extern "C" int aoship_internal_layer_last_adapter_major(aoship_layer_t *l) {
+  if (!l) return set_err("aoship_internal_layer_last_adapter_major: null layer");
+  return l->last_am;
 }
 
 /* Diagnostic (no counterpart in the reference): whether the prefill MLP's LoRA shrinks run as
@@ -1797,9 +1824,57 @@ static void plan_sk(aoship_layer *l, Carve &cv, aos_gemm_params &g, bool swiglu)
   g.timeout = l->wait_dev;
 }
 
+/* The adapter-major shrink of sp (modules m0 .. of the plan's tables) over the users that plan A
+ * lists: K slices for about 1024 workgroups, at least 8 groups a slice, at most 16 slices, and
+ * the slices' partial sums within 256 MB. */
+static void plan_amshrink(Carve &cv, const PrefillPlan &P, const aos_tshrink_params &sp, int m0,
+                          const aos_amplan_params &A, aos_amshrink_params &q) {
+  memset(&q, 0, sizeof(q));
+  q.x = sp.x;
+  q.perm = sp.perm;
+  q.T = sp.T;
+  q.in = sp.in;
+  q.nmod = sp.nmod;
+  q.tu_cap = sp.tu_cap;
+  int cw = 0;
+  for (int i = 0; i < sp.nmod; ++i) {
+    q.rpad[i] = sp.rpad[i];
+    q.A[i] = P.gp.tab[m0 + i].A;
+    cw += sp.rpad[i];
+  }
+  q.tu = sp.tu;
+  q.coef = sp.coef;
+  q.ctab = A.ctab;
+  q.users = A.users;
+  q.SA = sp.SA;
+  q.s_stride = sp.s_stride;
+  q.zero_row = sp.zero_row;
+  q.cb = A.cb;
+  q.csets = ceil_div(cw, 128);
+  const int G = sp.in / 64;
+  int ks = ceil_div(1024, q.cb * q.csets);
+  if (ks > 16) ks = 16;
+  if (ks > G / 8) ks = G / 8;
+  if (ks < 1) ks = 1;
+  while (ks > 1 && (size_t)ks * q.cb * q.csets * AOS_GEMM_BM * 128 * 4 > ((size_t)256 << 20)) --ks;
+  q.ks = ks;
+  q.part = ks > 1 ? cv.b.take<float>((size_t)ks * q.cb * q.csets * AOS_GEMM_BM * 128) : nullptr;
+}
+
+/* A shrink that can run adapter-major: a launch of its own, every module present. */
+static bool am_fits(const aos_tshrink_params &sp, bool fused) {
+  if (fused || sp.nmod == 0) return false;
+  for (int i = 0; i < sp.nmod; ++i)
+    if (sp.rpad[i] < 16) return false;
+  return true;
+}
+
 struct MlpPrefill {
   PrefillPlan P;
   aos_tshrink_params sx, sh;
+  aos_amplan_params amp;
+  aos_amshrink_params amx, amh;
+  bool use_am_x = false, use_am_h = false; /* the x / h shrink's wide-union tiles run adapter-major */
   aos_gemm_params g1, g2;
   aos_xexp_params xe;
   bool fused_x = false, fused_h = false; /* the x / h shrink runs in the GEMM launch */
@@ -1832,6 +1907,42 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
   if (M.fused_h) fuse_shrink(l, cv, M.P, M.sh, M.g2);
   plan_sk(l, cv, M.g1, true);
   plan_sk(l, cv, M.g2, false);
+  /* the tiles whose union holds at least prefill_am_tu adapters: their shrinks adapter-major */
+  const int n = (int)l->table.size();
+  M.use_am_x = M.use_am_h = false;
+  if (M.P.lora && l->prefill_am_tu > 0 && n <= AOS_AM_MAX_N && M.P.tu_cap >= l->prefill_am_tu) {
+    M.use_am_x = am_fits(M.sx, M.fused_x);
+    M.use_am_h = am_fits(M.sh, M.fused_h);
+  }
+  if (M.use_am_x || M.use_am_h) {
+    aos_amplan_params &A = M.amp;
+    memset(&A, 0, sizeof(A));
+    A.T = T;
+    A.n = n;
+    A.tu_cap = M.P.tu_cap;
+    A.cb = ceil_div(8 * T, AOS_GEMM_BM) + n;
+    A.am_tu = l->prefill_am_tu;
+    A.tu = M.P.gp.tu;
+    A.list = M.P.gp.list;
+    A.coef = M.P.gp.coef;
+    A.count = cv.counters((size_t)n);
+    A.done = cv.counters(1);
+    A.ctab = cv.b.take<uint32_t>((size_t)A.cb);
+    A.users = cv.b.take<uint32_t>((size_t)n * T);
+    aos_tshrink_params *sps[2] = {&M.sx, &M.sh};
+    const bool on[2] = {M.use_am_x, M.use_am_h};
+    for (int k = 0; k < 2; ++k) {
+      if (!on[k]) continue;
+      aos_tshrink_params &sp = *sps[k];
+      aos_am_zero &z = A.zb[A.nz++];
+      z.SA = sp.SA;
+      z.s_stride = sp.s_stride;
+      z.nmod = sp.nmod;
+      for (int i = 0; i < sp.nmod; ++i) z.rpad[i] = sp.rpad[i];
+      sp.am_tu = A.am_tu;
+      plan_amshrink(cv, M.P, sp, k == 0 ? 0 : 2, A, k == 0 ? M.amx : M.amh);
+    }
+  }
   if (M.P.lora && M.sh.nmod == 0) M.g2.out_perm = perm; /* h is in sorted order even without a down expand */
   if (M.P.lora && M.sx.nmod == 0) M.g1.in_perm = perm;
   /* the gate/up expand of wide tile unions in a launch of its own (the SwiGLU GEMM holds both
@@ -1882,6 +1993,17 @@ static int launch_tshrink(aoship_layer *l, const aos_tshrink_params &sp, int slo
   aos_tshrink_params q = sp;
   q.gen = next_gen(&l->gen);
   return launch_err(aos_launch_tshrink(&q, &c0), "lora shrink (prefill)");
+}
+
+/* Launch an adapter-major shrink and, with its K split, the sum of its slices (slot + 1). */
+static int launch_amshrink(aoship_layer *l, const aos_amshrink_params &q, int slot) {
+  aos_launch_ctx c0 = launch_ctx(l, slot);
+  if (launch_err(aos_launch_amshrink(&q, &c0), "lora adapter-major shrink (prefill)")) return -1;
+  if (q.ks < 2) return 0;
+  aos_amshrink_params r = q;
+  r.reduce = 1;
+  aos_launch_ctx c1 = launch_ctx(l, slot + 1);
+  return launch_err(aos_launch_amshrink(&r, &c1), "lora adapter-major shrink sum (prefill)");
 }
 
 static int chunk_prefill_t(int T) { return T < AOS_PREFILL_MAX_T ? T : AOS_PREFILL_MAX_T; }
@@ -2309,7 +2431,13 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       l->last_perm = M.P.lora ? M.P.gp.perm : nullptr;
       l->last_perm_T = M.P.lora ? Tc : 0;
       if (launch_gplan(l, M.P)) return -1;
+      l->last_am = (M.use_am_x ? 1 : 0) | (M.use_am_h ? 2 : 0);
+      if (M.use_am_x || M.use_am_h) {
+        aos_launch_ctx ca = launch_ctx(l, KS_PAMPLAN);
+        if (launch_err(aos_launch_amplan(&M.amp, &ca), "lora adapter-major plan (prefill)")) return -1;
+      }
       if (!M.fused_x && launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
+      if (M.use_am_x && launch_amshrink(l, M.amx, KS_PAMX)) return -1;
       l->last_xe = M.use_xe ? 1 : 0;
       if (M.use_xe) {
         aos_launch_ctx cx = launch_ctx(l, KS_PXEXP);
@@ -2320,6 +2448,7 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       aos_launch_ctx c2 = launch_ctx(l, KS_GEMM_GU);
       if (launch_err(aos_launch_gemm(&M.g1, 1, &c2), "q4 gemm gate/up")) return -1;
       if (!M.fused_h && launch_tshrink(l, M.sh, KS_PSHRINK_H)) return -1;
+      if (M.use_am_h && launch_amshrink(l, M.amh, KS_PAMH)) return -1;
       if (M.g2.s_cols || M.g2.sk_nwg) M.g2.gen = next_gen(&l->gen);
       aos_launch_ctx c4 = launch_ctx(l, KS_GEMM_DOWN);
       if (launch_err(aos_launch_gemm(&M.g2, 0, &c4), "q4 gemm down")) return -1;

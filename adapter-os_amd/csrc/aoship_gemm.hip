@@ -289,38 +289,26 @@ __global__ void __launch_bounds__(GP_NT) aos_gplan_kernel(aos_gplan_params p) {
     if (t < T) rw[q].load(p.rings + t);
   }
   __syncthreads();
-  /* group of each token: its set's hash, inserted into the table; the slot keeps the lowest token.
-   * Within a wave the lanes of one set elect their lowest lane (its token is the set's lowest in
-   * the wave), which alone touches the table: one pair of LDS atomics per set and wave. */
+  /* group of each token: its set's hash, inserted into the table by every token (linear probing:
+   * the first insert of a hash claims an empty slot, later ones of the same hash stop there, other
+   * hashes probe on; slots are never cleared), and the slot keeps the lowest token */
   uint32_t slot[RPT];
 #pragma unroll
   for (int q = 0; q < RPT; ++q) {
     const int t = tid + q * GP_NT;
-    uint32_t h = 0;
+    slot[q] = 0;
     if (t < T) {
       uint16_t ids[8];
-      h = set_hash(ids, ring_set(rw[q], n, bound_s, ids));
+      uint32_t h = set_hash(ids, ring_set(rw[q], n, bound_s, ids));
       h = h == GP_EMPTY ? GP_EMPTY - 1u : h;
-    }
-    slot[q] = 0;
-    uint64_t todo = __ballot(t < T);
-    while (todo) { /* uniform: todo is the same in every lane */
-      const int leader = __ffsll((long long)todo) - 1;
-      const uint32_t h0 = aos_shfl(h, leader);
-      const uint64_t same = __ballot(h == h0) & todo;
-      uint32_t sl = 0;
-      if (lane == leader) {
-        sl = (h0 * 0x9E3779B1u) >> 19; /* 13 bits: GP_HT slots */
-        for (;;) {
-          const uint32_t old = atomicCAS(&tab_h[sl], GP_EMPTY, h0);
-          if (old == GP_EMPTY || old == h0) break;
-          sl = (sl + 1) & (GP_HT - 1);
-        }
-        atomicMin(&tab_f[sl], (uint32_t)t);
+      uint32_t sl = (h * 0x9E3779B1u) >> 19; /* 13 bits: GP_HT slots */
+      for (;;) {
+        const uint32_t old = atomicCAS(&tab_h[sl], GP_EMPTY, h);
+        if (old == GP_EMPTY || old == h) break;
+        sl = (sl + 1) & (GP_HT - 1);
       }
-      sl = aos_shfl(sl, leader);
-      if ((same >> lane) & 1ull) slot[q] = sl;
-      todo &= ~same;
+      atomicMin(&tab_f[sl], (uint32_t)t);
+      slot[q] = sl;
     }
   }
   __syncthreads();
@@ -457,10 +445,13 @@ __global__ void __launch_bounds__(GP_NT) aos_gplan_kernel(aos_gplan_params p) {
       }
     }
   }
-  /* coefficient rows of the tile: each token's row by one thread, summed in ring order per union
-   * slot (an adapter named twice adds up in order), zeros elsewhere */
+  /* coefficient rows of the tile: each token's (slot, coefficient) pairs by one thread, summed in
+   * ring order per union slot (an adapter named twice adds up in order), staged in LDS (the hash
+   * table's second half is free); then the rows, zeros elsewhere, with consecutive threads on
+   * consecutive entries */
+  int *cu = (int *)tab_f;
+  float *cc = (float *)(tab_f + 8 * BM);
   if (tid < tn) {
-    float *row = p.coef + (size_t)(p0 + tid) * p.tu_cap;
     int us[8];
     float cv[8];
 #pragma unroll
@@ -485,13 +476,20 @@ __global__ void __launch_bounds__(GP_NT) aos_gplan_kernel(aos_gplan_params p) {
         }
       }
     }
-    for (int u = 0; u < U; ++u) {
-      float v = 0.0f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
-        if (us[s] == u) v = cv[s];
-      row[u] = v;
+    for (int s = 0; s < 8; ++s) {
+      cu[tid * 8 + s] = us[s];
+      cc[tid * 8 + s] = cv[s];
     }
+  }
+  __syncthreads();
+  for (int e = tid; e < tn * U; e += GP_NT) {
+    const int r = e / U, u = e - r * U;
+    float v = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (cu[r * 8 + s] == u) v = cc[r * 8 + s];
+    p.coef[(size_t)(p0 + r) * p.tu_cap + u] = v;
   }
 }
 
@@ -521,6 +519,7 @@ __global__ void __launch_bounds__(256) aos_tshrink_kernel(aos_tshrink_params p) 
   const int i = lane & 31, c = lane >> 5;
   const int kz = blockIdx.x, cs = blockIdx.y, mt = blockIdx.z;
   const int TU = __builtin_amdgcn_readfirstlane(p.tu[mt]);
+  if (p.am_tu > 0 && TU >= p.am_tu) return; /* the adapter-major shrink's tile (uniform, as below) */
   const int C = tile_cols(p, TU);
   const int csets = (C + 127) / 128;
   if (cs >= csets) return; /* uniform; such workgroups take no part in the meeting below */
@@ -675,6 +674,317 @@ __global__ void __launch_bounds__(256) aos_tshrink_kernel(aos_tshrink_params p) 
       o.y = (uint32_t)aos_f32_to_bf16(cf * sum[2][e2]) | ((uint32_t)aos_f32_to_bf16(cf * sum[3][e2]) << 16);
       *(u32x2 *)(p.SA + (size_t)(m0 + r + e2) * p.s_stride + cc) = o;
     }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* adapter-major shrink                                                                       */
+/* ------------------------------------------------------------------------------------------ */
+
+constexpr int AM_NT = 512; /* plan threads */
+constexpr int AM_ZB = 8;    /* zeroing workgroups per tile */
+constexpr int AM_CB = 8;    /* coefficients each thread has in flight */
+
+/* Workgroup (x, mt) of the tiles with tu >= am_tu. x = 0: counts the tile's users per union slot
+ * in LDS, reserves each slot's range of its adapter's list with one atomic add and places the
+ * users; the last of these to arrive builds the chunk table and resets the counts. x = 1 ..
+ * AM_ZB: zero rows (x - 1) * 128 / AM_ZB .. of the tile's union columns in each SA buffer (the
+ * users' entries are overwritten by the shrink). */
+__global__ void __launch_bounds__(AM_NT) aos_amplan_kernel(aos_amplan_params p) {
+  __shared__ uint32_t lc[AOS_TILE_U_MAX], base[AOS_TILE_U_MAX];
+  __shared__ uint32_t cst[AM_NT];
+  __shared__ uint32_t last;
+  const int tid = threadIdx.x, mt = blockIdx.y;
+  const int TU = __builtin_amdgcn_readfirstlane(p.tu[mt]);
+  const bool am = p.am_tu > 0 && TU >= p.am_tu;
+  const int m0 = mt * BM, tn = p.T - m0 < BM ? p.T - m0 : BM;
+  if (blockIdx.x > 0) {
+    if (!am) return;
+    const int r0 = (blockIdx.x - 1) * BM / AM_ZB, r1 = blockIdx.x * BM / AM_ZB < tn ? blockIdx.x * BM / AM_ZB : tn;
+#pragma unroll
+    for (int z = 0; z < 2; ++z) {
+      if (z >= p.nz) break;
+      int C = 0;
+      for (int i = 0; i < p.zb[z].nmod; ++i) C += TU * p.zb[z].rpad[i];
+      const int c8 = C / 8; /* C is a multiple of 16 */
+      uint16_t *SA = p.zb[z].SA;
+      const size_t st = (size_t)p.zb[z].s_stride;
+      for (int e = tid; e < (r1 - r0) * c8; e += AM_NT) {
+        const int r = e / c8, q = e - r * c8;
+        *(u32x4 *)(SA + (size_t)(m0 + r0 + r) * st + 8 * q) = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    return;
+  }
+  if (am) {
+    const float *cf = p.coef + (size_t)m0 * p.tu_cap;
+    const uint16_t *ls = p.list + (size_t)mt * p.tu_cap;
+    for (int u = tid; u < TU; u += AM_NT) lc[u] = 0;
+    __syncthreads();
+    const int ne = tn * TU;
+    /* entry e = r * TU + u, AM_CB of a thread's entries loaded before any is used */
+    auto coefs = [&](int e0, float (&v)[AM_CB], int (&uu)[AM_CB], int (&rr)[AM_CB]) {
+#pragma unroll
+      for (int k = 0; k < AM_CB; ++k) {
+        const int e = e0 + k * AM_NT + tid;
+        rr[k] = e / TU;
+        uu[k] = e - rr[k] * TU;
+        v[k] = e < ne ? cf[(size_t)rr[k] * p.tu_cap + uu[k]] : 0.0f;
+      }
+    };
+    for (int e0 = 0; e0 < ne; e0 += AM_CB * AM_NT) {
+      float v[AM_CB];
+      int uu[AM_CB], rr[AM_CB];
+      coefs(e0, v, uu, rr);
+#pragma unroll
+      for (int k = 0; k < AM_CB; ++k)
+        if (v[k] != 0.0f) atomicAdd(&lc[uu[k]], 1u);
+    }
+    __syncthreads();
+    for (int u = tid; u < TU; u += AM_NT) {
+      base[u] = lc[u] ? __hip_atomic_fetch_add(&p.count[ls[u]], lc[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      lc[u] = 0;
+    }
+    __syncthreads();
+    for (int e0 = 0; e0 < ne; e0 += AM_CB * AM_NT) {
+      float v[AM_CB];
+      int uu[AM_CB], rr[AM_CB];
+      coefs(e0, v, uu, rr);
+#pragma unroll
+      for (int k = 0; k < AM_CB; ++k)
+        if (v[k] != 0.0f) {
+          const uint32_t kk = base[uu[k]] + atomicAdd(&lc[uu[k]], 1u);
+          p.users[(size_t)ls[uu[k]] * p.T + kk] = ((uint32_t)(m0 + rr[k]) << 16) | (uint32_t)uu[k];
+        }
+    }
+  }
+  /* arrive once this workgroup's atomics and stores are complete */
+  aos_mem_wait();
+  __syncthreads();
+  if (tid == 0) last = aos_arrive(p.done) == gridDim.y - 1u ? 1u : 0u;
+  __syncthreads();
+  if (!last) return;
+  /* the chunk table: thread t takes adapters t * per .. (every count is final) */
+  const int per = (p.n + AM_NT - 1) / AM_NT;
+  const int a0 = tid * per, a1 = a0 + per < p.n ? a0 + per : p.n;
+  uint32_t mine = 0;
+  for (int a = a0; a < a1; ++a)
+    mine += (__hip_atomic_load(&p.count[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + BM - 1) / BM;
+  cst[tid] = mine;
+  __syncthreads();
+  for (int off = 1; off < AM_NT; off <<= 1) { /* inclusive scan */
+    const uint32_t v = tid >= off ? cst[tid - off] : 0u;
+    __syncthreads();
+    cst[tid] += v;
+    __syncthreads();
+  }
+  uint32_t c = cst[tid] - mine;
+  for (int a = a0; a < a1; ++a) {
+    const uint32_t n = __hip_atomic_load(&p.count[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t j = 0; j * BM < n; ++j, ++c) {
+      const uint32_t nu = n - j * BM < (uint32_t)BM ? n - j * BM : (uint32_t)BM;
+      if (c < (uint32_t)p.cb) p.ctab[c] = ((uint32_t)a << 16) | (j << 8) | nu;
+    }
+    __hip_atomic_store(&p.count[a], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  for (uint32_t e = cst[AM_NT - 1] + tid; e < (uint32_t)p.cb; e += AM_NT) p.ctab[e] = 0u;
+  if (tid == 0) aos_reset(p.done);
+}
+
+/* Row r's user of a chunk, staged in LDS for the stores: SA row p, its tile's union size, slot u,
+ * coefficient. */
+struct AmUser {
+  uint32_t p, tu, u;
+  float cf;
+};
+
+__device__ __forceinline__ void am_users(const aos_amshrink_params &p, const uint32_t *ul, int nu, AmUser *meta,
+                                         int tid) {
+  if (tid < nu) {
+    const uint32_t w = ul[tid];
+    const uint32_t pp = w >> 16, u = w & 0xffffu;
+    meta[tid] = AmUser{pp, (uint32_t)p.tu[pp / BM], u, p.coef[(size_t)pp * p.tu_cap + u]};
+  }
+}
+
+/* Module of adapter column col (modules in order, rpad_i columns each): its index, the column
+ * within it and the sum of the rpad of the modules before it. */
+__device__ __forceinline__ void am_module(const aos_amshrink_params &p, int col, int &mi, int &j, int &rbefore) {
+  mi = 0;
+  rbefore = 0;
+  while (mi < p.nmod - 1 && col >= rbefore + p.rpad[mi]) {
+    rbefore += p.rpad[mi];
+    ++mi;
+  }
+  j = col - rbefore;
+}
+
+/* Workgroup (K slice kz, chunk c, column set cs of 128 adapter columns), kz fastest; wave w takes
+ * the 32 columns cs * 128 + 32 w .., all the chunk's users (four 32-row sub-tiles): the tile
+ * shrink's K loop over the users' gathered rows. Waves without columns (an adapter of fewer than
+ * 128 columns) only stage rows. (Two waves per 32-column block, each on half the rows, so that
+ * every SIMD has matrix work at 64 columns, was slower: 343 against 275 us for the rank-64 down
+ * shrink at 4096 tokens; both load the block's A rows, and the kernel is bound by its loads.) */
+__global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p) {
+  constexpr int MT = BM / 32, TILE = BM * 128;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, c = lane >> 5;
+  const int kz = blockIdx.x, ch = blockIdx.y, cs = blockIdx.z;
+  const uint32_t ct = __builtin_amdgcn_readfirstlane(p.ctab[ch]);
+  const int nu = (int)(ct & 255u);
+  if (nu == 0) return;
+  const int a = (int)(ct >> 16), jc = (int)((ct >> 8) & 255u);
+  const uint32_t *ul = p.users + (size_t)a * p.T + jc * BM;
+  int CW = 0;
+  for (int m = 0; m < p.nmod; ++m) CW += p.rpad[m];
+  const int G = p.in / 64;
+  const int g_lo = (int)((long)kz * G / p.ks), g_hi = (int)((long)(kz + 1) * G / p.ks);
+
+  const int col = cs * 128 + 32 * wave + i;
+  const bool wact = cs * 128 + 32 * wave < CW; /* wave-uniform: the wave has columns */
+  int mi = 0, jj = 0, rbefore = 0;
+  const uint16_t *arow = p.zero_row;
+  size_t kstep = 0;
+  if (col < CW) {
+    am_module(p, col, mi, jj, rbefore);
+    const uint16_t *A = p.A[mi][a];
+    if (A) {
+      arow = A + (size_t)jj * p.in;
+      kstep = 1;
+    }
+  }
+  auto aload = [&](int g, u32x4 (&av)[4]) {
+    const int gc = g < g_hi ? g : g_hi - 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) av[s] = aos_gld16(arow + kstep * ((size_t)gc * 64 + 16 * s + 8 * c));
+  };
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int s = 0; s < MT; ++s) acc[s] = f32x16{};
+  if (g_lo < g_hi) {
+    Stager<256> st0, st1;
+#pragma unroll
+    for (int k = 0; k < Stager<256>::CH; ++k) {
+      const int idx = tid + k * 256;
+      const int r = idx >> 3, chk = idx & 7;
+      const int pp = (int)(ul[r < nu ? r : nu - 1] >> 16);
+      const int tok = p.perm ? (int)p.perm[pp] : pp;
+      st0.off[k] = tok * p.in + chk * 8;
+      st1.off[k] = st0.off[k];
+    }
+    u32x4 a0[4], a1[4];
+    st0.load(p.x, g_lo);
+    st1.load(p.x, g_lo + 1 < g_hi ? g_lo + 1 : g_hi - 1);
+    aload(g_lo, a0);
+    aload(g_lo + 1, a1);
+    st0.store(smem, tid);
+    lds_barrier();
+    auto step = [&](int g, Stager<256> &hold, Stager<256> &ld, u32x4 (&av)[4]) {
+      const unsigned char *tb = smem + ((g - g_lo) & 1) * TILE;
+      ld.load(p.x, g + 2 < g_hi ? g + 2 : g_hi - 1);
+      if (wact) {
+#pragma unroll
+        for (int s = 0; s < MT; ++s) {
+          const int r = s * 32 + i;
+          u32x4 xv[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) xv[k] = *(const u32x4 *)(tb + tile_off(r, 2 * k + c));
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[s] = aos_mfma32(xv[k], av[k], acc[s]);
+        }
+      }
+      aload(g + 2, av);
+      hold.store(smem + (((g - g_lo) & 1) ^ 1) * TILE, tid);
+      lds_barrier();
+    };
+    int g = g_lo;
+    for (; g + 1 < g_hi; g += 2) {
+      step(g, st1, st0, a0);
+      step(g + 1, st0, st1, a1);
+    }
+    if (g < g_hi) step(g, st1, st0, a0);
+  }
+
+  if (p.ks > 1) {
+    /* this slice's partial sums, [row][128 columns] */
+    if (col < CW) {
+      float *dst = p.part + (((size_t)kz * p.cb + ch) * p.csets + cs) * BM * 128 + (col - cs * 128);
+#pragma unroll
+      for (int s = 0; s < MT; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = s * 32 + 8 * q + 4 * c + e;
+            if (r < nu) dst[(size_t)r * 128] = acc[s][4 * q + e];
+          }
+    }
+    return;
+  }
+  /* one slice: SA directly (the tile buffers are free past the K loop's last barrier) */
+  AmUser *meta = (AmUser *)smem;
+  __syncthreads();
+  am_users(p, ul, nu, meta, tid);
+  __syncthreads();
+  if (col < CW) {
+    const int rp = p.rpad[mi];
+#pragma unroll
+    for (int s = 0; s < MT; ++s)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = s * 32 + 8 * q + 4 * c + e;
+          if (r < nu) {
+            const AmUser m = meta[r];
+            p.SA[(size_t)m.p * p.s_stride + m.tu * rbefore + m.u * rp + jj] = aos_f32_to_bf16(m.cf * acc[s][4 * q + e]);
+          }
+        }
+  }
+}
+
+/* Workgroup (chunk c, column set cs): sums the slices' partials in slice order, four columns of
+ * one row per thread step, and stores SA = bf16(coef * sum). */
+__global__ void __launch_bounds__(256) aos_amreduce_kernel(aos_amshrink_params p) {
+  __shared__ AmUser meta[BM];
+  const int tid = threadIdx.x, ch = blockIdx.x, cs = blockIdx.y;
+  const uint32_t ct = __builtin_amdgcn_readfirstlane(p.ctab[ch]);
+  const int nu = (int)(ct & 255u);
+  if (nu == 0) return;
+  const int a = (int)(ct >> 16), jc = (int)((ct >> 8) & 255u);
+  am_users(p, p.users + (size_t)a * p.T + jc * BM, nu, meta, tid);
+  __syncthreads();
+  int CW = 0;
+  for (int m = 0; m < p.nmod; ++m) CW += p.rpad[m];
+  const int cn = CW - cs * 128 < 128 ? CW - cs * 128 : 128;
+  const int ncg = cn / 4; /* rpad_i are multiples of 16: a group of 4 columns lies in one module */
+  const size_t slab = (size_t)p.cb * p.csets * BM * 128;
+  const float *src = p.part + ((size_t)ch * p.csets + cs) * BM * 128;
+  for (int e = tid; e < nu * ncg; e += 256) {
+    const int r = e / ncg, cg = e - r * ncg;
+    const float *s0 = src + (size_t)r * 128 + cg * 4;
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < p.ks; k0 += 4) {
+      f32x4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int kk = k0 + k < p.ks ? k0 + k : p.ks - 1;
+        v[k] = *(const f32x4 *)(s0 + (size_t)kk * slab);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k0 + k < p.ks) sum += v[k];
+    }
+    int mi, jj, rbefore;
+    am_module(p, cs * 128 + cg * 4, mi, jj, rbefore);
+    const AmUser m = meta[r];
+    u32x2 o;
+    o.x = (uint32_t)aos_f32_to_bf16(m.cf * sum[0]) | ((uint32_t)aos_f32_to_bf16(m.cf * sum[1]) << 16);
+    o.y = (uint32_t)aos_f32_to_bf16(m.cf * sum[2]) | ((uint32_t)aos_f32_to_bf16(m.cf * sum[3]) << 16);
+    *(u32x2 *)(p.SA + (size_t)m.p * p.s_stride + m.tu * rbefore + m.u * p.rpad[mi] + jj) = o;
   }
 }
 
@@ -1577,6 +1887,45 @@ extern "C" int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_
   if (!p->counters || !p->flags || !p->gen) return (int)hipErrorInvalidValue;
   dim3 grid(p->ks, p->csets, p->mtiles);
   AOS_LAUNCH(ctx, aos_tshrink_kernel, grid, dim3(256), 2 * BM * 128, *p);
+  return (int)hipGetLastError();
+}
+
+extern "C" int aos_launch_amplan(const aos_amplan_params *p, const aos_launch_ctx *ctx) {
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->n < 1 || p->n > AOS_AM_MAX_N || p->am_tu < 1 || p->tu_cap < 1 ||
+      p->tu_cap > AOS_TILE_U_MAX || p->cb < (8 * p->T + BM - 1) / BM + p->n || p->cb > 65535 || !p->count ||
+      !p->done || !p->ctab || !p->users || !p->tu || !p->list || !p->coef || p->nz < 0 || p->nz > 2)
+    return (int)hipErrorInvalidValue;
+  for (int z = 0; z < p->nz; ++z) {
+    const aos_am_zero &zb = p->zb[z];
+    if (!zb.SA || zb.nmod < 1 || zb.nmod > 3 || zb.s_stride % 8) return (int)hipErrorInvalidValue;
+    int cols = 0;
+    for (int i = 0; i < zb.nmod; ++i) {
+      if (zb.rpad[i] < 0 || zb.rpad[i] % 16) return (int)hipErrorInvalidValue;
+      cols += p->tu_cap * zb.rpad[i];
+    }
+    if (cols > zb.s_stride) return (int)hipErrorInvalidValue;
+  }
+  AOS_LAUNCH(ctx, aos_amplan_kernel, dim3(1 + AM_ZB, (p->T + BM - 1) / BM), dim3(AM_NT), 0, *p);
+  return (int)hipGetLastError();
+}
+
+extern "C" int aos_launch_amshrink(const aos_amshrink_params *p, const aos_launch_ctx *ctx) {
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->nmod < 1 || p->nmod > 3 || p->ks < 1 || p->cb < 1 ||
+      p->cb > 65535 || p->in % 64 || p->in < 64 * p->ks || !p->ctab || !p->users || !p->tu || !p->coef || !p->SA ||
+      !p->zero_row || (p->ks > 1 && !p->part))
+    return (int)hipErrorInvalidValue;
+  int cols = 0;
+  for (int i = 0; i < p->nmod; ++i) {
+    if (p->rpad[i] < 16 || p->rpad[i] % 16 || !p->A[i]) return (int)hipErrorInvalidValue;
+    cols += p->rpad[i];
+  }
+  if (p->csets != (cols + 127) / 128 || p->s_stride % 8) return (int)hipErrorInvalidValue;
+  if (p->reduce) {
+    if (p->ks < 2) return (int)hipErrorInvalidValue;
+    AOS_LAUNCH(ctx, aos_amreduce_kernel, dim3(p->cb, p->csets), dim3(256), 0, *p);
+  } else {
+    AOS_LAUNCH(ctx, aos_amshrink_kernel, dim3(p->ks, p->cb, p->csets), dim3(256), 2 * BM * 128, *p);
+  }
   return (int)hipGetLastError();
 }
 

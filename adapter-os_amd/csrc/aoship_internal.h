@@ -385,7 +385,62 @@ typedef struct {
   uint16_t *SA;            /* [T][s_stride] bf16, sorted rows */
   int s_stride;            /* >= sum over modules of tu_cap * rpad_i, multiple of 64 */
   const uint16_t *zero_row;
+  int am_tu;               /* > 0: tiles with tu >= am_tu are the adapter-major shrink's */
 } aos_tshrink_params;
+
+/* Adapter-major LoRA shrink: the alternative to the tile shrink when tile unions are much wider
+ * than the adapters a token routes to (tokens that do not cluster). Users of adapter a: the
+ * sorted positions p with a nonzero coefficient for a (union slot u of p's tile), in chunks of 128.
+ * aos_amplan (one launch after the group plan) lists them: users[a * T + k] = (p << 16) | u for
+ * k < count[a]; chunk c of the launch, ctab[c] = (a << 16) | (j << 8) | nu, is the j-th chunk of
+ * adapter a, users[a * T + 128 j + r] for r < nu, adapters in index order; ctab[c] = 0 for the
+ * unused tail up to cb (users of one adapter in no particular order: each user's sums depend on its own row
+ * only); its other workgroups zero, in each SA buffer zb[], the entries of the tile's union columns
+ * that no user covers (coefficient 0). Only tiles with tu >= am_tu take part (the tile shrink,
+ * given the same am_tu, skips them). The last plan workgroup to finish builds ctab from the counts
+ * and resets count[] and done[0] (both zero at rest). aos_amshrink, per chunk c, column set cs of the adapter's
+ * columns (modules in order, rpad_i each) and K slice kz:
+ * S[r][col] = sum_k x[row(p)][k] A_i,a[j][k] (row(p) = perm[p], or p without a permutation),
+ * SA[p][off_i(tile(p)) + u * rpad_i + j] = bf16(coef[p][u] * S), off_i as in the tile shrink;
+ * with ks > 1 slices each slice stores float32 partials and the reduce launch (reduce = 1, grid
+ * cb x csets) sums them in slice order. */
+#define AOS_AM_MAX_N 1024 /* adapters the adapter-major shrink takes */
+#define AOS_AM_TU 8       /* union size (adapters) from which a prefill tile's shrinks run adapter-major */
+typedef struct {
+  uint16_t *SA;
+  int s_stride, nmod;
+  int rpad[3];
+} aos_am_zero;
+
+typedef struct {
+  int T, n, tu_cap, cb, am_tu;
+  const int *tu;
+  const uint16_t *list;    /* [mtiles][tu_cap] */
+  const float *coef;       /* [T][tu_cap] */
+  uint32_t *count;         /* [n], zero at rest */
+  uint32_t *done;          /* [1], zero at rest */
+  uint32_t *ctab;          /* [cb] */
+  uint32_t *users;         /* [n][T] */
+  int nz;
+  aos_am_zero zb[2];
+} aos_amplan_params;
+
+typedef struct {
+  const uint16_t *x;       /* [T][in] */
+  const uint16_t *perm;    /* [T] or NULL */
+  int T, in, nmod, tu_cap, ks, cb, csets; /* grid: ks x cb x csets (reduce: cb x csets) */
+  /* csets: ceil(sum of rpad_i / 128) */
+  int rpad[3];
+  const uint16_t *const *A[3]; /* per module: [n] device A pointers (NULL: adapter without it) */
+  const int *tu;
+  const float *coef;
+  const uint32_t *ctab, *users; /* ctab[c] = (a << 16) | (j << 8) | users in the chunk (0: unused) */
+  uint16_t *SA;
+  int s_stride;
+  float *part;             /* [ks][cb][csets][128][128] float32 when ks > 1 */
+  const uint16_t *zero_row;
+  int reduce;
+} aos_amshrink_params;
 
 /* int4 GEMM with the LoRA expand over the tile union: y[p][o] = sum_k x[p][k] w[o][k] +
  * sum_c SA[p][off + c] B_{list[u]}[o][c - u * rpad] (the expand as extra K steps of 64 union
@@ -559,6 +614,8 @@ int aos_fused_params_ok(const aos_gemv_fused_params *fp, int swiglu); /* 1: cons
 int aos_launch_route_gate_up(const aos_route_gu_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
+int aos_launch_amplan(const aos_amplan_params *p, const aos_launch_ctx *ctx);
+int aos_launch_amshrink(const aos_amshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_xexp(const aos_xexp_params *p, const aos_launch_ctx *ctx);
 int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);

@@ -251,6 +251,38 @@ def test_mlp_prefill_expand_launch(hip, T):
     assert tol_ratio(out[50 * cfg.rank], out[0]) <= REL_TOL / 2
 
 
+@pytest.mark.parametrize("cid,T,mixed", [(5, 1024, 50), (5, 1100, 50), (3, 2048, 6), (1, 300, 4)])
+def test_mlp_prefill_adapter_major(hip, cid, T, mixed):
+    """The prefill LoRA shrinks adapter-major (each adapter's users gathered into tiles of their
+    own, K split into slices whose sums add in slice order) for no tile (0), every tile (1) and the
+    tiles whose union holds at least `mixed` adapters, so that both forms meet in one call: on the
+    32B-shaped stress layer (64 rank-64 adapters, K = 8, adversarial routing; a ragged last tile at
+    1100 tokens), the 7B-shaped layer (rank 16, clustered) and the 0.5B-shaped one (rank 8, padded
+    to 16). Each form is bit-identical run to run and within tolerance of the oracle on every
+    tile; the forms agree with each other up to float32 summation order."""
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    layer.set_prefill_shrink(False)
+    out = {}
+    for tu in (0, 1, mixed):
+        layer.set_prefill_adapter_major(tu)
+        y = _run_mlp(hip, layer, xb, rings)
+        assert layer.last_adapter_major() == (3 if tu else 0), f"tu={tu}: adapter-major state"
+        assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), f"tu={tu}: run-to-run outputs differ"
+        out[tu] = W.bf16_bits_to_f32(y).reshape(T, -1)
+    layer.set_prefill_adapter_major(-1)
+    perm = layer.last_perm()
+    sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
+    ref = oracle_mlp(cid, xf[sample], rings[sample])
+    for tu, y in out.items():
+        ratio = assert_parity(f"config {cid} prefill T={T} adapter-major from {tu}", y[sample], ref)
+        assert ratio <= REL_TOL, f"tu={tu}: max tolerance ratio {ratio:.4g}"
+    assert tol_ratio(out[1], out[0]) <= REL_TOL / 2
+    assert tol_ratio(out[mixed], out[0]) <= REL_TOL / 2
+
+
 @pytest.mark.parametrize("cid,T", [(1, 300), (3, 2048)])
 def test_mlp_prefill_shrink_modes(hip, cid, T):
     """The prefill LoRA shrinks as the first workgroups of the GEMM launches (default) and as
