@@ -138,6 +138,8 @@ def lib():
         L.aoship_internal_layer_last_expand.argtypes = [_P]
         L.aoship_internal_layer_set_prefill_adapter_major.restype = C.c_int
         L.aoship_internal_layer_set_prefill_adapter_major.argtypes = [_P, C.c_int]
+        L.aoship_internal_layer_set_prefill_expand_adapter_major.restype = C.c_int
+        L.aoship_internal_layer_set_prefill_expand_adapter_major.argtypes = [_P, C.c_int]
         L.aoship_internal_layer_last_adapter_major.restype = C.c_int
         L.aoship_internal_layer_last_adapter_major.argtypes = [_P]
         L.aoship_internal_layer_last_perm.restype = C.c_int
@@ -468,8 +470,15 @@ class Layer:
         _check(lib().aoship_internal_layer_set_prefill_adapter_major(self.h, int(tu)),
                "aoship_internal_layer_set_prefill_adapter_major")
 
+    def set_prefill_expand_adapter_major(self, tu: int = -1) -> None:
+        """Diagnostic: the union size (adapters) from which a prefill tile's gate/up LoRA expand runs
+        adapter-major, its sums added in LDS in adapter order (0: never; negative: the default)."""
+        _check(lib().aoship_internal_layer_set_prefill_expand_adapter_major(self.h, int(tu)),
+               "aoship_internal_layer_set_prefill_expand_adapter_major")
+
     def last_adapter_major(self) -> int:
-        """Diagnostic: the last prefill MLP's adapter-major shrinks (bit 0 x, bit 1 h)."""
+        """Diagnostic: the last prefill MLP's adapter-major launches (bit 0 the x shrink, bit 1 the
+        h shrink, bit 2 the gate/up expand)."""
         r = lib().aoship_internal_layer_last_adapter_major(self.h)
         if r < 0:
             raise AosError(last_error())

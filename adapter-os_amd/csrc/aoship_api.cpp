@@ -638,6 +638,8 @@ enum {
   KS_PAMXR,
   KS_PAMH,
   KS_PAMHR,
+  KS_PXAML,
+  KS_PXAM,
   KS_COUNT
 };
 static const char *kStatNames[KS_COUNT] = {
@@ -645,7 +647,8 @@ static const char *kStatNames[KS_COUNT] = {
     "q4_gemv_down",  "q4_gemv_proj",    "prefill_group_plan",
     "lora_tile_shrink_x", "q4_gemm_gate_up", "lora_tile_shrink_h", "q4_gemm_down",   "q4_gemm_proj",
     "decode_mlp", "mlp1", "lora_tile_expand_gate_up", "lora_adapter_plan", "lora_adapter_shrink_x",
-    "lora_adapter_reduce_x", "lora_adapter_shrink_h", "lora_adapter_reduce_h"};
+    "lora_adapter_reduce_x", "lora_adapter_shrink_h", "lora_adapter_reduce_h", "lora_adapter_expand_list",
+    "lora_adapter_expand_gate_up"};
 
 struct aoship_layer {
   int layer_idx = 0;
@@ -678,7 +681,10 @@ struct aoship_layer {
   int last_xe = 0;                  /* the last prefill MLP ran the expand launch */
   int prefill_am_tu = AOS_AM_TU;    /* union adapters from which a tile's shrinks run adapter-major
                                        (0: never) */
-  int last_am = 0;                  /* the last prefill MLP's adapter-major shrinks: bit 0 x, bit 1 h */
+  int last_am = 0;                  /* the last prefill MLP's adapter-major launches: bit 0 the x shrink,
+                                       bit 1 the h shrink, bit 2 the gate/up expand */
+  int prefill_xam_tu = AOS_XAM_TU;  /* union adapters from which a tile's gate/up expand runs
+                                       adapter-major (0: never) */
   bool mlp1 = false;             /* one token: the MLP (and its routing) in one launch, down in LDS
                                   * (opt-in: slower than the two launches so far) */
   /* decode GEMV geometry forced per launch kind (0 gate/up, 1 down, 2 projections): row blocks per
@@ -1084,8 +1090,21 @@ extern "C" int aoship_internal_layer_set_prefill_adapter_major(aoship_layer_t *l
   return 0;
 }
 
-/* Diagnostic (no counterpart in the reference): the adapter-major shrinks of the layer's last
- * prefill MLP (its last chunk of tokens): bit 0 the x shrink, bit 1 the h shrink. */
+/* Diagnostic (no counterpart in the reference): the union size (adapters) from which a tile's
+ * prefill MLP gate/up LoRA expand runs adapter-major (each adapter's users gathered into MFMA tiles,
+ * their sums added in LDS in adapter order) instead of over the tile's union in the expand launch
+ * (tu 0: never; negative: the default, AOS_XAM_TU). Applies with the expand launch and the
+ * adapter-major shrinks' user lists, up to AOS_XAM_MAX_N bound adapters and ranks of 64. Results
+ * agree within float32 summation order; each form is deterministic run to run. */
+extern "C" int aoship_internal_layer_set_prefill_expand_adapter_major(aoship_layer_t *l, int tu) {
+  if (!l) return set_err("aoship_internal_layer_set_prefill_expand_adapter_major: null layer");
+  l->prefill_xam_tu = tu < 0 ? AOS_XAM_TU : tu;
+  return 0;
+}
+
+/* Diagnostic (no counterpart in the reference): the adapter-major launches of the layer's last
+ * prefill MLP (its last chunk of tokens): bit 0 the x shrink, bit 1 the h shrink, bit 2 the gate/up
+ * expand. */
 extern "C" int aoship_internal_layer_last_adapter_major(aoship_layer_t *l) {
   if (!l) return set_err("aoship_internal_layer_last_adapter_major: null layer");
   return l->last_am;
@@ -1874,7 +1893,9 @@ struct MlpPrefill {
   aos_tshrink_params sx, sh;
   aos_amplan_params amp;
   aos_amshrink_params amx, amh;
+  aos_amx_params ame;
   bool use_am_x = false, use_am_h = false; /* the x / h shrink's wide-union tiles run adapter-major */
+  bool use_xam = false;                    /* ... and the gate/up expand of the widest */
   aos_gemm_params g1, g2;
   aos_xexp_params xe;
   bool fused_x = false, fused_h = false; /* the x / h shrink runs in the GEMM launch */
@@ -1970,6 +1991,48 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
     X.xe_cols = l->prefill_xe_cols;
     X.rmax = rxe;
     M.use_xe = true;
+  }
+  /* the tiles whose union holds at least prefill_xam_tu adapters (a subset of the expand launch's
+   * and of the adapter-major shrinks' tiles): their gate/up expand adapter-major */
+  M.use_xam = false;
+  const int xt = l->prefill_xam_tu;
+  if (M.use_xe && M.use_am_x && n <= AOS_XAM_MAX_N && xt > 0 && xt >= l->prefill_am_tu &&
+      xt * rxe >= l->prefill_xe_cols && M.P.tu_cap >= xt && M.g1.rpad0 >= 16 && M.g1.rpad0 <= 64 &&
+      M.g1.rpad1 >= 16 && M.g1.rpad1 <= 64) {
+    aos_amplan_params &A = M.amp;
+    A.tinfo = cv.b.take<uint32_t>((size_t)M.P.mtiles * M.P.tu_cap);
+    A.inv = cv.b.take<uint16_t>((size_t)M.P.mtiles * n);
+    A.xl = cv.b.take<uint32_t>((size_t)M.P.mtiles + 1);
+    A.xam_tu = xt;
+    aos_amx_params &Q = M.ame;
+    memset(&Q, 0, sizeof(Q));
+    Q.T = T;
+    Q.n = n;
+    Q.tu_cap = M.P.tu_cap;
+    Q.mtiles = M.P.mtiles;
+    Q.RB = Wg.RB;
+    Q.tu = M.P.gp.tu;
+    Q.tinfo = A.tinfo;
+    Q.inv = A.inv;
+    Q.xl = A.xl;
+    Q.users = A.users;
+    const int ranges = ceil_div(M.P.mtiles, AOS_XAM_RT);
+    Q.rl = cv.b.take<uint32_t>((size_t)ranges * AOS_XAM_RT * AOS_GEMM_BM * 8);
+    Q.ct = cv.b.take<uint32_t>((size_t)ranges * (AOS_XAM_RT * 8 + AOS_XAM_MAX_N));
+    Q.nch = cv.b.take<uint32_t>((size_t)ranges);
+    Q.cidx = cv.b.take<uint32_t>((size_t)n * T);
+    Q.SAc = cv.b.take<uint16_t>((size_t)ranges * AOS_XAM_RT * AOS_GEMM_BM * 8 * (M.g1.rpad0 + M.g1.rpad1));
+    M.amx.cidx = Q.cidx;
+    M.amx.SAc = (uint16_t *)Q.SAc;
+    M.amx.xam_tu = xt;
+    Q.rpad[0] = M.g1.rpad0;
+    Q.rpad[1] = M.g1.rpad1;
+    Q.Bf[0] = M.P.gp.tab[0].Bf;
+    Q.Bf[1] = M.P.gp.tab[1].Bf;
+    Q.zero = l->zeros.as<uint16_t>();
+    Q.xd = M.xe.xd;
+    M.xe.xam_tu = xt;
+    M.use_xam = true;
   }
   M.bytes = cv.b.off + 256;
   M.ctr = cv.coff + 64;
@@ -2431,13 +2494,23 @@ extern "C" int aoship_mlp_forward(aoship_layer_t *l, const aoship_bf16_t *x, int
       l->last_perm = M.P.lora ? M.P.gp.perm : nullptr;
       l->last_perm_T = M.P.lora ? Tc : 0;
       if (launch_gplan(l, M.P)) return -1;
-      l->last_am = (M.use_am_x ? 1 : 0) | (M.use_am_h ? 2 : 0);
+      l->last_am = (M.use_am_x ? 1 : 0) | (M.use_am_h ? 2 : 0) | (M.use_xam ? 4 : 0);
       if (M.use_am_x || M.use_am_h) {
         aos_launch_ctx ca = launch_ctx(l, KS_PAMPLAN);
         if (launch_err(aos_launch_amplan(&M.amp, &ca), "lora adapter-major plan (prefill)")) return -1;
       }
+      if (M.use_xam) { /* before the x shrink, which writes the compact rows it lists */
+        aos_amx_params q = M.ame;
+        q.list = 1;
+        aos_launch_ctx cl = launch_ctx(l, KS_PXAML);
+        if (launch_err(aos_launch_amx(&q, &cl), "lora adapter-major expand lists (prefill)")) return -1;
+      }
       if (!M.fused_x && launch_tshrink(l, M.sx, KS_PSHRINK_X)) return -1;
       if (M.use_am_x && launch_amshrink(l, M.amx, KS_PAMX)) return -1;
+      if (M.use_xam) {
+        aos_launch_ctx ce = launch_ctx(l, KS_PXAM);
+        if (launch_err(aos_launch_amx(&M.ame, &ce), "lora adapter-major expand gate/up (prefill)")) return -1;
+      }
       l->last_xe = M.use_xe ? 1 : 0;
       if (M.use_xe) {
         aos_launch_ctx cx = launch_ctx(l, KS_PXEXP);

@@ -757,6 +757,16 @@ __global__ void __launch_bounds__(AM_NT) aos_amplan_kernel(aos_amplan_params p) 
           p.users[(size_t)ls[uu[k]] * p.T + kk] = ((uint32_t)(m0 + rr[k]) << 16) | (uint32_t)uu[k];
         }
     }
+    if (p.tinfo) { /* each slot's range of its adapter's users, and the slot of each adapter */
+      __syncthreads();
+      for (int u = tid; u < TU; u += AM_NT) p.tinfo[(size_t)mt * p.tu_cap + u] = (base[u] << 8) | lc[u];
+      if (p.xam_tu > 0 && TU >= p.xam_tu) {
+        uint16_t *inv = p.inv + (size_t)mt * p.n;
+        for (int a = tid; a < p.n; a += AM_NT) inv[a] = 0xffffu;
+        __syncthreads();
+        for (int u = tid; u < TU; u += AM_NT) inv[ls[u]] = (uint16_t)u;
+      }
+    }
   }
   /* arrive once this workgroup's atomics and stores are complete */
   aos_mem_wait();
@@ -788,7 +798,225 @@ __global__ void __launch_bounds__(AM_NT) aos_amplan_kernel(aos_amplan_params p) 
     __hip_atomic_store(&p.count[a], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   for (uint32_t e = cst[AM_NT - 1] + tid; e < (uint32_t)p.cb; e += AM_NT) p.ctab[e] = 0u;
+  if (tid == 0 && p.xl) { /* the adapter-major expand's tiles, in order */
+    uint32_t k = 0;
+    for (int t = 0; t < (int)gridDim.y; ++t)
+      if (p.xam_tu > 0 && p.tu[t] >= p.xam_tu) p.xl[k++] = (uint32_t)t;
+    p.xl[gridDim.y] = k;
+  }
   if (tid == 0) aos_reset(p.done);
+}
+
+/* Exclusive scan of a[0, n) (n <= 4 * 256) in place by 256 threads, a[n] = the total. */
+__device__ __forceinline__ void scan256(uint32_t *a, int n, uint32_t *tmp) {
+  const int tid = threadIdx.x;
+  uint32_t v[4], s = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = 4 * tid + k < n ? a[4 * tid + k] : 0u;
+    s += v[k];
+  }
+  tmp[tid] = s;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const uint32_t w = tid >= off ? tmp[tid - off] : 0u;
+    __syncthreads();
+    tmp[tid] += w;
+    __syncthreads();
+  }
+  uint32_t run = tmp[tid] - s;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (4 * tid + k < n) {
+      a[4 * tid + k] = run;
+      run += v[k];
+    }
+  if (tid == 255) a[n] = tmp[255];
+  __syncthreads();
+}
+
+constexpr int XAM_RL = AOS_XAM_RT * BM * 8;            /* users a range holds at most */
+constexpr int XAM_CT = AOS_XAM_RT * 8 + AOS_XAM_MAX_N; /* its chunks at most */
+
+/* Range r of the adapter-major expand's tiles: its users in adapter order (tiles in range order
+ * within an adapter), as (local row << 16) | slot, and its chunks. */
+__global__ void __launch_bounds__(256) aos_amxlist_kernel(aos_amx_params p) {
+  constexpr int RT = AOS_XAM_RT;
+  __shared__ uint32_t off[AOS_XAM_MAX_N * RT + 1], bas[AOS_XAM_MAX_N * RT + 1], tmp[256];
+  __shared__ uint32_t tl[RT];
+  const int tid = threadIdx.x, r = blockIdx.x;
+  const int xc = (int)p.xl[p.mtiles];
+  const int t0 = r * RT, nt = xc - t0 < RT ? xc - t0 : RT;
+  if (nt <= 0) {
+    if (tid == 0) p.nch[r] = 0;
+    return;
+  }
+  if (tid < nt) tl[tid] = p.xl[t0 + tid];
+  __syncthreads();
+  const int ne = p.n * RT; /* entry (a, t): adapter a's users in tile t of the range */
+  for (int e = tid; e < ne; e += 256) {
+    const int a = e / RT, t = e - a * RT;
+    uint32_t c = 0, b = 0;
+    if (t < nt) {
+      const uint32_t tile = tl[t];
+      const uint32_t u = p.inv[(size_t)tile * p.n + a];
+      if (u != 0xffffu) {
+        const uint32_t w = p.tinfo[(size_t)tile * p.tu_cap + u];
+        c = w & 255u;
+        b = w >> 8;
+      }
+    }
+    off[e] = c;
+    bas[e] = b;
+  }
+  __syncthreads();
+  scan256(off, ne, tmp);
+  const uint32_t total = off[ne];
+  uint32_t *rl = p.rl + (size_t)r * XAM_RL;
+  for (uint32_t k = tid; k < total; k += 256) {
+    int lo = 0, hi = ne - 1; /* the last entry starting at or before k */
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= k) lo = mid;
+      else hi = mid - 1;
+    }
+    const int a = lo / RT, t = lo - a * RT;
+    const size_t ui = (size_t)a * p.T + bas[lo] + (k - off[lo]);
+    const uint32_t w = p.users[ui];
+    rl[k] = ((uint32_t)(t * BM) + ((w >> 16) - tl[t] * BM)) << 16 | (w & 0xffffu);
+    p.cidx[ui] = (uint32_t)r * XAM_RL + k;
+  }
+  __syncthreads();
+  for (int a = tid; a < p.n; a += 256) bas[a] = (off[(a + 1) * RT] - off[a * RT] + BM - 1) / BM;
+  __syncthreads();
+  scan256(bas, p.n, tmp);
+  uint32_t *ct = p.ct + (size_t)r * XAM_CT;
+  for (int a = tid; a < p.n; a += 256) {
+    const uint32_t s = off[a * RT], len = off[(a + 1) * RT] - s;
+    for (uint32_t j = 0; j * BM < len; ++j) {
+      const uint32_t nu = len - j * BM < (uint32_t)BM ? len - j * BM : (uint32_t)BM;
+      ct[bas[a] + j] = ((s + j * BM) << 15) | ((uint32_t)a << 8) | nu;
+    }
+  }
+  if (tid == 0) p.nch[r] = bas[p.n];
+}
+
+/* Workgroup (range r, module m, 32-row block r0), r0 fastest: the range's float32 sums for the
+ * block in LDS ([RT * 128 rows][32]); the chunks in order, wave w taking users 32 w .. of each:
+ * A operand the users' SA columns of the chunk's adapter (gathered rows), B operand its B rows
+ * r0 * 32 .. in fragment order, one 32 x 32 product (rank / 16 steps), added to the users' rows
+ * (distinct within a chunk; a barrier between chunks keeps each row's adds in chunk order, which
+ * is adapter order); chunk k + XAM_D's loads are issued after chunk k's products and the users of
+ * chunk k + 2 XAM_D loaded then. Every load is unconditional (ranks below 64 read the zero buffer
+ * for the missing K steps, whose products add zeros; lanes past the chunk's users repeat its last
+ * one and add into a spare LDS row): a load under a branch makes the compiler wait for every load
+ * in flight where the branches join, which took the 4-deep prefetch down to one chunk at a time
+ * (1.57 ms for C5's 8 widest tiles). Last, each tile's 128 x 32 block stored in accumulator order. */
+constexpr int XAM_D = 4;
+__global__ void __launch_bounds__(256, 2) aos_amxexp_kernel(aos_amx_params p) {
+  constexpr int RT = AOS_XAM_RT, MT = BM / 32;
+  extern __shared__ __attribute__((aligned(16))) float accs[]; /* [RT * BM + 1][32]: the last row spare */
+  __shared__ uint32_t tl[RT], ctl[XAM_CT];
+  __shared__ const uint16_t *bps[AOS_XAM_MAX_N];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, c = lane >> 5;
+  const int b = blockIdx.x, r0 = b % p.RB, m = (b / p.RB) & 1, r = b / (2 * p.RB);
+  const int xc = __builtin_amdgcn_readfirstlane((int)p.xl[p.mtiles]);
+  const int t0 = r * RT, nt = xc - t0 < RT ? xc - t0 : RT;
+  if (nt <= 0) return; /* uniform */
+  const int nch = __builtin_amdgcn_readfirstlane((int)p.nch[r]);
+  for (int e = tid; e < (RT * BM + 1) * 32 / 4; e += 256) ((f32x4 *)accs)[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (tid < nt) tl[tid] = p.xl[t0 + tid];
+  for (int a = tid; a < p.n; a += 256) bps[a] = p.Bf[m][a];
+  for (int k = tid; k < nch; k += 256) ctl[k] = p.ct[(size_t)r * XAM_CT + k];
+  __syncthreads();
+  const int rp = p.rpad[m], ks = rp >> 4, roff = m ? p.rpad[0] : 0, cw = p.rpad[0] + p.rpad[1];
+  const uint32_t *rl = p.rl + (size_t)r * XAM_RL;
+  const int j = wave * 32 + i; /* this lane's user of a chunk */
+  struct Stage {
+    u32x4 av[4], bv[4];
+    uint32_t loc[8]; /* LDS rows of the 16 accumulator rows, two per word (the spare row: no user) */
+  };
+  Stage st[XAM_D];
+  uint32_t ent[XAM_D];
+  auto users_of = [&](int k, uint32_t &e) {
+    const uint32_t w = ctl[k < nch ? k : nch - 1];
+    const int nu = (int)(w & 255u), s = (int)(w >> 15);
+    e = rl[s + (j < nu ? j : nu - 1)];
+  };
+  auto issue = [&](int k, uint32_t e, Stage &S) {
+    const uint32_t w = ctl[k < nch ? k : nch - 1];
+    const int nu = k < nch ? (int)(w & 255u) : 0, a = (int)((w >> 8) & 127u);
+    const int s0 = (int)(w >> 15);
+    const uint16_t *sa = p.SAc + ((size_t)r * XAM_RL + s0 + (j < (int)(w & 255u) ? j : (int)(w & 255u) - 1)) * cw + roff + 8 * c;
+    const uint16_t *bb = bps[a];
+    const uint16_t *bo = bb ? bb + ((size_t)r0 * (rp >> 3) + c) * 256 + i * 8 : p.zero;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      S.av[s] = aos_gld16(s < ks ? sa + 16 * s : p.zero);
+      S.bv[s] = aos_gld16(s < ks && bb ? bo + 512 * s : p.zero);
+    }
+    constexpr uint32_t SPARE = RT * BM;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      const int r1 = 8 * (v >> 2) + 4 * c + (v & 3);
+      const uint32_t e0 = aos_shfl(e, r1), e1 = aos_shfl(e, r1 + 1); /* every lane takes part */
+      const uint32_t l0 = wave * 32 + r1 < nu ? e0 >> 16 : SPARE;
+      const uint32_t l1 = wave * 32 + r1 + 1 < nu ? e1 >> 16 : SPARE;
+      S.loc[v >> 1] = l0 | (l1 << 16);
+    }
+  };
+  auto products = [&](const Stage &S) {
+    f32x16 d = f32x16{};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) d = aos_mfma32(S.av[s], S.bv[s], d);
+    return d;
+  };
+  auto add = [&](const f32x16 &d, const Stage &S) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t lr = (S.loc[v >> 1] >> (16 * (v & 1))) & 0xffffu;
+      accs[lr * 32 + i] += d[v];
+    }
+  };
+  if (nch > 0) {
+#pragma unroll
+    for (int d = 0; d < XAM_D; ++d) {
+      uint32_t e0;
+      users_of(d, e0);
+      issue(d, e0, st[d]);
+      users_of(d + XAM_D, ent[d]);
+    }
+    /* every prologue load complete (vmcnt 0; expcnt and lgkmcnt at their maxima): the compiler
+     * otherwise merges the prologue's load order into the loop head's and waits there, every
+     * round, for all but the last two loads in flight */
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    /* whole rounds of XAM_D chunks (a chunk past the last adds into the spare row only); chunk
+     * k + 1's products are formed before the barrier that ends chunk k's adds */
+    f32x16 dd[2];
+    dd[0] = products(st[0]);
+    for (int k0 = 0; k0 < nch; k0 += XAM_D) {
+#pragma unroll
+      for (int d = 0; d < XAM_D; ++d) {
+        add(dd[d & 1], st[d]);
+        dd[(d + 1) & 1] = products(st[(d + 1) % XAM_D]);
+        lds_barrier();
+        issue(k0 + d + XAM_D, ent[d], st[d]);
+        users_of(k0 + d + 2 * XAM_D, ent[d]);
+      }
+    }
+  }
+  lds_barrier();
+  for (int t = 0; t < nt; ++t) {
+    f32x4 *dst = (f32x4 *)p.xd + (((size_t)m * p.mtiles + tl[t]) * p.RB + r0) * MT * 256;
+    for (int w = tid; w < MT * 256; w += 256) {
+      const int mt = w >> 8, q = (w >> 6) & 3, l = w & 63;
+      const int row = t * BM + mt * 32 + 8 * q + 4 * (l >> 5);
+      const float *src = accs + row * 32 + (l & 31);
+      dst[w] = f32x4{src[0], src[32], src[64], src[96]};
+    }
+  }
 }
 
 /* Row r's user of a chunk, staged in LDS for the stores: SA row p, its tile's union size, slot u,
@@ -796,6 +1024,7 @@ __global__ void __launch_bounds__(AM_NT) aos_amplan_kernel(aos_amplan_params p) 
 struct AmUser {
   uint32_t p, tu, u;
   float cf;
+  uint32_t ci; /* row of the compact copy (~0: none) */
 };
 
 __device__ __forceinline__ void am_users(const aos_amshrink_params &p, const uint32_t *ul, int nu, AmUser *meta,
@@ -803,7 +1032,9 @@ __device__ __forceinline__ void am_users(const aos_amshrink_params &p, const uin
   if (tid < nu) {
     const uint32_t w = ul[tid];
     const uint32_t pp = w >> 16, u = w & 0xffffu;
-    meta[tid] = AmUser{pp, (uint32_t)p.tu[pp / BM], u, p.coef[(size_t)pp * p.tu_cap + u]};
+    const uint32_t tu = (uint32_t)p.tu[pp / BM];
+    const bool cp = p.SAc && p.xam_tu > 0 && tu >= (uint32_t)p.xam_tu;
+    meta[tid] = AmUser{pp, tu, u, p.coef[(size_t)pp * p.tu_cap + u], cp ? p.cidx[ul - p.users + tid] : ~0u};
   }
 }
 
@@ -940,7 +1171,9 @@ __global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p
           const int r = s * 32 + 8 * q + 4 * c + e;
           if (r < nu) {
             const AmUser m = meta[r];
-            p.SA[(size_t)m.p * p.s_stride + m.tu * rbefore + m.u * rp + jj] = aos_f32_to_bf16(m.cf * acc[s][4 * q + e]);
+            const uint16_t v = aos_f32_to_bf16(m.cf * acc[s][4 * q + e]);
+            p.SA[(size_t)m.p * p.s_stride + m.tu * rbefore + m.u * rp + jj] = v;
+            if (m.ci != ~0u) p.SAc[(size_t)m.ci * CW + col] = v;
           }
         }
   }
@@ -985,6 +1218,7 @@ __global__ void __launch_bounds__(256) aos_amreduce_kernel(aos_amshrink_params p
     o.x = (uint32_t)aos_f32_to_bf16(m.cf * sum[0]) | ((uint32_t)aos_f32_to_bf16(m.cf * sum[1]) << 16);
     o.y = (uint32_t)aos_f32_to_bf16(m.cf * sum[2]) | ((uint32_t)aos_f32_to_bf16(m.cf * sum[3]) << 16);
     *(u32x2 *)(p.SA + (size_t)m.p * p.s_stride + m.tu * rbefore + m.u * p.rpad[mi] + jj) = o;
+    if (m.ci != ~0u) *(u32x2 *)(p.SAc + (size_t)m.ci * CW + cs * 128 + cg * 4) = o;
   }
 }
 
@@ -1809,6 +2043,7 @@ __global__ void __launch_bounds__(64 * XW, 3) aos_xexp_kernel(aos_xexp_params p)
   gemm_tile_of((int)blockIdx.x - m * mb * nb, mb, nb, mbi, nbk);
   const int TU = __builtin_amdgcn_readfirstlane(g0.tu[mbi]);
   if (TU * p.rmax < p.xe_cols) return; /* uniform: the GEMM expands this tile */
+  if (p.xam_tu > 0 && TU >= p.xam_tu) return; /* the adapter-major expand's tile */
   const aos_gemm_params &q = p.g[m];
   const int rb = nbk * XW + wave;
   const bool live = rb < RB;
@@ -1906,6 +2141,34 @@ extern "C" int aos_launch_amplan(const aos_amplan_params *p, const aos_launch_ct
     if (cols > zb.s_stride) return (int)hipErrorInvalidValue;
   }
   AOS_LAUNCH(ctx, aos_amplan_kernel, dim3(1 + AM_ZB, (p->T + BM - 1) / BM), dim3(AM_NT), 0, *p);
+  return (int)hipGetLastError();
+}
+
+extern "C" int aos_launch_amx(const aos_amx_params *p, const aos_launch_ctx *ctx) {
+  if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->n < 1 || p->n > AOS_XAM_MAX_N || p->tu_cap < p->n ||
+      p->mtiles != (p->T + BM - 1) / BM || p->RB < 1 || !p->tu || !p->tinfo || !p->inv || !p->xl || !p->users ||
+      !p->rl || !p->ct || !p->nch || !p->cidx)
+    return (int)hipErrorInvalidValue;
+  const int ranges = (p->mtiles + AOS_XAM_RT - 1) / AOS_XAM_RT;
+  if (p->list) {
+    AOS_LAUNCH(ctx, aos_amxlist_kernel, dim3(ranges), dim3(256), 0, *p);
+    return (int)hipGetLastError();
+  }
+  for (int m = 0; m < 2; ++m)
+    if (p->rpad[m] < 16 || p->rpad[m] > 64 || p->rpad[m] % 16 || !p->Bf[m]) return (int)hipErrorInvalidValue;
+  if (!p->SAc || !p->cidx || !p->xd || !p->zero) return (int)hipErrorInvalidValue;
+  const size_t lds = (size_t)(AOS_XAM_RT * BM + 1) * 32 * 4;
+  /* dynamic LDS above 64 KiB must be allowed once per device */
+  static uint64_t allowed = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return (int)hipErrorInvalidValue;
+  if (!(allowed >> dev & 1u)) {
+    const hipError_t e = hipFuncSetAttribute((const void *)aos_amxexp_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)lds);
+    if (e != hipSuccess) return (int)e;
+    allowed |= 1ull << dev;
+  }
+  AOS_LAUNCH(ctx, aos_amxexp_kernel, dim3(ranges * 2 * p->RB), dim3(256), lds, *p);
   return (int)hipGetLastError();
 }
 

@@ -423,7 +423,46 @@ typedef struct {
   uint32_t *users;         /* [n][T] */
   int nz;
   aos_am_zero zb[2];
+  /* for the adapter-major expand (NULL / 0: none): per tile the users' range of each union slot
+   * in users[a] ((base << 8) | count, tiles of the lists), the slot of each adapter (0xffff: none;
+   * tiles with tu >= xam_tu, n <= AOS_XAM_MAX_N), and the tiles with tu >= xam_tu in order, their
+   * count in xl[mtiles] */
+  uint32_t *tinfo;         /* [mtiles][tu_cap] */
+  uint16_t *inv;           /* [mtiles][n] */
+  uint32_t *xl;            /* [mtiles + 1] */
+  int xam_tu;
 } aos_amplan_params;
+
+/* Adapter-major gate/up expand of the tiles with tu >= xam_tu (in the order of xl, in ranges of
+ * AOS_XAM_RT tiles; the expand launch skips them): for each range, module m and 32-row block r0,
+ * d[p][o] = sum over the adapters a of p in index order of sum_j SA[p][off_m + u_a rpad_m + j]
+ * B_m,a[o][j], accumulated in LDS and stored into xd in the expand launch's accumulator order.
+ * The list launch (list = 1, grid = ranges) gathers each range's users in adapter order
+ * (rl[k] = (local row << 16) | union slot) and cuts them into chunks of at most 128 of one adapter
+ * (ct[c] = (first entry << 15) | (a << 8) | users, nch[r] chunks); it records each user's entry
+ * cidx[a][k] = r * AOS_XAM_RT * 1024 + entry, where the x shrink writes the user's SA row (gate
+ * then up columns) into SAc, the rows the expand reads. */
+#define AOS_XAM_MAX_N 128
+#define AOS_XAM_RT 4
+#define AOS_XAM_TU 32 /* union size (adapters) from which a tile's gate/up expand runs adapter-major */
+typedef struct {
+  int T, n, tu_cap, mtiles, RB;
+  const int *tu;
+  const uint32_t *tinfo;
+  const uint16_t *inv;
+  const uint32_t *xl;
+  const uint32_t *users;   /* [n][T] */
+  uint32_t *rl;            /* [ranges][AOS_XAM_RT * 128 * 8] */
+  uint32_t *ct;            /* [ranges][AOS_XAM_RT * 8 + AOS_XAM_MAX_N] */
+  uint32_t *nch;           /* [ranges] */
+  uint32_t *cidx;          /* [n][T] */
+  const uint16_t *SAc;     /* [ranges][AOS_XAM_RT * 1024][rpad[0] + rpad[1]] */
+  int rpad[2];             /* gate, up: multiples of 16 up to 64 */
+  const uint16_t *const *Bf[2];
+  const uint16_t *zero;    /* >= 64 zero elements */
+  float *xd;
+  int list;
+} aos_amx_params;
 
 typedef struct {
   const uint16_t *x;       /* [T][in] */
@@ -440,6 +479,11 @@ typedef struct {
   float *part;             /* [ks][cb][csets][128][128] float32 when ks > 1 */
   const uint16_t *zero_row;
   int reduce;
+  /* users of tiles with tu >= xam_tu (the adapter-major expand's) also go to the compact copy:
+   * SAc[cidx[a][k]][col], col over the adapter's columns (NULL: none) */
+  const uint32_t *cidx;    /* [n][T], parallel to users */
+  uint16_t *SAc;
+  int xam_tu;
 } aos_amshrink_params;
 
 /* int4 GEMM with the LoRA expand over the tile union: y[p][o] = sum_k x[p][k] w[o][k] +
@@ -499,6 +543,7 @@ typedef struct {
   aos_gemm_params g[2];
   float *xd;
   int xe_cols, rmax;
+  int xam_tu;              /* > 0: tiles with tu >= xam_tu are the adapter-major expand's */
 } aos_xexp_params;
 
 /* Where a launch goes: its stream and, when profiling, the HIP events the dispatch itself
@@ -616,6 +661,7 @@ int aos_launch_gplan(const aos_gplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_tshrink(const aos_tshrink_params *p, const aos_launch_ctx *ctx);
 int aos_launch_amplan(const aos_amplan_params *p, const aos_launch_ctx *ctx);
 int aos_launch_amshrink(const aos_amshrink_params *p, const aos_launch_ctx *ctx);
+int aos_launch_amx(const aos_amx_params *p, const aos_launch_ctx *ctx);
 int aos_launch_gemm(const aos_gemm_params *p, int swiglu, const aos_launch_ctx *ctx);
 int aos_launch_xexp(const aos_xexp_params *p, const aos_launch_ctx *ctx);
 int aos_gemm_shrink_fits(int T, int RB, int s_cols, int swiglu);

@@ -269,7 +269,7 @@ def test_mlp_prefill_adapter_major(hip, cid, T, mixed):
     for tu in (0, 1, mixed):
         layer.set_prefill_adapter_major(tu)
         y = _run_mlp(hip, layer, xb, rings)
-        assert layer.last_adapter_major() == (3 if tu else 0), f"tu={tu}: adapter-major state"
+        assert layer.last_adapter_major() & 3 == (3 if tu else 0), f"tu={tu}: adapter-major state"
         assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), f"tu={tu}: run-to-run outputs differ"
         out[tu] = W.bf16_bits_to_f32(y).reshape(T, -1)
     layer.set_prefill_adapter_major(-1)
@@ -281,6 +281,47 @@ def test_mlp_prefill_adapter_major(hip, cid, T, mixed):
         assert ratio <= REL_TOL, f"tu={tu}: max tolerance ratio {ratio:.4g}"
     assert tol_ratio(out[1], out[0]) <= REL_TOL / 2
     assert tol_ratio(out[mixed], out[0]) <= REL_TOL / 2
+
+
+@pytest.mark.parametrize("cid,T,xe_cols,am_tu,forms",
+                         [(5, 1024, -1, -1, (0, 8, 50)), (5, 1100, -1, -1, (0, 8, 50)), (3, 2048, 64, 1, (0, 4, 6)),
+                          (1, 300, 32, 1, (0, 2, 3))])
+def test_mlp_prefill_expand_adapter_major(hip, cid, T, xe_cols, am_tu, forms):
+    """The gate/up LoRA expand adapter-major (each adapter's users gathered into MFMA tiles against
+    its B rows, the sums of a range of 4 tiles added in LDS in adapter order) for no tile, every
+    expand-launch tile, and the tiles whose union holds at least forms[2] adapters, the others
+    expanded over their unions in the same call (a tile expands adapter-major only if it is an
+    expand-launch tile: union columns of the wider module >= the launch's width): on the 32B-shaped stress layer (64 rank-64
+    adapters, K = 8, adversarial routing; 1024 tokens, and 1100 with a ragged last tile), the
+    7B-shaped layer (rank 16) and the 0.5B-shaped one (rank 8 padded to 16), the last two with the
+    expand launch from 64 and 32 union columns. Each form is bit-identical run to run and within
+    tolerance of the oracle on every tile; the forms agree up to float32 summation order."""
+    cfg = W.CONFIGS[cid]
+    xb, xf = W.activations(cfg, T)
+    rings, _ = rings_for(cid, T)
+    layer, ads = gpu_layer(hip, cid)
+    layer.set_prefill_shrink(False)
+    layer.set_prefill_expand(xe_cols)
+    layer.set_prefill_adapter_major(am_tu)
+    out = {}
+    for tu in forms:
+        layer.set_prefill_expand_adapter_major(tu)
+        y = _run_mlp(hip, layer, xb, rings)
+        assert layer.last_expand() == 1, f"tu={tu}: expand launch state"
+        assert layer.last_adapter_major() == (7 if tu else 3), f"tu={tu}: adapter-major state"
+        assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), f"tu={tu}: run-to-run outputs differ"
+        out[tu] = W.bf16_bits_to_f32(y).reshape(T, -1)
+    layer.set_prefill_expand_adapter_major(-1)
+    layer.set_prefill_adapter_major(-1)
+    layer.set_prefill_expand(-1)
+    perm = layer.last_perm()
+    sample = np.union1d(tile_sample(perm, T), [0, 1, T - 2, T - 1])
+    ref = oracle_mlp(cid, xf[sample], rings[sample])
+    for tu, y in out.items():
+        ratio = assert_parity(f"config {cid} prefill T={T} expand adapter-major from {tu}", y[sample], ref)
+        assert ratio <= REL_TOL, f"tu={tu}: max tolerance ratio {ratio:.4g}"
+    assert tol_ratio(out[forms[1]], out[0]) <= REL_TOL / 2
+    assert tol_ratio(out[forms[2]], out[0]) <= REL_TOL / 2
 
 
 @pytest.mark.parametrize("cid,T", [(1, 300), (3, 2048)])
