@@ -1998,7 +1998,7 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
   const int xt = l->prefill_xam_tu;
   if (M.use_xe && M.use_am_x && n <= AOS_XAM_MAX_N && xt > 0 && xt >= l->prefill_am_tu &&
       xt * rxe >= l->prefill_xe_cols && M.P.tu_cap >= xt && M.g1.rpad0 >= 16 && M.g1.rpad0 <= 64 &&
-      M.g1.rpad1 >= 16 && M.g1.rpad1 <= 64) {
+      M.g1.rpad1 == M.g1.rpad0) {
     aos_amplan_params &A = M.amp;
     A.tinfo = cv.b.take<uint32_t>((size_t)M.P.mtiles * M.P.tu_cap);
     A.inv = cv.b.take<uint16_t>((size_t)M.P.mtiles * n);
@@ -2017,8 +2017,8 @@ static void plan_mlp_prefill(aoship_layer *l, int T, const uint16_t *x, const ao
     Q.xl = A.xl;
     Q.users = A.users;
     const int ranges = ceil_div(M.P.mtiles, AOS_XAM_RT);
-    Q.rl = cv.b.take<uint32_t>((size_t)ranges * AOS_XAM_RT * AOS_GEMM_BM * 8);
-    Q.ct = cv.b.take<uint32_t>((size_t)ranges * (AOS_XAM_RT * 8 + AOS_XAM_MAX_N));
+    Q.rlp = cv.b.take<uint16_t>((size_t)ranges * AOS_XAM_CT * AOS_GEMM_BM);
+    Q.ct = cv.b.take<uint32_t>((size_t)ranges * AOS_XAM_CT);
     Q.nch = cv.b.take<uint32_t>((size_t)ranges);
     Q.cidx = cv.b.take<uint32_t>((size_t)n * T);
     Q.SAc = cv.b.take<uint16_t>((size_t)ranges * AOS_XAM_RT * AOS_GEMM_BM * 8 * (M.g1.rpad0 + M.g1.rpad1));

@@ -835,14 +835,17 @@ __device__ __forceinline__ void scan256(uint32_t *a, int n, uint32_t *tmp) {
   __syncthreads();
 }
 
-constexpr int XAM_RL = AOS_XAM_RT * BM * 8;            /* users a range holds at most */
-constexpr int XAM_CT = AOS_XAM_RT * 8 + AOS_XAM_MAX_N; /* its chunks at most */
+constexpr int XAM_RL = AOS_XAM_RT * BM * 8; /* users a range holds at most */
+constexpr int XAM_CT = AOS_XAM_CT;
+constexpr uint16_t XAM_SPARE = AOS_XAM_RT * BM; /* the spare LDS row */
 
 /* Range r of the adapter-major expand's tiles: its users in adapter order (tiles in range order
- * within an adapter), as (local row << 16) | slot, and its chunks. */
+ * within an adapter), their entries in the compact copy, the chunks, and each chunk's local rows
+ * padded to 128 with the spare row (one all-spare chunk after the last). */
 __global__ void __launch_bounds__(256) aos_amxlist_kernel(aos_amx_params p) {
   constexpr int RT = AOS_XAM_RT;
-  __shared__ uint32_t off[AOS_XAM_MAX_N * RT + 1], bas[AOS_XAM_MAX_N * RT + 1], tmp[256];
+  __shared__ uint32_t off[AOS_XAM_MAX_N * RT + 1], bas[AOS_XAM_MAX_N * RT + 1], tmp[256], ctl[XAM_CT];
+  __shared__ uint16_t lrow[XAM_RL];
   __shared__ uint32_t tl[RT];
   const int tid = threadIdx.x, r = blockIdx.x;
   const int xc = (int)p.xl[p.mtiles];
@@ -872,7 +875,6 @@ __global__ void __launch_bounds__(256) aos_amxlist_kernel(aos_amx_params p) {
   __syncthreads();
   scan256(off, ne, tmp);
   const uint32_t total = off[ne];
-  uint32_t *rl = p.rl + (size_t)r * XAM_RL;
   for (uint32_t k = tid; k < total; k += 256) {
     int lo = 0, hi = ne - 1; /* the last entry starting at or before k */
     while (lo < hi) {
@@ -882,40 +884,56 @@ __global__ void __launch_bounds__(256) aos_amxlist_kernel(aos_amx_params p) {
     }
     const int a = lo / RT, t = lo - a * RT;
     const size_t ui = (size_t)a * p.T + bas[lo] + (k - off[lo]);
-    const uint32_t w = p.users[ui];
-    rl[k] = ((uint32_t)(t * BM) + ((w >> 16) - tl[t] * BM)) << 16 | (w & 0xffffu);
+    lrow[k] = (uint16_t)(t * BM + ((p.users[ui] >> 16) - tl[t] * BM));
     p.cidx[ui] = (uint32_t)r * XAM_RL + k;
   }
   __syncthreads();
   for (int a = tid; a < p.n; a += 256) bas[a] = (off[(a + 1) * RT] - off[a * RT] + BM - 1) / BM;
   __syncthreads();
   scan256(bas, p.n, tmp);
+  const int nch = (int)bas[p.n];
   uint32_t *ct = p.ct + (size_t)r * XAM_CT;
   for (int a = tid; a < p.n; a += 256) {
     const uint32_t s = off[a * RT], len = off[(a + 1) * RT] - s;
     for (uint32_t j = 0; j * BM < len; ++j) {
       const uint32_t nu = len - j * BM < (uint32_t)BM ? len - j * BM : (uint32_t)BM;
-      ct[bas[a] + j] = ((s + j * BM) << 15) | ((uint32_t)a << 8) | nu;
+      const uint32_t w = ((s + j * BM) << 15) | ((uint32_t)a << 8) | nu;
+      ctl[bas[a] + j] = w;
+      ct[bas[a] + j] = w;
     }
   }
-  if (tid == 0) p.nch[r] = bas[p.n];
+  if (tid == 0) {
+    ctl[nch] = 0u;
+    ct[nch] = 0u;
+    p.nch[r] = (uint32_t)nch;
+  }
+  __syncthreads();
+  uint16_t *rlp = p.rlp + (size_t)r * XAM_CT * BM;
+  for (int e = tid; e < (nch + 1) * BM; e += 256) {
+    const uint32_t w = ctl[e >> 7];
+    const uint32_t slot = (uint32_t)e & 127u;
+    rlp[e] = slot < (w & 255u) ? lrow[(w >> 15) + slot] : XAM_SPARE;
+  }
 }
 
 /* Workgroup (range r, module m, 32-row block r0), r0 fastest: the range's float32 sums for the
- * block in LDS ([RT * 128 rows][32]); the chunks in order, wave w taking users 32 w .. of each:
- * A operand the users' SA columns of the chunk's adapter (gathered rows), B operand its B rows
- * r0 * 32 .. in fragment order, one 32 x 32 product (rank / 16 steps), added to the users' rows
- * (distinct within a chunk; a barrier between chunks keeps each row's adds in chunk order, which
- * is adapter order); chunk k + XAM_D's loads are issued after chunk k's products and the users of
- * chunk k + 2 XAM_D loaded then. Every load is unconditional (ranks below 64 read the zero buffer
- * for the missing K steps, whose products add zeros; lanes past the chunk's users repeat its last
- * one and add into a spare LDS row): a load under a branch makes the compiler wait for every load
- * in flight where the branches join, which took the 4-deep prefetch down to one chunk at a time
- * (1.57 ms for C5's 8 widest tiles). Last, each tile's 128 x 32 block stored in accumulator order. */
+ * block in LDS ([RT * 128 rows + 1 spare][32]); the chunks in order, wave w taking users 32 w .. of
+ * each: A operand the users' rows of the compact SA copy, B operand the adapter's B rows r0 * 32 ..
+ * in fragment order, one 32 x 32 product (KS = rank / 16 steps), added to the users' rows (distinct
+ * within a chunk; a barrier between chunks keeps each row's adds in chunk order, which is adapter
+ * order); slots past a chunk's users add into the spare row. Chunk k + XAM_D's loads are issued
+ * after chunk k's adds; chunk k + 1's products are formed before the barrier that ends them. The
+ * loads are buffer loads whose per-lane offsets never change (the chunk moves the base; an adapter
+ * without the module reads through a zero-size range: zeros), all unconditional: a load under a
+ * branch makes the compiler wait for every load in flight where the branches join, which took the
+ * 4-deep prefetch down to one chunk at a time (1.57 ms for C5's 8 widest tiles). LDS float atomic
+ * adds instead of the read-add-writes: 6x slower. Last, each tile's 128 x 32 block stored in
+ * accumulator order. */
 constexpr int XAM_D = 4;
+template <int KS>
 __global__ void __launch_bounds__(256, 2) aos_amxexp_kernel(aos_amx_params p) {
-  constexpr int RT = AOS_XAM_RT, MT = BM / 32;
-  extern __shared__ __attribute__((aligned(16))) float accs[]; /* [RT * BM + 1][32]: the last row spare */
+  constexpr int RT = AOS_XAM_RT, MT = BM / 32, RP = 16 * KS, CW = 2 * RP;
+  extern __shared__ __attribute__((aligned(16))) float accs[]; /* [RT * BM + 1][32] */
   __shared__ uint32_t tl[RT], ctl[XAM_CT];
   __shared__ const uint16_t *bps[AOS_XAM_MAX_N];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -929,81 +947,71 @@ __global__ void __launch_bounds__(256, 2) aos_amxexp_kernel(aos_amx_params p) {
   for (int e = tid; e < (RT * BM + 1) * 32 / 4; e += 256) ((f32x4 *)accs)[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   if (tid < nt) tl[tid] = p.xl[t0 + tid];
   for (int a = tid; a < p.n; a += 256) bps[a] = p.Bf[m][a];
-  for (int k = tid; k < nch; k += 256) ctl[k] = p.ct[(size_t)r * XAM_CT + k];
+  for (int k = tid; k <= nch; k += 256) ctl[k] = p.ct[(size_t)r * XAM_CT + k];
   __syncthreads();
-  const int rp = p.rpad[m], ks = rp >> 4, roff = m ? p.rpad[0] : 0, cw = p.rpad[0] + p.rpad[1];
-  const uint32_t *rl = p.rl + (size_t)r * XAM_RL;
-  const int j = wave * 32 + i; /* this lane's user of a chunk */
+  const uint32_t bbytes = (uint32_t)p.RB * 32 * RP * 2;
+  /* per-lane byte offsets: user 32 wave + i's row of the chunk, K piece 8 c; B row r0 * 32 + i */
+  const int va = ((wave * 32 + i) * CW + (m ? RP : 0) + 8 * c) * 2;
+  const int vb = ((r0 * (RP / 8) + c) * 256 + i * 8) * 2;
+  const uint16_t *rlp = p.rlp + (size_t)r * XAM_CT * BM + wave * 32 + 4 * c;
   struct Stage {
-    u32x4 av[4], bv[4];
-    uint32_t loc[8]; /* LDS rows of the 16 accumulator rows, two per word (the spare row: no user) */
+    u32x4 av[KS], bv[KS];
+    u32x2 lo[4]; /* LDS rows of the 16 accumulator rows 8 q + 4 c + e, e = 0..3 in lo[q] */
   };
   Stage st[XAM_D];
-  uint32_t ent[XAM_D];
-  auto users_of = [&](int k, uint32_t &e) {
-    const uint32_t w = ctl[k < nch ? k : nch - 1];
-    const int nu = (int)(w & 255u), s = (int)(w >> 15);
-    e = rl[s + (j < nu ? j : nu - 1)];
-  };
-  auto issue = [&](int k, uint32_t e, Stage &S) {
-    const uint32_t w = ctl[k < nch ? k : nch - 1];
-    const int nu = k < nch ? (int)(w & 255u) : 0, a = (int)((w >> 8) & 127u);
-    const int s0 = (int)(w >> 15);
-    const uint16_t *sa = p.SAc + ((size_t)r * XAM_RL + s0 + (j < (int)(w & 255u) ? j : (int)(w & 255u) - 1)) * cw + roff + 8 * c;
+  auto issue = [&](int k, Stage &S) {
+    const int kk = k < nch ? k : nch; /* past the last: the all-spare chunk */
+    const uint32_t w = ctl[kk];
+    const uint32_t s0 = (uint32_t)r * XAM_RL + (w >> 15), a = (w >> 8) & 127u;
+    /* the chunk's own rows only: lanes past its users read zeros without a memory access */
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)(p.SAc + (size_t)s0 * CW), (short)0,
+                                                                        (int)((w & 255u) * CW * 2), 0x00020000);
     const uint16_t *bb = bps[a];
-    const uint16_t *bo = bb ? bb + ((size_t)r0 * (rp >> 3) + c) * 256 + i * 8 : p.zero;
+    /* a wave without users in the chunk (or an adapter without the module) reads zeros */
+    const bool wb = bb && (uint32_t)(wave * 32) < (w & 255u);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)bb, (short)0, wb ? (int)bbytes : 0, 0x00020000);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      S.av[s] = aos_gld16(s < ks ? sa + 16 * s : p.zero);
-      S.bv[s] = aos_gld16(s < ks && bb ? bo + 512 * s : p.zero);
+    for (int s = 0; s < KS; ++s) {
+      S.av[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, va + 32 * s, 0, 0));
+      S.bv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, vb + 1024 * s, 0, 0));
     }
-    constexpr uint32_t SPARE = RT * BM;
+    const uint16_t *lr = rlp + (size_t)kk * BM;
 #pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      const int r1 = 8 * (v >> 2) + 4 * c + (v & 3);
-      const uint32_t e0 = aos_shfl(e, r1), e1 = aos_shfl(e, r1 + 1); /* every lane takes part */
-      const uint32_t l0 = wave * 32 + r1 < nu ? e0 >> 16 : SPARE;
-      const uint32_t l1 = wave * 32 + r1 + 1 < nu ? e1 >> 16 : SPARE;
-      S.loc[v >> 1] = l0 | (l1 << 16);
-    }
+    for (int q = 0; q < 4; ++q) S.lo[q] = *(const __attribute__((address_space(1))) u32x2 *)(lr + 8 * q);
   };
   auto products = [&](const Stage &S) {
     f32x16 d = f32x16{};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) d = aos_mfma32(S.av[s], S.bv[s], d);
+    for (int s = 0; s < KS; ++s) d = aos_mfma32(S.av[s], S.bv[s], d);
     return d;
   };
   auto add = [&](const f32x16 &d, const Stage &S) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const uint32_t lr = (S.loc[v >> 1] >> (16 * (v & 1))) & 0xffffu;
-      accs[lr * 32 + i] += d[v];
-    }
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wd = e < 2 ? S.lo[q].x : S.lo[q].y;
+        const uint32_t lr = (wd >> (16 * (e & 1))) & 0xffffu;
+        accs[lr * 32 + i] += d[4 * q + e];
+      }
   };
   if (nch > 0) {
 #pragma unroll
-    for (int d = 0; d < XAM_D; ++d) {
-      uint32_t e0;
-      users_of(d, e0);
-      issue(d, e0, st[d]);
-      users_of(d + XAM_D, ent[d]);
-    }
+    for (int d = 0; d < XAM_D; ++d) issue(d, st[d]);
     /* every prologue load complete (vmcnt 0; expcnt and lgkmcnt at their maxima): the compiler
      * otherwise merges the prologue's load order into the loop head's and waits there, every
-     * round, for all but the last two loads in flight */
+     * round, for all but the last few loads in flight */
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    /* whole rounds of XAM_D chunks (a chunk past the last adds into the spare row only); chunk
-     * k + 1's products are formed before the barrier that ends chunk k's adds */
     f32x16 dd[2];
     dd[0] = products(st[0]);
-    for (int k0 = 0; k0 < nch; k0 += XAM_D) {
+    for (int k0 = 0; k0 < nch; k0 += XAM_D) { /* whole rounds: chunks past the last add into the spare row */
 #pragma unroll
       for (int d = 0; d < XAM_D; ++d) {
         add(dd[d & 1], st[d]);
         dd[(d + 1) & 1] = products(st[(d + 1) % XAM_D]);
         lds_barrier();
-        issue(k0 + d + XAM_D, ent[d], st[d]);
-        users_of(k0 + d + 2 * XAM_D, ent[d]);
+        issue(k0 + d + XAM_D, st[d]);
       }
     }
   }
@@ -2147,28 +2155,34 @@ extern "C" int aos_launch_amplan(const aos_amplan_params *p, const aos_launch_ct
 extern "C" int aos_launch_amx(const aos_amx_params *p, const aos_launch_ctx *ctx) {
   if (p->T < 1 || p->T > AOS_PREFILL_MAX_T || p->n < 1 || p->n > AOS_XAM_MAX_N || p->tu_cap < p->n ||
       p->mtiles != (p->T + BM - 1) / BM || p->RB < 1 || !p->tu || !p->tinfo || !p->inv || !p->xl || !p->users ||
-      !p->rl || !p->ct || !p->nch || !p->cidx)
+      !p->rlp || !p->ct || !p->nch || !p->cidx)
     return (int)hipErrorInvalidValue;
   const int ranges = (p->mtiles + AOS_XAM_RT - 1) / AOS_XAM_RT;
   if (p->list) {
     AOS_LAUNCH(ctx, aos_amxlist_kernel, dim3(ranges), dim3(256), 0, *p);
     return (int)hipGetLastError();
   }
-  for (int m = 0; m < 2; ++m)
-    if (p->rpad[m] < 16 || p->rpad[m] > 64 || p->rpad[m] % 16 || !p->Bf[m]) return (int)hipErrorInvalidValue;
-  if (!p->SAc || !p->cidx || !p->xd || !p->zero) return (int)hipErrorInvalidValue;
+  const int rp = p->rpad[0];
+  if (rp < 16 || rp > 64 || rp % 16 || p->rpad[1] != rp || !p->Bf[0] || !p->Bf[1] || !p->SAc || !p->xd)
+    return (int)hipErrorInvalidValue;
   const size_t lds = (size_t)(AOS_XAM_RT * BM + 1) * 32 * 4;
-  /* dynamic LDS above 64 KiB must be allowed once per device */
-  static uint64_t allowed = 0;
+  const void *fn[4] = {(const void *)aos_amxexp_kernel<1>, (const void *)aos_amxexp_kernel<2>,
+                       (const void *)aos_amxexp_kernel<3>, (const void *)aos_amxexp_kernel<4>};
+  /* dynamic LDS above 64 KiB must be allowed once per device and kernel */
+  static uint64_t allowed[4] = {0, 0, 0, 0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return (int)hipErrorInvalidValue;
-  if (!(allowed >> dev & 1u)) {
-    const hipError_t e = hipFuncSetAttribute((const void *)aos_amxexp_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)lds);
+  const int ks = rp / 16;
+  if (!(allowed[ks - 1] >> dev & 1u)) {
+    const hipError_t e = hipFuncSetAttribute(fn[ks - 1], hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
-    allowed |= 1ull << dev;
+    allowed[ks - 1] |= 1ull << dev;
   }
-  AOS_LAUNCH(ctx, aos_amxexp_kernel, dim3(ranges * 2 * p->RB), dim3(256), lds, *p);
+  const dim3 grid(ranges * 2 * p->RB), block(256);
+  if (ks == 1) AOS_LAUNCH(ctx, aos_amxexp_kernel<1>, grid, block, lds, *p);
+  else if (ks == 2) AOS_LAUNCH(ctx, aos_amxexp_kernel<2>, grid, block, lds, *p);
+  else if (ks == 3) AOS_LAUNCH(ctx, aos_amxexp_kernel<3>, grid, block, lds, *p);
+  else AOS_LAUNCH(ctx, aos_amxexp_kernel<4>, grid, block, lds, *p);
   return (int)hipGetLastError();
 }
 

@@ -437,14 +437,15 @@ typedef struct {
  * AOS_XAM_RT tiles; the expand launch skips them): for each range, module m and 32-row block r0,
  * d[p][o] = sum over the adapters a of p in index order of sum_j SA[p][off_m + u_a rpad_m + j]
  * B_m,a[o][j], accumulated in LDS and stored into xd in the expand launch's accumulator order.
- * The list launch (list = 1, grid = ranges) gathers each range's users in adapter order
- * (rl[k] = (local row << 16) | union slot) and cuts them into chunks of at most 128 of one adapter
- * (ct[c] = (first entry << 15) | (a << 8) | users, nch[r] chunks); it records each user's entry
+ * The list launch (list = 1, grid = ranges) gathers each range's users in adapter order and cuts
+ * them into chunks of at most 128 of one adapter (ct[c] = (first entry << 15) | (a << 8) | users,
+ * nch[r] chunks, ct[nch] = 0), each chunk's local rows in rlp; it records each user's entry
  * cidx[a][k] = r * AOS_XAM_RT * 1024 + entry, where the x shrink writes the user's SA row (gate
  * then up columns) into SAc, the rows the expand reads. */
 #define AOS_XAM_MAX_N 128
 #define AOS_XAM_RT 4
 #define AOS_XAM_TU 32 /* union size (adapters) from which a tile's gate/up expand runs adapter-major */
+#define AOS_XAM_CT (AOS_XAM_RT * 8 + AOS_XAM_MAX_N + 4) /* chunks of a range at most, and the spare one */
 typedef struct {
   int T, n, tu_cap, mtiles, RB;
   const int *tu;
@@ -452,12 +453,13 @@ typedef struct {
   const uint16_t *inv;
   const uint32_t *xl;
   const uint32_t *users;   /* [n][T] */
-  uint32_t *rl;            /* [ranges][AOS_XAM_RT * 128 * 8] */
-  uint32_t *ct;            /* [ranges][AOS_XAM_RT * 8 + AOS_XAM_MAX_N] */
+  uint16_t *rlp;           /* [ranges][AOS_XAM_CT][128]: each chunk's users' local rows, the spare row
+                              (AOS_XAM_RT * 128) past them and in the chunk after the last */
+  uint32_t *ct;            /* [ranges][AOS_XAM_CT] */
   uint32_t *nch;           /* [ranges] */
   uint32_t *cidx;          /* [n][T] */
   const uint16_t *SAc;     /* [ranges][AOS_XAM_RT * 1024][rpad[0] + rpad[1]] */
-  int rpad[2];             /* gate, up: multiples of 16 up to 64 */
+  int rpad[2];             /* gate and up, equal: a multiple of 16 up to 64 */
   const uint16_t *const *Bf[2];
   const uint16_t *zero;    /* >= 64 zero elements */
   float *xd;
