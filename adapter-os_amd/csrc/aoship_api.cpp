@@ -1828,10 +1828,13 @@ static void plan_sk(aoship_layer *l, Carve &cv, aos_gemm_params &g, bool swiglu)
   const int slots = aos_gemm_sk_slots(swiglu ? 1 : 0) & ~7; /* one share per XCD */
   if (slots <= 0) return;
   const int mb = (g.T + AOS_GEMM_BM - 1) / AOS_GEMM_BM;
-  /* with a multiple of 8 token tiles the plain grid gives each XCD its own tiles (interleaved),
-   * which balances tiles whose adapter unions differ in size; stream-K's equal shares of K groups
-   * do not (a tile's expand steps fall to whichever workgroup ends its tasks) */
-  if (mb % 8 == 0) return;
+  /* with a multiple of 8 token tiles the SwiGLU GEMM's plain grid gives each XCD its own tiles
+   * (interleaved), which balances tiles whose adapter unions differ in size; stream-K's equal shares
+   * of K groups do not (a tile's expand steps fall to whichever workgroup ends its tasks). The down
+   * GEMM's expand is a small part of its K (rank-64 unions of up to 64 adapters against 27648
+   * weight columns on the 32B-shaped layer), and there stream-K wins back its last plain round:
+   * 1.575 -> 1.434 ms at 4096 tokens */
+  if (mb % 8 == 0 && swiglu) return;
   const uint64_t tasks = (uint64_t)mb * ((g.w0.RB + wv - 1) / wv);
   const uint64_t last = tasks % (uint64_t)slots; /* workgroups of the plain grid's last round */
   if (last == 0 || last * 10 >= (uint64_t)slots * 9) return;
