@@ -577,3 +577,58 @@ def test_mlp_rank_not_multiple_of_16_and_missing_modules(hip, T):
                              rings)
     ratio = assert_parity(f"test_mlp_rank_not_multiple_of_16_and_missing_modules T={T}", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
     assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
+
+
+@pytest.mark.parametrize("case", ["rank40_missing_modules", "160_adapters"])
+def test_mlp_prefill_adapter_major_edges(hip, case):
+    """The adapter-major prefill paths at their edges, against the oracle and bit-identical run to
+    run: rank-40 adapters (rows padded to 48: three MFMA steps per chunk) some of which have no
+    up_proj or no down_proj (their A rows read as zeros in the shrink, their B through an empty
+    range in the expand), every tile adapter-major in the shrinks and the gate/up expand; and 160
+    adapters (K = 2 of random sets at 300 tokens), more than the adapter-major expand takes, so the
+    shrinks run adapter-major and the expand over the tile unions."""
+    import dataclasses
+
+    import oracle
+
+    if case == "rank40_missing_modules":
+        cfg = dataclasses.replace(W.CONFIGS[1], rank=40, n_adapters=6)
+        missing = {1: "up_proj", 4: "up_proj", 2: "down_proj"}
+        T = 200
+    else:
+        cfg = dataclasses.replace(W.CONFIGS[1], n_adapters=160)
+        missing = {}
+        T = 300
+    lora = [{m: W.lora_weights(cfg, a, m) for m in cfg.modules if missing.get(a) != m} for a in range(cfg.n_adapters)]
+    base = {m: W.base_weights(cfg, m) for m in cfg.modules}
+    layer = hip.Layer(0)
+    for m, (p, s, b) in base.items():
+        layer.set_base(m, p, s, b)
+    ads = []
+    for a, mods in enumerate(lora):
+        ad = hip.LoraAdapter(a, 1, W.lora_scale(cfg))
+        for m, (A, B) in mods.items():
+            ad.set_module(0, m, A, B)
+        ads.append(ad)
+    layer.set_adapters(ads)
+    layer.set_prefill_shrink(False)
+    if case == "rank40_missing_modules":
+        layer.set_prefill_expand(48)
+        layer.set_prefill_adapter_major(1)
+        layer.set_prefill_expand_adapter_major(1)
+        want = 7
+    else:
+        want = 3
+    f, w = W.router_inputs(cfg, T)
+    rings = oracle.route_batch(oracle.priors(f, w), cfg.k, cfg.tau, cfg.eps, 1.0,
+                               np.arange(cfg.n_adapters, dtype=np.uint64))
+    xb, xf = W.activations(cfg, T)
+    y = _run_mlp(hip, layer, xb, rings)
+    assert layer.last_expand() == 1, "expand launch state"
+    assert layer.last_adapter_major() == want, "adapter-major state"
+    assert np.array_equal(y, _run_mlp(hip, layer, xb, rings)), "run-to-run outputs differ"
+    scales = np.full(cfg.n_adapters, W.lora_scale(cfg), np.float32)
+    ref = oracle.mlp_forward(xf, base["gate_proj"], base["up_proj"], base["down_proj"], lora, scales, cfg.rank,
+                             rings)
+    ratio = assert_parity(f"test_mlp_prefill_adapter_major_edges {case} T={T}", W.bf16_bits_to_f32(y).reshape(ref.shape), ref)
+    assert ratio <= REL_TOL, f"max tolerance ratio {ratio:.4g}"
