@@ -1872,7 +1872,8 @@ static void plan_amshrink(Carve &cv, const PrefillPlan &P, const aos_tshrink_par
   q.s_stride = sp.s_stride;
   q.zero_row = sp.zero_row;
   q.cb = A.cb;
-  q.csets = ceil_div(cw, 128);
+  q.setw = cw <= 64 ? 64 : 128; /* 2-wave workgroups for adapters of 64 columns or fewer */
+  q.csets = ceil_div(cw, q.setw);
   const int G = sp.in / 64;
   int ks = ceil_div(1024, q.cb * q.csets);
   if (ks > 16) ks = 16;

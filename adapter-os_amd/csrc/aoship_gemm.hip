@@ -1058,14 +1058,16 @@ __device__ __forceinline__ void am_module(const aos_amshrink_params &p, int col,
   j = col - rbefore;
 }
 
-/* Workgroup (K slice kz, chunk c, column set cs of 128 adapter columns), kz fastest; wave w takes
- * the 32 columns cs * 128 + 32 w .., all the chunk's users (four 32-row sub-tiles): the tile
- * shrink's K loop over the users' gathered rows. Waves without columns (an adapter of fewer than
- * 128 columns) only stage rows. (Two waves per 32-column block, each on half the rows, so that
- * every SIMD has matrix work at 64 columns, was slower: 343 against 275 us for the rank-64 down
- * shrink at 4096 tokens; both load the block's A rows, and the kernel is bound by its loads.) */
-__global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p) {
-  constexpr int MT = BM / 32, TILE = BM * 128;
+/* Workgroup of NW waves (K slice kz, chunk c, column set cs of 32 NW adapter columns), kz fastest;
+ * wave w takes the 32 columns cs * 32 NW + 32 w .., all the chunk's users (four 32-row sub-tiles):
+ * the tile shrink's K loop over the users' gathered rows, staged by all 64 NW threads. Waves
+ * without columns only stage rows. Adapters of 64 columns or fewer run 2-wave workgroups, four
+ * per CU, so that every wave has matrix work and twice the chunks per CU have loads in flight.
+ * (Two waves per 32-column block, each on half the rows, was slower: 343 against 275 us for the
+ * rank-64 down shrink at 4096 tokens; both load the block's A rows.) */
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) aos_amshrink_kernel(aos_amshrink_params p) {
+  constexpr int MT = BM / 32, TILE = BM * 128, NT = 64 * NW;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1081,8 +1083,8 @@ __global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p
   const int G = p.in / 64;
   const int g_lo = (int)((long)kz * G / p.ks), g_hi = (int)((long)(kz + 1) * G / p.ks);
 
-  const int col = cs * 128 + 32 * wave + i;
-  const bool wact = cs * 128 + 32 * wave < CW; /* wave-uniform: the wave has columns */
+  const int col = cs * 32 * NW + 32 * wave + i;
+  const bool wact = cs * 32 * NW + 32 * wave < CW; /* wave-uniform: the wave has columns */
   int mi = 0, jj = 0, rbefore = 0;
   const uint16_t *arow = p.zero_row;
   size_t kstep = 0;
@@ -1104,10 +1106,10 @@ __global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p
 #pragma unroll
   for (int s = 0; s < MT; ++s) acc[s] = f32x16{};
   if (g_lo < g_hi) {
-    Stager<256> st0, st1;
+    Stager<NT> st0, st1;
 #pragma unroll
-    for (int k = 0; k < Stager<256>::CH; ++k) {
-      const int idx = tid + k * 256;
+    for (int k = 0; k < Stager<NT>::CH; ++k) {
+      const int idx = tid + k * NT;
       const int r = idx >> 3, chk = idx & 7;
       const int pp = (int)(ul[r < nu ? r : nu - 1] >> 16);
       const int tok = p.perm ? (int)p.perm[pp] : pp;
@@ -1121,7 +1123,7 @@ __global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p
     aload(g_lo + 1, a1);
     st0.store(smem, tid);
     lds_barrier();
-    auto step = [&](int g, Stager<256> &hold, Stager<256> &ld, u32x4 (&av)[4]) {
+    auto step = [&](int g, Stager<NT> &hold, Stager<NT> &ld, u32x4 (&av)[4]) {
       const unsigned char *tb = smem + ((g - g_lo) & 1) * TILE;
       ld.load(p.x, g + 2 < g_hi ? g + 2 : g_hi - 1);
       if (wact) {
@@ -1150,7 +1152,7 @@ __global__ void __launch_bounds__(256) aos_amshrink_kernel(aos_amshrink_params p
   if (p.ks > 1) {
     /* this slice's partial sums, [row][128 columns] */
     if (col < CW) {
-      float *dst = p.part + (((size_t)kz * p.cb + ch) * p.csets + cs) * BM * 128 + (col - cs * 128);
+      float *dst = p.part + (((size_t)kz * p.cb + ch) * p.csets + cs) * BM * 128 + (col - cs * 32 * NW);
 #pragma unroll
       for (int s = 0; s < MT; ++s)
 #pragma unroll
@@ -1200,7 +1202,7 @@ __global__ void __launch_bounds__(256) aos_amreduce_kernel(aos_amshrink_params p
   __syncthreads();
   int CW = 0;
   for (int m = 0; m < p.nmod; ++m) CW += p.rpad[m];
-  const int cn = CW - cs * 128 < 128 ? CW - cs * 128 : 128;
+  const int cn = CW - cs * p.setw < p.setw ? CW - cs * p.setw : p.setw;
   const int ncg = cn / 4; /* rpad_i are multiples of 16: a group of 4 columns lies in one module */
   const size_t slab = (size_t)p.cb * p.csets * BM * 128;
   const float *src = p.part + ((size_t)ch * p.csets + cs) * BM * 128;
@@ -1220,13 +1222,13 @@ __global__ void __launch_bounds__(256) aos_amreduce_kernel(aos_amshrink_params p
         if (k0 + k < p.ks) sum += v[k];
     }
     int mi, jj, rbefore;
-    am_module(p, cs * 128 + cg * 4, mi, jj, rbefore);
+    am_module(p, cs * p.setw + cg * 4, mi, jj, rbefore);
     const AmUser m = meta[r];
     u32x2 o;
     o.x = (uint32_t)aos_f32_to_bf16(m.cf * sum[0]) | ((uint32_t)aos_f32_to_bf16(m.cf * sum[1]) << 16);
     o.y = (uint32_t)aos_f32_to_bf16(m.cf * sum[2]) | ((uint32_t)aos_f32_to_bf16(m.cf * sum[3]) << 16);
     *(u32x2 *)(p.SA + (size_t)m.p * p.s_stride + m.tu * rbefore + m.u * p.rpad[mi] + jj) = o;
-    if (m.ci != ~0u) *(u32x2 *)(p.SAc + (size_t)m.ci * CW + cs * 128 + cg * 4) = o;
+    if (m.ci != ~0u) *(u32x2 *)(p.SAc + (size_t)m.ci * CW + cs * p.setw + cg * 4) = o;
   }
 }
 
@@ -2196,12 +2198,17 @@ extern "C" int aos_launch_amshrink(const aos_amshrink_params *p, const aos_launc
     if (p->rpad[i] < 16 || p->rpad[i] % 16 || !p->A[i]) return (int)hipErrorInvalidValue;
     cols += p->rpad[i];
   }
-  if (p->csets != (cols + 127) / 128 || p->s_stride % 8) return (int)hipErrorInvalidValue;
+  if ((p->setw != 64 && p->setw != 128) || (p->setw == 64 && cols > 64) || p->csets != (cols + p->setw - 1) / p->setw ||
+      p->s_stride % 8)
+    return (int)hipErrorInvalidValue;
   if (p->reduce) {
     if (p->ks < 2) return (int)hipErrorInvalidValue;
     AOS_LAUNCH(ctx, aos_amreduce_kernel, dim3(p->cb, p->csets), dim3(256), 0, *p);
   } else {
-    AOS_LAUNCH(ctx, aos_amshrink_kernel, dim3(p->ks, p->cb, p->csets), dim3(256), 2 * BM * 128, *p);
+    if (p->setw == 64)
+      AOS_LAUNCH(ctx, aos_amshrink_kernel<2>, dim3(p->ks, p->cb, p->csets), dim3(128), 2 * BM * 128, *p);
+    else
+      AOS_LAUNCH(ctx, aos_amshrink_kernel<4>, dim3(p->ks, p->cb, p->csets), dim3(256), 2 * BM * 128, *p);
   }
   return (int)hipGetLastError();
 }

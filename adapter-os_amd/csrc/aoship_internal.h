@@ -470,7 +470,8 @@ typedef struct {
   const uint16_t *x;       /* [T][in] */
   const uint16_t *perm;    /* [T] or NULL */
   int T, in, nmod, tu_cap, ks, cb, csets; /* grid: ks x cb x csets (reduce: cb x csets) */
-  /* csets: ceil(sum of rpad_i / 128) */
+  int setw;                /* columns of a set: 64 (2-wave workgroups) or 128; csets = ceil(sum of
+                              rpad_i / setw) */
   int rpad[3];
   const uint16_t *const *A[3]; /* per module: [n] device A pointers (NULL: adapter without it) */
   const int *tu;
